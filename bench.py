@@ -1,0 +1,228 @@
+"""Benchmark of the fused int4 frozen-base LoRA linear on one MI355X.
+
+Workload: int4 group-64 frozen Linear 3072 -> 12288 with
+LoRA r=32, alpha=32, M=4096 tokens, forward + backward (y, t, dx, dA, dB)
+per step. Inputs are synthetic, seeded (numpy PCG64: W=0, X=1, A=2, B=3,
+dY=4), resident in HBM before timing starts.
+
+Prints ONE JSON line. `value` is whole-step algorithmic TFLOP/s,
+F = 4MNK + 6Mr(K+N) per step. `roofline` is for the dominant kernel, with
+its average launch time taken from HIP events that the library records
+around each of its launches on the launch stream. `cpu_baseline` times the
+reference's CPU algorithm (the oracle's f32 dequant + f32 GEMMs) on a
+bounded token sample of the same layer.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+
+WORKLOADS = {
+    # name: (M, K, N, r, alpha, fmt, group)
+    "ns": (4096, 3072, 12288, 32, 32.0, "int4", 64),
+    "c1": (1024, 3072, 3072, 16, 16.0, "int4", 64),
+    "c2": (4096, 3072, 12288, 32, 32.0, "fp8", 0),
+}
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--workload", default="ns", choices=sorted(WORKLOADS))
+    p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    return p.parse_args()
+
+
+def flops_step(M, K, N, r):
+    return 4.0 * M * N * K + 6.0 * M * r * (K + N)
+
+
+def make_inputs(M, K, N, r):
+    import numpy as np
+
+    g = lambda seed: np.random.Generator(np.random.PCG64(seed))  # noqa: E731
+    w = (g(0).standard_normal((N, K), dtype=np.float32) * np.float32(0.02))
+    x = g(1).standard_normal((M, K), dtype=np.float32)
+    bound = 1.0 / np.sqrt(K)
+    a = g(2).uniform(-bound, bound, (K, r)).astype(np.float32)
+    b = (g(3).standard_normal((r, N), dtype=np.float32) * np.float32(1e-3))
+    dy = g(4).standard_normal((M, N), dtype=np.float32)
+    return w, x, a, b, dy
+
+
+def load_traffic(kernel, workload):
+    """HBM bytes per launch from committed rocprofv3 --pmc summaries, if any."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            d = json.load(f)
+        v = d.get(workload, {}).get(kernel)
+        return None if v is None else float(v)
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: every box of this build has one MI355X and the path is "
+              f"single-device; --gpus {args.gpus} is not supported (run with --gpus 1).", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    from loractl_amd import device as D
+
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda:0")
+    M, K, N, r, alpha, fmt, group = WORKLOADS[args.workload]
+    s = alpha / r
+    w, x, a, b, dy = make_inputs(M, K, N, r)
+    wt = torch.from_numpy(w).to(dev)
+    wq = D.quantize_int4(wt, group) if fmt == "int4" else D.quantize_fp8(wt, True)
+    del wt
+    xb = torch.from_numpy(x).to(dev).to(torch.bfloat16)
+    ab = torch.from_numpy(a).to(dev).to(torch.bfloat16)
+    bb = torch.from_numpy(b).to(dev).to(torch.bfloat16)
+    dyb = torch.from_numpy(dy).to(dev).to(torch.bfloat16)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    t = torch.empty((M, r), dtype=torch.bfloat16, device=dev)
+    dx = torch.empty((M, K), dtype=torch.bfloat16, device=dev)
+    da = torch.empty((K, r), dtype=torch.float32, device=dev)
+    db = torch.empty((r, N), dtype=torch.float32, device=dev)
+    D.reserve(M, N, K, r)
+
+    def step():
+        D.lora_fwd(xb, wq, ab, bb, s, y=y, t=t)
+        D.lora_bwd(xb, dyb, wq, ab, bb, s, t, out=(dx, da, db))
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    for v in (y, dx, da, db):
+        if not torch.isfinite(v).all() or not v.abs().max() > 0:
+            raise RuntimeError("implausible output (all-zero or non-finite)")
+
+    def timed(n):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(n):
+            step()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1)
+
+    ms_total = timed(args.steps)
+    ms_step = ms_total / args.steps
+    # sanity of the protocol (crates/loractl-bench/src/lib.rs:39-115): 2x iterations ~ 2x time
+    ratio = timed(2 * args.steps) / ms_total
+    F = flops_step(M, K, N, r)
+    value = F / (ms_step * 1e-3) / 1e12
+
+    # per-kernel launch times from the library's HIP events
+    D.profile_reset()
+    D.profile_enable(True)
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    prof = D.profile_read()
+    D.profile_enable(False)
+    kernels = {k: {"avg_us": 1e3 * ms / n, "launches": n} for k, (ms, n) in prof.items() if n}
+    per_kernel_flops = {"fwd_main": 2.0 * M * N * (K + r), "bwd_dx": 2.0 * M * K * (N + r)}
+    dom = max(("fwd_main", "bwd_dx"), key=lambda k: prof[k][0])
+    dom_us = kernels[dom]["avg_us"]
+    achieved = per_kernel_flops[dom] / (dom_us * 1e-6) / 1e12
+    roofline = {
+        "kernel": dom,
+        "bound": "mfma",
+        "achieved": round(achieved, 2),
+        "peak": PEAK_BF16_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+        "traffic": load_traffic(dom, args.workload),
+        "flops_per_launch": per_kernel_flops[dom],
+        "avg_launch_us": round(dom_us, 2),
+    }
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(wq, x, a, b, dy, M, K, N, r, s, group, fmt, args.cpu_seconds)
+
+    out = {
+        "metric": "int4-base LoRA linear fwd+bwd TFLOP/s",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded PCG64; W~N(0,0.02) quantized on device, X,dY~N(0,1), A~U(+-1/sqrt(K)), B~N(0,1e-3))",
+        "config": {
+            "workload": f"{fmt}{'-g' + str(group) if fmt == 'int4' else '-per-channel'} frozen Linear {K}->{N} "
+                        f"+ LoRA r={r} alpha={alpha:g}, M={M} tokens, forward+backward (y, dx, dA, dB)",
+            "M": M, "K": K, "N": N, "rank": r, "group": group, "format": fmt,
+            "parallelism": "single-gpu",
+        },
+        "pct_of_mfma_peak": round(100.0 * value / PEAK_BF16_TFLOPS, 2),
+        "flops_per_step": F,
+        "sanity_x2_ratio": round(ratio, 3),
+        "kernels_us": {k: round(v["avg_us"], 2) for k, v in kernels.items()},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+def cpu_baseline(wq, x, a, b, dy, M, K, N, r, s, group, fmt, budget_s):
+    """The reference's CPU algorithm (f32 dequant of the whole weight, f32
+    GEMMs) on the first m_s tokens of the same layer, on this host's cores."""
+    import numpy as np
+
+    import oracle as O
+
+    if fmt != "int4":
+        return None
+    packed = wq.data.cpu().numpy()
+    scales = wq.scales.cpu().numpy()
+    m_s = 64
+    st = O.CpuStepInt4(packed, scales, group, x[:m_s], a, b, s, dy[:m_s])
+    t0 = time.perf_counter()
+    threads = st.run()  # warmup (first touch of the work buffers)
+    first = time.perf_counter() - t0
+    reps = max(1, int(budget_s / max(first, 1e-3)))
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        st.run()
+    dt = (time.perf_counter() - t0) / reps
+    F = flops_step(m_s, K, N, r)
+    return {
+        "value": round(F / dt / 1e12, 5),
+        "unit": "TFLOP/s",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": f"{m_s} of {M} tokens of the same {K}->{N} r={r} int4-g{group} layer, fwd+bwd, {reps} reps "
+                  f"of {dt:.3f} s (f32 dequant of the full weight twice per step + f32 GEMMs, OpenMP)",
+    }
+
+
+if __name__ == "__main__":
+    main()

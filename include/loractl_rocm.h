@@ -1,0 +1,156 @@
+/*
+ * loractl_rocm.h — C ABI of libloractl_rocm.so, the MI355X (gfx950) kernels
+ * for loractl's quantized frozen-base LoRA linear.
+ *
+ * Reference interfaces replaced (laurigates/loractl, crates/loractl-core):
+ *   - QuantBackend::quant_matmul_t (src/quant.rs:172-178) and its Autodiff
+ *     override QuantMatmulT (src/quant.rs:210-263)
+ *       -> lrq_quant_matmul_t / lrq_quant_matmul_t_bwd
+ *   - site() = BaseLinear::forward + LoraAdapters::apply
+ *     (src/mmdit.rs:483-536, src/adapters.rs:75-85, src/lora.rs:199-203)
+ *       -> lrq_lora_fwd / lrq_lora_bwd (the fused drop-in: base + delta)
+ *   - quantize_linear_weight (src/quant.rs:74-82) -> lrq_quantize_int4
+ *   - dequantize to f32 (src/quant.rs:232, :250) -> lrq_dequant
+ *   - e4m3fn LUT decode * scale (src/fp8.rs:39-56, :279-329) -> lrq_dequant
+ *     on an LRQ_FMT_FP8 weight
+ *   - fp8 repack encoder (reference/fp8_reference.py:83-91; no counterpart in
+ *     the crate) -> lrq_quantize_fp8
+ *
+ * Conventions
+ *   - Every tensor pointer is a DEVICE pointer owned by the caller; the
+ *     library never frees it. Row-major, densely packed, 16-byte aligned.
+ *   - bf16 tensors are passed as uint16_t bit patterns.
+ *   - Calls are stream-ordered and asynchronous on the context's stream
+ *     (lrq_set_stream); call lrq_sync or synchronize the stream to wait.
+ *   - Every call returns 0 on success or a negative LRQ_E* code; the message
+ *     is in lrq_last_error(ctx). No C++ exception crosses the ABI. Shape and
+ *     layout violations return LRQ_EINVAL (the reference panics there:
+ *     src/quant.rs:76-80), never a silent fallback.
+ *   - A context belongs to one host thread at a time; distinct contexts may
+ *     be used concurrently. Hot calls allocate only when the context's
+ *     workspace must grow (pre-size it with lrq_reserve).
+ *
+ * Weight layouts (file layout [d_out = n, d_in = k], as QuantLinear keeps it,
+ * src/mmdit.rs:413-444):
+ *   LRQ_FMT_INT4: data = uint8 [n, k/2]; byte j of a row holds k=2j in its low
+ *     nibble and k=2j+1 in its high nibble, each nibble storing q+8 with
+ *     q in [-7, 7]; scales = f32 [n, k/group]; dequant = q * scale (f32).
+ *   LRQ_FMT_FP8: data = e4m3fn bytes [n, k]; scales = f32 [n] (per_channel)
+ *     or [1]; dequant = LUT[byte] * scale (f32).
+ *   LoRA factors in burn layout: A = [k, r] (d_in x rank), B = [r, n].
+ */
+#ifndef LORACTL_ROCM_H
+#define LORACTL_ROCM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LRQ_ABI_VERSION 1
+
+enum {
+  LRQ_OK = 0,
+  LRQ_EINVAL = -1,       /* bad shape, alignment, group size or argument */
+  LRQ_EUNSUPPORTED = -2, /* valid request this build does not implement */
+  LRQ_EHIP = -3,         /* a HIP runtime call failed */
+  LRQ_ENOMEM = -4        /* device allocation for the workspace failed */
+};
+
+enum { LRQ_FMT_INT4 = 1, LRQ_FMT_FP8 = 2 };
+
+typedef struct lrq_ctx lrq_ctx;
+
+/* A frozen base weight: plain pointers and sizes, no ownership. */
+typedef struct lrq_weight {
+  int32_t format;       /* LRQ_FMT_INT4 or LRQ_FMT_FP8 */
+  int32_t group;        /* int4: block size along k, a multiple of 32 dividing k */
+  int64_t n;            /* d_out */
+  int64_t k;            /* d_in (a multiple of 32) */
+  const void* data;     /* device: packed int4 [n, k/2] or fp8 bytes [n, k] */
+  const float* scales;  /* device: int4 [n, k/group]; fp8 [n] or [1] */
+  int32_t per_channel;  /* fp8: 1 when scales has n entries, 0 for one scalar */
+  int32_t reserved;
+  const float* bias;    /* device f32 [n] or NULL (src/mmdit.rs:426-427) */
+} lrq_weight;
+
+/* Library version (LRQ_ABI_VERSION). */
+int lrq_version(void);
+
+/* Create a context on HIP device `device`; it owns a stream and a workspace. */
+int lrq_create(int device, lrq_ctx** out);
+int lrq_destroy(lrq_ctx* ctx);
+
+/* Run subsequent calls on `stream` (a hipStream_t; NULL restores the
+ * context's own stream). */
+int lrq_set_stream(lrq_ctx* ctx, void* stream);
+int lrq_sync(lrq_ctx* ctx);
+const char* lrq_last_error(const lrq_ctx* ctx);
+
+/* Pre-size the workspace for calls with up to m tokens, n outputs, k inputs
+ * and rank r, so that later hot calls do not allocate. */
+int lrq_reserve(lrq_ctx* ctx, int64_t m, int64_t n, int64_t k, int64_t r);
+
+/* quantize_linear_weight (src/quant.rs:74-82) at Q4S with block `group`:
+ * w f32 [n, k] -> packed [n, k/2] + scales [n, k/group], bit-exact with the
+ * closed form scale = absmax/7, q = clamp(round_half_away(w/scale), -7, 7). */
+int lrq_quantize_int4(lrq_ctx* ctx, const float* w, int64_t n, int64_t k, int64_t group,
+                      uint8_t* packed, float* scales);
+
+/* fp8 repack (reference/fp8_reference.py:83-91): scale = max(amax/448, 1e-12)
+ * per tensor or per output row, byte = RNE e4m3fn of w/scale, saturating to
+ * +-448, sign kept. scales has n entries (per_channel) or 1. */
+int lrq_quantize_fp8(lrq_ctx* ctx, const float* w, int64_t n, int64_t k, int per_channel,
+                     uint8_t* bytes, float* scales);
+
+/* Dequantize the whole weight to f32 [n, k] (src/quant.rs:232; fp8.rs:306-318).
+ * Debug/parity surface: bit-exact with the CPU definition. */
+int lrq_dequant(lrq_ctx* ctx, const lrq_weight* w, float* out);
+
+/* The bf16 GEMM operand the fused kernels feed to the matrix cores:
+ * bf16_rne(dequant) for int4; the exact e4m3fn value (no scale) for fp8. */
+int lrq_dequant_bf16(lrq_ctx* ctx, const lrq_weight* w, uint16_t* out);
+
+/* QuantBackend::quant_matmul_t (src/quant.rs:172-178): y[m, n] = x[m, k] .
+ * dequant(w)^T (+ bias), bf16 in/out, f32 accumulation. */
+int lrq_quant_matmul_t(lrq_ctx* ctx, const lrq_weight* w, const uint16_t* x, int64_t m,
+                       uint16_t* y);
+
+/* QuantMatmulT::backward (src/quant.rs:221-235): dx[m, k] = dy[m, n] . dequant(w). */
+int lrq_quant_matmul_t_bwd(lrq_ctx* ctx, const lrq_weight* w, const uint16_t* dy, int64_t m,
+                           uint16_t* dx);
+
+/* The fused site forward (src/mmdit.rs:526-536 with a registered delta):
+ *   y = x . dequant(w)^T (+ bias) + scaling * (x . A) . B
+ * x [m, k], A [k, r], B [r, n], y [m, n], all bf16. When t_out is not NULL it
+ * receives t = scaling * x . A as bf16 [m, r], the activation lrq_lora_bwd
+ * needs. 1 <= r <= 64. */
+int lrq_lora_fwd(lrq_ctx* ctx, const lrq_weight* w, const uint16_t* x, int64_t m,
+                 const uint16_t* a, const uint16_t* b, int64_t r, float scaling, uint16_t* y,
+                 uint16_t* t_out);
+
+/* The fused site backward (gradients to x, A, B; none to the frozen weight):
+ *   u  = scaling * dy . B^T
+ *   dx = dy . dequant(w) + u . A^T          bf16 [m, k]
+ *   dA = x^T . u                            f32  [k, r]
+ *   dB = t^T . dy   (t from lrq_lora_fwd)   f32  [r, n]
+ * Any of dx, da, db may be NULL to skip that output. */
+int lrq_lora_bwd(lrq_ctx* ctx, const lrq_weight* w, const uint16_t* x, const uint16_t* dy,
+                 int64_t m, const uint16_t* a, const uint16_t* b, int64_t r, float scaling,
+                 const uint16_t* t, uint16_t* dx, float* da, float* db);
+
+/* Per-kernel timing: when enabled, every launch is bracketed by HIP events
+ * on the launch stream; lrq_profile_read returns the summed milliseconds and
+ * the launch count for kernel id `kid` (0 <= kid < lrq_profile_count()). */
+int lrq_profile_enable(lrq_ctx* ctx, int on);
+int lrq_profile_reset(lrq_ctx* ctx);
+int lrq_profile_count(void);
+const char* lrq_profile_name(int kid);
+int lrq_profile_read(lrq_ctx* ctx, int kid, double* total_ms, int64_t* launches);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LORACTL_ROCM_H */

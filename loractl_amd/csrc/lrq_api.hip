@@ -1,0 +1,473 @@
+// The C ABI of libloractl_rocm.so (include/loractl_rocm.h): context, stream,
+// workspace, argument validation, per-kernel timing, and the call sequences
+// of the fused forward and backward.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "lrq_kernels.h"
+
+void set_num_cus(int n);
+
+struct lrq_ctx {
+  int device = 0;
+  hipStream_t own = nullptr;
+  hipStream_t stream = nullptr;
+  char* ws = nullptr;
+  size_t ws_bytes = 0;
+  char err[512] = {0};
+  bool prof = false;
+  struct Rec {
+    int kid;
+    hipEvent_t a, b;
+  };
+  std::vector<Rec> pending;
+  std::vector<hipEvent_t> pool;
+  double total_ms[KID_COUNT] = {0};
+  int64_t launches[KID_COUNT] = {0};
+};
+
+namespace {
+
+const char* kNames[KID_COUNT] = {"quantize_int4", "quantize_fp8", "dequant", "fwd_main", "bwd_dx",
+                                 "lora_prep",     "lora_t",       "lora_u",  "lora_da",  "lora_db"};
+
+int fail(lrq_ctx* c, int code, const char* fmt, ...) {
+  if (c) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(c->err, sizeof(c->err), fmt, ap);
+    va_end(ap);
+  }
+  return code;
+}
+
+int hip_fail(lrq_ctx* c, hipError_t e, const char* what) {
+  return fail(c, LRQ_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int64_t round_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
+
+hipEvent_t take_event(lrq_ctx* c) {
+  if (!c->pool.empty()) {
+    hipEvent_t e = c->pool.back();
+    c->pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+// Run one launcher; when profiling, bracket it with events on the stream.
+template <class F>
+int run(lrq_ctx* c, int kid, const char* what, F&& f) {
+  hipEvent_t a = nullptr, b = nullptr;
+  if (c->prof) {
+    a = take_event(c);
+    if (a) (void)hipEventRecord(a, c->stream);
+  }
+  hipError_t e = f();
+  if (e != hipSuccess) return hip_fail(c, e, what);
+  if (c->prof && a) {
+    b = take_event(c);
+    if (b) {
+      (void)hipEventRecord(b, c->stream);
+      c->pending.push_back({kid, a, b});
+    } else {
+      c->pool.push_back(a);
+    }
+  }
+  return LRQ_OK;
+}
+
+int flush_profile(lrq_ctx* c) {
+  for (auto& r : c->pending) {
+    hipError_t e = hipEventSynchronize(r.b);
+    if (e != hipSuccess) return hip_fail(c, e, "hipEventSynchronize");
+    float ms = 0.0f;
+    e = hipEventElapsedTime(&ms, r.a, r.b);
+    if (e != hipSuccess) return hip_fail(c, e, "hipEventElapsedTime");
+    c->total_ms[r.kid] += ms;
+    c->launches[r.kid] += 1;
+    c->pool.push_back(r.a);
+    c->pool.push_back(r.b);
+  }
+  c->pending.clear();
+  return LRQ_OK;
+}
+
+// Bump allocator over the context workspace (256-byte aligned slices).
+struct Slab {
+  char* base;
+  size_t off = 0;
+  template <class T>
+  T* take(int64_t count) {
+    T* p = reinterpret_cast<T*>(base ? base + off : nullptr);
+    off += (size_t)round_up((int64_t)(count * (int64_t)sizeof(T)), 256);
+    return p;
+  }
+};
+
+int ensure_ws(lrq_ctx* c, size_t bytes) {
+  if (bytes <= c->ws_bytes) return LRQ_OK;
+  // stream-ordered users of the old buffer must finish before it goes
+  hipError_t e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) return hip_fail(c, e, "hipStreamSynchronize");
+  if (c->ws) (void)hipFree(c->ws);
+  c->ws = nullptr;
+  c->ws_bytes = 0;
+  size_t want = (size_t)round_up((int64_t)bytes, 1 << 20);
+  e = hipMalloc(&c->ws, want);
+  if (e != hipSuccess) {
+    c->ws = nullptr;
+    return fail(c, LRQ_ENOMEM, "workspace of %zu bytes: %s", want, hipGetErrorString(e));
+  }
+  c->ws_bytes = want;
+  return LRQ_OK;
+}
+
+// Workspace layout of the fused calls (sizes only when base == nullptr).
+struct LoraWs {
+  uint16_t *at, *bt, *tp, *ap, *tt, *up, *ut;
+  float* partial;
+  size_t bytes;
+};
+
+LoraWs lora_layout(char* base, int64_t m, int64_t n, int64_t k, int rp) {
+  Slab s{base};
+  LoraWs w{};
+  const int64_t mp = round_up(m > 0 ? m : 1, 64);
+  w.at = s.take<uint16_t>((int64_t)rp * k);
+  w.bt = s.take<uint16_t>(n * rp);
+  w.tp = s.take<uint16_t>(m * rp);
+  w.ap = s.take<uint16_t>(k * rp);
+  w.tt = s.take<uint16_t>((int64_t)rp * mp);
+  w.up = s.take<uint16_t>(m * rp);
+  w.ut = s.take<uint16_t>((int64_t)rp * mp);
+  const int64_t p_nt_t = (int64_t)skinny_nt_splits(m, k) * m * rp;
+  const int64_t p_nt_u = (int64_t)skinny_nt_splits(m, n) * m * rp;
+  const int64_t p_tn_a = (int64_t)skinny_tn_splits(m, k) * k * rp;
+  const int64_t p_tn_b = (int64_t)skinny_tn_splits(m, n) * n * rp;
+  int64_t p = p_nt_t;
+  if (p_nt_u > p) p = p_nt_u;
+  if (p_tn_a > p) p = p_tn_a;
+  if (p_tn_b > p) p = p_tn_b;
+  w.partial = s.take<float>(p > 0 ? p : 1);
+  w.bytes = s.off;
+  return w;
+}
+
+int check_weight(lrq_ctx* c, const lrq_weight* w, bool gemm) {
+  if (!w) return fail(c, LRQ_EINVAL, "weight descriptor is NULL");
+  if (w->format != LRQ_FMT_INT4 && w->format != LRQ_FMT_FP8)
+    return fail(c, LRQ_EINVAL, "weight format %d is neither LRQ_FMT_INT4 nor LRQ_FMT_FP8", w->format);
+  if (w->n < 0 || w->k < 0) return fail(c, LRQ_EINVAL, "negative weight shape [%lld, %lld]",
+                                        (long long)w->n, (long long)w->k);
+  if (w->k % 32 != 0)
+    return fail(c, LRQ_EINVAL, "linear weight [%lld, %lld]: the input dim must be a multiple of 32",
+                (long long)w->n, (long long)w->k);
+  if (w->format == LRQ_FMT_INT4) {
+    if (w->group <= 0 || w->group % 32 != 0 || w->k % w->group != 0)
+      return fail(c, LRQ_EINVAL,
+                  "linear weight [%lld, %lld]: the input dim must be a multiple of the quant block "
+                  "(%d), and the block a multiple of 32",
+                  (long long)w->n, (long long)w->k, w->group);
+  }
+  if (gemm && w->n % 8 != 0)
+    return fail(c, LRQ_EINVAL, "d_out %lld must be a multiple of 8 for the fused kernels", (long long)w->n);
+  if (w->n * w->k > 0 && (!w->data || !w->scales))
+    return fail(c, LRQ_EINVAL, "weight data/scales pointer is NULL");
+  if (!aligned16(w->data)) return fail(c, LRQ_EINVAL, "weight data must be 16-byte aligned");
+  if (w->bias && !aligned16(w->bias)) return fail(c, LRQ_EINVAL, "bias must be 16-byte aligned");
+  return LRQ_OK;
+}
+
+int begin(lrq_ctx* c) {
+  if (!c) return LRQ_EINVAL;
+  c->err[0] = 0;
+  hipError_t e = hipSetDevice(c->device);
+  if (e != hipSuccess) return hip_fail(c, e, "hipSetDevice");
+  return LRQ_OK;
+}
+
+#define LRQ_TRY(x)            \
+  do {                        \
+    int _rc = (x);            \
+    if (_rc != LRQ_OK) return _rc; \
+  } while (0)
+
+}  // namespace
+
+extern "C" {
+
+int lrq_version(void) { return LRQ_ABI_VERSION; }
+
+int lrq_create(int device, lrq_ctx** out) {
+  if (!out) return LRQ_EINVAL;
+  *out = nullptr;
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || device < 0 || device >= count) return LRQ_EINVAL;
+  lrq_ctx* c = new (std::nothrow) lrq_ctx();
+  if (!c) return LRQ_ENOMEM;
+  c->device = device;
+  if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking) != hipSuccess) {
+    delete c;
+    return LRQ_EHIP;
+  }
+  c->stream = c->own;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) == hipSuccess) set_num_cus(prop.multiProcessorCount);
+  *out = c;
+  return LRQ_OK;
+}
+
+int lrq_destroy(lrq_ctx* c) {
+  if (!c) return LRQ_OK;
+  (void)hipSetDevice(c->device);
+  (void)hipStreamSynchronize(c->stream);
+  for (auto& r : c->pending) {
+    (void)hipEventDestroy(r.a);
+    (void)hipEventDestroy(r.b);
+  }
+  for (auto e : c->pool) (void)hipEventDestroy(e);
+  if (c->ws) (void)hipFree(c->ws);
+  if (c->own) (void)hipStreamDestroy(c->own);
+  delete c;
+  return LRQ_OK;
+}
+
+int lrq_set_stream(lrq_ctx* c, void* stream) {
+  LRQ_TRY(begin(c));
+  c->stream = stream ? reinterpret_cast<hipStream_t>(stream) : c->own;
+  return LRQ_OK;
+}
+
+int lrq_sync(lrq_ctx* c) {
+  LRQ_TRY(begin(c));
+  hipError_t e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) return hip_fail(c, e, "hipStreamSynchronize");
+  return LRQ_OK;
+}
+
+const char* lrq_last_error(const lrq_ctx* c) { return c ? c->err : "null context"; }
+
+int lrq_reserve(lrq_ctx* c, int64_t m, int64_t n, int64_t k, int64_t r) {
+  LRQ_TRY(begin(c));
+  if (m < 0 || n < 0 || k < 0 || r < 0 || r > 64) return fail(c, LRQ_EINVAL, "bad reserve shape");
+  const int rp = (int)round_up(r > 0 ? r : 16, 16);
+  size_t need = lora_layout(nullptr, m, n, k, rp).bytes;
+  const size_t fp8_need = (size_t)round_up(n * 4, 256);
+  if (fp8_need > need) need = fp8_need;
+  return ensure_ws(c, need);
+}
+
+int lrq_quantize_int4(lrq_ctx* c, const float* w, int64_t n, int64_t k, int64_t group,
+                      uint8_t* packed, float* scales) {
+  LRQ_TRY(begin(c));
+  if (n < 0 || k < 0) return fail(c, LRQ_EINVAL, "negative shape");
+  if (group < 32 || group > 2048 || (group & (group - 1)) != 0)
+    return fail(c, LRQ_EINVAL, "quant block %lld must be a power of two in [32, 2048]", (long long)group);
+  if (k % group != 0)
+    return fail(c, LRQ_EINVAL,
+                "linear weight [%lld, %lld]: the input dim must be a multiple of the quant block (%lld)",
+                (long long)n, (long long)k, (long long)group);
+  if (!aligned16(w) || !aligned16(packed)) return fail(c, LRQ_EINVAL, "w and packed must be 16-byte aligned");
+  return run(c, KID_QUANT_INT4, "quantize_int4",
+             [&] { return launch_quantize_int4(c->stream, w, n, k, (int)group, packed, scales); });
+}
+
+int lrq_quantize_fp8(lrq_ctx* c, const float* w, int64_t n, int64_t k, int per_channel,
+                     uint8_t* bytes, float* scales) {
+  LRQ_TRY(begin(c));
+  if (n < 0 || k < 0 || k % 4 != 0) return fail(c, LRQ_EINVAL, "fp8 quantize needs k %% 4 == 0");
+  if (!aligned16(w) || !aligned16(bytes)) return fail(c, LRQ_EINVAL, "w and bytes must be 16-byte aligned");
+  LRQ_TRY(ensure_ws(c, (size_t)round_up((n > 0 ? n : 1) * 4, 256)));
+  float* amax = reinterpret_cast<float*>(c->ws);
+  return run(c, KID_QUANT_FP8, "quantize_fp8", [&] {
+    return launch_quantize_fp8(c->stream, w, n, k, per_channel, bytes, scales, amax);
+  });
+}
+
+int lrq_dequant(lrq_ctx* c, const lrq_weight* w, float* out) {
+  LRQ_TRY(begin(c));
+  LRQ_TRY(check_weight(c, w, false));
+  if (!aligned16(out)) return fail(c, LRQ_EINVAL, "out must be 16-byte aligned");
+  return run(c, KID_DEQUANT, "dequant", [&] { return launch_dequant(c->stream, w, out, false); });
+}
+
+int lrq_dequant_bf16(lrq_ctx* c, const lrq_weight* w, uint16_t* out) {
+  LRQ_TRY(begin(c));
+  LRQ_TRY(check_weight(c, w, false));
+  if (!aligned16(out)) return fail(c, LRQ_EINVAL, "out must be 16-byte aligned");
+  return run(c, KID_DEQUANT, "dequant_bf16", [&] { return launch_dequant(c->stream, w, out, true); });
+}
+
+static int fwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t m, const uint16_t* a,
+                    const uint16_t* b, int64_t r, float scaling, uint16_t* y, uint16_t* t_out) {
+  LRQ_TRY(begin(c));
+  LRQ_TRY(check_weight(c, w, true));
+  if (m < 0) return fail(c, LRQ_EINVAL, "negative token count");
+  if (!aligned16(x) || !aligned16(y)) return fail(c, LRQ_EINVAL, "x and y must be 16-byte aligned");
+  const bool lora = a != nullptr && b != nullptr && r > 0;
+  if (lora && (r < 1 || r > 64)) return fail(c, LRQ_EINVAL, "rank %lld outside [1, 64]", (long long)r);
+  FwdArgs fa{};
+  fa.x = x;
+  fa.m = m;
+  fa.n = w->n;
+  fa.k = w->k;
+  fa.wdata = reinterpret_cast<const uint8_t*>(w->data);
+  fa.wscale = w->scales;
+  fa.group = w->group;
+  fa.per_channel = w->per_channel;
+  fa.bias = w->bias;
+  fa.y = y;
+  if (lora) {
+    const int rp = (int)round_up(r, 16);
+    LRQ_TRY(ensure_ws(c, lora_layout(nullptr, m, w->n, w->k, rp).bytes));
+    LoraWs ws = lora_layout(c->ws, m, w->n, w->k, rp);
+    // A [k, r] -> At [rp, k]; B [r, n] -> Bt [n, rp] (zero-padded rank)
+    LRQ_TRY(run(c, KID_LORA_PREP, "lora_prep", [&] {
+      hipError_t e = launch_pad_transpose(c->stream, a, w->k, r, r, ws.at, rp, w->k, true);
+      if (e != hipSuccess) return e;
+      return launch_pad_transpose(c->stream, b, r, w->n, w->n, ws.bt, w->n, rp, true);
+    }));
+    // t = s . x . A   (bf16 [m, rp] for the fused step, [m, r] for the caller)
+    LRQ_TRY(run(c, KID_LORA_T, "lora_t", [&] {
+      return launch_skinny_nt(c->stream, x, ws.at, m, w->k, (int)r, rp, scaling, ws.partial,
+                              skinny_nt_splits(m, w->k), ws.tp, nullptr, 0, t_out, (int)r);
+    }));
+    fa.t = ws.tp;
+    fa.bt = ws.bt;
+    fa.rp = rp;
+  }
+  int kid = KID_FWD_MAIN;
+  return run(c, KID_FWD_MAIN, "fwd_main", [&] { return launch_fwd_main(c->stream, w->format, fa, &kid); });
+}
+
+int lrq_quant_matmul_t(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t m, uint16_t* y) {
+  return fwd_impl(c, w, x, m, nullptr, nullptr, 0, 1.0f, y, nullptr);
+}
+
+int lrq_lora_fwd(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t m, const uint16_t* a,
+                 const uint16_t* b, int64_t r, float scaling, uint16_t* y, uint16_t* t_out) {
+  if (c && (r < 1 || r > 64 || !a || !b)) {
+    c->err[0] = 0;
+    return fail(c, LRQ_EINVAL, "lrq_lora_fwd needs A, B and 1 <= r <= 64 (got r=%lld)", (long long)r);
+  }
+  return fwd_impl(c, w, x, m, a, b, r, scaling, y, t_out);
+}
+
+static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const uint16_t* dy, int64_t m,
+                    const uint16_t* a, const uint16_t* b, int64_t r, float scaling, const uint16_t* t,
+                    uint16_t* dx, float* da, float* db) {
+  LRQ_TRY(begin(c));
+  LRQ_TRY(check_weight(c, w, true));
+  if (m < 0) return fail(c, LRQ_EINVAL, "negative token count");
+  if (!aligned16(dy)) return fail(c, LRQ_EINVAL, "dy must be 16-byte aligned");
+  if (dx && !aligned16(dx)) return fail(c, LRQ_EINVAL, "dx must be 16-byte aligned");
+  const bool lora = a != nullptr && b != nullptr && r > 0;
+  BwdArgs ba{};
+  ba.dy = dy;
+  ba.m = m;
+  ba.n = w->n;
+  ba.k = w->k;
+  ba.wdata = reinterpret_cast<const uint8_t*>(w->data);
+  ba.wscale = w->scales;
+  ba.group = w->group;
+  ba.per_channel = w->per_channel;
+  ba.dx = dx;
+  if (lora) {
+    if (r > 64) return fail(c, LRQ_EINVAL, "rank %lld outside [1, 64]", (long long)r);
+    if ((da && (!x || !aligned16(x))) || (db && !t))
+      return fail(c, LRQ_EINVAL, "dA needs x and dB needs t (16-byte aligned)");
+    const int rp = (int)round_up(r, 16);
+    const int64_t mp = round_up(m > 0 ? m : 1, 64);
+    LRQ_TRY(ensure_ws(c, lora_layout(nullptr, m, w->n, w->k, rp).bytes));
+    LoraWs ws = lora_layout(c->ws, m, w->n, w->k, rp);
+    LRQ_TRY(run(c, KID_LORA_PREP, "lora_prep", [&] {
+      hipError_t e = launch_pad_transpose(c->stream, a, w->k, r, r, ws.ap, w->k, rp, false);
+      if (e != hipSuccess || !db) return e;
+      return launch_pad_transpose(c->stream, t, m, r, r, ws.tt, rp, mp, true);
+    }));
+    // u = s . dy . B^T   ([m, rp] for dx, [rp, mp] for dA)
+    LRQ_TRY(run(c, KID_LORA_U, "lora_u", [&] {
+      return launch_skinny_nt(c->stream, dy, b, m, w->n, (int)r, rp, scaling, ws.partial,
+                              skinny_nt_splits(m, w->n), ws.up, ws.ut, mp, nullptr, 0);
+    }));
+    ba.u = ws.up;
+    ba.ap = ws.ap;
+    ba.rp = rp;
+    if (dx) {
+      int kid = KID_BWD_DX;
+      LRQ_TRY(run(c, KID_BWD_DX, "bwd_dx", [&] { return launch_bwd_dx(c->stream, w->format, ba, &kid); }));
+    }
+    if (da) {
+      LRQ_TRY(run(c, KID_LORA_DA, "lora_da", [&] {
+        return launch_skinny_tn(c->stream, x, ws.ut, mp, m, w->k, (int)r, rp, ws.partial,
+                                skinny_tn_splits(m, w->k), da, r, 1);
+      }));
+    }
+    if (db) {
+      LRQ_TRY(run(c, KID_LORA_DB, "lora_db", [&] {
+        return launch_skinny_tn(c->stream, dy, ws.tt, mp, m, w->n, (int)r, rp, ws.partial,
+                                skinny_tn_splits(m, w->n), db, 1, w->n);
+      }));
+    }
+    return LRQ_OK;
+  }
+  if (!dx) return LRQ_OK;
+  int kid = KID_BWD_DX;
+  return run(c, KID_BWD_DX, "bwd_dx", [&] { return launch_bwd_dx(c->stream, w->format, ba, &kid); });
+}
+
+int lrq_quant_matmul_t_bwd(lrq_ctx* c, const lrq_weight* w, const uint16_t* dy, int64_t m, uint16_t* dx) {
+  return bwd_impl(c, w, nullptr, dy, m, nullptr, nullptr, 0, 1.0f, nullptr, dx, nullptr, nullptr);
+}
+
+int lrq_lora_bwd(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const uint16_t* dy, int64_t m,
+                 const uint16_t* a, const uint16_t* b, int64_t r, float scaling, const uint16_t* t,
+                 uint16_t* dx, float* da, float* db) {
+  if (c && (r < 1 || r > 64 || !a || !b)) {
+    c->err[0] = 0;
+    return fail(c, LRQ_EINVAL, "lrq_lora_bwd needs A, B and 1 <= r <= 64 (got r=%lld)", (long long)r);
+  }
+  return bwd_impl(c, w, x, dy, m, a, b, r, scaling, t, dx, da, db);
+}
+
+int lrq_profile_enable(lrq_ctx* c, int on) {
+  LRQ_TRY(begin(c));
+  c->prof = on != 0;
+  return LRQ_OK;
+}
+
+int lrq_profile_reset(lrq_ctx* c) {
+  LRQ_TRY(begin(c));
+  LRQ_TRY(flush_profile(c));
+  for (int i = 0; i < KID_COUNT; ++i) {
+    c->total_ms[i] = 0.0;
+    c->launches[i] = 0;
+  }
+  return LRQ_OK;
+}
+
+int lrq_profile_count(void) { return KID_COUNT; }
+
+const char* lrq_profile_name(int kid) { return (kid >= 0 && kid < KID_COUNT) ? kNames[kid] : ""; }
+
+int lrq_profile_read(lrq_ctx* c, int kid, double* total_ms, int64_t* launches) {
+  LRQ_TRY(begin(c));
+  if (kid < 0 || kid >= KID_COUNT) return fail(c, LRQ_EINVAL, "kernel id %d out of range", kid);
+  LRQ_TRY(flush_profile(c));
+  if (total_ms) *total_ms = c->total_ms[kid];
+  if (launches) *launches = c->launches[kid];
+  return LRQ_OK;
+}
+
+}  // extern "C"

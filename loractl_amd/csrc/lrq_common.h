@@ -1,0 +1,127 @@
+// Shared device helpers for the gfx950 kernels: bf16 packing, int4/fp8
+// decode, and the matrix-core (MFMA) fragment layouts used by every GEMM.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+#define LRQ_DEV __device__ __forceinline__
+
+// ---------------------------------------------------------------- bf16
+// Round-to-nearest-even f32 -> bf16 bits for two values packed (lo, hi).
+// On gfx950 this lowers to v_cvt_pk_bf16_f32.
+LRQ_DEV uint32_t pack_bf16x2(float lo, float hi) {
+  __bf16 a = (__bf16)lo;
+  __bf16 b = (__bf16)hi;
+  uint16_t ua = __builtin_bit_cast(uint16_t, a);
+  uint16_t ub = __builtin_bit_cast(uint16_t, b);
+  return (uint32_t)ua | ((uint32_t)ub << 16);
+}
+
+LRQ_DEV float bf16_lo(uint32_t v) { return __builtin_bit_cast(float, v << 16); }
+LRQ_DEV float bf16_hi(uint32_t v) { return __builtin_bit_cast(float, v & 0xffff0000u); }
+
+LRQ_DEV uint16_t f32_to_bf16_bits(float f) {
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
+}
+
+// ---------------------------------------------------------------- int4
+// One dword holds 8 nibbles (k = 0..7 of a run: byte j = k 2j | 2j+1 << 4),
+// each q+8. Dequantize all 8 to f32 as fma(u, s, -8s) == RN((u-8)*s) ==
+// RN(q*s), i.e. bit-identical to the f32 product q*s, then round to bf16.
+// out[0..3] are bf16 pairs (k0,k1) (k2,k3) (k4,k5) (k6,k7).
+LRQ_DEV void dequant8_int4_f32(uint32_t w, float s, float f[8]) {
+  const float nb = -8.0f * s;
+  const uint32_t lo = w & 0x0f0f0f0fu;         // k = 0,2,4,6 in bytes 0..3
+  const uint32_t hi = (w >> 4) & 0x0f0f0f0fu;  // k = 1,3,5,7
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    f[2 * j] = __builtin_fmaf((float)((lo >> (8 * j)) & 0xffu), s, nb);
+    f[2 * j + 1] = __builtin_fmaf((float)((hi >> (8 * j)) & 0xffu), s, nb);
+  }
+}
+
+LRQ_DEV u32x4 dequant8_int4_bf16(uint32_t w, float s) {
+  float f[8];
+  dequant8_int4_f32(w, s, f);
+  u32x4 o;
+  o[0] = pack_bf16x2(f[0], f[1]);
+  o[1] = pack_bf16x2(f[2], f[3]);
+  o[2] = pack_bf16x2(f[4], f[5]);
+  o[3] = pack_bf16x2(f[6], f[7]);
+  return o;
+}
+
+// ---------------------------------------------------------------- fp8 e4m3fn
+// Exact e4m3fn -> f32 (the value of src/fp8.rs:45-56's table): subnormal
+// m*2^-9, normal (1+m/8)*2^(e-7), NaN at |b| == 0x7f, no infinities.
+LRQ_DEV float fp8_e4m3fn_to_f32(uint32_t b) {
+  const uint32_t sign = (b & 0x80u) << 24;
+  const uint32_t e = (b >> 3) & 0xfu;
+  const uint32_t m = b & 7u;
+  float v;
+  if (e == 0) {
+    v = (float)m * 0.001953125f;  // m * 2^-9, exact
+    v = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, v) | sign);
+  } else if (e == 15 && m == 7) {
+    v = __builtin_bit_cast(float, sign | 0x7fc00000u);
+  } else {
+    v = __builtin_bit_cast(float, sign | ((e + 120u) << 23) | (m << 20));
+  }
+  return v;
+}
+
+// Four e4m3fn bytes -> four f32 with the gfx950 converter (OCP e4m3fn:
+// exact values, NaN at 0x7f/0xff). f[j] is byte j.
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+LRQ_DEV void fp8x4_to_f32(uint32_t w, float f[4]) {
+  const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+  const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+  f[0] = lo[0];
+  f[1] = lo[1];
+  f[2] = hi[0];
+  f[3] = hi[1];
+}
+
+// Four e4m3fn bytes -> four bf16 (exact: 3 mantissa bits fit bf16's 7).
+// Returns two dwords of bf16 pairs (byte 0 in the low half of dword 0).
+LRQ_DEV u32x2 fp8x4_to_bf16(uint32_t w) {
+  float f[4];
+  fp8x4_to_f32(w, f);
+  u32x2 o;
+  o[0] = pack_bf16x2(f[0], f[1]);
+  o[1] = pack_bf16x2(f[2], f[3]);
+  return o;
+}
+
+// ---------------------------------------------------------------- MFMA
+// v_mfma_f32_32x32x16_bf16: A-role lane l supplies row (l & 31) and the 8
+// reduction values at offset 8 * (l >> 5) of the 16-wide k slice; B-role
+// lane l supplies column (l & 31) with the same k mapping. Accumulator
+// element v of lane l is C[row = 8*(v>>2) + 4*(l>>5) + (v&3)][col = l & 31].
+LRQ_DEV f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// v_mfma_f32_16x16x32_bf16: A-role lane l supplies row (l & 15), 8 values at
+// k offset 8 * (l >> 4); B-role likewise for column (l & 15). Accumulator
+// element v of lane l is C[row = 4*(l>>4) + v][col = l & 15].
+LRQ_DEV f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+LRQ_DEV bf16x8 as_bf16x8(const u32x4& v) { return __builtin_bit_cast(bf16x8, v); }
+
+LRQ_DEV u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+LRQ_DEV void st16(void* p, const u32x4& v) { *reinterpret_cast<u32x4*>(p) = v; }
+
+// 8 consecutive bf16 (16 bytes) from global with a validity predicate.
+LRQ_DEV u32x4 ld16_pred(const void* p, bool ok) {
+  u32x4 z = {0u, 0u, 0u, 0u};
+  return ok ? ld16(p) : z;
+}

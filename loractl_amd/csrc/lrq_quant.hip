@@ -1,0 +1,237 @@
+// Weight-format kernels: int4 block quantization (src/quant.rs:74-82 closed
+// form), fp8 e4m3fn repack (reference/fp8_reference.py:83-91), and the
+// dequantize kernels that expose the f32 values (src/quant.rs:232,
+// src/fp8.rs:306-318) and the bf16 matrix-core operands.
+//
+// All of these are HBM-bound byte/integer work: one thread per 8-value run,
+// 16-byte stores where the layout allows it, no LDS.
+#include "lrq_common.h"
+#include "lrq_kernels.h"
+
+// ------------------------------------------------------------------ int4 quantize
+// One thread per (row, 32-value half-block); a block of `group` values is
+// covered by group/32 consecutive threads that reduce absmax with lane
+// shuffles (group/32 <= 64 lanes, a power of two or not: a plain loop over
+// the partner lanes keeps it exact).
+__global__ void __launch_bounds__(256) k_quantize_int4(const float* __restrict__ w, int64_t n,
+                                                       int64_t k, int g, uint8_t* __restrict__ packed,
+                                                       float* __restrict__ scales) {
+  const int64_t runs_per_row = k / 32;
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (tid >= n * runs_per_row) return;
+  const int64_t row = tid / runs_per_row;
+  const int64_t run = tid % runs_per_row;
+  const float* src = w + row * k + run * 32;
+  float v[32];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 32; i += 4) {
+    f32x4 t = *reinterpret_cast<const f32x4*>(src + i);
+    v[i] = t[0]; v[i + 1] = t[1]; v[i + 2] = t[2]; v[i + 3] = t[3];
+  }
+#pragma unroll
+  for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  // absmax over the whole block: the block's runs are consecutive tids,
+  // hence consecutive lanes of one wavefront (g/32 divides... g is a multiple
+  // of 32 and rows start at run 0, but a block may straddle two wavefronts
+  // when g/32 does not divide 64; the host restricts g/32 to a divisor of 64).
+  const int rpb = g / 32;
+  if (rpb > 1) {
+    const int lane = threadIdx.x & 63;
+    const int first = lane - (int)(run % rpb);
+    float m = 0.0f;
+    for (int j = 0; j < rpb; ++j) m = fmaxf(m, __shfl(amax, first + j, 64));
+    amax = m;
+  }
+  const float s = amax / 7.0f;  // correctly rounded f32 division
+  if (run % rpb == 0) scales[row * (k / g) + run / rpb] = s;
+  uint32_t out[4];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      int q = 0;
+      if (s != 0.0f) {
+        float r = roundf(v[d * 8 + j] / s);  // half away from zero
+        r = fminf(fmaxf(r, -7.0f), 7.0f);
+        q = (int)r;
+      }
+      word |= (uint32_t)(q + 8) << (4 * j);
+    }
+    out[d] = word;
+  }
+  u32x4 o = {out[0], out[1], out[2], out[3]};
+  st16(packed + row * (k / 2) + run * 16, o);
+}
+
+// ------------------------------------------------------------------ fp8 quantize
+// Exact RNE e4m3fn encode of an f32 that is already divided by the scale.
+__device__ __forceinline__ uint32_t fp8_encode_rne(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return sign | 0x7fu;     // NaN
+  if (a >= 0x43e00000u) return sign | 0x7eu;    // |x| >= 448: saturate
+  if (a < 0x3c800000u) {                        // |x| < 2^-6: subnormal grid 2^-9
+    const float ax = __builtin_bit_cast(float, a) * 512.0f;  // exact
+    const float r = __builtin_rintf(ax);                      // RNE
+    return sign | (uint32_t)r;                                // 8 rolls into 0x08
+  }
+  // normal: keep 3 mantissa bits with RNE on the f32 bit pattern
+  const uint32_t lsb = (a >> 20) & 1u;
+  const uint32_t rounded = a + 0x7ffffu + lsb;
+  const uint32_t e = (rounded >> 23) - 120u;  // fp8 exponent field
+  const uint32_t m = (rounded >> 20) & 7u;
+  uint32_t code = (e << 3) | m;
+  if (code > 0x7eu) code = 0x7eu;
+  return sign | code;
+}
+
+// Per-row (or whole-tensor) amax -> scale. One block per row for per-channel;
+// for a scalar scale a first pass writes per-row amax and a second block folds.
+__global__ void __launch_bounds__(256) k_rowabsmax(const float* __restrict__ w, int64_t k,
+                                                   float* __restrict__ out) {
+  const int64_t row = blockIdx.x;
+  const float* src = w + row * k;
+  float m = 0.0f;
+  for (int64_t i = threadIdx.x; i < k; i += blockDim.x) m = fmaxf(m, fabsf(src[i]));
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  __shared__ float red[4];
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) out[row] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+__global__ void __launch_bounds__(256) k_fp8_scales(float* __restrict__ amax, int64_t n,
+                                                    int per_channel, float* __restrict__ scales) {
+  if (per_channel) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+      float s = amax[i] / 448.0f;
+      scales[i] = s < 1e-12f ? 1e-12f : s;
+    }
+  } else if (blockIdx.x == 0) {
+    float m = 0.0f;
+    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) m = fmaxf(m, amax[i]);
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    __shared__ float red[4];
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float s = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])) / 448.0f;
+      scales[0] = s < 1e-12f ? 1e-12f : s;
+    }
+  }
+}
+
+__global__ void __launch_bounds__(256) k_fp8_encode(const float* __restrict__ w, int64_t n, int64_t k,
+                                                    int per_channel, const float* __restrict__ scales,
+                                                    uint8_t* __restrict__ out) {
+  // one thread per 4 consecutive values (k % 32 == 0 so rows hold whole runs)
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = n * k / 4;
+  if (tid >= total) return;
+  const int64_t row = (tid * 4) / k;
+  const float s = per_channel ? scales[row] : scales[0];
+  f32x4 v = *reinterpret_cast<const f32x4*>(w + tid * 4);
+  uint32_t word = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) word |= fp8_encode_rne(v[j] / s) << (8 * j);
+  reinterpret_cast<uint32_t*>(out)[tid] = word;
+}
+
+// ------------------------------------------------------------------ dequantize
+// int4 -> f32 (bit-exact q*s) or bf16 operand; one thread per 8-value run.
+template <bool BF16>
+__global__ void __launch_bounds__(256) k_dequant_int4(const uint8_t* __restrict__ packed,
+                                                      const float* __restrict__ scales, int64_t n,
+                                                      int64_t k, int g, void* __restrict__ out) {
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t runs = n * (k / 8);
+  if (tid >= runs) return;
+  const int64_t row = tid / (k / 8);
+  const int64_t kk = (tid % (k / 8)) * 8;
+  const uint32_t word = reinterpret_cast<const uint32_t*>(packed + row * (k / 2))[kk / 8];
+  const float s = scales[row * (k / g) + kk / g];
+  if (BF16) {
+    st16(reinterpret_cast<uint16_t*>(out) + row * k + kk, dequant8_int4_bf16(word, s));
+  } else {
+    float f[8];
+    dequant8_int4_f32(word, s, f);
+    float* o = reinterpret_cast<float*>(out) + row * k + kk;
+    f32x4 a = {f[0], f[1], f[2], f[3]};
+    f32x4 b = {f[4], f[5], f[6], f[7]};
+    *reinterpret_cast<f32x4*>(o) = a;
+    *reinterpret_cast<f32x4*>(o + 4) = b;
+  }
+}
+
+// fp8 -> f32 (LUT value * scale, one f32 rounding) or the unscaled bf16 operand.
+template <bool BF16>
+__global__ void __launch_bounds__(256) k_dequant_fp8(const uint8_t* __restrict__ bytes,
+                                                     const float* __restrict__ scales, int64_t n,
+                                                     int64_t k, int per_channel, void* __restrict__ out) {
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t quads = n * k / 4;
+  if (tid >= quads) return;
+  const uint32_t word = reinterpret_cast<const uint32_t*>(bytes)[tid];
+  if (BF16) {
+    reinterpret_cast<u32x2*>(out)[tid] = fp8x4_to_bf16(word);
+  } else {
+    const int64_t row = (tid * 4) / k;
+    const float s = per_channel ? scales[row] : scales[0];
+    f32x4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = fp8_e4m3fn_to_f32((word >> (8 * j)) & 0xffu) * s;
+    reinterpret_cast<f32x4*>(out)[tid] = o;
+  }
+}
+
+// ------------------------------------------------------------------ launchers
+static inline unsigned blocks_for(int64_t items, int per_block) {
+  return (unsigned)((items + per_block - 1) / per_block);
+}
+
+hipError_t launch_quantize_int4(hipStream_t st, const float* w, int64_t n, int64_t k, int g,
+                                uint8_t* packed, float* scales) {
+  const int64_t items = n * (k / 32);
+  if (items == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_quantize_int4, dim3(blocks_for(items, 256)), dim3(256), 0, st, w, n, k, g,
+                     packed, scales);
+  return hipGetLastError();
+}
+
+hipError_t launch_quantize_fp8(hipStream_t st, const float* w, int64_t n, int64_t k,
+                               int per_channel, uint8_t* bytes, float* scales, float* amax_ws) {
+  if (n == 0 || k == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_rowabsmax, dim3((unsigned)n), dim3(256), 0, st, w, k, amax_ws);
+  hipLaunchKernelGGL(k_fp8_scales, dim3(per_channel ? blocks_for(n, 256) : 1), dim3(256), 0, st,
+                     amax_ws, n, per_channel, scales);
+  hipLaunchKernelGGL(k_fp8_encode, dim3(blocks_for(n * k / 4, 256)), dim3(256), 0, st, w, n, k,
+                     per_channel, scales, bytes);
+  return hipGetLastError();
+}
+
+hipError_t launch_dequant(hipStream_t st, const lrq_weight* w, void* out, bool bf16) {
+  const int64_t n = w->n, k = w->k;
+  if (n == 0 || k == 0) return hipSuccess;
+  const uint8_t* d = reinterpret_cast<const uint8_t*>(w->data);
+  if (w->format == LRQ_FMT_INT4) {
+    const int64_t runs = n * (k / 8);
+    if (bf16)
+      hipLaunchKernelGGL(k_dequant_int4<true>, dim3(blocks_for(runs, 256)), dim3(256), 0, st, d,
+                         w->scales, n, k, w->group, out);
+    else
+      hipLaunchKernelGGL(k_dequant_int4<false>, dim3(blocks_for(runs, 256)), dim3(256), 0, st, d,
+                         w->scales, n, k, w->group, out);
+  } else {
+    const int64_t quads = n * k / 4;
+    if (bf16)
+      hipLaunchKernelGGL(k_dequant_fp8<true>, dim3(blocks_for(quads, 256)), dim3(256), 0, st, d,
+                         w->scales, n, k, w->per_channel, out);
+    else
+      hipLaunchKernelGGL(k_dequant_fp8<false>, dim3(blocks_for(quads, 256)), dim3(256), 0, st, d,
+                         w->scales, n, k, w->per_channel, out);
+  }
+  return hipGetLastError();
+}

@@ -1,0 +1,260 @@
+"""Torch-facing calls into libloractl_rocm.so.
+
+PyTorch is only the device-memory and stream plumbing here: tensors are
+allocated by torch on the GPU and their device pointers are handed to the C
+ABI, which launches the hand-written gfx950 kernels on torch's current
+stream. There is no CPU or eager-torch fallback: a missing library, a CPU
+tensor or an unsupported shape raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import _lib as L
+
+_tls = threading.local()
+
+
+class Context:
+    """One lrq_ctx per (thread, device); follows torch's current stream."""
+
+    def __init__(self, device: int):
+        self.lib = L.load()
+        h = ctypes.c_void_p()
+        rc = self.lib.lrq_create(device, ctypes.byref(h))
+        if rc != 0:
+            raise L.LrqError(rc, f"lrq_create(device={device}) failed")
+        self.h = h
+        self.device = device
+
+    def __del__(self):
+        try:
+            if getattr(self, "h", None):
+                self.lib.lrq_destroy(self.h)
+        except Exception:
+            pass
+
+    def check(self, rc: int, what: str):
+        if rc != 0:
+            msg = self.lib.lrq_last_error(self.h).decode(errors="replace")
+            raise L.LrqError(rc, f"{what}: {msg}")
+
+    def bind_stream(self):
+        s = torch.cuda.current_stream(self.device).cuda_stream
+        self.check(self.lib.lrq_set_stream(self.h, ctypes.c_void_p(s)), "lrq_set_stream")
+
+
+def context(device: Optional[int] = None) -> Context:
+    if device is None:
+        device = torch.cuda.current_device()
+    ctxs = getattr(_tls, "ctxs", None)
+    if ctxs is None:
+        ctxs = _tls.ctxs = {}
+    c = ctxs.get(device)
+    if c is None:
+        c = ctxs[device] = Context(device)
+    c.bind_stream()
+    return c
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _need(t: torch.Tensor, dtype: torch.dtype, name: str, shape=None):
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor (no CPU fallback)")
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} must have shape {tuple(shape)}, got {tuple(t.shape)}")
+
+
+@dataclass
+class PackedWeight:
+    """A frozen base weight in device memory, file layout [d_out, d_in].
+
+    int4: ``data`` uint8 [n, k/2] (nibbles q+8, low nibble = even k) and
+    ``scales`` f32 [n, k/group]. fp8: ``data`` uint8 e4m3fn [n, k] and
+    ``scales`` f32 [n] (per_channel) or [1]. ``bias`` optional f32 [n].
+    """
+
+    fmt: int
+    n: int
+    k: int
+    data: torch.Tensor
+    scales: torch.Tensor
+    group: int = 0
+    per_channel: bool = False
+    bias: Optional[torch.Tensor] = None
+
+    def desc(self) -> L.LrqWeight:
+        return L.LrqWeight(
+            format=self.fmt,
+            group=self.group,
+            n=self.n,
+            k=self.k,
+            data=self.data.data_ptr(),
+            scales=self.scales.data_ptr(),
+            per_channel=int(self.per_channel),
+            reserved=0,
+            bias=None if self.bias is None else self.bias.data_ptr(),
+        )
+
+    @property
+    def device(self) -> torch.device:
+        return self.data.device
+
+    def with_bias(self, bias: Optional[torch.Tensor]) -> "PackedWeight":
+        return PackedWeight(self.fmt, self.n, self.k, self.data, self.scales, self.group,
+                            self.per_channel, bias)
+
+
+# ------------------------------------------------------------------ formats
+def quantize_int4(w: torch.Tensor, group: int) -> PackedWeight:
+    """quantize_linear_weight at Q4S (src/quant.rs:74-82) on the GPU."""
+    _need(w, torch.float32, "w")
+    n, k = w.shape
+    ctx = context(w.device.index)
+    packed = torch.empty((n, k // 2), dtype=torch.uint8, device=w.device)
+    scales = torch.empty((n, max(k // group, 0) if group > 0 else 0), dtype=torch.float32, device=w.device)
+    ctx.check(ctx.lib.lrq_quantize_int4(ctx.h, _ptr(w), n, k, group, _ptr(packed), _ptr(scales)),
+              "lrq_quantize_int4")
+    return PackedWeight(L.LRQ_FMT_INT4, n, k, packed, scales, group=group)
+
+
+def quantize_fp8(w: torch.Tensor, per_channel: bool) -> PackedWeight:
+    """fp8 e4m3fn repack (reference/fp8_reference.py:83-91) on the GPU."""
+    _need(w, torch.float32, "w")
+    n, k = w.shape
+    ctx = context(w.device.index)
+    data = torch.empty((n, k), dtype=torch.uint8, device=w.device)
+    scales = torch.empty((n if per_channel else 1,), dtype=torch.float32, device=w.device)
+    ctx.check(ctx.lib.lrq_quantize_fp8(ctx.h, _ptr(w), n, k, int(per_channel), _ptr(data), _ptr(scales)),
+              "lrq_quantize_fp8")
+    return PackedWeight(L.LRQ_FMT_FP8, n, k, data, scales, per_channel=per_channel)
+
+
+def dequant(w: PackedWeight) -> torch.Tensor:
+    """f32 [n, k] dequantized weight (bit-exact with the CPU definition)."""
+    ctx = context(w.device.index)
+    out = torch.empty((w.n, w.k), dtype=torch.float32, device=w.device)
+    d = w.desc()
+    ctx.check(ctx.lib.lrq_dequant(ctx.h, ctypes.byref(d), _ptr(out)), "lrq_dequant")
+    return out
+
+
+def dequant_bf16(w: PackedWeight) -> torch.Tensor:
+    """The bf16 matrix-core operand (bf16(q*s) for int4, the fp8 value for fp8)."""
+    ctx = context(w.device.index)
+    out = torch.empty((w.n, w.k), dtype=torch.bfloat16, device=w.device)
+    d = w.desc()
+    ctx.check(ctx.lib.lrq_dequant_bf16(ctx.h, ctypes.byref(d), _ptr(out)), "lrq_dequant_bf16")
+    return out
+
+
+# ------------------------------------------------------------------ linear
+def quant_matmul_t(x: torch.Tensor, w: PackedWeight) -> torch.Tensor:
+    """y[m, n] = x[m, k] . dequant(w)^T (+ bias): QuantBackend::quant_matmul_t."""
+    _need(x, torch.bfloat16, "x")
+    m = x.shape[0]
+    if x.dim() != 2 or x.shape[1] != w.k:
+        raise ValueError(f"x must be [m, {w.k}], got {tuple(x.shape)}")
+    ctx = context(x.device.index)
+    y = torch.empty((m, w.n), dtype=torch.bfloat16, device=x.device)
+    d = w.desc()
+    ctx.check(ctx.lib.lrq_quant_matmul_t(ctx.h, ctypes.byref(d), _ptr(x), m, _ptr(y)), "lrq_quant_matmul_t")
+    return y
+
+
+def quant_matmul_t_bwd(dy: torch.Tensor, w: PackedWeight) -> torch.Tensor:
+    """dx[m, k] = dy[m, n] . dequant(w): QuantMatmulT::backward."""
+    _need(dy, torch.bfloat16, "dy")
+    m = dy.shape[0]
+    if dy.dim() != 2 or dy.shape[1] != w.n:
+        raise ValueError(f"dy must be [m, {w.n}], got {tuple(dy.shape)}")
+    ctx = context(dy.device.index)
+    dx = torch.empty((m, w.k), dtype=torch.bfloat16, device=dy.device)
+    d = w.desc()
+    ctx.check(ctx.lib.lrq_quant_matmul_t_bwd(ctx.h, ctypes.byref(d), _ptr(dy), m, _ptr(dx)),
+              "lrq_quant_matmul_t_bwd")
+    return dx
+
+
+def lora_fwd(x: torch.Tensor, w: PackedWeight, a: torch.Tensor, b: torch.Tensor, scaling: float,
+             y: Optional[torch.Tensor] = None, t: Optional[torch.Tensor] = None):
+    """Fused site forward. x bf16 [m,k], a bf16 [k,r], b bf16 [r,n] -> (y [m,n], t [m,r])."""
+    _need(x, torch.bfloat16, "x")
+    m = x.shape[0]
+    r = a.shape[1]
+    _need(a, torch.bfloat16, "A", (w.k, r))
+    _need(b, torch.bfloat16, "B", (r, w.n))
+    ctx = context(x.device.index)
+    if y is None:
+        y = torch.empty((m, w.n), dtype=torch.bfloat16, device=x.device)
+    if t is None:
+        t = torch.empty((m, r), dtype=torch.bfloat16, device=x.device)
+    d = w.desc()
+    ctx.check(ctx.lib.lrq_lora_fwd(ctx.h, ctypes.byref(d), _ptr(x), m, _ptr(a), _ptr(b), r,
+                                   float(scaling), _ptr(y), _ptr(t)), "lrq_lora_fwd")
+    return y, t
+
+
+def lora_bwd(x: torch.Tensor, dy: torch.Tensor, w: PackedWeight, a: torch.Tensor, b: torch.Tensor,
+             scaling: float, t: torch.Tensor, need_dx: bool = True, need_da: bool = True,
+             need_db: bool = True, out=None):
+    """Fused site backward -> (dx bf16 [m,k] | None, dA f32 [k,r] | None, dB f32 [r,n] | None)."""
+    _need(dy, torch.bfloat16, "dy")
+    _need(x, torch.bfloat16, "x")
+    _need(t, torch.bfloat16, "t")
+    m = dy.shape[0]
+    r = a.shape[1]
+    _need(a, torch.bfloat16, "A", (w.k, r))
+    _need(b, torch.bfloat16, "B", (r, w.n))
+    ctx = context(dy.device.index)
+    if out is not None:
+        dx, da, db = out
+    else:
+        dx = torch.empty((m, w.k), dtype=torch.bfloat16, device=dy.device) if need_dx else None
+        da = torch.empty((w.k, r), dtype=torch.float32, device=dy.device) if need_da else None
+        db = torch.empty((r, w.n), dtype=torch.float32, device=dy.device) if need_db else None
+    d = w.desc()
+    ctx.check(ctx.lib.lrq_lora_bwd(ctx.h, ctypes.byref(d), _ptr(x), _ptr(dy), m, _ptr(a), _ptr(b), r,
+                                   float(scaling), _ptr(t), _ptr(dx), _ptr(da), _ptr(db)), "lrq_lora_bwd")
+    return dx, da, db
+
+
+# ------------------------------------------------------------------ profiling
+def profile_enable(on: bool, device: Optional[int] = None):
+    ctx = context(device)
+    ctx.check(ctx.lib.lrq_profile_enable(ctx.h, int(on)), "lrq_profile_enable")
+
+
+def profile_reset(device: Optional[int] = None):
+    ctx = context(device)
+    ctx.check(ctx.lib.lrq_profile_reset(ctx.h), "lrq_profile_reset")
+
+
+def profile_read(device: Optional[int] = None) -> dict:
+    """{kernel name: (total ms, launches)} for every kernel id."""
+    ctx = context(device)
+    out = {}
+    for kid in range(ctx.lib.lrq_profile_count()):
+        ms = ctypes.c_double()
+        n = ctypes.c_int64()
+        ctx.check(ctx.lib.lrq_profile_read(ctx.h, kid, ctypes.byref(ms), ctypes.byref(n)), "lrq_profile_read")
+        out[ctx.lib.lrq_profile_name(kid).decode()] = (ms.value, n.value)
+    return out
+
+
+def reserve(m: int, n: int, k: int, r: int, device: Optional[int] = None):
+    ctx = context(device)
+    ctx.check(ctx.lib.lrq_reserve(ctx.h, m, n, k, r), "lrq_reserve")

@@ -1,0 +1,109 @@
+"""Bit-exact parity of the GPU weight-format kernels with the CPU oracle:
+int4 quantize/pack/dequant and fp8 e4m3fn encode/decode."""
+
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from gpu_helpers import rng
+from loractl_amd import device as D
+from loractl_amd._lib import LrqError
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def _int4_case(N, K, g, seed):
+    w = (rng(seed).standard_normal((N, K)) * 0.5).astype(np.float32)
+    if N > 2 and K >= 64:
+        w[1, :g] = 0.0                          # an all-zero block
+        w[2, :32] = 0.0
+        w[2, :6] = [7.0, 2.5, -2.5, 0.5, -0.5, 6.5]  # exact .5 ties at scale 1
+    return w
+
+
+@pytest.mark.parametrize("N,K,g", [(8, 64, 32), (40, 96, 32), (64, 256, 32), (128, 512, 64), (72, 1024, 128),
+                                   (3, 2048, 2048)])
+def test_quantize_int4_bit_exact(cuda, N, K, g):
+    w = _int4_case(N, K, g, seed=N + K)
+    wq = D.quantize_int4(torch.from_numpy(w).to(cuda), g)
+    p_ref, s_ref = O.quantize_int4_packed(w, g)
+    assert np.array_equal(wq.data.cpu().numpy(), p_ref)
+    assert np.array_equal(wq.scales.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+    dq = D.dequant(wq).cpu().numpy()
+    dq_ref = O.dequant_int4(p_ref, s_ref, K, g)
+    assert np.array_equal(dq.view(np.uint32), dq_ref.view(np.uint32))
+    bf = D.dequant_bf16(wq).view(torch.int16).cpu().numpy().view(np.uint16)
+    assert np.array_equal(bf, O.bf16_bits(dq_ref))
+
+
+def test_int4_reference_golden_on_gpu(cuda):
+    """quant_int4_golden.json dequantized on the GPU equals the torch golden."""
+    g = json.load(open(os.path.join(GOLD, "quant_int4_golden.json")))
+    w = np.array(g["w"], np.float32)
+    wq = D.quantize_int4(torch.from_numpy(w).to(cuda), 32)
+    assert np.array_equal(D.dequant(wq).cpu().numpy(), np.array(g["dq"], np.float32))
+
+
+def test_quantize_int4_rejects_bad_blocks(cuda):
+    with pytest.raises(LrqError, match="LRQ_EINVAL"):
+        D.quantize_int4(torch.zeros(4, 96, device=cuda), 64)
+    with pytest.raises(LrqError, match="LRQ_EINVAL"):
+        D.quantize_int4(torch.zeros(4, 96, device=cuda), 48)
+
+
+@pytest.mark.parametrize("per_channel", [False, True])
+def test_quantize_fp8_bit_exact(cuda, per_channel):
+    w = (rng(7).standard_normal((48, 160)) * 0.3).astype(np.float32)
+    w[3] = 0.0  # all-zero row: scale clamps to 1e-12
+    w[5, 7] = -4.2e-8
+    pw = D.quantize_fp8(torch.from_numpy(w).to(cuda), per_channel)
+    b_ref, s_ref = O.fp8_quantize(w, per_channel)
+    assert np.array_equal(pw.scales.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+    assert np.array_equal(pw.data.cpu().numpy(), b_ref)
+
+
+def test_fp8_encoder_reproduces_reference_fixture_pairs_on_gpu(cuda):
+    z = np.load(os.path.join(GOLD, "fp8_pairs.npz"))
+    for n in [str(v) for v in z["names"]]:
+        key = n.split("=")[0]
+        w, want_b, want_s = z[key + "_w"], z[key + "_bytes"], z[key + "_scale"]
+        if w.shape[1] % 4:
+            continue
+        pw = D.quantize_fp8(torch.from_numpy(np.ascontiguousarray(w)).to(cuda), want_s.size > 1)
+        assert np.array_equal(pw.scales.cpu().numpy().view(np.uint32), want_s.view(np.uint32)), n
+        assert np.array_equal(pw.data.cpu().numpy(), want_b), n
+
+
+def test_fp8_decode_all_256_bytes(cuda):
+    """Every e4m3fn byte decodes to the torch LUT golden (bf16 operand and f32 dequant)."""
+    lut = json.load(open(os.path.join(GOLD, "fp8_lut_golden.json")))["lut"]
+    data = np.arange(256, dtype=np.uint8).reshape(8, 32)
+    scale = np.ones(8, np.float32)
+    pw = D.PackedWeight(D.L.LRQ_FMT_FP8, 8, 32, torch.from_numpy(data).to(cuda),
+                        torch.from_numpy(scale).to(cuda), per_channel=True)
+    f = D.dequant(pw).cpu().numpy().reshape(-1)
+    bf = D.dequant_bf16(pw).float().cpu().numpy().reshape(-1)
+    for b, want in enumerate(lut):
+        if want is None:
+            assert np.isnan(f[b]) and np.isnan(bf[b]), hex(b)
+        else:
+            assert np.float32(want).view(np.uint32) == f[b].view(np.uint32), hex(b)
+            assert np.float32(want).view(np.uint32) == bf[b].view(np.uint32), hex(b)
+
+
+@pytest.mark.parametrize("case", ["scalar", "per_channel", "scale_shape_one"])
+def test_fp8_dequant_golden_on_gpu(cuda, case):
+    """fp8_dequant_golden.json ([5,3] weights) embedded in a [5,32] weight."""
+    c = json.load(open(os.path.join(GOLD, "fp8_dequant_golden.json")))[case]
+    b = np.zeros((5, 32), np.uint8)
+    b[:, :3] = np.array(c["weight_bytes"], np.uint8).reshape(5, 3)
+    scale = np.array(c["scale"], np.float32).reshape(-1)
+    pw = D.PackedWeight(D.L.LRQ_FMT_FP8, 5, 32, torch.from_numpy(b).to(cuda), torch.from_numpy(scale).to(cuda),
+                        per_channel=scale.size > 1)
+    out = D.dequant(pw).cpu().numpy()[:, :3].reshape(-1)
+    assert np.array_equal(out.view(np.uint32), np.array(c["expected"], np.float32).view(np.uint32))

@@ -1,0 +1,184 @@
+"""Parity of the fused quantized LoRA linear (forward and backward) on the GPU,
+through the C ABI, against the CPU oracle on identical seeded inputs
+(tolerance: rel_deviation <= 1e-2 and cosine >= 0.999 for bf16 outputs),
+and at BASELINE sizes against a torch fp32 reference built from the
+bit-exact dequantized weight."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from gpu_helpers import case_inputs, check, to_dev
+from loractl_amd import device as D
+from loractl_amd._lib import LrqError
+
+pytestmark = pytest.mark.gpu
+
+# (M, K, N, group): ragged M, K % 64 == 32, N not a tile multiple, exact tiles
+SHAPES = [(1, 64, 64, 32), (5, 64, 8, 32), (37, 96, 72, 32), (130, 192, 520, 64), (256, 256, 256, 64),
+          (300, 320, 264, 64), (513, 512, 392, 128)]
+
+
+def _weight(w, fmt, g, dev, per_channel=True):
+    t = torch.from_numpy(w).to(dev)
+    if fmt == "int4":
+        wq = D.quantize_int4(t, g)
+        p, s = O.quantize_int4_packed(w, g)
+        return wq, O.dequant_int4(p, s, w.shape[1], g)
+    wq = D.quantize_fp8(t, per_channel)
+    b, s = O.fp8_quantize(w, per_channel)
+    return wq, O.fp8_dequant(b, s)
+
+
+@pytest.mark.parametrize("M,K,N,g", SHAPES)
+@pytest.mark.parametrize("fmt", ["int4", "fp8"])
+def test_quant_matmul_t_and_bwd(cuda, fmt, M, K, N, g):
+    w, x, _, _, dy = case_inputs(M, K, N, 0, seed=M + N)
+    wq, wdq = _weight(w, fmt, g, cuda)
+    y = D.quant_matmul_t(to_dev(x, cuda), wq)
+    dx = D.quant_matmul_t_bwd(to_dev(dy, cuda), wq)
+    y_ref, _ = O.linear_fwd(x, wdq)
+    dx_ref, _, _ = O.linear_bwd(x, wdq, None, None, 1.0, dy)
+    check(f"{fmt} y", y, y_ref)
+    check(f"{fmt} dx", dx, dx_ref)
+
+
+def test_quant_matmul_t_reference_golden(cuda):
+    """quant_int4_golden.json: y = x . dq^T on the GPU within bf16 rounding."""
+    import json, os
+    g = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "quant_int4_golden.json")))
+    w = np.array(g["w"], np.float32)
+    x = np.array(g["x"], np.float32)
+    wq = D.quantize_int4(torch.from_numpy(w).to(cuda), 32)
+    y = D.quant_matmul_t(to_dev(x, cuda), wq)
+    check("golden y", y, np.array(g["y"], np.float32))
+
+
+@pytest.mark.parametrize("M,K,N,g", SHAPES)
+@pytest.mark.parametrize("r", [16, 32])
+def test_lora_fwd_bwd_int4(cuda, M, K, N, g, r):
+    w, x, a, b, dy = case_inputs(M, K, N, r, seed=3 * M + N + r)
+    wq, wdq = _weight(w, "int4", g, cuda)
+    s = 16.0 / r
+    xd, ad, bd = to_dev(x, cuda), to_dev(a, cuda), to_dev(b, cuda)
+    y, t = D.lora_fwd(xd, wq, ad, bd, s)
+    dx, da, db = D.lora_bwd(xd, to_dev(dy, cuda), wq, ad, bd, s, t)
+    y_ref, t_ref = O.linear_fwd(x, wdq, a, b, s)
+    dx_ref, da_ref, db_ref = O.linear_bwd(x, wdq, a, b, s, dy)
+    check("t", t, t_ref)
+    check("y", y, y_ref)
+    check("dx", dx, dx_ref)
+    check("dA", da, da_ref)
+    check("dB", db, db_ref)
+    # the LoRA term itself (y - base) must be right, not just drowned by the base
+    base = D.quant_matmul_t(xd, wq).float().cpu().numpy()
+    check("y-base", y.float().cpu().numpy() - base, y_ref - O.linear_fwd(x, wdq)[0], tol_rel=0.1, tol_cos=0.99)
+
+
+@pytest.mark.parametrize("r", [1, 3, 8, 17, 64])
+def test_lora_ranks(cuda, r):
+    M, K, N, g = 70, 128, 96, 64
+    w, x, a, b, dy = case_inputs(M, K, N, r, seed=r, b_sigma=0.05)
+    wq, wdq = _weight(w, "int4", g, cuda)
+    s = 2.0
+    xd, ad, bd = to_dev(x, cuda), to_dev(a, cuda), to_dev(b, cuda)
+    y, t = D.lora_fwd(xd, wq, ad, bd, s)
+    dx, da, db = D.lora_bwd(xd, to_dev(dy, cuda), wq, ad, bd, s, t)
+    y_ref, _ = O.linear_fwd(x, wdq, a, b, s)
+    dx_ref, da_ref, db_ref = O.linear_bwd(x, wdq, a, b, s, dy)
+    check("y", y, y_ref)
+    check("dx", dx, dx_ref)
+    check("dA", da, da_ref)
+    check("dB", db, db_ref)
+
+
+@pytest.mark.parametrize("per_channel", [True, False])
+def test_lora_fwd_bwd_fp8(cuda, per_channel):
+    M, K, N, r = 200, 256, 200, 32
+    w, x, a, b, dy = case_inputs(M, K, N, r, seed=17)
+    wq, wdq = _weight(w, "fp8", 0, cuda, per_channel)
+    xd, ad, bd = to_dev(x, cuda), to_dev(a, cuda), to_dev(b, cuda)
+    y, t = D.lora_fwd(xd, wq, ad, bd, 1.0)
+    dx, da, db = D.lora_bwd(xd, to_dev(dy, cuda), wq, ad, bd, 1.0, t)
+    y_ref, _ = O.linear_fwd(x, wdq, a, b, 1.0)
+    dx_ref, da_ref, db_ref = O.linear_bwd(x, wdq, a, b, 1.0, dy)
+    check("y", y, y_ref)
+    check("dx", dx, dx_ref)
+    check("dA", da, da_ref)
+    check("dB", db, db_ref)
+
+
+def test_bias_epilogue(cuda):
+    M, K, N = 33, 128, 64
+    w, x, _, _, _ = case_inputs(M, K, N, 0, seed=5)
+    wq, wdq = _weight(w, "int4", 64, cuda)
+    bias = np.linspace(-1, 1, N).astype(np.float32)
+    wb = wq.with_bias(torch.from_numpy(bias).to(cuda))
+    y = D.quant_matmul_t(to_dev(x, cuda), wb)
+    y_ref, _ = O.linear_fwd(x, wdq, bias=bias)
+    check("y+bias", y, y_ref)
+
+
+def test_zero_b_delta_is_bitwise_no_op(cuda):
+    """lora.rs:262-276 on the fused kernel: B = 0 gives exactly the base output."""
+    M, K, N, r = 64, 256, 128, 16
+    w, x, a, _, _ = case_inputs(M, K, N, r, seed=8)
+    wq, _ = _weight(w, "int4", 64, cuda)
+    xd = to_dev(x, cuda)
+    y, _ = D.lora_fwd(xd, wq, to_dev(a, cuda), torch.zeros(r, N, dtype=torch.bfloat16, device=cuda), 1.0)
+    assert torch.equal(y, D.quant_matmul_t(xd, wq))
+
+
+def test_outputs_are_deterministic(cuda):
+    M, K, N, r = 300, 256, 200, 16
+    w, x, a, b, dy = case_inputs(M, K, N, r, seed=4)
+    wq, _ = _weight(w, "int4", 64, cuda)
+    args = (to_dev(x, cuda), wq, to_dev(a, cuda), to_dev(b, cuda), 1.0)
+    y1, t1 = D.lora_fwd(*args)
+    y2, t2 = D.lora_fwd(*args)
+    g1 = D.lora_bwd(args[0], to_dev(dy, cuda), wq, args[2], args[3], 1.0, t1)
+    g2 = D.lora_bwd(args[0], to_dev(dy, cuda), wq, args[2], args[3], 1.0, t2)
+    assert torch.equal(y1, y2) and torch.equal(t1, t2)
+    for u, v in zip(g1, g2):
+        assert torch.equal(u, v)
+
+
+def test_shape_errors_are_loud(cuda):
+    w = torch.randn(64, 96, device=cuda)
+    wq = D.quantize_int4(w, 32)
+    with pytest.raises(LrqError, match="LRQ_EINVAL"):
+        D.lora_fwd(torch.zeros(4, 96, dtype=torch.bfloat16, device=cuda), wq,
+                   torch.zeros(96, 65, dtype=torch.bfloat16, device=cuda),
+                   torch.zeros(65, 64, dtype=torch.bfloat16, device=cuda), 1.0)
+    bad = D.PackedWeight(wq.fmt, 60, 96, wq.data, wq.scales, group=32)  # d_out % 8 != 0
+    with pytest.raises(LrqError, match="multiple of 8"):
+        D.quant_matmul_t(torch.zeros(4, 96, dtype=torch.bfloat16, device=cuda), bad)
+    with pytest.raises(ValueError):
+        D.quant_matmul_t(torch.zeros(4, 96, dtype=torch.float32, device=cuda), wq)
+
+
+@pytest.mark.parametrize("M,K,N,r,fmt", [(4096, 3072, 12288, 32, "int4"), (1024, 3072, 3072, 16, "int4"),
+                                         (4096, 3072, 12288, 32, "fp8"), (16, 3072, 12288, 32, "int4")])
+def test_baseline_shapes_against_torch_fp32(cuda, M, K, N, r, fmt):
+    """Full BASELINE sizes: the fused kernels vs torch fp32 GEMMs over the
+    same bf16 inputs and the (bit-exact) dequantized weight."""
+    g = torch.Generator(device=cuda).manual_seed(M + N)
+    w = torch.randn(N, K, device=cuda, generator=g) * 0.02
+    wq = D.quantize_int4(w, 64) if fmt == "int4" else D.quantize_fp8(w, True)
+    wdq = D.dequant(wq)
+    x = torch.randn(M, K, device=cuda, generator=g).to(torch.bfloat16)
+    a = ((torch.rand(K, r, device=cuda, generator=g) * 2 - 1) / K ** 0.5).to(torch.bfloat16)
+    b = (torch.randn(r, N, device=cuda, generator=g) * 1e-3).to(torch.bfloat16)
+    dy = torch.randn(M, N, device=cuda, generator=g).to(torch.bfloat16)
+    y, t = D.lora_fwd(x, wq, a, b, 1.0)
+    dx, da, db = D.lora_bwd(x, dy, wq, a, b, 1.0, t)
+    xf, af, bf, dyf = x.float(), a.float(), b.float(), dy.float()
+    t_ref = xf @ af
+    u_ref = dyf @ bf.t()
+    y_ref = xf @ wdq.t() + t_ref @ bf
+    dx_ref = dyf @ wdq + u_ref @ af.t()
+    da_ref = xf.t() @ u_ref
+    db_ref = t_ref.t() @ dyf
+    for name, got, ref in (("y", y, y_ref), ("dx", dx, dx_ref), ("dA", da, da_ref), ("dB", db, db_ref)):
+        check(name, got, ref.cpu().numpy())
