@@ -227,7 +227,8 @@ hipError_t launch_skinny_nt(hipStream_t st, const uint16_t* p, const uint16_t* q
   const int used = (int)((C + c_per - 1) / c_per);
   hipLaunchKernelGGL(k_skinny_nt, dim3((unsigned)((M + 63) / 64), (unsigned)used), dim3(NT), 0, st,
                      p, q, M, C, R, rp, c_per, partial);
-  hipLaunchKernelGGL(k_nt_reduce, dim3(nblocks(ldT * rp)), dim3(NT), 0, st, partial, used, M, ldT,
+  const int64_t ld = outT ? ldT : M;  // without a transposed copy only the M real rows exist
+  hipLaunchKernelGGL(k_nt_reduce, dim3(nblocks(ld * rp)), dim3(NT), 0, st, partial, used, M, ld,
                      rp, R, s, out, outT, out_user, r_user);
   return hipGetLastError();
 }

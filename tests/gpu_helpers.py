@@ -29,7 +29,7 @@ def to_dev(v, dev, dtype=torch.bfloat16):
 
 
 def check(name, got, ref, tol_rel=TOL_REL, tol_cos=TOL_COS):
-    g = got.float().cpu().numpy() if isinstance(got, torch.Tensor) else np.asarray(got, np.float32)
+    g = got.detach().float().cpu().numpy() if isinstance(got, torch.Tensor) else np.asarray(got, np.float32)
     rel = O.rel_deviation(g, ref)
     cos = O.cosine(g, ref) if np.abs(ref).max() > 0 else (1.0 if not np.abs(g).max() else 0.0)
     assert rel <= tol_rel and cos >= tol_cos, f"{name}: rel_dev={rel:.3e} cos={cos:.6f}"
