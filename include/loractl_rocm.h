@@ -78,12 +78,12 @@ typedef struct lrq_weight {
 /* Library version (LRQ_ABI_VERSION). */
 int lrq_version(void);
 
-/* Create a context on HIP device `device`; it owns a stream and a workspace. */
+/* Create a context on HIP device `device`; it owns a workspace and starts
+ * on the device's null stream. */
 int lrq_create(int device, lrq_ctx** out);
 int lrq_destroy(lrq_ctx* ctx);
 
-/* Run subsequent calls on `stream` (a hipStream_t; NULL restores the
- * context's own stream). */
+/* Run subsequent calls on `stream` (a hipStream_t; NULL is the null stream). */
 int lrq_set_stream(lrq_ctx* ctx, void* stream);
 int lrq_sync(lrq_ctx* ctx);
 const char* lrq_last_error(const lrq_ctx* ctx);

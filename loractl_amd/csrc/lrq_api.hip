@@ -15,7 +15,6 @@ void set_num_cus(int n);
 
 struct lrq_ctx {
   int device = 0;
-  hipStream_t own = nullptr;
   hipStream_t stream = nullptr;
   char* ws = nullptr;
   size_t ws_bytes = 0;
@@ -217,11 +216,11 @@ int lrq_create(int device, lrq_ctx** out) {
   lrq_ctx* c = new (std::nothrow) lrq_ctx();
   if (!c) return LRQ_ENOMEM;
   c->device = device;
-  if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking) != hipSuccess) {
+  if (hipSetDevice(device) != hipSuccess) {
     delete c;
     return LRQ_EHIP;
   }
-  c->stream = c->own;
+  c->stream = nullptr;  // the null stream until lrq_set_stream says otherwise
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, device) == hipSuccess) set_num_cus(prop.multiProcessorCount);
   *out = c;
@@ -238,14 +237,13 @@ int lrq_destroy(lrq_ctx* c) {
   }
   for (auto e : c->pool) (void)hipEventDestroy(e);
   if (c->ws) (void)hipFree(c->ws);
-  if (c->own) (void)hipStreamDestroy(c->own);
   delete c;
   return LRQ_OK;
 }
 
 int lrq_set_stream(lrq_ctx* c, void* stream) {
   LRQ_TRY(begin(c));
-  c->stream = stream ? reinterpret_cast<hipStream_t>(stream) : c->own;
+  c->stream = reinterpret_cast<hipStream_t>(stream);  // NULL: the device's null stream
   return LRQ_OK;
 }
 
