@@ -307,46 +307,59 @@ int lrq_dequant_bf16(lrq_ctx* c, const lrq_weight* w, uint16_t* out) {
   return run(c, KID_DEQUANT, "dequant_bf16", [&] { return launch_dequant(c->stream, w, out, true); });
 }
 
+static GemmArgs gemm_args(const lrq_weight* w, bool bwd, const uint16_t* act, int64_t m, uint16_t* out) {
+  GemmArgs g{};
+  g.act = act;
+  g.m = m;
+  g.l = bwd ? w->n : w->k;
+  g.e = bwd ? w->k : w->n;
+  g.wk = w->k;
+  g.wdata = reinterpret_cast<const uint8_t*>(w->data);
+  g.wscale = w->scales;
+  g.group = w->group;
+  g.per_channel = w->per_channel;
+  g.bias = bwd ? nullptr : w->bias;
+  g.out = out;
+  return g;
+}
+
+static int check_gemm(lrq_ctx* c, const lrq_weight* w, int64_t m) {
+  LRQ_TRY(check_weight(c, w, true));
+  if (m < 0) return fail(c, LRQ_EINVAL, "negative token count");
+  if (w->n <= 0 || w->k <= 0)
+    return fail(c, LRQ_EINVAL, "the fused kernels need d_out > 0 and d_in > 0 (got [%lld, %lld])",
+                (long long)w->n, (long long)w->k);
+  return LRQ_OK;
+}
+
 static int fwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t m, const uint16_t* a,
                     const uint16_t* b, int64_t r, float scaling, uint16_t* y, uint16_t* t_out) {
   LRQ_TRY(begin(c));
-  LRQ_TRY(check_weight(c, w, true));
-  if (m < 0) return fail(c, LRQ_EINVAL, "negative token count");
+  LRQ_TRY(check_gemm(c, w, m));
   if (!aligned16(x) || !aligned16(y)) return fail(c, LRQ_EINVAL, "x and y must be 16-byte aligned");
   const bool lora = a != nullptr && b != nullptr && r > 0;
-  if (lora && (r < 1 || r > 64)) return fail(c, LRQ_EINVAL, "rank %lld outside [1, 64]", (long long)r);
-  FwdArgs fa{};
-  fa.x = x;
-  fa.m = m;
-  fa.n = w->n;
-  fa.k = w->k;
-  fa.wdata = reinterpret_cast<const uint8_t*>(w->data);
-  fa.wscale = w->scales;
-  fa.group = w->group;
-  fa.per_channel = w->per_channel;
-  fa.bias = w->bias;
-  fa.y = y;
+  GemmArgs ga = gemm_args(w, false, x, m, y);
   if (lora) {
+    if (r > 64) return fail(c, LRQ_EINVAL, "rank %lld outside [1, 64]", (long long)r);
+    if (!aligned16(b)) return fail(c, LRQ_EINVAL, "B must be 16-byte aligned");
     const int rp = (int)round_up(r, 16);
     LRQ_TRY(ensure_ws(c, lora_layout(nullptr, m, w->n, w->k, rp).bytes));
     LoraWs ws = lora_layout(c->ws, m, w->n, w->k, rp);
-    // A [k, r] -> At [rp, k]; B [r, n] -> Bt [n, rp] (zero-padded rank)
+    // A [k, r] -> At [rp, k] (zero-padded rank) for the t pre-pass
     LRQ_TRY(run(c, KID_LORA_PREP, "lora_prep", [&] {
-      hipError_t e = launch_pad_transpose(c->stream, a, w->k, r, r, ws.at, rp, w->k, true);
-      if (e != hipSuccess) return e;
-      return launch_pad_transpose(c->stream, b, r, w->n, w->n, ws.bt, w->n, rp, true);
+      return launch_pad_transpose(c->stream, a, w->k, r, r, ws.at, rp, w->k, true);
     }));
     // t = s . x . A   (bf16 [m, rp] for the fused step, [m, r] for the caller)
     LRQ_TRY(run(c, KID_LORA_T, "lora_t", [&] {
       return launch_skinny_nt(c->stream, x, ws.at, m, w->k, (int)r, rp, scaling, ws.partial,
                               skinny_nt_splits(m, w->k), ws.tp, nullptr, 0, t_out, (int)r);
     }));
-    fa.t = ws.tp;
-    fa.bt = ws.bt;
-    fa.rp = rp;
+    ga.lact = ws.tp;
+    ga.lw = b;
+    ga.r = (int)r;
+    ga.rp = rp;
   }
-  int kid = KID_FWD_MAIN;
-  return run(c, KID_FWD_MAIN, "fwd_main", [&] { return launch_fwd_main(c->stream, w->format, fa, &kid); });
+  return run(c, KID_FWD_MAIN, "fwd_main", [&] { return launch_gemm(c->stream, false, w->format, ga); });
 }
 
 int lrq_quant_matmul_t(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t m, uint16_t* y) {
@@ -366,46 +379,36 @@ static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const ui
                     const uint16_t* a, const uint16_t* b, int64_t r, float scaling, const uint16_t* t,
                     uint16_t* dx, float* da, float* db) {
   LRQ_TRY(begin(c));
-  LRQ_TRY(check_weight(c, w, true));
-  if (m < 0) return fail(c, LRQ_EINVAL, "negative token count");
+  LRQ_TRY(check_gemm(c, w, m));
   if (!aligned16(dy)) return fail(c, LRQ_EINVAL, "dy must be 16-byte aligned");
   if (dx && !aligned16(dx)) return fail(c, LRQ_EINVAL, "dx must be 16-byte aligned");
   const bool lora = a != nullptr && b != nullptr && r > 0;
-  BwdArgs ba{};
-  ba.dy = dy;
-  ba.m = m;
-  ba.n = w->n;
-  ba.k = w->k;
-  ba.wdata = reinterpret_cast<const uint8_t*>(w->data);
-  ba.wscale = w->scales;
-  ba.group = w->group;
-  ba.per_channel = w->per_channel;
-  ba.dx = dx;
+  GemmArgs ga = gemm_args(w, true, dy, m, dx);
   if (lora) {
     if (r > 64) return fail(c, LRQ_EINVAL, "rank %lld outside [1, 64]", (long long)r);
     if ((da && (!x || !aligned16(x))) || (db && !t))
       return fail(c, LRQ_EINVAL, "dA needs x and dB needs t (16-byte aligned)");
+    if (!aligned16(b)) return fail(c, LRQ_EINVAL, "B must be 16-byte aligned");
     const int rp = (int)round_up(r, 16);
     const int64_t mp = round_up(m > 0 ? m : 1, 64);
     LRQ_TRY(ensure_ws(c, lora_layout(nullptr, m, w->n, w->k, rp).bytes));
     LoraWs ws = lora_layout(c->ws, m, w->n, w->k, rp);
-    LRQ_TRY(run(c, KID_LORA_PREP, "lora_prep", [&] {
-      hipError_t e = launch_pad_transpose(c->stream, a, w->k, r, r, ws.ap, w->k, rp, false);
-      if (e != hipSuccess || !db) return e;
-      return launch_pad_transpose(c->stream, t, m, r, r, ws.tt, rp, mp, true);
-    }));
+    if (db) {
+      // t [m, r] -> tt [rp, mp] (zero-padded) for the dB reduction over tokens
+      LRQ_TRY(run(c, KID_LORA_PREP, "lora_prep", [&] {
+        return launch_pad_transpose(c->stream, t, m, r, r, ws.tt, rp, mp, true);
+      }));
+    }
     // u = s . dy . B^T   ([m, rp] for dx, [rp, mp] for dA)
     LRQ_TRY(run(c, KID_LORA_U, "lora_u", [&] {
       return launch_skinny_nt(c->stream, dy, b, m, w->n, (int)r, rp, scaling, ws.partial,
                               skinny_nt_splits(m, w->n), ws.up, ws.ut, mp, nullptr, 0);
     }));
-    ba.u = ws.up;
-    ba.ap = ws.ap;
-    ba.rp = rp;
-    if (dx) {
-      int kid = KID_BWD_DX;
-      LRQ_TRY(run(c, KID_BWD_DX, "bwd_dx", [&] { return launch_bwd_dx(c->stream, w->format, ba, &kid); }));
-    }
+    ga.lact = ws.up;
+    ga.lw = a;
+    ga.r = (int)r;
+    ga.rp = rp;
+    if (dx) LRQ_TRY(run(c, KID_BWD_DX, "bwd_dx", [&] { return launch_gemm(c->stream, true, w->format, ga); }));
     if (da) {
       LRQ_TRY(run(c, KID_LORA_DA, "lora_da", [&] {
         return launch_skinny_tn(c->stream, x, ws.ut, mp, m, w->k, (int)r, rp, ws.partial,
@@ -421,8 +424,7 @@ static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const ui
     return LRQ_OK;
   }
   if (!dx) return LRQ_OK;
-  int kid = KID_BWD_DX;
-  return run(c, KID_BWD_DX, "bwd_dx", [&] { return launch_bwd_dx(c->stream, w->format, ba, &kid); });
+  return run(c, KID_BWD_DX, "bwd_dx", [&] { return launch_gemm(c->stream, true, w->format, ga); });
 }
 
 int lrq_quant_matmul_t_bwd(lrq_ctx* c, const lrq_weight* w, const uint16_t* dy, int64_t m, uint16_t* dx) {

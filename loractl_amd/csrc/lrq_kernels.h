@@ -12,38 +12,25 @@ hipError_t launch_quantize_fp8(hipStream_t st, const float* w, int64_t n, int64_
                                int per_channel, uint8_t* bytes, float* scales, float* amax_ws);
 hipError_t launch_dequant(hipStream_t st, const lrq_weight* w, void* out, bool bf16);
 
-// Arguments of the fused forward: y = x . dq(w)^T (+bias) + t . bt^T
-struct FwdArgs {
-  const uint16_t* x;  // [m, k]
-  int64_t m, n, k;
+// Arguments of the fused GEMM (lrq_gemm.hip), one struct for both passes:
+//   forward  : act = x  [m, k], l = k, e = n; lact = t [m, rp]; lw = B [r, n]
+//   backward : act = dy [m, n], l = n, e = k; lact = u [m, rp]; lw = A [k, r]
+// The weight is always the file-layout [n, k] packed tensor (wk = k).
+struct GemmArgs {
+  const uint16_t* act;
+  int64_t m, l, e, wk;
   const uint8_t* wdata;
   const float* wscale;
   int group;
   int per_channel;
-  const float* bias;   // [n] or null
-  const uint16_t* t;   // [m, rp] (already scaled), null when no LoRA
-  const uint16_t* bt;  // [n, rp]
-  int rp;              // padded rank, multiple of 16, 0 = no LoRA
-  uint16_t* y;         // [m, n]
+  const float* bias;     // forward only, [n] or null
+  const uint16_t* lact;  // [m, rp] pre-scaled LoRA activation, or null
+  const uint16_t* lw;    // the weight-side LoRA factor (user layout)
+  int r, rp;             // rank and rank padded to 16 (rp == 0: no LoRA)
+  uint16_t* out;         // [m, e]
 };
 
-// Arguments of the fused backward dx: dx = dy . dq(w) + u . ap^T
-struct BwdArgs {
-  const uint16_t* dy;  // [m, n]
-  int64_t m, n, k;
-  const uint8_t* wdata;
-  const float* wscale;
-  int group;
-  int per_channel;
-  const uint16_t* u;   // [m, rp] (already scaled) or null
-  const uint16_t* ap;  // [k, rp]
-  int rp;
-  uint16_t* dx;        // [m, k]
-};
-
-// lrq_gemm.hip
-hipError_t launch_fwd_main(hipStream_t st, int fmt, const FwdArgs& a, int* kid);
-hipError_t launch_bwd_dx(hipStream_t st, int fmt, const BwdArgs& a, int* kid);
+hipError_t launch_gemm(hipStream_t st, bool bwd, int fmt, const GemmArgs& a);
 
 // lrq_lora.hip
 // out[m, j] = s * sum_c p[m, c] * q[j, c] over c < C, for j < R (rows j >= R
