@@ -65,7 +65,7 @@ typedef struct lrq_ctx lrq_ctx;
 /* A frozen base weight: plain pointers and sizes, no ownership. */
 typedef struct lrq_weight {
   int32_t format;       /* LRQ_FMT_INT4 or LRQ_FMT_FP8 */
-  int32_t group;        /* int4: block size along k, a multiple of 32 dividing k */
+  int32_t group;        /* int4: block size along k, a power of two >= 32 dividing k */
   int64_t n;            /* d_out */
   int64_t k;            /* d_in (a multiple of 32) */
   const void* data;     /* device: packed int4 [n, k/2] or fp8 bytes [n, k] */

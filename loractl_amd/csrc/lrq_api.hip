@@ -173,10 +173,10 @@ int check_weight(lrq_ctx* c, const lrq_weight* w, bool gemm) {
     return fail(c, LRQ_EINVAL, "linear weight [%lld, %lld]: the input dim must be a multiple of 32",
                 (long long)w->n, (long long)w->k);
   if (w->format == LRQ_FMT_INT4) {
-    if (w->group <= 0 || w->group % 32 != 0 || w->k % w->group != 0)
+    if (w->group < 32 || (w->group & (w->group - 1)) != 0 || w->k % w->group != 0)
       return fail(c, LRQ_EINVAL,
                   "linear weight [%lld, %lld]: the input dim must be a multiple of the quant block "
-                  "(%d), and the block a multiple of 32",
+                  "(%d), and the block a power of two >= 32",
                   (long long)w->n, (long long)w->k, w->group);
   }
   if (gemm && w->n % 8 != 0)
@@ -317,6 +317,8 @@ static GemmArgs gemm_args(const lrq_weight* w, bool bwd, const uint16_t* act, in
   g.wdata = reinterpret_cast<const uint8_t*>(w->data);
   g.wscale = w->scales;
   g.group = w->group;
+  g.gshift = 0;
+  while (w->group > 0 && (1 << g.gshift) < w->group) ++g.gshift;
   g.per_channel = w->per_channel;
   g.bias = bwd ? nullptr : w->bias;
   g.out = out;
@@ -326,6 +328,10 @@ static GemmArgs gemm_args(const lrq_weight* w, bool bwd, const uint16_t* act, in
 static int check_gemm(lrq_ctx* c, const lrq_weight* w, int64_t m) {
   LRQ_TRY(check_weight(c, w, true));
   if (m < 0) return fail(c, LRQ_EINVAL, "negative token count");
+  const int64_t wbytes = w->n * (w->format == LRQ_FMT_INT4 ? w->k / 2 : w->k);
+  if (wbytes >= (int64_t)1 << 31)
+    return fail(c, LRQ_EUNSUPPORTED, "packed weight of %lld bytes: the fused kernels address at most 2 GiB",
+                (long long)wbytes);
   if (w->n <= 0 || w->k <= 0)
     return fail(c, LRQ_EINVAL, "the fused kernels need d_out > 0 and d_in > 0 (got [%lld, %lld])",
                 (long long)w->n, (long long)w->k);

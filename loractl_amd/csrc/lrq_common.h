@@ -120,6 +120,21 @@ LRQ_DEV bf16x8 as_bf16x8(const u32x4& v) { return __builtin_bit_cast(bf16x8, v);
 LRQ_DEV u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 LRQ_DEV void st16(void* p, const u32x4& v) { *reinterpret_cast<u32x4*>(p) = v; }
 
+// ---------------------------------------------------------------- buffer loads
+// Raw buffer loads with a wave-uniform resource: an offset at or past
+// num_records reads zeros, so bounds handling needs no branches.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr uint32_t LRQ_OOB = 0x80000000u;  // an offset past any resource
+
+LRQ_DEV rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+LRQ_DEV u32x4 bload16(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0); }
+LRQ_DEV u32x2 bload8(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0); }
+LRQ_DEV uint32_t bload4(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0); }
+LRQ_DEV float bloadf(rsrc_t r, uint32_t off) { return __builtin_bit_cast(float, bload4(r, off)); }
+LRQ_DEV uint32_t clamp_bytes(int64_t b) { return b <= 0 ? 0u : (b >= 0xffffffffll ? 0xffffffffu : (uint32_t)b); }
+
 // 8 consecutive bf16 (16 bytes) from global with a validity predicate.
 LRQ_DEV u32x4 ld16_pred(const void* p, bool ok) {
   u32x4 z = {0u, 0u, 0u, 0u};

@@ -84,82 +84,98 @@ k_gemm(GemmArgs a, int tiles_m) {
   const int g = lane >> 5, l32 = lane & 31;
 
   // ---------------- activation operand: rows of this wavefront, 64 contiguous bytes per step
-  const uint16_t* arow[MJ];
-  bool arow_ok[MJ];
+  // (buffer resource based at the wavefront's first token row: rows past M
+  // fall outside num_records and read zeros)
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  const int64_t mw = m0 + wv * (32 * MJ);
+  const int64_t mrows = (M - mw) < (32 * MJ) ? (M - mw) : (32 * MJ);
+  const rsrc_t ract = make_rsrc(a.act + (mw < M ? mw : 0) * L, clamp_bytes(mrows * L * 2));
+  uint32_t aoff[MJ];
 #pragma unroll
-  for (int j = 0; j < MJ; ++j) {
-    const int64_t m = m0 + wave * (32 * MJ) + j * 32 + l32;
-    arow_ok[j] = m < M;
-    arow[j] = a.act + (arow_ok[j] ? m : (M - 1)) * L + g * 32;
-  }
+  for (int j = 0; j < MJ; ++j) aoff[j] = (uint32_t)(((j * 32 + l32) * L + g * 32) * 2);
   u32x4 act[2][MJ][4];
   auto load_act = [&](u32x4 (&dst)[MJ][4], int64_t k0) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      // L % 8 == 0: each 8-value chunk is all in or all out; out-of-range
-      // chunks read a clamped in-bounds address and are zeroed
+      // L % 8 == 0: each 8-value chunk is all in or all out
       const bool kok = k0 + g * 32 + c * 8 < L;
-      const int64_t kc = kok ? k0 + c * 8 : -(int64_t)(g * 32);
 #pragma unroll
-      for (int j = 0; j < MJ; ++j) {
-        const u32x4 v = ld16(arow[j] + kc);
-        dst[j][c] = (arow_ok[j] && kok) ? v : zero4();
-      }
+      for (int j = 0; j < MJ; ++j)
+        dst[j][c] = bload16(ract, kok ? aoff[j] + (uint32_t)((k0 + c * 8) * 2) : LRQ_OOB);
     }
   };
 
   // ---------------- weight operand: packed loads (two register sets)
-  const int kgroups = (FMT == LRQ_FMT_INT4) ? (int)(K / a.group) : 0;
-  // backward mapping: id = tid; kc = id % KCH (8 k), nc = id / KCH (8 n)
+  // All offsets are 32-bit (the host limits packed weights to 2 GiB) and the
+  // int4 group index is a shift (the block size is a power of two).
+  const uint32_t kgroups = (FMT == LRQ_FMT_INT4) ? (uint32_t)(K >> a.gshift) : 0u;
+  const uint32_t rowb = (uint32_t)((FMT == LRQ_FMT_INT4) ? K / 2 : K);  // packed bytes per row
+  // forward: resources based at the tile's first weight row (rows past E read zeros)
+  // backward: the whole weight (rows are the reduction index n)
+  const int64_t wrow0 = BWD ? 0 : e0;
+  const int64_t wrows = BWD ? a.l : ((E - e0) < RA ? (E - e0) : RA);
+  const rsrc_t rw = make_rsrc(a.wdata + wrow0 * rowb, clamp_bytes(wrows * rowb));
+  const rsrc_t rs = make_rsrc(a.wscale + (FMT == LRQ_FMT_INT4 ? wrow0 * kgroups : 0),
+                              clamp_bytes(FMT == LRQ_FMT_INT4 ? wrows * kgroups * 4
+                                                              : (a.per_channel ? (wrow0 + wrows) * 4 : 4)));
+  // backward mapping: kc = tid % KCH (8 k), nc = (tid / KCH) % 8 (8 n); threads past
+  // 8*KCH redo a block and write it to a private dummy slot
   const bool wthr_ok = BWD ? (tid < 8 * C::KCH) : true;
-  const int bkc = BWD ? (wthr_ok ? tid % C::KCH : 0) : 0;
-  const int bnc = BWD ? (wthr_ok ? tid / C::KCH : 0) : 0;
+  const int bkc = BWD ? tid % C::KCH : 0;
+  const int bnc = BWD ? (tid / C::KCH) % 8 : 0;
+  // backward per-thread column: packed byte offset and scale column, or out of bounds
+  // (a column past K gets offsets past every resource: row offsets stay below
+  // 2^31, so LRQ_OOB + row offset neither wraps nor lands inside)
+  const int64_t bcol = e0 + bkc * 8;
+  const bool bcol_ok = bcol < K;
+  const uint32_t bcolb = bcol_ok ? (uint32_t)((FMT == LRQ_FMT_INT4) ? bcol / 2 : bcol) : LRQ_OOB;
+  const uint32_t bscol4 = bcol_ok ? ((FMT == LRQ_FMT_INT4) ? (uint32_t)(bcol >> a.gshift) * 4u : 0u) : LRQ_OOB;
+  // forward per-chunk row offsets
+  uint32_t frow[BWD ? 1 : C::CH], fsrow[BWD ? 1 : C::CH], fpart[BWD ? 1 : C::CH];
+  if (!BWD) {
+#pragma unroll
+    for (int c = 0; c < C::CH; ++c) {
+      const int id = tid + NT * c;
+      const int row = id / C::WPR;
+      frow[c] = (uint32_t)row * rowb;
+      fsrow[c] = (uint32_t)row * kgroups;
+      fpart[c] = (uint32_t)(id % C::WPR) * (FMT == LRQ_FMT_INT4 ? 32u : 16u);
+    }
+  }
 
   u32x4 wf[2][BWD ? 1 : C::CH];            // forward packed chunks
   float wfs[2][BWD ? 1 : C::CH];           // forward chunk scales (int4)
   uint32_t wb[2][BWD ? 8 * C::WORDS : 1];  // backward 8 rows x 8 k
   float wbs[2][BWD ? 8 : 1];               // backward row scales
 
-  auto load_w = [&](int set, int64_t r0) {
+  auto load_w = [&](int set, int64_t r0_) {
+    const uint32_t r0 = (uint32_t)r0_;
     if (!BWD) {
       // forward: rows n = e0 + row, reduction k = r0 + part * (32 | 16)
 #pragma unroll
       for (int c = 0; c < C::CH; ++c) {
-        const int id = tid + NT * c;
-        const int row = id / C::WPR, part = id % C::WPR;
-        const int64_t n = e0 + row;
-        const int64_t kk = r0 + part * (FMT == LRQ_FMT_INT4 ? 32 : 16);
-        const bool ok = (n < E) && (kk < K);
-        const int64_t nn = ok ? n : 0, kq = ok ? kk : 0;
+        const uint32_t kk = r0 + fpart[c];
+        const bool kok = kk < (uint32_t)K;
         if (FMT == LRQ_FMT_INT4) {
-          const u32x4 v = ld16(a.wdata + nn * (K / 2) + kq / 2);
-          const float s = a.wscale[nn * kgroups + kq / a.group];
-          wf[set][c] = v;
-          wfs[set][c] = ok ? s : 0.0f;
+          wf[set][c] = bload16(rw, kok ? frow[c] + kk / 2 : LRQ_OOB);
+          wfs[set][c] = bloadf(rs, kok ? (fsrow[c] + (kk >> a.gshift)) * 4 : LRQ_OOB);
         } else {
-          const u32x4 v = ld16(a.wdata + nn * K + kq);
-          wf[set][c] = ok ? v : zero4();
+          wf[set][c] = bload16(rw, kok ? frow[c] + kk : LRQ_OOB);
         }
       }
     } else {
-      // backward: rows n = r0 + nc*8 + i, columns k = e0 + kc*8
-      const int64_t k = e0 + bkc * 8;
+      // backward: rows n = r0 + nc*8 + i, column bcol
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const int64_t n = r0 + bnc * 8 + i;
-        const bool ok = (n < L) && (k < K);
-        const int64_t nn = ok ? n : 0, kq = ok ? k : 0;
+        const uint32_t n = r0 + (uint32_t)(bnc * 8 + i);
         if (FMT == LRQ_FMT_INT4) {
-          const uint32_t v = *reinterpret_cast<const uint32_t*>(a.wdata + nn * (K / 2) + kq / 2);
-          const float s = a.wscale[nn * kgroups + kq / a.group];
-          wb[set][i] = v;
-          wbs[set][i] = ok ? s : 0.0f;
+          wb[set][i] = bload4(rw, n * rowb + bcolb);
+          wbs[set][i] = bloadf(rs, n * kgroups * 4u + bscol4);
         } else {
-          const u32x2 v = *reinterpret_cast<const u32x2*>(a.wdata + nn * K + kq);
-          const float s = a.per_channel ? a.wscale[nn] : a.wscale[0];
+          const u32x2 v = bload8(rw, n * rowb + bcolb);
           wb[set][2 * i] = v[0];
           wb[set][2 * i + 1] = v[1];
-          wbs[set][i] = ok ? s : 0.0f;
+          wbs[set][i] = bloadf(rs, (a.per_channel ? n * 4u : 0u) + bscol4);
         }
       }
     }

@@ -22,6 +22,7 @@ struct GemmArgs {
   const uint8_t* wdata;
   const float* wscale;
   int group;
+  int gshift;            // log2(group) (int4 blocks are powers of two)
   int per_channel;
   const float* bias;     // forward only, [n] or null
   const uint16_t* lact;  // [m, rp] pre-scaled LoRA activation, or null
