@@ -247,19 +247,40 @@ k_gemm(GemmArgs a, int tiles_m) {
   };
 
   // one reduction step on LDS buffer `buf` with activations act[p]; the
-  // dequantization of register set `wset` into `nbuf` rides along.
+  // dequantization of register set `wset` into `nbuf` rides along. The
+  // fragments of sub-step kk+1 are read from LDS while sub-step kk's
+  // matrix-core work runs, and the schedule interleaves every matrix-core
+  // instruction with ~3 VALU (dequantization) and spreads the LDS writes and
+  // global loads between them, so one wavefront per SIMD keeps the matrix
+  // pipe fed while it converts the next tile.
   auto step = [&](int p, int buf, int wset, int nbuf) {
     const uint16_t* sA = lds + buf * C::BUF;
+    bf16x8 fa[2][NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) fa[0][i] = afrag(sA, i * 32 + l32, g * 4);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      bf16x8 fa[NI];
+      const int cur = kk & 1;
+      if (kk < 3) {
 #pragma unroll
-      for (int i = 0; i < NI; ++i) fa[i] = afrag(sA, i * 32 + l32, g * 4 + kk);
+        for (int i = 0; i < NI; ++i) fa[cur ^ 1][i] = afrag(sA, i * 32 + l32, g * 4 + kk + 1);
+      }
 #pragma unroll
       for (int i = 0; i < NI; ++i)
 #pragma unroll
-        for (int j = 0; j < MJ; ++j) acc[i][j] = mfma32(fa[i], as_bf16x8(act[p][j][kk]), acc[i][j]);
+        for (int j = 0; j < MJ; ++j) acc[i][j] = mfma32(fa[cur][i], as_bf16x8(act[p][j][kk]), acc[i][j]);
       store_w(wset, nbuf, kk);
+    }
+    constexpr int NM = 4 * NI * MJ;           // matrix-core instructions in the step
+    constexpr int NW = BWD ? 8 : 4 * C::CH;   // LDS tile writes
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // VALU
+      if (m % (NI * MJ) < NI && m < NM - NI * MJ)
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read (next sub-step)
+      if ((m * NW) / NM != ((m + 1) * NW) / NM) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
+      if (m % 4 == 1) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
     }
   };
 
