@@ -37,6 +37,14 @@
  *     q in [-7, 7]; scales = f32 [n, k/group]; dequant = q * scale (f32).
  *   LRQ_FMT_FP8: data = e4m3fn bytes [n, k]; scales = f32 [n] (per_channel)
  *     or [1]; dequant = LUT[byte] * scale (f32).
+ *   Those row layouts (LRQ_LAYOUT_ROWS) are the interchange format. The fused
+ *   kernels read LRQ_LAYOUT_BLOCKED, produced once per weight by
+ *   lrq_weight_block: 64 (n) x 64 (k) blocks contiguous in memory, block
+ *   (nb, kb) at (nb * KB + kb) * block bytes with KB = ceil(k / 64); inside a
+ *   block the rows keep the row-layout byte order (int4: 32 bytes per row,
+ *   fp8: 64). int4 scales become [NB][Gp][64] (NB = ceil(n/64),
+ *   Gp = 64*KB/group); fp8 scales are unchanged. Padding rows/columns hold
+ *   q = 0 with scale 0 (int4) or byte 0 (fp8).
  *   LoRA factors in burn layout: A = [k, r] (d_in x rank), B = [r, n].
  */
 #ifndef LORACTL_ROCM_H
@@ -59,6 +67,7 @@ enum {
 };
 
 enum { LRQ_FMT_INT4 = 1, LRQ_FMT_FP8 = 2 };
+enum { LRQ_LAYOUT_ROWS = 0, LRQ_LAYOUT_BLOCKED = 1 };
 
 typedef struct lrq_ctx lrq_ctx;
 
@@ -71,7 +80,7 @@ typedef struct lrq_weight {
   const void* data;     /* device: packed int4 [n, k/2] or fp8 bytes [n, k] */
   const float* scales;  /* device: int4 [n, k/group]; fp8 [n] or [1] */
   int32_t per_channel;  /* fp8: 1 when scales has n entries, 0 for one scalar */
-  int32_t reserved;
+  int32_t layout;       /* LRQ_LAYOUT_ROWS or LRQ_LAYOUT_BLOCKED */
   const float* bias;    /* device f32 [n] or NULL (src/mmdit.rs:426-427) */
 } lrq_weight;
 
@@ -104,6 +113,17 @@ int lrq_quantize_int4(lrq_ctx* ctx, const float* w, int64_t n, int64_t k, int64_
 int lrq_quantize_fp8(lrq_ctx* ctx, const float* w, int64_t n, int64_t k, int per_channel,
                      uint8_t* bytes, float* scales);
 
+/* Sizes of the blocked layout of a weight: data bytes and scale count
+ * (0 for fp8, whose scales keep their shape). No device work. */
+int lrq_weight_blocked_size(int format, int64_t n, int64_t k, int64_t group, int64_t* data_bytes,
+                            int64_t* scale_count);
+
+/* Re-lay a LRQ_LAYOUT_ROWS weight into LRQ_LAYOUT_BLOCKED (data_out of
+ * data_bytes, scales_out of scale_count floats; fp8 scales are not copied).
+ * A one-time step per frozen weight (no counterpart in the reference: burn
+ * keeps its packed storage private, src/quant.rs:57-60). */
+int lrq_weight_block(lrq_ctx* ctx, const lrq_weight* rows, uint8_t* data_out, float* scales_out);
+
 /* Dequantize the whole weight to f32 [n, k] (src/quant.rs:232; fp8.rs:306-318).
  * Debug/parity surface: bit-exact with the CPU definition. */
 int lrq_dequant(lrq_ctx* ctx, const lrq_weight* w, float* out);
@@ -113,7 +133,8 @@ int lrq_dequant(lrq_ctx* ctx, const lrq_weight* w, float* out);
 int lrq_dequant_bf16(lrq_ctx* ctx, const lrq_weight* w, uint16_t* out);
 
 /* QuantBackend::quant_matmul_t (src/quant.rs:172-178): y[m, n] = x[m, k] .
- * dequant(w)^T (+ bias), bf16 in/out, f32 accumulation. */
+ * dequant(w)^T (+ bias), bf16 in/out, f32 accumulation. The fused calls
+ * (this and the three below) take a LRQ_LAYOUT_BLOCKED weight. */
 int lrq_quant_matmul_t(lrq_ctx* ctx, const lrq_weight* w, const uint16_t* x, int64_t m,
                        uint16_t* y);
 

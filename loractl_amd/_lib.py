@@ -19,6 +19,8 @@ LRQ_EHIP = -3
 LRQ_ENOMEM = -4
 LRQ_FMT_INT4 = 1
 LRQ_FMT_FP8 = 2
+LRQ_LAYOUT_ROWS = 0
+LRQ_LAYOUT_BLOCKED = 1
 
 _ERRNAMES = {
     LRQ_EINVAL: "LRQ_EINVAL",
@@ -39,7 +41,7 @@ class LrqWeight(ctypes.Structure):
         ("data", ctypes.c_void_p),
         ("scales", ctypes.c_void_p),
         ("per_channel", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("layout", ctypes.c_int32),
         ("bias", ctypes.c_void_p),
     ]
 
@@ -67,6 +69,8 @@ SIGNATURES = {
     "lrq_reserve": (_i32, [_vp, _i64, _i64, _i64, _i64]),
     "lrq_quantize_int4": (_i32, [_vp, _vp, _i64, _i64, _i64, _vp, _vp]),
     "lrq_quantize_fp8": (_i32, [_vp, _vp, _i64, _i64, _i32, _vp, _vp]),
+    "lrq_weight_blocked_size": (_i32, [_i32, _i64, _i64, _i64, ctypes.POINTER(_i64), ctypes.POINTER(_i64)]),
+    "lrq_weight_block": (_i32, [_vp, _wp, _vp, _vp]),
     "lrq_dequant": (_i32, [_vp, _wp, _vp]),
     "lrq_dequant_bf16": (_i32, [_vp, _wp, _vp]),
     "lrq_quant_matmul_t": (_i32, [_vp, _wp, _vp, _i64, _vp]),

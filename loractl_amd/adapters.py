@@ -97,7 +97,10 @@ class QuantLinear:
             raise ValueError("QuantLinear holds at least one chunk")
         self.weight = list(weight)
         self.bias = bias
-        self._joined = concat_chunks(self.weight)
+        if len(self.weight) == 1:
+            self._joined = D.compute_weight(self.weight[0])
+        else:
+            self._joined = D.block(concat_chunks(self.weight))
 
     @property
     def d_in(self) -> int:

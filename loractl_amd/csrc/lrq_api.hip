@@ -33,7 +33,8 @@ struct lrq_ctx {
 namespace {
 
 const char* kNames[KID_COUNT] = {"quantize_int4", "quantize_fp8", "dequant", "fwd_main", "bwd_dx",
-                                 "lora_prep",     "lora_t",       "lora_u",  "lora_da",  "lora_db"};
+                                 "lora_prep",     "lora_t",       "lora_u",  "lora_da",  "lora_db",
+                                 "block"};
 
 int fail(lrq_ctx* c, int code, const char* fmt, ...) {
   if (c) {
@@ -179,6 +180,10 @@ int check_weight(lrq_ctx* c, const lrq_weight* w, bool gemm) {
                   "(%d), and the block a power of two >= 32",
                   (long long)w->n, (long long)w->k, w->group);
   }
+  if (w->layout != LRQ_LAYOUT_ROWS && w->layout != LRQ_LAYOUT_BLOCKED)
+    return fail(c, LRQ_EINVAL, "weight layout %d is neither LRQ_LAYOUT_ROWS nor LRQ_LAYOUT_BLOCKED", w->layout);
+  if (gemm && w->layout != LRQ_LAYOUT_BLOCKED)
+    return fail(c, LRQ_EINVAL, "the fused kernels read LRQ_LAYOUT_BLOCKED weights: call lrq_weight_block once");
   if (gemm && w->n % 8 != 0)
     return fail(c, LRQ_EINVAL, "d_out %lld must be a multiple of 8 for the fused kernels", (long long)w->n);
   if (w->n * w->k > 0 && (!w->data || !w->scales))
@@ -293,6 +298,26 @@ int lrq_quantize_fp8(lrq_ctx* c, const float* w, int64_t n, int64_t k, int per_c
   });
 }
 
+int lrq_weight_blocked_size(int format, int64_t n, int64_t k, int64_t group, int64_t* data_bytes,
+                            int64_t* scale_count) {
+  if ((format != LRQ_FMT_INT4 && format != LRQ_FMT_FP8) || n < 0 || k < 0 || !data_bytes || !scale_count)
+    return LRQ_EINVAL;
+  if (format == LRQ_FMT_INT4 && (group < 32 || (group & (group - 1)) != 0 || k % group != 0)) return LRQ_EINVAL;
+  blocked_sizes(format, n, k, format == LRQ_FMT_INT4 ? group : 64, data_bytes, scale_count);
+  return LRQ_OK;
+}
+
+int lrq_weight_block(lrq_ctx* c, const lrq_weight* w, uint8_t* data_out, float* scales_out) {
+  LRQ_TRY(begin(c));
+  LRQ_TRY(check_weight(c, w, false));
+  if (w->layout != LRQ_LAYOUT_ROWS) return fail(c, LRQ_EINVAL, "lrq_weight_block takes a LRQ_LAYOUT_ROWS weight");
+  if (w->format == LRQ_FMT_INT4 && ((w->group & (w->group - 1)) != 0))
+    return fail(c, LRQ_EINVAL, "int4 block %d must be a power of two", w->group);
+  if (!aligned16(data_out)) return fail(c, LRQ_EINVAL, "data_out must be 16-byte aligned");
+  if (w->format == LRQ_FMT_INT4 && !scales_out) return fail(c, LRQ_EINVAL, "scales_out is NULL");
+  return run(c, KID_BLOCK, "weight_block", [&] { return launch_block(c->stream, w, data_out, scales_out); });
+}
+
 int lrq_dequant(lrq_ctx* c, const lrq_weight* w, float* out) {
   LRQ_TRY(begin(c));
   LRQ_TRY(check_weight(c, w, false));
@@ -320,6 +345,7 @@ static GemmArgs gemm_args(const lrq_weight* w, bool bwd, const uint16_t* act, in
   g.gshift = 0;
   while (w->group > 0 && (1 << g.gshift) < w->group) ++g.gshift;
   g.per_channel = w->per_channel;
+  g.nib = 0x0f0f0f0fu;
   g.bias = bwd ? nullptr : w->bias;
   g.out = out;
   return g;
@@ -328,7 +354,8 @@ static GemmArgs gemm_args(const lrq_weight* w, bool bwd, const uint16_t* act, in
 static int check_gemm(lrq_ctx* c, const lrq_weight* w, int64_t m) {
   LRQ_TRY(check_weight(c, w, true));
   if (m < 0) return fail(c, LRQ_EINVAL, "negative token count");
-  const int64_t wbytes = w->n * (w->format == LRQ_FMT_INT4 ? w->k / 2 : w->k);
+  int64_t wbytes = 0, nscales = 0;
+  blocked_sizes(w->format, w->n, w->k, w->group, &wbytes, &nscales);
   if (wbytes >= (int64_t)1 << 31)
     return fail(c, LRQ_EUNSUPPORTED, "packed weight of %lld bytes: the fused kernels address at most 2 GiB",
                 (long long)wbytes);

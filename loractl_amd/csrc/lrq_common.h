@@ -13,14 +13,13 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 #define LRQ_DEV __device__ __forceinline__
 
 // ---------------------------------------------------------------- bf16
-// Round-to-nearest-even f32 -> bf16 bits for two values packed (lo, hi).
-// On gfx950 this lowers to v_cvt_pk_bf16_f32.
+// Round-to-nearest-even f32 -> bf16 bits for two values packed (lo, hi):
+// one v_cvt_pk_bf16_f32 on gfx950.
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 LRQ_DEV uint32_t pack_bf16x2(float lo, float hi) {
-  __bf16 a = (__bf16)lo;
-  __bf16 b = (__bf16)hi;
-  uint16_t ua = __builtin_bit_cast(uint16_t, a);
-  uint16_t ub = __builtin_bit_cast(uint16_t, b);
-  return (uint32_t)ua | ((uint32_t)ub << 16);
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
 LRQ_DEV float bf16_lo(uint32_t v) { return __builtin_bit_cast(float, v << 16); }
@@ -34,21 +33,26 @@ LRQ_DEV uint16_t f32_to_bf16_bits(float f) {
 // One dword holds 8 nibbles (k = 0..7 of a run: byte j = k 2j | 2j+1 << 4),
 // each q+8. Dequantize all 8 to f32 as fma(u, s, -8s) == RN((u-8)*s) ==
 // RN(q*s), i.e. bit-identical to the f32 product q*s, then round to bf16.
-// out[0..3] are bf16 pairs (k0,k1) (k2,k3) (k4,k5) (k6,k7).
-LRQ_DEV void dequant8_int4_f32(uint32_t w, float s, float f[8]) {
+// `nib` must be 0x0f0f0f0f; callers pass it from a kernel argument so the
+// compiler keeps whole-byte extracts (v_cvt_f32_ubyte0..3) instead of
+// narrowing them to bit-field extracts.
+LRQ_DEV void dequant8_int4_f32(uint32_t w, float s, float f[8], uint32_t nib = 0x0f0f0f0fu) {
   const float nb = -8.0f * s;
-  const uint32_t lo = w & 0x0f0f0f0fu;         // k = 0,2,4,6 in bytes 0..3
-  const uint32_t hi = (w >> 4) & 0x0f0f0f0fu;  // k = 1,3,5,7
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    f[2 * j] = __builtin_fmaf((float)((lo >> (8 * j)) & 0xffu), s, nb);
-    f[2 * j + 1] = __builtin_fmaf((float)((hi >> (8 * j)) & 0xffu), s, nb);
-  }
+  const uint32_t lo = w & nib;         // k = 0,2,4,6 in bytes 0..3
+  const uint32_t hi = (w >> 4) & nib;  // k = 1,3,5,7
+  f[0] = __builtin_fmaf((float)(lo & 0xffu), s, nb);
+  f[1] = __builtin_fmaf((float)(hi & 0xffu), s, nb);
+  f[2] = __builtin_fmaf((float)((lo >> 8) & 0xffu), s, nb);
+  f[3] = __builtin_fmaf((float)((hi >> 8) & 0xffu), s, nb);
+  f[4] = __builtin_fmaf((float)((lo >> 16) & 0xffu), s, nb);
+  f[5] = __builtin_fmaf((float)((hi >> 16) & 0xffu), s, nb);
+  f[6] = __builtin_fmaf((float)(lo >> 24), s, nb);
+  f[7] = __builtin_fmaf((float)(hi >> 24), s, nb);
 }
 
-LRQ_DEV u32x4 dequant8_int4_bf16(uint32_t w, float s) {
+LRQ_DEV u32x4 dequant8_int4_bf16(uint32_t w, float s, uint32_t nib = 0x0f0f0f0fu) {
   float f[8];
-  dequant8_int4_f32(w, s, f);
+  dequant8_int4_f32(w, s, f, nib);
   u32x4 o;
   o[0] = pack_bf16x2(f[0], f[1]);
   o[1] = pack_bf16x2(f[2], f[3]);

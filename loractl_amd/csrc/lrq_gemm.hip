@@ -56,18 +56,29 @@ LRQ_DEV int xcd_remap(int bid, int nblk) {
 
 LRQ_DEV u32x4 zero4() { return (u32x4){0u, 0u, 0u, 0u}; }
 
+// Blocked-layout sizes (see lrq_quant.hip): data bytes and int4 scale count.
+LRQ_DEV void blocked_sizes_dev(int fmt, int64_t n, int64_t k, int64_t* data_bytes, int64_t* nscales,
+                               int gshift) {
+  const int64_t NB = (n + 63) / 64, KB = (k + 63) / 64;
+  *data_bytes = NB * KB * 64 * (fmt == LRQ_FMT_INT4 ? 32 : 64);
+  *nscales = (fmt == LRQ_FMT_INT4) ? NB * ((KB * 64) >> gshift) * 64 : 0;
+}
+
 template <bool BWD, int FMT, int NI>
 struct Cfg {
-  static constexpr int RA = 32 * NI;
-  // forward: each thread owns CH 16-byte chunks of packed weight rows
-  static constexpr int WPR = (FMT == LRQ_FMT_INT4) ? 2 : 4;  // 16-byte chunks per row per step
+  static constexpr int RA = 32 * NI;  // a multiple of 64 (whole weight blocks)
+  // forward: 16-byte chunks of the packed weight tile per step, per thread
+  static constexpr int WPR = (FMT == LRQ_FMT_INT4) ? 2 : 4;  // chunks per block row (64 k)
   static constexpr int CH = RA * WPR / NT;
   // backward: one 8 (n) x 8 (k) block per thread; RA/8 k-chunks x 8 n-chunks
   static constexpr int KCH = RA / 8;
   static constexpr int WORDS = (FMT == LRQ_FMT_INT4) ? 1 : 2;  // dwords per 8 k of one row
-  static constexpr int BUF = RA * LD;
-  static constexpr int LDS_ELEMS = 2 * BUF + (BWD ? NT * 8 : 0);  // + per-thread dummy slots
+  static constexpr int WBUF = RA * LD;                          // weight tile (bf16)
+  static constexpr int XBUF = RB * BK;                          // activation tile (bf16)
+  static constexpr int LDS_ELEMS = 2 * WBUF + 2 * XBUF + (BWD ? NT * 8 : 0);
 };
+
+typedef __attribute__((address_space(3))) void lds_void;
 
 template <bool BWD, int FMT, int NI>
 __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1)))
@@ -75,125 +86,159 @@ k_gemm(GemmArgs a, int tiles_m) {
   using C = Cfg<BWD, FMT, NI>;
   constexpr int RA = C::RA;
   __shared__ __attribute__((aligned(16))) uint16_t lds[C::LDS_ELEMS];
+  uint16_t* const sW = lds;                     // [2][RA][LD]
+  uint16_t* const sX = lds + 2 * C::WBUF;       // [2][256][64], 16-byte chunks XOR-swizzled by row
+  uint16_t* const sDummy = sX + 2 * C::XBUF;    // backward: per-thread slots for idle threads
 
+  // XCD-contiguous logical order, then groups of GM token tiles walked
+  // weight-tile by weight-tile: the 32 concurrent workgroups of an XCD cover
+  // a GM x 8 block, so activation and weight slices are shared in its L2
   const int logical = xcd_remap(blockIdx.x, gridDim.x);
-  const int tm = logical % tiles_m, ta = logical / tiles_m;
+  const int tiles_a = gridDim.x / tiles_m;
+  constexpr int GM = 4;
+  const int grp = logical / (GM * tiles_a), within = logical % (GM * tiles_a);
+  const int gm = min(GM, tiles_m - grp * GM);
+  const int tm = grp * GM + within % gm, ta = within / gm;
   const int64_t m0 = (int64_t)tm * RB, e0 = (int64_t)ta * RA;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t M = a.m, L = a.l, E = a.e, K = a.wk;
   const int g = lane >> 5, l32 = lane & 31;
-
-  // ---------------- activation operand: rows of this wavefront, 64 contiguous bytes per step
-  // (buffer resource based at the wavefront's first token row: rows past M
-  // fall outside num_records and read zeros)
   const int wv = __builtin_amdgcn_readfirstlane(wave);
+
+  // ---------------- activation operand: DMA into LDS, one reduction step ahead
+  // Wave wv moves its own 64 token rows (8 KB per step) with 8 buffer loads
+  // whose lanes cover 8 rows x 128 contiguous bytes each; lane l of load c
+  // lands at row c*8 + l/8, physical chunk l%8, which holds logical chunk
+  // (l%8) ^ (l/8). Rows past M read zeros through the resource size.
   const int64_t mw = m0 + wv * (32 * MJ);
   const int64_t mrows = (M - mw) < (32 * MJ) ? (M - mw) : (32 * MJ);
   const rsrc_t ract = make_rsrc(a.act + (mw < M ? mw : 0) * L, clamp_bytes(mrows * L * 2));
-  uint32_t aoff[MJ];
+  const int drow = lane >> 3, dq = (lane & 7) ^ (lane >> 3);
+  const uint32_t doff0 = (uint32_t)((drow * L + dq * 8) * 2);
+  auto dma_act = [&](int buf, int64_t k0) {
+    const bool kok = k0 + dq * 8 < L;  // L % 8 == 0
+    const uint32_t koff = (uint32_t)(k0 * 2);
+    lds_void* base = (lds_void*)(sX + buf * C::XBUF + wv * (32 * MJ) * BK);
 #pragma unroll
-  for (int j = 0; j < MJ; ++j) aoff[j] = (uint32_t)(((j * 32 + l32) * L + g * 32) * 2);
-  u32x4 act[2][MJ][4];
-  auto load_act = [&](u32x4 (&dst)[MJ][4], int64_t k0) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      // L % 8 == 0: each 8-value chunk is all in or all out
-      const bool kok = k0 + g * 32 + c * 8 < L;
-#pragma unroll
-      for (int j = 0; j < MJ; ++j)
-        dst[j][c] = bload16(ract, kok ? aoff[j] + (uint32_t)((k0 + c * 8) * 2) : LRQ_OOB);
+    for (int c = 0; c < 4 * MJ; ++c) {
+      const uint32_t off = kok ? doff0 + (uint32_t)(c * 8 * L * 2) + koff : LRQ_OOB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ract, (lds_void*)((__attribute__((address_space(3))) char*)base + c * 8 * BK * 2),
+                                               16, off, 0, 0, 0);
     }
   };
+  auto bfrag = [&](int buf, int j, int q) -> bf16x8 {
+    const int rl = j * 32 + l32;  // wave-local row
+    const int phys = q ^ (rl & 7);
+    return as_bf16x8(ld16(sX + buf * C::XBUF + (wv * (32 * MJ) + rl) * BK + phys * 8));
+  };
 
-  // ---------------- weight operand: packed loads (two register sets)
-  // All offsets are 32-bit (the host limits packed weights to 2 GiB) and the
-  // int4 group index is a shift (the block size is a power of two).
-  const uint32_t kgroups = (FMT == LRQ_FMT_INT4) ? (uint32_t)(K >> a.gshift) : 0u;
-  const uint32_t rowb = (uint32_t)((FMT == LRQ_FMT_INT4) ? K / 2 : K);  // packed bytes per row
-  // forward: resources based at the tile's first weight row (rows past E read zeros)
-  // backward: the whole weight (rows are the reduction index n)
-  const int64_t wrow0 = BWD ? 0 : e0;
-  const int64_t wrows = BWD ? a.l : ((E - e0) < RA ? (E - e0) : RA);
-  const rsrc_t rw = make_rsrc(a.wdata + wrow0 * rowb, clamp_bytes(wrows * rowb));
-  const rsrc_t rs = make_rsrc(a.wscale + (FMT == LRQ_FMT_INT4 ? wrow0 * kgroups : 0),
-                              clamp_bytes(FMT == LRQ_FMT_INT4 ? wrows * kgroups * 4
-                                                              : (a.per_channel ? (wrow0 + wrows) * 4 : 4)));
+  // ---------------- weight operand (blocked layout): packed loads, two register sets
+  const int64_t KB = (K + 63) / 64;
+  const uint32_t blkb = (FMT == LRQ_FMT_INT4) ? 2048u : 4096u;  // bytes per 64x64 block
+  const uint32_t rowb = (FMT == LRQ_FMT_INT4) ? 32u : 64u;      // bytes per block row
+  const uint32_t Gp = (FMT == LRQ_FMT_INT4) ? (uint32_t)((KB * 64) >> a.gshift) : 0u;
+  int64_t wbytes, nsc;
+  blocked_sizes_dev(FMT, (BWD ? L : E), K, &wbytes, &nsc, a.gshift);
+  // forward: resources based at the tile's first block row; backward: whole weight
+  const int64_t nb0 = BWD ? 0 : e0 / 64;
+  const rsrc_t rw = make_rsrc(a.wdata + nb0 * KB * blkb, clamp_bytes(wbytes - nb0 * KB * blkb));
+  const rsrc_t rs = (FMT == LRQ_FMT_INT4)
+                        ? make_rsrc(a.wscale + nb0 * Gp * 64, clamp_bytes((nsc - nb0 * Gp * 64) * 4))
+                        : make_rsrc(a.wscale, a.per_channel ? clamp_bytes(L * 4) : 4u);
+
+  // forward per-chunk constants: block bi, byte offset inside the block, row, part
+  uint32_t fblk[BWD ? 1 : C::CH], finb[BWD ? 1 : C::CH], fsrow[BWD ? 1 : C::CH], fpart[BWD ? 1 : C::CH];
+  if (!BWD) {
+#pragma unroll
+    for (int c = 0; c < C::CH; ++c) {
+      const int id = tid + NT * c;
+      const int per_blk = 64 * C::WPR;
+      const int bi = id / per_blk, inb = id % per_blk;
+      fblk[c] = (uint32_t)bi * (uint32_t)KB * blkb;
+      finb[c] = (uint32_t)inb * 16u;
+      fsrow[c] = (uint32_t)bi * Gp * 64u + (uint32_t)(inb / C::WPR);
+      fpart[c] = (uint32_t)(inb % C::WPR);
+    }
+  }
   // backward mapping: kc = tid % KCH (8 k), nc = (tid / KCH) % 8 (8 n); threads past
   // 8*KCH redo a block and write it to a private dummy slot
   const bool wthr_ok = BWD ? (tid < 8 * C::KCH) : true;
   const int bkc = BWD ? tid % C::KCH : 0;
   const int bnc = BWD ? (tid / C::KCH) % 8 : 0;
-  // backward per-thread column: packed byte offset and scale column, or out of bounds
-  // (a column past K gets offsets past every resource: row offsets stay below
-  // 2^31, so LRQ_OOB + row offset neither wraps nor lands inside)
   const int64_t bcol = e0 + bkc * 8;
-  const bool bcol_ok = bcol < K;
-  const uint32_t bcolb = bcol_ok ? (uint32_t)((FMT == LRQ_FMT_INT4) ? bcol / 2 : bcol) : LRQ_OOB;
-  const uint32_t bscol4 = bcol_ok ? ((FMT == LRQ_FMT_INT4) ? (uint32_t)(bcol >> a.gshift) * 4u : 0u) : LRQ_OOB;
-  // forward per-chunk row offsets
-  uint32_t frow[BWD ? 1 : C::CH], fsrow[BWD ? 1 : C::CH], fpart[BWD ? 1 : C::CH];
-  if (!BWD) {
-#pragma unroll
-    for (int c = 0; c < C::CH; ++c) {
-      const int id = tid + NT * c;
-      const int row = id / C::WPR;
-      frow[c] = (uint32_t)row * rowb;
-      fsrow[c] = (uint32_t)row * kgroups;
-      fpart[c] = (uint32_t)(id % C::WPR) * (FMT == LRQ_FMT_INT4 ? 32u : 16u);
-    }
-  }
+  const bool bcol_ok = bcol < KB * 64;  // columns in [K, 64*KB) are zero padding
+  const uint32_t bcolbyte = bcol_ok ? (uint32_t)((bcol >> 6) * blkb + ((FMT == LRQ_FMT_INT4) ? (bcol & 63) / 2 : (bcol & 63)))
+                                    : LRQ_OOB;
+  const uint32_t bscol = bcol_ok ? ((FMT == LRQ_FMT_INT4) ? (uint32_t)(bcol >> a.gshift) * 64u * 4u : 0u) : LRQ_OOB;
 
   u32x4 wf[2][BWD ? 1 : C::CH];            // forward packed chunks
   float wfs[2][BWD ? 1 : C::CH];           // forward chunk scales (int4)
   uint32_t wb[2][BWD ? 8 * C::WORDS : 1];  // backward 8 rows x 8 k
   float wbs[2][BWD ? 8 : 1];               // backward row scales
 
-  auto load_w = [&](int set, int64_t r0_) {
-    const uint32_t r0 = (uint32_t)r0_;
+  auto load_w = [&](int set, int kt) {
     if (!BWD) {
-      // forward: rows n = e0 + row, reduction k = r0 + part * (32 | 16)
 #pragma unroll
       for (int c = 0; c < C::CH; ++c) {
-        const uint32_t kk = r0 + fpart[c];
-        const bool kok = kk < (uint32_t)K;
+        const uint32_t off = fblk[c] + (uint32_t)kt * blkb + finb[c];
+        wf[set][c] = bload16(rw, off);
         if (FMT == LRQ_FMT_INT4) {
-          wf[set][c] = bload16(rw, kok ? frow[c] + kk / 2 : LRQ_OOB);
-          wfs[set][c] = bloadf(rs, kok ? (fsrow[c] + (kk >> a.gshift)) * 4 : LRQ_OOB);
-        } else {
-          wf[set][c] = bload16(rw, kok ? frow[c] + kk : LRQ_OOB);
+          const uint32_t j = ((uint32_t)kt * 64u + fpart[c] * 32u) >> a.gshift;
+          wfs[set][c] = bloadf(rs, (fsrow[c] + j * 64u) * 4u);
         }
       }
     } else {
-      // backward: rows n = r0 + nc*8 + i, column bcol
+      // rows n = kt*64 + nc*8 + i: block row kt, in-block rows nc*8 + i
+      const uint32_t rbase = (uint32_t)kt * (uint32_t)KB * blkb + (uint32_t)(bnc * 8) * rowb + bcolbyte;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const uint32_t n = r0 + (uint32_t)(bnc * 8 + i);
         if (FMT == LRQ_FMT_INT4) {
-          wb[set][i] = bload4(rw, n * rowb + bcolb);
-          wbs[set][i] = bloadf(rs, n * kgroups * 4u + bscol4);
+          wb[set][i] = bload4(rw, rbase + (uint32_t)i * rowb);
         } else {
-          const u32x2 v = bload8(rw, n * rowb + bcolb);
+          const u32x2 v = bload8(rw, rbase + (uint32_t)i * rowb);
           wb[set][2 * i] = v[0];
           wb[set][2 * i + 1] = v[1];
-          wbs[set][i] = bloadf(rs, (a.per_channel ? n * 4u : 0u) + bscol4);
         }
+      }
+      if (FMT == LRQ_FMT_INT4) {
+        const uint32_t soff = ((uint32_t)kt * Gp * 64u + (uint32_t)(bnc * 8)) * 4u + bscol;
+        const u32x4 s0 = bload16(rs, soff), s1 = bload16(rs, soff + 16u);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          wbs[set][i] = __builtin_bit_cast(float, s0[i]);
+          wbs[set][4 + i] = __builtin_bit_cast(float, s1[i]);
+        }
+      } else if (a.per_channel) {
+        const uint32_t soff = bcol_ok ? ((uint32_t)kt * 64u + (uint32_t)(bnc * 8)) * 4u : LRQ_OOB;
+        const u32x4 s0 = bload16(rs, soff), s1 = bload16(rs, soff + 16u);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          wbs[set][i] = __builtin_bit_cast(float, s0[i]);
+          wbs[set][4 + i] = __builtin_bit_cast(float, s1[i]);
+        }
+      } else {
+        const float s = bloadf(rs, bcol_ok ? 0u : LRQ_OOB);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) wbs[set][i] = s;
       }
     }
   };
 
-  // dequantize one register set into LDS buffer `buf`; `part` in 0..3 selects
+  // dequantize one register set into weight buffer `buf`; `part` in 0..3 selects
   // a quarter of the work so it can be spread over the four MFMA sub-steps.
   uint32_t bpk[BWD ? 32 : 1];  // backward: packed row pairs [pair][k]
   auto store_w = [&](int set, int buf, int part) {
-    uint16_t* sA = lds + buf * C::BUF;
+    uint16_t* sA = sW + buf * C::WBUF;
     if (!BWD) {
 #pragma unroll
       for (int c = 0; c < C::CH; ++c) {
         const int id = tid + NT * c;
-        const int row = id / C::WPR, pt = id % C::WPR;
+        const int per_blk = 64 * C::WPR;
+        const int row = (id / per_blk) * 64 + (id % per_blk) / C::WPR;
+        const int pt = (id % per_blk) % C::WPR;
         if (FMT == LRQ_FMT_INT4) {
           uint16_t* dst = sA + row * LD + pt * 32 + part * 8;
-          st16(dst, dequant8_int4_bf16(wf[set][c][part], wfs[set][c]));
+          st16(dst, dequant8_int4_bf16(wf[set][c][part], wfs[set][c], a.nib));
         } else {
           uint16_t* dst = sA + row * LD + pt * 16 + part * 4;
           const u32x2 p = fp8x4_to_bf16(wf[set][c][part]);
@@ -204,8 +249,8 @@ k_gemm(GemmArgs a, int tiles_m) {
       // rows 2*part, 2*part+1 -> 8 packed dwords (one per k); writes at part 3
       float f0[8], f1[8];
       if (FMT == LRQ_FMT_INT4) {
-        dequant8_int4_f32(wb[set][2 * part], wbs[set][2 * part], f0);
-        dequant8_int4_f32(wb[set][2 * part + 1], wbs[set][2 * part + 1], f1);
+        dequant8_int4_f32(wb[set][2 * part], wbs[set][2 * part], f0, a.nib);
+        dequant8_int4_f32(wb[set][2 * part + 1], wbs[set][2 * part + 1], f1, a.nib);
       } else {
         fp8x4_to_f32(wb[set][4 * part], f0);
         fp8x4_to_f32(wb[set][4 * part + 1], f0 + 4);
@@ -224,7 +269,7 @@ k_gemm(GemmArgs a, int tiles_m) {
         for (int q = 0; q < 8; ++q) {
           const int R = bkc * 8 + q;
           const int phys = bnc ^ ((R >> 3) & 7);
-          uint16_t* dst = wthr_ok ? (sA + R * LD + phys * 8) : (lds + 2 * C::BUF + tid * 8);
+          uint16_t* dst = wthr_ok ? (sA + R * LD + phys * 8) : (sDummy + tid * 8);
           u32x4 o = {bpk[q], bpk[8 + q], bpk[16 + q], bpk[24 + q]};
           st16(dst, o);
         }
@@ -246,71 +291,73 @@ k_gemm(GemmArgs a, int tiles_m) {
     return as_bf16x8(ld16(sA + R * LD + phys * 8));
   };
 
-  // one reduction step on LDS buffer `buf` with activations act[p]; the
-  // dequantization of register set `wset` into `nbuf` rides along. The
-  // fragments of sub-step kk+1 are read from LDS while sub-step kk's
-  // matrix-core work runs, and the schedule interleaves every matrix-core
-  // instruction with ~3 VALU (dequantization) and spreads the LDS writes and
-  // global loads between them, so one wavefront per SIMD keeps the matrix
-  // pipe fed while it converts the next tile.
-  auto step = [&](int p, int buf, int wset, int nbuf) {
-    const uint16_t* sA = lds + buf * C::BUF;
-    bf16x8 fa[2][NI];
+  // one reduction step on buffers `buf`; the dequantization of register set
+  // `wset` into weight buffer `nbuf` rides along. Fragments of sub-step kk+1
+  // are read while sub-step kk's matrix-core work runs, and the schedule
+  // interleaves every matrix-core instruction with ~3 VALU (dequantization)
+  // and spreads LDS writes and global loads between them.
+  auto step = [&](int buf, int wset, int nbuf) {
+    const uint16_t* sA = sW + buf * C::WBUF;
+    bf16x8 fa[2][NI], fb[2][MJ];
 #pragma unroll
     for (int i = 0; i < NI; ++i) fa[0][i] = afrag(sA, i * 32 + l32, g * 4);
+#pragma unroll
+    for (int j = 0; j < MJ; ++j) fb[0][j] = bfrag(buf, j, g * 4);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       const int cur = kk & 1;
       if (kk < 3) {
 #pragma unroll
         for (int i = 0; i < NI; ++i) fa[cur ^ 1][i] = afrag(sA, i * 32 + l32, g * 4 + kk + 1);
+#pragma unroll
+        for (int j = 0; j < MJ; ++j) fb[cur ^ 1][j] = bfrag(buf, j, g * 4 + kk + 1);
       }
 #pragma unroll
       for (int i = 0; i < NI; ++i)
 #pragma unroll
-        for (int j = 0; j < MJ; ++j) acc[i][j] = mfma32(fa[cur][i], as_bf16x8(act[p][j][kk]), acc[i][j]);
+        for (int j = 0; j < MJ; ++j) acc[i][j] = mfma32(fa[cur][i], fb[cur][j], acc[i][j]);
       store_w(wset, nbuf, kk);
     }
-    constexpr int NM = 4 * NI * MJ;           // matrix-core instructions in the step
-    constexpr int NW = BWD ? 8 : 4 * C::CH;   // LDS tile writes
+    constexpr int NM = 4 * NI * MJ;               // matrix-core instructions in the step
+    constexpr int NR = 3 * (NI + MJ);             // fragment reads after the first sub-step
+    constexpr int NW = BWD ? 8 : 4 * C::CH;       // LDS tile writes
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
       __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // VALU
-      if (m % (NI * MJ) < NI && m < NM - NI * MJ)
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read (next sub-step)
+      if ((m * NR) / NM != ((m + 1) * NR) / NM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
       if ((m * NW) / NM != ((m + 1) * NW) / NM) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
       if (m % 4 == 1) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
     }
   };
 
   const int nk = (int)((L + BK - 1) / BK);
-  auto kclamp = [&](int kt) -> int64_t { return (int64_t)(kt < nk ? kt : nk - 1) * BK; };
+  auto kc_ = [&](int kt) -> int { return kt < nk ? kt : nk - 1; };
 
-  // prologue: tile 0 -> LDS buffer 0, tile 1 raw -> set 1, act(0) -> act[0]
+  // prologue: act(0) -> sX[0]; weight tile 0 -> sW[0]; tile 1 raw -> set 1
+  dma_act(0, 0);
   load_w(0, 0);
-  load_w(1, kclamp(1));
-  load_act(act[0], 0);
+  load_w(1, kc_(1));
 #pragma unroll
   for (int part = 0; part < 4; ++part) store_w(0, 0, part);
   __syncthreads();
 
   int kt = 0;
   for (; kt + 1 < nk; kt += 2) {
-    // even step: compute buffer 0 / act[0]; dequantize set 1 (tile kt+1) into buffer 1
-    load_act(act[1], kclamp(kt + 1));
-    load_w(0, kclamp(kt + 2));
-    step(0, 0, 1, 1);
+    // even step: compute buffers 0; stage act(kt+1) and weight tile kt+1 into buffers 1
+    dma_act(1, (int64_t)(kt + 1) * BK);
+    load_w(0, kc_(kt + 2));
+    step(0, 1, 1);
     __syncthreads();
-    // odd step: compute buffer 1 / act[1]; dequantize set 0 (tile kt+2) into buffer 0
-    load_act(act[0], kclamp(kt + 2));
-    load_w(1, kclamp(kt + 3));
-    step(1, 1, 0, 0);
+    // odd step: compute buffers 1; stage act(kt+2) and weight tile kt+2 into buffers 0
+    dma_act(0, (int64_t)kc_(kt + 2) * BK);
+    load_w(1, kc_(kt + 3));
+    step(1, 0, 0);
     __syncthreads();
   }
   if (kt < nk) {
-    // last (even) step; the dequantized tile it stages is never read
-    step(0, 0, 1, 1);
+    // last (even) step; what it stages is never read
+    step(0, 1, 1);
     __syncthreads();
   }
 
@@ -328,10 +375,10 @@ k_gemm(GemmArgs a, int tiles_m) {
   }
 
   // LoRA: one rank-wide step. A-role rows: B^T (forward, B is [r, E]) or A
-  // (backward, A is [E, r]) staged through LDS buffer 0; B-role: t or u
+  // (backward, A is [E, r]) staged through weight buffer 0; B-role: t or u
   // [M, rp] (zero-padded, pre-scaled) from global.
   if (a.rp > 0) {
-    uint16_t* sA = lds;
+    uint16_t* sA = sW;
     const int rp = a.rp, r = a.r;
     if (!BWD) {
       // B[j][e0 + c*8 .. +8] -> sA[(c*8 + q) * LD + j]

@@ -3,7 +3,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "../../include/loractl_rocm.h"
+#include "loractl_rocm.h"
 
 // lrq_quant.hip
 hipError_t launch_quantize_int4(hipStream_t st, const float* w, int64_t n, int64_t k, int g,
@@ -11,6 +11,8 @@ hipError_t launch_quantize_int4(hipStream_t st, const float* w, int64_t n, int64
 hipError_t launch_quantize_fp8(hipStream_t st, const float* w, int64_t n, int64_t k,
                                int per_channel, uint8_t* bytes, float* scales, float* amax_ws);
 hipError_t launch_dequant(hipStream_t st, const lrq_weight* w, void* out, bool bf16);
+void blocked_sizes(int fmt, int64_t n, int64_t k, int64_t group, int64_t* data_bytes, int64_t* scale_count);
+hipError_t launch_block(hipStream_t st, const lrq_weight* w, uint8_t* data, float* scales);
 
 // Arguments of the fused GEMM (lrq_gemm.hip), one struct for both passes:
 //   forward  : act = x  [m, k], l = k, e = n; lact = t [m, rp]; lw = B [r, n]
@@ -23,6 +25,7 @@ struct GemmArgs {
   const float* wscale;
   int group;
   int gshift;            // log2(group) (int4 blocks are powers of two)
+  uint32_t nib;          // 0x0f0f0f0f, passed opaquely (see dequant8_int4_f32)
   int per_channel;
   const float* bias;     // forward only, [n] or null
   const uint16_t* lact;  // [m, rp] pre-scaled LoRA activation, or null
@@ -66,5 +69,6 @@ enum {
   KID_LORA_U,
   KID_LORA_DA,
   KID_LORA_DB,
+  KID_BLOCK,
   KID_COUNT
 };

@@ -140,19 +140,66 @@ __global__ void __launch_bounds__(256) k_fp8_encode(const float* __restrict__ w,
   reinterpret_cast<uint32_t*>(out)[tid] = word;
 }
 
+// ------------------------------------------------------------------ blocked layout
+// The fused GEMMs read the frozen weight in 64 (n) x 64 (k) blocks that are
+// contiguous in memory (int4: 64 rows x 32 bytes; fp8: 64 rows x 64 bytes),
+// block (nb, kb) at (nb * KB + kb) * block bytes, KB = ceil(k / 64); int4
+// scales as [NB][Gp][64] (Gp = 64*KB / group). Rows past n and columns past
+// k are padding: int4 nibbles 8 (q = 0) with scale 0, fp8 bytes 0.
+LRQ_DEV int64_t blk_data_off(int fmt, int64_t n, int64_t k, int64_t KB) {
+  const int64_t rb = (fmt == LRQ_FMT_INT4) ? 32 : 64;  // bytes per block row
+  const int64_t kb = k >> 6, kin = k & 63;
+  return (((n >> 6) * KB + kb) * 64 + (n & 63)) * rb + ((fmt == LRQ_FMT_INT4) ? (kin >> 1) : kin);
+}
+
+// one thread per 16 output bytes of the blocked data
+__global__ void __launch_bounds__(256) k_block_data(const uint8_t* __restrict__ src, int64_t n, int64_t k,
+                                                    int fmt, int64_t NB, int64_t KB, uint8_t* __restrict__ dst) {
+  const int64_t rb = (fmt == LRQ_FMT_INT4) ? 32 : 64;
+  const int64_t chunks = NB * KB * 64 * (rb / 16);
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (tid >= chunks) return;
+  const int64_t per_row = rb / 16, per_blk = 64 * per_row;
+  const int64_t blk = tid / per_blk, inb = tid % per_blk;
+  const int64_t nb = blk / KB, kb = blk % KB;
+  const int64_t row = nb * 64 + inb / per_row;
+  const int64_t kcol = kb * 64 + (inb % per_row) * ((fmt == LRQ_FMT_INT4) ? 32 : 16);
+  u32x4 v;
+  const uint32_t fill = (fmt == LRQ_FMT_INT4) ? 0x88888888u : 0u;
+  v[0] = v[1] = v[2] = v[3] = fill;
+  if (row < n && kcol < k) {
+    const int64_t rowb = (fmt == LRQ_FMT_INT4) ? k / 2 : k;
+    v = ld16(src + row * rowb + ((fmt == LRQ_FMT_INT4) ? kcol / 2 : kcol));
+  }
+  st16(dst + tid * 16, v);
+}
+
+__global__ void __launch_bounds__(256) k_block_scales(const float* __restrict__ src, int64_t n, int64_t G,
+                                                      int64_t NB, int64_t Gp, float* __restrict__ dst) {
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (tid >= NB * Gp * 64) return;
+  const int64_t r = tid & 63, j = (tid >> 6) % Gp, nb = (tid >> 6) / Gp;
+  const int64_t row = nb * 64 + r;
+  dst[tid] = (row < n && j < G) ? src[row * G + j] : 0.0f;
+}
+
 // ------------------------------------------------------------------ dequantize
 // int4 -> f32 (bit-exact q*s) or bf16 operand; one thread per 8-value run.
 template <bool BF16>
 __global__ void __launch_bounds__(256) k_dequant_int4(const uint8_t* __restrict__ packed,
                                                       const float* __restrict__ scales, int64_t n,
-                                                      int64_t k, int g, void* __restrict__ out) {
+                                                      int64_t k, int g, int blocked, void* __restrict__ out) {
   const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t runs = n * (k / 8);
   if (tid >= runs) return;
   const int64_t row = tid / (k / 8);
   const int64_t kk = (tid % (k / 8)) * 8;
-  const uint32_t word = reinterpret_cast<const uint32_t*>(packed + row * (k / 2))[kk / 8];
-  const float s = scales[row * (k / g) + kk / g];
+  const int64_t KB = (k + 63) / 64;
+  const int64_t Gp = KB * 64 / g;
+  const int64_t doff = blocked ? blk_data_off(LRQ_FMT_INT4, row, kk, KB) : row * (k / 2) + kk / 2;
+  const int64_t soff = blocked ? (((row >> 6) * Gp + kk / g) * 64 + (row & 63)) : row * (k / g) + kk / g;
+  const uint32_t word = *reinterpret_cast<const uint32_t*>(packed + doff);
+  const float s = scales[soff];
   if (BF16) {
     st16(reinterpret_cast<uint16_t*>(out) + row * k + kk, dequant8_int4_bf16(word, s));
   } else {
@@ -170,15 +217,17 @@ __global__ void __launch_bounds__(256) k_dequant_int4(const uint8_t* __restrict_
 template <bool BF16>
 __global__ void __launch_bounds__(256) k_dequant_fp8(const uint8_t* __restrict__ bytes,
                                                      const float* __restrict__ scales, int64_t n,
-                                                     int64_t k, int per_channel, void* __restrict__ out) {
+                                                     int64_t k, int per_channel, int blocked,
+                                                     void* __restrict__ out) {
   const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t quads = n * k / 4;
   if (tid >= quads) return;
-  const uint32_t word = reinterpret_cast<const uint32_t*>(bytes)[tid];
+  const int64_t row = (tid * 4) / k, kk = (tid * 4) % k;
+  const int64_t doff = blocked ? blk_data_off(LRQ_FMT_FP8, row, kk, (k + 63) / 64) : tid * 4;
+  const uint32_t word = *reinterpret_cast<const uint32_t*>(bytes + doff);
   if (BF16) {
     reinterpret_cast<u32x2*>(out)[tid] = fp8x4_to_bf16(word);
   } else {
-    const int64_t row = (tid * 4) / k;
     const float s = per_channel ? scales[row] : scales[0];
     f32x4 o;
 #pragma unroll
@@ -216,22 +265,43 @@ hipError_t launch_dequant(hipStream_t st, const lrq_weight* w, void* out, bool b
   const int64_t n = w->n, k = w->k;
   if (n == 0 || k == 0) return hipSuccess;
   const uint8_t* d = reinterpret_cast<const uint8_t*>(w->data);
+  const int blocked = w->layout == LRQ_LAYOUT_BLOCKED;
   if (w->format == LRQ_FMT_INT4) {
     const int64_t runs = n * (k / 8);
     if (bf16)
       hipLaunchKernelGGL(k_dequant_int4<true>, dim3(blocks_for(runs, 256)), dim3(256), 0, st, d,
-                         w->scales, n, k, w->group, out);
+                         w->scales, n, k, w->group, blocked, out);
     else
       hipLaunchKernelGGL(k_dequant_int4<false>, dim3(blocks_for(runs, 256)), dim3(256), 0, st, d,
-                         w->scales, n, k, w->group, out);
+                         w->scales, n, k, w->group, blocked, out);
   } else {
     const int64_t quads = n * k / 4;
     if (bf16)
       hipLaunchKernelGGL(k_dequant_fp8<true>, dim3(blocks_for(quads, 256)), dim3(256), 0, st, d,
-                         w->scales, n, k, w->per_channel, out);
+                         w->scales, n, k, w->per_channel, blocked, out);
     else
       hipLaunchKernelGGL(k_dequant_fp8<false>, dim3(blocks_for(quads, 256)), dim3(256), 0, st, d,
-                         w->scales, n, k, w->per_channel, out);
+                         w->scales, n, k, w->per_channel, blocked, out);
   }
+  return hipGetLastError();
+}
+
+void blocked_sizes(int fmt, int64_t n, int64_t k, int64_t group, int64_t* data_bytes, int64_t* scale_count) {
+  const int64_t NB = (n + 63) / 64, KB = (k + 63) / 64;
+  *data_bytes = NB * KB * 64 * (fmt == LRQ_FMT_INT4 ? 32 : 64);
+  *scale_count = (fmt == LRQ_FMT_INT4) ? NB * (KB * 64 / group) * 64 : 0;
+}
+
+hipError_t launch_block(hipStream_t st, const lrq_weight* w, uint8_t* data, float* scales) {
+  const int64_t n = w->n, k = w->k;
+  const int64_t NB = (n + 63) / 64, KB = (k + 63) / 64;
+  int64_t db = 0, sc = 0;
+  blocked_sizes(w->format, n, k, w->group, &db, &sc);
+  if (db == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_block_data, dim3(blocks_for(db / 16, 256)), dim3(256), 0, st,
+                     reinterpret_cast<const uint8_t*>(w->data), n, k, w->format, NB, KB, data);
+  if (w->format == LRQ_FMT_INT4 && sc > 0)
+    hipLaunchKernelGGL(k_block_scales, dim3(blocks_for(sc, 256)), dim3(256), 0, st, w->scales, n,
+                       k / w->group, NB, KB * 64 / w->group, scales);
   return hipGetLastError();
 }

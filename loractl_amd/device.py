@@ -11,7 +11,7 @@ from __future__ import annotations
 
 import ctypes
 import threading
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 from typing import Optional
 
 import torch
@@ -95,6 +95,8 @@ class PackedWeight:
     group: int = 0
     per_channel: bool = False
     bias: Optional[torch.Tensor] = None
+    layout: int = L.LRQ_LAYOUT_ROWS
+    _blocked: Optional["PackedWeight"] = field(default=None, repr=False, compare=False)
 
     def desc(self) -> L.LrqWeight:
         return L.LrqWeight(
@@ -105,7 +107,7 @@ class PackedWeight:
             data=self.data.data_ptr(),
             scales=self.scales.data_ptr(),
             per_channel=int(self.per_channel),
-            reserved=0,
+            layout=self.layout,
             bias=None if self.bias is None else self.bias.data_ptr(),
         )
 
@@ -113,12 +115,48 @@ class PackedWeight:
     def device(self) -> torch.device:
         return self.data.device
 
+    @property
+    def blocked(self) -> bool:
+        return self.layout == L.LRQ_LAYOUT_BLOCKED
+
     def with_bias(self, bias: Optional[torch.Tensor]) -> "PackedWeight":
-        return PackedWeight(self.fmt, self.n, self.k, self.data, self.scales, self.group,
-                            self.per_channel, bias)
+        w = PackedWeight(self.fmt, self.n, self.k, self.data, self.scales, self.group,
+                         self.per_channel, bias, self.layout)
+        if self._blocked is not None:
+            w._blocked = self._blocked.with_bias(bias)
+        return w
+
+
+def compute_weight(w: PackedWeight) -> PackedWeight:
+    """The blocked form the fused kernels read (made once per weight and cached)."""
+    if w.blocked:
+        return w
+    if w._blocked is None:
+        w._blocked = block(w)
+    return w._blocked
 
 
 # ------------------------------------------------------------------ formats
+def block(w: PackedWeight) -> PackedWeight:
+    """Re-lay a row-layout weight into the blocked layout the fused kernels read."""
+    if w.blocked:
+        return w
+    ctx = context(w.device.index)
+    db = ctypes.c_int64()
+    ns = ctypes.c_int64()
+    rc = ctx.lib.lrq_weight_blocked_size(w.fmt, w.n, w.k, w.group if w.fmt == L.LRQ_FMT_INT4 else 64,
+                                         ctypes.byref(db), ctypes.byref(ns))
+    ctx.check(rc, "lrq_weight_blocked_size")
+    data = torch.empty((db.value,), dtype=torch.uint8, device=w.device)
+    if w.fmt == L.LRQ_FMT_INT4:
+        scales = torch.empty((ns.value,), dtype=torch.float32, device=w.device)
+    else:
+        scales = w.scales
+    d = w.desc()
+    ctx.check(ctx.lib.lrq_weight_block(ctx.h, ctypes.byref(d), _ptr(data), _ptr(scales)), "lrq_weight_block")
+    return PackedWeight(w.fmt, w.n, w.k, data, scales, w.group, w.per_channel, w.bias, L.LRQ_LAYOUT_BLOCKED)
+
+
 def quantize_int4(w: torch.Tensor, group: int) -> PackedWeight:
     """quantize_linear_weight at Q4S (src/quant.rs:74-82) on the GPU."""
     _need(w, torch.float32, "w")
@@ -170,7 +208,7 @@ def quant_matmul_t(x: torch.Tensor, w: PackedWeight) -> torch.Tensor:
         raise ValueError(f"x must be [m, {w.k}], got {tuple(x.shape)}")
     ctx = context(x.device.index)
     y = torch.empty((m, w.n), dtype=torch.bfloat16, device=x.device)
-    d = w.desc()
+    d = compute_weight(w).desc()
     ctx.check(ctx.lib.lrq_quant_matmul_t(ctx.h, ctypes.byref(d), _ptr(x), m, _ptr(y)), "lrq_quant_matmul_t")
     return y
 
@@ -183,7 +221,7 @@ def quant_matmul_t_bwd(dy: torch.Tensor, w: PackedWeight) -> torch.Tensor:
         raise ValueError(f"dy must be [m, {w.n}], got {tuple(dy.shape)}")
     ctx = context(dy.device.index)
     dx = torch.empty((m, w.k), dtype=torch.bfloat16, device=dy.device)
-    d = w.desc()
+    d = compute_weight(w).desc()
     ctx.check(ctx.lib.lrq_quant_matmul_t_bwd(ctx.h, ctypes.byref(d), _ptr(dy), m, _ptr(dx)),
               "lrq_quant_matmul_t_bwd")
     return dx
@@ -202,7 +240,7 @@ def lora_fwd(x: torch.Tensor, w: PackedWeight, a: torch.Tensor, b: torch.Tensor,
         y = torch.empty((m, w.n), dtype=torch.bfloat16, device=x.device)
     if t is None:
         t = torch.empty((m, r), dtype=torch.bfloat16, device=x.device)
-    d = w.desc()
+    d = compute_weight(w).desc()
     ctx.check(ctx.lib.lrq_lora_fwd(ctx.h, ctypes.byref(d), _ptr(x), m, _ptr(a), _ptr(b), r,
                                    float(scaling), _ptr(y), _ptr(t)), "lrq_lora_fwd")
     return y, t
@@ -226,7 +264,7 @@ def lora_bwd(x: torch.Tensor, dy: torch.Tensor, w: PackedWeight, a: torch.Tensor
         dx = torch.empty((m, w.k), dtype=torch.bfloat16, device=dy.device) if need_dx else None
         da = torch.empty((w.k, r), dtype=torch.float32, device=dy.device) if need_da else None
         db = torch.empty((r, w.n), dtype=torch.float32, device=dy.device) if need_db else None
-    d = w.desc()
+    d = compute_weight(w).desc()
     ctx.check(ctx.lib.lrq_lora_bwd(ctx.h, ctypes.byref(d), _ptr(x), _ptr(dy), m, _ptr(a), _ptr(b), r,
                                    float(scaling), _ptr(t), _ptr(dx), _ptr(da), _ptr(db)), "lrq_lora_bwd")
     return dx, da, db

@@ -87,7 +87,10 @@ def quantize_linear_weight(weight: torch.Tensor, value: QuantValue = QuantValue.
     _check_block(d_out, d_in, group)
     if value is QuantValue.Q8S:
         raise NotImplementedError("compute.backend rocm implements Q4S (int4) and fp8 bases; Q8S is not built")
-    return D.quantize_int4(weight.float().contiguous(), group)
+    if group & (group - 1):
+        raise ValueError(f"compute.backend rocm needs a power-of-two quant block, got {group}")
+    # quantize in the interchange row layout, keep the blocked layout the fused kernels read
+    return D.block(D.quantize_int4(weight.float().contiguous(), group))
 
 
 def dequant_chunk_rows(d_out: int, d_in: int, chunk_bytes: int) -> List[int]:
@@ -103,13 +106,15 @@ def dequant_chunk_rows(d_out: int, d_in: int, chunk_bytes: int) -> List[int]:
 def quantize_linear_weight_chunked(weight: torch.Tensor, value: QuantValue = QuantValue.Q4S,
                                    chunk_bytes: int = DEFAULT_DEQUANT_CHUNK_MIB << 20,
                                    group: int = QUANT_BLOCK) -> List[D.PackedWeight]:
+    """Row chunks in the interchange row layout (QuantLinear joins and blocks them)."""
     d_out, d_in = weight.shape
+    _check_block(d_out, d_in, group)
+    if value is QuantValue.Q8S:
+        raise NotImplementedError("compute.backend rocm implements Q4S (int4) and fp8 bases; Q8S is not built")
     rows = dequant_chunk_rows(d_out, d_in, chunk_bytes)
-    if len(rows) == 1:
-        return [quantize_linear_weight(weight, value, group)]
     out, start = [], 0
     for r in rows:
-        out.append(quantize_linear_weight(weight[start:start + r], value, group))
+        out.append(D.quantize_int4(weight[start:start + r].float().contiguous(), group))
         start += r
     return out
 
@@ -124,6 +129,8 @@ def concat_chunks(chunks: List[D.PackedWeight]) -> D.PackedWeight:
         raise ValueError("row chunks of one weight must share format, d_in and block")
     if c0.fmt == D.L.LRQ_FMT_FP8 and any(c.per_channel != c0.per_channel for c in chunks):
         raise ValueError("fp8 row chunks must share the scale kind")
+    if any(c.blocked for c in chunks):
+        raise ValueError("row chunks are joined in the row layout; block the joined weight afterwards")
     data = torch.cat([c.data for c in chunks], 0).contiguous()
     if c0.fmt == D.L.LRQ_FMT_FP8 and not c0.per_channel:
         if any(not torch.equal(c.scales, c0.scales) for c in chunks):

@@ -107,3 +107,37 @@ def test_fp8_dequant_golden_on_gpu(cuda, case):
                         per_channel=scale.size > 1)
     out = D.dequant(pw).cpu().numpy()[:, :3].reshape(-1)
     assert np.array_equal(out.view(np.uint32), np.array(c["expected"], np.float32).view(np.uint32))
+
+
+@pytest.mark.parametrize("fmt,N,K,g", [("int4", 72, 96, 32), ("int4", 130, 256, 64), ("int4", 64, 512, 128),
+                                       ("fp8", 40, 96, 0), ("fp8", 200, 320, 0)])
+def test_blocked_layout_roundtrip(cuda, fmt, N, K, g):
+    """The blocked device layout dequantizes bit-identically to the row layout
+    (padding rows and columns included), and places bytes where the layout
+    definition says (spot-checked against the row layout)."""
+    w = (rng(N * K).standard_normal((N, K)) * 0.3).astype(np.float32)
+    t = torch.from_numpy(w).to(cuda)
+    rows = D.quantize_int4(t, g) if fmt == "int4" else D.quantize_fp8(t, True)
+    blk = D.block(rows)
+    assert blk.blocked and not rows.blocked
+    a = D.dequant(rows).cpu().numpy()
+    b = D.dequant(blk).cpu().numpy()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert torch.equal(D.dequant_bf16(rows), D.dequant_bf16(blk))
+    # layout spot checks: row n, byte j of the row layout sits at block (n/64, k/64)
+    KB = (K + 63) // 64
+    rb = 32 if fmt == "int4" else 64
+    src = rows.data.cpu().numpy()
+    dst = blk.data.cpu().numpy()
+    for n_, kk in [(0, 0), (N - 1, K - 8), (N // 2, K // 2)]:
+        kk -= kk % (2 if fmt == "int4" else 1)
+        off = (((n_ // 64) * KB + kk // 64) * 64 + n_ % 64) * rb + ((kk % 64) // 2 if fmt == "int4" else kk % 64)
+        assert dst[off] == src[n_, kk // 2 if fmt == "int4" else kk]
+    if fmt == "int4":
+        NB = (N + 63) // 64
+        Gp = KB * 64 // g
+        sc = blk.scales.cpu().numpy().reshape(NB, Gp, 64)
+        ref = rows.scales.cpu().numpy()
+        assert np.array_equal(sc[(N - 1) // 64, (K - 1) // g, (N - 1) % 64], ref[N - 1, (K - 1) // g])
+        if N % 64:
+            assert not sc[NB - 1, :, N % 64:].any()  # padding rows carry scale 0
