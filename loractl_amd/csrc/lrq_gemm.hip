@@ -205,16 +205,16 @@ k_gemm(GemmArgs a, int tiles_m) {
         const u32x4 s0 = bload16(rs, soff), s1 = bload16(rs, soff + 16u);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          wbs[set][i] = __builtin_bit_cast(float, s0[i]);
-          wbs[set][4 + i] = __builtin_bit_cast(float, s1[i]);
+          wbs[set][i] = __uint_as_float(s0[i]);
+          wbs[set][4 + i] = __uint_as_float(s1[i]);
         }
       } else if (a.per_channel) {
         const uint32_t soff = bcol_ok ? ((uint32_t)kt * 64u + (uint32_t)(bnc * 8)) * 4u : LRQ_OOB;
         const u32x4 s0 = bload16(rs, soff), s1 = bload16(rs, soff + 16u);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          wbs[set][i] = __builtin_bit_cast(float, s0[i]);
-          wbs[set][4 + i] = __builtin_bit_cast(float, s1[i]);
+          wbs[set][i] = __uint_as_float(s0[i]);
+          wbs[set][4 + i] = __uint_as_float(s1[i]);
         }
       } else {
         const float s = bloadf(rs, bcol_ok ? 0u : LRQ_OOB);
@@ -318,16 +318,16 @@ k_gemm(GemmArgs a, int tiles_m) {
         for (int j = 0; j < MJ; ++j) acc[i][j] = mfma32(fa[cur][i], fb[cur][j], acc[i][j]);
       store_w(wset, nbuf, kk);
     }
-    constexpr int NM = 4 * NI * MJ;               // matrix-core instructions in the step
-    constexpr int NR = 3 * (NI + MJ);             // fragment reads after the first sub-step
+    constexpr int PS = NI * MJ;                   // matrix-core instructions per sub-step
+    constexpr int NM = 4 * PS;                    // ... per step
     constexpr int NW = BWD ? 8 : 4 * C::CH;       // LDS tile writes
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
       __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // VALU
-      if ((m * NR) / NM != ((m + 1) * NR) / NM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+      if (m / PS < 3 && (m % PS) < NI + MJ) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // next sub-step's reads
       if ((m * NW) / NM != ((m + 1) * NW) / NM) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
-      if (m % 4 == 1) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+      if (m % 5 == 2) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
     }
   };
 
