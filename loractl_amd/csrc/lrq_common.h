@@ -130,8 +130,24 @@ LRQ_DEV void st16(void* p, const u32x4& v) { *reinterpret_cast<u32x4*>(p) = v; }
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 constexpr uint32_t LRQ_OOB = 0x80000000u;  // an offset past any resource
 
+// Hide a value's provenance from the optimizer (no instruction is emitted).
+// Applied to a selected buffer offset, it keeps the compiler from sinking the
+// load into the arms of the select, which would turn a branch-free step into
+// divergent branches.
+LRQ_DEV uint32_t opaque_u32(uint32_t v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+// `base` and `bytes` must be wave-uniform; they are read from the first
+// active lane so the descriptor provably lives in scalar registers (without
+// that, the compiler may wrap every load in a per-lane loop).
 LRQ_DEV rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+  const uint64_t p = (uint64_t)base;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
+  void* u = (void*)(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(u, (short)0, __builtin_amdgcn_readfirstlane(bytes), 0x00020000);
 }
 LRQ_DEV u32x4 bload16(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0); }
 LRQ_DEV u32x2 bload8(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0); }

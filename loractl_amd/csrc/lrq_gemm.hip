@@ -17,18 +17,21 @@
 //     backward the reduction runs along n while the packed rows are
 //     contiguous along k, so each thread dequantizes an 8x8 block and writes
 //     it transposed (XOR-swizzled 16-byte chunks keep the LDS banks apart);
-//   - the activation operand (x or dy) goes straight from global memory into
-//     matrix-core registers, one reduction step ahead: each wavefront reads
-//     only its own 64 tokens, so it needs no LDS;
+//   - the activation operand (x or dy) is copied global -> LDS by buffer
+//     loads with an LDS destination (no register round trip), one reduction
+//     step ahead; each wavefront moves and reads only its own 64 tokens, in
+//     XOR-swizzled 16-byte chunks;
 //   - v_mfma_f32_32x32x16_bf16 with the weight as the A-role operand, so the
 //     accumulators hold 4 consecutive output features of one token and the
 //     epilogue writes 8-byte runs. The reduction index is permuted inside a
 //     step (lane group g takes k = 32g + 8kk .. +8 in sub-step kk) so each
 //     lane's activation bytes are 64 contiguous bytes;
 //   - the loop is unrolled by two steps so every buffer index is static and
-//     the whole step is one basic block: loads are clamped in bounds and
-//     zeroed by selects, the next tile's dequantization is interleaved with
-//     the current tile's matrix-core work, and one barrier ends each step;
+//     the whole step is one basic block: buffer loads past a resource's size
+//     return zeros, so edges need no branches (buffer descriptors are forced
+//     scalar and selected offsets made opaque so the compiler cannot
+//     reintroduce branches), the next tile's dequantization is interleaved
+//     with the current tile's matrix-core work, and one barrier ends a step;
 //   - the LoRA term is one more rank-wide step after the main loop (the
 //     weight-side factor B or A staged through LDS, t or u from global);
 //   - fp8 per-output-channel scales factor out of the forward reduction and
@@ -121,7 +124,7 @@ k_gemm(GemmArgs a, int tiles_m) {
     lds_void* base = (lds_void*)(sX + buf * C::XBUF + wv * (32 * MJ) * BK);
 #pragma unroll
     for (int c = 0; c < 4 * MJ; ++c) {
-      const uint32_t off = kok ? doff0 + (uint32_t)(c * 8 * L * 2) + koff : LRQ_OOB;
+      const uint32_t off = opaque_u32(kok ? doff0 + (uint32_t)(c * 8 * L * 2) + koff : LRQ_OOB);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(ract, (lds_void*)((__attribute__((address_space(3))) char*)base + c * 8 * BK * 2),
                                                16, off, 0, 0, 0);
     }
@@ -171,6 +174,10 @@ k_gemm(GemmArgs a, int tiles_m) {
                                     : LRQ_OOB;
   const uint32_t bscol = bcol_ok ? ((FMT == LRQ_FMT_INT4) ? (uint32_t)(bcol >> a.gshift) * 64u * 4u : 0u) : LRQ_OOB;
 
+  // backward fp8: per-channel scale offsets, or the one scalar scale (loop invariant)
+  const uint32_t fp8_pc_off = (a.per_channel && bcol_ok) ? 0u : LRQ_OOB;
+  const float fp8_scalar = (BWD && FMT == LRQ_FMT_FP8 && !a.per_channel) ? bloadf(rs, bcol_ok ? 0u : LRQ_OOB) : 0.0f;
+
   u32x4 wf[2][BWD ? 1 : C::CH];            // forward packed chunks
   float wfs[2][BWD ? 1 : C::CH];           // forward chunk scales (int4)
   uint32_t wb[2][BWD ? 8 * C::WORDS : 1];  // backward 8 rows x 8 k
@@ -208,18 +215,16 @@ k_gemm(GemmArgs a, int tiles_m) {
           wbs[set][i] = __uint_as_float(s0[i]);
           wbs[set][4 + i] = __uint_as_float(s1[i]);
         }
-      } else if (a.per_channel) {
-        const uint32_t soff = bcol_ok ? ((uint32_t)kt * 64u + (uint32_t)(bnc * 8)) * 4u : LRQ_OOB;
+      } else {
+        // per-channel rows read their scales; with one scalar scale the loads
+        // fall outside the 4-byte resource (zeros) and the scalar is added
+        const uint32_t soff = fp8_pc_off + (uint32_t)kt * 256u + (uint32_t)(bnc * 32);
         const u32x4 s0 = bload16(rs, soff), s1 = bload16(rs, soff + 16u);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          wbs[set][i] = __uint_as_float(s0[i]);
-          wbs[set][4 + i] = __uint_as_float(s1[i]);
+          wbs[set][i] = __uint_as_float(s0[i]) + fp8_scalar;
+          wbs[set][4 + i] = __uint_as_float(s1[i]) + fp8_scalar;
         }
-      } else {
-        const float s = bloadf(rs, bcol_ok ? 0u : LRQ_OOB);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) wbs[set][i] = s;
       }
     }
   };
@@ -321,10 +326,14 @@ k_gemm(GemmArgs a, int tiles_m) {
     constexpr int PS = NI * MJ;                   // matrix-core instructions per sub-step
     constexpr int NM = 4 * PS;                    // ... per step
     constexpr int NW = BWD ? 8 : 4 * C::CH;       // LDS tile writes
+    // VALU per step (dequantization + addressing), measured from the ISA:
+    // ~105 per 16-byte chunk forward, ~215 for the backward 8x8 block
+    constexpr int NV = BWD ? 216 : 106 * C::CH;
+    constexpr int VPM = (NV + NM - 1) / NM;
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // VALU
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, VPM, 0);  // VALU
       if (m / PS < 3 && (m % PS) < NI + MJ) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // next sub-step's reads
       if ((m * NW) / NM != ((m + 1) * NW) / NM) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
       if (m % 5 == 2) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
