@@ -6,6 +6,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <algorithm>
 #include <new>
 #include <vector>
 
@@ -33,7 +34,7 @@ struct lrq_ctx {
 namespace {
 
 const char* kNames[KID_COUNT] = {"quantize_int4", "quantize_fp8", "dequant", "fwd_main", "bwd_dx",
-                                 "lora_prep",     "lora_t",       "lora_u",  "lora_da",  "lora_db",
+                                 "lora_t",        "lora_u",       "lora_da", "lora_db",  "lora_reduce",
                                  "block"};
 
 int fail(lrq_ctx* c, int code, const char* fmt, ...) {
@@ -116,14 +117,14 @@ struct Slab {
 };
 
 int ensure_ws(lrq_ctx* c, size_t bytes) {
-  if (bytes <= c->ws_bytes) return LRQ_OK;
+  if (c->ws && bytes <= c->ws_bytes) return LRQ_OK;
   // stream-ordered users of the old buffer must finish before it goes
   hipError_t e = hipStreamSynchronize(c->stream);
   if (e != hipSuccess) return hip_fail(c, e, "hipStreamSynchronize");
   if (c->ws) (void)hipFree(c->ws);
   c->ws = nullptr;
   c->ws_bytes = 0;
-  size_t want = (size_t)round_up((int64_t)bytes, 1 << 20);
+  size_t want = (size_t)round_up((int64_t)(bytes > 0 ? bytes : 1), 1 << 20);
   e = hipMalloc(&c->ws, want);
   if (e != hipSuccess) {
     c->ws = nullptr;
@@ -133,35 +134,36 @@ int ensure_ws(lrq_ctx* c, size_t bytes) {
   return LRQ_OK;
 }
 
-// Workspace layout of the fused calls (sizes only when base == nullptr).
+// Workspace layout of the fused calls (sizes only when base == nullptr): t
+// and u padded to rp columns (the GEMM epilogue operands) and the f32
+// partials of the LoRA reductions (t or u; dA and dB side by side).
 struct LoraWs {
-  uint16_t *at, *bt, *tp, *ap, *tt, *up, *ut;
-  float* partial;
+  uint16_t *tp, *up;
+  float *pn, *pa, *pb;
   size_t bytes;
 };
 
 LoraWs lora_layout(char* base, int64_t m, int64_t n, int64_t k, int rp) {
   Slab s{base};
   LoraWs w{};
-  const int64_t mp = round_up(m > 0 ? m : 1, 64);
-  w.at = s.take<uint16_t>((int64_t)rp * k);
-  w.bt = s.take<uint16_t>(n * rp);
   w.tp = s.take<uint16_t>(m * rp);
-  w.ap = s.take<uint16_t>(k * rp);
-  w.tt = s.take<uint16_t>((int64_t)rp * mp);
   w.up = s.take<uint16_t>(m * rp);
-  w.ut = s.take<uint16_t>((int64_t)rp * mp);
-  const int64_t p_nt_t = (int64_t)skinny_nt_splits(m, k) * m * rp;
-  const int64_t p_nt_u = (int64_t)skinny_nt_splits(m, n) * m * rp;
-  const int64_t p_tn_a = (int64_t)skinny_tn_splits(m, k) * k * rp;
-  const int64_t p_tn_b = (int64_t)skinny_tn_splits(m, n) * n * rp;
-  int64_t p = p_nt_t;
-  if (p_nt_u > p) p = p_nt_u;
-  if (p_tn_a > p) p = p_tn_a;
-  if (p_tn_b > p) p = p_tn_b;
-  w.partial = s.take<float>(p > 0 ? p : 1);
+  const int64_t nt = std::max((int64_t)lora_plan_nt(m, k, rp).splits, (int64_t)lora_plan_nt(m, n, rp).splits);
+  w.pn = s.take<float>(std::max(nt * m * rp, (int64_t)1));
+  w.pa = s.take<float>((int64_t)lora_plan_tn(m, k, rp).splits * k * rp);
+  w.pb = s.take<float>((int64_t)lora_plan_tn(m, n, rp).splits * n * rp);
   w.bytes = s.off;
   return w;
+}
+
+// Shape limit of the LoRA kernels: 32-bit buffer offsets over one slice.
+int check_lora_shapes(lrq_ctx* c, int64_t m, int64_t n, int64_t k, int rp) {
+  const LoraPlan pa = lora_plan_tn(m, k, rp), pb = lora_plan_tn(m, n, rp);
+  const int64_t span = std::max(std::max(16 * std::max(n, k), (pa.per + 256) * k), (pb.per + 256) * n) * 2;
+  if (span >= (int64_t)1 << 31)
+    return fail(c, LRQ_EUNSUPPORTED, "LoRA shape m=%lld n=%lld k=%lld exceeds 2 GiB per slice",
+                (long long)m, (long long)n, (long long)k);
+  return LRQ_OK;
 }
 
 int check_weight(lrq_ctx* c, const lrq_weight* w, bool gemm) {
@@ -376,16 +378,15 @@ static int fwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t 
     if (r > 64) return fail(c, LRQ_EINVAL, "rank %lld outside [1, 64]", (long long)r);
     if (!aligned16(b)) return fail(c, LRQ_EINVAL, "B must be 16-byte aligned");
     const int rp = (int)round_up(r, 16);
+    LRQ_TRY(check_lora_shapes(c, m, w->n, w->k, rp));
     LRQ_TRY(ensure_ws(c, lora_layout(nullptr, m, w->n, w->k, rp).bytes));
     LoraWs ws = lora_layout(c->ws, m, w->n, w->k, rp);
-    // A [k, r] -> At [rp, k] (zero-padded rank) for the t pre-pass
-    LRQ_TRY(run(c, KID_LORA_PREP, "lora_prep", [&] {
-      return launch_pad_transpose(c->stream, a, w->k, r, r, ws.at, rp, w->k, true);
-    }));
     // t = s . x . A   (bf16 [m, rp] for the fused step, [m, r] for the caller)
+    const LoraPlan pt = lora_plan_nt(m, w->k, rp);
     LRQ_TRY(run(c, KID_LORA_T, "lora_t", [&] {
-      return launch_skinny_nt(c->stream, x, ws.at, m, w->k, (int)r, rp, scaling, ws.partial,
-                              skinny_nt_splits(m, w->k), ws.tp, nullptr, 0, t_out, (int)r);
+      hipError_t e = launch_lora_nt(c->stream, x, a, false, r, (int)r, m, w->k, rp, pt, ws.pn);
+      if (e != hipSuccess) return e;
+      return launch_nt_reduce(c->stream, ws.pn, pt.splits, m, rp, (int)r, scaling, ws.tp, t_out);
     }));
     ga.lact = ws.tp;
     ga.lw = b;
@@ -423,37 +424,40 @@ static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const ui
       return fail(c, LRQ_EINVAL, "dA needs x and dB needs t (16-byte aligned)");
     if (!aligned16(b)) return fail(c, LRQ_EINVAL, "B must be 16-byte aligned");
     const int rp = (int)round_up(r, 16);
-    const int64_t mp = round_up(m > 0 ? m : 1, 64);
+    LRQ_TRY(check_lora_shapes(c, m, w->n, w->k, rp));
     LRQ_TRY(ensure_ws(c, lora_layout(nullptr, m, w->n, w->k, rp).bytes));
     LoraWs ws = lora_layout(c->ws, m, w->n, w->k, rp);
-    if (db) {
-      // t [m, r] -> tt [rp, mp] (zero-padded) for the dB reduction over tokens
-      LRQ_TRY(run(c, KID_LORA_PREP, "lora_prep", [&] {
-        return launch_pad_transpose(c->stream, t, m, r, r, ws.tt, rp, mp, true);
-      }));
-    }
-    // u = s . dy . B^T   ([m, rp] for dx, [rp, mp] for dA)
+    // u = s . dy . B^T   (bf16 [m, rp]: the dx epilogue operand and dA's factor)
+    const LoraPlan pu = lora_plan_nt(m, w->n, rp);
     LRQ_TRY(run(c, KID_LORA_U, "lora_u", [&] {
-      return launch_skinny_nt(c->stream, dy, b, m, w->n, (int)r, rp, scaling, ws.partial,
-                              skinny_nt_splits(m, w->n), ws.up, ws.ut, mp, nullptr, 0);
+      hipError_t e = launch_lora_nt(c->stream, dy, b, true, w->n, (int)r, m, w->n, rp, pu, ws.pn);
+      if (e != hipSuccess) return e;
+      return launch_nt_reduce(c->stream, ws.pn, pu.splits, m, rp, (int)r, scaling, ws.up, nullptr);
     }));
     ga.lact = ws.up;
     ga.lw = a;
     ga.r = (int)r;
     ga.rp = rp;
     if (dx) LRQ_TRY(run(c, KID_BWD_DX, "bwd_dx", [&] { return launch_gemm(c->stream, true, w->format, ga); }));
+    // dA = x^T . u -> f32 [k, r] and dB = t^T . dy -> f32 [r, n]: token-slice
+    // partials, then one reduction launch for both
+    TnJob jobs[2];
+    int nj = 0;
     if (da) {
+      const LoraPlan pa = lora_plan_tn(m, w->k, rp);
       LRQ_TRY(run(c, KID_LORA_DA, "lora_da", [&] {
-        return launch_skinny_tn(c->stream, x, ws.ut, mp, m, w->k, (int)r, rp, ws.partial,
-                                skinny_tn_splits(m, w->k), da, r, 1);
+        return launch_lora_tn(c->stream, x, ws.up, rp, m, w->k, (int)r, rp, pa, ws.pa);
       }));
+      jobs[nj++] = TnJob{ws.pa, w->k, rp, (int)r, pa.splits, da, r, 1};
     }
     if (db) {
+      const LoraPlan pb = lora_plan_tn(m, w->n, rp);
       LRQ_TRY(run(c, KID_LORA_DB, "lora_db", [&] {
-        return launch_skinny_tn(c->stream, dy, ws.tt, mp, m, w->n, (int)r, rp, ws.partial,
-                                skinny_tn_splits(m, w->n), db, 1, w->n);
+        return launch_lora_tn(c->stream, dy, t, r, m, w->n, (int)r, rp, pb, ws.pb);
       }));
+      jobs[nj++] = TnJob{ws.pb, w->n, rp, (int)r, pb.splits, db, 1, w->n};
     }
+    if (nj) LRQ_TRY(run(c, KID_LORA_RED, "lora_reduce", [&] { return launch_tn_reduce(c->stream, jobs, nj); }));
     return LRQ_OK;
   }
   if (!dx) return LRQ_OK;

@@ -37,25 +37,36 @@ struct GemmArgs {
 hipError_t launch_gemm(hipStream_t st, bool bwd, int fmt, const GemmArgs& a);
 
 // lrq_lora.hip
-// out[m, j] = s * sum_c p[m, c] * q[j, c] over c < C, for j < R (rows j >= R
-// of q read as zero); written as bf16 [m, rp], optionally as bf16 [rp, ldT]
-// (columns m >= M zeroed) and as bf16 [m, r_user].
-hipError_t launch_skinny_nt(hipStream_t st, const uint16_t* p, const uint16_t* q, int64_t M,
-                            int64_t C, int R, int rp, float s, float* partial, int splits,
-                            uint16_t* out, uint16_t* outT, int64_t ldT, uint16_t* out_user,
-                            int r_user);
-// out(c, j) = sum_m p[m, c] * qT[j, m] (qT has leading dimension ldq >= M
-// rounded up to 64, zero past M); written as f32 at out[c*sc + j*sj], j < R.
-hipError_t launch_skinny_tn(hipStream_t st, const uint16_t* p, const uint16_t* qT, int64_t ldq,
-                            int64_t M, int64_t C, int R, int rp, float* partial, int splits,
-                            float* out, int64_t sc, int64_t sj);
-// Small layout kernels for the LoRA factors.
-hipError_t launch_pad_transpose(hipStream_t st, const uint16_t* src, int64_t rows, int64_t cols,
-                                int64_t ld_src, uint16_t* dst, int64_t dst_rows, int64_t dst_cols,
-                                bool transpose);
-
-int skinny_nt_splits(int64_t M, int64_t C);
-int skinny_tn_splits(int64_t M, int64_t C);
+// A split of a LoRA reduction: `tiles` output tiles x `splits` slices of
+// `per` columns (nt) or tokens (tn).
+struct LoraPlan {
+  int64_t tiles;
+  int64_t per;
+  int splits;
+};
+LoraPlan lora_plan_nt(int64_t M, int64_t C, int rp);
+LoraPlan lora_plan_tn(int64_t M, int64_t C, int rp);
+// partial[s][m][j] = sum over slice s of p[m, c] * q(j, c) (f32) for j < rp,
+// q(j, c) = q[j * ldq + c] when qrow (B [r, n]), else q[c * ldq + j] (A
+// [k, r]); entries j >= R read as zero. plan.splits * M * rp floats.
+hipError_t launch_lora_nt(hipStream_t st, const uint16_t* p, const uint16_t* q, bool qrow, int64_t ldq,
+                          int R, int64_t M, int64_t C, int rp, const LoraPlan& plan, float* partial);
+// out = bf16(s * sum_s partial[s]) as [M, rp] (columns >= r zero) and/or [M, r].
+hipError_t launch_nt_reduce(hipStream_t st, const float* partial, int splits, int64_t M, int rp, int r, float s,
+                            uint16_t* out, uint16_t* out_user);
+// partial[s][c][j] = sum over slice s of p[m, c] * q[m * ldq + j] (f32) for
+// c < C, j < rp (columns j >= R of q read as zero); plan.splits * C * rp floats.
+hipError_t launch_lora_tn(hipStream_t st, const uint16_t* p, const uint16_t* q, int64_t ldq, int64_t M,
+                          int64_t C, int R, int rp, const LoraPlan& plan, float* partial);
+// out[c * sc + j * sj] = sum_s partial[s][c][j] (slice order) for c < C, j < R.
+struct TnJob {
+  const float* partial;
+  int64_t C;
+  int rp, R, splits;
+  float* out;
+  int64_t sc, sj;
+};
+hipError_t launch_tn_reduce(hipStream_t st, const TnJob* jobs, int njobs);
 
 // kernel ids for the profiler (lrq_profile_*)
 enum {
@@ -64,11 +75,11 @@ enum {
   KID_DEQUANT,
   KID_FWD_MAIN,
   KID_BWD_DX,
-  KID_LORA_PREP,
   KID_LORA_T,
   KID_LORA_U,
   KID_LORA_DA,
   KID_LORA_DB,
+  KID_LORA_RED,
   KID_BLOCK,
   KID_COUNT
 };

@@ -1,256 +1,448 @@
 // The low-rank (LoRA) side products of the fused linear, as matrix-core
-// kernels with a deterministic two-stage reduction (no atomics):
+// kernels that stream the big operand once and reduce deterministically:
 //
 //   t  = s . x  . A      [m, r]  (src/lora.rs:199-203, A-linear then scale)
 //   u  = s . dy . B^T    [m, r]  (autodiff of the B-linear, input side)
 //   dA = x^T . u         [k, r]  (weight grad of the A-linear)
 //   dB = t^T . dy        [r, n]  (weight grad of the B-linear)
 //
-// "nt" kernels reduce along a contiguous dimension (t, u); "tn" kernels
-// reduce along the token dimension m, which is strided in memory, so the
-// token tile is transposed into LDS before it feeds the matrix cores.
-// Stage 1 writes f32 partial sums per split of the reduction; stage 2 sums
-// the splits in a fixed order.
+// All four read one large bf16 operand (x or dy, HBM-bound) against one
+// small rank-wide factor. Two kernel shapes cover them:
+//
+//   nt (t, u): the reduction runs along the contiguous dimension of p (k for
+//     x, n for dy). A workgroup owns 128 tokens and one column slice; the
+//     factor slice (B rows as stored, or A transposed in registers) is
+//     staged once in LDS and shared by the 8 wavefronts, each of which
+//     streams its own 16 token rows (64-byte runs per row and load). Slices
+//     write f32 partials; a small kernel sums them in slice order and writes
+//     the bf16 result.
+//   tn (dA, dB): the reduction runs over tokens, which are strided in p.
+//     Each lane loads an 8 (tokens) x 8 (columns) block with eight 16-byte
+//     loads and transposes it in registers (byte permutes), so every load is
+//     a contiguous 256-byte run per 16 lanes; the token-major factor (u or t)
+//     is transposed once into LDS. Workgroups own 128 columns and a token
+//     slice and write f32 partials; one small kernel sums the slices of both
+//     reductions in slice order.
+//
+// Nothing depends on timing: every sum has a fixed order, and no workgroup
+// waits for another.
 #include "lrq_common.h"
 #include "lrq_kernels.h"
 
 namespace {
 
-constexpr int NT = 256;
-constexpr int TARGET_WG = 768;
+constexpr int LW = 8;          // wavefronts per workgroup
+constexpr int LNT = 64 * LW;   // threads per workgroup
+
+// Transpose-pack: the 16-bit element `e` (0..7) of eight 8-element rows into
+// one 8-element vector (rows in order).
+LRQ_DEV u32x4 column8(const u32x4 (&v)[8], int e) {
+  const int d = e >> 1;
+  const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+  u32x4 o;
+  o[0] = __builtin_amdgcn_perm(v[1][d], v[0][d], sel);
+  o[1] = __builtin_amdgcn_perm(v[3][d], v[2][d], sel);
+  o[2] = __builtin_amdgcn_perm(v[5][d], v[4][d], sel);
+  o[3] = __builtin_amdgcn_perm(v[7][d], v[6][d], sel);
+  return o;
+}
 
 // ------------------------------------------------------------------ nt
-// partial[s][m][j] = sum_{c in split s} p[m][c] * q[j][c]; 64 rows per
-// workgroup (16 per wavefront), c in steps of 32 (one 16x16x32 MFMA per
-// 16-wide j tile).
-__global__ void __launch_bounds__(NT) k_skinny_nt(const uint16_t* __restrict__ p,
-                                                  const uint16_t* __restrict__ q, int64_t M,
-                                                  int64_t C, int R, int rp, int64_t c_per,
-                                                  float* __restrict__ partial) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t m0 = (int64_t)blockIdx.x * 64 + wave * 16;
-  const int split = blockIdx.y;
-  const int64_t c_lo = split * c_per;
-  const int64_t c_hi = min(C, c_lo + c_per);
-  const int64_t mrow = m0 + (lane & 15);
-  const bool mok = mrow < M;
-  const int koff = (lane >> 4) * 8;
-  const int jt_n = rp / 16;
+struct NtArgs {
+  const uint16_t* p;   // [M, C] bf16
+  const uint16_t* q;   // QROW: [R, ldq], row j over c (B [r, n]); else [C, ldq], row c over j (A [k, r])
+  int64_t M, C, ldq;
+  int R;               // valid factor rank entries (the rest read as zero)
+  int64_t c_per;       // columns per slice (multiple of 32)
+  float* partial;      // [splits][M][rp] f32
+};
 
-  f32x4 acc[4];
-#pragma unroll
-  for (int t = 0; t < 4; ++t) acc[t] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+constexpr int NQ_BYTES = 100 * 1024;  // factor slice in LDS
 
-  const uint16_t* prow = p + (mok ? mrow : 0) * C;
-  for (int64_t c = c_lo; c < c_hi; c += 32) {
-    const int64_t cc = c + koff;
-    const bool cok = cc < c_hi;
-    const bf16x8 fa = as_bf16x8(ld16_pred(prow + cc, mok && cok));
+// Stage the factor slice [c_lo, c_hi) into LDS as sQ[j][c - c_lo] (stride
+// SQ), zero outside j < R and c < c_hi. B rows copy straight across; A
+// arrives as 8 (c) x 8 (j) blocks transposed in registers.
+template <bool QROW, int RP>
+LRQ_DEV void stage_factor(const NtArgs& a, int64_t c_lo, int64_t c_hi, uint16_t* sQ, int SQ, int nthreads) {
+  const int tid = threadIdx.x;
+  const int64_t cols = c_hi - c_lo;
+  if (QROW && (a.ldq & 7) == 0) {
+    const int cpr = (int)(a.c_per / 8);  // 16-byte chunks per row
+    for (int id = tid; id < RP * cpr; id += nthreads) {
+      const int j = id / cpr, cc = (id % cpr) * 8;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (j < a.R && cc < cols) v = ld16(a.q + (int64_t)j * a.ldq + c_lo + cc);
+      *reinterpret_cast<u32x4*>(sQ + j * SQ + cc) = v;
+    }
+  } else if (!QROW && (a.ldq & 7) == 0) {
+    const int jb = RP / 8;
+    for (int blk = tid; blk < jb * (int)(a.c_per / 8); blk += nthreads) {
+      const int j0 = (blk % jb) * 8, cc = (blk / jb) * 8;
+      u32x4 v[8];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      if (t < jt_n) {
-        const int j = t * 16 + (lane & 15);
-        const bf16x8 fb = as_bf16x8(ld16_pred(q + (int64_t)(j < R ? j : 0) * C + cc, cok && j < R));
-        acc[t] = mfma16(fa, fb, acc[t]);
+      for (int i = 0; i < 8; ++i) {
+        v[i] = (u32x4){0u, 0u, 0u, 0u};
+        if (j0 < a.ldq && cc + i < cols) v[i] = ld16(a.q + (c_lo + cc + i) * a.ldq + j0);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        u32x4 cv = column8(v, e);
+        if (j0 + e >= a.R) cv = (u32x4){0u, 0u, 0u, 0u};
+        *reinterpret_cast<u32x4*>(sQ + (j0 + e) * SQ + cc) = cv;
       }
     }
-  }
-  float* out = partial + (int64_t)split * M * rp;
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    if (t < jt_n) {
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int64_t m = m0 + 4 * (lane >> 4) + v;
-        if (m < M) out[m * rp + t * 16 + (lane & 15)] = acc[t][v];
-      }
+  } else {
+    for (int64_t id = tid; id < (int64_t)RP * a.c_per; id += nthreads) {
+      const int j = (int)(id / a.c_per);
+      const int64_t cc = id % a.c_per;
+      uint16_t v = 0;
+      if (j < a.R && cc < cols) v = QROW ? a.q[(int64_t)j * a.ldq + c_lo + cc] : a.q[(c_lo + cc) * a.ldq + j];
+      sQ[j * SQ + cc] = v;
     }
   }
 }
 
-__global__ void __launch_bounds__(NT) k_nt_reduce(const float* __restrict__ partial, int splits,
-                                                  int64_t M, int64_t ldT, int rp, int R, float s,
-                                                  uint16_t* __restrict__ out,
-                                                  uint16_t* __restrict__ outT,
-                                                  uint16_t* __restrict__ out_user, int r_user) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= ldT * rp) return;
-  // j fastest for the [m, rp] outputs
+// partial[split][m][j] = sum over the slice's columns of p[m, c] * q(j, c).
+// A workgroup owns 128 tokens (16 per wavefront) and one column slice; the
+// factor slice is staged once in LDS and shared by the 8 wavefronts, which
+// each stream their own 16 token rows through a ring of D loads.
+template <int NJT, bool QROW>
+__global__ void __launch_bounds__(LNT) k_lora_nt(NtArgs a) {
+  constexpr int RP = 16 * NJT;
+  __shared__ __attribute__((aligned(16))) uint16_t sQ[NQ_BYTES / 2];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int split = blockIdx.y;
+  const int64_t c_lo = split * a.c_per;
+  const int64_t c_hi = min(a.C, c_lo + a.c_per);
+  const int64_t C = a.C;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int SQ = (int)a.c_per + 8;
+
+  const int64_t m0 = (int64_t)blockIdx.x * 128 + wv * 16;  // this wavefront's tokens
+  const int64_t rows = max((int64_t)0, min((int64_t)16, a.M - m0));
+  const rsrc_t rpv = make_rsrc(a.p + min(m0, a.M) * C, clamp_bytes(rows * C * 2));
+  const uint32_t roff = (uint32_t)(l16 * C * 2);
+
+  f32x4 acc[NJT];
+#pragma unroll
+  for (int jt = 0; jt < NJT; ++jt) acc[jt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+
+  // chunks of 32 columns; lane group g reads 8 of them; chunks past the
+  // slice load zeros (out-of-range offsets) and add nothing
+  const int64_t nchunks = (c_hi - c_lo + 31) / 32;
+  constexpr int D = 8;
+  u32x4 pv[D];
+  auto load = [&](int k, int64_t it) {
+    const int64_t c = c_lo + it * 32 + g * 8;
+    pv[k] = bload16(rpv, opaque_u32(c < c_hi ? roff + (uint32_t)(c * 2) : LRQ_OOB));
+  };
+  auto compute = [&](int k, int64_t it) {
+    const int cc = (int)(it * 32) + g * 8;  // slice-relative; < c_per + 32
+#pragma unroll
+    for (int jt = 0; jt < NJT; ++jt) {
+      const int off = min(cc, (int)a.c_per - 8);  // chunks past the slice: zero p, any finite q
+      acc[jt] = mfma16(as_bf16x8(pv[k]), as_bf16x8(ld16(sQ + (jt * 16 + l16) * SQ + off)), acc[jt]);
+    }
+  };
+  // the first loads overlap the factor staging
+#pragma unroll
+  for (int k = 0; k < D; ++k) load(k, k);
+  stage_factor<QROW, RP>(a, c_lo, c_hi, sQ, SQ, LNT);
+  __syncthreads();
+  for (int64_t it = 0; it < nchunks; it += D) {
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+      compute(k, it + k);
+      load(k, it + k + D);
+    }
+  }
+
+  // accumulator: token 4g+v of the wavefront's 16, rank column 16jt + l16
+  float* part = a.partial + (int64_t)split * a.M * RP;
+#pragma unroll
+  for (int jt = 0; jt < NJT; ++jt)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int64_t m = m0 + 4 * g + v;
+      if (m < a.M) part[m * RP + jt * 16 + l16] = acc[jt][v];
+    }
+}
+
+// out[m, j] = bf16(s * sum over splits (in order) of partial[sp][m][j]); as
+// [M, rp] (columns >= r zero) and/or [M, r].
+__global__ void __launch_bounds__(256) k_nt_reduce(const float* __restrict__ partial, int splits, int64_t M,
+                                                   int rp, int r, float s, uint16_t* __restrict__ out,
+                                                   uint16_t* __restrict__ out_user) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= M * rp) return;
   const int64_t m = idx / rp;
   const int j = (int)(idx % rp);
-  if (m >= M) {  // zero the padding columns of the transposed copy
-    if (outT) outT[(int64_t)j * ldT + m] = 0;
-    return;
+  const int64_t stride = M * rp;
+  float sum = 0.0f;
+  for (int s0 = 0; s0 < splits; s0 += 8) {
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = (s0 + i < splits) ? partial[(s0 + i) * stride + idx] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sum += v[i];
   }
-  float v = 0.0f;
-  for (int sp = 0; sp < splits; ++sp) v += partial[(int64_t)sp * M * rp + idx];
-  v = (j < R) ? v * s : 0.0f;
-  const uint16_t h = f32_to_bf16_bits(v);
+  const uint16_t h = f32_to_bf16_bits(j < r ? sum * s : 0.0f);
   if (out) out[idx] = h;
-  if (outT) outT[(int64_t)j * ldT + m] = h;
-  if (out_user && j < r_user) out_user[m * r_user + j] = h;
+  if (out_user && j < r) out_user[m * r + j] = h;
 }
 
 // ------------------------------------------------------------------ tn
-// partial[s][c][j] = sum_{m in split s} p[m][c] * qT[j][m]; 64 c per
-// workgroup (16 per wavefront). The p tile [64 m][64 c] is transposed into
-// LDS as [c][m] so the A-role fragment (8 consecutive m) is one 16-byte read.
-constexpr int TLD = 64 + 8;
+struct TnArgs {
+  const uint16_t* p;   // [M, C] bf16
+  const uint16_t* q;   // [M, ldq] bf16, columns j < R
+  int64_t M, C, ldq;
+  int R;
+  int64_t m_per;       // tokens per slice (multiple of 256)
+  float* partial;      // [splits][C][rp]
+};
 
-__global__ void __launch_bounds__(NT) k_skinny_tn(const uint16_t* __restrict__ p,
-                                                  const uint16_t* __restrict__ qT, int64_t ldq,
-                                                  int64_t M, int64_t C, int rp, int64_t m_per,
-                                                  float* __restrict__ partial) {
-  __shared__ __attribute__((aligned(16))) uint16_t sT[64 * TLD];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t c0 = (int64_t)blockIdx.x * 64;
+// partial[split][c][j] = sum over the split's tokens of p[m, c] * q[m, j].
+// A workgroup (4 wavefronts) owns 128 columns and one token slice;
+// wavefront w takes tokens [128 it + 32 w, +32) of every 128-token chunk.
+constexpr int TW = 4;            // wavefronts per tn workgroup
+constexpr int TNT = 64 * TW;
+constexpr int TQ_BYTES = 64 * 1024;  // factor slice in LDS (later reused for the combine)
+
+template <int NJT>
+__global__ void __launch_bounds__(TNT) k_lora_tn(TnArgs a) {
+  constexpr int RP = 16 * NJT;
+  static_assert(TW * 128 * 16 * 4 <= TQ_BYTES, "combine buffer fits the factor slice");
+  __shared__ __attribute__((aligned(16))) uint16_t sQ[TQ_BYTES / 2];
+  float* const red = reinterpret_cast<float*>(sQ);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t c0 = (int64_t)blockIdx.x * 128;
   const int split = blockIdx.y;
-  const int64_t m_lo = split * m_per;
-  const int64_t m_hi = min(M, m_lo + m_per);
-  const int jt_n = rp / 16;
-  const int koff = (lane >> 4) * 8;
+  const int64_t m_lo = split * a.m_per;
+  const int64_t m_hi = min(a.M, m_lo + a.m_per);
+  const int64_t C = a.C;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int64_t toks = m_hi - m_lo;
 
-  f32x4 acc[4];
-#pragma unroll
-  for (int t = 0; t < 4; ++t) acc[t] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+  const int SQ = (int)a.m_per + 8;
+  const rsrc_t rpv = make_rsrc(a.p + m_lo * C, clamp_bytes(toks * C * 2));
+  const int64_t col = c0 + l16 * 8;
+  const uint32_t coff = (col < C) ? (uint32_t)(col * 2) : LRQ_OOB;
 
-  // loader: 2 chunks per thread, chunk id -> row id/8, columns (id%8)*8
-  u32x4 pr[2];
-  auto gload = [&](int64_t mb) {
+  f32x4 acc[8][NJT];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int id = tid + NT * h;
-      const int row = id >> 3, cc = (id & 7) * 8;
-      const int64_t m = mb + row;
-      const bool ok = (m < m_hi) && (c0 + cc < C);
-      pr[h] = ld16_pred(p + (ok ? m : 0) * C + c0 + cc, ok);
+  for (int q = 0; q < 8; ++q)
+#pragma unroll
+    for (int jt = 0; jt < NJT; ++jt) acc[q][jt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+
+  const int64_t nchunks = (toks + 127) / 128;
+  u32x4 pv[2][8];
+  auto load = [&](int set, int64_t it) {
+    const int64_t mrow = it * 128 + wv * 32 + g * 8;  // slice-relative token of row 0
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t off = opaque_u32(coff + (uint32_t)((mrow + i) * C * 2));
+      pv[set][i] = bload16(rpv, off);
+    }
+  };
+  auto compute = [&](int set, int64_t it) {
+    const int64_t mrow = it * 128 + wv * 32 + g * 8;
+    bf16x8 fq[NJT];
+#pragma unroll
+    for (int jt = 0; jt < NJT; ++jt) fq[jt] = as_bf16x8(ld16(sQ + (jt * 16 + l16) * SQ + mrow));
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const bf16x8 fa = as_bf16x8(column8(pv[set], q));
+#pragma unroll
+      for (int jt = 0; jt < NJT; ++jt) acc[q][jt] = mfma16(fa, fq[jt], acc[q][jt]);
     }
   };
 
-  gload(m_lo);
-  for (int64_t mb = m_lo; mb < m_hi; mb += 64) {
+  load(0, 0);  // overlaps the factor staging
+  // factor slice q [m_lo, m_hi) x R -> LDS as [j][m - m_lo] (stride SQ):
+  // 8 (tokens) x 8 (j) blocks, loaded as rows and transposed in registers
+  if ((a.ldq & 7) == 0) {
+    const rsrc_t rq = make_rsrc(a.q + m_lo * a.ldq, clamp_bytes(toks * a.ldq * 2));
+    const int jb = RP / 8;
+    for (int blk = tid; blk < jb * (int)(a.m_per / 8); blk += TNT) {
+      const int j0 = (blk % jb) * 8, mm = (blk / jb) * 8;
+      u32x4 v[8];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int id = tid + NT * h;
-      const int row = id >> 3, cc = (id & 7) * 8;
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t off = opaque_u32(j0 < a.ldq ? (uint32_t)(((mm + i) * a.ldq + j0) * 2) : LRQ_OOB);
+        v[i] = bload16(rq, off);
+      }
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        sT[(cc + 2 * e) * TLD + row] = (uint16_t)(pr[h][e] & 0xffffu);
-        sT[(cc + 2 * e + 1) * TLD + row] = (uint16_t)(pr[h][e] >> 16);
+      for (int e = 0; e < 8; ++e) {
+        u32x4 cv = column8(v, e);
+        if (j0 + e >= a.R) cv = (u32x4){0u, 0u, 0u, 0u};
+        *reinterpret_cast<u32x4*>(sQ + (j0 + e) * SQ + mm) = cv;
       }
     }
-    __syncthreads();
-    if (mb + 64 < m_hi) gload(mb + 64);
-#pragma unroll
-    for (int ms = 0; ms < 2; ++ms) {
-      const bf16x8 fa = as_bf16x8(ld16(sT + (wave * 16 + (lane & 15)) * TLD + ms * 32 + koff));
-      const int64_t mm = mb + ms * 32 + koff;
-      const bool mok = mm < m_hi;
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        if (t < jt_n) {
-          const int j = t * 16 + (lane & 15);
-          const bf16x8 fb = as_bf16x8(ld16_pred(qT + (int64_t)j * ldq + (mok ? mm : 0), mok));
-          acc[t] = mfma16(fa, fb, acc[t]);
-        }
-      }
+  } else {
+    for (int64_t id = tid; id < (int64_t)RP * a.m_per; id += TNT) {
+      const int j = (int)(id % RP);
+      const int64_t mm = id / RP;
+      uint16_t v = 0;
+      if (j < a.R && mm < toks) v = a.q[(m_lo + mm) * a.ldq + j];
+      sQ[j * SQ + mm] = v;
     }
-    __syncthreads();
   }
-  float* out = partial + (int64_t)split * C * rp;
+  __syncthreads();
+
+  int64_t it = 0;
+  for (; it + 1 < nchunks; it += 2) {
+    load(1, it + 1);
+    compute(0, it);
+    load(0, it + 2);
+    compute(1, it + 1);
+  }
+  if (it < nchunks) compute(0, it);
+  __syncthreads();  // the factor slice's LDS becomes the combine buffer
+
+  // combine the wavefronts (fixed order), one 16-wide rank tile per round;
+  // accumulator row 4g+v of MFMA q is column c0 + 8*(4g+v) + q
+  float* part = a.partial + (int64_t)split * C * RP;
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    if (t < jt_n) {
+  for (int jt = 0; jt < NJT; ++jt) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const int64_t c = c0 + wave * 16 + 4 * (lane >> 4) + v;
-        if (c < C) out[c * rp + t * 16 + (lane & 15)] = acc[t][v];
+        const int cl = 8 * (4 * g + v) + q;
+        red[(wv * 128 + cl) * 16 + l16] = acc[q][jt][v];
       }
+    __syncthreads();
+    for (int id = tid; id < 128 * 16; id += TNT) {
+      const int cl = id / 16, jl = id % 16;
+      float sum = 0.0f;
+#pragma unroll
+      for (int w = 0; w < TW; ++w) sum += red[(w * 128 + cl) * 16 + jl];
+      if (c0 + cl < C) part[(c0 + cl) * RP + jt * 16 + jl] = sum;
     }
+    __syncthreads();
   }
 }
 
-__global__ void __launch_bounds__(NT) k_tn_reduce(const float* __restrict__ partial, int splits,
-                                                  int64_t C, int rp, int R, float* __restrict__ out,
-                                                  int64_t sc, int64_t sj) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= C * rp) return;
-  const int64_t c = idx / rp;
-  const int j = (int)(idx % rp);
-  if (j >= R) return;
-  float v = 0.0f;
-  for (int sp = 0; sp < splits; ++sp) v += partial[(int64_t)sp * C * rp + idx];
-  out[c * sc + (int64_t)j * sj] = v;
+// out[c * sc + j * sj] = sum over splits (in order) of partial[s][c][j], for
+// one or two reductions in one launch.
+struct TnReduce {
+  const float* partial;
+  int64_t C;
+  int rp, R, splits;
+  float* out;
+  int64_t sc, sj;
+  int64_t blocks;
+};
+
+__global__ void __launch_bounds__(256) k_tn_reduce(TnReduce j0, TnReduce j1) {
+  const bool second = blockIdx.x >= j0.blocks;
+  const TnReduce& t = second ? j1 : j0;
+  const int64_t idx = (int64_t)(blockIdx.x - (second ? j0.blocks : 0)) * 256 + threadIdx.x;
+  const int64_t c = idx / t.R;
+  const int j = (int)(idx % t.R);
+  if (c >= t.C) return;
+  const float* src = t.partial + c * t.rp + j;
+  const int64_t stride = t.C * t.rp;
+  float sum = 0.0f;
+  for (int s0 = 0; s0 < t.splits; s0 += 8) {
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = (s0 + i < t.splits) ? src[(s0 + i) * stride] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sum += v[i];
+  }
+  t.out[c * t.sc + (int64_t)j * t.sj] = sum;
 }
 
-// ------------------------------------------------------------------ layout
-__global__ void __launch_bounds__(NT) k_pad_transpose(const uint16_t* __restrict__ src, int64_t rows,
-                                                      int64_t cols, int64_t ld_src,
-                                                      uint16_t* __restrict__ dst, int64_t dst_rows,
-                                                      int64_t dst_cols, int transpose) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= dst_rows * dst_cols) return;
-  const int64_t dr = idx / dst_cols, dc = idx % dst_cols;
-  // dst[dr][dc] = transpose ? src[dc][dr] : src[dr][dc]
-  const int64_t sr = transpose ? dc : dr, sc = transpose ? dr : dc;
-  dst[idx] = (sr < rows && sc < cols) ? src[sr * ld_src + sc] : (uint16_t)0;
-}
-
-inline unsigned nblocks(int64_t items) { return (unsigned)((items + NT - 1) / NT); }
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 }  // namespace
 
-int skinny_nt_splits(int64_t M, int64_t C) {
-  const int64_t tiles = (M + 63) / 64;
-  int64_t s = (TARGET_WG + tiles - 1) / tiles;
-  const int64_t smax = (C + 255) / 256;  // keep >= 256 columns per split
-  if (s > smax) s = smax;
-  if (s < 1) s = 1;
-  return (int)s;
+// nt: 128-token tiles x column slices (multiples of 32) so that the grid is
+// ~256 workgroups (one per CU, 8 wavefronts each), within the LDS factor slice.
+LoraPlan lora_plan_nt(int64_t M, int64_t C, int rp) {
+  LoraPlan p{};
+  const int64_t tiles = cdiv(M > 0 ? M : 1, 128);
+  const int64_t want = cdiv(256, tiles);
+  int64_t per = 32 * cdiv(cdiv(C, want), 32);
+  const int64_t cap = ((NQ_BYTES / 2) / rp - 8) / 32 * 32;
+  if (per > cap) per = cap;
+  if (per < 32) per = 32;
+  p.per = per;
+  p.splits = (int)cdiv(C, per);
+  p.tiles = tiles;
+  return p;
 }
 
-int skinny_tn_splits(int64_t M, int64_t C) {
-  const int64_t tiles = (C + 63) / 64;
-  int64_t s = (TARGET_WG + tiles - 1) / tiles;
-  const int64_t smax = (M + 127) / 128;  // keep >= 128 tokens per split
-  if (s > smax) s = smax;
-  if (s < 1) s = 1;
-  return (int)s;
+// tn: token slices (multiples of 128) so that column tiles x slices ~ 512
+// workgroups (two resident per CU), within the LDS factor slice.
+LoraPlan lora_plan_tn(int64_t M, int64_t C, int rp) {
+  LoraPlan p{};
+  const int64_t tiles = cdiv(C, 128);
+  const int64_t want = cdiv(512, tiles);
+  int64_t per = 128 * cdiv(cdiv(M > 0 ? M : 1, want), 128);
+  const int64_t cap = ((TQ_BYTES / 2) / rp - 8) / 128 * 128;
+  if (per > cap) per = cap;
+  if (per < 128) per = 128;
+  p.per = per;
+  p.splits = (int)cdiv(M > 0 ? M : 1, per);
+  p.tiles = tiles;
+  return p;
 }
 
-hipError_t launch_skinny_nt(hipStream_t st, const uint16_t* p, const uint16_t* q, int64_t M,
-                            int64_t C, int R, int rp, float s, float* partial, int splits,
-                            uint16_t* out, uint16_t* outT, int64_t ldT, uint16_t* out_user,
-                            int r_user) {
+hipError_t launch_lora_nt(hipStream_t st, const uint16_t* p, const uint16_t* q, bool qrow, int64_t ldq,
+                          int R, int64_t M, int64_t C, int rp, const LoraPlan& plan, float* partial) {
   if (M == 0) return hipSuccess;
-  const int64_t c_per = ((C + splits - 1) / splits + 31) / 32 * 32;
-  const int used = (int)((C + c_per - 1) / c_per);
-  hipLaunchKernelGGL(k_skinny_nt, dim3((unsigned)((M + 63) / 64), (unsigned)used), dim3(NT), 0, st,
-                     p, q, M, C, R, rp, c_per, partial);
-  const int64_t ld = outT ? ldT : M;  // without a transposed copy only the M real rows exist
-  hipLaunchKernelGGL(k_nt_reduce, dim3(nblocks(ld * rp)), dim3(NT), 0, st, partial, used, M, ld,
-                     rp, R, s, out, outT, out_user, r_user);
+  NtArgs a{p, q, M, C, ldq, R, plan.per, partial};
+  const dim3 grid((unsigned)plan.tiles, (unsigned)plan.splits);
+  switch ((qrow ? 4 : 0) + rp / 16 - 1) {
+    case 0: hipLaunchKernelGGL((k_lora_nt<1, false>), grid, dim3(LNT), 0, st, a); break;
+    case 1: hipLaunchKernelGGL((k_lora_nt<2, false>), grid, dim3(LNT), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((k_lora_nt<3, false>), grid, dim3(LNT), 0, st, a); break;
+    case 3: hipLaunchKernelGGL((k_lora_nt<4, false>), grid, dim3(LNT), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((k_lora_nt<1, true>), grid, dim3(LNT), 0, st, a); break;
+    case 5: hipLaunchKernelGGL((k_lora_nt<2, true>), grid, dim3(LNT), 0, st, a); break;
+    case 6: hipLaunchKernelGGL((k_lora_nt<3, true>), grid, dim3(LNT), 0, st, a); break;
+    case 7: hipLaunchKernelGGL((k_lora_nt<4, true>), grid, dim3(LNT), 0, st, a); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 
-hipError_t launch_skinny_tn(hipStream_t st, const uint16_t* p, const uint16_t* qT, int64_t ldq,
-                            int64_t M, int64_t C, int R, int rp, float* partial, int splits,
-                            float* out, int64_t sc, int64_t sj) {
+hipError_t launch_nt_reduce(hipStream_t st, const float* partial, int splits, int64_t M, int rp, int r, float s,
+                            uint16_t* out, uint16_t* out_user) {
+  if (M == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_nt_reduce, dim3((unsigned)cdiv(M * rp, 256)), dim3(256), 0, st, partial, splits, M, rp, r,
+                     s, out, out_user);
+  return hipGetLastError();
+}
+
+hipError_t launch_lora_tn(hipStream_t st, const uint16_t* p, const uint16_t* q, int64_t ldq, int64_t M,
+                          int64_t C, int R, int rp, const LoraPlan& plan, float* partial) {
   if (C == 0) return hipSuccess;
-  const int64_t m_per = ((M + splits - 1) / splits + 63) / 64 * 64;
-  const int used = M == 0 ? 1 : (int)((M + m_per - 1) / m_per);
-  hipLaunchKernelGGL(k_skinny_tn, dim3((unsigned)((C + 63) / 64), (unsigned)used), dim3(NT), 0, st,
-                     p, qT, ldq, M, C, rp, m_per, partial);
-  hipLaunchKernelGGL(k_tn_reduce, dim3(nblocks(C * rp)), dim3(NT), 0, st, partial, used, C, rp, R,
-                     out, sc, sj);
+  TnArgs a{p, q, M, C, ldq, R, plan.per, partial};
+  const dim3 grid((unsigned)plan.tiles, (unsigned)plan.splits);
+  switch (rp / 16) {
+    case 1: hipLaunchKernelGGL(k_lora_tn<1>, grid, dim3(TNT), 0, st, a); break;
+    case 2: hipLaunchKernelGGL(k_lora_tn<2>, grid, dim3(TNT), 0, st, a); break;
+    case 3: hipLaunchKernelGGL(k_lora_tn<3>, grid, dim3(TNT), 0, st, a); break;
+    case 4: hipLaunchKernelGGL(k_lora_tn<4>, grid, dim3(TNT), 0, st, a); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 
-hipError_t launch_pad_transpose(hipStream_t st, const uint16_t* src, int64_t rows, int64_t cols,
-                                int64_t ld_src, uint16_t* dst, int64_t dst_rows, int64_t dst_cols,
-                                bool transpose) {
-  if (dst_rows * dst_cols == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_pad_transpose, dim3(nblocks(dst_rows * dst_cols)), dim3(NT), 0, st, src, rows,
-                     cols, ld_src, dst, dst_rows, dst_cols, transpose ? 1 : 0);
+hipError_t launch_tn_reduce(hipStream_t st, const TnJob* jobs, int njobs) {
+  TnReduce t[2] = {};
+  int64_t total = 0;
+  for (int i = 0; i < njobs && i < 2; ++i) {
+    const TnJob& j = jobs[i];
+    t[i] = TnReduce{j.partial, j.C, j.rp, j.R, j.splits, j.out, j.sc, j.sj, cdiv(j.C * j.R, 256)};
+    total += t[i].blocks;
+  }
+  if (total == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_tn_reduce, dim3((unsigned)total), dim3(256), 0, st, t[0], t[1]);
   return hipGetLastError();
 }
