@@ -7,9 +7,12 @@
 // are the two small products of src/lora.rs:199-203 and their autodiff,
 // with t = s.x.A and u = s.dy.B^T computed by the skinny kernels.)
 //
-// One kernel template serves both passes. A workgroup of 4 wavefronts owns
-// an RA x 256 output tile (RA weight-side rows: n forward, k backward; 256
-// tokens, 64 per wavefront):
+// One kernel template serves both passes. A workgroup owns an RA x 256
+// output tile (RA weight-side rows: n forward, k backward; 256 tokens in 4
+// token groups of 64). Each token group is served by WN wavefronts that
+// split the RA rows; WN = 2 (the large-tile forward) puts two wavefronts on
+// each SIMD, so one's dequantization and LDS traffic overlap the other's
+// matrix-core work:
 //   - the packed weight tile of each 64-wide reduction step is read from
 //     HBM/L2 in packed form (int4 nibbles or fp8 bytes), dequantized in
 //     registers and written once per workgroup into a double-buffered LDS
@@ -40,16 +43,26 @@
 //     (fma(u, s, -8s) == q*s);
 //   - workgroup ids are remapped so each XCD (own L2) works on a contiguous
 //     range of tiles.
+
 #include "lrq_common.h"
 #include "lrq_kernels.h"
 
 namespace {
 
 constexpr int BK = 64;      // reduction step
-constexpr int LD = BK + 8;  // LDS row stride in bf16 (144 bytes)
-constexpr int NT = 256;     // threads per workgroup
+// LDS layouts (gfx950 LDS: 64 banks x 4 bytes; a 16-byte access serves 16
+// lanes per pass, so each group of 16 lanes must cover distinct banks):
+//   activation tile [rows][64] bf16, 128-byte rows (the buffer-load DMA
+//     writes whole rows), 16-byte chunk c of row r stored at chunk
+//     c ^ ((r >> 1) & 7);
+//   weight tiles: 144-byte rows (8 bf16 of padding), no swizzle; 16
+//     consecutive rows then cover all 64 banks, and every writer and reader
+//     is mapped so that 16 consecutive lanes touch 16 consecutive rows at one
+//     chunk, or (backward transposed writes) 8 lanes fill one whole row.
+constexpr int LD = BK + 8;  // weight-tile row stride (bf16)
+LRQ_DEV int swz(int r) { return (r >> 1) & 7; }
 constexpr int MJ = 2;       // 32-token tiles per wavefront
-constexpr int RB = 4 * 32 * MJ;
+constexpr int RB = 4 * 32 * MJ;  // tokens per workgroup (4 token groups of 64)
 
 LRQ_DEV int xcd_remap(int bid, int nblk) {
   const int q = nblk / 8, r = nblk % 8;
@@ -67,8 +80,12 @@ LRQ_DEV void blocked_sizes_dev(int fmt, int64_t n, int64_t k, int64_t* data_byte
   *nscales = (fmt == LRQ_FMT_INT4) ? NB * ((KB * 64) >> gshift) * 64 : 0;
 }
 
-template <bool BWD, int FMT, int NI>
+// WN wavefronts share each token group, splitting its RA weight-side rows:
+// WN = 2 gives 8 wavefronts (two per SIMD) with half the accumulators each.
+template <bool BWD, int FMT, int NI, int WN>
 struct Cfg {
+  static constexpr int NT = 256 * WN;  // threads per workgroup
+  static constexpr int NIW = NI / WN;  // 32-row tiles per wavefront
   static constexpr int RA = 32 * NI;  // a multiple of 64 (whole weight blocks)
   // forward: 16-byte chunks of the packed weight tile per step, per thread
   static constexpr int WPR = (FMT == LRQ_FMT_INT4) ? 2 : 4;  // chunks per block row (64 k)
@@ -79,15 +96,17 @@ struct Cfg {
   static constexpr int WBUF = RA * LD;                          // weight tile (bf16)
   static constexpr int XBUF = RB * BK;                          // activation tile (bf16)
   static constexpr int LDS_ELEMS = 2 * WBUF + 2 * XBUF + (BWD ? NT * 8 : 0);
+  static_assert(NI % WN == 0, "whole row tiles per wavefront");
+  static_assert(BWD || CH * NT == RA * WPR, "whole 16-byte weight chunks per thread");
 };
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-template <bool BWD, int FMT, int NI>
-__global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1)))
+template <bool BWD, int FMT, int NI, int WN>
+__global__ void __launch_bounds__(256 * WN) __attribute__((amdgpu_waves_per_eu(WN, WN)))
 k_gemm(GemmArgs a, int tiles_m) {
-  using C = Cfg<BWD, FMT, NI>;
-  constexpr int RA = C::RA;
+  using C = Cfg<BWD, FMT, NI, WN>;
+  constexpr int RA = C::RA, NT = C::NT, NIW = C::NIW;
   __shared__ __attribute__((aligned(16))) uint16_t lds[C::LDS_ELEMS];
   uint16_t* const sW = lds;                     // [2][RA][LD]
   uint16_t* const sX = lds + 2 * C::WBUF;       // [2][256][64], 16-byte chunks XOR-swizzled by row
@@ -107,32 +126,44 @@ k_gemm(GemmArgs a, int tiles_m) {
   const int64_t M = a.m, L = a.l, E = a.e, K = a.wk;
   const int g = lane >> 5, l32 = lane & 31;
   const int wv = __builtin_amdgcn_readfirstlane(wave);
+  const int tw = wv & 3, rh = wv >> 2;  // token group, weight-row part
 
   // ---------------- activation operand: DMA into LDS, one reduction step ahead
-  // Wave wv moves its own 64 token rows (8 KB per step) with 8 buffer loads
-  // whose lanes cover 8 rows x 128 contiguous bytes each; lane l of load c
-  // lands at row c*8 + l/8, physical chunk l%8, which holds logical chunk
-  // (l%8) ^ (l/8). Rows past M read zeros through the resource size.
-  const int64_t mw = m0 + wv * (32 * MJ);
+  // The WN wavefronts of token group tw move its 64 token rows (8 KB per
+  // step) with 8 buffer loads, 8/WN each, whose lanes cover 8 rows x 128
+  // contiguous bytes each; lane l of load c lands at row c*8 + l/8, physical
+  // chunk l%8, and fetches logical chunk (l%8) ^ swz(row). Rows past M read
+  // zeros through the resource size.
+  const int64_t mw = m0 + tw * (32 * MJ);
   const int64_t mrows = (M - mw) < (32 * MJ) ? (M - mw) : (32 * MJ);
   const rsrc_t ract = make_rsrc(a.act + (mw < M ? mw : 0) * L, clamp_bytes(mrows * L * 2));
-  const int drow = lane >> 3, dq = (lane & 7) ^ (lane >> 3);
-  const uint32_t doff0 = (uint32_t)((drow * L + dq * 8) * 2);
+  // (l%8) ^ swz(c*8 + l/8); swz(c*8 + l/8) = (4c + l/16) & 7 alternates with
+  // the parity of c, so two offsets cover all eight loads.
+  const int drow = lane >> 3;
+  const int dq0 = (lane & 7) ^ ((lane >> 4) & 7), dq1 = (lane & 7) ^ (((lane >> 4) + 4) & 7);
+  const uint32_t doff0 = (uint32_t)((drow * L + dq0 * 8) * 2), doff1 = (uint32_t)((drow * L + dq1 * 8) * 2);
   auto dma_act = [&](int buf, int64_t k0) {
-    const bool kok = k0 + dq * 8 < L;  // L % 8 == 0
+    const bool kok0 = k0 + dq0 * 8 < L, kok1 = k0 + dq1 * 8 < L;  // L % 8 == 0
     const uint32_t koff = (uint32_t)(k0 * 2);
-    lds_void* base = (lds_void*)(sX + buf * C::XBUF + wv * (32 * MJ) * BK);
+    lds_void* base = (lds_void*)(sX + buf * C::XBUF + tw * (32 * MJ) * BK);
 #pragma unroll
-    for (int c = 0; c < 4 * MJ; ++c) {
-      const uint32_t off = opaque_u32(kok ? doff0 + (uint32_t)(c * 8 * L * 2) + koff : LRQ_OOB);
+    for (int cc = 0; cc < 4 * MJ / WN; ++cc) {
+      const int c = rh * (4 * MJ / WN) + cc;
+      const bool kok = (c & 1) ? kok1 : kok0;
+      const uint32_t doff = (c & 1) ? doff1 : doff0;
+      const uint32_t off = opaque_u32(kok ? doff + (uint32_t)(c * 8 * L * 2) + koff : LRQ_OOB);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(ract, (lds_void*)((__attribute__((address_space(3))) char*)base + c * 8 * BK * 2),
                                                16, off, 0, 0, 0);
     }
   };
+  // fragment of wave-local row j*32 + l32, logical chunk q: byte offset
+  // (row * 128) ^ ((q ^ swz(l32)) * 16); swz(j*32 + l32) = swz(l32). The XOR
+  // is done per read from an opaque base so the eight chunk addresses are not
+  // all kept live in registers.
+  const uint32_t xrow = (uint32_t)((tw * (32 * MJ) + l32) * BK * 2) | (uint32_t)(swz(l32) * 16);
   auto bfrag = [&](int buf, int j, int q) -> bf16x8 {
-    const int rl = j * 32 + l32;  // wave-local row
-    const int phys = q ^ (rl & 7);
-    return as_bf16x8(ld16(sX + buf * C::XBUF + (wv * (32 * MJ) + rl) * BK + phys * 8));
+    const uint32_t off = (opaque_u32(xrow) ^ (uint32_t)(q * 16)) + (uint32_t)((buf * C::XBUF + j * 32 * BK) * 2);
+    return as_bf16x8(ld16(reinterpret_cast<const char*>(sX) + off));
   };
 
   // ---------------- weight operand (blocked layout): packed loads, two register sets
@@ -157,17 +188,19 @@ k_gemm(GemmArgs a, int tiles_m) {
       const int id = tid + NT * c;
       const int per_blk = 64 * C::WPR;
       const int bi = id / per_blk, inb = id % per_blk;
+      const int brow = inb % 64, bpart = inb / 64;  // 16 lanes: 16 rows, one chunk
       fblk[c] = (uint32_t)bi * (uint32_t)KB * blkb;
-      finb[c] = (uint32_t)inb * 16u;
-      fsrow[c] = (uint32_t)bi * Gp * 64u + (uint32_t)(inb / C::WPR);
-      fpart[c] = (uint32_t)(inb % C::WPR);
+      finb[c] = (uint32_t)brow * rowb + (uint32_t)bpart * 16u;
+      fsrow[c] = (uint32_t)bi * Gp * 64u + (uint32_t)brow;
+      fpart[c] = (uint32_t)bpart;
     }
   }
-  // backward mapping: kc = tid % KCH (8 k), nc = (tid / KCH) % 8 (8 n); threads past
+  // backward mapping: nc = tid % 8 (8 n), kc = (tid / 8) % KCH (8 k), so the 8
+  // lanes of one k-row group write one whole 128-byte tile row; threads past
   // 8*KCH redo a block and write it to a private dummy slot
   const bool wthr_ok = BWD ? (tid < 8 * C::KCH) : true;
-  const int bkc = BWD ? tid % C::KCH : 0;
-  const int bnc = BWD ? (tid / C::KCH) % 8 : 0;
+  const int bnc = BWD ? tid % 8 : 0;
+  const int bkc = BWD ? (tid / 8) % C::KCH : 0;
   const int64_t bcol = e0 + bkc * 8;
   const bool bcol_ok = bcol < KB * 64;  // columns in [K, 64*KB) are zero padding
   const uint32_t bcolbyte = bcol_ok ? (uint32_t)((bcol >> 6) * blkb + ((FMT == LRQ_FMT_INT4) ? (bcol & 63) / 2 : (bcol & 63)))
@@ -232,6 +265,7 @@ k_gemm(GemmArgs a, int tiles_m) {
   // dequantize one register set into weight buffer `buf`; `part` in 0..3 selects
   // a quarter of the work so it can be spread over the four MFMA sub-steps.
   uint32_t bpk[BWD ? 32 : 1];  // backward: packed row pairs [pair][k]
+  u32x2 fp8_half[(!BWD && FMT == LRQ_FMT_FP8) ? C::CH : 1];  // forward fp8: pending half chunk
   auto store_w = [&](int set, int buf, int part) {
     uint16_t* sA = sW + buf * C::WBUF;
     if (!BWD) {
@@ -239,15 +273,20 @@ k_gemm(GemmArgs a, int tiles_m) {
       for (int c = 0; c < C::CH; ++c) {
         const int id = tid + NT * c;
         const int per_blk = 64 * C::WPR;
-        const int row = (id / per_blk) * 64 + (id % per_blk) / C::WPR;
-        const int pt = (id % per_blk) % C::WPR;
+        const int row = (id / per_blk) * 64 + (id % per_blk) % 64;
+        const int pt = (id % per_blk) / 64;
         if (FMT == LRQ_FMT_INT4) {
           uint16_t* dst = sA + row * LD + pt * 32 + part * 8;
           st16(dst, dequant8_int4_bf16(wf[set][c][part], wfs[set][c], a.nib));
         } else {
-          uint16_t* dst = sA + row * LD + pt * 16 + part * 4;
+          // two 4-value halves make one 16-byte write
           const u32x2 p = fp8x4_to_bf16(wf[set][c][part]);
-          *reinterpret_cast<u32x2*>(dst) = p;
+          if (part & 1) {
+            uint16_t* dst = sA + row * LD + pt * 16 + (part >> 1) * 8;
+            st16(dst, (u32x4){fp8_half[c][0], fp8_half[c][1], p[0], p[1]});
+          } else {
+            fp8_half[c] = p;
+          }
         }
       }
     } else {
@@ -273,8 +312,7 @@ k_gemm(GemmArgs a, int tiles_m) {
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
           const int R = bkc * 8 + q;
-          const int phys = bnc ^ ((R >> 3) & 7);
-          uint16_t* dst = wthr_ok ? (sA + R * LD + phys * 8) : (sDummy + tid * 8);
+          uint16_t* dst = wthr_ok ? (sA + R * LD + bnc * 8) : (sDummy + tid * 8);
           u32x4 o = {bpk[q], bpk[8 + q], bpk[16 + q], bpk[24 + q]};
           st16(dst, o);
         }
@@ -282,9 +320,9 @@ k_gemm(GemmArgs a, int tiles_m) {
     }
   };
 
-  f32x16 acc[NI][MJ];
+  f32x16 acc[NIW][MJ];
 #pragma unroll
-  for (int i = 0; i < NI; ++i)
+  for (int i = 0; i < NIW; ++i)
 #pragma unroll
     for (int j = 0; j < MJ; ++j)
 #pragma unroll
@@ -292,8 +330,7 @@ k_gemm(GemmArgs a, int tiles_m) {
 
   // A-role fragment of row R, logical 8-column chunk c
   auto afrag = [&](const uint16_t* sA, int R, int c) -> bf16x8 {
-    const int phys = BWD ? (c ^ ((R >> 3) & 7)) : c;
-    return as_bf16x8(ld16(sA + R * LD + phys * 8));
+    return as_bf16x8(ld16(sA + R * LD + c * 8));
   };
 
   // one reduction step on buffers `buf`; the dequantization of register set
@@ -303,9 +340,9 @@ k_gemm(GemmArgs a, int tiles_m) {
   // and spreads LDS writes and global loads between them.
   auto step = [&](int buf, int wset, int nbuf) {
     const uint16_t* sA = sW + buf * C::WBUF;
-    bf16x8 fa[2][NI], fb[2][MJ];
+    bf16x8 fa[2][NIW], fb[2][MJ];
 #pragma unroll
-    for (int i = 0; i < NI; ++i) fa[0][i] = afrag(sA, i * 32 + l32, g * 4);
+    for (int i = 0; i < NIW; ++i) fa[0][i] = afrag(sA, (rh * NIW + i) * 32 + l32, g * 4);
 #pragma unroll
     for (int j = 0; j < MJ; ++j) fb[0][j] = bfrag(buf, j, g * 4);
 #pragma unroll
@@ -313,17 +350,17 @@ k_gemm(GemmArgs a, int tiles_m) {
       const int cur = kk & 1;
       if (kk < 3) {
 #pragma unroll
-        for (int i = 0; i < NI; ++i) fa[cur ^ 1][i] = afrag(sA, i * 32 + l32, g * 4 + kk + 1);
+        for (int i = 0; i < NIW; ++i) fa[cur ^ 1][i] = afrag(sA, (rh * NIW + i) * 32 + l32, g * 4 + kk + 1);
 #pragma unroll
         for (int j = 0; j < MJ; ++j) fb[cur ^ 1][j] = bfrag(buf, j, g * 4 + kk + 1);
       }
 #pragma unroll
-      for (int i = 0; i < NI; ++i)
+      for (int i = 0; i < NIW; ++i)
 #pragma unroll
         for (int j = 0; j < MJ; ++j) acc[i][j] = mfma32(fa[cur][i], fb[cur][j], acc[i][j]);
       store_w(wset, nbuf, kk);
     }
-    constexpr int PS = NI * MJ;                   // matrix-core instructions per sub-step
+    constexpr int PS = NIW * MJ;                  // matrix-core instructions per sub-step
     constexpr int NM = 4 * PS;                    // ... per step
     constexpr int NW = BWD ? 8 : 4 * C::CH;       // LDS tile writes
     // VALU per step (dequantization + addressing), measured from the ISA:
@@ -373,10 +410,10 @@ k_gemm(GemmArgs a, int tiles_m) {
   // fp8 forward: the per-output-channel scale factors out of the k reduction
   if (!BWD && FMT == LRQ_FMT_FP8) {
 #pragma unroll
-    for (int i = 0; i < NI; ++i)
+    for (int i = 0; i < NIW; ++i)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int64_t n = e0 + i * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
+        const int64_t n = e0 + (rh * NIW + i) * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
         const float s = (n < E) ? (a.per_channel ? a.wscale[n] : a.wscale[0]) : 0.0f;
 #pragma unroll
         for (int j = 0; j < MJ; ++j) acc[i][j][v] *= s;
@@ -410,15 +447,14 @@ k_gemm(GemmArgs a, int tiles_m) {
         const int64_t k = e0 + row;
         uint16_t v = 0;
         if (j < r && k < E) v = a.lw[k * r + j];
-        const int phys = (j >> 3) ^ ((row >> 3) & 7);
-        sA[row * LD + phys * 8 + (j & 7)] = v;
+        sA[row * LD + j] = v;
       }
     }
     __syncthreads();
     u32x4 lb[MJ][4];
 #pragma unroll
     for (int j = 0; j < MJ; ++j) {
-      const int64_t m = m0 + wave * (32 * MJ) + j * 32 + l32;
+      const int64_t m = m0 + tw * (32 * MJ) + j * 32 + l32;
       const bool ok = m < M;
       const uint16_t* src = a.lact + (ok ? m : (M - 1)) * rp + g * 8;
 #pragma unroll
@@ -434,8 +470,8 @@ k_gemm(GemmArgs a, int tiles_m) {
     for (int kk = 0; kk < 4; ++kk) {
       if (kk * 16 < rp) {
 #pragma unroll
-        for (int i = 0; i < NI; ++i) {
-          const bf16x8 fa = afrag(sA, i * 32 + l32, kk * 2 + g);
+        for (int i = 0; i < NIW; ++i) {
+          const bf16x8 fa = afrag(sA, (rh * NIW + i) * 32 + l32, kk * 2 + g);
 #pragma unroll
           for (int j = 0; j < MJ; ++j) acc[i][j] = mfma32(fa, as_bf16x8(lb[j][kk]), acc[i][j]);
         }
@@ -445,16 +481,16 @@ k_gemm(GemmArgs a, int tiles_m) {
 
   // epilogue: lane holds 4 consecutive weight-side rows (n or k) of one token
 #pragma unroll
-  for (int i = 0; i < NI; ++i) {
+  for (int i = 0; i < NIW; ++i) {
 #pragma unroll
     for (int vg = 0; vg < 4; ++vg) {
-      const int64_t e = e0 + i * 32 + 8 * vg + 4 * g;
+      const int64_t e = e0 + (rh * NIW + i) * 32 + 8 * vg + 4 * g;
       if (e >= E) continue;
       f32x4 bv = {0.0f, 0.0f, 0.0f, 0.0f};
       if (!BWD && a.bias) bv = *reinterpret_cast<const f32x4*>(a.bias + e);
 #pragma unroll
       for (int j = 0; j < MJ; ++j) {
-        const int64_t m = m0 + wave * (32 * MJ) + j * 32 + l32;
+        const int64_t m = m0 + tw * (32 * MJ) + j * 32 + l32;
         if (m < M) {
           u32x2 o;
           o[0] = pack_bf16x2(acc[i][j][4 * vg + 0] + bv[0], acc[i][j][4 * vg + 1] + bv[1]);
@@ -489,33 +525,34 @@ int pick_ni(int64_t extent, int64_t m, const int* cands, int ncands) {
   return best;
 }
 
-template <bool BWD, int FMT, int NI>
+template <bool BWD, int FMT, int NI, int WN>
 hipError_t run(hipStream_t st, const GemmArgs& a) {
   const int tiles_m = (int)((a.m + RB - 1) / RB);
   const int tiles_e = (int)((a.e + 32 * NI - 1) / (32 * NI));
-  hipLaunchKernelGGL((k_gemm<BWD, FMT, NI>), dim3(tiles_m * tiles_e), dim3(NT), 0, st, a, tiles_m);
+  hipLaunchKernelGGL((k_gemm<BWD, FMT, NI, WN>), dim3(tiles_m * tiles_e), dim3(256 * WN), 0, st, a, tiles_m);
   return hipGetLastError();
 }
 
 template <bool BWD, int FMT>
 hipError_t dispatch(hipStream_t st, const GemmArgs& a) {
-  // forward tiles: NI in {8, 4} (whole 16-byte chunks per thread); backward:
-  // NI in {8, 6, 4} (at most one 8x8 block per thread)
-  // (fp8 keeps to the smaller tiles: its wider raw chunks and the forward's
-  // channel-scale epilogue do not fit the register file at NI = 8)
+  // forward tiles: NI in {8, 4} (whole 16-byte chunks per thread), two
+  // wavefronts per token group where the chunks divide (int4 NI = 4 has one);
+  // backward: NI in {6, 4} (at most one 8x8
+  // block per thread), one wavefront per token group (NI = 8 exceeds the
+  // register file). fp8 keeps to the smaller forward tile: its wider raw
+  // chunks and the channel-scale epilogue do not fit at NI = 8.
   static const int fwd_c[] = {8, 4};
-  static const int bwd_c[] = {8, 6, 4};
+  static const int bwd_c[] = {6, 4};
   const int skip = (FMT == LRQ_FMT_FP8) ? 1 : 0;
   if constexpr (BWD) {
-    switch (pick_ni(a.e, a.m, bwd_c + skip, 3 - skip)) {
-      case 8: return run<BWD, FMT, (FMT == LRQ_FMT_FP8 ? 6 : 8)>(st, a);
-      case 6: return run<BWD, FMT, 6>(st, a);
-      default: return run<BWD, FMT, 4>(st, a);
+    switch (pick_ni(a.e, a.m, bwd_c, 2)) {
+      case 6: return run<BWD, FMT, 6, 1>(st, a);
+      default: return run<BWD, FMT, 4, 1>(st, a);
     }
   } else {
-    switch (pick_ni(a.e, a.m, fwd_c + skip, 2 - skip)) {
-      case 8: return run<BWD, FMT, (FMT == LRQ_FMT_FP8 ? 4 : 8)>(st, a);
-      default: return run<BWD, FMT, 4>(st, a);
+    switch (pick_ni(a.e, a.m, fwd_c, 2)) {
+      case 8: return run<BWD, FMT, (FMT == LRQ_FMT_FP8 ? 4 : 8), 2>(st, a);
+      default: return run<BWD, FMT, 4, (FMT == LRQ_FMT_FP8 ? 2 : 1)>(st, a);
     }
   }
 }
