@@ -123,6 +123,7 @@ LRQ_DEV bf16x8 as_bf16x8(const u32x4& v) { return __builtin_bit_cast(bf16x8, v);
 
 LRQ_DEV u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 LRQ_DEV void st16(void* p, const u32x4& v) { *reinterpret_cast<u32x4*>(p) = v; }
+LRQ_DEV void st8(void* p, const u32x2& v) { *reinterpret_cast<u32x2*>(p) = v; }
 
 // ---------------------------------------------------------------- buffer loads
 // Raw buffer loads with a wave-uniform resource: an offset at or past

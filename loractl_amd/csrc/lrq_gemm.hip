@@ -90,8 +90,11 @@ struct Cfg {
   // forward: 16-byte chunks of the packed weight tile per step, per thread
   static constexpr int WPR = (FMT == LRQ_FMT_INT4) ? 2 : 4;  // chunks per block row (64 k)
   static constexpr int CH = RA * WPR / NT;
-  // backward: one 8 (n) x 8 (k) block per thread; RA/8 k-chunks x 8 n-chunks
+  // backward: one BN (n) x 8 (k) block per thread; RA/8 k-chunks x 64/BN
+  // n-chunks (BN = 4 with 8 wavefronts keeps 32 values per thread)
   static constexpr int KCH = RA / 8;
+  static constexpr int BN = (WN == 2) ? 4 : 8;
+  static constexpr int NCH = 64 / BN;
   static constexpr int WORDS = (FMT == LRQ_FMT_INT4) ? 1 : 2;  // dwords per 8 k of one row
   static constexpr int WBUF = RA * LD;                          // weight tile (bf16)
   static constexpr int XBUF = RB * BK;                          // activation tile (bf16)
@@ -195,12 +198,12 @@ k_gemm(GemmArgs a, int tiles_m) {
       fpart[c] = (uint32_t)bpart;
     }
   }
-  // backward mapping: nc = tid % 8 (8 n), kc = (tid / 8) % KCH (8 k), so the 8
-  // lanes of one k-row group write one whole 128-byte tile row; threads past
-  // 8*KCH redo a block and write it to a private dummy slot
-  const bool wthr_ok = BWD ? (tid < 8 * C::KCH) : true;
-  const int bnc = BWD ? tid % 8 : 0;
-  const int bkc = BWD ? (tid / 8) % C::KCH : 0;
+  // backward mapping: nc = tid % NCH (BN n), kc = (tid / NCH) % KCH (8 k), so
+  // the NCH lanes of one k-row group write one whole 128-byte tile row;
+  // threads past NCH*KCH redo a block and write it to a private dummy slot
+  const bool wthr_ok = BWD ? (tid < C::NCH * C::KCH) : true;
+  const int bnc = BWD ? tid % C::NCH : 0;
+  const int bkc = BWD ? (tid / C::NCH) % C::KCH : 0;
   const int64_t bcol = e0 + bkc * 8;
   const bool bcol_ok = bcol < KB * 64;  // columns in [K, 64*KB) are zero padding
   const uint32_t bcolbyte = bcol_ok ? (uint32_t)((bcol >> 6) * blkb + ((FMT == LRQ_FMT_INT4) ? (bcol & 63) / 2 : (bcol & 63)))
@@ -213,8 +216,8 @@ k_gemm(GemmArgs a, int tiles_m) {
 
   u32x4 wf[2][BWD ? 1 : C::CH];            // forward packed chunks
   float wfs[2][BWD ? 1 : C::CH];           // forward chunk scales (int4)
-  uint32_t wb[2][BWD ? 8 * C::WORDS : 1];  // backward 8 rows x 8 k
-  float wbs[2][BWD ? 8 : 1];               // backward row scales
+  uint32_t wb[2][BWD ? C::BN * C::WORDS : 1];  // backward BN rows x 8 k
+  float wbs[2][BWD ? C::BN : 1];               // backward row scales
 
   auto load_w = [&](int set, int kt) {
     if (!BWD) {
@@ -228,10 +231,10 @@ k_gemm(GemmArgs a, int tiles_m) {
         }
       }
     } else {
-      // rows n = kt*64 + nc*8 + i: block row kt, in-block rows nc*8 + i
-      const uint32_t rbase = (uint32_t)kt * (uint32_t)KB * blkb + (uint32_t)(bnc * 8) * rowb + bcolbyte;
+      // rows n = kt*64 + nc*BN + i: block row kt, in-block rows nc*BN + i
+      const uint32_t rbase = (uint32_t)kt * (uint32_t)KB * blkb + (uint32_t)(bnc * C::BN) * rowb + bcolbyte;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < C::BN; ++i) {
         if (FMT == LRQ_FMT_INT4) {
           wb[set][i] = bload4(rw, rbase + (uint32_t)i * rowb);
         } else {
@@ -241,22 +244,22 @@ k_gemm(GemmArgs a, int tiles_m) {
         }
       }
       if (FMT == LRQ_FMT_INT4) {
-        const uint32_t soff = ((uint32_t)kt * Gp * 64u + (uint32_t)(bnc * 8)) * 4u + bscol;
-        const u32x4 s0 = bload16(rs, soff), s1 = bload16(rs, soff + 16u);
+        const uint32_t soff = ((uint32_t)kt * Gp * 64u + (uint32_t)(bnc * C::BN)) * 4u + bscol;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          wbs[set][i] = __uint_as_float(s0[i]);
-          wbs[set][4 + i] = __uint_as_float(s1[i]);
+        for (int h = 0; h < C::BN / 4; ++h) {
+          const u32x4 sv = bload16(rs, soff + 16u * h);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) wbs[set][4 * h + i] = __uint_as_float(sv[i]);
         }
       } else {
         // per-channel rows read their scales; with one scalar scale the loads
         // fall outside the 4-byte resource (zeros) and the scalar is added
-        const uint32_t soff = fp8_pc_off + (uint32_t)kt * 256u + (uint32_t)(bnc * 32);
-        const u32x4 s0 = bload16(rs, soff), s1 = bload16(rs, soff + 16u);
+        const uint32_t soff = fp8_pc_off + (uint32_t)kt * 256u + (uint32_t)(bnc * C::BN * 4);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          wbs[set][i] = __uint_as_float(s0[i]) + fp8_scalar;
-          wbs[set][4 + i] = __uint_as_float(s1[i]) + fp8_scalar;
+        for (int h = 0; h < C::BN / 4; ++h) {
+          const u32x4 sv = bload16(rs, soff + 16u * h);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) wbs[set][4 * h + i] = __uint_as_float(sv[i]) + fp8_scalar;
         }
       }
     }
@@ -264,7 +267,7 @@ k_gemm(GemmArgs a, int tiles_m) {
 
   // dequantize one register set into weight buffer `buf`; `part` in 0..3 selects
   // a quarter of the work so it can be spread over the four MFMA sub-steps.
-  uint32_t bpk[BWD ? 32 : 1];  // backward: packed row pairs [pair][k]
+  uint32_t bpk[BWD ? 4 * C::BN : 1];  // backward: packed row pairs [pair][k]
   u32x2 fp8_half[(!BWD && FMT == LRQ_FMT_FP8) ? C::CH : 1];  // forward fp8: pending half chunk
   auto store_w = [&](int set, int buf, int part) {
     uint16_t* sA = sW + buf * C::WBUF;
@@ -290,31 +293,38 @@ k_gemm(GemmArgs a, int tiles_m) {
         }
       }
     } else {
-      // rows 2*part, 2*part+1 -> 8 packed dwords (one per k); writes at part 3
+      // BN = 8: rows 2*part, 2*part+1 -> 8 packed dwords (one per k).
+      // BN = 4: row pair part/2, k half part%2 -> 4 packed dwords.
+      // The transposed tile rows are written at part 3.
+      const int pr = (C::BN == 8) ? part : (part >> 1);
+      const int q0 = (C::BN == 8) ? 0 : 4 * (part & 1), nq = (C::BN == 8) ? 8 : 4;
       float f0[8], f1[8];
       if (FMT == LRQ_FMT_INT4) {
-        dequant8_int4_f32(wb[set][2 * part], wbs[set][2 * part], f0, a.nib);
-        dequant8_int4_f32(wb[set][2 * part + 1], wbs[set][2 * part + 1], f1, a.nib);
+        dequant8_int4_f32(wb[set][2 * pr], wbs[set][2 * pr], f0, a.nib);
+        dequant8_int4_f32(wb[set][2 * pr + 1], wbs[set][2 * pr + 1], f1, a.nib);
       } else {
-        fp8x4_to_f32(wb[set][4 * part], f0);
-        fp8x4_to_f32(wb[set][4 * part + 1], f0 + 4);
-        fp8x4_to_f32(wb[set][4 * part + 2], f1);
-        fp8x4_to_f32(wb[set][4 * part + 3], f1 + 4);
+        fp8x4_to_f32(wb[set][4 * pr], f0);
+        fp8x4_to_f32(wb[set][4 * pr + 1], f0 + 4);
+        fp8x4_to_f32(wb[set][4 * pr + 2], f1);
+        fp8x4_to_f32(wb[set][4 * pr + 3], f1 + 4);
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
-          f0[q] *= wbs[set][2 * part];
-          f1[q] *= wbs[set][2 * part + 1];
+          f0[q] *= wbs[set][2 * pr];
+          f1[q] *= wbs[set][2 * pr + 1];
         }
       }
 #pragma unroll
-      for (int q = 0; q < 8; ++q) bpk[part * 8 + q] = pack_bf16x2(f0[q], f1[q]);
+      for (int q = q0; q < q0 + nq; ++q) bpk[pr * 8 + q] = pack_bf16x2(f0[q], f1[q]);
       if (part == 3) {
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
           const int R = bkc * 8 + q;
-          uint16_t* dst = wthr_ok ? (sA + R * LD + bnc * 8) : (sDummy + tid * 8);
-          u32x4 o = {bpk[q], bpk[8 + q], bpk[16 + q], bpk[24 + q]};
-          st16(dst, o);
+          uint16_t* dst = wthr_ok ? (sA + R * LD + bnc * C::BN) : (sDummy + tid * 8);
+          if constexpr (C::BN == 8) {
+            st16(dst, (u32x4){bpk[q], bpk[8 + q], bpk[16 + q], bpk[24 + q]});
+          } else {
+            st8(dst, (u32x2){bpk[q], bpk[8 + q]});
+          }
         }
       }
     }
@@ -365,7 +375,7 @@ k_gemm(GemmArgs a, int tiles_m) {
     constexpr int NW = BWD ? 8 : 4 * C::CH;       // LDS tile writes
     // VALU per step (dequantization + addressing), measured from the ISA:
     // ~105 per 16-byte chunk forward, ~215 for the backward 8x8 block
-    constexpr int NV = BWD ? 216 : 106 * C::CH;
+    constexpr int NV = BWD ? 27 * C::BN : 106 * C::CH;
     constexpr int VPM = (NV + NM - 1) / NM;
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
@@ -546,7 +556,7 @@ hipError_t dispatch(hipStream_t st, const GemmArgs& a) {
   const int skip = (FMT == LRQ_FMT_FP8) ? 1 : 0;
   if constexpr (BWD) {
     switch (pick_ni(a.e, a.m, bwd_c, 2)) {
-      case 6: return run<BWD, FMT, 6, 1>(st, a);
+      case 6: return run<BWD, FMT, 6, 2>(st, a);
       default: return run<BWD, FMT, 4, 1>(st, a);
     }
   } else {
