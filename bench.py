@@ -6,7 +6,14 @@ per step. Inputs are synthetic, seeded (numpy PCG64: W=0, X=1, A=2, B=3,
 dY=4), resident in HBM before timing starts.
 
 Prints ONE JSON line. `value` is whole-step algorithmic TFLOP/s,
-F = 4MNK + 6Mr(K+N) per step. `roofline` is for the dominant kernel, with
+F = 4MNK + 6Mr(K+N) per step.
+
+`--workload skinny` measures the few-token forward instead (M=16, same
+layer, forward only, HBM-bound): `value` is algorithmic GB/s,
+W_B + 2MK + 2MN + 4r(K+N) bytes per forward, with the packed weight rotated
+over more than 256 MB of distinct copies so the Infinity Cache cannot serve
+it, and the forwards replayed from a HIP graph so host launch overhead is
+not in the timed region. `roofline` is for the dominant kernel, with
 its average launch time taken from HIP events that the library records
 around each of its launches on the launch stream. `cpu_baseline` times the
 reference's CPU algorithm (the oracle's f32 dequant + f32 GEMMs) on a
@@ -32,7 +39,9 @@ WORKLOADS = {
     "ns": (4096, 3072, 12288, 32, 32.0, "int4", 64),
     "c1": (1024, 3072, 3072, 16, 16.0, "int4", 64),
     "c2": (4096, 3072, 12288, 32, 32.0, "fp8", 0),
+    "skinny": (16, 3072, 12288, 32, 32.0, "int4", 64),  # forward only, HBM-bound
 }
+INFINITY_CACHE_BYTES = 256 << 20
 
 
 def parse():
@@ -88,6 +97,8 @@ def main():
 
     torch.cuda.set_device(0)
     dev = torch.device("cuda:0")
+    if args.workload == "skinny":
+        return bench_skinny(args, dev)
     M, K, N, r, alpha, fmt, group = WORKLOADS[args.workload]
     s = alpha / r
     w, x, a, b, dy = make_inputs(M, K, N, r)
@@ -190,6 +201,151 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
+
+
+def bench_skinny(args, dev):
+    import math
+
+    import torch
+
+    from loractl_amd import _lib as L
+    from loractl_amd import device as D
+
+    M, K, N, r, alpha, fmt, group = WORKLOADS[args.workload]
+    s = alpha / r
+    w, x, a, b, _ = make_inputs(M, K, N, r)
+    wq = D.quantize_int4(torch.from_numpy(w).to(dev), group)
+    wb = D.compute_weight(wq)
+    wbytes = wb.data.numel() + 4 * wb.scales.numel()
+    ncopy = max(2, math.ceil(1.15 * INFINITY_CACHE_BYTES / wbytes))
+    copies = [wb] + [D.PackedWeight(wb.fmt, wb.n, wb.k, wb.data.clone(), wb.scales.clone(), wb.group,
+                                    wb.per_channel, None, L.LRQ_LAYOUT_BLOCKED) for _ in range(ncopy - 1)]
+    xb = torch.from_numpy(x).to(dev).to(torch.bfloat16)
+    ab = torch.from_numpy(a).to(dev).to(torch.bfloat16)
+    bb = torch.from_numpy(b).to(dev).to(torch.bfloat16)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    t = torch.empty((M, r), dtype=torch.bfloat16, device=dev)
+    D.reserve(M, N, K, r)
+
+    def fwd(i):
+        D.lora_fwd(xb, copies[i % ncopy], ab, bb, s, y=y, t=t)
+
+    for i in range(args.warmup):
+        fwd(i)
+    torch.cuda.synchronize()
+    if not torch.isfinite(y).all() or not y.abs().max() > 0:
+        raise RuntimeError("implausible output (all-zero or non-finite)")
+    # one graph of `steps` forwards over the rotating copies
+    n_graph = args.steps
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        fwd(0)  # bind the library to the capture stream before capturing
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(n_graph):
+                fwd(i)
+    torch.cuda.synchronize()
+
+    def timed(reps):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1)
+
+    timed(2)
+    ms_total = timed(4)
+    ms_fwd = ms_total / (4 * n_graph)
+    ratio = timed(8) / ms_total
+    wb_alg = N * K / 2 + 4 * N * K / group  # W_B (packed int4 + f32 group scales)
+    bytes_fwd = wb_alg + 2 * M * K + 2 * M * N + 4 * r * (K + N)
+    value = bytes_fwd / (ms_fwd * 1e-3) / 1e9
+
+    D.profile_reset()
+    D.profile_enable(True)
+    for i in range(args.steps):
+        fwd(i)
+    torch.cuda.synchronize()
+    prof = D.profile_read()
+    D.profile_enable(False)
+    kernels = {k: 1e3 * ms / n for k, (ms, n) in prof.items() if n}
+    rp = (r + 15) // 16 * 16
+    # the few-token kernel's own traffic: packed weight as stored (blocked
+    # data + scales), x, y, B and the padded t
+    k_bytes = wbytes + 2 * M * K + 2 * M * N + 2 * r * N + 2 * M * rp
+    achieved = k_bytes / (kernels["fwd_main"] * 1e-6) / 1e9
+    roofline = {
+        "kernel": "fwd_main",
+        "bound": "hbm",
+        "achieved": round(achieved, 1),
+        "peak": PEAK_HBM_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / PEAK_HBM_GBS, 4),
+        "traffic": load_traffic("fwd_main", args.workload),
+        "bytes_per_launch": k_bytes,
+        "avg_launch_us": round(kernels["fwd_main"], 3),
+    }
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline_fwd(wq, x, a, b, M, K, N, r, s, group, args.cpu_seconds, bytes_fwd)
+    out = {
+        "metric": "int4-base LoRA linear skinny-M forward GB/s",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_fwd, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded PCG64; W~N(0,0.02) quantized on device, X~N(0,1), A~U(+-1/sqrt(K)), B~N(0,1e-3))",
+        "config": {
+            "workload": f"int4-g{group} frozen Linear {K}->{N} + LoRA r={r} alpha={alpha:g}, M={M} tokens, "
+                        f"forward (y, t); packed weight rotated over {ncopy} copies "
+                        f"({ncopy * wbytes / 2**20:.0f} MiB), forwards replayed from a HIP graph",
+            "M": M, "K": K, "N": N, "rank": r, "group": group, "format": fmt,
+            "parallelism": "single-gpu",
+        },
+        "pct_of_hbm_peak": round(100.0 * value / PEAK_HBM_GBS, 2),
+        "bytes_per_step": bytes_fwd,
+        "sanity_x2_ratio": round(ratio, 3),
+        "kernels_us": {k: round(v, 3) for k, v in kernels.items()},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+def cpu_baseline_fwd(wq, x, a, b, M, K, N, r, s, group, budget_s, bytes_fwd):
+    """The reference's CPU forward (f32 dequant of the whole weight, f32
+    GEMMs) on the whole few-token workload, on this host's cores."""
+    import oracle as O
+
+    st = O.CpuFwdInt4(wq.data.cpu().numpy(), wq.scales.cpu().numpy(), group, x, a, b, s)
+    t0 = time.perf_counter()
+    threads = st.run()
+    first = time.perf_counter() - t0
+    reps = max(1, int(budget_s / max(first, 1e-3)))
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        st.run()
+    dt = (time.perf_counter() - t0) / reps
+    return {
+        "value": round(bytes_fwd / dt / 1e9, 3),
+        "unit": "GB/s",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": f"the whole workload (M={M}, {K}->{N} r={r} int4-g{group}), forward, {reps} reps of {dt:.4f} s "
+                  f"(f32 dequant of the full weight + f32 GEMMs, OpenMP)",
+    }
 
 
 def cpu_baseline(wq, x, a, b, dy, M, K, N, r, s, group, fmt, budget_s):

@@ -35,7 +35,7 @@ namespace {
 
 const char* kNames[KID_COUNT] = {"quantize_int4", "quantize_fp8", "dequant", "fwd_main", "bwd_dx",
                                  "lora_t",        "lora_u",       "lora_da", "lora_db",  "lora_reduce",
-                                 "block"};
+                                 "block",         "fwd_epi"};
 
 int fail(lrq_ctx* c, int code, const char* fmt, ...) {
   if (c) {
@@ -268,6 +268,10 @@ int lrq_reserve(lrq_ctx* c, int64_t m, int64_t n, int64_t k, int64_t r) {
   if (m < 0 || n < 0 || k < 0 || r < 0 || r > 64) return fail(c, LRQ_EINVAL, "bad reserve shape");
   const int rp = (int)round_up(r > 0 ? r : 16, 16);
   size_t need = lora_layout(nullptr, m, n, k, rp).bytes;
+  if (m >= 1) {  // the few-token forward, at up to 16 tokens
+    const size_t sk = skinny_ws_bytes(skinny_plan(n, k, rp, get_num_cus()), m < 16 ? m : 16, n, rp);
+    if (sk > need) need = sk;
+  }
   const size_t fp8_need = (size_t)round_up(n * 4, 256);
   if (fp8_need > need) need = fp8_need;
   return ensure_ws(c, need);
@@ -377,6 +381,27 @@ static int fwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t 
   if (lora) {
     if (r > 64) return fail(c, LRQ_EINVAL, "rank %lld outside [1, 64]", (long long)r);
     if (!aligned16(b)) return fail(c, LRQ_EINVAL, "B must be 16-byte aligned");
+  }
+  if (m >= 1 && m <= 16) {
+    // few tokens: stream the packed weight once (split-k partials, t's
+    // partials alongside), then one epilogue launch
+    const int rp = lora ? (int)round_up(r, 16) : 0;
+    const SkinnyPlan p = skinny_plan(w->n, w->k, rp, get_num_cus());
+    LRQ_TRY(ensure_ws(c, skinny_ws_bytes(p, m, w->n, rp)));
+    float* part = reinterpret_cast<float*>(c->ws);
+    float* tpart = part + round_up((int64_t)p.S * m * w->n, 64);
+    if (lora) {
+      ga.lw = b;
+      ga.r = (int)r;
+      ga.rp = rp;
+    }
+    LRQ_TRY(run(c, KID_FWD_MAIN, "fwd_main",
+                [&] { return launch_skinny_part(c->stream, w->format, ga, lora ? a : nullptr, p, part, tpart); }));
+    return run(c, KID_FWD_EPI, "fwd_epi", [&] {
+      return launch_skinny_epi(c->stream, w->format, ga, p, part, tpart, scaling, lora ? t_out : nullptr);
+    });
+  }
+  if (lora) {
     const int rp = (int)round_up(r, 16);
     LRQ_TRY(check_lora_shapes(c, m, w->n, w->k, rp));
     LRQ_TRY(ensure_ws(c, lora_layout(nullptr, m, w->n, w->k, rp).bytes));

@@ -153,6 +153,8 @@ LRQ_DEV rsrc_t make_rsrc(const void* base, uint32_t bytes) {
 LRQ_DEV u32x4 bload16(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0); }
 LRQ_DEV u32x2 bload8(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0); }
 LRQ_DEV uint32_t bload4(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0); }
+// zero-extended 16-bit load
+LRQ_DEV uint32_t bload2(rsrc_t r, uint32_t off) { return (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0); }
 LRQ_DEV float bloadf(rsrc_t r, uint32_t off) { return __builtin_bit_cast(float, bload4(r, off)); }
 LRQ_DEV uint32_t clamp_bytes(int64_t b) { return b <= 0 ? 0u : (b >= 0xffffffffll ? 0xffffffffu : (uint32_t)b); }
 

@@ -570,6 +570,7 @@ hipError_t dispatch(hipStream_t st, const GemmArgs& a) {
 }  // namespace
 
 void set_num_cus(int n) { g_num_cus = n > 0 ? n : 256; }
+int get_num_cus() { return g_num_cus; }
 
 hipError_t launch_gemm(hipStream_t st, bool bwd, int fmt, const GemmArgs& a) {
   if (a.m == 0 || a.e == 0) return hipSuccess;

@@ -72,6 +72,9 @@ def lib():
         L.lrq_o_cpu_step_int4.restype = ctypes.c_int
         L.lrq_o_cpu_step_int4.argtypes = [vp, vp, _i64, vp, vp, vp, ctypes.c_float, vp,
                                           _i64, _i64, _i64, _i64, vp, vp, vp, vp, vp, vp, vp]
+        L.lrq_o_cpu_fwd_int4.restype = ctypes.c_int
+        L.lrq_o_cpu_fwd_int4.argtypes = [vp, vp, _i64, vp, vp, vp, ctypes.c_float,
+                                         _i64, _i64, _i64, _i64, vp, vp, vp]
         _lib = L
     return _lib
 
@@ -243,6 +246,30 @@ def cosine(a, b) -> float:
 
 
 # ---------------------------------------------------------------- cpu baseline
+class CpuFwdInt4:
+    """The reference CPU algorithm (f32 dequant + f32 GEMMs) over one forward."""
+
+    def __init__(self, packed, scales, group, X, A, B, s):
+        self.packed = _c(packed, np.uint8)
+        self.scales = _c(scales, np.float32)
+        self.g = group
+        self.X = _c(X, np.float32)
+        self.A = _c(A, np.float32)
+        self.B = _c(B, np.float32)
+        self.s = float(s)
+        self.M, self.K = self.X.shape
+        self.N = self.B.shape[1]
+        self.r = self.A.shape[1]
+        self.Wdq = np.empty((self.N, self.K), np.float32)
+        self.T = np.empty((self.M, self.r), np.float32)
+        self.Y = np.empty((self.M, self.N), np.float32)
+
+    def run(self) -> int:
+        return lib().lrq_o_cpu_fwd_int4(
+            _ptr(self.packed), _ptr(self.scales), self.g, _ptr(self.X), _ptr(self.A), _ptr(self.B),
+            self.s, self.M, self.N, self.K, self.r, _ptr(self.Wdq), _ptr(self.T), _ptr(self.Y))
+
+
 class CpuStepInt4:
     """The reference CPU algorithm (f32 dequant + f32 GEMMs) over one fwd+bwd."""
 

@@ -394,6 +394,36 @@ static void sgemm_tn(const float* A, const float* B, float* C, int64_t M, int64_
 }
 
 /*
+ * The forward alone, the reference CPU way (quant.rs:175-176 with the LoRA
+ * term of lora.rs:199-203): materialize Wdq f32 [N,K], Y = X Wdq^T,
+ * T = s X A, Y += T B. Work buffers Wdq [N*K], T [M*r], Y [M*N].
+ * Returns the number of threads used.
+ */
+EXPORT int lrq_o_cpu_fwd_int4(const uint8_t* packed, const float* scales, int64_t g,
+                              const float* X, const float* A, const float* B, float s,
+                              int64_t M, int64_t N, int64_t K, int64_t r,
+                              float* Wdq, float* T, float* Y) {
+#pragma omp parallel for schedule(static)
+  for (int64_t n = 0; n < N; ++n) {
+    const int64_t nb = K / g;
+    for (int64_t k = 0; k < K; ++k) {
+      uint8_t b = packed[n * (K / 2) + k / 2];
+      int q = (int)((k & 1) ? (b >> 4) : (b & 0xF)) - 8;
+      Wdq[n * K + k] = (float)q * scales[n * nb + k / g];
+    }
+  }
+  sgemm_nt(X, Wdq, Y, M, N, K, 0);
+  sgemm_nn(X, A, T, M, r, K, 0);
+  for (int64_t i = 0; i < M * r; ++i) T[i] *= s;
+  sgemm_nn(T, B, Y, M, N, r, 1);
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}
+
+/*
  * One forward+backward of the int4 LoRA linear, the reference CPU way:
  * materialize Wdq f32 [N,K] (every pass, as quant.rs does), f32 GEMMs for the
  * base and the four LoRA products. X, dY [M,*] f32; A [K,r], B [r,N].

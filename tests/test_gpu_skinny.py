@@ -1,0 +1,85 @@
+"""The few-token forward (m <= 16 takes its own HBM-streaming kernel) against
+the CPU oracle on identical seeded inputs, and against the large-m kernel on
+the same rows (both round dequantized weights to bf16 and accumulate in f32,
+so they agree to f32 summation order)."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from gpu_helpers import case_inputs, check, to_dev
+from loractl_amd import device as D
+
+pytestmark = pytest.mark.gpu
+
+
+def _weight(w, fmt, g, dev, per_channel=True):
+    t = torch.from_numpy(w).to(dev)
+    if fmt == "int4":
+        wq = D.quantize_int4(t, g)
+        p, s = O.quantize_int4_packed(w, g)
+        return wq, O.dequant_int4(p, s, w.shape[1], g)
+    wq = D.quantize_fp8(t, per_channel)
+    b, s = O.fp8_quantize(w, per_channel)
+    return wq, O.fp8_dequant(b, s)
+
+
+# (fmt, group, per_channel): int4 blocks smaller, equal and larger than the 64-wide step
+FORMATS = [("int4", 32, True), ("int4", 64, True), ("int4", 128, True), ("fp8", 0, True), ("fp8", 0, False)]
+
+
+@pytest.mark.parametrize("M", [1, 7, 16])
+@pytest.mark.parametrize("K,N", [(96, 72), (1088, 520), (3072, 264)])
+@pytest.mark.parametrize("fmt,g,pc", FORMATS)
+def test_skinny_base_and_lora(cuda, M, K, N, fmt, g, pc):
+    if fmt == "int4" and K % g:
+        pytest.skip("int4 blocks must divide d_in")
+    r = 17
+    w, x, a, b, _ = case_inputs(M, K, N, r, seed=11 * M + K + N, b_sigma=0.05)
+    wq, wdq = _weight(w, fmt, g, cuda, pc)
+    xd, ad, bd = to_dev(x, cuda), to_dev(a, cuda), to_dev(b, cuda)
+    base = D.quant_matmul_t(xd, wq)
+    check(f"{fmt} base", base, O.linear_fwd(x, wdq)[0])
+    y, t = D.lora_fwd(xd, wq, ad, bd, 0.5)
+    y_ref, t_ref = O.linear_fwd(x, wdq, a, b, 0.5)
+    check("t", t, t_ref)
+    check("y", y, y_ref)
+
+
+@pytest.mark.parametrize("r", [1, 16, 33, 64])
+def test_skinny_ranks_and_bias(cuda, r):
+    M, K, N, g = 9, 640, 200, 64
+    w, x, a, b, _ = case_inputs(M, K, N, r, seed=r, b_sigma=0.05)
+    wq, wdq = _weight(w, "int4", g, cuda)
+    bias = np.linspace(-1, 1, N).astype(np.float32)
+    wb = wq.with_bias(torch.from_numpy(bias).to(cuda))
+    y, _ = D.lora_fwd(to_dev(x, cuda), wb, to_dev(a, cuda), to_dev(b, cuda), 2.0)
+    y_ref, _ = O.linear_fwd(x, wdq, a, b, 2.0, bias=bias)
+    check("y", y, y_ref)
+
+
+@pytest.mark.parametrize("fmt", ["int4", "fp8"])
+def test_skinny_matches_large_m_kernel(cuda, fmt):
+    """Rows 0..15 of a 300-token call (large-m kernel) against the same 16
+    tokens alone (few-token kernel): equal up to f32 summation order, so
+    within a couple of bf16 ulps elementwise."""
+    M, K, N, r = 300, 1024, 328, 32
+    w, x, a, b, _ = case_inputs(M, K, N, r, seed=21)
+    wq, _ = _weight(w, fmt, 64, cuda)
+    xd, ad, bd = to_dev(x, cuda), to_dev(a, cuda), to_dev(b, cuda)
+    y_big, t_big = D.lora_fwd(xd, wq, ad, bd, 1.0)
+    y_small, t_small = D.lora_fwd(xd[:16].contiguous(), wq, ad, bd, 1.0)
+    tb, ts = t_big[:16].float(), t_small.float()  # split reductions may differ in order
+    assert ((tb - ts).abs() <= 2.0 ** -7 * tb.abs() + 1e-6).all()
+    yb, ys = y_big[:16].float(), y_small.float()
+    assert ((yb - ys).abs() <= 2.0 ** -7 * yb.abs() + 1e-3 * yb.abs().max()).all()
+
+
+def test_skinny_zero_b_is_bitwise_no_op(cuda):
+    M, K, N, r = 4, 256, 128, 16
+    w, x, a, _, _ = case_inputs(M, K, N, r, seed=8)
+    wq, _ = _weight(w, "int4", 64, cuda)
+    xd = to_dev(x, cuda)
+    y, _ = D.lora_fwd(xd, wq, to_dev(a, cuda), torch.zeros(r, N, dtype=torch.bfloat16, device=cuda), 1.0)
+    assert torch.equal(y, D.quant_matmul_t(xd, wq))

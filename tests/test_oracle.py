@@ -278,3 +278,18 @@ def test_cpu_baseline_step_matches_oracle():
     dX, dA, dB = O.linear_bwd(X, wdq, A, B, 1.0, dY)
     for got, ref in ((st.Y, Y), (st.dX, dX), (st.dA, dA), (st.dB, dB), (st.T, T)):
         assert O.rel_deviation(got, ref) < 1e-5
+
+
+def test_cpu_baseline_forward_matches_oracle():
+    """The timed few-token CPU baseline (forward only) computes the oracle's forward."""
+    rng = np.random.Generator(np.random.PCG64(3))
+    M, K, N, r, g = 16, 256, 200, 32, 64
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    p, s = O.quantize_int4_packed(w, g)
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    A = rng.uniform(-0.1, 0.1, (K, r)).astype(np.float32)
+    B = (rng.standard_normal((r, N)) * 1e-2).astype(np.float32)
+    st = O.CpuFwdInt4(p, s, g, X, A, B, 0.5)
+    st.run()
+    Y, T = O.linear_fwd(X, O.dequant_int4(p, s, K, g), A, B, 0.5)
+    assert O.rel_deviation(st.Y, Y) < 1e-5 and O.rel_deviation(st.T, T) < 1e-5
