@@ -175,7 +175,7 @@ def main():
         cpu = cpu_baseline(wq, x, a, b, dy, M, K, N, r, s, group, fmt, args.cpu_seconds)
 
     out = {
-        "metric": "int4-base LoRA linear fwd+bwd TFLOP/s",
+        "metric": f"{fmt}-base LoRA linear fwd+bwd TFLOP/s",
         "value": round(value, 2),
         "unit": "TFLOP/s",
         "n_gpus": 1,

@@ -556,12 +556,14 @@ hipError_t dispatch(hipStream_t st, const GemmArgs& a) {
   const int skip = (FMT == LRQ_FMT_FP8) ? 1 : 0;
   if constexpr (BWD) {
     switch (pick_ni(a.e, a.m, bwd_c, 2)) {
-      case 6: return run<BWD, FMT, 6, 2>(st, a);
+      // int4: two wavefronts per SIMD (4x8 blocks) hide the dequantization;
+      // fp8: 8x8 blocks keep each row's 64 packed bytes in one load
+      case 6: return run<BWD, FMT, 6, (FMT == LRQ_FMT_INT4 ? 2 : 1)>(st, a);
       default: return run<BWD, FMT, 4, 1>(st, a);
     }
   } else {
     switch (pick_ni(a.e, a.m, fwd_c, 2)) {
-      case 8: return run<BWD, FMT, (FMT == LRQ_FMT_FP8 ? 4 : 8), 2>(st, a);
+      case 8: return run<BWD, FMT, 8, 2>(st, a);
       default: return run<BWD, FMT, 4, (FMT == LRQ_FMT_FP8 ? 2 : 1)>(st, a);
     }
   }
