@@ -42,6 +42,7 @@ WORKLOADS = {
     "skinny": (16, 3072, 12288, 32, 32.0, "int4", 64),  # forward only, HBM-bound
 }
 INFINITY_CACHE_BYTES = 256 << 20
+GPU_SPIN_CYCLES = 100_000_000  # ~50 ms: longer than the host needs to enqueue a profiled loop
 
 
 def parse():
@@ -145,9 +146,12 @@ def main():
     F = flops_step(M, K, N, r)
     value = F / (ms_step * 1e-3) / 1e12
 
-    # per-kernel launch times from the library's HIP events
+    # per-kernel launch times from the library's HIP events; the GPU first
+    # spins so that every profiled launch is queued behind it (the events
+    # then bracket GPU time only, not host enqueue gaps)
     D.profile_reset()
     D.profile_enable(True)
+    torch.cuda._sleep(GPU_SPIN_CYCLES)
     for _ in range(args.steps):
         step()
     torch.cuda.synchronize()
@@ -269,6 +273,7 @@ def bench_skinny(args, dev):
 
     D.profile_reset()
     D.profile_enable(True)
+    torch.cuda._sleep(GPU_SPIN_CYCLES)
     for i in range(args.steps):
         fwd(i)
     torch.cuda.synchronize()
