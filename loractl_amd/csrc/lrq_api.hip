@@ -418,7 +418,7 @@ static int fwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t 
     ga.r = (int)r;
     ga.rp = rp;
   }
-  return run(c, KID_FWD_MAIN, "fwd_main", [&] { return launch_gemm(c->stream, false, w->format, ga); });
+  return run(c, KID_FWD_MAIN, "fwd_main", [&] { return launch_fwd(c->stream, w->format, ga); });
 }
 
 int lrq_quant_matmul_t(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t m, uint16_t* y) {

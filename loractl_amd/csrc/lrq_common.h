@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "loractl_rocm.h"
+
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -125,6 +127,15 @@ LRQ_DEV u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 LRQ_DEV void st16(void* p, const u32x4& v) { *reinterpret_cast<u32x4*>(p) = v; }
 LRQ_DEV void st8(void* p, const u32x2& v) { *reinterpret_cast<u32x2*>(p) = v; }
 
+// ---------------------------------------------------------------- workgroup order
+// Workgroup ids are dealt round-robin over the 8 XCDs (each with its own L2);
+// map them to a logical order in which XCD x owns a contiguous range.
+LRQ_DEV int xcd_remap(int bid, int nblk) {
+  const int q = nblk / 8, r = nblk % 8;
+  const int x = bid % 8, i = bid / 8;
+  return x * q + min(x, r) + i;
+}
+
 // ---------------------------------------------------------------- buffer loads
 // Raw buffer loads with a wave-uniform resource: an offset at or past
 // num_records reads zeros, so bounds handling needs no branches.
@@ -157,6 +168,19 @@ LRQ_DEV uint32_t bload4(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_bu
 LRQ_DEV uint32_t bload2(rsrc_t r, uint32_t off) { return (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0); }
 LRQ_DEV float bloadf(rsrc_t r, uint32_t off) { return __builtin_bit_cast(float, bload4(r, off)); }
 LRQ_DEV uint32_t clamp_bytes(int64_t b) { return b <= 0 ? 0u : (b >= 0xffffffffll ? 0xffffffffu : (uint32_t)b); }
+
+LRQ_DEV u32x4 zero4() { return (u32x4){0u, 0u, 0u, 0u}; }
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Blocked-layout sizes (lrq_quant.hip writes the layout): data bytes and
+// int4 scale count.
+LRQ_DEV void blocked_sizes_dev(int fmt, int64_t n, int64_t k, int64_t* data_bytes, int64_t* nscales,
+                               int gshift) {
+  const int64_t NB = (n + 63) / 64, KB = (k + 63) / 64;
+  *data_bytes = NB * KB * 64 * (fmt == LRQ_FMT_INT4 ? 32 : 64);
+  *nscales = (fmt == LRQ_FMT_INT4) ? NB * ((KB * 64) >> gshift) * 64 : 0;
+}
 
 // 8 consecutive bf16 (16 bytes) from global with a validity predicate.
 LRQ_DEV u32x4 ld16_pred(const void* p, bool ok) {

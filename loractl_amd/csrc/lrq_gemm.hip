@@ -64,22 +64,6 @@ LRQ_DEV int swz(int r) { return (r >> 1) & 7; }
 constexpr int MJ = 2;       // 32-token tiles per wavefront
 constexpr int RB = 4 * 32 * MJ;  // tokens per workgroup (4 token groups of 64)
 
-LRQ_DEV int xcd_remap(int bid, int nblk) {
-  const int q = nblk / 8, r = nblk % 8;
-  const int x = bid % 8, i = bid / 8;
-  return x * q + min(x, r) + i;
-}
-
-LRQ_DEV u32x4 zero4() { return (u32x4){0u, 0u, 0u, 0u}; }
-
-// Blocked-layout sizes (see lrq_quant.hip): data bytes and int4 scale count.
-LRQ_DEV void blocked_sizes_dev(int fmt, int64_t n, int64_t k, int64_t* data_bytes, int64_t* nscales,
-                               int gshift) {
-  const int64_t NB = (n + 63) / 64, KB = (k + 63) / 64;
-  *data_bytes = NB * KB * 64 * (fmt == LRQ_FMT_INT4 ? 32 : 64);
-  *nscales = (fmt == LRQ_FMT_INT4) ? NB * ((KB * 64) >> gshift) * 64 : 0;
-}
-
 // WN wavefronts share each token group, splitting its RA weight-side rows:
 // WN = 2 gives 8 wavefronts (two per SIMD) with half the accumulators each.
 template <bool BWD, int FMT, int NI, int WN>
@@ -102,8 +86,6 @@ struct Cfg {
   static_assert(NI % WN == 0, "whole row tiles per wavefront");
   static_assert(BWD || CH * NT == RA * WPR, "whole 16-byte weight chunks per thread");
 };
-
-typedef __attribute__((address_space(3))) void lds_void;
 
 template <bool BWD, int FMT, int NI, int WN>
 __global__ void __launch_bounds__(256 * WN) __attribute__((amdgpu_waves_per_eu(WN, WN)))

@@ -35,6 +35,8 @@ struct GemmArgs {
 };
 
 hipError_t launch_gemm(hipStream_t st, bool bwd, int fmt, const GemmArgs& a);
+// lrq_fwd.hip: the forward for m > 16 (weight dequantized into registers)
+hipError_t launch_fwd(hipStream_t st, int fmt, const GemmArgs& a);
 int get_num_cus();
 
 // lrq_skinny.hip: the forward for m <= 16 in two launches. `part` streams the
