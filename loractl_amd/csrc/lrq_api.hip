@@ -138,7 +138,7 @@ int ensure_ws(lrq_ctx* c, size_t bytes) {
 // and u padded to rp columns (the GEMM epilogue operands) and the f32
 // partials of the LoRA reductions (t or u; dA and dB side by side).
 struct LoraWs {
-  uint16_t *tp, *up;
+  uint16_t *tp, *up, *bt;
   float *pn, *pa, *pb;
   size_t bytes;
 };
@@ -148,6 +148,7 @@ LoraWs lora_layout(char* base, int64_t m, int64_t n, int64_t k, int rp) {
   LoraWs w{};
   w.tp = s.take<uint16_t>(m * rp);
   w.up = s.take<uint16_t>(m * rp);
+  w.bt = s.take<uint16_t>(n * rp);
   const int64_t nt = std::max((int64_t)lora_plan_nt(m, k, rp).splits, (int64_t)lora_plan_nt(m, n, rp).splits);
   w.pn = s.take<float>(std::max(nt * m * rp, (int64_t)1));
   w.pa = s.take<float>((int64_t)lora_plan_tn(m, k, rp).splits * k * rp);
@@ -411,10 +412,10 @@ static int fwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t 
     LRQ_TRY(run(c, KID_LORA_T, "lora_t", [&] {
       hipError_t e = launch_lora_nt(c->stream, x, a, false, r, (int)r, m, w->k, rp, pt, ws.pn);
       if (e != hipSuccess) return e;
-      return launch_nt_reduce(c->stream, ws.pn, pt.splits, m, rp, (int)r, scaling, ws.tp, t_out);
+      return launch_nt_reduce(c->stream, ws.pn, pt.splits, m, rp, (int)r, scaling, ws.tp, t_out, b, w->n, ws.bt);
     }));
     ga.lact = ws.tp;
-    ga.lw = b;
+    ga.lw = ws.bt;
     ga.r = (int)r;
     ga.rp = rp;
   }

@@ -4,13 +4,13 @@
 //   y[m, n] = x[m, k] . bf16(dq(w))[n, k]^T (+bias) + t[m, :] . B[:, n]
 //
 // (src/quant.rs:175-176 for the base product, src/lora.rs:199-203 for the
-// LoRA term; t = bf16(s . x . A) comes from the LoRA side kernels.)
+// LoRA term; t = bf16(s . x . A) and bt = B^T come from the LoRA side
+// kernels.)
 //
-// A workgroup of four wavefronts (one per SIMD) owns a 256 (n) x 256 (token)
-// output tile. Wavefront w owns weight rows 64w .. 64w+63 of it for all 256
-// tokens: 2 x 8 accumulator tiles of v_mfma_f32_32x32x16_bf16 (256 f32 per
-// lane). The design keeps LDS traffic and dequantization work per
-// matrix-core instruction small:
+// Output tiles are 256 (n) x 256 (tokens). A persistent grid of one
+// workgroup per CU walks its tiles; four wavefronts (one per SIMD) each own
+// 64 weight rows of a tile for all 256 tokens: 2 x 8 accumulator tiles of
+// v_mfma_f32_32x32x16_bf16 (256 f32 per lane).
 //   - weight (A role): each lane loads the packed bytes of its own row
 //     straight from the blocked layout (int4: 16 bytes = 32 k of one row,
 //     fp8: 32 bytes), dequantizes in registers to the exact bf16 operand
@@ -18,26 +18,31 @@
 //     feeds the matrix cores. The reduction index is permuted inside a
 //     64-wide step: lane group g (lanes 32g .. 32g+31) takes k = 32g + 8kk ..
 //     +8 in sub-step kk, so a lane's packed bytes are contiguous. No weight
-//     row is shared between wavefronts, so each weight element is
-//     dequantized once per workgroup, and the weight never passes LDS;
+//     row is shared between wavefronts: each weight element is dequantized
+//     once per tile and the weight never passes LDS;
 //   - activations (B role): the 256 x 64 x-tile of a step is copied global ->
 //     LDS by buffer loads with an LDS destination (each wavefront moves 64
-//     token rows) and read by all four wavefronts: 1/64 byte of LDS reads per
-//     flop, half of what a shared dequantized weight tile would add;
-//   - the pipeline: x tiles in NBUF LDS buffers, packed weights in NBUF
-//     register sets, both NBUF-1 steps ahead. The one barrier of a step sits
-//     between its third and fourth sub-steps, after the last fragment reads of
-//     the current buffer: the fourth sub-step's matrix-core work then covers
-//     the barrier and the next step's first fragment reads;
+//     token rows) and read by all four wavefronts;
+//   - the pipeline: x tiles in NBUF LDS buffers and packed weights in NBUF
+//     register sets, NBUF-1 steps ahead, continuing across tiles: the last
+//     steps of a tile prefetch the first steps of the workgroup's next tile,
+//     so that tile's loads are in flight while this tile's epilogue (LoRA
+//     step, bias, stores) runs, and the stores drain under the next tile's
+//     matrix-core work. The one barrier of a step sits between its third and
+//     fourth sub-steps, after the last fragment reads of the current buffer;
 //   - edges: buffer loads past a resource's size return zeros (partial token
-//     and weight tiles, the k tail, and the zero steps that pad the unrolled
-//     loop); padding weight rows hold q = 0 with scale 0;
+//     and weight tiles, the k tail and the zero steps that round a tile's
+//     steps up to a multiple of NBUF); padding weight rows hold q = 0 with
+//     scale 0;
 //   - epilogue: fp8 per-channel scales multiply the f32 accumulators (they
-//     factor out of the k reduction), then the LoRA term is one more
-//     rank-wide matrix-core step (B^T staged in LDS at the start, t from
-//     global), then bias and 8-byte bf16 stores;
-//   - workgroup ids are remapped so each XCD (own L2) works on a contiguous
-//     range of tiles, grouped four token tiles deep.
+//     factor out of the k reduction), then the LoRA term is one rank-wide
+//     matrix-core step (the tile's t and bt rows, copied into LDS while the
+//     tile's main loop runs), then the bias; each wavefront then passes its
+//     bf16 output rows through LDS so that every store writes whole 128-byte
+//     row segments (8 rows per instruction);
+//   - tile order: workgroup b's i-th tile is virtual tile b + i*G, mapped so
+//     each XCD (own L2) works on a contiguous range of tiles, grouped four
+//     token tiles deep.
 
 #include "lrq_common.h"
 #include "lrq_kernels.h"
@@ -48,67 +53,80 @@ constexpr int BK = 64;              // reduction step
 constexpr int NWV = 4;              // wavefronts per workgroup (one per SIMD)
 constexpr int NIW = 2;              // 32-row weight tiles per wavefront
 constexpr int MJ = 8;               // 32-token tiles per wavefront
-constexpr int RA = NWV * NIW * 32;  // weight rows per workgroup (256)
-constexpr int RB = MJ * 32;         // tokens per workgroup (256)
+constexpr int RA = NWV * NIW * 32;  // weight rows per tile (256)
+constexpr int RB = MJ * 32;         // tokens per tile (256)
 constexpr int XBUF = RB * BK;       // bf16 per activation buffer (32 KB)
-constexpr int LDL = 72;             // staged B^T row stride (bf16): 144-byte rows
+constexpr int GM = 4;               // token tiles per group of the tile order
 
 // activation LDS tile [256 rows][64] bf16: 128-byte rows, 16-byte chunk c of
 // row r at chunk c ^ swz(r), so the 16 lanes of a read pass (16 rows at one
 // logical chunk) cover all 64 banks
 LRQ_DEV int swz(int r) { return (r >> 1) & 7; }
 
+// Per-tile load sources: the activation rows of wavefront w's DMA share and
+// the wavefront's weight block row (data and int4 scales).
+struct TileSrc {
+  int64_t m0, e0;
+  rsrc_t act, wd, ws;
+};
+
 template <int FMT, int NBUF>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
-k_fwd(GemmArgs a, int tiles_m) {
+k_fwd(GemmArgs a, int tiles_m, int ntiles) {
   constexpr bool I4 = FMT == LRQ_FMT_INT4;
   constexpr int WV = I4 ? 1 : 2;  // 16-byte packed loads per row tile per step
   __shared__ __attribute__((aligned(16))) uint16_t sX0[XBUF];
   __shared__ __attribute__((aligned(16))) uint16_t sX1[XBUF];
   __shared__ __attribute__((aligned(16))) uint16_t sX2[NBUF > 2 ? XBUF : 8];
-  __shared__ __attribute__((aligned(16))) uint16_t sB[RA * LDL];  // B^T [256 n][rp]
+  // epilogue region: the tile's LoRA operands (t rows, then bt rows, each
+  // [256][rp]) copied in during the tile, then each wavefront's output rows
+  __shared__ __attribute__((aligned(16))) uint16_t sE[4 * 128 * 64];
 
-  const int logical = xcd_remap(blockIdx.x, gridDim.x);
-  const int tiles_a = gridDim.x / tiles_m;
-  constexpr int GM = 4;
-  const int grp = logical / (GM * tiles_a), within = logical % (GM * tiles_a);
-  const int gm = min(GM, tiles_m - grp * GM);
-  const int tm = grp * GM + within % gm, ta = within / gm;
-  const int64_t m0 = (int64_t)tm * RB, e0 = (int64_t)ta * RA;
+  const int G = gridDim.x;
+  int vb = blockIdx.x;
+  if (vb >= ntiles) return;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5, l32 = lane & 31;
   const int64_t M = a.m, K = a.l, E = a.e;
+  const int tiles_a = ntiles / tiles_m;
 
-  // ---------------- B^T staging for the LoRA step (read after the main loop)
-  const int rp = a.rp, r = a.r;
-  if (rp > 0) {
-    // B[j][e0 + c*8 .. +8] -> sB[(c*8 + q) * LDL + j]
-    constexpr int cpr = RA / 8;
-    for (int id = tid; id < rp * cpr; id += 256) {
-      const int j = id / cpr, c = id % cpr;
-      const int64_t n = e0 + c * 8;
-      u32x4 v = zero4();
-      if (j < r && n < E) v = ld16(a.lw + (int64_t)j * E + n);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        sB[(c * 8 + 2 * q) * LDL + j] = (uint16_t)(v[q] & 0xffffu);
-        sB[(c * 8 + 2 * q + 1) * LDL + j] = (uint16_t)(v[q] >> 16);
-      }
-    }
-  }
+  const int64_t KB = (K + 63) / 64;
+  constexpr uint32_t blkb = I4 ? 2048u : 4096u;  // bytes per 64x64 block
+  constexpr uint32_t rowb = I4 ? 32u : 64u;      // bytes per block row
+  const uint32_t Gp = I4 ? (uint32_t)((KB * 64) >> a.gshift) : 0u;
+  int64_t wbytes, nsc;
+  blocked_sizes_dev(FMT, E, K, &wbytes, &nsc, a.gshift);
+  const int nk = (int)KB;
+  const int nkp = (nk + NBUF - 1) / NBUF * NBUF;  // steps per tile, rounded up
+
+  // sources of virtual tile v (zero-size resources when v is past the grid)
+  auto tile_src = [&](int v) -> TileSrc {
+    TileSrc t;
+    const bool ok = v < ntiles;
+    const int logical = xcd_remap(ok ? v : 0, ntiles);
+    const int grp = logical / (GM * tiles_a), within = logical % (GM * tiles_a);
+    const int gm = min(GM, tiles_m - grp * GM);
+    const int tm = grp * GM + within % gm, ta = within / gm;
+    t.m0 = (int64_t)tm * RB;
+    t.e0 = (int64_t)ta * RA;
+    const int64_t mw = t.m0 + 64 * w;
+    const int64_t mrows = ok ? ((M - mw) < 64 ? (M - mw) : 64) : 0;
+    t.act = make_rsrc(a.act + (mw < M ? mw : 0) * K, clamp_bytes(mrows * K * 2));
+    const int64_t nb = t.e0 / 64 + w;
+    t.wd = make_rsrc(a.wdata + nb * KB * blkb, ok ? clamp_bytes(wbytes - nb * KB * blkb) : 0u);
+    t.ws = make_rsrc(a.wscale + (I4 ? nb * Gp * 64 : 0), (I4 && ok) ? clamp_bytes((nsc - nb * Gp * 64) * 4) : 0u);
+    return t;
+  };
 
   // ---------------- activation DMA: wavefront w moves token rows 64w .. +64
   // 8 buffer loads per step; lane l of load c lands at row 64w + 8c + l/8,
   // physical chunk l%8, and fetches logical chunk (l%8) ^ swz(row), where
   // swz(64w + 8c + l/8) = (4c + l/16) & 7 alternates with the parity of c.
-  const int64_t mw = m0 + 64 * w;
-  const int64_t mrows = (M - mw) < 64 ? (M - mw) : 64;
-  const rsrc_t ract = make_rsrc(a.act + (mw < M ? mw : 0) * K, clamp_bytes(mrows * K * 2));
   const int drow = lane >> 3;
   const int dq0 = (lane & 7) ^ ((lane >> 4) & 7), dq1 = (lane & 7) ^ (((lane >> 4) + 4) & 7);
   const uint32_t doff0 = (uint32_t)((drow * K + dq0 * 8) * 2), doff1 = (uint32_t)((drow * K + dq1 * 8) * 2);
-  auto dma = [&](uint16_t* buf, int kt) {
+  auto dma = [&](uint16_t* buf, const rsrc_t& ract, int kt) {
     const int64_t k0 = (int64_t)kt * BK;
     const bool kok0 = k0 + dq0 * 8 < K, kok1 = k0 + dq1 * 8 < K;  // K % 8 == 0
     const uint32_t koff = (uint32_t)(k0 * 2);
@@ -134,36 +152,25 @@ k_fwd(GemmArgs a, int tiles_m) {
     return as_bf16x8(ld16(reinterpret_cast<const char*>(buf) + xk[kk] + (uint32_t)(j * 32 * BK * 2)));
   };
 
-  // ---------------- weight: this wavefront's block row of the blocked layout
-  const int64_t KB = (K + 63) / 64;
-  constexpr uint32_t blkb = I4 ? 2048u : 4096u;  // bytes per 64x64 block
-  constexpr uint32_t rowb = I4 ? 32u : 64u;      // bytes per block row
-  const uint32_t Gp = I4 ? (uint32_t)((KB * 64) >> a.gshift) : 0u;
-  int64_t wbytes, nsc;
-  blocked_sizes_dev(FMT, E, K, &wbytes, &nsc, a.gshift);
-  const int64_t nb = e0 / 64 + w;
-  const rsrc_t rw = make_rsrc(a.wdata + nb * KB * blkb, clamp_bytes(wbytes - nb * KB * blkb));
-  const rsrc_t rs = make_rsrc(a.wscale + (I4 ? nb * Gp * 64 : 0), I4 ? clamp_bytes((nsc - nb * Gp * 64) * 4) : 0u);
-  // lane offsets: row tile i at row 32i + l32 of the block, lane group g's
-  // 16 (int4) or 32 (fp8) bytes
+  // ---------------- weight: lane offsets inside the wavefront's block row:
+  // row tile i at row 32i + l32 of the block, lane group g's 16 (int4) or 32
+  // (fp8) bytes
   const uint32_t woff = (uint32_t)l32 * rowb + (uint32_t)g * (I4 ? 16u : 32u);
   const uint32_t soff = (uint32_t)l32 * 4u;
-  const int nk = (int)KB;
-
   u32x4 wp[NBUF][NIW * WV];  // packed weight bytes per register set
   float wsc[NBUF][NIW];      // int4 group scales per register set
-  auto load_w = [&](int set, int kt) {
-    // steps past the last one read zeros (bytes and scales): they add nothing
+  auto load_w = [&](int set, const TileSrc& t, int kt) {
+    // steps past the tile's last one read zeros (bytes and scales)
     const uint32_t kb = opaque_u32(kt < nk ? (uint32_t)kt * blkb : LRQ_OOB);
 #pragma unroll
     for (int i = 0; i < NIW; ++i)
 #pragma unroll
-      for (int h = 0; h < WV; ++h) wp[set][i * WV + h] = bload16(rw, kb + woff + (uint32_t)i * 32u * rowb + 16u * h);
+      for (int h = 0; h < WV; ++h) wp[set][i * WV + h] = bload16(t.wd, kb + woff + (uint32_t)i * 32u * rowb + 16u * h);
     if (I4) {
       const uint32_t j = ((uint32_t)kt * 64u + (uint32_t)g * 32u) >> a.gshift;
       const uint32_t so = opaque_u32(kt < nk ? (j * 64u) * 4u + soff : LRQ_OOB);
 #pragma unroll
-      for (int i = 0; i < NIW; ++i) wsc[set][i] = bloadf(rs, so + (uint32_t)i * 128u);
+      for (int i = 0; i < NIW; ++i) wsc[set][i] = bloadf(t.ws, so + (uint32_t)i * 128u);
     }
   };
   // A-role fragment of row tile i, sub-step kk, from register set `set`
@@ -175,20 +182,23 @@ k_fwd(GemmArgs a, int tiles_m) {
   };
 
   f32x16 acc[NIW][MJ];
+  auto zero_acc = [&]() {
 #pragma unroll
-  for (int i = 0; i < NIW; ++i)
+    for (int i = 0; i < NIW; ++i)
 #pragma unroll
-    for (int j = 0; j < MJ; ++j)
+      for (int j = 0; j < MJ; ++j)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+        for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+  };
 
   uint16_t* const bufs[3] = {sX0, sX1, sX2};
   bf16x8 fa[2][NIW], fb[2][MJ];
 
-  // One step on LDS buffer `b` and register set `b` (b = kt % NBUF; the
+  // One step on LDS buffer `b` and register set `b` (b = step % NBUF; the
   // unrolled loop makes both static). On entry fa[0] and fb[0] hold sub-step
-  // 0's fragments; on exit they hold the next step's.
-  auto step = [&](const int b, const int kt) {
+  // 0's fragments; on exit they hold the next step's. After the barrier the
+  // step refills buffer and set b with step `lkt` of tile `ls`.
+  auto step = [&](const int b, const TileSrc& ls, const int lkt) {
     const uint16_t* buf = bufs[b];
     const int nb_ = (b + 1) % NBUF;
 #pragma unroll
@@ -200,12 +210,12 @@ k_fwd(GemmArgs a, int tiles_m) {
 #pragma unroll
         for (int i = 0; i < NIW; ++i) fa[cur ^ 1][i] = wfrag(b, i, kk + 1);
       } else {
-        // every read of buffer b is issued: one barrier, then refill it
-        // (NBUF steps ahead) and register set b, and read the next step's
-        // first fragments from buffer nb_ while sub-step 3 runs
+        // every read of buffer b is issued: one barrier, then refill buffer
+        // and register set b, and read the next step's first fragments from
+        // buffer nb_ while sub-step 3 runs
         __syncthreads();
-        dma(bufs[b], kt + NBUF);
-        load_w(b, kt + NBUF);
+        dma(bufs[b], ls.act, lkt);
+        load_w(b, ls, lkt);
 #pragma unroll
         for (int j = 0; j < MJ; ++j) fb[cur ^ 1][j] = xfrag(bufs[nb_], j, 0);
 #pragma unroll
@@ -218,90 +228,152 @@ k_fwd(GemmArgs a, int tiles_m) {
     }
   };
 
-  // prologue: NBUF steps of x and packed weights in flight
+  const int rp = a.rp;
+  // LoRA operands of a tile: t rows [m0, m0+256) and bt rows [e0, e0+256),
+  // 256 * rp bf16 each, contiguous in global memory (rows past M or E read
+  // zeros); copied to sE as [256][rp] each, 16 bytes per lane per load
+  const rsrc_t rbt = make_rsrc(a.lw, rp > 0 ? clamp_bytes(E * rp * 2) : 0u);
+  const rsrc_t rt = make_rsrc(a.lact, rp > 0 ? clamp_bytes(M * rp * 2) : 0u);
+  const int lora_loads = rp / 8;  // 16-byte loads per lane per operand: 256*rp*2 / (256*16)
+  auto dma_lora = [&](int64_t m0, int64_t e0) {
+    __attribute__((address_space(3))) char* base = (__attribute__((address_space(3))) char*)(lds_void*)sE;
+    const uint32_t tb = (uint32_t)(m0 * rp * 2), bb = (uint32_t)(e0 * rp * 2);
+    for (int c = 0; c < lora_loads; ++c) {
+      const uint32_t o = (uint32_t)((c * 256 + w * 64) * 16);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rt, (lds_void*)(base + o), 16, opaque_u32(tb + o + lane * 16), 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rbt, (lds_void*)(base + 256 * rp * 2 + o), 16,
+                                               opaque_u32(bb + o + lane * 16), 0, 0, 0);
+    }
+  };
+
+  // epilogue of the tile at (m0, e0)
+  auto epilogue = [&](int64_t m0, int64_t e0) {
+    // fp8 forward: the per-output-channel scale factors out of the k reduction
+    if (!I4) {
+#pragma unroll
+      for (int i = 0; i < NIW; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int64_t n = e0 + 64 * w + 32 * i + 8 * (v >> 2) + 4 * g + (v & 3);
+          const float s = (n < E) ? (a.per_channel ? a.wscale[n] : a.wscale[0]) : 0.0f;
+#pragma unroll
+          for (int j = 0; j < MJ; ++j) acc[i][j][v] *= s;
+        }
+    }
+    // LoRA: one rank-wide step from sE; A role = bt rows 64w + 32i + l32,
+    // B role = t rows 32j + l32, rank columns 16kk + 8g .. +8
+    if (rp > 0) {
+      const uint16_t* sT = sE;
+      const uint16_t* sBt = sE + 256 * rp;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        if (kk * 16 < rp) {
+          bf16x8 la[NIW];
+#pragma unroll
+          for (int i = 0; i < NIW; ++i) la[i] = as_bf16x8(ld16(sBt + (64 * w + 32 * i + l32) * rp + kk * 16 + g * 8));
+#pragma unroll
+          for (int j = 0; j < MJ; ++j) {
+            const bf16x8 lb = as_bf16x8(ld16(sT + (32 * j + l32) * rp + kk * 16 + g * 8));
+#pragma unroll
+            for (int i = 0; i < NIW; ++i) acc[i][j] = mfma32(la[i], lb, acc[i][j]);
+          }
+        }
+      }
+    }
+    // every wavefront's LoRA reads are done before sE takes output rows
+    __syncthreads();
+    // output: per half of the tokens, the wavefront's [128 tokens][64 n]
+    // bf16 rows go to its sE slice (16-byte chunk c of row r at c ^ swz(r)),
+    // then back out as whole 128-byte row segments, 8 rows per store
+    uint16_t* sO = sE + w * 128 * 64;
+    f32x4 bv[NIW][4];
+#pragma unroll
+    for (int i = 0; i < NIW; ++i)
+#pragma unroll
+      for (int vg = 0; vg < 4; ++vg) {
+        const int64_t n = e0 + 64 * w + 32 * i + 8 * vg + 4 * g;
+        bv[i][vg] = (a.bias && n < E) ? *reinterpret_cast<const f32x4*>(a.bias + n) : (f32x4){0.f, 0.f, 0.f, 0.f};
+      }
+    const rsrc_t ry = make_rsrc(a.out, clamp_bytes(M * E * 2));
+    const int rr = lane >> 3, cc = lane & 7;
+    const int64_t ncol = e0 + 64 * w + 8 * cc;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int row = 32 * jj + l32;
+#pragma unroll
+        for (int i = 0; i < NIW; ++i)
+#pragma unroll
+          for (int vg = 0; vg < 4; ++vg) {
+            const f32x16& c = acc[i][4 * h + jj];
+            u32x2 o;
+            o[0] = pack_bf16x2(c[4 * vg + 0] + bv[i][vg][0], c[4 * vg + 1] + bv[i][vg][1]);
+            o[1] = pack_bf16x2(c[4 * vg + 2] + bv[i][vg][2], c[4 * vg + 3] + bv[i][vg][3]);
+            const int chunk = (4 * i + vg) ^ swz(row);
+            st8(sO + row * 64 + chunk * 8 + g * 4, o);
+          }
+      }
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wavefront's rows are in LDS
+#pragma unroll
+      for (int p = 0; p < 16; ++p) {
+        const int row = 8 * p + rr;
+        const u32x4 v = ld16(sO + row * 64 + (cc ^ swz(row)) * 8);
+        const int64_t m = m0 + 128 * h + row;
+        // rows past M and columns past E fall outside the resource or are skipped
+        const uint32_t off = (m < M && ncol < E) ? (uint32_t)((m * E + ncol) * 2) : LRQ_OOB;
+        __builtin_amdgcn_raw_buffer_store_b128(v, ry, opaque_u32(off), 0, 0);
+      }
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // reads done before the next half's writes
+    }
+  };
+
+  // prologue: the first tile's first NBUF steps in flight
+  TileSrc cur = tile_src(vb), nxt = tile_src(vb + G);
 #pragma unroll
   for (int b = 0; b < NBUF; ++b) {
-    dma(bufs[b], b);
-    load_w(b, b);
+    dma(bufs[b], cur.act, b);
+    load_w(b, cur, b);
   }
+  if (rp > 0) dma_lora(cur.m0, cur.e0);
+  zero_acc();
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < MJ; ++j) fb[0][j] = xfrag(bufs[0], j, 0);
 #pragma unroll
   for (int i = 0; i < NIW; ++i) fa[0][i] = wfrag(0, i, 0);
 
-  for (int kt = 0; kt < nk; kt += NBUF) {
+  for (;;) {
+    int kt = 0;
+    for (; kt + NBUF < nkp; kt += NBUF) {
 #pragma unroll
-    for (int b = 0; b < NBUF; ++b) step(b, kt + b);
+      for (int b = 0; b < NBUF; ++b) step(b, cur, kt + NBUF + b);
+    }
+    // last NBUF steps: prefetch the next tile's first steps
+#pragma unroll
+    for (int b = 0; b < NBUF; ++b) step(b, nxt, b);
+    epilogue(cur.m0, cur.e0);
+    vb += G;
+    if (vb >= ntiles) break;
+    zero_acc();
+    cur = nxt;
+    nxt = tile_src(vb + G);
+    // every wavefront's output reads of sE are done before the next tile's
+    // LoRA operands land there
+    __syncthreads();
+    if (rp > 0) dma_lora(cur.m0, cur.e0);
   }
-
-  // drain the look-ahead copies before the epilogue reads LDS
+  // drain the look-ahead copies before the workgroup ends
   __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-
-  // fp8 forward: the per-output-channel scale factors out of the k reduction
-  if (!I4) {
-#pragma unroll
-    for (int i = 0; i < NIW; ++i)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int64_t n = e0 + 64 * w + 32 * i + 8 * (v >> 2) + 4 * g + (v & 3);
-        const float s = (n < E) ? (a.per_channel ? a.wscale[n] : a.wscale[0]) : 0.0f;
-#pragma unroll
-        for (int j = 0; j < MJ; ++j) acc[i][j][v] *= s;
-      }
-  }
-
-  // LoRA: one rank-wide step; A role = B^T rows from LDS, B role = t [M, rp]
-  // (zero-padded, pre-scaled) from global
-  if (rp > 0) {
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      if (kk * 16 < rp) {
-        bf16x8 la[NIW];
-#pragma unroll
-        for (int i = 0; i < NIW; ++i)
-          la[i] = as_bf16x8(ld16(sB + (64 * w + 32 * i + l32) * LDL + kk * 16 + g * 8));
-#pragma unroll
-        for (int j = 0; j < MJ; ++j) {
-          const int64_t m = m0 + 32 * j + l32;
-          const u32x4 v = ld16(a.lact + (m < M ? m : (M - 1)) * rp + kk * 16 + g * 8);
-          const bf16x8 lb = as_bf16x8(m < M ? v : zero4());
-#pragma unroll
-          for (int i = 0; i < NIW; ++i) acc[i][j] = mfma32(la[i], lb, acc[i][j]);
-        }
-      }
-    }
-  }
-
-  // epilogue: lane holds 4 consecutive n of one token per accumulator group
-#pragma unroll
-  for (int i = 0; i < NIW; ++i) {
-#pragma unroll
-    for (int vg = 0; vg < 4; ++vg) {
-      const int64_t n = e0 + 64 * w + 32 * i + 8 * vg + 4 * g;
-      if (n >= E) continue;
-      f32x4 bv = {0.0f, 0.0f, 0.0f, 0.0f};
-      if (a.bias) bv = *reinterpret_cast<const f32x4*>(a.bias + n);
-#pragma unroll
-      for (int j = 0; j < MJ; ++j) {
-        const int64_t m = m0 + 32 * j + l32;
-        if (m < M) {
-          u32x2 o;
-          o[0] = pack_bf16x2(acc[i][j][4 * vg + 0] + bv[0], acc[i][j][4 * vg + 1] + bv[1]);
-          o[1] = pack_bf16x2(acc[i][j][4 * vg + 2] + bv[2], acc[i][j][4 * vg + 3] + bv[3]);
-          *reinterpret_cast<u32x2*>(a.out + m * E + n) = o;
-        }
-      }
-    }
-  }
 }
 
 template <int FMT, int NBUF>
 hipError_t run(hipStream_t st, const GemmArgs& a) {
   const int tiles_m = (int)((a.m + RB - 1) / RB);
   const int tiles_e = (int)((a.e + RA - 1) / RA);
-  hipLaunchKernelGGL((k_fwd<FMT, NBUF>), dim3(tiles_m * tiles_e), dim3(256), 0, st, a, tiles_m);
+  const int ntiles = tiles_m * tiles_e;
+  const int grid = ntiles < get_num_cus() ? ntiles : get_num_cus();
+  hipLaunchKernelGGL((k_fwd<FMT, NBUF>), dim3(grid), dim3(256), 0, st, a, tiles_m, ntiles);
   return hipGetLastError();
 }
 

@@ -35,7 +35,8 @@ struct GemmArgs {
 };
 
 hipError_t launch_gemm(hipStream_t st, bool bwd, int fmt, const GemmArgs& a);
-// lrq_fwd.hip: the forward for m > 16 (weight dequantized into registers)
+// lrq_fwd.hip: the forward for m > 16 (weight dequantized into registers);
+// a.lw is bt = B^T [n, rp] (zero-padded columns), a.lact is t [m, rp]
 hipError_t launch_fwd(hipStream_t st, int fmt, const GemmArgs& a);
 int get_num_cus();
 
@@ -72,9 +73,11 @@ LoraPlan lora_plan_tn(int64_t M, int64_t C, int rp);
 // [k, r]); entries j >= R read as zero. plan.splits * M * rp floats.
 hipError_t launch_lora_nt(hipStream_t st, const uint16_t* p, const uint16_t* q, bool qrow, int64_t ldq,
                           int R, int64_t M, int64_t C, int rp, const LoraPlan& plan, float* partial);
-// out = bf16(s * sum_s partial[s]) as [M, rp] (columns >= r zero) and/or [M, r].
+// out = bf16(s * sum_s partial[s]) as [M, rp] (columns >= r zero) and/or [M, r];
+// with bt set, also bt = B^T as [N, rp] (columns >= r zero) from B [r, N].
 hipError_t launch_nt_reduce(hipStream_t st, const float* partial, int splits, int64_t M, int rp, int r, float s,
-                            uint16_t* out, uint16_t* out_user);
+                            uint16_t* out, uint16_t* out_user, const uint16_t* B = nullptr, int64_t N = 0,
+                            uint16_t* bt = nullptr);
 // partial[s][c][j] = sum over slice s of p[m, c] * q[m * ldq + j] (f32) for
 // c < C, j < rp (columns j >= R of q read as zero); plan.splits * C * rp floats.
 hipError_t launch_lora_tn(hipStream_t st, const uint16_t* p, const uint16_t* q, int64_t ldq, int64_t M,
