@@ -81,6 +81,8 @@ k_fwd(GemmArgs a, int tiles_m, int ntiles) {
   // epilogue region: the tile's LoRA operands (t rows, then bt rows, each
   // [256][rp]) copied in during the tile, then each wavefront's output rows
   __shared__ __attribute__((aligned(16))) uint16_t sE[4 * 128 * 64];
+  // the tile's bias [256] and fp8 channel scales [256], f32
+  __shared__ __attribute__((aligned(16))) float sAux[2 * RA];
 
   const int G = gridDim.x;
   int vb = blockIdx.x;
@@ -132,11 +134,13 @@ k_fwd(GemmArgs a, int tiles_m, int ntiles) {
     const uint32_t koff = (uint32_t)(k0 * 2);
     __attribute__((address_space(3))) char* base =
         (__attribute__((address_space(3))) char*)(lds_void*)(buf + 64 * w * BK);
+    // the per-load offsets are formed here from opaque bases each step, so
+    // the compiler does not keep 16 hoisted copies live across the loop
+    const uint32_t o0 = opaque_u32(doff0) + koff, o1 = opaque_u32(doff1) + koff;
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
       const bool kok = (c & 1) ? kok1 : kok0;
-      const uint32_t doff = (c & 1) ? doff1 : doff0;
-      const uint32_t off = opaque_u32(kok ? doff + (uint32_t)(c * 8 * K * 2) + koff : LRQ_OOB);
+      const uint32_t off = opaque_u32(kok ? ((c & 1) ? o1 : o0) + (uint32_t)(c * 8 * K * 2) : LRQ_OOB);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(ract, (lds_void*)(base + c * 8 * BK * 2), 16, off, 0, 0, 0);
     }
   };
@@ -235,7 +239,14 @@ k_fwd(GemmArgs a, int tiles_m, int ntiles) {
   const rsrc_t rbt = make_rsrc(a.lw, rp > 0 ? clamp_bytes(E * rp * 2) : 0u);
   const rsrc_t rt = make_rsrc(a.lact, rp > 0 ? clamp_bytes(M * rp * 2) : 0u);
   const int lora_loads = rp / 8;  // 16-byte loads per lane per operand: 256*rp*2 / (256*16)
-  auto dma_lora = [&](int64_t m0, int64_t e0) {
+  const bool has_bias = a.bias != nullptr;
+  const bool pc = !I4 && a.per_channel;
+  const rsrc_t rbias = make_rsrc(a.bias, has_bias ? clamp_bytes(E * 4) : 0u);
+  const rsrc_t rsc = make_rsrc(a.wscale, pc ? clamp_bytes(E * 4) : 0u);
+  // copies for the tile at (m0, e0), issued at its start: LoRA operands to sE,
+  // bias and fp8 channel scales of its 256 output columns to sAux (columns
+  // past E read zeros)
+  auto dma_aux = [&](int64_t m0, int64_t e0) {
     __attribute__((address_space(3))) char* base = (__attribute__((address_space(3))) char*)(lds_void*)sE;
     const uint32_t tb = (uint32_t)(m0 * rp * 2), bb = (uint32_t)(e0 * rp * 2);
     for (int c = 0; c < lora_loads; ++c) {
@@ -244,20 +255,33 @@ k_fwd(GemmArgs a, int tiles_m, int ntiles) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rbt, (lds_void*)(base + 256 * rp * 2 + o), 16,
                                                opaque_u32(bb + o + lane * 16), 0, 0, 0);
     }
+    __attribute__((address_space(3))) char* abase = (__attribute__((address_space(3))) char*)(lds_void*)sAux;
+    const uint32_t co = opaque_u32((uint32_t)(e0 * 4 + lane * 16));
+    if (w == 0 && has_bias) __builtin_amdgcn_raw_ptr_buffer_load_lds(rbias, (lds_void*)abase, 16, co, 0, 0, 0);
+    if (w == 1 && pc) __builtin_amdgcn_raw_ptr_buffer_load_lds(rsc, (lds_void*)(abase + RA * 4), 16, co, 0, 0, 0);
   };
 
-  // epilogue of the tile at (m0, e0)
+  // epilogue of the tile at (m0, e0). Its per-lane values are derived from
+  // an opaque copy of the lane id, so the compiler recomputes them per tile
+  // instead of hoisting them out of the tile loop (where they would only be
+  // spilled: the main loop holds the registers).
   auto epilogue = [&](int64_t m0, int64_t e0) {
+    const int lane = (int)opaque_u32((uint32_t)threadIdx.x & 63u);
+    const int g = lane >> 5, l32 = lane & 31;
     // fp8 forward: the per-output-channel scale factors out of the k reduction
     if (!I4) {
+      const float s0 = a.per_channel ? 0.0f : a.wscale[0];
 #pragma unroll
       for (int i = 0; i < NIW; ++i)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int64_t n = e0 + 64 * w + 32 * i + 8 * (v >> 2) + 4 * g + (v & 3);
-          const float s = (n < E) ? (a.per_channel ? a.wscale[n] : a.wscale[0]) : 0.0f;
+        for (int vg = 0; vg < 4; ++vg) {
+          // per-channel scales of columns past E are zero (those columns are not stored)
+          const f32x4 sv = pc ? *reinterpret_cast<const f32x4*>(sAux + RA + 64 * w + 32 * i + 8 * vg + 4 * g)
+                              : (f32x4){s0, s0, s0, s0};
 #pragma unroll
-          for (int j = 0; j < MJ; ++j) acc[i][j][v] *= s;
+          for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int j = 0; j < MJ; ++j) acc[i][j][4 * vg + q] *= sv[q];
         }
     }
     // LoRA: one rank-wide step from sE; A role = bt rows 64w + 32i + l32,
@@ -286,42 +310,42 @@ k_fwd(GemmArgs a, int tiles_m, int ntiles) {
     // bf16 rows go to its sE slice (16-byte chunk c of row r at c ^ swz(r)),
     // then back out as whole 128-byte row segments, 8 rows per store
     uint16_t* sO = sE + w * 128 * 64;
-    f32x4 bv[NIW][4];
-#pragma unroll
-    for (int i = 0; i < NIW; ++i)
-#pragma unroll
-      for (int vg = 0; vg < 4; ++vg) {
-        const int64_t n = e0 + 64 * w + 32 * i + 8 * vg + 4 * g;
-        bv[i][vg] = (a.bias && n < E) ? *reinterpret_cast<const f32x4*>(a.bias + n) : (f32x4){0.f, 0.f, 0.f, 0.f};
-      }
-    const rsrc_t ry = make_rsrc(a.out, clamp_bytes(M * E * 2));
+    // output rows of this tile: a resource from row m0, so rows past M fall
+    // outside it
+    const rsrc_t ry = make_rsrc(a.out + m0 * E, clamp_bytes((M - m0) * E * 2));
     const int rr = lane >> 3, cc = lane & 7;
     const int64_t ncol = e0 + 64 * w + 8 * cc;
+    const uint32_t ybase0 = (uint32_t)(ncol * 2);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
         const int row = 32 * jj + l32;
+        // one 32-token tile at a time, so few accumulators are in flight
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < NIW; ++i)
 #pragma unroll
           for (int vg = 0; vg < 4; ++vg) {
+            const f32x4 bv = has_bias ? *reinterpret_cast<const f32x4*>(sAux + 64 * w + 32 * i + 8 * vg + 4 * g)
+                                      : (f32x4){0.f, 0.f, 0.f, 0.f};
             const f32x16& c = acc[i][4 * h + jj];
             u32x2 o;
-            o[0] = pack_bf16x2(c[4 * vg + 0] + bv[i][vg][0], c[4 * vg + 1] + bv[i][vg][1]);
-            o[1] = pack_bf16x2(c[4 * vg + 2] + bv[i][vg][2], c[4 * vg + 3] + bv[i][vg][3]);
+            o[0] = pack_bf16x2(c[4 * vg + 0] + bv[0], c[4 * vg + 1] + bv[1]);
+            o[1] = pack_bf16x2(c[4 * vg + 2] + bv[2], c[4 * vg + 3] + bv[3]);
             const int chunk = (4 * i + vg) ^ swz(row);
             st8(sO + row * 64 + chunk * 8 + g * 4, o);
           }
       }
       __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wavefront's rows are in LDS
+      const uint32_t ybase = ybase0 + (uint32_t)(128 * h * E * 2);
 #pragma unroll
       for (int p = 0; p < 16; ++p) {
         const int row = 8 * p + rr;
         const u32x4 v = ld16(sO + row * 64 + (cc ^ swz(row)) * 8);
-        const int64_t m = m0 + 128 * h + row;
-        // rows past M and columns past E fall outside the resource or are skipped
-        const uint32_t off = (m < M && ncol < E) ? (uint32_t)((m * E + ncol) * 2) : LRQ_OOB;
+        // columns past E are skipped (offset past the resource); rows past M
+        // are past it already
+        const uint32_t off = ncol < E ? ybase + (uint32_t)(row * E * 2) : LRQ_OOB;
         __builtin_amdgcn_raw_buffer_store_b128(v, ry, opaque_u32(off), 0, 0);
       }
       __builtin_amdgcn_s_waitcnt(0xc07f);  // reads done before the next half's writes
@@ -329,13 +353,13 @@ k_fwd(GemmArgs a, int tiles_m, int ntiles) {
   };
 
   // prologue: the first tile's first NBUF steps in flight
-  TileSrc cur = tile_src(vb), nxt = tile_src(vb + G);
+  TileSrc cur = tile_src(vb);
 #pragma unroll
   for (int b = 0; b < NBUF; ++b) {
     dma(bufs[b], cur.act, b);
     load_w(b, cur, b);
   }
-  if (rp > 0) dma_lora(cur.m0, cur.e0);
+  dma_aux(cur.m0, cur.e0);
   zero_acc();
   __syncthreads();
 #pragma unroll
@@ -350,6 +374,7 @@ k_fwd(GemmArgs a, int tiles_m, int ntiles) {
       for (int b = 0; b < NBUF; ++b) step(b, cur, kt + NBUF + b);
     }
     // last NBUF steps: prefetch the next tile's first steps
+    const TileSrc nxt = tile_src(vb + G);
 #pragma unroll
     for (int b = 0; b < NBUF; ++b) step(b, nxt, b);
     epilogue(cur.m0, cur.e0);
@@ -357,11 +382,10 @@ k_fwd(GemmArgs a, int tiles_m, int ntiles) {
     if (vb >= ntiles) break;
     zero_acc();
     cur = nxt;
-    nxt = tile_src(vb + G);
     // every wavefront's output reads of sE are done before the next tile's
     // LoRA operands land there
     __syncthreads();
-    if (rp > 0) dma_lora(cur.m0, cur.e0);
+    dma_aux(cur.m0, cur.e0);
   }
   // drain the look-ahead copies before the workgroup ends
   __builtin_amdgcn_s_waitcnt(0);
