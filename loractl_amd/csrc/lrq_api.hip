@@ -5,6 +5,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <algorithm>
 #include <new>
@@ -412,7 +413,10 @@ static int fwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t 
     LRQ_TRY(run(c, KID_LORA_T, "lora_t", [&] {
       hipError_t e = launch_lora_nt(c->stream, x, a, false, r, (int)r, m, w->k, rp, pt, ws.pn);
       if (e != hipSuccess) return e;
-      return launch_nt_reduce(c->stream, ws.pn, pt.splits, m, rp, (int)r, scaling, ws.tp, t_out, b, w->n, ws.bt);
+      // fp8: B^T divided by the weight scale (the GEMM scales base + LoRA)
+      const bool f8 = w->format == LRQ_FMT_FP8;
+      return launch_nt_reduce(c->stream, ws.pn, pt.splits, m, rp, (int)r, scaling, ws.tp, t_out, b, w->n, ws.bt,
+                              f8 ? w->scales : nullptr, f8 && w->per_channel);
     }));
     ga.lact = ws.tp;
     ga.lw = ws.bt;

@@ -268,22 +268,6 @@ k_fwd(GemmArgs a, int tiles_m, int ntiles) {
   auto epilogue = [&](int64_t m0, int64_t e0) {
     const int lane = (int)opaque_u32((uint32_t)threadIdx.x & 63u);
     const int g = lane >> 5, l32 = lane & 31;
-    // fp8 forward: the per-output-channel scale factors out of the k reduction
-    if (!I4) {
-      const float s0 = a.per_channel ? 0.0f : a.wscale[0];
-#pragma unroll
-      for (int i = 0; i < NIW; ++i)
-#pragma unroll
-        for (int vg = 0; vg < 4; ++vg) {
-          // per-channel scales of columns past E are zero (those columns are not stored)
-          const f32x4 sv = pc ? *reinterpret_cast<const f32x4*>(sAux + RA + 64 * w + 32 * i + 8 * vg + 4 * g)
-                              : (f32x4){s0, s0, s0, s0};
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-#pragma unroll
-            for (int j = 0; j < MJ; ++j) acc[i][j][4 * vg + q] *= sv[q];
-        }
-    }
     // LoRA: one rank-wide step from sE; A role = bt rows 64w + 32i + l32,
     // B role = t rows 32j + l32, rank columns 16kk + 8g .. +8
     if (rp > 0) {
@@ -304,12 +288,19 @@ k_fwd(GemmArgs a, int tiles_m, int ntiles) {
         }
       }
     }
+    // keep the accumulators in AGPRs here: the packing below then copies one
+    // tile at a time to VGPRs, instead of the whole set before the LoRA step
+#pragma unroll
+    for (int i = 0; i < NIW; ++i)
+#pragma unroll
+      for (int j = 0; j < MJ; ++j) asm volatile("" : "+a"(acc[i][j]));
     // every wavefront's LoRA reads are done before sE takes output rows
     __syncthreads();
     // output: per half of the tokens, the wavefront's [128 tokens][64 n]
     // bf16 rows go to its sE slice (16-byte chunk c of row r at c ^ swz(r)),
     // then back out as whole 128-byte row segments, 8 rows per store
     uint16_t* sO = sE + w * 128 * 64;
+    const float s0 = (!I4 && !pc) ? a.wscale[0] : 1.0f;
     // output rows of this tile: a resource from row m0, so rows past M fall
     // outside it
     const rsrc_t ry = make_rsrc(a.out + m0 * E, clamp_bytes((M - m0) * E * 2));
@@ -329,10 +320,16 @@ k_fwd(GemmArgs a, int tiles_m, int ntiles) {
           for (int vg = 0; vg < 4; ++vg) {
             const f32x4 bv = has_bias ? *reinterpret_cast<const f32x4*>(sAux + 64 * w + 32 * i + 8 * vg + 4 * g)
                                       : (f32x4){0.f, 0.f, 0.f, 0.f};
+            // fp8: the per-output-channel scale factors out of the k
+            // reduction (the LoRA operand bt arrives divided by it);
+            // per-channel scales of columns past E are zero (not stored)
+            const f32x4 sv = I4 ? (f32x4){1.f, 1.f, 1.f, 1.f}
+                                : (pc ? *reinterpret_cast<const f32x4*>(sAux + RA + 64 * w + 32 * i + 8 * vg + 4 * g)
+                                      : (f32x4){s0, s0, s0, s0});
             const f32x16& c = acc[i][4 * h + jj];
             u32x2 o;
-            o[0] = pack_bf16x2(c[4 * vg + 0] + bv[0], c[4 * vg + 1] + bv[1]);
-            o[1] = pack_bf16x2(c[4 * vg + 2] + bv[2], c[4 * vg + 3] + bv[3]);
+            o[0] = pack_bf16x2(__builtin_fmaf(c[4 * vg + 0], sv[0], bv[0]), __builtin_fmaf(c[4 * vg + 1], sv[1], bv[1]));
+            o[1] = pack_bf16x2(__builtin_fmaf(c[4 * vg + 2], sv[2], bv[2]), __builtin_fmaf(c[4 * vg + 3], sv[3], bv[3]));
             const int chunk = (4 * i + vg) ^ swz(row);
             st8(sO + row * 64 + chunk * 8 + g * 4, o);
           }

@@ -12,6 +12,8 @@ hipError_t launch_quantize_fp8(hipStream_t st, const float* w, int64_t n, int64_
                                int per_channel, uint8_t* bytes, float* scales, float* amax_ws);
 hipError_t launch_dequant(hipStream_t st, const lrq_weight* w, void* out, bool bf16);
 void blocked_sizes(int fmt, int64_t n, int64_t k, int64_t group, int64_t* data_bytes, int64_t* scale_count);
+// bytes of one section of the blocked data (the row-blocked or the transposed part)
+int64_t blocked_part_bytes(int fmt, int64_t n, int64_t k);
 hipError_t launch_block(hipStream_t st, const lrq_weight* w, uint8_t* data, float* scales);
 
 // Arguments of the fused GEMM (lrq_gemm.hip), one struct for both passes:
@@ -74,10 +76,11 @@ LoraPlan lora_plan_tn(int64_t M, int64_t C, int rp);
 hipError_t launch_lora_nt(hipStream_t st, const uint16_t* p, const uint16_t* q, bool qrow, int64_t ldq,
                           int R, int64_t M, int64_t C, int rp, const LoraPlan& plan, float* partial);
 // out = bf16(s * sum_s partial[s]) as [M, rp] (columns >= r zero) and/or [M, r];
-// with bt set, also bt = B^T as [N, rp] (columns >= r zero) from B [r, N].
+// with bt set, also bt = B^T as [N, rp] (columns >= r zero) from B [r, N],
+// divided by bdiv[n] (bdiv_rows) or bdiv[0] when bdiv is set (an fp8 weight scale).
 hipError_t launch_nt_reduce(hipStream_t st, const float* partial, int splits, int64_t M, int rp, int r, float s,
                             uint16_t* out, uint16_t* out_user, const uint16_t* B = nullptr, int64_t N = 0,
-                            uint16_t* bt = nullptr);
+                            uint16_t* bt = nullptr, const float* bdiv = nullptr, bool bdiv_rows = false);
 // partial[s][c][j] = sum over slice s of p[m, c] * q[m * ldq + j] (f32) for
 // c < C, j < rp (columns j >= R of q read as zero); plan.splits * C * rp floats.
 hipError_t launch_lora_tn(hipStream_t st, const uint16_t* p, const uint16_t* q, int64_t ldq, int64_t M,
