@@ -468,7 +468,7 @@ static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const ui
     ga.lw = a;
     ga.r = (int)r;
     ga.rp = rp;
-    if (dx) LRQ_TRY(run(c, KID_BWD_DX, "bwd_dx", [&] { return launch_gemm(c->stream, true, w->format, ga); }));
+    if (dx) LRQ_TRY(run(c, KID_BWD_DX, "bwd_dx", [&] { return launch_dx(c->stream, w->format, ga); }));
     // dA = x^T . u -> f32 [k, r] and dB = t^T . dy -> f32 [r, n]: token-slice
     // partials, then one reduction launch for both
     TnJob jobs[2];
@@ -491,7 +491,7 @@ static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const ui
     return LRQ_OK;
   }
   if (!dx) return LRQ_OK;
-  return run(c, KID_BWD_DX, "bwd_dx", [&] { return launch_gemm(c->stream, true, w->format, ga); });
+  return run(c, KID_BWD_DX, "bwd_dx", [&] { return launch_dx(c->stream, w->format, ga); });
 }
 
 int lrq_quant_matmul_t_bwd(lrq_ctx* c, const lrq_weight* w, const uint16_t* dy, int64_t m, uint16_t* dx) {

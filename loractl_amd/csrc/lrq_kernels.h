@@ -12,14 +12,15 @@ hipError_t launch_quantize_fp8(hipStream_t st, const float* w, int64_t n, int64_
                                int per_channel, uint8_t* bytes, float* scales, float* amax_ws);
 hipError_t launch_dequant(hipStream_t st, const lrq_weight* w, void* out, bool bf16);
 void blocked_sizes(int fmt, int64_t n, int64_t k, int64_t group, int64_t* data_bytes, int64_t* scale_count);
-// bytes of one section of the blocked data (the row-blocked or the transposed part)
-int64_t blocked_part_bytes(int fmt, int64_t n, int64_t k);
 hipError_t launch_block(hipStream_t st, const lrq_weight* w, uint8_t* data, float* scales);
 
-// Arguments of the fused GEMM (lrq_gemm.hip), one struct for both passes:
-//   forward  : act = x  [m, k], l = k, e = n; lact = t [m, rp]; lw = B [r, n]
-//   backward : act = dy [m, n], l = n, e = k; lact = u [m, rp]; lw = A [k, r]
-// The weight is always the file-layout [n, k] packed tensor (wk = k).
+// Arguments of the fused GEMMs, one struct for both passes:
+//   forward  (lrq_fwd.hip, lrq_skinny.hip): act = x [m, k], l = k, e = n;
+//            lact = t [m, rp]; lw = bt = B^T [n, rp] (lrq_fwd.hip) or
+//            B [r, n] (lrq_skinny.hip)
+//   backward (lrq_dx.hip): act = dy [m, n], l = n, e = k; lact = u [m, rp];
+//            lw = A [k, r]
+// The weight is the blocked packed tensor of the [n, k] file layout (wk = k).
 struct GemmArgs {
   const uint16_t* act;
   int64_t m, l, e, wk;
@@ -36,7 +37,9 @@ struct GemmArgs {
   uint16_t* out;         // [m, e]
 };
 
-hipError_t launch_gemm(hipStream_t st, bool bwd, int fmt, const GemmArgs& a);
+// lrq_dx.hip: dx = dy . bf16(dq(W)) + u . A^T (weight dequantized into a
+// transposed LDS tile)
+hipError_t launch_dx(hipStream_t st, int fmt, const GemmArgs& a);
 // lrq_fwd.hip: the forward for m > 16 (weight dequantized into registers);
 // a.lw is bt = B^T [n, rp] (zero-padded columns), a.lact is t [m, rp]
 hipError_t launch_fwd(hipStream_t st, int fmt, const GemmArgs& a);
