@@ -44,7 +44,14 @@
  *   block the rows keep the row-layout byte order (int4: 32 bytes per row,
  *   fp8: 64). int4 scales become [NB][Gp][64] (NB = ceil(n/64),
  *   Gp = 64*KB/group); fp8 scales are unchanged. Padding rows/columns hold
- *   q = 0 with scale 0 (int4) or byte 0 (fp8).
+ *   q = 0 with scale 0 (int4) or byte 0 (fp8). A transposed section of the
+ *   same byte size follows, read by the input-gradient kernel (its reduction
+ *   runs along n): the same blocking applied to W^T [k, n] (block (kb, nb)
+ *   at (kb * NB + nb) * block bytes, rows along k), int4 nibbles holding q
+ *   in two's complement, and for int4 a second scale table ST [KGt][NB*64]
+ *   (KGt = ceil(64*KB/group), ST[kg][n] = scale of row n, group kg) after
+ *   the [NB][Gp][64] one. The blocked weight thus takes twice the packed
+ *   bytes (38 MB for an int4 12288 x 3072 weight).
  *   LoRA factors in burn layout: A = [k, r] (d_in x rank), B = [r, n].
  */
 #ifndef LORACTL_ROCM_H
@@ -113,8 +120,8 @@ int lrq_quantize_int4(lrq_ctx* ctx, const float* w, int64_t n, int64_t k, int64_
 int lrq_quantize_fp8(lrq_ctx* ctx, const float* w, int64_t n, int64_t k, int per_channel,
                      uint8_t* bytes, float* scales);
 
-/* Sizes of the blocked layout of a weight: data bytes and scale count
- * (0 for fp8, whose scales keep their shape). No device work. */
+/* Sizes of the blocked layout of a weight, both sections: data bytes and
+ * scale count (0 for fp8, whose scales keep their shape). No device work. */
 int lrq_weight_blocked_size(int format, int64_t n, int64_t k, int64_t group, int64_t* data_bytes,
                             int64_t* scale_count);
 

@@ -138,8 +138,11 @@ int ensure_ws(lrq_ctx* c, size_t bytes) {
 // Workspace layout of the fused calls (sizes only when base == nullptr): t
 // and u padded to rp columns (the GEMM epilogue operands) and the f32
 // partials of the LoRA reductions (t or u; dA and dB side by side).
+// LoRA workspace: t and u padded to rp columns, the weight-side factor rows
+// of the fused GEMM's LoRA step (B^T [n, rp] forward, A [k, rp] backward),
+// and the side kernels' f32 partials.
 struct LoraWs {
-  uint16_t *tp, *up, *bt;
+  uint16_t *tp, *up, *fr;
   float *pn, *pa, *pb;
   size_t bytes;
 };
@@ -149,7 +152,7 @@ LoraWs lora_layout(char* base, int64_t m, int64_t n, int64_t k, int rp) {
   LoraWs w{};
   w.tp = s.take<uint16_t>(m * rp);
   w.up = s.take<uint16_t>(m * rp);
-  w.bt = s.take<uint16_t>(n * rp);
+  w.fr = s.take<uint16_t>(std::max(n, k) * rp);
   const int64_t nt = std::max((int64_t)lora_plan_nt(m, k, rp).splits, (int64_t)lora_plan_nt(m, n, rp).splits);
   w.pn = s.take<float>(std::max(nt * m * rp, (int64_t)1));
   w.pa = s.take<float>((int64_t)lora_plan_tn(m, k, rp).splits * k * rp);
@@ -347,8 +350,12 @@ static GemmArgs gemm_args(const lrq_weight* w, bool bwd, const uint16_t* act, in
   g.l = bwd ? w->n : w->k;
   g.e = bwd ? w->k : w->n;
   g.wk = w->k;
-  g.wdata = reinterpret_cast<const uint8_t*>(w->data);
-  g.wscale = w->scales;
+  // forward: the row section of the blocked layout; backward: the transposed
+  // section (and, int4, its scale table) that follows it
+  int64_t db = 0, sc = 0;
+  if (bwd) blocked_sections(w->format, w->n, w->k, w->group, &db, &sc);
+  g.wdata = reinterpret_cast<const uint8_t*>(w->data) + db;
+  g.wscale = w->scales + sc;
   g.group = w->group;
   g.gshift = 0;
   while (w->group > 0 && (1 << g.gshift) < w->group) ++g.gshift;
@@ -363,7 +370,7 @@ static int check_gemm(lrq_ctx* c, const lrq_weight* w, int64_t m) {
   LRQ_TRY(check_weight(c, w, true));
   if (m < 0) return fail(c, LRQ_EINVAL, "negative token count");
   int64_t wbytes = 0, nscales = 0;
-  blocked_sizes(w->format, w->n, w->k, w->group, &wbytes, &nscales);
+  blocked_sections(w->format, w->n, w->k, w->group, &wbytes, &nscales);
   if (wbytes >= (int64_t)1 << 31)
     return fail(c, LRQ_EUNSUPPORTED, "packed weight of %lld bytes: the fused kernels address at most 2 GiB",
                 (long long)wbytes);
@@ -415,11 +422,11 @@ static int fwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t 
       if (e != hipSuccess) return e;
       // fp8: B^T divided by the weight scale (the GEMM scales base + LoRA)
       const bool f8 = w->format == LRQ_FMT_FP8;
-      return launch_nt_reduce(c->stream, ws.pn, pt.splits, m, rp, (int)r, scaling, ws.tp, t_out, b, w->n, ws.bt,
-                              f8 ? w->scales : nullptr, f8 && w->per_channel);
+      return launch_nt_reduce(c->stream, ws.pn, pt.splits, m, rp, (int)r, scaling, ws.tp, t_out, b, w->n, false,
+                              ws.fr, f8 ? w->scales : nullptr, f8 && w->per_channel);
     }));
     ga.lact = ws.tp;
-    ga.lw = ws.bt;
+    ga.lw = ws.fr;
     ga.r = (int)r;
     ga.rp = rp;
   }
@@ -462,13 +469,15 @@ static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const ui
     LRQ_TRY(run(c, KID_LORA_U, "lora_u", [&] {
       hipError_t e = launch_lora_nt(c->stream, dy, b, true, w->n, (int)r, m, w->n, rp, pu, ws.pn);
       if (e != hipSuccess) return e;
-      return launch_nt_reduce(c->stream, ws.pn, pu.splits, m, rp, (int)r, scaling, ws.up, nullptr);
+      // and A [k, r] padded to [k, rp]: the dx GEMM's weight-side LoRA rows
+      return launch_nt_reduce(c->stream, ws.pn, pu.splits, m, rp, (int)r, scaling, ws.up, nullptr, a, w->k, true,
+                              ws.fr);
     }));
     ga.lact = ws.up;
-    ga.lw = a;
+    ga.lw = ws.fr;
     ga.r = (int)r;
     ga.rp = rp;
-    if (dx) LRQ_TRY(run(c, KID_BWD_DX, "bwd_dx", [&] { return launch_dx(c->stream, w->format, ga); }));
+    if (dx) LRQ_TRY(run(c, KID_BWD_DX, "bwd_dx", [&] { return launch_bwd(c->stream, w->format, ga); }));
     // dA = x^T . u -> f32 [k, r] and dB = t^T . dy -> f32 [r, n]: token-slice
     // partials, then one reduction launch for both
     TnJob jobs[2];
@@ -491,7 +500,7 @@ static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const ui
     return LRQ_OK;
   }
   if (!dx) return LRQ_OK;
-  return run(c, KID_BWD_DX, "bwd_dx", [&] { return launch_dx(c->stream, w->format, ga); });
+  return run(c, KID_BWD_DX, "bwd_dx", [&] { return launch_bwd(c->stream, w->format, ga); });
 }
 
 int lrq_quant_matmul_t_bwd(lrq_ctx* c, const lrq_weight* w, const uint16_t* dy, int64_t m, uint16_t* dx) {

@@ -11,16 +11,19 @@ hipError_t launch_quantize_int4(hipStream_t st, const float* w, int64_t n, int64
 hipError_t launch_quantize_fp8(hipStream_t st, const float* w, int64_t n, int64_t k,
                                int per_channel, uint8_t* bytes, float* scales, float* amax_ws);
 hipError_t launch_dequant(hipStream_t st, const lrq_weight* w, void* out, bool bf16);
+// whole blocked layout (both sections)
 void blocked_sizes(int fmt, int64_t n, int64_t k, int64_t group, int64_t* data_bytes, int64_t* scale_count);
+// the row-blocked section alone (the transposed section starts at these offsets)
+void blocked_sections(int fmt, int64_t n, int64_t k, int64_t group, int64_t* data_bytes, int64_t* scale_count);
 hipError_t launch_block(hipStream_t st, const lrq_weight* w, uint8_t* data, float* scales);
 
 // Arguments of the fused GEMMs, one struct for both passes:
-//   forward  (lrq_fwd.hip, lrq_skinny.hip): act = x [m, k], l = k, e = n;
-//            lact = t [m, rp]; lw = bt = B^T [n, rp] (lrq_fwd.hip) or
+//   forward  (lrq_gemm.hip, lrq_skinny.hip): act = x [m, k], l = k, e = n;
+//            lact = t [m, rp]; lw = B^T [n, rp] (lrq_gemm.hip) or
 //            B [r, n] (lrq_skinny.hip)
-//   backward (lrq_dx.hip): act = dy [m, n], l = n, e = k; lact = u [m, rp];
-//            lw = A [k, r]
-// The weight is the blocked packed tensor of the [n, k] file layout (wk = k).
+//   backward (lrq_gemm.hip): act = dy [m, n], l = n, e = k; lact = u [m, rp];
+//            lw = A [k, rp]
+// The weight is a section of the blocked layout (wk = k).
 struct GemmArgs {
   const uint16_t* act;
   int64_t m, l, e, wk;
@@ -37,12 +40,12 @@ struct GemmArgs {
   uint16_t* out;         // [m, e]
 };
 
-// lrq_dx.hip: dx = dy . bf16(dq(W)) + u . A^T (weight dequantized into a
-// transposed LDS tile)
-hipError_t launch_dx(hipStream_t st, int fmt, const GemmArgs& a);
-// lrq_fwd.hip: the forward for m > 16 (weight dequantized into registers);
-// a.lw is bt = B^T [n, rp] (zero-padded columns), a.lact is t [m, rp]
+// lrq_gemm.hip: the forward for m > 16 and the input gradient, weight
+// dequantized into registers. a.lw is the weight-side LoRA rows [e, rp]
+// (B^T forward, A backward; zero-padded columns), a.lact is t or u [m, rp].
+// The backward's a.wdata / a.wscale point at the transposed section.
 hipError_t launch_fwd(hipStream_t st, int fmt, const GemmArgs& a);
+hipError_t launch_bwd(hipStream_t st, int fmt, const GemmArgs& a);
 int get_num_cus();
 
 // lrq_skinny.hip: the forward for m <= 16 in two launches. `part` streams the
@@ -79,11 +82,13 @@ LoraPlan lora_plan_tn(int64_t M, int64_t C, int rp);
 hipError_t launch_lora_nt(hipStream_t st, const uint16_t* p, const uint16_t* q, bool qrow, int64_t ldq,
                           int R, int64_t M, int64_t C, int rp, const LoraPlan& plan, float* partial);
 // out = bf16(s * sum_s partial[s]) as [M, rp] (columns >= r zero) and/or [M, r];
-// with bt set, also bt = B^T as [N, rp] (columns >= r zero) from B [r, N],
+// with fr set, also the fused GEMM's weight-side LoRA rows fr [N, rp]
+// (columns >= r zero): B^T from B [r, N], or (b_rows) A [N, r] itself,
 // divided by bdiv[n] (bdiv_rows) or bdiv[0] when bdiv is set (an fp8 weight scale).
 hipError_t launch_nt_reduce(hipStream_t st, const float* partial, int splits, int64_t M, int rp, int r, float s,
                             uint16_t* out, uint16_t* out_user, const uint16_t* B = nullptr, int64_t N = 0,
-                            uint16_t* bt = nullptr, const float* bdiv = nullptr, bool bdiv_rows = false);
+                            bool b_rows = false, uint16_t* fr = nullptr, const float* bdiv = nullptr,
+                            bool bdiv_rows = false);
 // partial[s][c][j] = sum over slice s of p[m, c] * q[m * ldq + j] (f32) for
 // c < C, j < rp (columns j >= R of q read as zero); plan.splits * C * rp floats.
 hipError_t launch_lora_tn(hipStream_t st, const uint16_t* p, const uint16_t* q, int64_t ldq, int64_t M,

@@ -170,29 +170,30 @@ __global__ void __launch_bounds__(LNT) k_lora_nt(NtArgs a) {
 }
 
 // out[m, j] = bf16(s * sum over splits (in order) of partial[sp][m][j]); as
-// [M, rp] (columns >= r zero) and/or [M, r]. Threads past M * rp write
-// bt = B^T as [N, rp] (columns >= r zero) from B [r, N] when bt is set: the
-// up factor as the forward GEMM's LoRA step reads it. With bdiv, each value
-// is divided by bdiv[n] (bdiv_rows) or bdiv[0] and rounded to bf16: the
-// forward multiplies its accumulators (base + LoRA) by the fp8 weight scale,
-// so the LoRA factor arrives pre-divided by it.
+// [M, rp] (columns >= r zero) and/or [M, r]. Threads past M * rp write the
+// weight-side LoRA rows fr [N, rp] (columns >= r zero) when fr is set, as
+// the fused GEMM's LoRA step reads them: B^T from B [r, N] (forward), or A
+// [N, r] row for row (b_rows, backward). With bdiv, each value is divided by
+// bdiv[n] (bdiv_rows) or bdiv[0] and rounded to bf16: the forward multiplies
+// its accumulators (base + LoRA) by the fp8 weight scale, so the LoRA factor
+// arrives pre-divided by it.
 __global__ void __launch_bounds__(256) k_nt_reduce(const float* __restrict__ partial, int splits, int64_t M,
                                                    int rp, int r, float s, uint16_t* __restrict__ out,
                                                    uint16_t* __restrict__ out_user, const uint16_t* __restrict__ B,
-                                                   int64_t N, uint16_t* __restrict__ bt,
+                                                   int64_t N, int b_rows, uint16_t* __restrict__ fr,
                                                    const float* __restrict__ bdiv, int bdiv_rows) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= M * rp) {
     const int64_t i2 = idx - M * rp;
-    if (!bt || i2 >= N * rp) return;
+    if (!fr || i2 >= N * rp) return;
     const int64_t n = i2 / rp;
     const int j = (int)(i2 % rp);
-    uint16_t v = j < r ? B[(int64_t)j * N + n] : (uint16_t)0;
+    uint16_t v = j < r ? B[b_rows ? n * r + j : (int64_t)j * N + n] : (uint16_t)0;
     if (bdiv && j < r) {
       const float d = bdiv[bdiv_rows ? n : 0];
       v = f32_to_bf16_bits(__builtin_bit_cast(float, (uint32_t)v << 16) / d);
     }
-    bt[i2] = v;
+    fr[i2] = v;
     return;
   }
   const int64_t m = idx / rp;
@@ -431,12 +432,12 @@ hipError_t launch_lora_nt(hipStream_t st, const uint16_t* p, const uint16_t* q, 
 }
 
 hipError_t launch_nt_reduce(hipStream_t st, const float* partial, int splits, int64_t M, int rp, int r, float s,
-                            uint16_t* out, uint16_t* out_user, const uint16_t* B, int64_t N, uint16_t* bt,
-                            const float* bdiv, bool bdiv_rows) {
-  const int64_t total = M * rp + (bt ? N * rp : 0);
+                            uint16_t* out, uint16_t* out_user, const uint16_t* B, int64_t N, bool b_rows,
+                            uint16_t* fr, const float* bdiv, bool bdiv_rows) {
+  const int64_t total = M * rp + (fr ? N * rp : 0);
   if (total == 0) return hipSuccess;
   hipLaunchKernelGGL(k_nt_reduce, dim3((unsigned)cdiv(total, 256)), dim3(256), 0, st, partial, splits, M, rp, r,
-                     s, out, out_user, B, N, bt, bdiv, bdiv_rows ? 1 : 0);
+                     s, out, out_user, B, N, b_rows ? 1 : 0, fr, bdiv, bdiv_rows ? 1 : 0);
   return hipGetLastError();
 }
 

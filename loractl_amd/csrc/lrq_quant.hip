@@ -145,7 +145,8 @@ __global__ void __launch_bounds__(256) k_fp8_encode(const float* __restrict__ w,
 // contiguous in memory (int4: 64 rows x 32 bytes; fp8: 64 rows x 64 bytes),
 // block (nb, kb) at (nb * KB + kb) * block bytes, KB = ceil(k / 64); int4
 // scales as [NB][Gp][64] (Gp = 64*KB / group). Rows past n and columns past
-// k are padding: int4 nibbles 8 (q = 0) with scale 0, fp8 bytes 0.
+// k are padding: int4 nibbles 8 (q = 0) with scale 0, fp8 bytes 0. A second,
+// transposed section of the same size follows (k_block_data_t).
 LRQ_DEV int64_t blk_data_off(int fmt, int64_t n, int64_t k, int64_t KB) {
   const int64_t rb = (fmt == LRQ_FMT_INT4) ? 32 : 64;  // bytes per block row
   const int64_t kb = k >> 6, kin = k & 63;
@@ -181,6 +182,55 @@ __global__ void __launch_bounds__(256) k_block_scales(const float* __restrict__ 
   const int64_t r = tid & 63, j = (tid >> 6) % Gp, nb = (tid >> 6) / Gp;
   const int64_t row = nb * 64 + r;
   dst[tid] = (row < n && j < G) ? src[row * G + j] : 0.0f;
+}
+
+// Transposed section, read by the input-gradient GEMM (its reduction runs
+// along n): the blocked layout of W^T [k, n], i.e. 64 (k) x 64 (n) blocks,
+// block (kb, nb) at (kb * NB + nb) * block bytes, block row r = k. int4: 32
+// bytes per row, byte c holding n = 2c in its low nibble and 2c+1 in its high
+// nibble, each nibble q in two's complement (the kernel sign-extends it);
+// fp8: 64 bytes per row. Padding is q = 0 (int4) or byte 0 (fp8). One thread
+// per 16 output bytes (32 or 16 values of one k row, gathered from as many
+// rows of the row layout).
+__global__ void __launch_bounds__(256) k_block_data_t(const uint8_t* __restrict__ src, int64_t n, int64_t k,
+                                                      int fmt, int64_t NB, int64_t KB, uint8_t* __restrict__ dst) {
+  const bool i4 = fmt == LRQ_FMT_INT4;
+  const int64_t per_row = i4 ? 2 : 4;  // 16-byte chunks per block row
+  const int64_t chunks = KB * NB * 64 * per_row;
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (tid >= chunks) return;
+  const int64_t per_blk = 64 * per_row;
+  const int64_t blk = tid / per_blk, inb = tid % per_blk;
+  const int64_t kb = blk / NB, nb = blk % NB;
+  const int64_t kk = kb * 64 + inb / per_row;
+  const int64_t n0 = nb * 64 + (inb % per_row) * (i4 ? 32 : 16);
+  u32x4 v = zero4();
+  if (kk < k) {
+    if (i4) {
+      for (int e = 0; e < 32; ++e) {
+        if (n0 + e >= n) break;
+        const uint32_t byte = src[(n0 + e) * (k / 2) + kk / 2];
+        const uint32_t u = (kk & 1) ? (byte >> 4) : (byte & 15u);  // q + 8
+        v[e >> 3] |= ((u - 8u) & 15u) << (4 * (e & 7));
+      }
+    } else {
+      for (int e = 0; e < 16; ++e) {
+        if (n0 + e >= n) break;
+        v[e >> 2] |= (uint32_t)src[(n0 + e) * k + kk] << (8 * (e & 3));
+      }
+    }
+  }
+  st16(dst + tid * 16, v);
+}
+
+// int4 scales of the transposed section: ST [KGt][NB*64], ST[kg][n] = scale
+// of row n, group kg (zero for padding rows and groups).
+__global__ void __launch_bounds__(256) k_block_scales_t(const float* __restrict__ src, int64_t n, int64_t G,
+                                                        int64_t KGt, int64_t NP, float* __restrict__ dst) {
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (tid >= KGt * NP) return;
+  const int64_t kg = tid / NP, row = tid % NP;
+  dst[tid] = (row < n && kg < G) ? src[row * G + kg] : 0.0f;
 }
 
 // ------------------------------------------------------------------ dequantize
@@ -286,22 +336,42 @@ hipError_t launch_dequant(hipStream_t st, const lrq_weight* w, void* out, bool b
   return hipGetLastError();
 }
 
-void blocked_sizes(int fmt, int64_t n, int64_t k, int64_t group, int64_t* data_bytes, int64_t* scale_count) {
+void blocked_sections(int fmt, int64_t n, int64_t k, int64_t group, int64_t* data_bytes, int64_t* scale_count) {
   const int64_t NB = (n + 63) / 64, KB = (k + 63) / 64;
   *data_bytes = NB * KB * 64 * (fmt == LRQ_FMT_INT4 ? 32 : 64);
   *scale_count = (fmt == LRQ_FMT_INT4) ? NB * (KB * 64 / group) * 64 : 0;
+}
+
+int64_t blocked_t_scale_count(int fmt, int64_t n, int64_t k, int64_t group) {
+  if (fmt != LRQ_FMT_INT4) return 0;
+  const int64_t NB = (n + 63) / 64, KB = (k + 63) / 64;
+  return (KB * 64 + group - 1) / group * NB * 64;
+}
+
+void blocked_sizes(int fmt, int64_t n, int64_t k, int64_t group, int64_t* data_bytes, int64_t* scale_count) {
+  int64_t db = 0, sc = 0;
+  blocked_sections(fmt, n, k, group, &db, &sc);
+  *data_bytes = 2 * db;
+  *scale_count = sc + blocked_t_scale_count(fmt, n, k, group);
 }
 
 hipError_t launch_block(hipStream_t st, const lrq_weight* w, uint8_t* data, float* scales) {
   const int64_t n = w->n, k = w->k;
   const int64_t NB = (n + 63) / 64, KB = (k + 63) / 64;
   int64_t db = 0, sc = 0;
-  blocked_sizes(w->format, n, k, w->group, &db, &sc);
+  blocked_sections(w->format, n, k, w->group, &db, &sc);
   if (db == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_block_data, dim3(blocks_for(db / 16, 256)), dim3(256), 0, st,
-                     reinterpret_cast<const uint8_t*>(w->data), n, k, w->format, NB, KB, data);
-  if (w->format == LRQ_FMT_INT4 && sc > 0)
+  const uint8_t* src = reinterpret_cast<const uint8_t*>(w->data);
+  hipLaunchKernelGGL(k_block_data, dim3(blocks_for(db / 16, 256)), dim3(256), 0, st, src, n, k, w->format, NB, KB,
+                     data);
+  hipLaunchKernelGGL(k_block_data_t, dim3(blocks_for(db / 16, 256)), dim3(256), 0, st, src, n, k, w->format, NB,
+                     KB, data + db);
+  if (w->format == LRQ_FMT_INT4 && sc > 0) {
     hipLaunchKernelGGL(k_block_scales, dim3(blocks_for(sc, 256)), dim3(256), 0, st, w->scales, n,
                        k / w->group, NB, KB * 64 / w->group, scales);
+    const int64_t st_count = blocked_t_scale_count(w->format, n, k, w->group);
+    hipLaunchKernelGGL(k_block_scales_t, dim3(blocks_for(st_count, 256)), dim3(256), 0, st, w->scales, n,
+                       k / w->group, st_count / (NB * 64), NB * 64, scales + sc);
+  }
   return hipGetLastError();
 }

@@ -133,11 +133,33 @@ def test_blocked_layout_roundtrip(cuda, fmt, N, K, g):
         kk -= kk % (2 if fmt == "int4" else 1)
         off = (((n_ // 64) * KB + kk // 64) * 64 + n_ % 64) * rb + ((kk % 64) // 2 if fmt == "int4" else kk % 64)
         assert dst[off] == src[n_, kk // 2 if fmt == "int4" else kk]
+    # the transposed section after it: W^T blocked, block (k/64, n/64), rows
+    # along k; int4 nibbles hold q (two's complement), byte c of a row holds
+    # n = 2c (low) and 2c+1 (high)
+    NB = (N + 63) // 64
+    t0 = NB * KB * 64 * rb
+    assert dst.size == 2 * t0
+    for n_, kk in [(0, 0), (N - 1, K - 1), (N // 2 + 1, K // 2 + 3), (N - 2, 1)]:
+        off = t0 + ((kk // 64) * NB + n_ // 64) * 64 * rb + (kk % 64) * rb
+        if fmt == "int4":
+            u = (src[n_, kk // 2] >> (4 * (kk % 2))) & 15  # q + 8 in the row layout
+            nib = (dst[off + (n_ % 64) // 2] >> (4 * (n_ % 2))) & 15
+            assert nib == (int(u) - 8) & 15
+        else:
+            assert dst[off + n_ % 64] == src[n_, kk]
+    if N % 64:  # padding depth columns of the last block column are zero (N is even here)
+        last = dst[t0 + (NB - 1) * 64 * rb:t0 + NB * 64 * rb].reshape(64, rb)
+        assert not last[:, ((N % 64) // 2 if fmt == "int4" else N % 64):].any()
     if fmt == "int4":
-        NB = (N + 63) // 64
         Gp = KB * 64 // g
-        sc = blk.scales.cpu().numpy().reshape(NB, Gp, 64)
+        allsc = blk.scales.cpu().numpy()
+        sc = allsc[:NB * Gp * 64].reshape(NB, Gp, 64)
         ref = rows.scales.cpu().numpy()
         assert np.array_equal(sc[(N - 1) // 64, (K - 1) // g, (N - 1) % 64], ref[N - 1, (K - 1) // g])
         if N % 64:
             assert not sc[NB - 1, :, N % 64:].any()  # padding rows carry scale 0
+        # transposed scale table ST [ceil(64 KB / g)][NB*64]: ST[kg][n] = scale(n, kg)
+        KGt = (KB * 64 + g - 1) // g
+        st = allsc[NB * Gp * 64:].reshape(KGt, NB * 64)
+        assert np.array_equal(st[:K // g, :N], ref.T)
+        assert not st[:, N:].any() and not st[K // g:].any()
