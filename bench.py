@@ -220,7 +220,11 @@ def bench_skinny(args, dev):
     w, x, a, b, _ = make_inputs(M, K, N, r)
     wq = D.quantize_int4(torch.from_numpy(w).to(dev), group)
     wb = D.compute_weight(wq)
-    wbytes = wb.data.numel() + 4 * wb.scales.numel()
+    # the row section of the blocked layout, the part the few-token kernel
+    # reads: half the data (the transposed section follows) and the first
+    # [NB][Gp][64] scales
+    NB, KB = (N + 63) // 64, (K + 63) // 64
+    wbytes = wb.data.numel() // 2 + 4 * NB * (KB * 64 // group) * 64
     ncopy = max(2, math.ceil(1.15 * INFINITY_CACHE_BYTES / wbytes))
     copies = [wb] + [D.PackedWeight(wb.fmt, wb.n, wb.k, wb.data.clone(), wb.scales.clone(), wb.group,
                                     wb.per_channel, None, L.LRQ_LAYOUT_BLOCKED) for _ in range(ncopy - 1)]
