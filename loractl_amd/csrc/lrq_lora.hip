@@ -59,20 +59,29 @@ struct NtArgs {
 
 constexpr int NQ_BYTES = 100 * 1024;  // factor slice in LDS
 
+// LDS row stride of the factor slice: whole 512-column runs plus 8 bf16 of
+// padding (16 consecutive rows at one column then cover all banks)
+LRQ_DEV int nt_stride(int64_t c_per) { return (int)((c_per + 511) / 512 * 512) + 8; }
+
 // Stage the factor slice [c_lo, c_hi) into LDS as sQ[j][c - c_lo] (stride
-// SQ), zero outside j < R and c < c_hi. B rows copy straight across; A
-// arrives as 8 (c) x 8 (j) blocks transposed in registers.
+// SQ), zero outside j < R and c < c_hi. B rows are copied global -> LDS by
+// buffer loads with an LDS destination, all issued at once (one load moves
+// 512 columns of one row; a row's loads end on its stride's run boundary,
+// and chunks past the slice or the rank read zeros). A arrives as 8 (c) x 8
+// (j) blocks transposed in registers.
 template <bool QROW, int RP>
 LRQ_DEV void stage_factor(const NtArgs& a, int64_t c_lo, int64_t c_hi, uint16_t* sQ, int SQ, int nthreads) {
   const int tid = threadIdx.x;
   const int64_t cols = c_hi - c_lo;
   if (QROW && (a.ldq & 7) == 0) {
-    const int cpr = (int)(a.c_per / 8);  // 16-byte chunks per row
-    for (int id = tid; id < RP * cpr; id += nthreads) {
-      const int j = id / cpr, cc = (id % cpr) * 8;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (j < a.R && cc < cols) v = ld16(a.q + (int64_t)j * a.ldq + c_lo + cc);
-      *reinterpret_cast<u32x4*>(sQ + j * SQ + cc) = v;
+    const int lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6), nw = nthreads / 64;
+    const rsrc_t rq = make_rsrc(a.q, clamp_bytes((int64_t)a.R * a.ldq * 2));
+    const int runs = (int)((a.c_per + 511) / 512);
+    for (int t = wv; t < RP * runs; t += nw) {
+      const int j = t / runs, c0 = (t % runs) * 512;
+      const int cc = c0 + lane * 8;
+      const uint32_t off = (j < a.R && cc < cols) ? (uint32_t)(((int64_t)j * a.ldq + c_lo + cc) * 2) : LRQ_OOB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lds_void*)(sQ + j * SQ + c0), 16, opaque_u32(off), 0, 0, 0);
     }
   } else if (!QROW && (a.ldq & 7) == 0) {
     const int jb = RP / 8;
@@ -117,7 +126,7 @@ __global__ void __launch_bounds__(LNT) k_lora_nt(NtArgs a) {
   const int64_t c_hi = min(a.C, c_lo + a.c_per);
   const int64_t C = a.C;
   const int l16 = lane & 15, g = lane >> 4;
-  const int SQ = (int)a.c_per + 8;
+  const int SQ = nt_stride(a.c_per);
 
   const int64_t m0 = (int64_t)blockIdx.x * 128 + wv * 16;  // this wavefront's tokens
   const int64_t rows = max((int64_t)0, min((int64_t)16, a.M - m0));
@@ -381,13 +390,14 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 }  // namespace
 
 // nt: 128-token tiles x column slices (multiples of 32) so that the grid is
-// ~256 workgroups (one per CU, 8 wavefronts each), within the LDS factor slice.
+// ~256 workgroups (one per CU, 8 wavefronts each), within the LDS factor
+// slice (rp rows of nt_stride(per) bf16: a cap of whole 512-column runs).
 LoraPlan lora_plan_nt(int64_t M, int64_t C, int rp) {
   LoraPlan p{};
   const int64_t tiles = cdiv(M > 0 ? M : 1, 128);
   const int64_t want = cdiv(256, tiles);
   int64_t per = 32 * cdiv(cdiv(C, want), 32);
-  const int64_t cap = ((NQ_BYTES / 2) / rp - 8) / 32 * 32;
+  const int64_t cap = ((NQ_BYTES / 2) / rp - 8) / 512 * 512;
   if (per > cap) per = cap;
   if (per < 32) per = 32;
   p.per = per;
