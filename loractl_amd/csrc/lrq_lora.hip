@@ -26,6 +26,8 @@
 //
 // Nothing depends on timing: every sum has a fixed order, and no workgroup
 // waits for another.
+#include <algorithm>
+
 #include "lrq_common.h"
 #include "lrq_kernels.h"
 
@@ -406,12 +408,13 @@ LoraPlan lora_plan_nt(int64_t M, int64_t C, int rp) {
   return p;
 }
 
-// tn: token slices (multiples of 128) so that column tiles x slices ~ 512
-// workgroups (two resident per CU), within the LDS factor slice.
+// tn: token slices (multiples of 128) so that column tiles x slices fill at
+// most the 512 workgroup slots (two resident per CU): a partial second round
+// would cost a whole slice's time. Within the LDS factor slice.
 LoraPlan lora_plan_tn(int64_t M, int64_t C, int rp) {
   LoraPlan p{};
   const int64_t tiles = cdiv(C, 128);
-  const int64_t want = cdiv(512, tiles);
+  const int64_t want = std::max<int64_t>(1, 512 / tiles);
   int64_t per = 128 * cdiv(cdiv(M > 0 ? M : 1, want), 128);
   const int64_t cap = ((TQ_BYTES / 2) / rp - 8) / 128 * 128;
   if (per > cap) per = cap;
