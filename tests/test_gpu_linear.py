@@ -170,7 +170,10 @@ def test_shape_errors_are_loud(cuda):
 @pytest.mark.parametrize("M,K,N,r,fmt", [(4096, 3072, 12288, 32, "int4"), (1024, 3072, 3072, 16, "int4"),
                                          (4096, 3072, 12288, 32, "fp8"), (16, 3072, 12288, 32, "int4"),
                                          # ragged edges on the large-tile paths (tokens, d_in, d_out)
-                                         (4000, 3008, 12280, 16, "int4"), (4000, 3008, 12280, 16, "fp8")])
+                                         (4000, 3008, 12280, 16, "int4"), (4000, 3008, 12280, 16, "fp8"),
+                                         # the MLP-down shape: 192-row forward tiles, 256-row input-gradient
+                                         # tiles (the shapes above take the other pairing), exact and ragged
+                                         (4096, 12288, 3072, 32, "int4"), (4000, 12224, 3064, 16, "fp8")])
 def test_baseline_shapes_against_torch_fp32(cuda, M, K, N, r, fmt):
     """Full BASELINE sizes: the fused kernels vs torch fp32 GEMMs over the
     same bf16 inputs and the (bit-exact) dequantized weight."""
