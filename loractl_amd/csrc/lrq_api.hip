@@ -36,7 +36,7 @@ namespace {
 
 const char* kNames[KID_COUNT] = {"quantize_int4", "quantize_fp8", "dequant", "fwd_main", "bwd_dx",
                                  "lora_t",        "lora_u",       "lora_da", "lora_db",  "lora_reduce",
-                                 "block",         "fwd_epi"};
+                                 "block",         "fwd_epi",      "lora_dadb"};
 
 int fail(lrq_ctx* c, int code, const char* fmt, ...) {
   if (c) {
@@ -479,24 +479,26 @@ static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const ui
     ga.rp = rp;
     if (dx) LRQ_TRY(run(c, KID_BWD_DX, "bwd_dx", [&] { return launch_bwd(c->stream, w->format, ga); }));
     // dA = x^T . u -> f32 [k, r] and dB = t^T . dy -> f32 [r, n]: token-slice
-    // partials, then one reduction launch for both
+    // partials in one launch (dB's longer workgroups dispatched first), then
+    // one reduction launch for both
+    TnSpec specs[2];
     TnJob jobs[2];
     int nj = 0;
-    if (da) {
-      const LoraPlan pa = lora_plan_tn(m, w->k, rp);
-      LRQ_TRY(run(c, KID_LORA_DA, "lora_da", [&] {
-        return launch_lora_tn(c->stream, x, ws.up, rp, m, w->k, (int)r, rp, pa, ws.pa);
-      }));
-      jobs[nj++] = TnJob{ws.pa, w->k, rp, (int)r, pa.splits, da, r, 1};
-    }
     if (db) {
       const LoraPlan pb = lora_plan_tn(m, w->n, rp);
-      LRQ_TRY(run(c, KID_LORA_DB, "lora_db", [&] {
-        return launch_lora_tn(c->stream, dy, t, r, m, w->n, (int)r, rp, pb, ws.pb);
-      }));
+      specs[nj] = TnSpec{dy, t, r, m, w->n, (int)r, pb, ws.pb};
       jobs[nj++] = TnJob{ws.pb, w->n, rp, (int)r, pb.splits, db, 1, w->n};
     }
-    if (nj) LRQ_TRY(run(c, KID_LORA_RED, "lora_reduce", [&] { return launch_tn_reduce(c->stream, jobs, nj); }));
+    if (da) {
+      const LoraPlan pa = lora_plan_tn(m, w->k, rp);
+      specs[nj] = TnSpec{x, ws.up, rp, m, w->k, (int)r, pa, ws.pa};
+      jobs[nj++] = TnJob{ws.pa, w->k, rp, (int)r, pa.splits, da, r, 1};
+    }
+    if (nj) {
+      const int kid = nj == 2 ? KID_LORA_DADB : (db ? KID_LORA_DB : KID_LORA_DA);
+      LRQ_TRY(run(c, kid, kNames[kid], [&] { return launch_lora_tn(c->stream, specs, nj, rp); }));
+      LRQ_TRY(run(c, KID_LORA_RED, "lora_reduce", [&] { return launch_tn_reduce(c->stream, jobs, nj); }));
+    }
     return LRQ_OK;
   }
   if (!dx) return LRQ_OK;

@@ -90,9 +90,18 @@ hipError_t launch_nt_reduce(hipStream_t st, const float* partial, int splits, in
                             bool b_rows = false, uint16_t* fr = nullptr, const float* bdiv = nullptr,
                             bool bdiv_rows = false);
 // partial[s][c][j] = sum over slice s of p[m, c] * q[m * ldq + j] (f32) for
-// c < C, j < rp (columns j >= R of q read as zero); plan.splits * C * rp floats.
-hipError_t launch_lora_tn(hipStream_t st, const uint16_t* p, const uint16_t* q, int64_t ldq, int64_t M,
-                          int64_t C, int R, int rp, const LoraPlan& plan, float* partial);
+// c < C, j < rp (columns j >= R of q read as zero); plan.splits * C * rp
+// floats. One or two such jobs per launch (the first job's workgroups are
+// dispatched first).
+struct TnSpec {
+  const uint16_t* p;
+  const uint16_t* q;
+  int64_t ldq, M, C;
+  int R;
+  LoraPlan plan;
+  float* partial;
+};
+hipError_t launch_lora_tn(hipStream_t st, const TnSpec* jobs, int njobs, int rp);
 // out[c * sc + j * sj] = sum_s partial[s][c][j] (slice order) for c < C, j < R.
 struct TnJob {
   const float* partial;
@@ -117,5 +126,6 @@ enum {
   KID_LORA_RED,
   KID_BLOCK,
   KID_FWD_EPI,
+  KID_LORA_DADB,
   KID_COUNT
 };

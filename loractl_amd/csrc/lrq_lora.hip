@@ -229,27 +229,32 @@ struct TnArgs {
   const uint16_t* q;   // [M, ldq] bf16, columns j < R
   int64_t M, C, ldq;
   int R;
-  int64_t m_per;       // tokens per slice (multiple of 256)
+  int64_t m_per;       // tokens per slice (multiple of 128)
   float* partial;      // [splits][C][rp]
+  int tiles, blocks;   // column tiles of 128, tiles x slices
 };
 
-// partial[split][c][j] = sum over the split's tokens of p[m, c] * q[m, j].
-// A workgroup (4 wavefronts) owns 128 columns and one token slice;
+// partial[split][c][j] = sum over the split's tokens of p[m, c] * q[m, j],
+// for one or two jobs in one launch (the first j0.blocks workgroups run job
+// 0). A workgroup (4 wavefronts) owns 128 columns and one token slice;
 // wavefront w takes tokens [128 it + 32 w, +32) of every 128-token chunk.
 constexpr int TW = 4;            // wavefronts per tn workgroup
 constexpr int TNT = 64 * TW;
 constexpr int TQ_BYTES = 64 * 1024;  // factor slice in LDS (later reused for the combine)
 
 template <int NJT>
-__global__ void __launch_bounds__(TNT) k_lora_tn(TnArgs a) {
+__global__ void __launch_bounds__(TNT) k_lora_tn(TnArgs j0, TnArgs j1) {
   constexpr int RP = 16 * NJT;
   static_assert(TW * 128 * 16 * 4 <= TQ_BYTES, "combine buffer fits the factor slice");
   __shared__ __attribute__((aligned(16))) uint16_t sQ[TQ_BYTES / 2];
   float* const red = reinterpret_cast<float*>(sQ);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int64_t c0 = (int64_t)blockIdx.x * 128;
-  const int split = blockIdx.y;
+  const bool second = (int)blockIdx.x >= j0.blocks;
+  const TnArgs a = second ? j1 : j0;
+  const int bid = (int)blockIdx.x - (second ? j0.blocks : 0);
+  const int64_t c0 = (int64_t)(bid % a.tiles) * 128;
+  const int split = bid / a.tiles;
   const int64_t m_lo = split * a.m_per;
   const int64_t m_hi = min(a.M, m_lo + a.m_per);
   const int64_t C = a.C;
@@ -454,16 +459,22 @@ hipError_t launch_nt_reduce(hipStream_t st, const float* partial, int splits, in
   return hipGetLastError();
 }
 
-hipError_t launch_lora_tn(hipStream_t st, const uint16_t* p, const uint16_t* q, int64_t ldq, int64_t M,
-                          int64_t C, int R, int rp, const LoraPlan& plan, float* partial) {
-  if (C == 0) return hipSuccess;
-  TnArgs a{p, q, M, C, ldq, R, plan.per, partial};
-  const dim3 grid((unsigned)plan.tiles, (unsigned)plan.splits);
+hipError_t launch_lora_tn(hipStream_t st, const TnSpec* jobs, int njobs, int rp) {
+  TnArgs t[2] = {};
+  int64_t total = 0;
+  for (int i = 0; i < njobs && i < 2; ++i) {
+    const TnSpec& j = jobs[i];
+    const int64_t blocks = j.C > 0 ? j.plan.tiles * j.plan.splits : 0;
+    t[i] = TnArgs{j.p, j.q, j.M, j.C, j.ldq, j.R, j.plan.per, j.partial, (int)j.plan.tiles, (int)blocks};
+    total += blocks;
+  }
+  if (total == 0) return hipSuccess;
+  const dim3 grid((unsigned)total);
   switch (rp / 16) {
-    case 1: hipLaunchKernelGGL(k_lora_tn<1>, grid, dim3(TNT), 0, st, a); break;
-    case 2: hipLaunchKernelGGL(k_lora_tn<2>, grid, dim3(TNT), 0, st, a); break;
-    case 3: hipLaunchKernelGGL(k_lora_tn<3>, grid, dim3(TNT), 0, st, a); break;
-    case 4: hipLaunchKernelGGL(k_lora_tn<4>, grid, dim3(TNT), 0, st, a); break;
+    case 1: hipLaunchKernelGGL(k_lora_tn<1>, grid, dim3(TNT), 0, st, t[0], t[1]); break;
+    case 2: hipLaunchKernelGGL(k_lora_tn<2>, grid, dim3(TNT), 0, st, t[0], t[1]); break;
+    case 3: hipLaunchKernelGGL(k_lora_tn<3>, grid, dim3(TNT), 0, st, t[0], t[1]); break;
+    case 4: hipLaunchKernelGGL(k_lora_tn<4>, grid, dim3(TNT), 0, st, t[0], t[1]); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
