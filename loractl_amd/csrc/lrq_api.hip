@@ -138,12 +138,18 @@ int ensure_ws(lrq_ctx* c, size_t bytes) {
 // Workspace layout of the fused calls (sizes only when base == nullptr): t
 // and u padded to rp columns (the GEMM epilogue operands) and the f32
 // partials of the LoRA reductions (t or u; dA and dB side by side).
+// f32 partials of the fused GEMMs when they split the depth (few output
+// tiles): the larger of the forward's and the backward's
+int64_t gemm_part_floats(int64_t m, int64_t n, int64_t k) {
+  return std::max(gemm_split_floats(m, n, k), gemm_split_floats(m, k, n));
+}
+
 // LoRA workspace: t and u padded to rp columns, the weight-side factor rows
 // of the fused GEMM's LoRA step (B^T [n, rp] forward, A [k, rp] backward),
-// and the side kernels' f32 partials.
+// the side kernels' f32 partials and the fused GEMMs' split partials.
 struct LoraWs {
   uint16_t *tp, *up, *fr;
-  float *pn, *pa, *pb;
+  float *pn, *pa, *pb, *gp;
   size_t bytes;
 };
 
@@ -157,6 +163,7 @@ LoraWs lora_layout(char* base, int64_t m, int64_t n, int64_t k, int rp) {
   w.pn = s.take<float>(std::max(nt * m * rp, (int64_t)1));
   w.pa = s.take<float>((int64_t)lora_plan_tn(m, k, rp).splits * k * rp);
   w.pb = s.take<float>((int64_t)lora_plan_tn(m, n, rp).splits * n * rp);
+  w.gp = s.take<float>(std::max(gemm_part_floats(m, n, k), (int64_t)1));
   w.bytes = s.off;
   return w;
 }
@@ -273,6 +280,13 @@ int lrq_reserve(lrq_ctx* c, int64_t m, int64_t n, int64_t k, int64_t r) {
   if (m < 0 || n < 0 || k < 0 || r < 0 || r > 64) return fail(c, LRQ_EINVAL, "bad reserve shape");
   const int rp = (int)round_up(r > 0 ? r : 16, 16);
   size_t need = lora_layout(nullptr, m, n, k, rp).bytes;
+  // the fused GEMMs' split partials are not monotonic in the token count
+  // (fewer tiles, more depth ranges): their largest size over m' <= m, which
+  // peaks at a whole number of 256-token tiles
+  const int64_t gp_m = gemm_part_floats(m, n, k);
+  int64_t gp_max = gp_m;
+  for (int64_t mm = 256; mm < m; mm += 256) gp_max = std::max(gp_max, gemm_part_floats(mm, n, k));
+  need += (size_t)(gp_max - gp_m) * 4;
   if (m >= 1) {  // the few-token forward, at up to 16 tokens
     const size_t sk = skinny_ws_bytes(skinny_plan(n, k, rp, get_num_cus()), m < 16 ? m : 16, n, rp);
     if (sk > need) need = sk;
@@ -429,6 +443,13 @@ static int fwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t 
     ga.lw = ws.fr;
     ga.r = (int)r;
     ga.rp = rp;
+    ga.part = ws.gp;
+  } else {
+    const int64_t pf = gemm_split_floats(m, w->n, w->k);
+    if (pf > 0) {
+      LRQ_TRY(ensure_ws(c, (size_t)pf * 4));
+      ga.part = reinterpret_cast<float*>(c->ws);
+    }
   }
   return run(c, KID_FWD_MAIN, "fwd_main", [&] { return launch_fwd(c->stream, w->format, ga); });
 }
@@ -477,6 +498,7 @@ static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const ui
     ga.lw = ws.fr;
     ga.r = (int)r;
     ga.rp = rp;
+    ga.part = ws.gp;
     if (dx) LRQ_TRY(run(c, KID_BWD_DX, "bwd_dx", [&] { return launch_bwd(c->stream, w->format, ga); }));
     // dA = x^T . u -> f32 [k, r] and dB = t^T . dy -> f32 [r, n]: token-slice
     // partials in one launch (dB's longer workgroups dispatched first), then
@@ -502,6 +524,11 @@ static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const ui
     return LRQ_OK;
   }
   if (!dx) return LRQ_OK;
+  const int64_t pf = gemm_split_floats(m, w->k, w->n);
+  if (pf > 0) {
+    LRQ_TRY(ensure_ws(c, (size_t)pf * 4));
+    ga.part = reinterpret_cast<float*>(c->ws);
+  }
   return run(c, KID_BWD_DX, "bwd_dx", [&] { return launch_bwd(c->stream, w->format, ga); });
 }
 

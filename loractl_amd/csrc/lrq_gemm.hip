@@ -62,7 +62,14 @@
 //     every store writes whole 128-byte (RA = 256) or 64-byte row segments;
 //   - tile order: workgroup b's i-th tile is virtual tile b + i*G, mapped so
 //     each XCD (own L2) works on a contiguous range of tiles, grouped four
-//     token tiles deep.
+//     token tiles deep;
+//   - split depth: with fewer tiles than CUs (few tokens, or a narrow output)
+//     the depth range of every tile is cut into S ranges of whole steps; a
+//     work unit is (tile, range), the persistent grid walks units as it walks
+//     tiles, each unit writes its f32 accumulators to a partial buffer
+//     [S][m][e] (range 0 adds the LoRA term), and k_split_reduce sums the S
+//     partials in range order, applies the forward fp8 scales and bias and
+//     rounds once to bf16.
 
 #include "lrq_common.h"
 #include "lrq_kernels.h"
@@ -109,16 +116,18 @@ LRQ_DEV float row_bcast_n(float v, int n) {
   }
 }
 
-// Per-tile load sources: the activation rows of wavefront w's DMA share, the
-// weight block row(s) (data; forward int4 scales) and, backward int4, the
-// byte offsets of the two row tiles' group rows in the transposed scale table.
+// Per-unit load sources: the activation rows of wavefront w's DMA share, the
+// weight block row(s) (data; forward int4 scales), backward int4 the byte
+// offsets of the two row tiles' group rows in the transposed scale table,
+// and the unit's first step and depth range.
 struct TileSrc {
   int64_t m0, e0;
   rsrc_t act, wd, ws;
   uint32_t sk0, sk1;
+  int k0, sp;
 };
 
-template <bool BWD, int FMT, bool R192>
+template <bool BWD, int FMT, bool R192, bool SPLIT>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 k_gemm(GemmArgs a, int tiles_m, int ntiles) {
   constexpr bool I4 = FMT == LRQ_FMT_INT4;
@@ -136,8 +145,10 @@ k_gemm(GemmArgs a, int tiles_m, int ntiles) {
   __shared__ __attribute__((aligned(16))) float sAux[BWD ? 4 : 2 * 256];
 
   const int G = gridDim.x;
+  const int S = SPLIT ? a.splits : 1;
+  const int nunits = ntiles * S;
   int vb = blockIdx.x;
-  if (vb >= ntiles) return;
+  if (vb >= nunits) return;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5, l32 = lane & 31;
@@ -155,7 +166,9 @@ k_gemm(GemmArgs a, int tiles_m, int ntiles) {
   int64_t wbytes, nsc;
   blocked_sizes_dev(FMT, E, K, &wbytes, &nsc, a.gshift);
   const int nk = (int)KB;
-  const int nkp = (nk + NBUF - 1) / NBUF * NBUF;  // steps per tile, rounded up
+  // steps per unit: the whole depth rounded up to whole pipeline rounds, or
+  // one split range (a multiple of NBUF; the last range may run past nk)
+  const int nkp = SPLIT ? a.spl : (nk + NBUF - 1) / NBUF * NBUF;
 
   // backward scales: int4 ST [KGt][64*KB] (row n = depth, group kg of the
   // output row k); fp8 the channel scales [n] or one scalar
@@ -168,11 +181,15 @@ k_gemm(GemmArgs a, int tiles_m, int ntiles) {
   // fp8 with one scalar scale: the per-channel loads read zeros, plus this
   const float s0add = (BWD && !I4 && !pc) ? a.wscale[0] : 0.0f;
 
-  // sources of virtual tile v (zero-size resources when v is past the grid)
+  // sources of virtual unit v (zero-size resources when v is past the grid);
+  // the S ranges of a tile are consecutive units
   auto tile_src = [&](int v) -> TileSrc {
     TileSrc t;
-    const bool ok = v < ntiles;
-    const int logical = xcd_remap(ok ? v : 0, ntiles);
+    const bool ok = v < nunits;
+    const int lu = xcd_remap(ok ? v : 0, nunits);
+    const int logical = SPLIT ? lu / S : lu;
+    t.sp = SPLIT ? lu % S : 0;
+    t.k0 = t.sp * nkp;
     const int grp = logical / (GM * tiles_a), within = logical % (GM * tiles_a);
     const int gm = min(GM, tiles_m - grp * GM);
     const int tm = grp * GM + within % gm, ta = within / gm;
@@ -484,12 +501,57 @@ k_gemm(GemmArgs a, int tiles_m, int ntiles) {
     }
   };
 
+  // split-depth epilogue: range 0 adds the LoRA term; every range stores
+  // its f32 accumulators to part[range][m][e], four consecutive e per 16-byte
+  // store (rows past M fall outside the resource, columns past E are skipped)
+  auto epilogue_partial = [&](const TileSrc& u) {
+    const int lane = (int)opaque_u32((uint32_t)threadIdx.x & 63u);
+    const int g = lane >> 5, l32 = lane & 31;
+    if (rp > 0 && u.sp == 0) {
+      const uint16_t* sT = sE;
+      const uint16_t* sBt = sE + 256 * rp;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        if (kk * 16 < rp) {
+          bf16x8 la[2];
+          la[0] = as_bf16x8(ld16(sBt + (ro0 + l32) * rp + kk * 16 + g * 8));
+          la[1] = as_bf16x8(ld16(sBt + (ro1 + l32) * rp + kk * 16 + g * 8));
+#pragma unroll
+          for (int j = 0; j < MJ; ++j) {
+            const int tj = R192 ? ((j + 4 * H) & 7) : j;
+            const bf16x8 lb = as_bf16x8(ld16(sT + (32 * tj + l32) * rp + kk * 16 + g * 8));
+            acc[0][j] = mfma32(la[0], lb, acc[0][j]);
+            if (j < MJ1) acc[1][j] = mfma32(la[1], lb, acc[1][j]);
+          }
+        }
+      }
+    }
+    const rsrc_t rp_ = make_rsrc(a.part + ((int64_t)u.sp * M + u.m0) * E, clamp_bytes((M - u.m0) * E * 4));
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < (i == 0 ? MJ : MJ1); ++j) {
+        const int tj = R192 ? ((j + 4 * H) & 7) : j;
+        const uint32_t rowoff = (uint32_t)((32 * tj + l32) * E * 4);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int vg = 0; vg < 4; ++vg) {
+          const int64_t e = u.e0 + (i ? ro1 : ro0) + 8 * vg + 4 * g;
+          const f32x16& c = acc[i][j];
+          const u32x4 v = {__float_as_uint(c[4 * vg]), __float_as_uint(c[4 * vg + 1]), __float_as_uint(c[4 * vg + 2]),
+                           __float_as_uint(c[4 * vg + 3])};
+          const uint32_t off = e < E ? rowoff + (uint32_t)(e * 4) : LRQ_OOB;
+          __builtin_amdgcn_raw_buffer_store_b128(v, rp_, opaque_u32(off), 0, 0);
+        }
+      }
+  };
+
   // prologue: the first tile's first two steps in flight
   TileSrc cur = tile_src(vb);
 #pragma unroll
   for (int b = 0; b < NBUF; ++b) {
-    dma(bufs[b], cur.act, b);
-    load_w(b, cur, b);
+    dma(bufs[b], cur.act, cur.k0 + b);
+    load_w(b, cur, cur.k0 + b);
   }
   dma_aux(cur.m0, cur.e0);
   zero_acc();
@@ -503,15 +565,18 @@ k_gemm(GemmArgs a, int tiles_m, int ntiles) {
     int kt = 0;
     for (; kt + NBUF < nkp; kt += NBUF) {
 #pragma unroll
-      for (int b = 0; b < NBUF; ++b) step(b, cur, kt + NBUF + b);
+      for (int b = 0; b < NBUF; ++b) step(b, cur, cur.k0 + kt + NBUF + b);
     }
-    // last two steps: prefetch the next tile's first steps
+    // last two steps: prefetch the next unit's first steps
     const TileSrc nxt = tile_src(vb + G);
 #pragma unroll
-    for (int b = 0; b < NBUF; ++b) step(b, nxt, b);
-    epilogue(cur.m0, cur.e0);
+    for (int b = 0; b < NBUF; ++b) step(b, nxt, nxt.k0 + b);
+    if (SPLIT)
+      epilogue_partial(cur);
+    else
+      epilogue(cur.m0, cur.e0);
     vb += G;
-    if (vb >= ntiles) break;
+    if (vb >= nunits) break;
     zero_acc();
     cur = nxt;
     // every wavefront's output reads of sE are done before the next tile's
@@ -523,14 +588,15 @@ k_gemm(GemmArgs a, int tiles_m, int ntiles) {
   __builtin_amdgcn_s_waitcnt(0);
 }
 
-template <bool BWD, int FMT, bool R192>
+template <bool BWD, int FMT, bool R192, bool SPLIT>
 hipError_t run(hipStream_t st, const GemmArgs& a) {
   constexpr int RA = R192 ? 192 : 256;
   const int tiles_m = (int)((a.m + RB - 1) / RB);
   const int tiles_e = (int)((a.e + RA - 1) / RA);
   const int ntiles = tiles_m * tiles_e;
-  const int grid = ntiles < get_num_cus() ? ntiles : get_num_cus();
-  hipLaunchKernelGGL((k_gemm<BWD, FMT, R192>), dim3(grid), dim3(256), 0, st, a, tiles_m, ntiles);
+  const int nunits = ntiles * (SPLIT ? a.splits : 1);
+  const int grid = nunits < get_num_cus() ? nunits : get_num_cus();
+  hipLaunchKernelGGL((k_gemm<BWD, FMT, R192, SPLIT>), dim3(grid), dim3(256), 0, st, a, tiles_m, ntiles);
   return hipGetLastError();
 }
 
@@ -544,12 +610,81 @@ bool use_r192(int64_t m, int64_t e) {
   return 0.8 * (double)r192 < (double)r256 - 1e-9;
 }
 
+// out[m, e] = bf16(sc(e) * sum over ranges (in order) of part[s][m][e] +
+// bias(e)); sc = the forward fp8 channel scale or scalar, else 1. Four
+// consecutive e per thread (e % 4 == 0).
+__global__ void __launch_bounds__(256) k_split_reduce(const float* __restrict__ part, int S, int64_t M, int64_t E,
+                                                      const float* __restrict__ scale, int per_channel,
+                                                      const float* __restrict__ bias, uint16_t* __restrict__ out) {
+  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (q >= M * E / 4) return;
+  const int64_t e = (q * 4) % E;
+  f32x4 sum = {0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < S; ++s) {
+    const f32x4 v = reinterpret_cast<const f32x4*>(part + (int64_t)s * M * E)[q];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sum[i] += v[i];
+  }
+  f32x4 sc = {1.f, 1.f, 1.f, 1.f}, bv = {0.f, 0.f, 0.f, 0.f};
+  if (scale) sc = per_channel ? *reinterpret_cast<const f32x4*>(scale + e) : (f32x4){scale[0], scale[0], scale[0], scale[0]};
+  if (bias) bv = *reinterpret_cast<const f32x4*>(bias + e);
+  u32x2 o;
+  o[0] = pack_bf16x2(__builtin_fmaf(sum[0], sc[0], bv[0]), __builtin_fmaf(sum[1], sc[1], bv[1]));
+  o[1] = pack_bf16x2(__builtin_fmaf(sum[2], sc[2], bv[2]), __builtin_fmaf(sum[3], sc[3], bv[3]));
+  reinterpret_cast<u32x2*>(out)[q] = o;
+}
+
+// Depth ranges: with fewer output tiles than CUs, as many ranges as fill the
+// CUs once, of at least four steps each (at most 16 ranges).
+struct SplitPlan {
+  bool r192;
+  int S, spl;
+};
+SplitPlan plan_split(int64_t m, int64_t e, int64_t depth) {
+  SplitPlan p{};
+  p.r192 = use_r192(m, e);
+  const int64_t RA = p.r192 ? 192 : 256;
+  const int64_t tiles = (m + RB - 1) / RB * ((e + RA - 1) / RA), cus = get_num_cus();
+  const int64_t nk = (depth + 63) / 64;
+  int64_t S = 1;
+  if (tiles > 0 && tiles < cus) {
+    S = cus / tiles;
+    if (S > nk / 4) S = nk / 4;
+    if (S > 16) S = 16;
+    if (S < 1) S = 1;
+  }
+  int64_t spl = (nk + S - 1) / S;
+  spl = (spl + NBUF - 1) / NBUF * NBUF;
+  p.spl = (int)spl;
+  p.S = (int)((nk + spl - 1) / spl);  // every range holds at least one step
+  return p;
+}
+
+
+template <bool BWD, bool SPLIT>
+hipError_t run_fmt(hipStream_t st, int fmt, bool r192, const GemmArgs& a) {
+  if (fmt == LRQ_FMT_INT4)
+    return r192 ? run<BWD, LRQ_FMT_INT4, true, SPLIT>(st, a) : run<BWD, LRQ_FMT_INT4, false, SPLIT>(st, a);
+  return r192 ? run<BWD, LRQ_FMT_FP8, true, SPLIT>(st, a) : run<BWD, LRQ_FMT_FP8, false, SPLIT>(st, a);
+}
+
 template <bool BWD>
 hipError_t dispatch(hipStream_t st, int fmt, const GemmArgs& a) {
   if (a.m == 0 || a.e == 0) return hipSuccess;
-  const bool r192 = use_r192(a.m, a.e);
-  if (fmt == LRQ_FMT_INT4) return r192 ? run<BWD, LRQ_FMT_INT4, true>(st, a) : run<BWD, LRQ_FMT_INT4, false>(st, a);
-  return r192 ? run<BWD, LRQ_FMT_FP8, true>(st, a) : run<BWD, LRQ_FMT_FP8, false>(st, a);
+  const SplitPlan p = plan_split(a.m, a.e, a.l);
+  if (p.S <= 1) return run_fmt<BWD, false>(st, fmt, p.r192, a);
+  if (!a.part) return hipErrorInvalidValue;
+  GemmArgs b = a;
+  b.splits = p.S;
+  b.spl = p.spl;
+  hipError_t err = run_fmt<BWD, true>(st, fmt, p.r192, b);
+  if (err != hipSuccess) return err;
+  // forward fp8: channel scales (or the scalar) and the bias in the reduction
+  const bool f8 = !BWD && fmt == LRQ_FMT_FP8;
+  const int64_t quads = a.m * a.e / 4;
+  hipLaunchKernelGGL(k_split_reduce, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, st, a.part, p.S, a.m, a.e,
+                     f8 ? a.wscale : nullptr, a.per_channel, BWD ? nullptr : a.bias, a.out);
+  return hipGetLastError();
 }
 
 }  // namespace
@@ -559,4 +694,9 @@ void set_num_cus(int n) { g_num_cus_ = n > 0 ? n : 256; }
 int get_num_cus() { return g_num_cus_; }
 
 hipError_t launch_fwd(hipStream_t st, int fmt, const GemmArgs& a) { return dispatch<false>(st, fmt, a); }
+int64_t gemm_split_floats(int64_t m, int64_t e, int64_t depth) {
+  if (m <= 0 || e <= 0) return 0;
+  const SplitPlan p = plan_split(m, e, depth);
+  return p.S > 1 ? (int64_t)p.S * m * e : 0;
+}
 hipError_t launch_bwd(hipStream_t st, int fmt, const GemmArgs& a) { return dispatch<true>(st, fmt, a); }

@@ -38,14 +38,20 @@ struct GemmArgs {
   const uint16_t* lw;    // the weight-side LoRA factor (user layout)
   int r, rp;             // rank and rank padded to 16 (rp == 0: no LoRA)
   uint16_t* out;         // [m, e]
+  float* part;           // lrq_gemm.hip split-depth partials [S][m][e] (gemm_split_floats), or null
+  int splits, spl;       // set by lrq_gemm.hip: depth ranges and steps per range
 };
 
 // lrq_gemm.hip: the forward for m > 16 and the input gradient, weight
 // dequantized into registers. a.lw is the weight-side LoRA rows [e, rp]
 // (B^T forward, A backward; zero-padded columns), a.lact is t or u [m, rp].
 // The backward's a.wdata / a.wscale point at the transposed section.
+// With fewer output tiles than CUs the depth is split into S ranges whose
+// f32 partials a.part must hold: gemm_split_floats(m, e, depth) floats (0
+// when the shape is not split).
 hipError_t launch_fwd(hipStream_t st, int fmt, const GemmArgs& a);
 hipError_t launch_bwd(hipStream_t st, int fmt, const GemmArgs& a);
+int64_t gemm_split_floats(int64_t m, int64_t e, int64_t depth);
 int get_num_cus();
 
 // lrq_skinny.hip: the forward for m <= 16 in two launches. `part` streams the
