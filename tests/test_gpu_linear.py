@@ -129,6 +129,31 @@ def test_bias_epilogue(cuda):
     check("y+bias", y, y_ref)
 
 
+@pytest.mark.parametrize("fmt,per_channel", [("int4", True), ("fp8", True), ("fp8", False)])
+def test_split_depth_bias_and_scales(cuda, fmt, per_channel):
+    """Few output tiles (M = 200, d_out = 3072): the depth is split into
+    ranges whose f32 partials a reduction sums; the bias and the forward fp8
+    channel scales (or the scalar) are applied there, once."""
+    M, K, N, r = 200, 3072, 3072, 16
+    g = torch.Generator(device=cuda).manual_seed(7)
+    w = torch.randn(N, K, device=cuda, generator=g) * 0.02
+    wq = D.quantize_int4(w, 64) if fmt == "int4" else D.quantize_fp8(w, per_channel)
+    bias = torch.randn(N, device=cuda, generator=g) * 0.1
+    wq = wq.with_bias(bias)
+    wdq = D.dequant(wq)
+    x = torch.randn(M, K, device=cuda, generator=g).to(torch.bfloat16)
+    a = ((torch.rand(K, r, device=cuda, generator=g) * 2 - 1) / K ** 0.5).to(torch.bfloat16)
+    b = (torch.randn(r, N, device=cuda, generator=g) * 1e-2).to(torch.bfloat16)
+    dy = torch.randn(M, N, device=cuda, generator=g).to(torch.bfloat16)
+    y, t = D.lora_fwd(x, wq, a, b, 0.5)
+    dx, _, _ = D.lora_bwd(x, dy, wq, a, b, 0.5, t)
+    xf, af, bf, dyf = x.float(), a.float(), b.float(), dy.float()
+    y_ref = xf @ wdq.t() + 0.5 * (xf @ af) @ bf + bias
+    dx_ref = dyf @ wdq + 0.5 * (dyf @ bf.t()) @ af.t()
+    check("y", y, y_ref.cpu().numpy())
+    check("dx", dx, dx_ref.cpu().numpy())
+
+
 def test_zero_b_delta_is_bitwise_no_op(cuda):
     """lora.rs:262-276 on the fused kernel: B = 0 gives exactly the base output."""
     M, K, N, r = 64, 256, 128, 16
@@ -173,7 +198,9 @@ def test_shape_errors_are_loud(cuda):
                                          (4000, 3008, 12280, 16, "int4"), (4000, 3008, 12280, 16, "fp8"),
                                          # the MLP-down shape: 192-row forward tiles, 256-row input-gradient
                                          # tiles (the shapes above take the other pairing), exact and ragged
-                                         (4096, 12288, 3072, 32, "int4"), (4000, 12224, 3064, 16, "fp8")])
+                                         (4096, 12288, 3072, 32, "int4"), (4000, 12224, 3064, 16, "fp8"),
+                                         # split depth (fewer output tiles than CUs): both passes
+                                         (256, 3072, 12288, 32, "fp8"), (300, 3008, 12280, 16, "int4")])
 def test_baseline_shapes_against_torch_fp32(cuda, M, K, N, r, fmt):
     """Full BASELINE sizes: the fused kernels vs torch fp32 GEMMs over the
     same bf16 inputs and the (bit-exact) dequantized weight."""
