@@ -64,6 +64,8 @@ constexpr int NQ_BYTES = 100 * 1024;  // factor slice in LDS
 // LDS row stride of the factor slice: whole 512-column runs plus 8 bf16 of
 // padding (16 consecutive rows at one column then cover all banks)
 LRQ_DEV int nt_stride(int64_t c_per) { return (int)((c_per + 511) / 512 * 512) + 8; }
+// columns of the factor slice that fit in LDS at once (whole runs)
+constexpr int nt_cap(int rp) { return ((NQ_BYTES / 2) / rp - 8) / 512 * 512; }
 
 // Stage the factor slice [c_lo, c_hi) into LDS as sQ[j][c - c_lo] (stride
 // SQ), zero outside j < R and c < c_hi. B rows are copied global -> LDS by
@@ -72,13 +74,14 @@ LRQ_DEV int nt_stride(int64_t c_per) { return (int)((c_per + 511) / 512 * 512) +
 // and chunks past the slice or the rank read zeros). A arrives as 8 (c) x 8
 // (j) blocks transposed in registers.
 template <bool QROW, int RP>
-LRQ_DEV void stage_factor(const NtArgs& a, int64_t c_lo, int64_t c_hi, uint16_t* sQ, int SQ, int nthreads) {
+LRQ_DEV void stage_factor(const NtArgs& a, int64_t c_lo, int64_t c_hi, int width, uint16_t* sQ, int SQ,
+                          int nthreads) {
   const int tid = threadIdx.x;
   const int64_t cols = c_hi - c_lo;
   if (QROW && (a.ldq & 7) == 0) {
     const int lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6), nw = nthreads / 64;
     const rsrc_t rq = make_rsrc(a.q, clamp_bytes((int64_t)a.R * a.ldq * 2));
-    const int runs = (int)((a.c_per + 511) / 512);
+    const int runs = (width + 511) / 512;
     for (int t = wv; t < RP * runs; t += nw) {
       const int j = t / runs, c0 = (t % runs) * 512;
       const int cc = c0 + lane * 8;
@@ -87,7 +90,7 @@ LRQ_DEV void stage_factor(const NtArgs& a, int64_t c_lo, int64_t c_hi, uint16_t*
     }
   } else if (!QROW && (a.ldq & 7) == 0) {
     const int jb = RP / 8;
-    for (int blk = tid; blk < jb * (int)(a.c_per / 8); blk += nthreads) {
+    for (int blk = tid; blk < jb * (width / 8); blk += nthreads) {
       const int j0 = (blk % jb) * 8, cc = (blk / jb) * 8;
       u32x4 v[8];
 #pragma unroll
@@ -103,9 +106,9 @@ LRQ_DEV void stage_factor(const NtArgs& a, int64_t c_lo, int64_t c_hi, uint16_t*
       }
     }
   } else {
-    for (int64_t id = tid; id < (int64_t)RP * a.c_per; id += nthreads) {
-      const int j = (int)(id / a.c_per);
-      const int64_t cc = id % a.c_per;
+    for (int64_t id = tid; id < (int64_t)RP * width; id += nthreads) {
+      const int j = (int)(id / width);
+      const int64_t cc = id % width;
       uint16_t v = 0;
       if (j < a.R && cc < cols) v = QROW ? a.q[(int64_t)j * a.ldq + c_lo + cc] : a.q[(c_lo + cc) * a.ldq + j];
       sQ[j * SQ + cc] = v;
@@ -128,7 +131,9 @@ __global__ void __launch_bounds__(LNT) k_lora_nt(NtArgs a) {
   const int64_t c_hi = min(a.C, c_lo + a.c_per);
   const int64_t C = a.C;
   const int l16 = lane & 15, g = lane >> 4;
-  const int SQ = nt_stride(a.c_per);
+  // the slice is staged in sub-slices of at most nt_cap(RP) columns
+  const int sub = (int)min(a.c_per, (int64_t)nt_cap(RP));
+  const int SQ = nt_stride(sub);
 
   const int64_t m0 = (int64_t)blockIdx.x * 128 + wv * 16;  // this wavefront's tokens
   const int64_t rows = max((int64_t)0, min((int64_t)16, a.M - m0));
@@ -140,32 +145,37 @@ __global__ void __launch_bounds__(LNT) k_lora_nt(NtArgs a) {
   for (int jt = 0; jt < NJT; ++jt) acc[jt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
 
   // chunks of 32 columns; lane group g reads 8 of them; chunks past the
-  // slice load zeros (out-of-range offsets) and add nothing
-  const int64_t nchunks = (c_hi - c_lo + 31) / 32;
+  // sub-slice load zeros (out-of-range offsets) and add nothing
   constexpr int D = 8;
   u32x4 pv[D];
-  auto load = [&](int k, int64_t it) {
-    const int64_t c = c_lo + it * 32 + g * 8;
-    pv[k] = bload16(rpv, opaque_u32(c < c_hi ? roff + (uint32_t)(c * 2) : LRQ_OOB));
+  auto load = [&](int k, int64_t s_lo, int64_t s_hi, int64_t it) {
+    const int64_t c = s_lo + it * 32 + g * 8;
+    pv[k] = bload16(rpv, opaque_u32(c < s_hi ? roff + (uint32_t)(c * 2) : LRQ_OOB));
   };
   auto compute = [&](int k, int64_t it) {
-    const int cc = (int)(it * 32) + g * 8;  // slice-relative; < c_per + 32
+    const int cc = (int)(it * 32) + g * 8;  // sub-slice-relative; < sub + 32
 #pragma unroll
     for (int jt = 0; jt < NJT; ++jt) {
-      const int off = min(cc, (int)a.c_per - 8);  // chunks past the slice: zero p, any finite q
+      const int off = min(cc, sub - 8);  // chunks past the sub-slice: zero p, any finite q
       acc[jt] = mfma16(as_bf16x8(pv[k]), as_bf16x8(ld16(sQ + (jt * 16 + l16) * SQ + off)), acc[jt]);
     }
   };
-  // the first loads overlap the factor staging
+  for (int64_t s_lo = c_lo; s_lo < c_hi; s_lo += sub) {
+    const int64_t s_hi = min(c_hi, s_lo + sub);
+    const int64_t nchunks = (s_hi - s_lo + 31) / 32;
+    // every wavefront's reads of the previous sub-slice are done
+    if (s_lo != c_lo) __syncthreads();
+    // the first loads overlap the factor staging
 #pragma unroll
-  for (int k = 0; k < D; ++k) load(k, k);
-  stage_factor<QROW, RP>(a, c_lo, c_hi, sQ, SQ, LNT);
-  __syncthreads();
-  for (int64_t it = 0; it < nchunks; it += D) {
+    for (int k = 0; k < D; ++k) load(k, s_lo, s_hi, k);
+    stage_factor<QROW, RP>(a, s_lo, s_hi, sub, sQ, SQ, LNT);
+    __syncthreads();
+    for (int64_t it = 0; it < nchunks; it += D) {
 #pragma unroll
-    for (int k = 0; k < D; ++k) {
-      compute(k, it + k);
-      load(k, it + k + D);
+      for (int k = 0; k < D; ++k) {
+        compute(k, it + k);
+        load(k, s_lo, s_hi, it + k + D);
+      }
     }
   }
 
@@ -397,15 +407,13 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 }  // namespace
 
 // nt: 128-token tiles x column slices (multiples of 32) so that the grid is
-// ~256 workgroups (one per CU, 8 wavefronts each), within the LDS factor
-// slice (rp rows of nt_stride(per) bf16: a cap of whole 512-column runs).
+// ~256 workgroups (one per CU, 8 wavefronts each); a slice wider than the
+// LDS factor slice holds (nt_cap) is staged and streamed in sub-slices.
 LoraPlan lora_plan_nt(int64_t M, int64_t C, int rp) {
   LoraPlan p{};
   const int64_t tiles = cdiv(M > 0 ? M : 1, 128);
   const int64_t want = cdiv(256, tiles);
   int64_t per = 32 * cdiv(cdiv(C, want), 32);
-  const int64_t cap = ((NQ_BYTES / 2) / rp - 8) / 512 * 512;
-  if (per > cap) per = cap;
   if (per < 32) per = 32;
   p.per = per;
   p.splits = (int)cdiv(C, per);
