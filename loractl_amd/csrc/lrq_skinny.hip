@@ -241,14 +241,16 @@ __global__ void __launch_bounds__(SK_NT) k_sk_epi(SkArgs sa, float scaling, uint
   const rsrc_t rtp = make_rsrc(sa.tpart, clamp_bytes((int64_t)TS * 16 * rp * 4));
   for (int i = tid; i < 16 * rp; i += SK_NT) {
     const int m = i / rp, j = i % rp;
-    float part[16];
-#pragma unroll
-    for (int q = 0; q < 16; ++q)
-      part[q] = bloadf(rtp, opaque_u32(q < TS ? (uint32_t)(((q * 16 + m) * rp + j) * 4) : LRQ_OOB));
+    // slices in order, 16 loads issued together per batch
     float v = 0.0f;
+    for (int q0 = 0; q0 < TS; q0 += 16) {
+      float part[16];
 #pragma unroll
-    for (int q = 0; q < 16; ++q) v += part[q];
-    for (int q = 16; q < TS; ++q) v += sa.tpart[((int64_t)q * 16 + m) * rp + j];
+      for (int q = 0; q < 16; ++q)
+        part[q] = bloadf(rtp, opaque_u32(q0 + q < TS ? (uint32_t)((((q0 + q) * 16 + m) * rp + j) * 4) : LRQ_OOB));
+#pragma unroll
+      for (int q = 0; q < 16; ++q) v += part[q];
+    }
     const uint32_t hb = pack_bf16x2(scaling * v, 0.0f) & 0xffffu;  // t as the caller sees it
     tt[m][j] = __uint_as_float(hb << 16);
     if (blockIdx.x == 0 && t_out && m < M && j < r) t_out[(int64_t)m * r + j] = (uint16_t)hb;
@@ -287,10 +289,17 @@ __global__ void __launch_bounds__(SK_NT) k_sk_epi(SkArgs sa, float scaling, uint
       base0 += __uint_as_float(pv[i][s][0]);
       base1 += __uint_as_float(pv[i][s][1]);
     }
-    for (int s = 8; s < S; ++s) {
-      const float2 p = *reinterpret_cast<const float2*>(sa.part + ((int64_t)s * M + m) * E + n);
-      base0 += p.x;
-      base1 += p.y;
+    // splits past the first eight, in order, eight loads issued together
+    for (int s0 = 8; s0 < S; s0 += 8) {
+      u32x2 pw[8];
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+        pw[s] = bload8(rpt, opaque_u32(s0 + s < S ? (uint32_t)((((int64_t)(s0 + s) * M + m) * E + n) * 4) : LRQ_OOB));
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        base0 += __uint_as_float(pw[s][0]);
+        base1 += __uint_as_float(pw[s][1]);
+      }
     }
     float l0 = 0.0f, l1 = 0.0f;
 #pragma unroll

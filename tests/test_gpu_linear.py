@@ -200,7 +200,10 @@ def test_shape_errors_are_loud(cuda):
                                          # tiles (the shapes above take the other pairing), exact and ragged
                                          (4096, 12288, 3072, 32, "int4"), (4000, 12224, 3064, 16, "fp8"),
                                          # split depth (fewer output tiles than CUs): both passes
-                                         (256, 3072, 12288, 32, "fp8"), (300, 3008, 12280, 16, "int4")])
+                                         (256, 3072, 12288, 32, "fp8"), (300, 3008, 12280, 16, "int4"),
+                                         # few tokens with a deep d_in (Qwen MLP down): more than 16 t
+                                         # slices and 8 reduction splits in the few-token epilogue
+                                         (16, 9728, 2560, 16, "int4"), (5, 9728, 2560, 16, "fp8")])
 def test_baseline_shapes_against_torch_fp32(cuda, M, K, N, r, fmt):
     """Full BASELINE sizes: the fused kernels vs torch fp32 GEMMs over the
     same bf16 inputs and the (bit-exact) dequantized weight."""
