@@ -290,6 +290,11 @@ int lrq_reserve(lrq_ctx* c, int64_t m, int64_t n, int64_t k, int64_t r) {
   if (m >= 1) {  // the few-token forward, at up to 16 tokens
     const size_t sk = skinny_ws_bytes(skinny_plan(n, k, rp, get_num_cus()), m < 16 ? m : 16, n, rp);
     if (sk > need) need = sk;
+    // the few-token input gradient: its partials follow the LoRA workspace
+    const int64_t mm = m < 16 ? m : 16;
+    const size_t skd = lora_layout(nullptr, mm, n, k, rp).bytes +
+                       skinny_ws_bytes(skinny_plan(k, n, 0, get_num_cus()), mm, k, 0);
+    if (skd > need) need = skd;
   }
   const size_t fp8_need = (size_t)round_up(n * 4, 256);
   if (fp8_need > need) need = fp8_need;
@@ -419,9 +424,9 @@ static int fwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t 
       ga.rp = rp;
     }
     LRQ_TRY(run(c, KID_FWD_MAIN, "fwd_main",
-                [&] { return launch_skinny_part(c->stream, w->format, ga, lora ? a : nullptr, p, part, tpart); }));
+                [&] { return launch_skinny_part(c->stream, w->format, false, ga, lora ? a : nullptr, p, part, tpart); }));
     return run(c, KID_FWD_EPI, "fwd_epi", [&] {
-      return launch_skinny_epi(c->stream, w->format, ga, p, part, tpart, scaling, lora ? t_out : nullptr);
+      return launch_skinny_epi(c->stream, w->format, false, ga, p, part, tpart, scaling, lora ? t_out : nullptr);
     });
   }
   if (lora) {
@@ -467,6 +472,24 @@ int lrq_lora_fwd(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t m, 
   return fwd_impl(c, w, x, m, a, b, r, scaling, y, t_out);
 }
 
+// The input gradient: the few-token path for m <= 16 (partials at `skpart`),
+// else the fused GEMM.
+static hipError_t launch_dx(lrq_ctx* c, const lrq_weight* w, const GemmArgs& ga, int64_t m, float* skpart) {
+  if (m >= 1 && m <= 16) {
+    const SkinnyPlan p = skinny_plan(w->k, w->n, 0, get_num_cus());
+    hipError_t e = launch_skinny_part(c->stream, w->format, true, ga, nullptr, p, skpart, nullptr);
+    if (e != hipSuccess) return e;
+    return launch_skinny_epi(c->stream, w->format, true, ga, p, skpart, nullptr, 1.0f, nullptr);
+  }
+  return launch_bwd(c->stream, w->format, ga);
+}
+
+// workspace bytes of the few-token input gradient's partials (0 for m > 16)
+static size_t skinny_dx_bytes(const lrq_weight* w, int64_t m) {
+  if (m < 1 || m > 16) return 0;
+  return skinny_ws_bytes(skinny_plan(w->k, w->n, 0, get_num_cus()), m, w->k, 0);
+}
+
 static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const uint16_t* dy, int64_t m,
                     const uint16_t* a, const uint16_t* b, int64_t r, float scaling, const uint16_t* t,
                     uint16_t* dx, float* da, float* db) {
@@ -483,8 +506,10 @@ static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const ui
     if (!aligned16(b)) return fail(c, LRQ_EINVAL, "B must be 16-byte aligned");
     const int rp = (int)round_up(r, 16);
     LRQ_TRY(check_lora_shapes(c, m, w->n, w->k, rp));
-    LRQ_TRY(ensure_ws(c, lora_layout(nullptr, m, w->n, w->k, rp).bytes));
+    const size_t lbytes = lora_layout(nullptr, m, w->n, w->k, rp).bytes;
+    LRQ_TRY(ensure_ws(c, lbytes + (dx ? skinny_dx_bytes(w, m) : 0)));
     LoraWs ws = lora_layout(c->ws, m, w->n, w->k, rp);
+    float* skpart = reinterpret_cast<float*>(c->ws + lbytes);
     // u = s . dy . B^T   (bf16 [m, rp]: the dx epilogue operand and dA's factor)
     const LoraPlan pu = lora_plan_nt(m, w->n, rp);
     LRQ_TRY(run(c, KID_LORA_U, "lora_u", [&] {
@@ -499,7 +524,7 @@ static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const ui
     ga.r = (int)r;
     ga.rp = rp;
     ga.part = ws.gp;
-    if (dx) LRQ_TRY(run(c, KID_BWD_DX, "bwd_dx", [&] { return launch_bwd(c->stream, w->format, ga); }));
+    if (dx) LRQ_TRY(run(c, KID_BWD_DX, "bwd_dx", [&] { return launch_dx(c, w, ga, m, skpart); }));
     // dA = x^T . u -> f32 [k, r] and dB = t^T . dy -> f32 [r, n]: token-slice
     // partials in one launch (dB's longer workgroups dispatched first), then
     // one reduction launch for both
@@ -524,12 +549,11 @@ static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const ui
     return LRQ_OK;
   }
   if (!dx) return LRQ_OK;
-  const int64_t pf = gemm_split_floats(m, w->k, w->n);
-  if (pf > 0) {
-    LRQ_TRY(ensure_ws(c, (size_t)pf * 4));
-    ga.part = reinterpret_cast<float*>(c->ws);
-  }
-  return run(c, KID_BWD_DX, "bwd_dx", [&] { return launch_bwd(c->stream, w->format, ga); });
+  const int64_t pf = (m >= 1 && m <= 16) ? 0 : gemm_split_floats(m, w->k, w->n);
+  LRQ_TRY(ensure_ws(c, std::max((size_t)pf * 4, skinny_dx_bytes(w, m))));
+  if (pf > 0) ga.part = reinterpret_cast<float*>(c->ws);
+  float* skpart = reinterpret_cast<float*>(c->ws);
+  return run(c, KID_BWD_DX, "bwd_dx", [&] { return launch_dx(c, w, ga, m, skpart); });
 }
 
 int lrq_quant_matmul_t_bwd(lrq_ctx* c, const lrq_weight* w, const uint16_t* dy, int64_t m, uint16_t* dx) {

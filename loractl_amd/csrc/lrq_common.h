@@ -136,6 +136,35 @@ LRQ_DEV int xcd_remap(int bid, int nblk) {
   return x * q + min(x, r) + i;
 }
 
+// ---------------------------------------------------------------- lane broadcast
+// Lane n of each 16-lane row, broadcast to the whole row (DPP row_newbcast).
+template <int N>
+LRQ_DEV float row_bcast(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x150 + N, 0xf, 0xf,
+                                                               true));
+}
+// n is a constant once the callers' loops are unrolled; the switch folds away
+LRQ_DEV float row_bcast_n(float v, int n) {
+  switch (n) {
+    case 0: return row_bcast<0>(v);
+    case 1: return row_bcast<1>(v);
+    case 2: return row_bcast<2>(v);
+    case 3: return row_bcast<3>(v);
+    case 4: return row_bcast<4>(v);
+    case 5: return row_bcast<5>(v);
+    case 6: return row_bcast<6>(v);
+    case 7: return row_bcast<7>(v);
+    case 8: return row_bcast<8>(v);
+    case 9: return row_bcast<9>(v);
+    case 10: return row_bcast<10>(v);
+    case 11: return row_bcast<11>(v);
+    case 12: return row_bcast<12>(v);
+    case 13: return row_bcast<13>(v);
+    case 14: return row_bcast<14>(v);
+    default: return row_bcast<15>(v);
+  }
+}
+
 // ---------------------------------------------------------------- buffer loads
 // Raw buffer loads with a wave-uniform resource: an offset at or past
 // num_records reads zeros, so bounds handling needs no branches.

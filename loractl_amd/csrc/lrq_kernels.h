@@ -54,12 +54,16 @@ hipError_t launch_bwd(hipStream_t st, int fmt, const GemmArgs& a);
 int64_t gemm_split_floats(int64_t m, int64_t e, int64_t depth);
 int get_num_cus();
 
-// lrq_skinny.hip: the forward for m <= 16 in two launches. `part` streams the
-// packed weight once and writes f32 partials of x . W^T per reduction split
-// ([S][m][n]) and, when a.rp > 0, of x . A per k slice ([TS][16][rp], from
-// the down factor A [k, r]); `epi` sums them in a fixed order and writes
+// lrq_skinny.hip: the forward for m <= 16 in two launches. `part` streams
+// the packed weight once and writes f32 partials of x . W^T per reduction
+// split ([S][m][n]) and, when a.rp > 0, of x . A per k slice ([TS][16][rp],
+// from the down factor A [k, r]); `epi` sums them in a fixed order and writes
 // y = bf16(sc * base + t . B + bias) with t = bf16(scaling * x . A), and t
 // itself ([m, r]) when t_out is set. a.lw is B [r, n].
+// With bwd, the same two launches give the input gradient for m <= 16 from
+// the transposed section (GemmArgs of the backward, a plan of
+// skinny_plan(k, n, 0, .)): dx = bf16(sum of partials + u . A^T), with u
+// (a.lact [m, rp]) and A (a.lw [k, rp]) given.
 struct SkinnyPlan {
   int S, KS;  // reduction splits of the base, 64-wide blocks per split
   int TS;     // k slices of t (0 without LoRA)
@@ -67,10 +71,10 @@ struct SkinnyPlan {
 };
 SkinnyPlan skinny_plan(int64_t n, int64_t k, int rp, int num_cus);
 size_t skinny_ws_bytes(const SkinnyPlan& p, int64_t m, int64_t n, int rp);
-hipError_t launch_skinny_part(hipStream_t st, int fmt, const GemmArgs& a, const uint16_t* A, const SkinnyPlan& p,
-                              float* part, float* tpart);
-hipError_t launch_skinny_epi(hipStream_t st, int fmt, const GemmArgs& a, const SkinnyPlan& p, const float* part,
-                             const float* tpart, float scaling, uint16_t* t_out);
+hipError_t launch_skinny_part(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, const uint16_t* A,
+                              const SkinnyPlan& p, float* part, float* tpart);
+hipError_t launch_skinny_epi(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, const SkinnyPlan& p,
+                             const float* part, const float* tpart, float scaling, uint16_t* t_out);
 
 // lrq_lora.hip
 // A split of a LoRA reduction: `tiles` output tiles x `splits` slices of

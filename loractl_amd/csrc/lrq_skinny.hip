@@ -49,7 +49,7 @@ struct SkArgs {
   float* tpart;       // [TS][16][rp]
 };
 
-template <int FMT>
+template <int FMT, bool BWD>
 __global__ void __launch_bounds__(SK_NT) k_sk_part(SkArgs sa) {
   constexpr bool I4 = FMT == LRQ_FMT_INT4;
   // cross-wavefront reduction buffer: [4 wavefronts][64 columns][16 tokens]
@@ -58,7 +58,7 @@ __global__ void __launch_bounds__(SK_NT) k_sk_part(SkArgs sa) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c16 = lane & 15, kq = lane >> 4;
-  const int64_t M = a.m, K = a.wk, E = a.e;
+  const int64_t M = a.m, K = a.l, E = a.e;  // K: the depth (d_in forward, d_out backward)
   const int64_t KB = (K + 63) / 64;
   const int TS = sa.p.TS;
 
@@ -142,7 +142,15 @@ __global__ void __launch_bounds__(SK_NT) k_sk_part(SkArgs sa) {
   constexpr uint32_t rowb = I4 ? 32u : 64u;
   const rsrc_t rw = make_rsrc(a.wdata + nb * KB * blkb, clamp_bytes(KB * (int64_t)blkb));
   const int64_t Gp = I4 ? ((KB * 64) >> a.gshift) : 0;
-  const rsrc_t rs = I4 ? make_rsrc(a.wscale + nb * Gp * 64, clamp_bytes(Gp * 64 * 4)) : make_rsrc(a.wscale, 4u);
+  // forward: int4 group scales of the block row ([NB][Gp][64]); backward: the
+  // per-depth scales (int4 the transposed table ST [KGt][64 KB], fp8 the
+  // channel scales [depth] or one scalar)
+  const int64_t NP = KB * 64;
+  const int64_t KGt = (BWD && I4) ? (((E + 63) / 64 * 64 + (1 << a.gshift) - 1) >> a.gshift) : 0;
+  const rsrc_t rs = BWD ? (I4 ? make_rsrc(a.wscale, clamp_bytes(KGt * NP * 4))
+                              : make_rsrc(a.wscale, a.per_channel ? clamp_bytes(K * 4) : 0u))
+                        : (I4 ? make_rsrc(a.wscale + nb * Gp * 64, clamp_bytes(Gp * 64 * 4)) : make_rsrc(a.wscale, 4u));
+  const float s0add = (BWD && !I4 && !a.per_channel) ? a.wscale[0] : 0.0f;
   const rsrc_t rx = make_rsrc(a.act, clamp_bytes(M * K * 2));
   const uint32_t woff = (uint32_t)c16 * rowb + (uint32_t)kq * (I4 ? 8u : 16u);
   const uint32_t xoff = (uint32_t)(((int64_t)c16 * K + kq * 16) * 2);
@@ -152,7 +160,7 @@ __global__ void __launch_bounds__(SK_NT) k_sk_part(SkArgs sa) {
   u32x4 xf[SK_WB][2];
   u32x2 w4[I4 ? SK_WB : 1][4];
   u32x2 w8[I4 ? 1 : SK_WB][4][2];
-  float sc[I4 ? SK_WB : 1][4];
+  float sc[(I4 || BWD) ? SK_WB : 1][4];  // forward int4: per row tile; backward: lane c16's depth (fp8: [b][0])
 #pragma unroll
   for (int b = 0; b < SK_WB; ++b) {
     const bool ok = b < nkb;
@@ -163,13 +171,23 @@ __global__ void __launch_bounds__(SK_NT) k_sk_part(SkArgs sa) {
       const bool xok = ok && k < K;  // K % 8 == 0
       xf[b][jj] = bload16(rx, opaque_u32(xok ? xoff + (uint32_t)(((int64_t)kb * 64 + jj * 8) * 2) : LRQ_OOB));
     }
+    // backward: lane (kq, c16) holds the scale of depth 64 kb + 16 kq + c16,
+    // which the 16 lanes of its DPP row (one kq) broadcast among themselves
+    const uint32_t dpos = kb * 64u + (uint32_t)(kq * 16 + c16);
+    if (BWD && !I4) sc[b][0] = bloadf(rs, opaque_u32(ok ? dpos * 4u : LRQ_OOB)) + s0add;
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) {
       const uint32_t wo = kb * blkb + (uint32_t)(rt * 16) * rowb + woff;
       if constexpr (I4) {
         w4[b][rt] = bload8(rw, opaque_u32(ok ? wo : LRQ_OOB));
-        const uint32_t j = (kb * 64u + (uint32_t)kq * 16u) >> a.gshift;
-        sc[b][rt] = bloadf(rs, opaque_u32(ok ? (j * 64u + (uint32_t)(rt * 16 + c16)) * 4u : LRQ_OOB));
+        if (BWD) {
+          // group of output rows 64 nb + 16 rt .. +16 (groups are >= 32 and aligned)
+          const uint32_t kg = (uint32_t)((nb * 64 + rt * 16) >> a.gshift);
+          sc[b][rt] = bloadf(rs, opaque_u32(ok ? (uint32_t)((kg * NP + dpos) * 4) : LRQ_OOB));
+        } else {
+          const uint32_t j = (kb * 64u + (uint32_t)kq * 16u) >> a.gshift;
+          sc[b][rt] = bloadf(rs, opaque_u32(ok ? (j * 64u + (uint32_t)(rt * 16 + c16)) * 4u : LRQ_OOB));
+        }
       } else {
         const u32x4 v = bload16(rw, opaque_u32(ok ? wo : LRQ_OOB));
         w8[b][rt][0] = (u32x2){v[0], v[1]};
@@ -194,7 +212,24 @@ __global__ void __launch_bounds__(SK_NT) k_sk_part(SkArgs sa) {
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj) {
         u32x4 wb;
-        if constexpr (I4) {
+        if constexpr (BWD) {
+          // transposed section: value e is q (a sign-extended nibble, or the
+          // e4m3 value) times the scale of its depth 16 kq + 8 jj + e, then bf16
+          float f[8];
+          if (I4) {
+            const uint32_t d = w4[b][rt][jj];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) f[e] = (float)((int)(d << (28 - 4 * e)) >> 28);
+          } else {
+            fp8x4_to_f32(w8[b][rt][jj][0], f);
+            fp8x4_to_f32(w8[b][rt][jj][1], f + 4);
+          }
+          const float S = sc[b][I4 ? rt : 0];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) f[e] = row_bcast_n(S, 8 * jj + e) * f[e];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) wb[q] = pack_bf16x2(f[2 * q], f[2 * q + 1]);
+        } else if constexpr (I4) {
           wb = dequant8_int4_bf16(w4[b][rt][jj], sc[b][rt], a.nib);
         } else {
           const u32x2 p0 = fp8x4_to_bf16(w8[b][rt][jj][0]), p1 = fp8x4_to_bf16(w8[b][rt][jj][1]);
@@ -228,10 +263,13 @@ __global__ void __launch_bounds__(SK_NT) k_sk_part(SkArgs sa) {
 
 // y[m, n] = bf16(sc[n] * sum_s part[s][m][n] + sum_j t[m, j] B[j, n] + bias[n]).
 // Every workgroup first reduces t = bf16(scale * sum_ts tpart[ts]) into LDS.
+// Backward: dx[m, k] = bf16(sum_s part[s][m][k] + sum_j u[m, j] A[k, j]) with
+// u = a.lact [m, rp] and A = a.lw [k, rp] given (no scale: the transposed
+// weight's scales are applied per value, no bias).
 // A thread owns two adjacent columns and four tokens. Every load is a
 // buffer load whose out-of-range offsets read zero, so none sits behind a
 // branch and all of a thread's loads issue together.
-template <int FMT>
+template <int FMT, bool BWD>
 __global__ void __launch_bounds__(SK_NT) k_sk_epi(SkArgs sa, float scaling, uint16_t* t_out) {
   const GemmArgs& a = sa.g;
   const int tid = threadIdx.x;
@@ -239,7 +277,14 @@ __global__ void __launch_bounds__(SK_NT) k_sk_epi(SkArgs sa, float scaling, uint
   const int rp = a.rp, r = a.r, S = sa.p.S, TS = sa.p.TS;
   __shared__ __attribute__((aligned(16))) float tt[16][64];
   const rsrc_t rtp = make_rsrc(sa.tpart, clamp_bytes((int64_t)TS * 16 * rp * 4));
-  for (int i = tid; i < 16 * rp; i += SK_NT) {
+  if (BWD) {
+    const rsrc_t ru = make_rsrc(a.lact, clamp_bytes(M * rp * 2));
+    for (int i = tid; i < 16 * rp; i += SK_NT) {
+      const int m = i / rp, j = i % rp;
+      tt[m][j] = __uint_as_float(bload2(ru, opaque_u32((uint32_t)((m * rp + j) * 2))) << 16);
+    }
+  }
+  for (int i = tid; i < (BWD ? 0 : 16 * rp); i += SK_NT) {
     const int m = i / rp, j = i % rp;
     // slices in order, 16 loads issued together per batch
     float v = 0.0f;
@@ -259,12 +304,29 @@ __global__ void __launch_bounds__(SK_NT) k_sk_epi(SkArgs sa, float scaling, uint
   const int64_t n = (int64_t)blockIdx.x * 128 + 2 * (tid & 63);  // E % 8 == 0: n < E implies n + 1 < E
   const int mg = tid >> 6;                                        // tokens 4 mg .. 4 mg + 3
   if (n >= E || 4 * mg >= M) return;
-  const rsrc_t rb = make_rsrc(a.lw, clamp_bytes((int64_t)r * E * 2));
+  const rsrc_t rb = make_rsrc(a.lw, clamp_bytes((int64_t)(BWD ? rp : r) * E * 2));
   const rsrc_t rpt = make_rsrc(sa.part, clamp_bytes((int64_t)S * M * E * 4));
   const rsrc_t rbias = make_rsrc(a.bias, a.bias ? clamp_bytes(E * 4) : 0u);
+  // bp[j]: the weight-side factor at columns n (low half) and n + 1 (high)
   uint32_t bp[64];
+  if (BWD) {
+    // rows n and n + 1 of A [k, rp], 8 values per load, interleaved
 #pragma unroll
-  for (int j = 0; j < 64; ++j) bp[j] = bload4(rb, opaque_u32(j < r ? (uint32_t)(((int64_t)j * E + n) * 2) : LRQ_OOB));
+    for (int q = 0; q < 8; ++q) {
+      const bool ok = q * 8 < rp;
+      const u32x4 v0 = bload16(rb, opaque_u32(ok ? (uint32_t)((n * rp + q * 8) * 2) : LRQ_OOB));
+      const u32x4 v1 = bload16(rb, opaque_u32(ok ? (uint32_t)(((n + 1) * rp + q * 8) * 2) : LRQ_OOB));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        bp[q * 8 + 2 * e] = __builtin_amdgcn_perm(v1[e], v0[e], 0x05040100u);
+        bp[q * 8 + 2 * e + 1] = __builtin_amdgcn_perm(v1[e], v0[e], 0x07060302u);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 64; ++j)
+      bp[j] = bload4(rb, opaque_u32(j < r ? (uint32_t)(((int64_t)j * E + n) * 2) : LRQ_OOB));
+  }
   u32x2 pv[4][8];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -274,7 +336,7 @@ __global__ void __launch_bounds__(SK_NT) k_sk_epi(SkArgs sa, float scaling, uint
       pv[i][s] = bload8(rpt, opaque_u32((s < S && m < M) ? (uint32_t)((((int64_t)s * M + m) * E + n) * 4) : LRQ_OOB));
   }
   float sc0 = 1.0f, sc1 = 1.0f;
-  if (FMT == LRQ_FMT_FP8) {
+  if (!BWD && FMT == LRQ_FMT_FP8) {
     sc0 = a.wscale[a.per_channel ? n : 0];
     sc1 = a.wscale[a.per_channel ? n + 1 : 0];
   }
@@ -359,29 +421,43 @@ size_t skinny_ws_bytes(const SkinnyPlan& p, int64_t m, int64_t n, int rp) {
   return (part + 255) / 256 * 256 + tp + 256;
 }
 
-hipError_t launch_skinny_part(hipStream_t st, int fmt, const GemmArgs& a, const uint16_t* A, const SkinnyPlan& p,
-                              float* part, float* tpart) {
+hipError_t launch_skinny_part(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, const uint16_t* A,
+                              const SkinnyPlan& p, float* part, float* tpart) {
   if (a.m <= 0 || a.m > 16 || p.S < 1 || p.KS < 1 || p.KS > SK_MAXKS) return hipErrorInvalidValue;
   SkArgs sa{a, A, p, part, tpart};
-  if (a.rp == 0) sa.p.TS = 0;
+  if (a.rp == 0 || bwd) sa.p.TS = 0;
   const int64_t NB = (a.e + 63) / 64;
   const unsigned grid = (unsigned)(NB * p.S + sa.p.TS);
-  if (fmt == LRQ_FMT_INT4)
-    hipLaunchKernelGGL(k_sk_part<LRQ_FMT_INT4>, dim3(grid), dim3(SK_NT), 0, st, sa);
-  else
-    hipLaunchKernelGGL(k_sk_part<LRQ_FMT_FP8>, dim3(grid), dim3(SK_NT), 0, st, sa);
+  if (fmt == LRQ_FMT_INT4) {
+    if (bwd)
+      hipLaunchKernelGGL((k_sk_part<LRQ_FMT_INT4, true>), dim3(grid), dim3(SK_NT), 0, st, sa);
+    else
+      hipLaunchKernelGGL((k_sk_part<LRQ_FMT_INT4, false>), dim3(grid), dim3(SK_NT), 0, st, sa);
+  } else {
+    if (bwd)
+      hipLaunchKernelGGL((k_sk_part<LRQ_FMT_FP8, true>), dim3(grid), dim3(SK_NT), 0, st, sa);
+    else
+      hipLaunchKernelGGL((k_sk_part<LRQ_FMT_FP8, false>), dim3(grid), dim3(SK_NT), 0, st, sa);
+  }
   return hipGetLastError();
 }
 
-hipError_t launch_skinny_epi(hipStream_t st, int fmt, const GemmArgs& a, const SkinnyPlan& p, const float* part,
-                             const float* tpart, float scaling, uint16_t* t_out) {
+hipError_t launch_skinny_epi(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, const SkinnyPlan& p,
+                             const float* part, const float* tpart, float scaling, uint16_t* t_out) {
   if (a.m <= 0 || a.m > 16) return hipErrorInvalidValue;
   SkArgs sa{a, nullptr, p, const_cast<float*>(part), const_cast<float*>(tpart)};
-  if (a.rp == 0) sa.p.TS = 0;
+  if (a.rp == 0 || bwd) sa.p.TS = 0;
   const unsigned grid = (unsigned)((a.e + 127) / 128);
-  if (fmt == LRQ_FMT_INT4)
-    hipLaunchKernelGGL(k_sk_epi<LRQ_FMT_INT4>, dim3(grid), dim3(SK_NT), 0, st, sa, scaling, t_out);
-  else
-    hipLaunchKernelGGL(k_sk_epi<LRQ_FMT_FP8>, dim3(grid), dim3(SK_NT), 0, st, sa, scaling, t_out);
+  if (fmt == LRQ_FMT_INT4) {
+    if (bwd)
+      hipLaunchKernelGGL((k_sk_epi<LRQ_FMT_INT4, true>), dim3(grid), dim3(SK_NT), 0, st, sa, scaling, t_out);
+    else
+      hipLaunchKernelGGL((k_sk_epi<LRQ_FMT_INT4, false>), dim3(grid), dim3(SK_NT), 0, st, sa, scaling, t_out);
+  } else {
+    if (bwd)
+      hipLaunchKernelGGL((k_sk_epi<LRQ_FMT_FP8, true>), dim3(grid), dim3(SK_NT), 0, st, sa, scaling, t_out);
+    else
+      hipLaunchKernelGGL((k_sk_epi<LRQ_FMT_FP8, false>), dim3(grid), dim3(SK_NT), 0, st, sa, scaling, t_out);
+  }
   return hipGetLastError();
 }
