@@ -290,10 +290,10 @@ int lrq_reserve(lrq_ctx* c, int64_t m, int64_t n, int64_t k, int64_t r) {
   if (m >= 1) {  // the few-token forward, at up to 16 tokens
     const size_t sk = skinny_ws_bytes(skinny_plan(n, k, rp, get_num_cus()), m < 16 ? m : 16, n, rp);
     if (sk > need) need = sk;
-    // the few-token input gradient: its partials follow the LoRA workspace
+    // the few-token input gradient: its partials (and u's) follow the LoRA workspace
     const int64_t mm = m < 16 ? m : 16;
     const size_t skd = lora_layout(nullptr, mm, n, k, rp).bytes +
-                       skinny_ws_bytes(skinny_plan(k, n, 0, get_num_cus()), mm, k, 0);
+                       skinny_ws_bytes(skinny_plan(k, n, rp, get_num_cus()), mm, k, rp);
     if (skd > need) need = skd;
   }
   const size_t fp8_need = (size_t)round_up(n * 4, 256);
@@ -506,46 +506,61 @@ static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const ui
     if (!aligned16(b)) return fail(c, LRQ_EINVAL, "B must be 16-byte aligned");
     const int rp = (int)round_up(r, 16);
     LRQ_TRY(check_lora_shapes(c, m, w->n, w->k, rp));
+    const bool few = dx && m >= 1 && m <= 16;
+    const SkinnyPlan sp = skinny_plan(w->k, w->n, rp, get_num_cus());
     const size_t lbytes = lora_layout(nullptr, m, w->n, w->k, rp).bytes;
-    LRQ_TRY(ensure_ws(c, lbytes + (dx ? skinny_dx_bytes(w, m) : 0)));
+    LRQ_TRY(ensure_ws(c, lbytes + (few ? skinny_ws_bytes(sp, m, w->k, rp) : 0)));
     LoraWs ws = lora_layout(c->ws, m, w->n, w->k, rp);
-    float* skpart = reinterpret_cast<float*>(c->ws + lbytes);
-    // u = s . dy . B^T   (bf16 [m, rp]: the dx epilogue operand and dA's factor)
-    const LoraPlan pu = lora_plan_nt(m, w->n, rp);
-    LRQ_TRY(run(c, KID_LORA_U, "lora_u", [&] {
-      hipError_t e = launch_lora_nt(c->stream, dy, b, true, w->n, (int)r, m, w->n, rp, pu, ws.pn);
-      if (e != hipSuccess) return e;
-      // and A [k, r] padded to [k, rp]: the dx GEMM's weight-side LoRA rows
-      return launch_nt_reduce(c->stream, ws.pn, pu.splits, m, rp, (int)r, scaling, ws.up, nullptr, a, w->k, true,
-                              ws.fr);
-    }));
-    ga.lact = ws.up;
-    ga.lw = ws.fr;
     ga.r = (int)r;
     ga.rp = rp;
-    ga.part = ws.gp;
-    if (dx) LRQ_TRY(run(c, KID_BWD_DX, "bwd_dx", [&] { return launch_dx(c, w, ga, m, skpart); }));
+    if (few) {
+      // few tokens: u = s . dy . B^T (bf16 [m, rp], dA's factor) comes out
+      // of the input gradient's own two launches, as t does in the forward
+      float* part = reinterpret_cast<float*>(c->ws + lbytes);
+      float* tpart = part + round_up((int64_t)sp.S * m * w->k, 64);
+      ga.lw = a;
+      LRQ_TRY(run(c, KID_BWD_DX, "bwd_dx", [&] {
+        hipError_t e = launch_skinny_part(c->stream, w->format, true, ga, b, sp, part, tpart);
+        if (e != hipSuccess) return e;
+        return launch_skinny_epi(c->stream, w->format, true, ga, sp, part, tpart, scaling, ws.up);
+      }));
+    } else {
+      // u = s . dy . B^T   (bf16 [m, rp]: the dx epilogue operand and dA's factor)
+      const LoraPlan pu = lora_plan_nt(m, w->n, rp);
+      LRQ_TRY(run(c, KID_LORA_U, "lora_u", [&] {
+        hipError_t e = launch_lora_nt(c->stream, dy, b, true, w->n, (int)r, m, w->n, rp, pu, ws.pn);
+        if (e != hipSuccess) return e;
+        // and A [k, r] padded to [k, rp]: the dx GEMM's weight-side LoRA rows
+        return launch_nt_reduce(c->stream, ws.pn, pu.splits, m, rp, (int)r, scaling, ws.up, nullptr, a, w->k,
+                                true, ws.fr);
+      }));
+      ga.lact = ws.up;
+      ga.lw = ws.fr;
+      ga.part = ws.gp;
+      if (dx) LRQ_TRY(run(c, KID_BWD_DX, "bwd_dx", [&] { return launch_bwd(c->stream, w->format, ga); }));
+    }
     // dA = x^T . u -> f32 [k, r] and dB = t^T . dy -> f32 [r, n]: token-slice
     // partials in one launch (dB's longer workgroups dispatched first), then
     // one reduction launch for both
+    // (a job of one token slice writes its result directly, unreduced)
     TnSpec specs[2];
     TnJob jobs[2];
-    int nj = 0;
+    int nj = 0, nr = 0;
     if (db) {
       const LoraPlan pb = lora_plan_tn(m, w->n, rp);
-      specs[nj] = TnSpec{dy, t, r, m, w->n, (int)r, pb, ws.pb};
-      jobs[nj++] = TnJob{ws.pb, w->n, rp, (int)r, pb.splits, db, 1, w->n};
+      specs[nj++] = TnSpec{dy, t, r, m, w->n, (int)r, pb, ws.pb, db, 1, w->n};
+      if (pb.splits > 1) jobs[nr++] = TnJob{ws.pb, w->n, rp, (int)r, pb.splits, db, 1, w->n};
     }
     if (da) {
       const LoraPlan pa = lora_plan_tn(m, w->k, rp);
-      specs[nj] = TnSpec{x, ws.up, rp, m, w->k, (int)r, pa, ws.pa};
-      jobs[nj++] = TnJob{ws.pa, w->k, rp, (int)r, pa.splits, da, r, 1};
+      specs[nj++] = TnSpec{x, ws.up, rp, m, w->k, (int)r, pa, ws.pa, da, r, 1};
+      if (pa.splits > 1) jobs[nr++] = TnJob{ws.pa, w->k, rp, (int)r, pa.splits, da, r, 1};
     }
     if (nj) {
       const int kid = nj == 2 ? KID_LORA_DADB : (db ? KID_LORA_DB : KID_LORA_DA);
       LRQ_TRY(run(c, kid, kNames[kid], [&] { return launch_lora_tn(c->stream, specs, nj, rp); }));
-      LRQ_TRY(run(c, KID_LORA_RED, "lora_reduce", [&] { return launch_tn_reduce(c->stream, jobs, nj); }));
     }
+    if (nr) LRQ_TRY(run(c, KID_LORA_RED, "lora_reduce", [&] { return launch_tn_reduce(c->stream, jobs, nr); }));
     return LRQ_OK;
   }
   if (!dx) return LRQ_OK;

@@ -62,8 +62,9 @@ int get_num_cus();
 // itself ([m, r]) when t_out is set. a.lw is B [r, n].
 // With bwd, the same two launches give the input gradient for m <= 16 from
 // the transposed section (GemmArgs of the backward, a plan of
-// skinny_plan(k, n, 0, .)): dx = bf16(sum of partials + u . A^T), with u
-// (a.lact [m, rp]) and A (a.lw [k, rp]) given.
+// skinny_plan(k, n, rp, .)): dx = bf16(sum of partials + u . A^T) with
+// u = bf16(scaling * dy . B^T) from the partials of dy . B^T (`A` of part is
+// then B [r, n]), written to t_out as [m, rp]; a.lw is A [k, r].
 struct SkinnyPlan {
   int S, KS;  // reduction splits of the base, 64-wide blocks per split
   int TS;     // k slices of t (0 without LoRA)
@@ -110,6 +111,8 @@ struct TnSpec {
   int R;
   LoraPlan plan;
   float* partial;
+  float* out;       // the result out[c * sc + j * sj], written directly when plan.splits == 1
+  int64_t sc, sj;
 };
 hipError_t launch_lora_tn(hipStream_t st, const TnSpec* jobs, int njobs, int rp);
 // out[c * sc + j * sj] = sum_s partial[s][c][j] (slice order) for c < C, j < R.

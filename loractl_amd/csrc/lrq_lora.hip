@@ -221,12 +221,12 @@ __global__ void __launch_bounds__(256) k_nt_reduce(const float* __restrict__ par
   const int j = (int)(idx % rp);
   const int64_t stride = M * rp;
   float sum = 0.0f;
-  for (int s0 = 0; s0 < splits; s0 += 8) {
-    float v[8];
+  for (int s0 = 0; s0 < splits; s0 += 16) {
+    float v[16];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = (s0 + i < splits) ? partial[(s0 + i) * stride + idx] : 0.0f;
+    for (int i = 0; i < 16; ++i) v[i] = (s0 + i < splits) ? partial[(s0 + i) * stride + idx] : 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) sum += v[i];
+    for (int i = 0; i < 16; ++i) sum += v[i];
   }
   const uint16_t h = f32_to_bf16_bits(j < r ? sum * s : 0.0f);
   if (out) out[idx] = h;
@@ -242,6 +242,8 @@ struct TnArgs {
   int64_t m_per;       // tokens per slice (multiple of 128)
   float* partial;      // [splits][C][rp]
   int tiles, blocks;   // column tiles of 128, tiles x slices
+  float* out;          // one slice: the result out[c * sc + j * sj] (j < R) instead of partial
+  int64_t sc, sj;
 };
 
 // partial[split][c][j] = sum over the split's tokens of p[m, c] * q[m, j],
@@ -365,7 +367,13 @@ __global__ void __launch_bounds__(TNT) k_lora_tn(TnArgs j0, TnArgs j1) {
       float sum = 0.0f;
 #pragma unroll
       for (int w = 0; w < TW; ++w) sum += red[(w * 128 + cl) * 16 + jl];
-      if (c0 + cl < C) part[(c0 + cl) * RP + jt * 16 + jl] = sum;
+      if (c0 + cl < C) {
+        if (a.out) {
+          if (jt * 16 + jl < a.R) a.out[(c0 + cl) * a.sc + (int64_t)(jt * 16 + jl) * a.sj] = sum;
+        } else {
+          part[(c0 + cl) * RP + jt * 16 + jl] = sum;
+        }
+      }
     }
     __syncthreads();
   }
@@ -407,12 +415,14 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 }  // namespace
 
 // nt: 128-token tiles x column slices (multiples of 32) so that the grid is
-// ~256 workgroups (one per CU, 8 wavefronts each); a slice wider than the
-// LDS factor slice holds (nt_cap) is staged and streamed in sub-slices.
+// ~256 workgroups (one per CU, 8 wavefronts each), in at most 32 slices (a
+// few tokens gain nothing from more workgroups, and the reduction reads
+// every slice); a slice wider than the LDS factor slice holds (nt_cap) is
+// staged and streamed in sub-slices.
 LoraPlan lora_plan_nt(int64_t M, int64_t C, int rp) {
   LoraPlan p{};
   const int64_t tiles = cdiv(M > 0 ? M : 1, 128);
-  const int64_t want = cdiv(256, tiles);
+  const int64_t want = std::min<int64_t>(32, cdiv(256, tiles));
   int64_t per = 32 * cdiv(cdiv(C, want), 32);
   if (per < 32) per = 32;
   p.per = per;
@@ -473,7 +483,8 @@ hipError_t launch_lora_tn(hipStream_t st, const TnSpec* jobs, int njobs, int rp)
   for (int i = 0; i < njobs && i < 2; ++i) {
     const TnSpec& j = jobs[i];
     const int64_t blocks = j.C > 0 ? j.plan.tiles * j.plan.splits : 0;
-    t[i] = TnArgs{j.p, j.q, j.M, j.C, j.ldq, j.R, j.plan.per, j.partial, (int)j.plan.tiles, (int)blocks};
+    t[i] = TnArgs{j.p,      j.q, j.M, j.C, j.ldq, j.R, j.plan.per, j.partial, (int)j.plan.tiles, (int)blocks,
+                  j.plan.splits == 1 ? j.out : nullptr, j.sc, j.sj};
     total += blocks;
   }
   if (total == 0) return hipSuccess;

@@ -27,8 +27,10 @@
 //   applies the fp8 per-channel scale, adds t . B (t rounded to bf16 as in
 //   the large-m path) and the bias, and writes y (and t).
 //
-// Dequantized weights round to bf16 exactly as in the large-m kernel
-// (fma(u, s, -8s) == q*s, then bf16). No atomics: results are bitwise
+// int4 with groups of 64 or more multiplies the integer q exactly and
+// applies the group scale in f32 per 64-wide block (see MQ below), which is
+// the oracle's f32 dequantization; groups of 32 and fp8 use the large-m
+// kernel's operand (bf16(q s), exact e4m3). No atomics: results are bitwise
 // reproducible.
 
 #include "lrq_common.h"
@@ -38,7 +40,7 @@ namespace {
 
 constexpr int SK_NT = 256;     // threads per workgroup (4 wavefronts)
 constexpr int SK_MAXKS = 16;   // reduction blocks per split, at most
-constexpr int SK_TSTEPS = 2;   // 32-wide k steps of a t slice per wavefront (slices <= 256)
+constexpr int SK_TSTEPS = 2;   // 32-wide k steps of a t (u) slice per wavefront (slices <= 256)
 constexpr int SK_WB = SK_MAXKS / 4;  // blocks per wavefront run, at most
 
 struct SkArgs {
@@ -49,7 +51,13 @@ struct SkArgs {
   float* tpart;       // [TS][16][rp]
 };
 
-template <int FMT, bool BWD>
+// MQ (int4 forward, groups of 64 or more, so one group per 64-wide block):
+// the matrix-core operand is the stored nibble u = q + 8 as the exact bf16
+// value 128 + u (bits 0x4300 | u, two bit operations per pair), each block
+// is multiplied into fresh accumulators, and the block's partial is scaled
+// in f32: s * (sum x (128 + u) - 136 sum x) = s * sum x q. The block sums of
+// x come from one more matrix-core step against ones.
+template <int FMT, bool BWD, bool MQ>
 __global__ void __launch_bounds__(SK_NT) k_sk_part(SkArgs sa) {
   constexpr bool I4 = FMT == LRQ_FMT_INT4;
   // cross-wavefront reduction buffer: [4 wavefronts][64 columns][16 tokens]
@@ -64,6 +72,7 @@ __global__ void __launch_bounds__(SK_NT) k_sk_part(SkArgs sa) {
 
   if ((int)blockIdx.x < TS) {
     // ---------------- t partial: tpart[ts][m][j] = sum over the slice of x[m, k] A[k, j]
+    // (backward: of dy[m, n] B[j, n], for u)
     const int ts = blockIdx.x, rp = a.rp, r = a.r;
     const int64_t kt0 = (int64_t)ts * sa.p.KT, kt1 = kt0 + sa.p.KT < K ? kt0 + sa.p.KT : K;
     const int nsteps = (int)((kt1 - kt0 + 31) / 32);  // <= 4 * SK_TSTEPS
@@ -75,13 +84,12 @@ __global__ void __launch_bounds__(SK_NT) k_sk_part(SkArgs sa) {
     // one k step per phase: each issues all its loads (out-of-range ones
     // read zero) before its matrix-core steps, in few enough registers that
     // the streaming workgroups keep their occupancy
+    u32x4 xf[SK_TSTEPS];
+    uint32_t bw[SK_TSTEPS][4][4];
 #pragma unroll
-    for (int ph = 0; ph < SK_TSTEPS; ++ph) {
-      u32x4 xf[1];
-      uint32_t bw[1][4][4];
-#pragma unroll
-      for (int i = 0; i < 1; ++i) {
-        const int st = wv + (SK_NT / 64) * ph;
+    for (int i = 0; i < SK_TSTEPS; ++i) {
+      {
+        const int st = wv + (SK_NT / 64) * i;
         const int64_t k = kt0 + (int64_t)st * 32 + kq * 8;
         const bool kok = st < nsteps && k < kt1;  // K % 8 == 0 and slices are multiples of 32
         xf[i] = bload16(rx, opaque_u32(kok ? (uint32_t)(((int64_t)c16 * K + k) * 2) : LRQ_OOB));
@@ -91,11 +99,16 @@ __global__ void __launch_bounds__(SK_NT) k_sk_part(SkArgs sa) {
           const bool ok = kok && j < r;
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            // A[k + 2q][j], A[k + 2q + 1][j]
-            const uint32_t off = (uint32_t)(((k + 2 * q) * r + j) * 2);
-            const uint32_t lo = bload2(ra, opaque_u32(ok ? off : LRQ_OOB));
-            const uint32_t hi = bload2(ra, opaque_u32(ok ? off + (uint32_t)(2 * r) : LRQ_OOB));
-            bw[i][jt][q] = lo | (hi << 16);
+            if (BWD) {
+              // B[j][k + 2q], B[j][k + 2q + 1] (one dword: the depth is a multiple of 8)
+              bw[i][jt][q] = bload4(ra, opaque_u32(ok ? (uint32_t)(((int64_t)j * K + k + 2 * q) * 2) : LRQ_OOB));
+            } else {
+              // A[k + 2q][j], A[k + 2q + 1][j]
+              const uint32_t off = (uint32_t)(((k + 2 * q) * r + j) * 2);
+              const uint32_t lo = bload2(ra, opaque_u32(ok ? off : LRQ_OOB));
+              const uint32_t hi = bload2(ra, opaque_u32(ok ? off + (uint32_t)(2 * r) : LRQ_OOB));
+              bw[i][jt][q] = lo | (hi << 16);
+            }
           }
         }
       }
@@ -103,11 +116,9 @@ __global__ void __launch_bounds__(SK_NT) k_sk_part(SkArgs sa) {
       // result read in a block other than the one that wrote it has come
       // back stale here, so the steps stay branch-free
 #pragma unroll
-      for (int i = 0; i < 1; ++i)
-#pragma unroll
-        for (int jt = 0; jt < 4; ++jt)
-          acc[jt] = mfma16(as_bf16x8(xf[i]), as_bf16x8((u32x4){bw[i][jt][0], bw[i][jt][1], bw[i][jt][2], bw[i][jt][3]}),
-                           acc[jt]);
+      for (int jt = 0; jt < 4; ++jt)
+        acc[jt] = mfma16(as_bf16x8(xf[i]), as_bf16x8((u32x4){bw[i][jt][0], bw[i][jt][1], bw[i][jt][2], bw[i][jt][3]}),
+                         acc[jt]);
       __builtin_amdgcn_sched_barrier(0);
     }
     // reduce the four wavefronts; C element v of lane l: token 4*(l/16) + v, column l%16
@@ -207,6 +218,34 @@ __global__ void __launch_bounds__(SK_NT) k_sk_part(SkArgs sa) {
     // blocks past this wavefront's run hold zeros: the steps stay
     // unconditional (a matrix-core result read in another block than the
     // one that wrote it has come back stale)
+    if constexpr (MQ) {
+      const u32x4 ones = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+      f32x4 xsum = {0.0f, 0.0f, 0.0f, 0.0f};
+      u32x4 xp[2];
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const u32x4 v = xf[b][jj];
+        xsum = mfma16(as_bf16x8(v), as_bf16x8(ones), xsum);
+        // k order 0 4 1 5 2 6 3 7, as the weight pairs below
+        xp[jj] = (u32x4){__builtin_amdgcn_perm(v[2], v[0], 0x05040100u), __builtin_amdgcn_perm(v[2], v[0], 0x07060302u),
+                         __builtin_amdgcn_perm(v[3], v[1], 0x05040100u), __builtin_amdgcn_perm(v[3], v[1], 0x07060302u)};
+      }
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt) {
+        f32x4 ab = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+          const uint32_t d = w4[b][rt][jj];
+          // (u_e, u_e+4) as bf16 (128 + u) pairs
+          const u32x4 wb = {(d & 0x000f000fu) | 0x43004300u, ((d >> 4) & 0x000f000fu) | 0x43004300u,
+                            ((d >> 8) & 0x000f000fu) | 0x43004300u, ((d >> 12) & 0x000f000fu) | 0x43004300u};
+          ab = mfma16(as_bf16x8(xp[jj]), as_bf16x8(wb), ab);
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[rt][v] = __builtin_fmaf(sc[b][rt], __builtin_fmaf(-136.0f, xsum[v], ab[v]), acc[rt][v]);
+      }
+      continue;
+    }
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) {
 #pragma unroll
@@ -264,8 +303,9 @@ __global__ void __launch_bounds__(SK_NT) k_sk_part(SkArgs sa) {
 // y[m, n] = bf16(sc[n] * sum_s part[s][m][n] + sum_j t[m, j] B[j, n] + bias[n]).
 // Every workgroup first reduces t = bf16(scale * sum_ts tpart[ts]) into LDS.
 // Backward: dx[m, k] = bf16(sum_s part[s][m][k] + sum_j u[m, j] A[k, j]) with
-// u = a.lact [m, rp] and A = a.lw [k, rp] given (no scale: the transposed
-// weight's scales are applied per value, no bias).
+// u = bf16(scaling * sum_ts tpart[ts]) (t_out gets u [m, rp]) and A = a.lw
+// [k, r] (no scale: the transposed weight's scales are applied per value,
+// no bias).
 // A thread owns two adjacent columns and four tokens. Every load is a
 // buffer load whose out-of-range offsets read zero, so none sits behind a
 // branch and all of a thread's loads issue together.
@@ -276,56 +316,44 @@ __global__ void __launch_bounds__(SK_NT) k_sk_epi(SkArgs sa, float scaling, uint
   const int64_t M = a.m, E = a.e;
   const int rp = a.rp, r = a.r, S = sa.p.S, TS = sa.p.TS;
   __shared__ __attribute__((aligned(16))) float tt[16][64];
-  const rsrc_t rtp = make_rsrc(sa.tpart, clamp_bytes((int64_t)TS * 16 * rp * 4));
-  if (BWD) {
-    const rsrc_t ru = make_rsrc(a.lact, clamp_bytes(M * rp * 2));
-    for (int i = tid; i < 16 * rp; i += SK_NT) {
-      const int m = i / rp, j = i % rp;
-      tt[m][j] = __uint_as_float(bload2(ru, opaque_u32((uint32_t)((m * rp + j) * 2))) << 16);
-    }
-  }
-  for (int i = tid; i < (BWD ? 0 : 16 * rp); i += SK_NT) {
-    const int m = i / rp, j = i % rp;
-    // slices in order, 16 loads issued together per batch
-    float v = 0.0f;
-    for (int q0 = 0; q0 < TS; q0 += 16) {
-      float part[16];
-#pragma unroll
-      for (int q = 0; q < 16; ++q)
-        part[q] = bloadf(rtp, opaque_u32(q0 + q < TS ? (uint32_t)((((q0 + q) * 16 + m) * rp + j) * 4) : LRQ_OOB));
-#pragma unroll
-      for (int q = 0; q < 16; ++q) v += part[q];
-    }
-    const uint32_t hb = pack_bf16x2(scaling * v, 0.0f) & 0xffffu;  // t as the caller sees it
-    tt[m][j] = __uint_as_float(hb << 16);
-    if (blockIdx.x == 0 && t_out && m < M && j < r) t_out[(int64_t)m * r + j] = (uint16_t)hb;
-  }
-  __syncthreads();
   const int64_t n = (int64_t)blockIdx.x * 128 + 2 * (tid & 63);  // E % 8 == 0: n < E implies n + 1 < E
   const int mg = tid >> 6;                                        // tokens 4 mg .. 4 mg + 3
-  if (n >= E || 4 * mg >= M) return;
-  const rsrc_t rb = make_rsrc(a.lw, clamp_bytes((int64_t)(BWD ? rp : r) * E * 2));
+  const bool live = n < E && 4 * mg < M;
+  // this thread's loads go out first, so that they share one memory round
+  // trip with the reduction of t below (dead threads' offsets read zero)
+  const rsrc_t rb = make_rsrc(a.lw, clamp_bytes((int64_t)r * E * 2));
   const rsrc_t rpt = make_rsrc(sa.part, clamp_bytes((int64_t)S * M * E * 4));
   const rsrc_t rbias = make_rsrc(a.bias, a.bias ? clamp_bytes(E * 4) : 0u);
   // bp[j]: the weight-side factor at columns n (low half) and n + 1 (high)
   uint32_t bp[64];
   if (BWD) {
-    // rows n and n + 1 of A [k, rp], 8 values per load, interleaved
+    // A[n][j] and A[n + 1][j] from A [k, r]: rows of 16-byte runs when r is
+    // a multiple of 8 and A is 16-byte aligned, else value by value
+    if ((r & 7) == 0 && (reinterpret_cast<uintptr_t>(a.lw) & 15) == 0) {
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const bool ok = q * 8 < rp;
-      const u32x4 v0 = bload16(rb, opaque_u32(ok ? (uint32_t)((n * rp + q * 8) * 2) : LRQ_OOB));
-      const u32x4 v1 = bload16(rb, opaque_u32(ok ? (uint32_t)(((n + 1) * rp + q * 8) * 2) : LRQ_OOB));
+      for (int q = 0; q < 8; ++q) {
+        const bool ok = live && q * 8 < r;
+        const u32x4 v0 = bload16(rb, opaque_u32(ok ? (uint32_t)((n * r + q * 8) * 2) : LRQ_OOB));
+        const u32x4 v1 = bload16(rb, opaque_u32(ok ? (uint32_t)(((n + 1) * r + q * 8) * 2) : LRQ_OOB));
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        bp[q * 8 + 2 * e] = __builtin_amdgcn_perm(v1[e], v0[e], 0x05040100u);
-        bp[q * 8 + 2 * e + 1] = __builtin_amdgcn_perm(v1[e], v0[e], 0x07060302u);
+        for (int e = 0; e < 4; ++e) {
+          bp[q * 8 + 2 * e] = __builtin_amdgcn_perm(v1[e], v0[e], 0x05040100u);
+          bp[q * 8 + 2 * e + 1] = __builtin_amdgcn_perm(v1[e], v0[e], 0x07060302u);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 64; ++j) {
+        const bool ok = live && j < r;
+        const uint32_t lo = bload2(rb, opaque_u32(ok ? (uint32_t)((n * r + j) * 2) : LRQ_OOB));
+        const uint32_t hi = bload2(rb, opaque_u32(ok ? (uint32_t)(((n + 1) * r + j) * 2) : LRQ_OOB));
+        bp[j] = lo | (hi << 16);
       }
     }
   } else {
 #pragma unroll
     for (int j = 0; j < 64; ++j)
-      bp[j] = bload4(rb, opaque_u32(j < r ? (uint32_t)(((int64_t)j * E + n) * 2) : LRQ_OOB));
+      bp[j] = bload4(rb, opaque_u32(live && j < r ? (uint32_t)(((int64_t)j * E + n) * 2) : LRQ_OOB));
   }
   u32x2 pv[4][8];
 #pragma unroll
@@ -333,14 +361,51 @@ __global__ void __launch_bounds__(SK_NT) k_sk_epi(SkArgs sa, float scaling, uint
     const int m = 4 * mg + i;
 #pragma unroll
     for (int s = 0; s < 8; ++s)
-      pv[i][s] = bload8(rpt, opaque_u32((s < S && m < M) ? (uint32_t)((((int64_t)s * M + m) * E + n) * 4) : LRQ_OOB));
+      pv[i][s] = bload8(rpt, opaque_u32((live && s < S && m < M) ? (uint32_t)((((int64_t)s * M + m) * E + n) * 4)
+                                                                   : LRQ_OOB));
   }
   float sc0 = 1.0f, sc1 = 1.0f;
   if (!BWD && FMT == LRQ_FMT_FP8) {
-    sc0 = a.wscale[a.per_channel ? n : 0];
-    sc1 = a.wscale[a.per_channel ? n + 1 : 0];
+    const rsrc_t rsc = make_rsrc(a.wscale, clamp_bytes((a.per_channel ? E : 1) * 4));
+    const uint32_t c0 = a.per_channel ? (uint32_t)(n * 4) : 0u;
+    sc0 = bloadf(rsc, opaque_u32(live ? c0 : LRQ_OOB));
+    sc1 = bloadf(rsc, opaque_u32(live ? c0 + (a.per_channel ? 4u : 0u) : LRQ_OOB));
   }
-  const u32x2 bias = bload8(rbias, (uint32_t)(n * 4));
+  const u32x2 bias = bload8(rbias, opaque_u32(live ? (uint32_t)(n * 4) : LRQ_OOB));
+
+  const rsrc_t rtp = make_rsrc(sa.tpart, clamp_bytes((int64_t)TS * 16 * rp * 4));
+  // two outputs per thread and pass (entries i and i + SK_NT of [16][rp]),
+  // slices in order, 16 loads of each issued together per batch
+  for (int i0 = tid; i0 < 16 * rp; i0 += 2 * SK_NT) {
+    float v[2] = {0.0f, 0.0f};
+    for (int q0 = 0; q0 < TS; q0 += 16) {
+      float part[2][16];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          const int i = i0 + h * SK_NT;
+          part[h][q] = bloadf(rtp, opaque_u32((q0 + q < TS && i < 16 * rp) ? (uint32_t)(((q0 + q) * 16 * rp + i) * 4)
+                                                                           : LRQ_OOB));
+        }
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int q = 0; q < 16; ++q) v[h] += part[h][q];
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int i = i0 + h * SK_NT;
+      if (i >= 16 * rp) break;
+      const int m = i / rp, j = i % rp;
+      const uint32_t hb = pack_bf16x2(scaling * v[h], 0.0f) & 0xffffu;  // t (u) as the caller sees it
+      tt[m][j] = __uint_as_float(hb << 16);
+      // t [m, r]; u [m, rp] (columns >= r zero), dA's factor
+      if (blockIdx.x == 0 && t_out && m < M && (BWD || j < r)) t_out[(int64_t)m * (BWD ? rp : r) + j] = (uint16_t)hb;
+    }
+  }
+  __syncthreads();
+  if (!live) return;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int m = 4 * mg + i;
@@ -425,19 +490,21 @@ hipError_t launch_skinny_part(hipStream_t st, int fmt, bool bwd, const GemmArgs&
                               const SkinnyPlan& p, float* part, float* tpart) {
   if (a.m <= 0 || a.m > 16 || p.S < 1 || p.KS < 1 || p.KS > SK_MAXKS) return hipErrorInvalidValue;
   SkArgs sa{a, A, p, part, tpart};
-  if (a.rp == 0 || bwd) sa.p.TS = 0;
+  if (a.rp == 0 || !A) sa.p.TS = 0;
   const int64_t NB = (a.e + 63) / 64;
   const unsigned grid = (unsigned)(NB * p.S + sa.p.TS);
   if (fmt == LRQ_FMT_INT4) {
     if (bwd)
-      hipLaunchKernelGGL((k_sk_part<LRQ_FMT_INT4, true>), dim3(grid), dim3(SK_NT), 0, st, sa);
+      hipLaunchKernelGGL((k_sk_part<LRQ_FMT_INT4, true, false>), dim3(grid), dim3(SK_NT), 0, st, sa);
+    else if (a.gshift >= 6)
+      hipLaunchKernelGGL((k_sk_part<LRQ_FMT_INT4, false, true>), dim3(grid), dim3(SK_NT), 0, st, sa);
     else
-      hipLaunchKernelGGL((k_sk_part<LRQ_FMT_INT4, false>), dim3(grid), dim3(SK_NT), 0, st, sa);
+      hipLaunchKernelGGL((k_sk_part<LRQ_FMT_INT4, false, false>), dim3(grid), dim3(SK_NT), 0, st, sa);
   } else {
     if (bwd)
-      hipLaunchKernelGGL((k_sk_part<LRQ_FMT_FP8, true>), dim3(grid), dim3(SK_NT), 0, st, sa);
+      hipLaunchKernelGGL((k_sk_part<LRQ_FMT_FP8, true, false>), dim3(grid), dim3(SK_NT), 0, st, sa);
     else
-      hipLaunchKernelGGL((k_sk_part<LRQ_FMT_FP8, false>), dim3(grid), dim3(SK_NT), 0, st, sa);
+      hipLaunchKernelGGL((k_sk_part<LRQ_FMT_FP8, false, false>), dim3(grid), dim3(SK_NT), 0, st, sa);
   }
   return hipGetLastError();
 }
@@ -446,7 +513,7 @@ hipError_t launch_skinny_epi(hipStream_t st, int fmt, bool bwd, const GemmArgs& 
                              const float* part, const float* tpart, float scaling, uint16_t* t_out) {
   if (a.m <= 0 || a.m > 16) return hipErrorInvalidValue;
   SkArgs sa{a, nullptr, p, const_cast<float*>(part), const_cast<float*>(tpart)};
-  if (a.rp == 0 || bwd) sa.p.TS = 0;
+  if (a.rp == 0 || !tpart) sa.p.TS = 0;
   const unsigned grid = (unsigned)((a.e + 127) / 128);
   if (fmt == LRQ_FMT_INT4) {
     if (bwd)

@@ -154,16 +154,17 @@ def test_split_depth_bias_and_scales(cuda, fmt, per_channel):
     check("dx", dx, dx_ref.cpu().numpy())
 
 
-@pytest.mark.parametrize("M", [1, 3, 16])
+@pytest.mark.parametrize("M,r", [(1, 17), (3, 32), (16, 17), (16, 64)])
 @pytest.mark.parametrize("fmt,per_channel,group", [("int4", True, 32), ("int4", True, 128), ("fp8", True, 0),
                                                    ("fp8", False, 0)])
-def test_few_token_input_gradient(cuda, M, fmt, per_channel, group):
+def test_few_token_input_gradient(cuda, M, r, fmt, per_channel, group):
     """m <= 16: the input gradient streams the transposed section once in
     depth splits (d_out = 2056, ragged past 32 blocks of 64); the transposed
     scales (int4 groups along d_in, fp8 channel scales or the scalar along
-    the depth) are applied per value, and u . A^T is added in the reduction."""
-    K, N, r = 1024, 2056, 17
-    g = torch.Generator(device=cuda).manual_seed(11 + M)
+    the depth) are applied per value, and u . A^T is added in the reduction;
+    u itself (s . dy . B^T) is reduced there too and feeds dA."""
+    K, N = 1024, 2056
+    g = torch.Generator(device=cuda).manual_seed(11 + M + r)
     w = torch.randn(N, K, device=cuda, generator=g) * 0.02
     wq = D.quantize_int4(w, group) if fmt == "int4" else D.quantize_fp8(w, per_channel)
     wdq = D.dequant(wq)
@@ -172,12 +173,15 @@ def test_few_token_input_gradient(cuda, M, fmt, per_channel, group):
     b = (torch.randn(r, N, device=cuda, generator=g) * 1e-1).to(torch.bfloat16)
     dy = torch.randn(M, N, device=cuda, generator=g).to(torch.bfloat16)
     y, t = D.lora_fwd(x, wq, a, b, 0.5)
-    dx, _, _ = D.lora_bwd(x, dy, wq, a, b, 0.5, t)
+    dx, da, db = D.lora_bwd(x, dy, wq, a, b, 0.5, t)
     dx0 = D.quant_matmul_t_bwd(dy, wq)
     dyf, af, bf = dy.float(), a.float(), b.float()
     u = (0.5 * (dyf @ bf.t())).to(torch.bfloat16).float()
     check("dx", dx, (dyf @ wdq + u @ af.t()).cpu().numpy())
     check("dx base", dx0, (dyf @ wdq).cpu().numpy())
+    # u comes out of the input gradient's launches and feeds dA
+    check("dA", da, (x.float().t() @ u).cpu().numpy())
+    check("dB", db, (t.float().t() @ dyf).cpu().numpy())
 
 
 def test_zero_b_delta_is_bitwise_no_op(cuda):
