@@ -62,8 +62,10 @@ hipEvent_t take_event(lrq_ctx* c) {
     c->pool.pop_back();
     return e;
   }
+  // timing only: no system-scope fence (a cache write-back per marker
+  // would be timed with the kernel it brackets)
   hipEvent_t e = nullptr;
-  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  if (hipEventCreateWithFlags(&e, hipEventDisableSystemFence) != hipSuccess) return nullptr;
   return e;
 }
 
