@@ -18,6 +18,11 @@ its average launch time taken from HIP events that the library records
 around each of its launches on the launch stream. `cpu_baseline` times the
 reference's CPU algorithm (the oracle's f32 dequant + f32 GEMMs) on a
 bounded token sample of the same layer.
+
+`--workload requant` measures the on-device load path: an fp8 checkpoint
+tensor of the same layer (e4m3fn bytes and per-row f32 scales, [12288,
+3072]) re-quantized to int4-g64 by one kernel; `value` is GB/s of fp8 bytes
+and scales in plus packed int4 and group scales out per call.
 """
 
 from __future__ import annotations
@@ -40,6 +45,7 @@ WORKLOADS = {
     "c1": (1024, 3072, 3072, 16, 16.0, "int4", 64),
     "c2": (4096, 3072, 12288, 32, 32.0, "fp8", 0),
     "skinny": (16, 3072, 12288, 32, 32.0, "int4", 64),  # forward only, HBM-bound
+    "requant": (0, 3072, 12288, 0, 0.0, "fp8", 64),  # fp8 checkpoint tensor -> int4, load time
 }
 INFINITY_CACHE_BYTES = 256 << 20
 GPU_SPIN_CYCLES = 100_000_000  # ~50 ms: longer than the host needs to enqueue a profiled loop
@@ -100,6 +106,8 @@ def main():
     dev = torch.device("cuda:0")
     if args.workload == "skinny":
         return bench_skinny(args, dev)
+    if args.workload == "requant":
+        return bench_requant(args, dev)
     M, K, N, r, alpha, fmt, group = WORKLOADS[args.workload]
     s = alpha / r
     w, x, a, b, dy = make_inputs(M, K, N, r)
@@ -331,6 +339,84 @@ def bench_skinny(args, dev):
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
+
+
+def bench_requant(args, dev):
+    """fp8 e4m3fn [N, K] + per-row scales -> int4 (Q4S, g64) on the device,
+    timed over `steps` calls with inputs resident; the CPU baseline is the
+    reference's host path (f32 decode, then the Q4S quantizer) on a row
+    sample."""
+    import numpy as np
+    import torch
+
+    from loractl_amd import device as D
+    from loractl_amd import fp8 as F
+
+    _, K, N, _, _, _, group = WORKLOADS["requant"]
+    w, _, _, _, _ = make_inputs(1, K, N, 1)
+    w8 = D.quantize_fp8(torch.from_numpy(w).to(dev), True)
+    w8 = F.fp8_weight("w", w8.data, w8.scales)
+    for _ in range(args.warmup):
+        D.requantize_fp8_int4(w8, group)
+    torch.cuda.synchronize()
+    out = D.requantize_fp8_int4(w8, group)
+    if not out.scales.abs().max() > 0:
+        raise RuntimeError("implausible output (all-zero scales)")
+
+    def timed(n):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(n):
+            D.requantize_fp8_int4(w8, group)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1)
+
+    ms = timed(args.steps) / args.steps
+    ratio = timed(2 * args.steps) / (ms * args.steps)
+    nbytes = N * K + 4 * N + N * K // 2 + 4 * N * (K // group)
+    value = nbytes / (ms * 1e-3) / 1e9
+    D.profile_reset()
+    D.profile_enable(True)
+    torch.cuda._sleep(GPU_SPIN_CYCLES)
+    for _ in range(args.steps):
+        D.requantize_fp8_int4(w8, group)
+    torch.cuda.synchronize()
+    prof = D.profile_read()
+    D.profile_enable(False)
+    kernels = {k: 1e3 * t / n for k, (t, n) in prof.items() if n}
+    achieved = nbytes / (kernels["quantize_int4"] * 1e-6) / 1e9
+    cpu = None
+    if not args.no_cpu_baseline:
+        import oracle as O
+
+        rows = 256
+        b8, s8 = w8.data[:rows].cpu().numpy(), w8.scales[:rows].cpu().numpy()
+        O.quantize_int4_packed(O.fp8_dequant(b8, s8), group)
+        reps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < min(args.cpu_seconds, 10.0):
+            O.quantize_int4_packed(O.fp8_dequant(b8, s8), group)
+            reps += 1
+        dt = (time.perf_counter() - t0) / reps
+        cpu = {"value": round(nbytes * rows / N / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+               "sample": f"{rows} of {N} rows, {reps} reps of {dt:.4f} s (f32 decode, then Q4S quantize)"}
+    print(json.dumps({
+        "metric": "fp8 checkpoint tensor -> int4 on-device requantization GB/s",
+        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "u8", "data": "synthetic (seeded PCG64 W~N(0,0.02), fp8 per-row repack on device)",
+        "config": {"workload": f"fp8 e4m3fn [{N}, {K}] + per-row f32 scales -> int4-g{group} (packed + scales)",
+                   "N": N, "K": K, "group": group, "parallelism": "single-gpu"},
+        "sanity_x2_ratio": round(ratio, 3),
+        "kernels_us": {k: round(v, 3) for k, v in kernels.items()},
+        "roofline": {"kernel": "quantize_int4", "bound": "hbm", "achieved": round(achieved, 1),
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                     "traffic": load_traffic("quantize_int4", "requant"), "bytes_per_launch": nbytes,
+                     "avg_launch_us": round(kernels["quantize_int4"], 3)},
+        "cpu_baseline": cpu,
+    }), flush=True)
 
 
 def cpu_baseline_fwd(wq, x, a, b, M, K, N, r, s, group, budget_s, bytes_fwd):

@@ -120,6 +120,16 @@ int lrq_quantize_int4(lrq_ctx* ctx, const float* w, int64_t n, int64_t k, int64_
 int lrq_quantize_fp8(lrq_ctx* ctx, const float* w, int64_t n, int64_t k, int per_channel,
                      uint8_t* bytes, float* scales);
 
+/* fp8 checkpoint tensor -> int4 on the device: e4m3fn bytes [n, k] and their
+ * f32 scale (one value, or one per output row when per_channel) decode to
+ * the f32 LUT[byte] * scale of src/fp8.rs:306-318, which is quantized as
+ * lrq_quantize_int4 does (src/quant.rs:74-82); the reference's load pass
+ * does both on the host, one tensor at a time, through an f32 copy
+ * (src/diffusion_trainer.rs:1143-1169). Bit-identical to lrq_dequant of the
+ * fp8 weight followed by lrq_quantize_int4. */
+int lrq_requantize_fp8_int4(lrq_ctx* ctx, const uint8_t* bytes, const float* scale, int per_channel, int64_t n,
+                            int64_t k, int64_t group, uint8_t* packed, float* scales);
+
 /* Sizes of the blocked layout of a weight, both sections: data bytes and
  * scale count (0 for fp8, whose scales keep their shape). No device work. */
 int lrq_weight_blocked_size(int format, int64_t n, int64_t k, int64_t group, int64_t* data_bytes,

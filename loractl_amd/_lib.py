@@ -69,6 +69,7 @@ SIGNATURES = {
     "lrq_reserve": (_i32, [_vp, _i64, _i64, _i64, _i64]),
     "lrq_quantize_int4": (_i32, [_vp, _vp, _i64, _i64, _i64, _vp, _vp]),
     "lrq_quantize_fp8": (_i32, [_vp, _vp, _i64, _i64, _i32, _vp, _vp]),
+    "lrq_requantize_fp8_int4": (_i32, [_vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp, _vp]),
     "lrq_weight_blocked_size": (_i32, [_i32, _i64, _i64, _i64, ctypes.POINTER(_i64), ctypes.POINTER(_i64)]),
     "lrq_weight_block": (_i32, [_vp, _wp, _vp, _vp]),
     "lrq_dequant": (_i32, [_vp, _wp, _vp]),

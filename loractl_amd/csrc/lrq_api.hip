@@ -318,6 +318,25 @@ int lrq_quantize_int4(lrq_ctx* c, const float* w, int64_t n, int64_t k, int64_t 
              [&] { return launch_quantize_int4(c->stream, w, n, k, (int)group, packed, scales); });
 }
 
+int lrq_requantize_fp8_int4(lrq_ctx* c, const uint8_t* bytes, const float* scale, int per_channel, int64_t n,
+                            int64_t k, int64_t group, uint8_t* packed, float* scales) {
+  LRQ_TRY(begin(c));
+  if (n < 0 || k < 0) return fail(c, LRQ_EINVAL, "negative shape");
+  if (group < 32 || group > 2048 || (group & (group - 1)) != 0)
+    return fail(c, LRQ_EINVAL, "quant block %lld must be a power of two in [32, 2048]", (long long)group);
+  if (k % group != 0)
+    return fail(c, LRQ_EINVAL,
+                "linear weight [%lld, %lld]: the input dim must be a multiple of the quant block (%lld)",
+                (long long)n, (long long)k, (long long)group);
+  if (n * k > 0 && (!bytes || !scale || !packed || !scales))
+    return fail(c, LRQ_EINVAL, "fp8 requantize: NULL pointer");
+  if (!aligned16(bytes) || !aligned16(packed)) return fail(c, LRQ_EINVAL, "bytes and packed must be 16-byte aligned");
+  return run(c, KID_QUANT_INT4, "quantize_int4", [&] {
+    return launch_requantize_fp8_int4(c->stream, bytes, scale, per_channel ? 1 : 0, n, k, (int)group, packed,
+                                      scales);
+  });
+}
+
 int lrq_quantize_fp8(lrq_ctx* c, const float* w, int64_t n, int64_t k, int per_channel,
                      uint8_t* bytes, float* scales) {
   LRQ_TRY(begin(c));

@@ -8,6 +8,10 @@
 // lrq_quant.hip
 hipError_t launch_quantize_int4(hipStream_t st, const float* w, int64_t n, int64_t k, int g,
                                 uint8_t* packed, float* scales);
+// the same from e4m3fn bytes [n, k] and their scalar (per_channel 0) or
+// per-row f32 scale: int4 of the f32 values LUT[byte] * scale
+hipError_t launch_requantize_fp8_int4(hipStream_t st, const uint8_t* bytes, const float* scale, int per_channel,
+                                      int64_t n, int64_t k, int g, uint8_t* packed, float* scales);
 hipError_t launch_quantize_fp8(hipStream_t st, const float* w, int64_t n, int64_t k,
                                int per_channel, uint8_t* bytes, float* scales, float* amax_ws);
 hipError_t launch_dequant(hipStream_t st, const lrq_weight* w, void* out, bool bf16);

@@ -13,21 +13,42 @@
 // covered by group/32 consecutive threads that reduce absmax with lane
 // shuffles (group/32 <= 64 lanes, a power of two or not: a plain loop over
 // the partner lanes keeps it exact).
-__global__ void __launch_bounds__(256) k_quantize_int4(const float* __restrict__ w, int64_t n,
-                                                       int64_t k, int g, uint8_t* __restrict__ packed,
-                                                       float* __restrict__ scales) {
+// FP8: the input is e4m3fn bytes [n, k] with a scalar or per-row f32 scale,
+// and each value is LUT[byte] * scale in f32 first (src/fp8.rs:306-318), the
+// reference's f32 snapshot of an fp8 checkpoint tensor, which its load pass
+// then quantizes (src/diffusion_trainer.rs:1143-1169); no f32 copy is kept.
+template <bool FP8>
+__global__ void __launch_bounds__(256) k_quantize_int4(const void* __restrict__ wv, const float* __restrict__ fsc,
+                                                       int per_channel, int64_t n, int64_t k, int g,
+                                                       uint8_t* __restrict__ packed, float* __restrict__ scales) {
   const int64_t runs_per_row = k / 32;
   const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (tid >= n * runs_per_row) return;
   const int64_t row = tid / runs_per_row;
   const int64_t run = tid % runs_per_row;
-  const float* src = w + row * k + run * 32;
   float v[32];
   float amax = 0.0f;
+  if constexpr (FP8) {
+    const uint8_t* src = static_cast<const uint8_t*>(wv) + row * k + run * 32;
+    const float sc = fsc[per_channel ? row : 0];
 #pragma unroll
-  for (int i = 0; i < 32; i += 4) {
-    f32x4 t = *reinterpret_cast<const f32x4*>(src + i);
-    v[i] = t[0]; v[i + 1] = t[1]; v[i + 2] = t[2]; v[i + 3] = t[3];
+    for (int i = 0; i < 32; i += 16) {
+      const u32x4 b = ld16(src + i);
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        float f[4];
+        fp8x4_to_f32(b[d], f);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[i + 4 * d + e] = f[e] * sc;
+      }
+    }
+  } else {
+    const float* src = static_cast<const float*>(wv) + row * k + run * 32;
+#pragma unroll
+    for (int i = 0; i < 32; i += 4) {
+      f32x4 t = *reinterpret_cast<const f32x4*>(src + i);
+      v[i] = t[0]; v[i + 1] = t[1]; v[i + 2] = t[2]; v[i + 3] = t[3];
+    }
   }
 #pragma unroll
   for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
@@ -295,8 +316,17 @@ hipError_t launch_quantize_int4(hipStream_t st, const float* w, int64_t n, int64
                                 uint8_t* packed, float* scales) {
   const int64_t items = n * (k / 32);
   if (items == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_quantize_int4, dim3(blocks_for(items, 256)), dim3(256), 0, st, w, n, k, g,
-                     packed, scales);
+  hipLaunchKernelGGL(k_quantize_int4<false>, dim3(blocks_for(items, 256)), dim3(256), 0, st, w, nullptr, 0, n, k,
+                     g, packed, scales);
+  return hipGetLastError();
+}
+
+hipError_t launch_requantize_fp8_int4(hipStream_t st, const uint8_t* bytes, const float* scale, int per_channel,
+                                      int64_t n, int64_t k, int g, uint8_t* packed, float* scales) {
+  const int64_t items = n * (k / 32);
+  if (items == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_quantize_int4<true>, dim3(blocks_for(items, 256)), dim3(256), 0, st, bytes, scale,
+                     per_channel, n, k, g, packed, scales);
   return hipGetLastError();
 }
 

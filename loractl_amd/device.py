@@ -169,6 +169,23 @@ def quantize_int4(w: torch.Tensor, group: int) -> PackedWeight:
     return PackedWeight(L.LRQ_FMT_INT4, n, k, packed, scales, group=group)
 
 
+def requantize_fp8_int4(w: PackedWeight, group: int) -> PackedWeight:
+    """An fp8 weight (e4m3fn bytes and scale) as int4 at Q4S on the GPU: the
+    f32 values LUT[byte] * scale (src/fp8.rs:306-318) quantized like
+    ``quantize_int4`` (src/quant.rs:74-82), without an f32 copy."""
+    if w.fmt != L.LRQ_FMT_FP8:
+        raise ValueError("requantize_fp8_int4 needs an fp8 weight")
+    if w.layout != L.LRQ_LAYOUT_ROWS:
+        raise ValueError("requantize_fp8_int4 reads the row layout of the fp8 bytes")
+    n, k = w.n, w.k
+    ctx = context(w.data.device.index)
+    packed = torch.empty((n, k // 2), dtype=torch.uint8, device=w.data.device)
+    scales = torch.empty((n, max(k // group, 0) if group > 0 else 0), dtype=torch.float32, device=w.data.device)
+    ctx.check(ctx.lib.lrq_requantize_fp8_int4(ctx.h, _ptr(w.data), _ptr(w.scales), int(w.per_channel), n, k, group,
+                                              _ptr(packed), _ptr(scales)), "lrq_requantize_fp8_int4")
+    return PackedWeight(L.LRQ_FMT_INT4, n, k, packed, scales, group=group, bias=w.bias)
+
+
 def quantize_fp8(w: torch.Tensor, per_channel: bool) -> PackedWeight:
     """fp8 e4m3fn repack (reference/fp8_reference.py:83-91) on the GPU."""
     _need(w, torch.float32, "w")

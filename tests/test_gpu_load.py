@@ -1,0 +1,76 @@
+"""The on-device load path on the GPU: fp8 checkpoint bytes re-quantized to
+int4 by one kernel, bit-exact against the oracle's f32 decode
+(src/fp8.rs:306-318) followed by its Q4S quantizer (src/quant.rs:74-82),
+and whole checkpoints through load_fp8_checkpoint."""
+
+import numpy as np
+import pytest
+import torch
+from safetensors.torch import save_file
+
+import oracle as O
+from gpu_helpers import check, to_dev
+from loractl_amd import device as D
+from loractl_amd import fp8 as F
+from loractl_amd.load import load_fp8_checkpoint
+
+pytestmark = pytest.mark.gpu
+
+WEIGHT_5X3 = [0.5, -0.5, 1.0, 1.5, -1.5, 2.75, -3.0, 448.0, 0.0, 0.001953125, -448.0, 0.25, -2.0, 3.5, -0.0625]
+
+
+def _fp8_case(n, k, per_channel, seed):
+    rng = np.random.Generator(np.random.PCG64(seed))
+    b = rng.integers(0, 256, (n, k), dtype=np.uint8)
+    b[(b & 0x7F) == 0x7F] = 0x3C  # no NaN codes
+    s = (rng.uniform(0.5, 2.0, n if per_channel else 1) * 1e-3).astype(np.float32)
+    return b, s
+
+
+@pytest.mark.parametrize("group", [32, 64, 128])
+@pytest.mark.parametrize("per_channel", [True, False])
+def test_requantize_fp8_int4_bit_exact(cuda, group, per_channel):
+    n, k = 72, 384
+    b, s = _fp8_case(n, k, per_channel, seed=group + per_channel)
+    w8 = F.fp8_weight("w", torch.from_numpy(b).to(cuda), torch.from_numpy(s).to(cuda))
+    w4 = D.requantize_fp8_int4(w8, group)
+    p_ref, s_ref = O.quantize_int4_packed(O.fp8_dequant(b, s), group)
+    assert np.array_equal(w4.data.cpu().numpy(), p_ref)
+    assert np.array_equal(w4.scales.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+    # the same as the two-step device path through an f32 copy
+    w4b = D.quantize_int4(D.dequant(w8), group)
+    assert torch.equal(w4.data, w4b.data) and torch.equal(w4.scales, w4b.scales)
+
+
+def test_load_fp8_checkpoint_end_to_end(cuda, tmp_path):
+    n, k, M = 64, 256, 24
+    b, s = _fp8_case(n, k, True, seed=5)
+    bias = np.linspace(-1, 1, n).astype(np.float32)
+    path = str(tmp_path / "ck.safetensors")
+    save_file({"blk.w.weight": torch.from_numpy(b).view(torch.float8_e4m3fn),
+               "blk.w.weight_scale": torch.from_numpy(s), "blk.w.comfy_quant": torch.zeros(2, dtype=torch.uint8),
+               "blk.odd.weight": torch.tensor(WEIGHT_5X3).reshape(5, 3).to(torch.float8_e4m3fn),
+               "blk.odd.weight_scale": torch.tensor(2.0), "blk.bias": torch.from_numpy(bias)}, path)
+    raw = load_fp8_checkpoint(path, cuda)
+    q4 = load_fp8_checkpoint(path, cuda, quant="int4", group=64)
+    assert sorted(raw) == ["blk.bias", "blk.odd.weight", "blk.w.weight"]
+    # fp8 kept as stored: its decode is the reference snapshot, exactly
+    wd = O.fp8_dequant(b, s)
+    assert np.array_equal(D.dequant(raw["blk.w.weight"]).cpu().numpy(), wd)
+    # int4 re-quantized on the device: bit-exact Q4S of that snapshot
+    p_ref, s_ref = O.quantize_int4_packed(wd, 64)
+    assert np.array_equal(q4["blk.w.weight"].data.cpu().numpy(), p_ref)
+    assert np.array_equal(q4["blk.w.weight"].scales.cpu().numpy(), s_ref)
+    # an input dim the fused kernels cannot take stays plain f32 (tests/fp8.rs expected values)
+    for d in (raw, q4):
+        assert torch.equal(d["blk.odd.weight"].cpu(), torch.tensor(WEIGHT_5X3).reshape(5, 3) * 2.0)
+        assert torch.equal(d["blk.bias"].cpu(), torch.from_numpy(bias))
+    # and the loaded weights drive the fused forward
+    rng = np.random.Generator(np.random.PCG64(9))
+    x = rng.standard_normal((M, k), dtype=np.float32)
+    xb = to_dev(x, cuda)
+    xr = xb.float().cpu().numpy()
+    y8 = D.quant_matmul_t(xb, raw["blk.w.weight"])
+    y4 = D.quant_matmul_t(xb, q4["blk.w.weight"])
+    check("y fp8", y8, O.linear_fwd(xr, wd)[0])
+    check("y int4", y4, O.linear_fwd(xr, O.dequant_int4(p_ref, s_ref, k, 64))[0])
