@@ -1,6 +1,6 @@
 """Benchmark of the fused int4 frozen-base LoRA linear on one MI355X.
 
-Workload: int4 group-64 frozen Linear 3072 -> 12288 with
+Workload (the north-star configuration): int4 group-64 frozen Linear 3072 -> 12288 with
 LoRA r=32, alpha=32, M=4096 tokens, forward + backward (y, t, dx, dA, dB)
 per step. Inputs are synthetic, seeded (numpy PCG64: W=0, X=1, A=2, B=3,
 dY=4), resident in HBM before timing starts.

@@ -1,7 +1,7 @@
 """Parity of the fused quantized LoRA linear (forward and backward) on the GPU,
 through the C ABI, against the CPU oracle on identical seeded inputs
 (tolerance: rel_deviation <= 1e-2 and cosine >= 0.999 for bf16 outputs),
-and at BASELINE sizes against a torch fp32 reference built from the
+and at the benchmark configurations' full sizes against a torch fp32 reference built from the
 bit-exact dequantized weight."""
 
 import numpy as np
@@ -235,7 +235,7 @@ def test_shape_errors_are_loud(cuda):
                                          # slices and 8 reduction splits in the few-token epilogue
                                          (16, 9728, 2560, 16, "int4"), (5, 9728, 2560, 16, "fp8")])
 def test_baseline_shapes_against_torch_fp32(cuda, M, K, N, r, fmt):
-    """Full BASELINE sizes: the fused kernels vs torch fp32 GEMMs over the
+    """The benchmark configurations at full size: the fused kernels vs torch fp32 GEMMs over the
     same bf16 inputs and the (bit-exact) dequantized weight."""
     g = torch.Generator(device=cuda).manual_seed(M + N)
     w = torch.randn(N, K, device=cuda, generator=g) * 0.02
