@@ -42,6 +42,30 @@ def test_requantize_fp8_int4_bit_exact(cuda, group, per_channel):
     assert torch.equal(w4.data, w4b.data) and torch.equal(w4.scales, w4b.scales)
 
 
+def test_requantize_exact_ties(cuda):
+    """Half-integer quotients (exact on fp8 input) round half away from zero,
+    as the oracle's Q4S does: 7, 6.5 ... 0.5 times a scale, amax 7."""
+    halves = [7.0, 6.5, 5.5, 4.5, 3.5, 2.5, 1.5, 0.5]
+    row = np.array(halves + [-h for h in halves] + [0.0] * 16, np.float32)  # one run of 32
+    w = np.stack([row * 2.0 ** e for e in range(-6, 2)])  # 8 rows, k = 32
+    b = torch.tensor(w).to(torch.float8_e4m3fn)
+    assert np.array_equal(b.float().numpy(), w)
+    s = np.ones(8, np.float32)
+    w8 = F.fp8_weight("w", b.view(torch.uint8).to(cuda), torch.from_numpy(s).to(cuda))
+    w4 = D.requantize_fp8_int4(w8, 32)
+    p_ref, s_ref = O.quantize_int4_packed(w, 32)
+    assert np.array_equal(w4.data.cpu().numpy(), p_ref)
+    assert np.array_equal(w4.scales.cpu().numpy(), s_ref)
+    # closed form: the scale is exactly 2^e, every quotient is the half-integer itself
+    got = w4.data.cpu().numpy().astype(np.int64)
+    q = np.stack([got & 15, got >> 4], axis=-1).reshape(8, 32) - 8
+    want = [7, 7, 6, 5, 4, 3, 2, 1, -7, -7, -6, -5, -4, -3, -2, -1] + [0] * 16
+    assert (q == np.array(want)).all()
+    assert np.array_equal(w4.scales.cpu().numpy()[:, 0], 2.0 ** np.arange(-6, 2, dtype=np.float32))
+    w4f = D.quantize_int4(torch.from_numpy(w).to(cuda), 32)
+    assert torch.equal(w4.data, w4f.data)
+
+
 def test_load_fp8_checkpoint_end_to_end(cuda, tmp_path):
     n, k, M = 64, 256, 24
     b, s = _fp8_case(n, k, True, seed=5)
