@@ -458,9 +458,10 @@ __global__ void __launch_bounds__(SK_NT) k_sk_epi(SkArgs sa, float scaling, uint
 SkinnyPlan skinny_plan(int64_t n, int64_t k, int rp, int num_cus) {
   SkinnyPlan p{};
   const int64_t KB = (k + 63) / 64, NB = (n + 63) / 64;
-  // enough workgroups for about three per CU, at most 16 blocks per split,
+  // enough workgroups for about 9/4 per CU (fewer, longer splits measured
+  // faster than three per CU: fewer partials), at most 16 blocks per split,
   // and split partials (S * m * n f32) no larger than a quarter of the weight
-  int64_t S = (3 * (int64_t)num_cus + NB - 1) / NB;
+  int64_t S = (9 * (int64_t)num_cus + 4 * NB - 1) / (4 * NB);
   const int64_t s_min = (KB + SK_MAXKS - 1) / SK_MAXKS;
   int64_t s_max = k / 512;
   if (s_max < s_min) s_max = s_min;
