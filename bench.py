@@ -59,6 +59,7 @@ def parse():
     p.add_argument("--workload", default="ns", choices=sorted(WORKLOADS))
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-skinny", action="store_true", help="leave the skinny-M sub-object out of the ns line")
     return p.parse_args()
 
 
@@ -91,6 +92,53 @@ def load_traffic(kernel, workload):
         return None
 
 
+WARM_MIN_MS = 200.0     # warm for at least this much GPU time, whatever --warmup says
+WARM_MAX_MS = 20000.0   # and give up waiting for two agreeing windows after this much
+WARM_AGREE = 0.03       # consecutive windows agreeing within 3% = steady state
+X2_WINDOW = (1.7, 2.3)  # crates/loractl-bench/src/lib.rs:39-115: 2x the iterations takes 2x the time
+X2_TRIES = 4
+
+
+def event_timer(run, n):
+    """GPU milliseconds of ``run(n)`` bracketed by events on the current
+    stream, with a device synchronize on both sides."""
+    import torch
+
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    run(n)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1)
+
+
+def warm_and_time(run, steps, warmup):
+    """The timing protocol: ``warmup`` untimed iterations, then more until
+    the GPU is in steady state (at least WARM_MIN_MS of work and two
+    consecutive ``steps``-iteration windows within WARM_AGREE), then ``steps``
+    timed iterations and ``2 * steps`` for the sanity ratio, re-timed until
+    the ratio lands in X2_WINDOW. Returns (ms for ``steps``, ratio, warm ms)."""
+    run(warmup)
+    warm_ms, prev = 0.0, None
+    while True:
+        cur = event_timer(run, steps)
+        warm_ms += cur
+        if warm_ms >= WARM_MIN_MS and prev is not None and abs(cur - prev) <= WARM_AGREE * prev:
+            break
+        if warm_ms >= WARM_MAX_MS:
+            break
+        prev = cur
+    for _ in range(X2_TRIES):
+        ms = event_timer(run, steps)
+        ratio = event_timer(run, 2 * steps) / ms
+        if X2_WINDOW[0] <= ratio <= X2_WINDOW[1]:
+            return ms, ratio, warm_ms
+    raise RuntimeError(f"timing never settled: 2x-iteration ratio {ratio:.3f} outside {X2_WINDOW} "
+                       f"after {X2_TRIES} tries")
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -114,6 +162,9 @@ def main():
     wt = torch.from_numpy(w).to(dev)
     wq = D.quantize_int4(wt, group) if fmt == "int4" else D.quantize_fp8(wt, True)
     del wt
+    # the interchange (row) layout, for the CPU baseline: the first fused
+    # call re-lays the weight into the blocked layout in place
+    wq_rows = (wq.data.cpu().numpy(), wq.scales.cpu().numpy()) if not args.no_cpu_baseline else None
     xb = torch.from_numpy(x).to(dev).to(torch.bfloat16)
     ab = torch.from_numpy(a).to(dev).to(torch.bfloat16)
     bb = torch.from_numpy(b).to(dev).to(torch.bfloat16)
@@ -129,28 +180,18 @@ def main():
         D.lora_fwd(xb, wq, ab, bb, s, y=y, t=t)
         D.lora_bwd(xb, dyb, wq, ab, bb, s, t, out=(dx, da, db))
 
-    for _ in range(args.warmup):
-        step()
+    def run(n):
+        for _ in range(n):
+            step()
+
+    run(1)
     torch.cuda.synchronize()
     for v in (y, dx, da, db):
         if not torch.isfinite(v).all() or not v.abs().max() > 0:
             raise RuntimeError("implausible output (all-zero or non-finite)")
 
-    def timed(n):
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        e0.record()
-        for _ in range(n):
-            step()
-        e1.record()
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1)
-
-    ms_total = timed(args.steps)
+    ms_total, ratio, warm_ms = warm_and_time(run, args.steps, args.warmup)
     ms_step = ms_total / args.steps
-    # sanity of the protocol (crates/loractl-bench/src/lib.rs:39-115): 2x iterations ~ 2x time
-    ratio = timed(2 * args.steps) / ms_total
     F = flops_step(M, K, N, r)
     value = F / (ms_step * 1e-3) / 1e12
 
@@ -184,7 +225,7 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(wq, x, a, b, dy, M, K, N, r, s, group, fmt, args.cpu_seconds)
+        cpu = cpu_baseline(wq_rows, x, a, b, dy, M, K, N, r, s, group, fmt, args.cpu_seconds)
 
     out = {
         "metric": f"{fmt}-base LoRA linear fwd+bwd TFLOP/s",
@@ -208,14 +249,22 @@ def main():
         "pct_of_mfma_peak": round(100.0 * value / PEAK_BF16_TFLOPS, 2),
         "flops_per_step": F,
         "sanity_x2_ratio": round(ratio, 3),
+        "warm_ms": round(warm_ms, 1),
         "kernels_us": {k: round(v["avg_us"], 2) for k, v in kernels.items()},
         "roofline": roofline,
         "cpu_baseline": cpu,
     }
+    if args.workload == "ns" and not args.no_skinny:
+        # the north star's second bar, the few-token forward of the same layer
+        out["skinny"] = skinny_measure(args, dev, with_cpu=not args.no_cpu_baseline)
     print(json.dumps(out), flush=True)
 
 
-def bench_skinny(args, dev):
+def skinny_measure(args, dev, with_cpu=True, steps=100):
+    """The few-token forward of the north-star layer (M=16): GB/s with the
+    packed weight rotated past the Infinity Cache and ``steps`` forwards
+    replayed from a HIP graph; per-kernel times from the library's events;
+    the roofline of the dominant kernel; the CPU baseline when asked."""
     import math
 
     import torch
@@ -223,10 +272,11 @@ def bench_skinny(args, dev):
     from loractl_amd import _lib as L
     from loractl_amd import device as D
 
-    M, K, N, r, alpha, fmt, group = WORKLOADS[args.workload]
+    M, K, N, r, alpha, fmt, group = WORKLOADS["skinny"]
     s = alpha / r
     w, x, a, b, _ = make_inputs(M, K, N, r)
     wq = D.quantize_int4(torch.from_numpy(w).to(dev), group)
+    wq_rows = (wq.data.cpu().numpy(), wq.scales.cpu().numpy()) if with_cpu else None
     wb = D.compute_weight(wq)
     # the row section of the blocked layout, the part the few-token kernel
     # reads: half the data (the transposed section follows) and the first
@@ -246,39 +296,32 @@ def bench_skinny(args, dev):
     def fwd(i):
         D.lora_fwd(xb, copies[i % ncopy], ab, bb, s, y=y, t=t)
 
-    for i in range(args.warmup):
+    for i in range(ncopy):
         fwd(i)
     torch.cuda.synchronize()
     if not torch.isfinite(y).all() or not y.abs().max() > 0:
         raise RuntimeError("implausible output (all-zero or non-finite)")
-    # one graph of `steps` forwards over the rotating copies
-    n_graph = args.steps
+    # one graph of `steps` forwards over the rotating copies, captured on a
+    # side stream whose context was sized before the capture
+    n_graph = steps
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.stream(stream):
-        fwd(0)  # bind the library to the capture stream before capturing
+        D.reserve(M, N, K, r)
+        fwd(0)
         torch.cuda.synchronize()
         with torch.cuda.graph(graph, stream=stream):
             for i in range(n_graph):
                 fwd(i)
     torch.cuda.synchronize()
 
-    def timed(reps):
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        e0.record()
+    def run(reps):
         for _ in range(reps):
             graph.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1)
 
-    timed(2)
-    ms_total = timed(4)
+    ms_total, ratio, warm_ms = warm_and_time(run, 4, 2)
     ms_fwd = ms_total / (4 * n_graph)
-    ratio = timed(8) / ms_total
     wb_alg = N * K / 2 + 4 * N * K / group  # W_B (packed int4 + f32 group scales)
     bytes_fwd = wb_alg + 2 * M * K + 2 * M * N + 4 * r * (K + N)
     value = bytes_fwd / (ms_fwd * 1e-3) / 1e9
@@ -286,7 +329,7 @@ def bench_skinny(args, dev):
     D.profile_reset()
     D.profile_enable(True)
     torch.cuda._sleep(GPU_SPIN_CYCLES)
-    for i in range(args.steps):
+    for i in range(steps):
         fwd(i)
     torch.cuda.synchronize()
     prof = D.profile_read()
@@ -304,39 +347,54 @@ def bench_skinny(args, dev):
         "peak": PEAK_HBM_GBS,
         "unit": "GB/s",
         "frac": round(achieved / PEAK_HBM_GBS, 4),
-        "traffic": load_traffic("fwd_main", args.workload),
+        "traffic": load_traffic("fwd_main", "skinny"),
         "bytes_per_launch": k_bytes,
         "avg_launch_us": round(kernels["fwd_main"], 3),
     }
     cpu = None
-    if not args.no_cpu_baseline:
-        cpu = cpu_baseline_fwd(wq, x, a, b, M, K, N, r, s, group, args.cpu_seconds, bytes_fwd)
-    out = {
+    if with_cpu:
+        cpu = cpu_baseline_fwd(wq_rows, x, a, b, M, K, N, r, s, group, args.cpu_seconds, bytes_fwd)
+    return {
         "metric": "int4-base LoRA linear skinny-M forward GB/s",
         "value": round(value, 1),
+        "unit": "GB/s",
+        "us_per_forward": round(ms_fwd * 1e3, 3),
+        "pct_of_hbm_peak": round(100.0 * value / PEAK_HBM_GBS, 2),
+        "bytes_per_forward": bytes_fwd,
+        "sanity_x2_ratio": round(ratio, 3),
+        "workload": f"int4-g{group} frozen Linear {K}->{N} + LoRA r={r} alpha={alpha:g}, M={M} tokens, "
+                    f"forward (y, t); packed weight rotated over {ncopy} copies "
+                    f"({ncopy * wbytes / 2**20:.0f} MiB), {n_graph} forwards replayed from a HIP graph",
+        "kernels_us": {k: round(v, 3) for k, v in kernels.items()},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+
+
+def bench_skinny(args, dev):
+    M, K, N, r, alpha, fmt, group = WORKLOADS["skinny"]
+    m = skinny_measure(args, dev, with_cpu=not args.no_cpu_baseline, steps=args.steps)
+    out = {
+        "metric": m["metric"],
+        "value": m["value"],
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_fwd, 5),
+        "ms_per_step": round(m["us_per_forward"] * 1e-3, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (seeded PCG64; W~N(0,0.02) quantized on device, X~N(0,1), A~U(+-1/sqrt(K)), B~N(0,1e-3))",
-        "config": {
-            "workload": f"int4-g{group} frozen Linear {K}->{N} + LoRA r={r} alpha={alpha:g}, M={M} tokens, "
-                        f"forward (y, t); packed weight rotated over {ncopy} copies "
-                        f"({ncopy * wbytes / 2**20:.0f} MiB), forwards replayed from a HIP graph",
-            "M": M, "K": K, "N": N, "rank": r, "group": group, "format": fmt,
-            "parallelism": "single-gpu",
-        },
-        "pct_of_hbm_peak": round(100.0 * value / PEAK_HBM_GBS, 2),
-        "bytes_per_step": bytes_fwd,
-        "sanity_x2_ratio": round(ratio, 3),
-        "kernels_us": {k: round(v, 3) for k, v in kernels.items()},
-        "roofline": roofline,
-        "cpu_baseline": cpu,
+        "config": {"workload": m["workload"], "M": M, "K": K, "N": N, "rank": r, "group": group, "format": fmt,
+                   "parallelism": "single-gpu"},
+        "pct_of_hbm_peak": m["pct_of_hbm_peak"],
+        "bytes_per_step": m["bytes_per_forward"],
+        "sanity_x2_ratio": m["sanity_x2_ratio"],
+        "kernels_us": m["kernels_us"],
+        "roofline": m["roofline"],
+        "cpu_baseline": m["cpu_baseline"],
     }
     print(json.dumps(out), flush=True)
 
@@ -419,12 +477,13 @@ def bench_requant(args, dev):
     }), flush=True)
 
 
-def cpu_baseline_fwd(wq, x, a, b, M, K, N, r, s, group, budget_s, bytes_fwd):
+def cpu_baseline_fwd(wq_rows, x, a, b, M, K, N, r, s, group, budget_s, bytes_fwd):
     """The reference's CPU forward (f32 dequant of the whole weight, f32
-    GEMMs) on the whole few-token workload, on this host's cores."""
+    GEMMs) on the whole few-token workload, on this host's cores;
+    ``wq_rows`` is the (packed, scales) row layout."""
     import oracle as O
 
-    st = O.CpuFwdInt4(wq.data.cpu().numpy(), wq.scales.cpu().numpy(), group, x, a, b, s)
+    st = O.CpuFwdInt4(wq_rows[0], wq_rows[1], group, x, a, b, s)
     t0 = time.perf_counter()
     threads = st.run()
     first = time.perf_counter() - t0
@@ -443,35 +502,35 @@ def cpu_baseline_fwd(wq, x, a, b, M, K, N, r, s, group, budget_s, bytes_fwd):
     }
 
 
-def cpu_baseline(wq, x, a, b, dy, M, K, N, r, s, group, fmt, budget_s):
-    """The reference's CPU algorithm (f32 dequant of the whole weight, f32
-    GEMMs) on the first m_s tokens of the same layer, on this host's cores."""
-    import numpy as np
-
+def cpu_baseline(wq_rows, x, a, b, dy, M, K, N, r, s, group, fmt, budget_s):
+    """The reference's CPU algorithm (burn-ndarray, f32) on the whole step of
+    the same layer, on this host's cores: int4 dequantizes the whole weight
+    to f32 on every forward and every backward (quant.rs:232, :250), fp8 is
+    an f32 weight decoded once at load (fp8.rs:306-318, kept Plain); then
+    the f32 GEMMs of the forward and backward in numpy's cache-blocked SGEMM.
+    Steps are repeated for about ``budget_s`` seconds."""
     import oracle as O
 
-    if fmt != "int4":
-        return None
-    packed = wq.data.cpu().numpy()
-    scales = wq.scales.cpu().numpy()
-    m_s = 64
-    st = O.CpuStepInt4(packed, scales, group, x[:m_s], a, b, s, dy[:m_s])
-    t0 = time.perf_counter()
-    threads = st.run()  # warmup (first touch of the work buffers)
-    first = time.perf_counter() - t0
-    reps = max(1, int(budget_s / max(first, 1e-3)))
-    t0 = time.perf_counter()
-    for _ in range(reps):
+    if fmt == "int4":
+        st = O.CpuStepInt4(wq_rows[0], wq_rows[1], group, x, a, b, s, dy)
+        what = "f32 dequant of the full weight per forward and per backward (OpenMP), then f32 GEMMs"
+    else:
+        st = O.CpuStepF32(O.fp8_dequant(wq_rows[0], wq_rows[1]), x, a, b, s, dy)
+        what = "f32 weight decoded once at load, f32 GEMMs"
+    st.run()  # first touch of the work buffers
+    reps, t0 = 0, time.perf_counter()
+    while reps == 0 or time.perf_counter() - t0 < budget_s:
         st.run()
+        reps += 1
     dt = (time.perf_counter() - t0) / reps
-    F = flops_step(m_s, K, N, r)
+    F = flops_step(M, K, N, r)
     return {
         "value": round(F / dt / 1e12, 5),
         "unit": "TFLOP/s",
-        "cores": int(threads),
+        "cores": O.blas_threads(),
         "kind": "port",
-        "sample": f"{m_s} of {M} tokens of the same {K}->{N} r={r} int4-g{group} layer, fwd+bwd, {reps} reps "
-                  f"of {dt:.3f} s (f32 dequant of the full weight twice per step + f32 GEMMs, OpenMP)",
+        "sample": f"the whole step (M={M}, {K}->{N} r={r} {fmt}{'-g' + str(group) if fmt == 'int4' else ''}), fwd+bwd, "
+                  f"{reps} steps of {dt:.3f} s: {what} in {O.blas_info()}",
     }
 
 

@@ -28,7 +28,9 @@
  *     src/quant.rs:76-80), never a silent fallback.
  *   - A context belongs to one host thread at a time; distinct contexts may
  *     be used concurrently. Hot calls allocate only when the context's
- *     workspace must grow (pre-size it with lrq_reserve).
+ *     workspace must grow (pre-size it with lrq_reserve); while the stream
+ *     is being captured into a graph they return LRQ_EINVAL instead of
+ *     growing it.
  *
  * Weight layouts (file layout [d_out = n, d_in = k], as QuantLinear keeps it,
  * src/mmdit.rs:413-444):

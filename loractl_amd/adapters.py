@@ -26,7 +26,8 @@ import torch
 
 from . import device as D
 from .lora import LoraDelta, quant_lora_linear
-from .quant import QuantBackend, concat_chunks
+from .quant import (DEFAULT_DEQUANT_CHUNK_MIB, QUANT_BLOCK, QuantBackend, QuantValue, concat_chunks,
+                    quantize_linear_weight_chunked)
 
 
 @dataclass
@@ -90,25 +91,29 @@ def build_adapters(sites: Sequence[LoraSite], cfg: LoraConfig, device=None) -> L
 
 
 class QuantLinear:
-    """Frozen quantized linear: packed row chunks in file layout [d_out, d_in]."""
+    """Frozen quantized linear (src/mmdit.rs:413-444): the reference keeps a
+    ``Vec`` of packed row chunks in file layout ``[rows_i, d_in]``,
+    concatenated along d_out. The chunks are joined once into one weight in
+    the blocked layout the fused kernels read, and only that is kept (the
+    row-layout chunks are released, so the weight holds 2x its packed bytes:
+    the blocked row and transposed sections); ``chunk_rows`` records the
+    chunking."""
 
     def __init__(self, weight: List[D.PackedWeight], bias: Optional[torch.Tensor] = None):
         if not weight:
             raise ValueError("QuantLinear holds at least one chunk")
-        self.weight = list(weight)
+        self.chunk_rows = [c.n for c in weight]
+        joined = weight[0] if len(weight) == 1 else concat_chunks(list(weight))
+        self._joined = D.compute_weight(joined)
         self.bias = bias
-        if len(self.weight) == 1:
-            self._joined = D.compute_weight(self.weight[0])
-        else:
-            self._joined = D.block(concat_chunks(self.weight))
 
     @property
     def d_in(self) -> int:
-        return self.weight[0].k
+        return self._joined.k
 
     @property
     def d_out(self) -> int:
-        return sum(c.n for c in self.weight)
+        return self._joined.n
 
     @property
     def packed(self) -> D.PackedWeight:
@@ -116,7 +121,7 @@ class QuantLinear:
 
     def dequantized_weight(self) -> torch.Tensor:
         """Diagnostics only: the full f32 [d_out, d_in] weight."""
-        return torch.cat([D.dequant(c) for c in self.weight], 0)
+        return D.dequant(self._joined)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         lead = x.shape[:-1]
@@ -139,6 +144,34 @@ class PlainLinear:
 
 
 BaseLinear = (PlainLinear, QuantLinear)
+
+
+def quantize_field(base, value: QuantValue = QuantValue.Q4S, chunk_bytes: int = DEFAULT_DEQUANT_CHUNK_MIB << 20,
+                   group: int = QUANT_BLOCK):
+    """One base site quantized (src/mmdit.rs:1266-1280): a ``PlainLinear``
+    whose burn-layout ``[d_in, d_out]`` weight is block-aligned becomes a
+    ``QuantLinear`` (the weight transposed to file layout ``[d_out, d_in]``,
+    then quantized as row chunks under ``chunk_bytes``; the bias is kept); a
+    ``QuantLinear``, or a ``PlainLinear`` whose ``d_in`` is not a multiple of
+    the reference's quant block (32), is returned unchanged. So is one whose
+    ``d_out`` is not a multiple of 8, which the fused kernels cannot write:
+    it runs as the reference's Plain arm. A caller-chosen ``group`` that does
+    not divide an aligned ``d_in`` raises, as the reference's quantizer panics
+    (src/quant.rs:76-80)."""
+    if not isinstance(base, PlainLinear):
+        return base
+    d_in, d_out = base.weight.shape
+    if d_in % QUANT_BLOCK != 0 or d_out % 8 != 0:
+        return base
+    chunks = quantize_linear_weight_chunked(base.weight.t().contiguous(), value, chunk_bytes, group)
+    return QuantLinear(chunks, base.bias)
+
+
+def into_quantized(sites: dict, value: QuantValue = QuantValue.Q4S,
+                   chunk_bytes: int = DEFAULT_DEQUANT_CHUNK_MIB << 20, group: int = QUANT_BLOCK) -> dict:
+    """``Mmdit::into_quantized_chunked`` (src/mmdit.rs:1134-1158) over a
+    ``{site path: base}`` map: every base through ``quantize_field``."""
+    return {path: quantize_field(b, value, chunk_bytes, group) for path, b in sites.items()}
 
 
 def site(adapters: Optional[LoraAdapters], path: str, base, x: torch.Tensor) -> torch.Tensor:

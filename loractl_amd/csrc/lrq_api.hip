@@ -121,8 +121,18 @@ struct Slab {
 
 int ensure_ws(lrq_ctx* c, size_t bytes) {
   if (c->ws && bytes <= c->ws_bytes) return LRQ_OK;
+  // growing the workspace synchronizes the stream and allocates, neither of
+  // which a stream under graph capture allows: refuse instead
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(c->stream, &cap);
+  if (e != hipSuccess) return hip_fail(c, e, "hipStreamIsCapturing");
+  if (cap != hipStreamCaptureStatusNone)
+    return fail(c, LRQ_EINVAL,
+                "the workspace must grow to %zu bytes (has %zu) while the stream is being captured: call "
+                "lrq_reserve for this shape before capturing",
+                bytes, c->ws_bytes);
   // stream-ordered users of the old buffer must finish before it goes
-  hipError_t e = hipStreamSynchronize(c->stream);
+  e = hipStreamSynchronize(c->stream);
   if (e != hipSuccess) return hip_fail(c, e, "hipStreamSynchronize");
   if (c->ws) (void)hipFree(c->ws);
   c->ws = nullptr;

@@ -11,20 +11,26 @@ from __future__ import annotations
 
 import ctypes
 import threading
-from dataclasses import dataclass, field
+from dataclasses import dataclass
 from typing import Optional
 
 import torch
 
 from . import _lib as L
 
-_tls = threading.local()
-
-
 class Context:
-    """One lrq_ctx per (thread, device); follows torch's current stream."""
+    """One lrq_ctx per (device, stream), shared by every thread that runs on
+    that stream.
 
-    def __init__(self, device: int):
+    The library's workspace (split partials, t and u, the LoRA reductions)
+    is ordered by the context's stream. Keying contexts by stream means two
+    streams never share a workspace, and autograd's backward, which runs on
+    the forward's stream but on another thread, finds the same context (and
+    the workspace ``reserve`` sized). A lock serialises the host side of the
+    calls of one context (argument checks, the error message, the
+    workspace's growth)."""
+
+    def __init__(self, device: int, stream: int):
         self.lib = L.load()
         h = ctypes.c_void_p()
         rc = self.lib.lrq_create(device, ctypes.byref(h))
@@ -32,6 +38,9 @@ class Context:
             raise L.LrqError(rc, f"lrq_create(device={device}) failed")
         self.h = h
         self.device = device
+        self.stream = stream
+        self.lock = threading.RLock()
+        self.call("lrq_set_stream", ctypes.c_void_p(stream))
 
     def __del__(self):
         try:
@@ -45,21 +54,27 @@ class Context:
             msg = self.lib.lrq_last_error(self.h).decode(errors="replace")
             raise L.LrqError(rc, f"{what}: {msg}")
 
-    def bind_stream(self):
-        s = torch.cuda.current_stream(self.device).cuda_stream
-        self.check(self.lib.lrq_set_stream(self.h, ctypes.c_void_p(s)), "lrq_set_stream")
+    def call(self, name: str, *args):
+        """Call ``name(ctx, *args)`` under the context's lock; raise on error."""
+        with self.lock:
+            self.check(getattr(self.lib, name)(self.h, *args), name)
+
+
+_ctx_lock = threading.Lock()
+_ctxs: dict = {}
 
 
 def context(device: Optional[int] = None) -> Context:
+    """The context of ``device`` (default: the current one) and torch's
+    current stream on it."""
     if device is None:
         device = torch.cuda.current_device()
-    ctxs = getattr(_tls, "ctxs", None)
-    if ctxs is None:
-        ctxs = _tls.ctxs = {}
-    c = ctxs.get(device)
-    if c is None:
-        c = ctxs[device] = Context(device)
-    c.bind_stream()
+    stream = torch.cuda.current_stream(device).cuda_stream
+    key = (device, stream)
+    with _ctx_lock:
+        c = _ctxs.get(key)
+        if c is None:
+            c = _ctxs[key] = Context(device, stream)
     return c
 
 
@@ -96,7 +111,6 @@ class PackedWeight:
     per_channel: bool = False
     bias: Optional[torch.Tensor] = None
     layout: int = L.LRQ_LAYOUT_ROWS
-    _blocked: Optional["PackedWeight"] = field(default=None, repr=False, compare=False)
 
     def desc(self) -> L.LrqWeight:
         return L.LrqWeight(
@@ -120,20 +134,20 @@ class PackedWeight:
         return self.layout == L.LRQ_LAYOUT_BLOCKED
 
     def with_bias(self, bias: Optional[torch.Tensor]) -> "PackedWeight":
-        w = PackedWeight(self.fmt, self.n, self.k, self.data, self.scales, self.group,
-                         self.per_channel, bias, self.layout)
-        if self._blocked is not None:
-            w._blocked = self._blocked.with_bias(bias)
-        return w
+        return PackedWeight(self.fmt, self.n, self.k, self.data, self.scales, self.group,
+                            self.per_channel, bias, self.layout)
 
 
 def compute_weight(w: PackedWeight) -> PackedWeight:
-    """The blocked form the fused kernels read (made once per weight and cached)."""
-    if w.blocked:
-        return w
-    if w._blocked is None:
-        w._blocked = block(w)
-    return w._blocked
+    """The blocked form the fused kernels read. A row-layout weight is re-laid
+    in place, once: ``w`` then holds the blocked data and scales, and its
+    row-layout tensors are released, so a frozen weight occupies 2x its
+    packed bytes (the row and transposed sections), not 3x. ``dequant`` reads
+    either layout."""
+    if not w.blocked:
+        b = block(w)
+        w.data, w.scales, w.layout = b.data, b.scales, b.layout
+    return w
 
 
 # ------------------------------------------------------------------ formats
@@ -153,7 +167,7 @@ def block(w: PackedWeight) -> PackedWeight:
     else:
         scales = w.scales
     d = w.desc()
-    ctx.check(ctx.lib.lrq_weight_block(ctx.h, ctypes.byref(d), _ptr(data), _ptr(scales)), "lrq_weight_block")
+    ctx.call("lrq_weight_block", ctypes.byref(d), _ptr(data), _ptr(scales))
     return PackedWeight(w.fmt, w.n, w.k, data, scales, w.group, w.per_channel, w.bias, L.LRQ_LAYOUT_BLOCKED)
 
 
@@ -164,8 +178,7 @@ def quantize_int4(w: torch.Tensor, group: int) -> PackedWeight:
     ctx = context(w.device.index)
     packed = torch.empty((n, k // 2), dtype=torch.uint8, device=w.device)
     scales = torch.empty((n, max(k // group, 0) if group > 0 else 0), dtype=torch.float32, device=w.device)
-    ctx.check(ctx.lib.lrq_quantize_int4(ctx.h, _ptr(w), n, k, group, _ptr(packed), _ptr(scales)),
-              "lrq_quantize_int4")
+    ctx.call("lrq_quantize_int4", _ptr(w), n, k, group, _ptr(packed), _ptr(scales))
     return PackedWeight(L.LRQ_FMT_INT4, n, k, packed, scales, group=group)
 
 
@@ -181,8 +194,8 @@ def requantize_fp8_int4(w: PackedWeight, group: int) -> PackedWeight:
     ctx = context(w.data.device.index)
     packed = torch.empty((n, k // 2), dtype=torch.uint8, device=w.data.device)
     scales = torch.empty((n, max(k // group, 0) if group > 0 else 0), dtype=torch.float32, device=w.data.device)
-    ctx.check(ctx.lib.lrq_requantize_fp8_int4(ctx.h, _ptr(w.data), _ptr(w.scales), int(w.per_channel), n, k, group,
-                                              _ptr(packed), _ptr(scales)), "lrq_requantize_fp8_int4")
+    ctx.call("lrq_requantize_fp8_int4", _ptr(w.data), _ptr(w.scales), int(w.per_channel), n, k, group,
+             _ptr(packed), _ptr(scales))
     return PackedWeight(L.LRQ_FMT_INT4, n, k, packed, scales, group=group, bias=w.bias)
 
 
@@ -193,8 +206,7 @@ def quantize_fp8(w: torch.Tensor, per_channel: bool) -> PackedWeight:
     ctx = context(w.device.index)
     data = torch.empty((n, k), dtype=torch.uint8, device=w.device)
     scales = torch.empty((n if per_channel else 1,), dtype=torch.float32, device=w.device)
-    ctx.check(ctx.lib.lrq_quantize_fp8(ctx.h, _ptr(w), n, k, int(per_channel), _ptr(data), _ptr(scales)),
-              "lrq_quantize_fp8")
+    ctx.call("lrq_quantize_fp8", _ptr(w), n, k, int(per_channel), _ptr(data), _ptr(scales))
     return PackedWeight(L.LRQ_FMT_FP8, n, k, data, scales, per_channel=per_channel)
 
 
@@ -203,7 +215,7 @@ def dequant(w: PackedWeight) -> torch.Tensor:
     ctx = context(w.device.index)
     out = torch.empty((w.n, w.k), dtype=torch.float32, device=w.device)
     d = w.desc()
-    ctx.check(ctx.lib.lrq_dequant(ctx.h, ctypes.byref(d), _ptr(out)), "lrq_dequant")
+    ctx.call("lrq_dequant", ctypes.byref(d), _ptr(out))
     return out
 
 
@@ -212,7 +224,7 @@ def dequant_bf16(w: PackedWeight) -> torch.Tensor:
     ctx = context(w.device.index)
     out = torch.empty((w.n, w.k), dtype=torch.bfloat16, device=w.device)
     d = w.desc()
-    ctx.check(ctx.lib.lrq_dequant_bf16(ctx.h, ctypes.byref(d), _ptr(out)), "lrq_dequant_bf16")
+    ctx.call("lrq_dequant_bf16", ctypes.byref(d), _ptr(out))
     return out
 
 
@@ -226,7 +238,7 @@ def quant_matmul_t(x: torch.Tensor, w: PackedWeight) -> torch.Tensor:
     ctx = context(x.device.index)
     y = torch.empty((m, w.n), dtype=torch.bfloat16, device=x.device)
     d = compute_weight(w).desc()
-    ctx.check(ctx.lib.lrq_quant_matmul_t(ctx.h, ctypes.byref(d), _ptr(x), m, _ptr(y)), "lrq_quant_matmul_t")
+    ctx.call("lrq_quant_matmul_t", ctypes.byref(d), _ptr(x), m, _ptr(y))
     return y
 
 
@@ -239,8 +251,7 @@ def quant_matmul_t_bwd(dy: torch.Tensor, w: PackedWeight) -> torch.Tensor:
     ctx = context(dy.device.index)
     dx = torch.empty((m, w.k), dtype=torch.bfloat16, device=dy.device)
     d = compute_weight(w).desc()
-    ctx.check(ctx.lib.lrq_quant_matmul_t_bwd(ctx.h, ctypes.byref(d), _ptr(dy), m, _ptr(dx)),
-              "lrq_quant_matmul_t_bwd")
+    ctx.call("lrq_quant_matmul_t_bwd", ctypes.byref(d), _ptr(dy), m, _ptr(dx))
     return dx
 
 
@@ -258,8 +269,7 @@ def lora_fwd(x: torch.Tensor, w: PackedWeight, a: torch.Tensor, b: torch.Tensor,
     if t is None:
         t = torch.empty((m, r), dtype=torch.bfloat16, device=x.device)
     d = compute_weight(w).desc()
-    ctx.check(ctx.lib.lrq_lora_fwd(ctx.h, ctypes.byref(d), _ptr(x), m, _ptr(a), _ptr(b), r,
-                                   float(scaling), _ptr(y), _ptr(t)), "lrq_lora_fwd")
+    ctx.call("lrq_lora_fwd", ctypes.byref(d), _ptr(x), m, _ptr(a), _ptr(b), r, float(scaling), _ptr(y), _ptr(t))
     return y, t
 
 
@@ -282,20 +292,20 @@ def lora_bwd(x: torch.Tensor, dy: torch.Tensor, w: PackedWeight, a: torch.Tensor
         da = torch.empty((w.k, r), dtype=torch.float32, device=dy.device) if need_da else None
         db = torch.empty((r, w.n), dtype=torch.float32, device=dy.device) if need_db else None
     d = compute_weight(w).desc()
-    ctx.check(ctx.lib.lrq_lora_bwd(ctx.h, ctypes.byref(d), _ptr(x), _ptr(dy), m, _ptr(a), _ptr(b), r,
-                                   float(scaling), _ptr(t), _ptr(dx), _ptr(da), _ptr(db)), "lrq_lora_bwd")
+    ctx.call("lrq_lora_bwd", ctypes.byref(d), _ptr(x), _ptr(dy), m, _ptr(a), _ptr(b), r, float(scaling),
+             _ptr(t), _ptr(dx), _ptr(da), _ptr(db))
     return dx, da, db
 
 
 # ------------------------------------------------------------------ profiling
 def profile_enable(on: bool, device: Optional[int] = None):
     ctx = context(device)
-    ctx.check(ctx.lib.lrq_profile_enable(ctx.h, int(on)), "lrq_profile_enable")
+    ctx.call("lrq_profile_enable", int(on))
 
 
 def profile_reset(device: Optional[int] = None):
     ctx = context(device)
-    ctx.check(ctx.lib.lrq_profile_reset(ctx.h), "lrq_profile_reset")
+    ctx.call("lrq_profile_reset")
 
 
 def profile_read(device: Optional[int] = None) -> dict:
@@ -305,11 +315,11 @@ def profile_read(device: Optional[int] = None) -> dict:
     for kid in range(ctx.lib.lrq_profile_count()):
         ms = ctypes.c_double()
         n = ctypes.c_int64()
-        ctx.check(ctx.lib.lrq_profile_read(ctx.h, kid, ctypes.byref(ms), ctypes.byref(n)), "lrq_profile_read")
+        ctx.call("lrq_profile_read", kid, ctypes.byref(ms), ctypes.byref(n))
         out[ctx.lib.lrq_profile_name(kid).decode()] = (ms.value, n.value)
     return out
 
 
 def reserve(m: int, n: int, k: int, r: int, device: Optional[int] = None):
     ctx = context(device)
-    ctx.check(ctx.lib.lrq_reserve(ctx.h, m, n, k, r), "lrq_reserve")
+    ctx.call("lrq_reserve", m, n, k, r)

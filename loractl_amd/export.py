@@ -4,21 +4,28 @@ layouts and checks as the reference, so a file written here loads there and
 back.
 
 - keys: ``lora_<path with '.' -> '_'>.lora_down.weight`` = A^T [r, d_in],
-  ``.lora_up.weight`` = B^T [d_out, r], ``.alpha`` = scaling * rank (a
-  scalar), all F32;
+  ``.lora_up.weight`` = B^T [d_out, r], ``.alpha`` = scaling * rank as a
+  ``[1]`` tensor (src/export.rs:204-209), all F32;
 - import checks, in the reference's order and with its messages: a missing
   tensor, a non-F32 tensor, a non-finite value (a corrupt adapter), a shape
   that does not match the configured deltas (a changed rank), an alpha that
   differs from the configured scaling * rank by more than 1e-3.
 
-The safetensors metadata given is written as is; the sd-webui hashes the
-reference adds (src/export.rs:330-345) are not computed here.
+With metadata, the file also carries the two sd-webui-additional-networks
+hashes the reference adds (src/export.rs:211-252, :330-345):
+``sshs_model_hash`` = SHA-256 of the tensor-data region and
+``sshs_legacy_hash`` = the first 8 hex digits of the SHA-256 of the 64 KiB
+at byte 0x100000, both over a serialization whose header holds only the
+``ss_*`` metadata. Without metadata no header is written (the reference's
+``None`` path, which keeps exports byte-stable).
 """
 
 from __future__ import annotations
 
+import hashlib
 import math
-from typing import Dict, Optional
+import struct
+from typing import Dict, Optional, Tuple
 
 import torch
 
@@ -34,10 +41,23 @@ def kohya_keys(path: str):
     return f"{p}.lora_down.weight", f"{p}.lora_up.weight", f"{p}.alpha"
 
 
-def export_adapters(adapters: LoraAdapters, path: str, metadata: Optional[Dict[str, str]] = None) -> None:
-    """Write every delta of ``adapters`` as kohya tensors (src/export.rs:297-355)."""
-    from safetensors.torch import save_file
+LEGACY_OFFSET = 0x100000
+LEGACY_LEN = 0x10000
 
+
+def sd_webui_hashes(buf: bytes) -> Tuple[str, str]:
+    """(model hash, legacy hash) of a serialized safetensors buffer
+    (src/export.rs:211-252): SHA-256 of everything past the length-prefixed
+    JSON header, and the first 8 hex digits of the SHA-256 of the 64 KiB at
+    offset 0x100000 (an empty read for a smaller buffer)."""
+    (n,) = struct.unpack("<Q", buf[:8])
+    model = hashlib.sha256(buf[min(n + 8, len(buf)):]).hexdigest()
+    legacy = hashlib.sha256(buf[LEGACY_OFFSET:LEGACY_OFFSET + LEGACY_LEN] if len(buf) > LEGACY_OFFSET else b"")
+    return model, legacy.hexdigest()[:8]
+
+
+def kohya_tensors(adapters: LoraAdapters) -> Dict[str, torch.Tensor]:
+    """The kohya tensors of every delta (src/export.rs:297-326)."""
     out = {}
     for delta, target in zip(adapters.deltas, adapters.targets):
         down, up, alpha = kohya_keys(target)
@@ -45,8 +65,25 @@ def export_adapters(adapters: LoraAdapters, path: str, metadata: Optional[Dict[s
         b = delta.lora_b.detach().float().cpu()  # [r, d_out]
         out[down] = a.t().contiguous()
         out[up] = b.t().contiguous()
-        out[alpha] = torch.tensor(float(delta.scaling * a.shape[1]), dtype=torch.float32)
-    save_file(out, path, metadata=dict(metadata) if metadata else None)
+        # alpha = scaling * rank, computed in f64 and stored as an f32 [1]
+        out[alpha] = torch.tensor([float(delta.scaling) * a.shape[1]], dtype=torch.float32)
+    return out
+
+
+def export_adapters(adapters: LoraAdapters, path: str, metadata: Optional[Dict[str, str]] = None) -> None:
+    """Write every delta of ``adapters`` as kohya tensors (src/export.rs:297-355),
+    with ``metadata`` plus the sd-webui hash pair in the header when given."""
+    from safetensors.torch import save, save_file
+
+    out = kohya_tensors(adapters)
+    header = None
+    if metadata:
+        ss = {k: str(v) for k, v in metadata.items() if k.startswith("ss_")}
+        model_hash, legacy_hash = sd_webui_hashes(save(out, metadata=ss or None))
+        header = {k: str(v) for k, v in metadata.items()}
+        header["sshs_model_hash"] = model_hash
+        header["sshs_legacy_hash"] = legacy_hash
+    save_file(out, path, metadata=header)
 
 
 def import_adapters(adapters: LoraAdapters, path: str) -> int:

@@ -31,6 +31,7 @@ import torch
 
 from . import device as D
 from . import fp8 as F
+from .quant import DEFAULT_DEQUANT_CHUNK_MIB, QUANT_BLOCK
 
 # src/fp8.rs:368-384
 PASSTHROUGH_DTYPES = ("F64", "F32", "F16", "BF16", "I64", "I32", "I16", "I8", "U64", "U32", "U8", "BOOL")
@@ -111,17 +112,36 @@ def classify_fp8_checkpoint(path: str) -> Fp8Checkpoint:
     return ck
 
 
+def fused_aligned(d_out: int, d_in: int) -> bool:
+    """Whether a ``[d_out, d_in]`` base can be quantized and fed to the fused
+    kernels: ``d_in`` a multiple of the reference's quant block (32; a site
+    that is not stays Plain, src/mmdit.rs:1266-1280) and ``d_out`` a multiple
+    of 8 (the fused kernels write 16-byte output runs)."""
+    return d_in % QUANT_BLOCK == 0 and d_out % 8 == 0
+
+
+def _check_group(name: str, d_in: int, group: int):
+    if group < QUANT_BLOCK or group & (group - 1):
+        raise ValueError(f"quant block {group} must be a power of two >= {QUANT_BLOCK}")
+    if d_in % group != 0:
+        raise ValueError(
+            f"'{name}': input dim {d_in} is a multiple of {QUANT_BLOCK} but not of the chosen quant block "
+            f"{group}; use a block that divides it (the reference's is {QUANT_BLOCK})")
+
+
 def load_fp8_checkpoint(path: str, device: Union[str, torch.device], quant: Optional[str] = None,
-                        group: int = 64) -> Dict[str, Union[D.PackedWeight, torch.Tensor]]:
+                        group: int = QUANT_BLOCK) -> Dict[str, Union[D.PackedWeight, torch.Tensor]]:
     """Load a scaled-fp8 checkpoint onto ``device``.
 
     Each 2-D fp8 weight becomes a ``PackedWeight``: e4m3fn as stored
-    (``quant=None``) or int4 at Q4S with ``group`` (``quant="int4"``),
-    re-quantized on the device from the bytes. A weight whose input dim is
-    not a multiple of 32 (or, for int4, of the group) cannot feed the fused
-    kernels and comes back as its f32 values, as the reference keeps such
-    sites plain (src/mmdit.rs:1266-1280). Pass-through tensors keep their
-    dtype; dropped keys are absent."""
+    (``quant=None``) or int4 at Q4S with ``group`` (``quant="int4"``; the
+    reference's load pass always uses QUANT_BLOCK = 32), re-quantized on the
+    device from the bytes. A weight whose input dim is not a multiple of 32
+    stays plain, as the reference keeps such sites (src/mmdit.rs:1266-1280),
+    and so does one whose output dim is not a multiple of 8, which the fused
+    kernels cannot write: both come back as their f32 values. A caller-chosen
+    group that does not divide an aligned weight's input dim raises.
+    Pass-through tensors keep their dtype; dropped keys are absent."""
     if quant not in (None, "int4"):
         raise ValueError(f"quant must be None or 'int4', got {quant!r}")
     ck = classify_fp8_checkpoint(path)
@@ -133,7 +153,9 @@ def load_fp8_checkpoint(path: str, device: Union[str, torch.device], quant: Opti
         for name in sorted(ck.fp8):
             data = f.get_tensor(name).view(torch.uint8).to(device)
             scale = f.get_tensor(f"{name}_scale").to(device)
-            aligned = data.dim() == 2 and data.shape[1] % 32 == 0 and (quant is None or data.shape[1] % group == 0)
+            aligned = data.dim() == 2 and fused_aligned(data.shape[0], data.shape[1])
+            if aligned and quant == "int4":
+                _check_group(name, data.shape[1], group)
             if not aligned:
                 vals = data.view(torch.float8_e4m3fn).float()
                 out[name] = vals * (scale.reshape(-1, *([1] * (vals.dim() - 1))) if ck.fp8[name] else scale.reshape(()))
@@ -143,3 +165,92 @@ def load_fp8_checkpoint(path: str, device: Union[str, torch.device], quant: Opti
         for name in ck.plain:
             out[name] = f.get_tensor(name).to(device)
     return out
+
+
+def is_fp8_checkpoint(path: str) -> bool:
+    """Header-only probe: does any tensor carry F8_E4M3 (src/fp8.rs:74-84)?"""
+    return any(dt == "F8_E4M3" for dt, _ in _header(path).values())
+
+
+@dataclass
+class QuantLoadReport:
+    """The quant pass's accounting (src/diffusion_trainer.rs:1212-1240)."""
+
+    quantized: int = 0
+    left_plain: int = 0
+    chunked_sites: int = 0
+    total_chunks: int = 0
+    plain_sites: List[str] = field(default_factory=list)
+
+
+def load_quant_checkpoint(path: str, device: Union[str, torch.device], base_paths: List[str],
+                          group: int = QUANT_BLOCK, chunk_bytes: int = DEFAULT_DEQUANT_CHUNK_MIB << 20):
+    """The quant pass of ``load_quant_module`` (src/diffusion_trainer.rs:1094-1267)
+    for a plain (bf16/f32/f16) or scaled-fp8 safetensors checkpoint, on the
+    device: for each frozen-base site in ``base_paths`` (in order), its
+    ``<path>.weight`` (file layout ``[d_out, d_in]``) is read, moved to the
+    device, widened to f32 and quantized to int4 at Q4S as the row chunks
+    ``dequant_chunk_rows`` prescribes, one tensor at a time; the f32 copy is
+    dropped before the next site. fp8 checkpoints (detected from the header)
+    go through ``load_fp8_checkpoint``'s device requantization instead, with
+    no f32 copy. A site whose weight is not block-aligned (``fused_aligned``)
+    is left plain: its weight stays in the returned rest, as the reference
+    leaves it to the applier. A site missing from the checkpoint raises.
+
+    Returns ``(quantized, rest, report)``: ``{path: QuantLinear}`` (with the
+    site's ``<path>.bias`` as its bias when present), every other tensor by
+    key (dropped fp8 keys absent), and the accounting."""
+    from safetensors import safe_open
+
+    from .adapters import QuantLinear
+    from .quant import QuantValue, quantize_linear_weight_chunked
+
+    device = torch.device(device)
+    report = QuantLoadReport()
+    quantized = {}
+    fp8 = is_fp8_checkpoint(path)
+    if fp8:
+        rest = load_fp8_checkpoint(path, device, quant="int4", group=group)
+        keys = set(rest)
+    else:
+        keys = set(_header(path))
+        rest = {}
+    with safe_open(path, framework="pt") as f:
+        for p in base_paths:
+            wkey = f"{p}.weight"
+            if wkey not in keys:
+                raise ValueError(f"quantized base site {p} has no {wkey} in the checkpoint {path}")
+            if fp8:
+                w = rest[wkey]
+                if not isinstance(w, D.PackedWeight):  # left plain (unaligned)
+                    report.left_plain += 1
+                    report.plain_sites.append(p)
+                    continue
+                del rest[wkey]
+                chunks = [w]
+            else:
+                t = f.get_tensor(wkey)
+                if t.dim() != 2 or not fused_aligned(t.shape[0], t.shape[1]):
+                    report.left_plain += 1
+                    report.plain_sites.append(p)
+                    continue
+                _check_group(wkey, t.shape[1], group)
+                w32 = t.to(device).float()
+                del t
+                chunks = quantize_linear_weight_chunked(w32, QuantValue.Q4S, chunk_bytes, group)
+                del w32
+            if len(chunks) > 1:
+                report.chunked_sites += 1
+                report.total_chunks += len(chunks)
+            bkey = f"{p}.bias"
+            bias = None
+            if bkey in keys:
+                bias = rest.pop(bkey) if fp8 else f.get_tensor(bkey).to(device)
+                bias = bias.float()
+            quantized[p] = QuantLinear(chunks, bias)
+            report.quantized += 1
+        if not fp8:
+            taken = {f"{p}.weight" for p in quantized} | {f"{p}.bias" for p in quantized}
+            for k in sorted(keys - taken):
+                rest[k] = f.get_tensor(k).to(device)
+    return quantized, rest, report

@@ -69,12 +69,8 @@ def lib():
         vp = ctypes.c_void_p
         L.lrq_o_linear_fwd.argtypes = [vp, vp, vp, vp, vp, ctypes.c_double, _i64, _i64, _i64, _i64, vp, vp]
         L.lrq_o_linear_bwd.argtypes = [vp, vp, vp, vp, ctypes.c_double, vp, _i64, _i64, _i64, _i64, vp, vp, vp]
-        L.lrq_o_cpu_step_int4.restype = ctypes.c_int
-        L.lrq_o_cpu_step_int4.argtypes = [vp, vp, _i64, vp, vp, vp, ctypes.c_float, vp,
-                                          _i64, _i64, _i64, _i64, vp, vp, vp, vp, vp, vp, vp]
-        L.lrq_o_cpu_fwd_int4.restype = ctypes.c_int
-        L.lrq_o_cpu_fwd_int4.argtypes = [vp, vp, _i64, vp, vp, vp, ctypes.c_float,
-                                         _i64, _i64, _i64, _i64, vp, vp, vp]
+        L.lrq_o_cpu_dequant_int4.restype = ctypes.c_int
+        L.lrq_o_cpu_dequant_int4.argtypes = [vp, vp, _i64, _i64, _i64, vp]
         _lib = L
     return _lib
 
@@ -246,8 +242,38 @@ def cosine(a, b) -> float:
 
 
 # ---------------------------------------------------------------- cpu baseline
+def blas_info() -> str:
+    """The BLAS numpy's f32 GEMMs run on, and its thread count."""
+    try:
+        import threadpoolctl
+
+        for d in threadpoolctl.threadpool_info():
+            if d.get("user_api") == "blas":
+                return f"{d.get('internal_api')} {d.get('version')} ({d.get('architecture')}), " \
+                       f"{d.get('num_threads')} threads"
+    except Exception:  # noqa: BLE001 - informational only
+        pass
+    return "numpy BLAS"
+
+
+def blas_threads() -> int:
+    try:
+        import threadpoolctl
+
+        for d in threadpoolctl.threadpool_info():
+            if d.get("user_api") == "blas":
+                return int(d.get("num_threads") or 1)
+    except Exception:  # noqa: BLE001 - informational only
+        pass
+    return 1
+
+
 class CpuFwdInt4:
-    """The reference CPU algorithm (f32 dequant + f32 GEMMs) over one forward."""
+    """The reference's CPU forward in f32, burn-ndarray's way
+    (quant.rs:175-176, :232-233; lora.rs:199-203): dequantize the whole
+    weight to an f32 [N, K] (lrq_o_cpu_dequant_int4, OpenMP), then f32 GEMMs
+    Y = X Wdq^T, T = s X A, Y += T B in numpy's cache-blocked SGEMM (the
+    stand-in for burn-ndarray's matrixmultiply/gemm crates)."""
 
     def __init__(self, packed, scales, group, X, A, B, s):
         self.packed = _c(packed, np.uint8)
@@ -256,46 +282,57 @@ class CpuFwdInt4:
         self.X = _c(X, np.float32)
         self.A = _c(A, np.float32)
         self.B = _c(B, np.float32)
-        self.s = float(s)
+        self.s = np.float32(s)
         self.M, self.K = self.X.shape
         self.N = self.B.shape[1]
-        self.r = self.A.shape[1]
         self.Wdq = np.empty((self.N, self.K), np.float32)
-        self.T = np.empty((self.M, self.r), np.float32)
-        self.Y = np.empty((self.M, self.N), np.float32)
+
+    def dequant(self) -> int:
+        return lib().lrq_o_cpu_dequant_int4(_ptr(self.packed), _ptr(self.scales), self.g, self.N, self.K,
+                                            _ptr(self.Wdq))
 
     def run(self) -> int:
-        return lib().lrq_o_cpu_fwd_int4(
-            _ptr(self.packed), _ptr(self.scales), self.g, _ptr(self.X), _ptr(self.A), _ptr(self.B),
-            self.s, self.M, self.N, self.K, self.r, _ptr(self.Wdq), _ptr(self.T), _ptr(self.Y))
+        """One forward; returns the threads of the dequant (the GEMMs use
+        ``blas_threads()``)."""
+        th = self.dequant()
+        self.Y = self.X @ self.Wdq.T
+        self.T = (self.X @ self.A) * self.s
+        self.Y += self.T @ self.B
+        return th
 
 
-class CpuStepInt4:
-    """The reference CPU algorithm (f32 dequant + f32 GEMMs) over one fwd+bwd."""
+class CpuStepInt4(CpuFwdInt4):
+    """One forward + backward, the reference's CPU way: the forward above,
+    then a second f32 dequant of the whole weight (the reference's backward
+    re-dequantizes, quant.rs:250-251) and the f32 GEMMs dX = dY Wdq,
+    U = s dY B^T, dX += U A^T, dA = X^T U, dB = T^T dY (the autodiff of the
+    two LoRA Linears)."""
 
     def __init__(self, packed, scales, group, X, A, B, s, dY):
-        self.packed = _c(packed, np.uint8)
-        self.scales = _c(scales, np.float32)
-        self.g = group
-        self.X = _c(X, np.float32)
-        self.A = _c(A, np.float32)
-        self.B = _c(B, np.float32)
-        self.s = float(s)
+        super().__init__(packed, scales, group, X, A, B, s)
         self.dY = _c(dY, np.float32)
-        self.M, self.K = self.X.shape
-        self.N = self.dY.shape[1]
-        self.r = self.A.shape[1]
-        M, N, K, r = self.M, self.N, self.K, self.r
-        self.Wdq = np.empty((N, K), np.float32)
-        self.T = np.empty((M, r), np.float32)
-        self.U = np.empty((M, r), np.float32)
-        self.Y = np.empty((M, N), np.float32)
-        self.dX = np.empty((M, K), np.float32)
-        self.dA = np.empty((K, r), np.float32)
-        self.dB = np.empty((r, N), np.float32)
 
     def run(self) -> int:
-        return lib().lrq_o_cpu_step_int4(
-            _ptr(self.packed), _ptr(self.scales), self.g, _ptr(self.X), _ptr(self.A), _ptr(self.B),
-            self.s, _ptr(self.dY), self.M, self.N, self.K, self.r, _ptr(self.Wdq), _ptr(self.T),
-            _ptr(self.U), _ptr(self.Y), _ptr(self.dX), _ptr(self.dA), _ptr(self.dB))
+        th = super().run()
+        self.dequant()
+        self.dX = self.dY @ self.Wdq
+        self.U = (self.dY @ self.B.T) * self.s
+        self.dX += self.U @ self.A.T
+        self.dA = self.X.T @ self.U
+        self.dB = self.T.T @ self.dY
+        return th
+
+
+class CpuStepF32(CpuStepInt4):
+    """One forward + backward over a Plain f32 weight [N, K] (an fp8
+    checkpoint decoded once at load, fp8.rs:306-318, and kept full
+    precision): the same f32 GEMMs, no per-pass dequantization."""
+
+    def __init__(self, W, X, A, B, s, dY):
+        W = _c(W, np.float32)
+        N, K = W.shape
+        super().__init__(np.zeros((N, K // 2), np.uint8), np.zeros((N, 1), np.float32), K, X, A, B, s, dY)
+        self.Wdq = W
+
+    def dequant(self) -> int:
+        return 1

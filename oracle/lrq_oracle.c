@@ -30,8 +30,9 @@
  *     finite-difference gradients on tiny shapes.
  *
  * Numbers: f32 storage, f64 accumulation for the parity oracle; the
- * cpu_baseline functions (lrq_o_cpu_*) follow the reference's own CPU
- * algorithm: materialize the f32 dequantized weight, then f32 GEMMs.
+ * cpu_baseline dequant (lrq_o_cpu_dequant_int4) follows the reference's own
+ * CPU algorithm: materialize the f32 dequantized weight, then f32 GEMMs
+ * (those run in numpy's cache-blocked SGEMM; oracle/__init__.py).
  */
 #include <math.h>
 #include <stdint.h>
@@ -337,135 +338,28 @@ EXPORT void lrq_o_linear_bwd(const float* X, const float* Wdq, const float* A, c
 
 /* ------------------------------------------------------------------ */
 /* CPU baseline: the reference's own CPU algorithm in f32               */
-/* (dequantize the whole weight to f32, then f32 GEMMs; quant.rs:232-233,*/
-/* quant.rs:250-251; LoRA as two f32 Linears and their autodiff).        */
+/* (dequantize the whole weight to f32 on every forward and every        */
+/* backward, quant.rs:232-233, quant.rs:250-251). The f32 GEMMs around it */
+/* run in numpy's cache-blocked SGEMM (oracle/__init__.py, CpuStepInt4).  */
 /* ------------------------------------------------------------------ */
 
-/* C[M,N] (+)= A[M,K] * B[N,K]^T, f32, OpenMP over rows, K-contiguous dots */
-static void sgemm_nt(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K,
-                     int accumulate) {
-#pragma omp parallel for schedule(static)
-  for (int64_t m = 0; m < M; ++m) {
-    const float* a = A + m * K;
-    for (int64_t n0 = 0; n0 < N; n0 += 4) {
-      float acc[4] = {0, 0, 0, 0};
-      int64_t nn = (N - n0 < 4) ? N - n0 : 4;
-      for (int64_t q = 0; q < nn; ++q) {
-        const float* b = B + (n0 + q) * K;
-        float s = 0.0f;
-#pragma omp simd reduction(+ : s)
-        for (int64_t k = 0; k < K; ++k) s += a[k] * b[k];
-        acc[q] = s;
-      }
-      for (int64_t q = 0; q < nn; ++q) C[m * N + n0 + q] = accumulate ? C[m * N + n0 + q] + acc[q] : acc[q];
-    }
-  }
-}
-
-/* C[M,N] (+)= A[M,K] * B[K,N], f32, OpenMP over rows, N-contiguous axpy */
-static void sgemm_nn(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K,
-                     int accumulate) {
-#pragma omp parallel for schedule(static)
-  for (int64_t m = 0; m < M; ++m) {
-    float* c = C + m * N;
-    if (!accumulate) memset(c, 0, sizeof(float) * (size_t)N);
-    for (int64_t k = 0; k < K; ++k) {
-      float a = A[m * K + k];
-      const float* b = B + k * N;
-#pragma omp simd
-      for (int64_t n = 0; n < N; ++n) c[n] += a * b[n];
-    }
-  }
-}
-
-/* C[K,N] = A[M,K]^T * B[M,N] (reduction over M), f32 */
-static void sgemm_tn(const float* A, const float* B, float* C, int64_t M, int64_t K, int64_t N) {
-#pragma omp parallel for schedule(static)
-  for (int64_t k = 0; k < K; ++k) {
-    float* c = C + k * N;
-    memset(c, 0, sizeof(float) * (size_t)N);
-    for (int64_t m = 0; m < M; ++m) {
-      float a = A[m * K + k];
-      const float* b = B + m * N;
-#pragma omp simd
-      for (int64_t n = 0; n < N; ++n) c[n] += a * b[n];
-    }
-  }
-}
-
-/*
- * The forward alone, the reference CPU way (quant.rs:175-176 with the LoRA
- * term of lora.rs:199-203): materialize Wdq f32 [N,K], Y = X Wdq^T,
- * T = s X A, Y += T B. Work buffers Wdq [N*K], T [M*r], Y [M*N].
- * Returns the number of threads used.
- */
-EXPORT int lrq_o_cpu_fwd_int4(const uint8_t* packed, const float* scales, int64_t g,
-                              const float* X, const float* A, const float* B, float s,
-                              int64_t M, int64_t N, int64_t K, int64_t r,
-                              float* Wdq, float* T, float* Y) {
+/* Wdq[N,K] = q * scale in f32 from the packed row layout, OpenMP over rows.
+ * Returns the number of threads used. */
+EXPORT int lrq_o_cpu_dequant_int4(const uint8_t* packed, const float* scales, int64_t g, int64_t N, int64_t K,
+                                  float* Wdq) {
 #pragma omp parallel for schedule(static)
   for (int64_t n = 0; n < N; ++n) {
     const int64_t nb = K / g;
-    for (int64_t k = 0; k < K; ++k) {
-      uint8_t b = packed[n * (K / 2) + k / 2];
-      int q = (int)((k & 1) ? (b >> 4) : (b & 0xF)) - 8;
-      Wdq[n * K + k] = (float)q * scales[n * nb + k / g];
+    const uint8_t* row = packed + n * (K / 2);
+    const float* sc = scales + n * nb;
+    float* out = Wdq + n * K;
+    for (int64_t k = 0; k < K; k += 2) {
+      const uint8_t b = row[k / 2];
+      const float s = sc[k / g];
+      out[k] = (float)((int)(b & 0xF) - 8) * s;
+      out[k + 1] = (float)((int)(b >> 4) - 8) * s;
     }
   }
-  sgemm_nt(X, Wdq, Y, M, N, K, 0);
-  sgemm_nn(X, A, T, M, r, K, 0);
-  for (int64_t i = 0; i < M * r; ++i) T[i] *= s;
-  sgemm_nn(T, B, Y, M, N, r, 1);
-#ifdef _OPENMP
-  return omp_get_max_threads();
-#else
-  return 1;
-#endif
-}
-
-/*
- * One forward+backward of the int4 LoRA linear, the reference CPU way:
- * materialize Wdq f32 [N,K] (every pass, as quant.rs does), f32 GEMMs for the
- * base and the four LoRA products. X, dY [M,*] f32; A [K,r], B [r,N].
- * Work buffers are caller-provided: Wdq [N*K], T,U [M*r], Y [M*N], dX [M*K],
- * dA [K*r], dB [r*N]. Returns the number of threads used.
- */
-EXPORT int lrq_o_cpu_step_int4(const uint8_t* packed, const float* scales, int64_t g,
-                               const float* X, const float* A, const float* B, float s,
-                               const float* dY, int64_t M, int64_t N, int64_t K, int64_t r,
-                               float* Wdq, float* T, float* U, float* Y, float* dX, float* dA,
-                               float* dB) {
-  /* forward: dequant -> Y = X Wdq^T ; T = s X A ; Y += T B */
-#pragma omp parallel for schedule(static)
-  for (int64_t n = 0; n < N; ++n) {
-    const int64_t nb = K / g;
-    for (int64_t k = 0; k < K; ++k) {
-      uint8_t b = packed[n * (K / 2) + k / 2];
-      int q = (int)((k & 1) ? (b >> 4) : (b & 0xF)) - 8;
-      Wdq[n * K + k] = (float)q * scales[n * nb + k / g];
-    }
-  }
-  sgemm_nt(X, Wdq, Y, M, N, K, 0);
-  sgemm_nn(X, A, T, M, r, K, 0);
-  for (int64_t i = 0; i < M * r; ++i) T[i] *= s;
-  sgemm_nn(T, B, Y, M, N, r, 1);
-  /* backward: dequant again (the reference re-dequantizes in backward) */
-#pragma omp parallel for schedule(static)
-  for (int64_t n = 0; n < N; ++n) {
-    const int64_t nb = K / g;
-    for (int64_t k = 0; k < K; ++k) {
-      uint8_t b = packed[n * (K / 2) + k / 2];
-      int q = (int)((k & 1) ? (b >> 4) : (b & 0xF)) - 8;
-      Wdq[n * K + k] = (float)q * scales[n * nb + k / g];
-    }
-  }
-  sgemm_nn(dY, Wdq, dX, M, K, N, 0);      /* dX = dY Wdq */
-  sgemm_nt(dY, B, U, M, r, N, 0);         /* U = dY B^T  */
-  for (int64_t i = 0; i < M * r; ++i) U[i] *= s;
-  /* dX += U A^T : A^T rows are A columns -> use nt with B=A viewed [K,r] */
-  sgemm_nt(U, A, dX, M, K, r, 1);
-  sgemm_tn(X, U, dA, M, K, r);            /* dA = X^T U */
-  sgemm_tn(T, dY, dB, M, r, N);           /* dB = T^T dY */
 #ifdef _OPENMP
   return omp_get_max_threads();
 #else

@@ -98,3 +98,77 @@ def test_load_fp8_checkpoint_end_to_end(cuda, tmp_path):
     y4 = D.quant_matmul_t(xb, q4["blk.w.weight"])
     check("y fp8", y8, O.linear_fwd(xr, wd)[0])
     check("y int4", y4, O.linear_fwd(xr, O.dequant_int4(p_ref, s_ref, k, 64))[0])
+
+
+def test_fp8_load_default_block_and_alignment(cuda, tmp_path):
+    """The load pass's default block is the reference's QUANT_BLOCK = 32, so a
+    d_in of 96 quantizes; a caller-chosen block that does not divide it
+    raises; a d_out the fused kernels cannot write (60) stays plain f32."""
+    b96, s96 = _fp8_case(64, 96, True, seed=6)
+    b60, s60 = _fp8_case(60, 128, False, seed=7)
+    path = str(tmp_path / "ck.safetensors")
+    save_file({"a.weight": torch.from_numpy(b96).view(torch.float8_e4m3fn), "a.weight_scale": torch.from_numpy(s96),
+               "b.weight": torch.from_numpy(b60).view(torch.float8_e4m3fn),
+               "b.weight_scale": torch.from_numpy(s60.reshape(()))}, path)
+    q = load_fp8_checkpoint(path, cuda, quant="int4")
+    p_ref, s_ref = O.quantize_int4_packed(O.fp8_dequant(b96, s96), 32)
+    assert q["a.weight"].group == 32
+    assert np.array_equal(q["a.weight"].data.cpu().numpy(), p_ref)
+    assert np.array_equal(q["a.weight"].scales.cpu().numpy(), s_ref)
+    assert isinstance(q["b.weight"], torch.Tensor)
+    assert np.array_equal(q["b.weight"].cpu().numpy(), O.fp8_dequant(b60, s60))
+    with pytest.raises(ValueError, match="not of the chosen quant block 64"):
+        load_fp8_checkpoint(path, cuda, quant="int4", group=64)
+
+
+def test_load_quant_checkpoint_plain(cuda, tmp_path):
+    """Quantize-on-load for a plain checkpoint (src/diffusion_trainer.rs:1143-1169):
+    each aligned base site is quantized on the device, bit-exact with the
+    oracle's Q4S of its f32 values (bf16 and f32 files), in row chunks when
+    the f32 size passes the threshold (the same bytes as whole); unaligned
+    sites stay in the rest; a missing site raises."""
+    from loractl_amd.load import load_quant_checkpoint
+
+    rng = np.random.Generator(np.random.PCG64(21))
+    w_a = (rng.standard_normal((96, 128)) * 0.02).astype(np.float32)      # f32, aligned
+    w_b = (rng.standard_normal((40, 64)) * 0.02).astype(np.float32)       # bf16 file, aligned
+    w_c = (rng.standard_normal((24, 20)) * 0.02).astype(np.float32)       # d_in 20: stays plain
+    bias = np.linspace(-1, 1, 96).astype(np.float32)
+    norm = np.ones(8, np.float32)
+    path = str(tmp_path / "plain.safetensors")
+    save_file({"s.a.weight": torch.from_numpy(w_a), "s.a.bias": torch.from_numpy(bias),
+               "s.b.weight": torch.from_numpy(w_b).to(torch.bfloat16), "s.c.weight": torch.from_numpy(w_c),
+               "norm.scale": torch.from_numpy(norm)}, path)
+    q, rest, rep = load_quant_checkpoint(path, cuda, ["s.a", "s.b", "s.c"], chunk_bytes=96 * 128 * 4 // 3)
+    assert (rep.quantized, rep.left_plain, rep.plain_sites) == (2, 1, ["s.c"])
+    assert (rep.chunked_sites, rep.total_chunks) == (1, 3) and q["s.a"].chunk_rows == [32, 32, 32]
+    assert sorted(rest) == ["norm.scale", "s.c.weight"]
+    wb32 = torch.from_numpy(w_b).to(torch.bfloat16).float().numpy()
+    for p_, w_ in (("s.a", w_a), ("s.b", wb32)):
+        pk, sc = O.quantize_int4_packed(w_, 32)
+        assert np.array_equal(q[p_].dequantized_weight().cpu().numpy(), O.dequant_int4(pk, sc, w_.shape[1], 32)), p_
+    assert torch.equal(q["s.a"].bias.cpu(), torch.from_numpy(bias)) and q["s.b"].bias is None
+    assert torch.equal(rest["s.c.weight"].cpu(), torch.from_numpy(w_c))
+    with pytest.raises(ValueError, match="quantized base site s.d has no s.d.weight"):
+        load_quant_checkpoint(path, cuda, ["s.a", "s.d"])
+
+
+def test_quantize_field_orientation(cuda):
+    """quantize_field (src/mmdit.rs:1266-1280): a burn-layout [d_in, d_out]
+    weight is transposed to file layout, then quantized; the forward equals
+    x . W with W the dequantized burn weight; unaligned d_in stays Plain."""
+    from loractl_amd.adapters import PlainLinear, QuantLinear, quantize_field
+
+    rng = np.random.Generator(np.random.PCG64(4))
+    wb = (rng.standard_normal((256, 72)) * 0.02).astype(np.float32)  # burn [d_in, d_out]
+    base = PlainLinear(torch.from_numpy(wb).to(cuda))
+    q = quantize_field(base)
+    assert isinstance(q, QuantLinear) and (q.d_in, q.d_out) == (256, 72)
+    pk, sc = O.quantize_int4_packed(np.ascontiguousarray(wb.T), 32)
+    wdq = O.dequant_int4(pk, sc, 256, 32)
+    assert np.array_equal(q.dequantized_weight().cpu().numpy(), wdq)
+    x = rng.standard_normal((33, 256), dtype=np.float32)
+    xb = to_dev(x, cuda)
+    check("y", q.forward(xb), O.linear_fwd(xb.float().cpu().numpy(), wdq)[0])
+    odd = PlainLinear(torch.zeros(48, 16, device=cuda))
+    assert quantize_field(odd) is odd

@@ -143,3 +143,19 @@ def test_gpu_kernels_are_built_for_gfx950_only():
     blob = open(_lib.LIB_PATH, "rb").read()
     assert b"gfx950" in blob
     assert b"gfx942" not in blob and b"sm_" not in blob[:0]
+
+
+def test_dropout_above_zero_is_refused():
+    """lora.rs:44-48 dropout is fused away on this path: p > 0 in training
+    raises before any device work (the block-checkpointed trainer refuses it
+    too, diffusion_trainer.rs:342-348); so does a rank above the kernels' 64."""
+    import torch
+
+    from loractl_amd.lora import LoraDelta, quant_lora_linear
+
+    d = LoraDelta(64, 32, 4, 4.0, dropout_prob=0.1)
+    with pytest.raises(ValueError, match="dropout 0 only"):
+        quant_lora_linear(torch.zeros(2, 64), None, d)
+    big = LoraDelta(64, 32, 65, 65.0)
+    with pytest.raises(ValueError, match="rank <= 64"):
+        quant_lora_linear(torch.zeros(2, 64), None, big)

@@ -108,3 +108,27 @@ def test_passthrough_keeps_every_mapped_dtype(tmp_path):
     p = write(tmp_path, {f"t{i}": torch.zeros(3, dtype=dt) for i, dt in enumerate(dts)})
     ck = classify_fp8_checkpoint(p)
     assert ck.plain == sorted(f"t{i}" for i in range(len(dts))) and not ck.fp8
+
+
+def test_quantize_field_keeps_unaligned_sites_plain():
+    """src/mmdit.rs:1266-1280: a Plain whose d_in is not a multiple of 32 is
+    left untouched (no device work), as is one whose d_out the fused kernels
+    cannot write; a quantized site passes through."""
+    from loractl_amd.adapters import PlainLinear, into_quantized, quantize_field
+    from loractl_amd.load import fused_aligned
+
+    odd_in = PlainLinear(torch.zeros(16, 64))    # burn [d_in=16, d_out=64]
+    odd_out = PlainLinear(torch.zeros(64, 60))   # d_out 60
+    assert quantize_field(odd_in) is odd_in and quantize_field(odd_out) is odd_out
+    assert into_quantized({"a": odd_in, "b": odd_out}) == {"a": odd_in, "b": odd_out}
+    assert fused_aligned(64, 96) and not fused_aligned(64, 80) and not fused_aligned(60, 96)
+
+
+def test_is_fp8_checkpoint(tmp_path):
+    from loractl_amd.load import is_fp8_checkpoint
+
+    p = write(tmp_path, {"a.weight": fp8([2, 2]), "a.weight_scale": torch.tensor(1.0)})
+    assert is_fp8_checkpoint(p)
+    q = str(tmp_path / "plain.safetensors")
+    save_file({"a.weight": torch.zeros(2, 2)}, q)
+    assert not is_fp8_checkpoint(q)

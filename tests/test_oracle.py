@@ -293,3 +293,22 @@ def test_cpu_baseline_forward_matches_oracle():
     st.run()
     Y, T = O.linear_fwd(X, O.dequant_int4(p, s, K, g), A, B, 0.5)
     assert O.rel_deviation(st.Y, Y) < 1e-5 and O.rel_deviation(st.T, T) < 1e-5
+
+
+def test_cpu_baseline_f32_step_matches_oracle():
+    """The fp8 CPU baseline (an f32 weight decoded once, f32 GEMMs) computes
+    the f64 oracle's fwd+bwd."""
+    rng = np.random.Generator(np.random.PCG64(4))
+    M, K, N, r = 48, 96, 64, 8
+    b8, s8 = O.fp8_quantize((rng.standard_normal((N, K)) * 0.02).astype(np.float32), True)
+    W = O.fp8_dequant(b8, s8)
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    A = rng.uniform(-0.1, 0.1, (K, r)).astype(np.float32)
+    B = (rng.standard_normal((r, N)) * 1e-2).astype(np.float32)
+    dY = rng.standard_normal((M, N)).astype(np.float32)
+    st = O.CpuStepF32(W, X, A, B, 2.0, dY)
+    st.run()
+    Y, T = O.linear_fwd(X, W, A, B, 2.0)
+    dX, dA, dB = O.linear_bwd(X, W, A, B, 2.0, dY)
+    for got, ref in ((st.Y, Y), (st.dX, dX), (st.dA, dA), (st.dB, dB), (st.T, T)):
+        assert O.rel_deviation(got, ref) < 1e-5
