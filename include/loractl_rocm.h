@@ -170,6 +170,23 @@ int lrq_lora_fwd(lrq_ctx* ctx, const lrq_weight* w, const uint16_t* x, int64_t m
                  const uint16_t* a, const uint16_t* b, int64_t r, float scaling, uint16_t* y,
                  uint16_t* t_out);
 
+/* Bytes of the fixed scratch array of lrq_lora_fwd_noalloc, per GPU. */
+#define LRQ_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/* lrq_lora_fwd without any allocation. No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Same
+ * arguments, kernels and results as lrq_lora_fwd; its workspace is a
+ * file-scope device array of LRQ_NOALLOC_SCRATCH_BYTES held by every GPU
+ * the library runs on until the process ends, so it calls no hipMalloc,
+ * hipFree or event creation. A shape whose forward needs more scratch than
+ * that returns LRQ_EINVAL. Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (two streams, two contexts, two threads)
+ * race and must be ordered by the caller. */
+int lrq_lora_fwd_noalloc(lrq_ctx* ctx, const lrq_weight* w, const uint16_t* x, int64_t m,
+                         const uint16_t* a, const uint16_t* b, int64_t r, float scaling, uint16_t* y,
+                         uint16_t* t_out);
+
 /* The fused site backward (gradients to x, A, B; none to the frozen weight):
  *   u  = scaling * dy . B^T
  *   dx = dy . dequant(w) + u . A^T          bf16 [m, k]

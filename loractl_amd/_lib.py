@@ -21,6 +21,7 @@ LRQ_FMT_INT4 = 1
 LRQ_FMT_FP8 = 2
 LRQ_LAYOUT_ROWS = 0
 LRQ_LAYOUT_BLOCKED = 1
+LRQ_NOALLOC_SCRATCH_BYTES = 32 << 20
 
 _ERRNAMES = {
     LRQ_EINVAL: "LRQ_EINVAL",
@@ -77,6 +78,7 @@ SIGNATURES = {
     "lrq_quant_matmul_t": (_i32, [_vp, _wp, _vp, _i64, _vp]),
     "lrq_quant_matmul_t_bwd": (_i32, [_vp, _wp, _vp, _i64, _vp]),
     "lrq_lora_fwd": (_i32, [_vp, _wp, _vp, _i64, _vp, _vp, _i64, _f32, _vp, _vp]),
+    "lrq_lora_fwd_noalloc": (_i32, [_vp, _wp, _vp, _i64, _vp, _vp, _i64, _f32, _vp, _vp]),
     "lrq_lora_bwd": (_i32, [_vp, _wp, _vp, _vp, _i64, _vp, _vp, _i64, _f32, _vp, _vp, _vp, _vp]),
     "lrq_profile_enable": (_i32, [_vp, _i32]),
     "lrq_profile_reset": (_i32, [_vp]),

@@ -8,6 +8,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <algorithm>
+#include <mutex>
 #include <new>
 #include <vector>
 
@@ -31,6 +32,27 @@ struct lrq_ctx {
   double total_ms[KID_COUNT] = {0};
   int64_t launches[KID_COUNT] = {0};
 };
+
+// The workspace of lrq_lora_fwd_noalloc: a file-scope device array, one
+// copy per GPU, held until the process ends. In host code its name is not a
+// device address; lrq_create looks up each device's copy once
+// (hipGetSymbolAddress, with that device current) and every later use goes
+// through that pointer.
+static __device__ __align__(256) char scratch[LRQ_NOALLOC_SCRATCH_BYTES];
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static char* g_scratch[kMaxDevices] = {};
+
+// Look up the current device's copy of `scratch` (once per device).
+static int init_scratch(int device) {
+  if (device < 0 || device >= kMaxDevices) return LRQ_EUNSUPPORTED;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch[device]) return LRQ_OK;
+  void* p = nullptr;
+  if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return LRQ_EHIP;
+  g_scratch[device] = static_cast<char*>(p);
+  return LRQ_OK;
+}
 
 namespace {
 
@@ -165,17 +187,20 @@ struct LoraWs {
   size_t bytes;
 };
 
-LoraWs lora_layout(char* base, int64_t m, int64_t n, int64_t k, int rp) {
+// fwd_only: the forward's slices alone (t, the B^T rows, t's partials and
+// the forward GEMM's split partials); u and the dA/dB partials take no bytes
+LoraWs lora_layout(char* base, int64_t m, int64_t n, int64_t k, int rp, bool fwd_only = false) {
   Slab s{base};
   LoraWs w{};
   w.tp = s.take<uint16_t>(m * rp);
-  w.up = s.take<uint16_t>(m * rp);
-  w.fr = s.take<uint16_t>(std::max(n, k) * rp);
-  const int64_t nt = std::max((int64_t)lora_plan_nt(m, k, rp).splits, (int64_t)lora_plan_nt(m, n, rp).splits);
+  w.up = s.take<uint16_t>(fwd_only ? 0 : m * rp);
+  w.fr = s.take<uint16_t>((fwd_only ? n : std::max(n, k)) * rp);
+  const int64_t nt = fwd_only ? lora_plan_nt(m, k, rp).splits
+                              : std::max((int64_t)lora_plan_nt(m, k, rp).splits, (int64_t)lora_plan_nt(m, n, rp).splits);
   w.pn = s.take<float>(std::max(nt * m * rp, (int64_t)1));
-  w.pa = s.take<float>((int64_t)lora_plan_tn(m, k, rp).splits * k * rp);
-  w.pb = s.take<float>((int64_t)lora_plan_tn(m, n, rp).splits * n * rp);
-  w.gp = s.take<float>(std::max(gemm_part_floats(m, n, k), (int64_t)1));
+  w.pa = s.take<float>(fwd_only ? 0 : (int64_t)lora_plan_tn(m, k, rp).splits * k * rp);
+  w.pb = s.take<float>(fwd_only ? 0 : (int64_t)lora_plan_tn(m, n, rp).splits * n * rp);
+  w.gp = s.take<float>(std::max(fwd_only ? gemm_split_floats(m, n, k) : gemm_part_floats(m, n, k), (int64_t)1));
   w.bytes = s.off;
   return w;
 }
@@ -252,6 +277,11 @@ int lrq_create(int device, lrq_ctx** out) {
     return LRQ_EHIP;
   }
   c->stream = nullptr;  // the null stream until lrq_set_stream says otherwise
+  const int rc = init_scratch(device);
+  if (rc != LRQ_OK) {
+    delete c;
+    return rc;
+  }
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, device) == hipSuccess) set_num_cus(prop.multiProcessorCount);
   *out = c;
@@ -430,8 +460,30 @@ static int check_gemm(lrq_ctx* c, const lrq_weight* w, int64_t m) {
   return LRQ_OK;
 }
 
+// Where the forward's workspace comes from: the context's (grown on demand)
+// or, for lrq_lora_fwd_noalloc, the device's static scratch array.
+struct WsSource {
+  bool scratch;
+  char* base;
+};
+
+static int acquire_ws(lrq_ctx* c, WsSource* src, size_t bytes, char** out) {
+  if (!src->scratch) {
+    LRQ_TRY(ensure_ws(c, bytes));
+    *out = c->ws;
+    return LRQ_OK;
+  }
+  if (bytes > (size_t)LRQ_NOALLOC_SCRATCH_BYTES)
+    return fail(c, LRQ_EINVAL,
+                "lrq_lora_fwd_noalloc: this shape needs %zu bytes of scratch, more than its fixed %zu; use "
+                "lrq_lora_fwd",
+                bytes, (size_t)LRQ_NOALLOC_SCRATCH_BYTES);
+  *out = src->base;
+  return LRQ_OK;
+}
+
 static int fwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t m, const uint16_t* a,
-                    const uint16_t* b, int64_t r, float scaling, uint16_t* y, uint16_t* t_out) {
+                    const uint16_t* b, int64_t r, float scaling, uint16_t* y, uint16_t* t_out, WsSource* src) {
   LRQ_TRY(begin(c));
   LRQ_TRY(check_gemm(c, w, m));
   if (!aligned16(x) || !aligned16(y)) return fail(c, LRQ_EINVAL, "x and y must be 16-byte aligned");
@@ -441,13 +493,14 @@ static int fwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t 
     if (r > 64) return fail(c, LRQ_EINVAL, "rank %lld outside [1, 64]", (long long)r);
     if (!aligned16(b)) return fail(c, LRQ_EINVAL, "B must be 16-byte aligned");
   }
+  char* ws = nullptr;
   if (m >= 1 && m <= 16) {
     // few tokens: stream the packed weight once (split-k partials, t's
     // partials alongside), then one epilogue launch
     const int rp = lora ? (int)round_up(r, 16) : 0;
     const SkinnyPlan p = skinny_plan(w->n, w->k, rp, get_num_cus());
-    LRQ_TRY(ensure_ws(c, skinny_ws_bytes(p, m, w->n, rp)));
-    float* part = reinterpret_cast<float*>(c->ws);
+    LRQ_TRY(acquire_ws(c, src, skinny_ws_bytes(p, m, w->n, rp), &ws));
+    float* part = reinterpret_cast<float*>(ws);
     float* tpart = part + round_up((int64_t)p.S * m * w->n, 64);
     if (lora) {
       ga.lw = b;
@@ -463,35 +516,36 @@ static int fwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t 
   if (lora) {
     const int rp = (int)round_up(r, 16);
     LRQ_TRY(check_lora_shapes(c, m, w->n, w->k, rp));
-    LRQ_TRY(ensure_ws(c, lora_layout(nullptr, m, w->n, w->k, rp).bytes));
-    LoraWs ws = lora_layout(c->ws, m, w->n, w->k, rp);
+    LRQ_TRY(acquire_ws(c, src, lora_layout(nullptr, m, w->n, w->k, rp, true).bytes, &ws));
+    LoraWs lw = lora_layout(ws, m, w->n, w->k, rp, true);
     // t = s . x . A   (bf16 [m, rp] for the fused step, [m, r] for the caller)
     const LoraPlan pt = lora_plan_nt(m, w->k, rp);
     LRQ_TRY(run(c, KID_LORA_T, "lora_t", [&] {
-      hipError_t e = launch_lora_nt(c->stream, x, a, false, r, (int)r, m, w->k, rp, pt, ws.pn);
+      hipError_t e = launch_lora_nt(c->stream, x, a, false, r, (int)r, m, w->k, rp, pt, lw.pn);
       if (e != hipSuccess) return e;
       // fp8: B^T divided by the weight scale (the GEMM scales base + LoRA)
       const bool f8 = w->format == LRQ_FMT_FP8;
-      return launch_nt_reduce(c->stream, ws.pn, pt.splits, m, rp, (int)r, scaling, ws.tp, t_out, b, w->n, false,
-                              ws.fr, f8 ? w->scales : nullptr, f8 && w->per_channel);
+      return launch_nt_reduce(c->stream, lw.pn, pt.splits, m, rp, (int)r, scaling, lw.tp, t_out, b, w->n, false,
+                              lw.fr, f8 ? w->scales : nullptr, f8 && w->per_channel);
     }));
-    ga.lact = ws.tp;
-    ga.lw = ws.fr;
+    ga.lact = lw.tp;
+    ga.lw = lw.fr;
     ga.r = (int)r;
     ga.rp = rp;
-    ga.part = ws.gp;
+    ga.part = lw.gp;
   } else {
     const int64_t pf = gemm_split_floats(m, w->n, w->k);
     if (pf > 0) {
-      LRQ_TRY(ensure_ws(c, (size_t)pf * 4));
-      ga.part = reinterpret_cast<float*>(c->ws);
+      LRQ_TRY(acquire_ws(c, src, (size_t)pf * 4, &ws));
+      ga.part = reinterpret_cast<float*>(ws);
     }
   }
   return run(c, KID_FWD_MAIN, "fwd_main", [&] { return launch_fwd(c->stream, w->format, ga); });
 }
 
 int lrq_quant_matmul_t(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t m, uint16_t* y) {
-  return fwd_impl(c, w, x, m, nullptr, nullptr, 0, 1.0f, y, nullptr);
+  WsSource src{false, nullptr};
+  return fwd_impl(c, w, x, m, nullptr, nullptr, 0, 1.0f, y, nullptr, &src);
 }
 
 int lrq_lora_fwd(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t m, const uint16_t* a,
@@ -500,7 +554,29 @@ int lrq_lora_fwd(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t m, 
     c->err[0] = 0;
     return fail(c, LRQ_EINVAL, "lrq_lora_fwd needs A, B and 1 <= r <= 64 (got r=%lld)", (long long)r);
   }
-  return fwd_impl(c, w, x, m, a, b, r, scaling, y, t_out);
+  WsSource src{false, nullptr};
+  return fwd_impl(c, w, x, m, a, b, r, scaling, y, t_out, &src);
+}
+
+int lrq_lora_fwd_noalloc(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t m, const uint16_t* a,
+                         const uint16_t* b, int64_t r, float scaling, uint16_t* y, uint16_t* t_out) {
+  if (!c) return LRQ_EINVAL;
+  c->err[0] = 0;
+  if (r < 1 || r > 64 || !a || !b)
+    return fail(c, LRQ_EINVAL, "lrq_lora_fwd_noalloc needs A, B and 1 <= r <= 64 (got r=%lld)", (long long)r);
+  char* base = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    base = (c->device >= 0 && c->device < kMaxDevices) ? g_scratch[c->device] : nullptr;
+  }
+  if (!base) return fail(c, LRQ_EHIP, "no scratch address for device %d", c->device);
+  WsSource src{true, base};
+  // no per-kernel event brackets: creating their events could allocate
+  const bool prof = c->prof;
+  c->prof = false;
+  const int rc = fwd_impl(c, w, x, m, a, b, r, scaling, y, t_out, &src);
+  c->prof = prof;
+  return rc;
 }
 
 // The input gradient: the few-token path for m <= 16 (partials at `skpart`),

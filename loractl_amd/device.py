@@ -273,6 +273,28 @@ def lora_fwd(x: torch.Tensor, w: PackedWeight, a: torch.Tensor, b: torch.Tensor,
     return y, t
 
 
+def lora_fwd_noalloc(x: torch.Tensor, w: PackedWeight, a: torch.Tensor, b: torch.Tensor, scaling: float,
+                     y: torch.Tensor, t: torch.Tensor):
+    """``lora_fwd`` through ``lrq_lora_fwd_noalloc``: the library allocates
+    nothing (its workspace is a fixed per-GPU scratch array); the caller
+    passes every output, and ``w`` must already be blocked. Calls that
+    overlap on one GPU race on that array."""
+    _need(x, torch.bfloat16, "x")
+    m = x.shape[0]
+    r = a.shape[1]
+    _need(a, torch.bfloat16, "A", (w.k, r))
+    _need(b, torch.bfloat16, "B", (r, w.n))
+    _need(y, torch.bfloat16, "y", (m, w.n))
+    _need(t, torch.bfloat16, "t", (m, r))
+    if not w.blocked:
+        raise ValueError("lora_fwd_noalloc takes a blocked weight (compute_weight) — blocking allocates")
+    ctx = context(x.device.index)
+    d = w.desc()
+    ctx.call("lrq_lora_fwd_noalloc", ctypes.byref(d), _ptr(x), m, _ptr(a), _ptr(b), r, float(scaling), _ptr(y),
+             _ptr(t))
+    return y, t
+
+
 def lora_bwd(x: torch.Tensor, dy: torch.Tensor, w: PackedWeight, a: torch.Tensor, b: torch.Tensor,
              scaling: float, t: torch.Tensor, need_dx: bool = True, need_da: bool = True,
              need_db: bool = True, out=None):
