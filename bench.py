@@ -46,7 +46,16 @@ WORKLOADS = {
     "c2": (4096, 3072, 12288, 32, 32.0, "fp8", 0),
     "skinny": (16, 3072, 12288, 32, 32.0, "int4", 64),  # forward only, HBM-bound
     "requant": (0, 3072, 12288, 0, 0.0, "fp8", 64),  # fp8 checkpoint tensor -> int4, load time
+    "c3": None,  # one synthetic MMDiT double-stream block's linear set (C3_SITES), image + text stream
+    "c5": None,  # a Qwen3-style 28-layer decoder's linears (C5_LAYER), M swept over C5_M
 }
+# C3: (d_in, d_out) of QKV, attn-out, MLP up, MLP down, adaLN-mod; int4 g64, r=32, alpha=32
+C3_SITES = [(3072, 9216), (3072, 3072), (3072, 12288), (12288, 3072), (3072, 18432)]
+C3_STREAMS = (("image", 4096), ("text", 512))
+# C5: q, k, v, o, gate, up, down of one layer; 28 layers; int4 g64, r=16, alpha=16
+C5_LAYER = [(2560, 4096), (2560, 1024), (2560, 1024), (4096, 2560), (2560, 9728), (2560, 9728), (9728, 2560)]
+C5_LAYERS = 28
+C5_M = (1, 16, 256, 2048)
 INFINITY_CACHE_BYTES = 256 << 20
 GPU_SPIN_CYCLES = 100_000_000  # ~50 ms: longer than the host needs to enqueue a profiled loop
 
@@ -156,6 +165,10 @@ def main():
         return bench_skinny(args, dev)
     if args.workload == "requant":
         return bench_requant(args, dev)
+    if args.workload == "c3":
+        return bench_c3(args, dev)
+    if args.workload == "c5":
+        return bench_c5(args, dev)
     M, K, N, r, alpha, fmt, group = WORKLOADS[args.workload]
     s = alpha / r
     w, x, a, b, dy = make_inputs(M, K, N, r)
@@ -474,6 +487,269 @@ def bench_requant(args, dev):
                      "traffic": load_traffic("quantize_int4", "requant"), "bytes_per_launch": nbytes,
                      "avg_launch_us": round(kernels["quantize_int4"], 3)},
         "cpu_baseline": cpu,
+    }), flush=True)
+
+
+class LinearSet:
+    """A set of fused int4 LoRA linear sites sharing one step: each site has
+    its own frozen weight (quantized on the device from seeded
+    W ~ N(0, 0.02), then blocked), LoRA factors and bf16 activations;
+    ``acts`` maps an activation key to x [M, K] / dy [M, N] buffers that
+    sites of the same shape may share. A step runs every site's forward
+    (y, t) then backward (dx, dA, dB)."""
+
+    def __init__(self, dev, sites, group=64, seed=0, keep_rows=0):
+        import torch
+
+        from loractl_amd import device as D
+
+        self.D = D
+        self.sites = []
+        self.rows = []
+        g = torch.Generator(device=dev).manual_seed(seed)
+        acts = {}
+        for i, (M, K, N, r, alpha) in enumerate(sites):
+            w = torch.randn(N, K, device=dev, generator=g) * 0.02
+            wq = D.quantize_int4(w, group)
+            if i < keep_rows:
+                self.rows.append((wq.data.cpu().numpy(), wq.scales.cpu().numpy()))
+            del w
+            D.compute_weight(wq)
+            key = (M, K, N)
+            if key not in acts:
+                x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+                dy = torch.randn(M, N, device=dev, generator=g).to(torch.bfloat16)
+                out = (torch.empty((M, N), dtype=torch.bfloat16, device=dev),
+                       torch.empty((M, r), dtype=torch.bfloat16, device=dev),
+                       torch.empty((M, K), dtype=torch.bfloat16, device=dev),
+                       torch.empty((K, r), dtype=torch.float32, device=dev),
+                       torch.empty((r, N), dtype=torch.float32, device=dev))
+                acts[key] = (x, dy, out)
+            a = ((torch.rand(K, r, device=dev, generator=g) * 2 - 1) / K ** 0.5).to(torch.bfloat16)
+            b = (torch.randn(r, N, device=dev, generator=g) * 1e-3).to(torch.bfloat16)
+            self.sites.append((M, K, N, r, alpha / r, wq, a, b) + acts[key])
+        for (M, K, N, r, *_rest) in sites:
+            D.reserve(M, N, K, r)
+
+    def step(self):
+        D = self.D
+        for (M, K, N, r, s, wq, a, b, x, dy, (y, t, dx, da, db)) in self.sites:
+            D.lora_fwd(x, wq, a, b, s, y=y, t=t)
+            D.lora_bwd(x, dy, wq, a, b, s, t, out=(dx, da, db))
+
+    def run(self, n):
+        for _ in range(n):
+            self.step()
+
+    def capture(self):
+        """Capture one step into a HIP graph on a side stream (its context's
+        workspace reserved first: the library refuses to grow it while
+        capturing); ``replay(n)`` then runs n steps with no host launch cost."""
+        import torch
+
+        D = self.D
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream):
+            for (M, K, N, r, *_r) in self.sites:
+                D.reserve(M, N, K, r)
+            self.step()
+            torch.cuda.synchronize()
+            with torch.cuda.graph(graph, stream=stream):
+                self.step()
+        torch.cuda.synchronize()
+        self.graph = graph
+
+    def replay(self, n):
+        for _ in range(n):
+            self.graph.replay()
+
+    def flops(self):
+        return sum(flops_step(M, K, N, r) for (M, K, N, r, *_r) in self.sites)
+
+    def kernel_flops(self):
+        """Algorithmic flops of the two fused GEMM kernels per step."""
+        f = sum(2.0 * M * N * (K + r) for (M, K, N, r, *_r) in self.sites)
+        b = sum(2.0 * M * K * (N + r) for (M, K, N, r, *_r) in self.sites)
+        return {"fwd_main": f, "bwd_dx": b}
+
+    def bytes(self, group=64):
+        """Algorithmic HBM bytes per step (SURVEY 8(d) model): packed weight,
+        activations and factors, forward plus backward."""
+        tot = 0.0
+        for (M, K, N, r, *_r) in self.sites:
+            wb = N * K / 2 + 4 * N * K / group
+            tot += wb + 2 * M * K + 2 * M * N + 4 * r * (K + N)
+            tot += wb + 2 * M * N + 4 * M * K + 8 * r * (K + N)
+        return tot
+
+    def check(self):
+        import torch
+
+        for (M, K, N, r, s, wq, a, b, x, dy, outs) in self.sites:
+            for v in outs:
+                if not torch.isfinite(v).all() or not v.abs().max() > 0:
+                    raise RuntimeError("implausible output (all-zero or non-finite)")
+
+
+def profile_kernels(run, n):
+    """Per-kernel GPU time of ``run(n)`` from the library's HIP events:
+    {kernel: (total ms, launches)} for the kernels that ran."""
+    import torch
+
+    from loractl_amd import device as D
+
+    D.profile_reset()
+    D.profile_enable(True)
+    torch.cuda._sleep(GPU_SPIN_CYCLES)
+    run(n)
+    torch.cuda.synchronize()
+    prof = D.profile_read()
+    D.profile_enable(False)
+    return {k: v for k, v in prof.items() if v[1]}
+
+
+def mfma_roofline(prof, kflops, steps):
+    """The roofline object of the dominant fused GEMM kernel: its algorithmic
+    flops over the profiled steps / its total launch time."""
+    dom = max((k for k in kflops if k in prof), key=lambda k: prof[k][0])
+    ms, n = prof[dom]
+    achieved = kflops[dom] * steps / (ms * 1e-3) / 1e12
+    return {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+            "flops_per_launch": kflops[dom] * steps / n, "avg_launch_us": round(1e3 * ms / n, 2)}
+
+
+def cpu_baseline_set(rows, sites, group, budget_s, scale=1.0, what=""):
+    """The reference's CPU step (f32 dequant per pass + f32 GEMMs, as
+    ``cpu_baseline``) over ``sites`` [(M, K, N, r, alpha)] with their packed
+    row-layout weights ``rows``; ``scale`` multiplies the sampled flops to
+    the whole workload when the sample is a part of it."""
+    import numpy as np
+
+    import oracle as O
+
+    steps = []
+    for i, ((M, K, N, r, alpha), (p, sc)) in enumerate(zip(sites, rows)):
+        rng = np.random.Generator(np.random.PCG64(100 + i))
+        x = rng.standard_normal((M, K), dtype=np.float32)
+        dy = rng.standard_normal((M, N), dtype=np.float32)
+        a = rng.uniform(-1 / np.sqrt(K), 1 / np.sqrt(K), (K, r)).astype(np.float32)
+        b = (rng.standard_normal((r, N), dtype=np.float32) * np.float32(1e-3))
+        steps.append(O.CpuStepInt4(p, sc, group, x, a, b, alpha / r, dy))
+    for st in steps:
+        st.run()
+    reps, t0 = 0, time.perf_counter()
+    while reps == 0 or time.perf_counter() - t0 < budget_s:
+        for st in steps:
+            st.run()
+        reps += 1
+    dt = (time.perf_counter() - t0) / reps
+    F = sum(flops_step(M, K, N, r) for (M, K, N, r, _a) in sites)
+    return {"value": round(F / dt / 1e12, 5), "unit": "TFLOP/s", "cores": O.blas_threads(), "kind": "port",
+            "sample": f"{what}{reps} steps of {dt:.3f} s: f32 dequant of each full weight per forward and per "
+                      f"backward (OpenMP), then f32 GEMMs in {O.blas_info()}",
+            "_seconds_per_step": dt * scale}
+
+
+def bench_c3(args, dev):
+    """C3: one synthetic MMDiT double-stream block's linear set, every site an
+    int4 g64 frozen base with LoRA r=32, on the image stream (M=4096) and the
+    text stream (M=512, its own weights), forward + backward per step."""
+    sites = [(M, K, N, 32, 32.0) for (_name, M) in C3_STREAMS for (K, N) in C3_SITES]
+    keep = 0 if args.no_cpu_baseline else len(sites)
+    ls = LinearSet(dev, sites, seed=3, keep_rows=keep)
+    ls.run(1)
+    import torch
+
+    torch.cuda.synchronize()
+    ls.check()
+    ls.capture()
+    ms, ratio, warm_ms = warm_and_time(ls.replay, args.steps, args.warmup)
+    ms_step = ms / args.steps
+    F = ls.flops()
+    value = F / (ms_step * 1e-3) / 1e12
+    prof = profile_kernels(ls.run, args.steps)
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline_set(ls.rows, sites, 64, args.cpu_seconds, what="the whole step (both streams), ")
+        cpu.pop("_seconds_per_step")
+    print(json.dumps({
+        "metric": "int4-base LoRA linear set fwd+bwd TFLOP/s (C3: MMDiT double-stream block)",
+        "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (torch seeded; W~N(0,0.02) quantized on device, X,dY~N(0,1), "
+                                 "A~U(+-1/sqrt(K)), B~N(0,1e-3))",
+        "config": {"workload": "C3: QKV 3072->9216, attn-out 3072->3072, MLP 3072->12288->3072, adaLN "
+                               "3072->18432, int4-g64 + LoRA r=32 on each; image stream M=4096 and text stream "
+                               "M=512 (own weights), forward+backward; one step replayed from a HIP graph",
+                   "parallelism": "single-gpu"},
+        "pct_of_mfma_peak": round(100.0 * value / PEAK_BF16_TFLOPS, 2), "flops_per_step": F,
+        "sanity_x2_ratio": round(ratio, 3), "warm_ms": round(warm_ms, 1),
+        "kernels_us": {k: round(1e3 * v[0] / v[1], 2) for k, v in prof.items()},
+        "kernel_share": {k: round(v[0] / sum(x[0] for x in prof.values()), 4) for k, v in prof.items()},
+        "roofline": mfma_roofline(prof, ls.kernel_flops(), args.steps),
+        "cpu_baseline": cpu,
+    }), flush=True)
+
+
+def bench_c5(args, dev):
+    """C5: the linears of a Qwen3-style 28-layer decoder (q/k/v/o/gate/up/down,
+    int4 g64, LoRA r=16), forward + backward per step, at each M of the
+    sweep. Every layer has its own weights (3.2 GB blocked, past the
+    Infinity Cache), so the few-token end streams HBM."""
+    import torch
+
+    sweep = {}
+    cpu = None
+    for M in C5_M:
+        sites = [(M, K, N, 16, 16.0) for _layer in range(C5_LAYERS) for (K, N) in C5_LAYER]
+        keep = len(C5_LAYER) if (not args.no_cpu_baseline) else 0
+        ls = LinearSet(dev, sites, seed=5, keep_rows=keep)
+        ls.run(1)
+        torch.cuda.synchronize()
+        ls.check()
+        ls.capture()
+        steps = args.steps if M >= 256 else max(args.steps, 20)
+        ms, ratio, warm_ms = warm_and_time(ls.replay, steps, args.warmup)
+        ms_step = ms / steps
+        F = ls.flops()
+        B = ls.bytes()
+        prof = profile_kernels(ls.run, steps)
+        entry = {"ms_per_step": round(ms_step, 4), "tflops": round(F / (ms_step * 1e-3) / 1e12, 2),
+                 "gbs": round(B / (ms_step * 1e-3) / 1e9, 1), "flops_per_step": F, "bytes_per_step": B,
+                 "sanity_x2_ratio": round(ratio, 3),
+                 "kernels_us": {k: round(1e3 * v[0] / v[1], 2) for k, v in prof.items()}}
+        if M >= 256:
+            entry["roofline"] = mfma_roofline(prof, ls.kernel_flops(), steps)
+        else:
+            total_ms = sum(v[0] for v in prof.values()) / steps
+            achieved = B / (total_ms * 1e-3) / 1e9
+            entry["roofline"] = {"kernel": "all (stream of 196 weights, both passes)", "bound": "hbm",
+                                 "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                                 "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                                 "bytes_per_step": B}
+        if not args.no_cpu_baseline:
+            c = cpu_baseline_set(ls.rows, sites[:len(C5_LAYER)], 64, args.cpu_seconds / len(C5_M),
+                                 scale=C5_LAYERS, what=f"1 of {C5_LAYERS} layers at M={M}, ")
+            entry["cpu_baseline"] = {k: v for k, v in c.items() if k != "_seconds_per_step"}
+        sweep[str(M)] = entry
+        del ls
+        torch.cuda.empty_cache()
+    head = sweep[str(C5_M[-1])]
+    print(json.dumps({
+        "metric": "int4-base LoRA linear set fwd+bwd TFLOP/s (C5: Qwen3-style decoder linears, M sweep)",
+        "value": head["tflops"], "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (torch seeded; W~N(0,0.02) quantized on device, X,dY~N(0,1), "
+                                 "A~U(+-1/sqrt(K)), B~N(0,1e-3))",
+        "config": {"workload": f"C5: {C5_LAYERS} layers x q/k/v/o/gate/up/down (2560 hidden, 9728 MLP, GQA "
+                               f"32q/8kv x 128), int4-g64 + LoRA r=16, forward+backward, one step replayed "
+                               f"from a HIP graph; value at M={C5_M[-1]}",
+                   "M_sweep": list(C5_M), "parallelism": "single-gpu"},
+        "pct_of_mfma_peak": round(100.0 * head["tflops"] / PEAK_BF16_TFLOPS, 2),
+        "sweep": sweep, "roofline": head["roofline"], "cpu_baseline": head.get("cpu_baseline"),
     }), flush=True)
 
 
