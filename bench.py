@@ -48,7 +48,9 @@ WORKLOADS = {
     "requant": (0, 3072, 12288, 0, 0.0, "fp8", 64),  # fp8 checkpoint tensor -> int4, load time
     "c3": None,  # one synthetic MMDiT double-stream block's linear set (C3_SITES), image + text stream
     "c5": None,  # a Qwen3-style 28-layer decoder's linears (C5_LAYER), M swept over C5_M
+    "mmdit": None,  # C4: the block-checkpointed synthetic MMDiT training step (loractl_amd.mmdit)
 }
+MMDIT_TOKENS = (4096, 512)  # image tokens (64x64 latent, 2x2 patches), text tokens
 # C3: (d_in, d_out) of QKV, attn-out, MLP up, MLP down, adaLN-mod; int4 g64, r=32, alpha=32
 C3_SITES = [(3072, 9216), (3072, 3072), (3072, 12288), (12288, 3072), (3072, 18432)]
 C3_STREAMS = (("image", 4096), ("text", 512))
@@ -69,6 +71,7 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-skinny", action="store_true", help="leave the skinny-M sub-object out of the ns line")
+    p.add_argument("--no-mmdit", action="store_true", help="leave the MMDiT step sub-object out of the ns line")
     return p.parse_args()
 
 
@@ -169,6 +172,8 @@ def main():
         return bench_c3(args, dev)
     if args.workload == "c5":
         return bench_c5(args, dev)
+    if args.workload == "mmdit":
+        return bench_mmdit(args, dev)
     M, K, N, r, alpha, fmt, group = WORKLOADS[args.workload]
     s = alpha / r
     w, x, a, b, dy = make_inputs(M, K, N, r)
@@ -270,6 +275,12 @@ def main():
     if args.workload == "ns" and not args.no_skinny:
         # the north star's second bar, the few-token forward of the same layer
         out["skinny"] = skinny_measure(args, dev, with_cpu=not args.no_cpu_baseline)
+    if args.workload == "ns" and not args.no_mmdit:
+        # the metric's second half: MMDiT train steps/s (C4)
+        del wq, xb, ab, bb, dyb, y, t, dx, da, db
+        torch.cuda.empty_cache()
+        out["mmdit"] = mmdit_measure(args, dev, steps=min(args.steps, 5), warmup=min(args.warmup, 2),
+                                     with_cpu=not args.no_cpu_baseline)
     print(json.dumps(out), flush=True)
 
 
@@ -751,6 +762,157 @@ def bench_c5(args, dev):
         "pct_of_mfma_peak": round(100.0 * head["tflops"] / PEAK_BF16_TFLOPS, 2),
         "sweep": sweep, "roofline": head["roofline"], "cpu_baseline": head.get("cpu_baseline"),
     }), flush=True)
+
+
+def mmdit_measure(args, dev, steps, warmup, with_cpu=True):
+    """C4: steps/s of the block-checkpointed synthetic MMDiT LoRA training
+    step (loractl_amd.mmdit.checkpointed_step + AdamW on the adapters), one
+    step = capture forward, head loss, per-block replay with backward, the
+    optimizer step; the loss is read back every step (the reference's
+    per-step fence)."""
+    import torch
+
+    from loractl_amd import device as D
+    from loractl_amd.mmdit import (Mmdit, MmditConfig, build_mmdit_adapters, checkpointed_step, flow_batch,
+                                   mmdit_step_flops)
+
+    cfg = MmditConfig()
+    img_tokens, txt_tokens = MMDIT_TOKENS
+    t0 = time.perf_counter()
+    model = Mmdit(cfg, dev, seed=0)
+    ad = build_mmdit_adapters(cfg, dev, seed=1)
+    setup_s = time.perf_counter() - t0
+    batch = flow_batch(cfg, img_tokens, txt_tokens, dev, seed=2)
+    params = [p for d in ad.deltas for p in (d.lora_a, d.lora_b)]
+    # burn's AdamWConfig defaults (beta 0.9/0.999, eps 1e-5); the trainer's weight decay default 0
+    opt = torch.optim.AdamW(params, lr=1e-4, eps=1e-5, weight_decay=0.0)
+    for (M, (K, N)) in [(m, kn) for m in MMDIT_TOKENS for kn in cfg.site_shapes().values()]:
+        D.reserve(M, N, K, cfg.rank)
+    losses = []
+
+    def step():
+        opt.zero_grad(set_to_none=True)
+        losses.append(checkpointed_step(model, ad, batch))
+        opt.step()
+
+    def run(n):
+        for _ in range(n):
+            step()
+
+    run(1)
+    torch.cuda.synchronize()
+    if not all(map(lambda v: v == v and v > 0, losses)):
+        raise RuntimeError(f"implausible loss {losses}")
+    ms, ratio, warm_ms = warm_and_time(run, steps, warmup)
+    ms_step = ms / steps
+    fl = mmdit_step_flops(cfg, img_tokens, txt_tokens)
+    prof = profile_kernels(run, 1)
+    fused = {k: v for k, v in prof.items()}
+    fused_ms = sum(v[0] for v in fused.values())
+    # the fused GEMMs' algorithmic flops per step: two forwards (capture and
+    # replay) and one input gradient of every site, LoRA step included
+    kflops = {"fwd_main": 0.0, "bwd_dx": 0.0}
+    for M in MMDIT_TOKENS:
+        for n, (K, N) in cfg.site_shapes().items():
+            rows = 1 if n == "mod" else M
+            kflops["fwd_main"] += 2 * 2.0 * rows * N * (K + cfg.rank) * cfg.layers
+            kflops["bwd_dx"] += 2.0 * rows * K * (N + cfg.rank) * cfg.layers
+    out = {
+        "metric": "MMDiT train steps/s (C4: 24 double-stream blocks, block checkpointing)",
+        "value": round(1e3 / ms_step, 4),
+        "unit": "steps/s",
+        "ms_per_step": round(ms_step, 2),
+        "tflops": round(fl["total"] / (ms_step * 1e-3) / 1e12, 2),
+        "flop_model": {k: fl[k] for k in ("proj", "attn", "lora", "total")},
+        "sanity_x2_ratio": round(ratio, 3),
+        "warm_ms": round(warm_ms, 1),
+        "setup_s": round(setup_s, 1),
+        "loss_first_last": [round(losses[0], 5), round(losses[-1], 5)],
+        "fused_kernels_ms_per_step": round(fused_ms, 2),
+        "fused_share_of_step": round(fused_ms / ms_step, 4),
+        "kernels_ms_per_step": {k: round(v[0], 3) for k, v in fused.items()},
+        "roofline": mfma_roofline(prof, kflops, 1),
+        "workload": f"batch 1 of {img_tokens} image + {txt_tokens} text tokens, hidden {cfg.hidden}, {cfg.heads} "
+                    f"heads, {cfg.layers} double-stream blocks, MLP x{cfg.mlp_ratio}, int4-g{cfg.group} frozen "
+                    f"base and LoRA r={cfg.rank} on all {len(cfg.site_paths())} block linears (modulation on the "
+                    f"conditioning vector), AdamW on the adapters, flow-matching MSE with t~U(0,1)",
+        "cpu_baseline": None,
+    }
+    del model, ad, opt, params
+    torch.cuda.empty_cache()
+    if with_cpu:
+        out["cpu_baseline"] = cpu_baseline_mmdit(cfg, img_tokens, txt_tokens, args.cpu_seconds)
+    return out
+
+
+def cpu_baseline_mmdit(cfg, img_tokens, txt_tokens, budget_s):
+    """The reference's CPU algorithm for one block of the step, scaled to the
+    trunk: the block's ten linears through the f32 dequant + f32 GEMM step
+    (dequant per pass: two forwards and one backward under block
+    checkpointing) and the attention matmuls (QK^T and PV twice forward,
+    their four gradients once) in numpy's SGEMM; norms and elementwise work
+    are left out, so the time is an under-count."""
+    import numpy as np
+
+    import oracle as O
+
+    rng = np.random.Generator(np.random.PCG64(9))
+    sites = []
+    for M in (img_tokens, txt_tokens):
+        for n, (K, N) in cfg.site_shapes().items():
+            rows = 1 if n == "mod" else M
+            w = (rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02))
+            p, sc = O.quantize_int4_packed(w, cfg.group)
+            x = rng.standard_normal((rows, K), dtype=np.float32)
+            dy = rng.standard_normal((rows, N), dtype=np.float32)
+            a = rng.uniform(-1 / np.sqrt(K), 1 / np.sqrt(K), (K, cfg.rank)).astype(np.float32)
+            b = (rng.standard_normal((cfg.rank, N), dtype=np.float32) * np.float32(1e-3))
+            sites.append(O.CpuStepInt4(p, sc, cfg.group, x, a, b, cfg.alpha / cfg.rank, dy))
+    L, nh, hd = img_tokens + txt_tokens, cfg.heads, cfg.head_dim
+    q, k, v, do = (rng.standard_normal((nh, L, hd), dtype=np.float32) for _ in range(4))
+
+    def attention():
+        for _ in range(2):  # capture forward and replay forward
+            s_ = q @ k.transpose(0, 2, 1)
+            s_ -= s_.max(-1, keepdims=True)
+            p_ = np.exp(s_)
+            p_ /= p_.sum(-1, keepdims=True)
+            o = p_ @ v
+        dv = p_.transpose(0, 2, 1) @ do
+        dp = do @ v.transpose(0, 2, 1)
+        ds = p_ * (dp - (dp * p_).sum(-1, keepdims=True))
+        dq = ds @ k
+        dk = ds.transpose(0, 2, 1) @ q
+        return o, dv, dq, dk
+
+    def block():
+        for st in sites:
+            st.run()      # forward + backward, each with its own f32 dequant
+            st.forward()  # the replay forward of block checkpointing
+        attention()
+
+    block()
+    reps, t0 = 0, time.perf_counter()
+    while reps == 0 or time.perf_counter() - t0 < budget_s:
+        block()
+        reps += 1
+    dt = (time.perf_counter() - t0) / reps
+    step_s = dt * cfg.layers
+    return {"value": round(1.0 / step_s, 6), "unit": "steps/s", "cores": O.blas_threads(), "kind": "port",
+            "sample": f"1 of {cfg.layers} blocks ({reps} reps of {dt:.2f} s, times {cfg.layers}): its 10 linears "
+                      f"as f32 dequant per pass + f32 GEMMs (2 forwards, 1 backward) and the attention matmuls, "
+                      f"in {O.blas_info()}; norms and elementwise work left out"}
+
+
+def bench_mmdit(args, dev):
+    m = mmdit_measure(args, dev, steps=args.steps, warmup=args.warmup, with_cpu=not args.no_cpu_baseline)
+    out = {"metric": m.pop("metric"), "value": m.pop("value"), "unit": "steps/s", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": m.pop("ms_per_step"), "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "bf16",
+           "data": "synthetic (torch seeded; random-init weights, latents and text embeddings ~N(0,1))",
+           "config": {"workload": m.pop("workload"), "parallelism": "single-gpu"}}
+    out.update(m)
+    print(json.dumps(out), flush=True)
 
 
 def cpu_baseline_fwd(wq_rows, x, a, b, M, K, N, r, s, group, budget_s, bytes_fwd):

@@ -1,0 +1,321 @@
+"""A synthetic double-stream MMDiT and its block-checkpointed LoRA training
+step, with every block linear running through the fused quantized LoRA op.
+
+This is the driver of the benchmark's C4 configuration ("MMDiT train
+steps/s"): 24 FLUX-style double-stream blocks, hidden 3072, 24 heads of
+128, MLP ratio 4, an int4 group-64 frozen base and LoRA r = 32 on every
+block linear, AdamW on the adapters only, batch 1 of 4096 image tokens (a
+64 x 64 latent in 2 x 2 patches) and 512 text tokens, flow-matching MSE.
+The reference's own model is single-stream (``mmdit.rs``); only the linear
+sites and the step structure carry over:
+
+- sites: each stream of each block has five quantized linears, all
+  injectable (``blocks.{i}.{img,txt}.{mod,qkv,out,up,down}``), run through
+  ``site()`` (``mmdit.rs:526-536``), so a registered delta fuses with its
+  base in one op;
+- ``checkpointed_step`` follows ``block_ckpt.rs:103-207``: a no-grad
+  capture forward stores each block's inputs, a small head graph gives the
+  loss and the trunk cotangent (the loss scale folded in once), then each
+  block is replayed last to first on its own graph, seeded by the incoming
+  cotangent, its adapter gradients accumulating on the deltas' parameters;
+  the per-site cost is two fused forwards and one fused backward;
+- the flow-matching target follows ``flow.rs``: ``x_t = (1 - t) x0 + t eps``,
+  target ``v = eps - x0`` (t = 0 is data), loss ``mean((pred - v)^2)``.
+
+Around the fused sites everything is PyTorch-ROCm (LayerNorm, modulation,
+per-head RMSNorm of q and k, RoPE, SDPA attention on its memory-efficient
+backend, GELU, the frozen bf16 embedders and head): those are outside the
+quantized-linear path. The modulation (adaLN) linears take the conditioning
+vector, one row per batch element, as in FLUX.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import Dict, List, Optional, Tuple
+
+import torch
+import torch.nn.functional as F
+
+from . import device as D
+from .adapters import LoraAdapters, QuantLinear, site
+from .lora import LoraDelta
+
+STREAMS = ("img", "txt")
+SITE_NAMES = ("mod", "qkv", "out", "up", "down")
+
+
+@dataclass
+class MmditConfig:
+    hidden: int = 3072
+    heads: int = 24
+    mlp_ratio: int = 4
+    layers: int = 24
+    patch_dim: int = 64      # 16 latent channels x 2 x 2 patch
+    txt_dim: int = 4096      # text-encoder width of the conditioning tokens
+    tdim: int = 256          # sinusoidal timestep embedding width
+    group: int = 64          # int4 quant block
+    rank: int = 32
+    alpha: float = 32.0
+
+    @property
+    def head_dim(self) -> int:
+        return self.hidden // self.heads
+
+    def site_shapes(self) -> Dict[str, Tuple[int, int]]:
+        """(d_in, d_out) of each site of one stream of one block."""
+        h = self.hidden
+        return {"mod": (h, 6 * h), "qkv": (h, 3 * h), "out": (h, h), "up": (h, self.mlp_ratio * h),
+                "down": (self.mlp_ratio * h, h)}
+
+    def site_paths(self) -> List[str]:
+        return [f"blocks.{i}.{s}.{n}" for i in range(self.layers) for s in STREAMS for n in SITE_NAMES]
+
+
+def timestep_embedding(t: torch.Tensor, dim: int, max_period: float = 10000.0) -> torch.Tensor:
+    """Sinusoidal embedding of ``1000 t`` (the FLUX/SD3 convention), [B, dim] f32."""
+    half = dim // 2
+    freqs = torch.exp(-math.log(max_period) * torch.arange(half, dtype=torch.float32, device=t.device) / half)
+    args = (t.float() * 1000.0)[:, None] * freqs[None]
+    return torch.cat([torch.cos(args), torch.sin(args)], dim=-1)
+
+
+def rope_tables(L: int, dim: int, device, theta: float = 10000.0):
+    """cos/sin [L, dim] (pairs (2j, 2j+1) share a frequency), f32."""
+    inv = 1.0 / theta ** (torch.arange(0, dim, 2, dtype=torch.float32, device=device) / dim)
+    ang = torch.arange(L, dtype=torch.float32, device=device)[:, None] * inv[None]
+    cos = torch.repeat_interleave(torch.cos(ang), 2, dim=-1)
+    sin = torch.repeat_interleave(torch.sin(ang), 2, dim=-1)
+    return cos, sin
+
+
+def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """Rotate (x_2j, x_2j+1) pairs; x [H, L, D] bf16, tables [L, D] f32."""
+    xf = x.float()
+    x2 = torch.stack((-xf[..., 1::2], xf[..., 0::2]), dim=-1).flatten(-2)
+    return (xf * cos + x2 * sin).to(x.dtype)
+
+
+@dataclass
+class Capture:
+    """What the capture forward keeps (``mmdit.rs:1474-1507``): each block's
+    input streams, the conditioning vector, RoPE tables and the trunk output."""
+
+    block_inputs: List[Tuple[torch.Tensor, torch.Tensor]] = field(default_factory=list)
+    vec: Optional[torch.Tensor] = None
+    rope: Optional[Tuple[torch.Tensor, torch.Tensor]] = None
+    x_img: Optional[torch.Tensor] = None
+    x_txt: Optional[torch.Tensor] = None
+
+
+class Mmdit:
+    """The frozen synthetic double-stream denoiser: int4 blocked base weights
+    for every block linear, bf16 plain embedders and head."""
+
+    def __init__(self, cfg: MmditConfig, device, seed: int = 0, w_std: float = 0.02):
+        self.cfg = cfg
+        self.device = torch.device(device)
+        self.site_fn = site  # how a block runs its linears: site() (a test may substitute a reference)
+        g = torch.Generator(device=self.device).manual_seed(seed)
+        h = cfg.hidden
+
+        def plain(d_in, d_out):
+            w = (torch.randn(d_out, d_in, device=self.device, generator=g) / math.sqrt(d_in)).to(torch.bfloat16)
+            return w, torch.zeros(d_out, device=self.device, dtype=torch.bfloat16)
+
+        self.img_in = plain(cfg.patch_dim, h)
+        self.txt_in = plain(cfg.txt_dim, h)
+        self.t_in = plain(cfg.tdim, h)
+        self.t_out = plain(h, h)
+        self.final_mod = plain(h, 2 * h)
+        self.final = plain(h, cfg.patch_dim)
+        self.bases: Dict[str, QuantLinear] = {}
+        for i in range(cfg.layers):
+            for s in STREAMS:
+                for n, (d_in, d_out) in cfg.site_shapes().items():
+                    w = torch.randn(d_out, d_in, device=self.device, generator=g) * w_std
+                    self.bases[f"blocks.{i}.{s}.{n}"] = QuantLinear([D.quantize_int4(w, cfg.group)])
+                    del w
+
+    # ------------------------------------------------------------ pieces
+    @staticmethod
+    def _linear(x, wb):
+        return F.linear(x, wb[0], wb[1])
+
+    def conditioning(self, t: torch.Tensor) -> torch.Tensor:
+        """vec [B, hidden] bf16 from the timestep (frozen)."""
+        e = timestep_embedding(t, self.cfg.tdim).to(torch.bfloat16)
+        return self._linear(F.silu(self._linear(e, self.t_in)), self.t_out)
+
+    def embed(self, img: torch.Tensor, txt: torch.Tensor):
+        return self._linear(img, self.img_in), self._linear(txt, self.txt_in)
+
+    def head(self, x_img: torch.Tensor, vec: torch.Tensor) -> torch.Tensor:
+        shift, scale = self._linear(F.silu(vec), self.final_mod).chunk(2, dim=-1)
+        h = F.layer_norm(x_img, (self.cfg.hidden,), eps=1e-6) * (1 + scale) + shift
+        return self._linear(h, self.final)
+
+    def block(self, i: int, x_img: torch.Tensor, x_txt: torch.Tensor, vec: torch.Tensor, rope,
+              adapters: Optional[LoraAdapters]):
+        """One double-stream block on [L_img, H] and [L_txt, H] bf16 streams."""
+        cfg = self.cfg
+        H, nh, hd = cfg.hidden, cfg.heads, cfg.head_dim
+        p = f"blocks.{i}"
+        site = self.site_fn
+        cvec = F.silu(vec)
+        mods, qs, ks, vs = {}, [], [], []
+        for s, x in (("txt", x_txt), ("img", x_img)):  # text tokens first in the joint sequence
+            m = site(adapters, f"{p}.{s}.mod", self.bases[f"{p}.{s}.mod"], cvec)
+            mods[s] = m.chunk(6, dim=-1)
+            sh1, sc1 = mods[s][0], mods[s][1]
+            h = F.layer_norm(x, (H,), eps=1e-6) * (1 + sc1) + sh1
+            qkv = site(adapters, f"{p}.{s}.qkv", self.bases[f"{p}.{s}.qkv"], h)
+            q, k, v = qkv.view(-1, 3, nh, hd).permute(1, 2, 0, 3).unbind(0)  # [nh, L, hd] each
+            qs.append(F.rms_norm(q, (hd,), eps=1e-6))
+            ks.append(F.rms_norm(k, (hd,), eps=1e-6))
+            vs.append(v)
+        cos, sin = rope
+        q = apply_rope(torch.cat(qs, dim=1), cos, sin)
+        k = apply_rope(torch.cat(ks, dim=1), cos, sin)
+        v = torch.cat(vs, dim=1)
+        with torch.nn.attention.sdpa_kernel([torch.nn.attention.SDPBackend.EFFICIENT_ATTENTION]):
+            o = F.scaled_dot_product_attention(q.unsqueeze(0).contiguous(), k.unsqueeze(0).contiguous(),
+                                               v.unsqueeze(0).contiguous())
+        o = o[0].transpose(0, 1).reshape(-1, H)  # [L, H]
+        lt = x_txt.shape[0]
+        outs = {}
+        for s, x, oo in (("txt", x_txt, o[:lt]), ("img", x_img, o[lt:])):
+            _, _, g1, sh2, sc2, g2 = mods[s]
+            x = x + g1 * site(adapters, f"{p}.{s}.out", self.bases[f"{p}.{s}.out"], oo.contiguous())
+            h2 = F.layer_norm(x, (H,), eps=1e-6) * (1 + sc2) + sh2
+            up = site(adapters, f"{p}.{s}.up", self.bases[f"{p}.{s}.up"], h2)
+            x = x + g2 * site(adapters, f"{p}.{s}.down", self.bases[f"{p}.{s}.down"],
+                              F.gelu(up, approximate="tanh"))
+            outs[s] = x
+        return outs["img"], outs["txt"]
+
+    # ------------------------------------------------------------ passes
+    def prepare(self, img, txt, t):
+        vec = self.conditioning(t)
+        x_img, x_txt = self.embed(img, txt)
+        rope = rope_tables(x_img.shape[0] + x_txt.shape[0], self.cfg.head_dim, self.device)
+        return x_img, x_txt, vec, rope
+
+    def forward(self, img, txt, t, adapters) -> torch.Tensor:
+        """The monolithic forward (autograd through every block)."""
+        with torch.no_grad():
+            x_img, x_txt, vec, rope = self.prepare(img, txt, t)
+        for i in range(self.cfg.layers):
+            x_img, x_txt = self.block(i, x_img, x_txt, vec, rope, adapters)
+        return self.head(x_img, vec)
+
+    @torch.no_grad()
+    def forward_capture(self, img, txt, t, adapters) -> Capture:
+        """Pre-trunk and trunk with no graph, keeping each block's inputs
+        (``mmdit.rs:1474-1507``)."""
+        x_img, x_txt, vec, rope = self.prepare(img, txt, t)
+        cap = Capture(vec=vec, rope=rope)
+        for i in range(self.cfg.layers):
+            cap.block_inputs.append((x_img, x_txt))
+            x_img, x_txt = self.block(i, x_img, x_txt, vec, rope, adapters)
+        cap.x_img, cap.x_txt = x_img, x_txt
+        return cap
+
+
+def build_mmdit_adapters(cfg: MmditConfig, device, seed: int = 1, b_std: float = 0.0) -> LoraAdapters:
+    """A delta on every block site (rank/alpha from the config); A is
+    Kaiming-uniform and B zero as ``lora.rs:123-137`` (``b_std`` > 0 draws B
+    from N(0, b_std) so a fresh set is not a no-op)."""
+    torch.manual_seed(seed)
+    deltas, targets = [], []
+    shapes = cfg.site_shapes()
+    for path in cfg.site_paths():
+        d_in, d_out = shapes[path.rsplit(".", 1)[1]]
+        d = LoraDelta(d_in, d_out, cfg.rank, cfg.alpha, device=device)
+        if b_std > 0:
+            with torch.no_grad():
+                d.lora_b.normal_(0.0, b_std)
+        deltas.append(d)
+        targets.append(path)
+    return LoraAdapters(deltas, targets)
+
+
+def flow_batch(cfg: MmditConfig, img_tokens: int, txt_tokens: int, device, seed: int = 2):
+    """A synthetic flow-matching batch (``flow.rs``): latent patches x0 and
+    text embeddings ~ N(0, 1), t ~ U(0, 1), noise eps; returns
+    (x_t bf16, txt bf16, t, target f32) with x_t = (1 - t) x0 + t eps and
+    the velocity target v = eps - x0."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    x0 = torch.randn(img_tokens, cfg.patch_dim, device=device, generator=g)
+    eps = torch.randn(img_tokens, cfg.patch_dim, device=device, generator=g)
+    txt = torch.randn(txt_tokens, cfg.txt_dim, device=device, generator=g).to(torch.bfloat16)
+    t = torch.rand(1, device=device, generator=g)
+    x_t = ((1 - t) * x0 + t * eps).to(torch.bfloat16)
+    return x_t, txt, t, eps - x0
+
+
+def flow_loss(pred: torch.Tensor, target: torch.Tensor) -> torch.Tensor:
+    d = pred.float() - target
+    return (d * d).mean()
+
+
+def monolithic_step(model: Mmdit, adapters: LoraAdapters, batch, loss_scale: float = 1.0) -> float:
+    """Loss and adapter gradients (on the deltas' ``.grad``) through one
+    autograd graph over the whole trunk."""
+    img, txt, t, target = batch
+    loss = flow_loss(model.forward(img, txt, t, adapters), target)
+    (loss * loss_scale).backward()
+    return float(loss.item())
+
+
+def checkpointed_step(model: Mmdit, adapters: LoraAdapters, batch, loss_scale: float = 1.0) -> float:
+    """One block-checkpointed step (``block_ckpt.rs:103-207``): capture, head
+    graph, reverse per-block replay. Returns the unscaled loss; adapter
+    gradients accumulate on the deltas' ``.grad`` (scaled by ``loss_scale``)."""
+    img, txt, t, target = batch
+    cap = model.forward_capture(img, txt, t, adapters)
+    # head graph: trunk output re-tracked, loss scale folded into the seed once
+    x_img = cap.x_img.detach().requires_grad_()
+    loss = flow_loss(model.head(x_img, cap.vec), target)
+    (loss * loss_scale).backward()
+    g_img = x_img.grad
+    g_txt = torch.zeros_like(cap.x_txt)  # the text stream's final output feeds no loss
+    del x_img
+    # reverse sweep, one standalone graph per block
+    for i in reversed(range(model.cfg.layers)):
+        xi, xt = (v.detach().requires_grad_() for v in cap.block_inputs[i])
+        oi, ot = model.block(i, xi, xt, cap.vec, cap.rope, adapters)
+        torch.autograd.backward([oi, ot], [g_img, g_txt])
+        g_img, g_txt = xi.grad, xt.grad
+        cap.block_inputs[i] = None  # this block's inputs are done
+    return float(loss.item())
+
+
+def mmdit_step_flops(cfg: MmditConfig, img_tokens: int, txt_tokens: int, batch: int = 1,
+                     grad_checkpointing: bool = True) -> Dict[str, float]:
+    """The step work model of ``bench.rs:274-311`` for the double-stream
+    trunk: dense block projections at 2 d_in d_out per token (the
+    modulation linears at one row per batch element), the two attention
+    matmuls at 4 L^2 hidden per block over the joint sequence; a frozen
+    base's backward costs one forward and attention's two, and block
+    checkpointing replays one more forward (x3 projections, x4 attention).
+    The LoRA terms are reported apart (``lora``), as the reference excludes
+    them."""
+    shapes = cfg.site_shapes()
+    proj = 0.0
+    lora = 0.0
+    for s, M in (("img", img_tokens * batch), ("txt", txt_tokens * batch)):
+        for n, (k, nn) in shapes.items():
+            rows = batch if n == "mod" else M
+            proj += 2.0 * rows * k * nn
+            lora += 2.0 * rows * cfg.rank * (k + nn)
+    proj *= cfg.layers
+    lora *= cfg.layers
+    L = img_tokens + txt_tokens
+    attn = 4.0 * L * L * cfg.hidden * batch * cfg.layers
+    pp = 3.0 if grad_checkpointing else 2.0
+    # LoRA: 2 forwards (1 x 2Mr(K+N)) and a backward of 2 x that with ckpt
+    lora_total = lora * (2.0 + 2.0) if grad_checkpointing else lora * 3.0
+    return {"proj": proj * pp, "attn": attn * (pp + 1.0), "lora": lora_total,
+            "total": proj * pp + attn * (pp + 1.0), "fwd_proj": proj, "fwd_attn": attn}

@@ -291,7 +291,7 @@ class CpuFwdInt4:
         return lib().lrq_o_cpu_dequant_int4(_ptr(self.packed), _ptr(self.scales), self.g, self.N, self.K,
                                             _ptr(self.Wdq))
 
-    def run(self) -> int:
+    def forward(self) -> int:
         """One forward; returns the threads of the dequant (the GEMMs use
         ``blas_threads()``)."""
         th = self.dequant()
@@ -299,6 +299,9 @@ class CpuFwdInt4:
         self.T = (self.X @ self.A) * self.s
         self.Y += self.T @ self.B
         return th
+
+    def run(self) -> int:
+        return self.forward()
 
 
 class CpuStepInt4(CpuFwdInt4):
@@ -313,7 +316,7 @@ class CpuStepInt4(CpuFwdInt4):
         self.dY = _c(dY, np.float32)
 
     def run(self) -> int:
-        th = super().run()
+        th = self.forward()
         self.dequant()
         self.dX = self.dY @ self.Wdq
         self.U = (self.dY @ self.B.T) * self.s
