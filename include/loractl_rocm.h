@@ -179,8 +179,9 @@ int lrq_lora_fwd(lrq_ctx* ctx, const lrq_weight* w, const uint16_t* x, int64_t m
  * arguments, kernels and results as lrq_lora_fwd; its workspace is a
  * file-scope device array of LRQ_NOALLOC_SCRATCH_BYTES held by every GPU
  * the library runs on until the process ends, so it calls no hipMalloc,
- * hipFree or event creation. A shape whose forward needs more scratch than
- * that returns LRQ_EINVAL. Every call on one GPU shares that GPU's array:
+ * hipFree or event creation. Its first 64 KiB hold the few-token kernels'
+ * arrival counters; a shape whose forward needs more scratch than the rest
+ * returns LRQ_EINVAL. Every call on one GPU shares that GPU's array:
  * calls that overlap on one GPU (two streams, two contexts, two threads)
  * race and must be ordered by the caller. */
 int lrq_lora_fwd_noalloc(lrq_ctx* ctx, const lrq_weight* w, const uint16_t* x, int64_t m,

@@ -19,7 +19,9 @@ void set_num_cus(int n);
 struct lrq_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
-  char* ws = nullptr;
+  char* ws_alloc = nullptr;   // the allocation: arrival counters, then the workspace
+  uint32_t* cnt = nullptr;    // LRQ_CNT_WORDS arrival counters of the few-token kernels
+  char* ws = nullptr;         // ws_alloc + LRQ_CNT_BYTES
   size_t ws_bytes = 0;
   char err[512] = {0};
   bool prof = false;
@@ -58,7 +60,7 @@ namespace {
 
 const char* kNames[KID_COUNT] = {"quantize_int4", "quantize_fp8", "dequant", "fwd_main", "bwd_dx",
                                  "lora_t",        "lora_u",       "lora_da", "lora_db",  "lora_reduce",
-                                 "block",         "fwd_epi",      "lora_dadb"};
+                                 "block",         "lora_dadb"};
 
 int fail(lrq_ctx* c, int code, const char* fmt, ...) {
   if (c) {
@@ -156,15 +158,22 @@ int ensure_ws(lrq_ctx* c, size_t bytes) {
   // stream-ordered users of the old buffer must finish before it goes
   e = hipStreamSynchronize(c->stream);
   if (e != hipSuccess) return hip_fail(c, e, "hipStreamSynchronize");
-  if (c->ws) (void)hipFree(c->ws);
-  c->ws = nullptr;
+  if (c->ws_alloc) (void)hipFree(c->ws_alloc);
+  c->ws_alloc = c->ws = nullptr;
+  c->cnt = nullptr;
   c->ws_bytes = 0;
   size_t want = (size_t)round_up((int64_t)(bytes > 0 ? bytes : 1), 1 << 20);
-  e = hipMalloc(&c->ws, want);
+  e = hipMalloc(&c->ws_alloc, want + LRQ_CNT_BYTES);
   if (e != hipSuccess) {
-    c->ws = nullptr;
+    c->ws_alloc = nullptr;
     return fail(c, LRQ_ENOMEM, "workspace of %zu bytes: %s", want, hipGetErrorString(e));
   }
+  // the few-token kernels' arrival counters start at zero (and each launch
+  // leaves them at zero)
+  e = hipMemsetAsync(c->ws_alloc, 0, LRQ_CNT_BYTES, c->stream);
+  if (e != hipSuccess) return hip_fail(c, e, "hipMemsetAsync");
+  c->cnt = reinterpret_cast<uint32_t*>(c->ws_alloc);
+  c->ws = c->ws_alloc + LRQ_CNT_BYTES;
   c->ws_bytes = want;
   return LRQ_OK;
 }
@@ -297,7 +306,7 @@ int lrq_destroy(lrq_ctx* c) {
     (void)hipEventDestroy(r.b);
   }
   for (auto e : c->pool) (void)hipEventDestroy(e);
-  if (c->ws) (void)hipFree(c->ws);
+  if (c->ws_alloc) (void)hipFree(c->ws_alloc);
   delete c;
   return LRQ_OK;
 }
@@ -312,6 +321,21 @@ int lrq_sync(lrq_ctx* c) {
   LRQ_TRY(begin(c));
   hipError_t e = hipStreamSynchronize(c->stream);
   if (e != hipSuccess) return hip_fail(c, e, "hipStreamSynchronize");
+  // a few-token epilogue that gave up waiting for t leaves a flag in the
+  // counters (the context's own and the device's scratch array)
+  char* scratch = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    scratch = g_scratch[c->device];
+  }
+  const uint32_t* counters[2] = {c->cnt, reinterpret_cast<const uint32_t*>(scratch)};
+  for (const uint32_t* cnt : counters) {
+    if (!cnt) continue;
+    uint32_t flag = 0;
+    e = hipMemcpy(&flag, cnt + SK_FAIL, sizeof(flag), hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return hip_fail(c, e, "hipMemcpy");
+    if (flag) return fail(c, LRQ_EHIP, "a few-token kernel timed out waiting for its t slices; its outputs are invalid");
+  }
   return LRQ_OK;
 }
 
@@ -462,23 +486,27 @@ static int check_gemm(lrq_ctx* c, const lrq_weight* w, int64_t m) {
 
 // Where the forward's workspace comes from: the context's (grown on demand)
 // or, for lrq_lora_fwd_noalloc, the device's static scratch array.
+// Both start with the few-token kernels' arrival counters (LRQ_CNT_BYTES).
 struct WsSource {
   bool scratch;
   char* base;
 };
 
-static int acquire_ws(lrq_ctx* c, WsSource* src, size_t bytes, char** out) {
+static int acquire_ws(lrq_ctx* c, WsSource* src, size_t bytes, char** out, uint32_t** cnt) {
   if (!src->scratch) {
     LRQ_TRY(ensure_ws(c, bytes));
     *out = c->ws;
+    *cnt = c->cnt;
     return LRQ_OK;
   }
-  if (bytes > (size_t)LRQ_NOALLOC_SCRATCH_BYTES)
+  const size_t cap = (size_t)LRQ_NOALLOC_SCRATCH_BYTES - LRQ_CNT_BYTES;
+  if (bytes > cap)
     return fail(c, LRQ_EINVAL,
                 "lrq_lora_fwd_noalloc: this shape needs %zu bytes of scratch, more than its fixed %zu; use "
                 "lrq_lora_fwd",
-                bytes, (size_t)LRQ_NOALLOC_SCRATCH_BYTES);
-  *out = src->base;
+                bytes, cap);
+  *cnt = reinterpret_cast<uint32_t*>(src->base);
+  *out = src->base + LRQ_CNT_BYTES;
   return LRQ_OK;
 }
 
@@ -494,12 +522,14 @@ static int fwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t 
     if (!aligned16(b)) return fail(c, LRQ_EINVAL, "B must be 16-byte aligned");
   }
   char* ws = nullptr;
+  uint32_t* cnt = nullptr;
   if (m >= 1 && m <= 16) {
-    // few tokens: stream the packed weight once (split-k partials, t's
-    // partials alongside), then one epilogue launch
+    // few tokens: one launch streams the packed weight once (split-k
+    // partials, t's partials alongside); the last arrival at each block row
+    // finishes it
     const int rp = lora ? (int)round_up(r, 16) : 0;
     const SkinnyPlan p = skinny_plan(w->n, w->k, rp, get_num_cus());
-    LRQ_TRY(acquire_ws(c, src, skinny_ws_bytes(p, m, w->n, rp), &ws));
+    LRQ_TRY(acquire_ws(c, src, skinny_ws_bytes(p, m, w->n, rp), &ws, &cnt));
     float* part = reinterpret_cast<float*>(ws);
     float* tpart = part + round_up((int64_t)p.S * m * w->n, 64);
     if (lora) {
@@ -507,16 +537,15 @@ static int fwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t 
       ga.r = (int)r;
       ga.rp = rp;
     }
-    LRQ_TRY(run(c, KID_FWD_MAIN, "fwd_main",
-                [&] { return launch_skinny_part(c->stream, w->format, false, ga, lora ? a : nullptr, p, part, tpart); }));
-    return run(c, KID_FWD_EPI, "fwd_epi", [&] {
-      return launch_skinny_epi(c->stream, w->format, false, ga, p, part, tpart, scaling, lora ? t_out : nullptr);
+    return run(c, KID_FWD_MAIN, "fwd_main", [&] {
+      return launch_skinny(c->stream, w->format, false, ga, lora ? a : nullptr, p, part, tpart, cnt, scaling,
+                           lora ? t_out : nullptr);
     });
   }
   if (lora) {
     const int rp = (int)round_up(r, 16);
     LRQ_TRY(check_lora_shapes(c, m, w->n, w->k, rp));
-    LRQ_TRY(acquire_ws(c, src, lora_layout(nullptr, m, w->n, w->k, rp, true).bytes, &ws));
+    LRQ_TRY(acquire_ws(c, src, lora_layout(nullptr, m, w->n, w->k, rp, true).bytes, &ws, &cnt));
     LoraWs lw = lora_layout(ws, m, w->n, w->k, rp, true);
     // t = s . x . A   (bf16 [m, rp] for the fused step, [m, r] for the caller)
     const LoraPlan pt = lora_plan_nt(m, w->k, rp);
@@ -536,7 +565,7 @@ static int fwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t 
   } else {
     const int64_t pf = gemm_split_floats(m, w->n, w->k);
     if (pf > 0) {
-      LRQ_TRY(acquire_ws(c, src, (size_t)pf * 4, &ws));
+      LRQ_TRY(acquire_ws(c, src, (size_t)pf * 4, &ws, &cnt));
       ga.part = reinterpret_cast<float*>(ws);
     }
   }
@@ -584,9 +613,7 @@ int lrq_lora_fwd_noalloc(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int
 static hipError_t launch_dx(lrq_ctx* c, const lrq_weight* w, const GemmArgs& ga, int64_t m, float* skpart) {
   if (m >= 1 && m <= 16) {
     const SkinnyPlan p = skinny_plan(w->k, w->n, 0, get_num_cus());
-    hipError_t e = launch_skinny_part(c->stream, w->format, true, ga, nullptr, p, skpart, nullptr);
-    if (e != hipSuccess) return e;
-    return launch_skinny_epi(c->stream, w->format, true, ga, p, skpart, nullptr, 1.0f, nullptr);
+    return launch_skinny(c->stream, w->format, true, ga, nullptr, p, skpart, nullptr, c->cnt, 1.0f, nullptr);
   }
   return launch_bwd(c->stream, w->format, ga);
 }
@@ -622,14 +649,12 @@ static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const ui
     ga.rp = rp;
     if (few) {
       // few tokens: u = s . dy . B^T (bf16 [m, rp], dA's factor) comes out
-      // of the input gradient's own two launches, as t does in the forward
+      // of the input gradient's own launch, as t does in the forward
       float* part = reinterpret_cast<float*>(c->ws + lbytes);
       float* tpart = part + round_up((int64_t)sp.S * m * w->k, 64);
       ga.lw = a;
       LRQ_TRY(run(c, KID_BWD_DX, "bwd_dx", [&] {
-        hipError_t e = launch_skinny_part(c->stream, w->format, true, ga, b, sp, part, tpart);
-        if (e != hipSuccess) return e;
-        return launch_skinny_epi(c->stream, w->format, true, ga, sp, part, tpart, scaling, ws.up);
+        return launch_skinny(c->stream, w->format, true, ga, b, sp, part, tpart, c->cnt, scaling, ws.up);
       }));
     } else {
       // u = s . dy . B^T   (bf16 [m, rp]: the dx epilogue operand and dA's factor)

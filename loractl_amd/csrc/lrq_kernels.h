@@ -58,28 +58,40 @@ hipError_t launch_bwd(hipStream_t st, int fmt, const GemmArgs& a);
 int64_t gemm_split_floats(int64_t m, int64_t e, int64_t depth);
 int get_num_cus();
 
-// lrq_skinny.hip: the forward for m <= 16 in two launches. `part` streams
-// the packed weight once and writes f32 partials of x . W^T per reduction
-// split ([S][m][n]) and, when a.rp > 0, of x . A per k slice ([TS][16][rp],
-// from the down factor A [k, r]); `epi` sums them in a fixed order and writes
-// y = bf16(sc * base + t . B + bias) with t = bf16(scaling * x . A), and t
-// itself ([m, r]) when t_out is set. a.lw is B [r, n].
-// With bwd, the same two launches give the input gradient for m <= 16 from
-// the transposed section (GemmArgs of the backward, a plan of
+// lrq_skinny.hip: the forward for m <= 16 in one launch. Split workgroups
+// stream the packed weight once and write f32 partials of x . W^T per
+// reduction split ([S][m][n]) and, when a.rp > 0, workgroups over k slices
+// write the partials of x . A ([TS][16][rp], from the down factor A [k, r]).
+// The last workgroup to arrive at a block row of 64 outputs sums them in a
+// fixed order and writes y = bf16(sc * base + t . B + bias) with
+// t = bf16(scaling * x . A), and t itself ([m, r]) when t_out is set. a.lw
+// is B [r, n]. `cnt` holds ceil(n / 64) <= LRQ_CNT_WORDS arrival counters,
+// zero on entry; the kernel leaves them zero.
+// With bwd, the same launch gives the input gradient for m <= 16 from the
+// transposed section (GemmArgs of the backward, a plan of
 // skinny_plan(k, n, rp, .)): dx = bf16(sum of partials + u . A^T) with
-// u = bf16(scaling * dy . B^T) from the partials of dy . B^T (`A` of part is
-// then B [r, n]), written to t_out as [m, rp]; a.lw is A [k, r].
+// u = bf16(scaling * dy . B^T) from the partials of dy . B^T (`A` is then
+// B [r, n]), written to t_out as [m, rp]; a.lw is A [k, r].
 struct SkinnyPlan {
   int S, KS;  // reduction splits of the base, 64-wide blocks per split
   int TS;     // k slices of t (0 without LoRA)
   int64_t KT; // k per t slice (a multiple of 32)
 };
+// arrival counters at the start of every workspace (zeroed when allocated):
+// block rows at [0, SK_MAX_NB), then, one 128-byte line each, the count of
+// finished t slices, the launch epoch (t is published stamped with it), the
+// epilogue count and the failure flag (set when an epilogue gave up waiting
+// for t; lrq_sync reports it)
+constexpr int64_t LRQ_CNT_WORDS = 16384;
+constexpr size_t LRQ_CNT_BYTES = (size_t)LRQ_CNT_WORDS * 4;
+constexpr int64_t SK_MAX_NB = LRQ_CNT_WORDS - 160;
+constexpr int64_t SK_TCNT = LRQ_CNT_WORDS - 128, SK_EPOCH = LRQ_CNT_WORDS - 96, SK_DCNT = LRQ_CNT_WORDS - 64,
+                  SK_FAIL = LRQ_CNT_WORDS - 32;
 SkinnyPlan skinny_plan(int64_t n, int64_t k, int rp, int num_cus);
 size_t skinny_ws_bytes(const SkinnyPlan& p, int64_t m, int64_t n, int rp);
-hipError_t launch_skinny_part(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, const uint16_t* A,
-                              const SkinnyPlan& p, float* part, float* tpart);
-hipError_t launch_skinny_epi(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, const SkinnyPlan& p,
-                             const float* part, const float* tpart, float scaling, uint16_t* t_out);
+hipError_t launch_skinny(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, const uint16_t* A,
+                         const SkinnyPlan& p, float* part, float* tpart, uint32_t* cnt, float scaling,
+                         uint16_t* t_out);
 
 // lrq_lora.hip
 // A split of a LoRA reduction: `tiles` output tiles x `splits` slices of
@@ -142,7 +154,6 @@ enum {
   KID_LORA_DB,
   KID_LORA_RED,
   KID_BLOCK,
-  KID_FWD_EPI,
   KID_LORA_DADB,
   KID_COUNT
 };

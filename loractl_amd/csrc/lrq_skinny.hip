@@ -8,10 +8,10 @@
 // With so few tokens the forward is a stream of the packed weight from HBM;
 // the matrix-core and dequantization work per byte is small, and what
 // matters is keeping enough loads in flight and finishing the math on each
-// block as its bytes arrive. Two launches:
+// block as its bytes arrive. One launch, k_sk:
 //
-// k_sk_part: workgroups (block row nb, reduction split s) own 64 weight rows
-//   x KS 64-wide reduction blocks; each of the four wavefronts takes a run of
+// - Split workgroups (block row nb, reduction split s) own 64 weight rows x
+//   KS 64-wide reduction blocks; each of the four wavefronts takes a run of
 //   those blocks for all 64 rows. A wavefront issues every load of its run
 //   at once, in block order (the x fragments, then per 16-row tile 8 packed
 //   bytes int4 or 16 bytes fp8 per lane; the 16 lanes of a k quarter read 16
@@ -19,19 +19,36 @@
 //   dequantizes and multiplies block by block as the loads land, with
 //   v_mfma_f32_16x16x32_bf16 (tokens as the A-role rows, weight rows as the
 //   B-role columns; lane quarter q takes k = 16q + 8j .. +8 in sub-step j;
-//   each x fragment serves the four row tiles). No wavefront waits for
-//   another until the four runs are summed in LDS; the f32 partial of each
-//   split goes to a workspace. A few more workgroups (scheduled first)
-//   compute the f32 partials of x . A over slices of k.
-// k_sk_epi: per output column, sums the split partials in a fixed order,
-//   applies the fp8 per-channel scale, adds t . B (t rounded to bf16 as in
-//   the large-m path) and the bias, and writes y (and t).
+//   each x fragment serves the four row tiles). The four runs meet in LDS
+//   and the split's f32 partial goes to a workspace.
+// - A few more workgroups (scheduled first) compute the f32 partials of
+//   x . A over slices of k and count themselves done; the last of them sums
+//   the slices in order, rounds t to bf16 (as the large-m path does) and
+//   publishes it (and t itself), every entry stamped with the launch's
+//   epoch in the same 8-byte store.
+// - Each split workgroup then arrives at its block row's counter, and the
+//   last of the S splits runs the block row's epilogue: the split partials
+//   summed in a fixed order, the fp8 per-channel scale, t . B and the bias,
+//   y written. The epilogue reads t with its other loads and takes it once
+//   every stamp is current, reading it again otherwise (the t workgroups
+//   can finish after some splits). That wait always ends: the t workgroups
+//   have the lowest ids, so they are dispatched before any split
+//   workgroup, and they wait on nothing; a cap on the polls (far above any
+//   real wait) ends it even so and flags the failure in the counter area.
+// - Cross-workgroup data is written and read at device scope (sc1: written
+//   through past the non-coherent per-XCD L2s before the store is
+//   acknowledged, and read past them), and each workgroup waits for its
+//   stores before it counts itself, so the epilogue sees every partial
+//   without a cache write-back or invalidate (a device-scope fence per
+//   workgroup costs tens of microseconds here). The counters start at zero and end at zero:
+//   the last split of a block row resets its counter, and the last of the
+//   epilogues resets the t and epilogue counters and advances the epoch.
 //
 // int4 with groups of 64 or more multiplies the integer q exactly and
 // applies the group scale in f32 per 64-wide block (see MQ below), which is
 // the oracle's f32 dequantization; groups of 32 and fp8 use the large-m
-// kernel's operand (bf16(q s), exact e4m3). No atomics: results are bitwise
-// reproducible.
+// kernel's operand (bf16(q s), exact e4m3). No atomic touches a result and
+// every sum has a fixed order: results are bitwise reproducible.
 
 #include "lrq_common.h"
 #include "lrq_kernels.h"
@@ -40,7 +57,7 @@ namespace {
 
 constexpr int SK_NT = 256;     // threads per workgroup (4 wavefronts)
 constexpr int SK_MAXKS = 16;   // reduction blocks per split, at most
-constexpr int SK_TSTEPS = 2;   // 32-wide k steps of a t (u) slice per wavefront (slices <= 256)
+constexpr int SK_TMAX = 32;    // t (u) slices, at most, while a slice needs no more than 4 steps per wavefront
 constexpr int SK_WB = SK_MAXKS / 4;  // blocks per wavefront run, at most
 
 struct SkArgs {
@@ -48,8 +65,144 @@ struct SkArgs {
   const uint16_t* A;  // [k, r] (LoRA down factor), or null
   SkinnyPlan p;
   float* part;        // [S][m][n]
-  float* tpart;       // [TS][16][rp]
+  float* tpart;       // [TS][16][rp] f32, then t itself [16][rp] as (bf16 value as f32, epoch stamp)
+  uint32_t* cnt;      // [ceil(n / 64)] arrival counters, zero on entry and exit
+  float scaling;
+  uint16_t* t_out;    // t [m, r] (backward: u [m, rp]), or null
 };
+
+// device-scope accesses of the cross-workgroup data: stores written through
+// and loads read past the per-XCD L2s (sc1), atomics at device scope
+// (system scope, sc0 sc1, measured the same)
+constexpr int XSCOPE = __HIP_MEMORY_SCOPE_AGENT;
+constexpr int XAUX = 16;  // sc1 on a buffer load
+LRQ_DEV void store_dev(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, XSCOPE); }
+LRQ_DEV u32x4 bload16_dev(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, XAUX); }
+LRQ_DEV float bloadf_dev(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, XAUX));
+}
+LRQ_DEV u32x2 bload8_dev(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, XAUX); }
+// the stamp of epoch ep (never 0, the value of unwritten memory)
+LRQ_DEV uint32_t stamp(uint32_t ep) { return ep + 1 == 0 ? 1u : ep + 1; }
+
+constexpr uint32_t SK_MAX_POLLS = 1u << 22;  // about 0.2 s of s_sleep 2
+
+LRQ_DEV uint32_t add_dev(uint32_t* c) { return __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, XSCOPE); }
+LRQ_DEV void zero_dev(uint32_t* c) { __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, XSCOPE); }
+
+
+// The epilogue of block row nb (output columns 64 nb .. +64), run by the last
+// workgroup to arrive there (all 256 threads, uniform control flow):
+//   y[m, n] = bf16(sc[n] * sum_s part[s][m][n] + sum_j t[m, j] B[j, n] + bias[n])
+// with t as published. Backward: dx[m, k] = bf16(sum_s part[s][m][k] +
+// sum_j u[m, j] A[k, j]) with u from the partials of dy . B^T and A = a.lw
+// [k, r]; no scale, no bias. `lds` holds 3072 floats.
+template <int FMT, bool BWD>
+LRQ_DEV void sk_epilogue(const SkArgs& sa, int64_t nb, float* lds) {
+  const GemmArgs& a = sa.g;
+  const int tid = threadIdx.x;
+  const int64_t M = a.m, E = a.e, n0 = nb * 64;
+  const int rp = a.rp, r = a.r, S = sa.p.S, TS = sa.p.TS;
+  float* tt = lds;                                                  // [16][64] t (bf16 values)
+  uint16_t* bs = reinterpret_cast<uint16_t*>(lds + 16 * 64);       // [64 ranks][64 columns] bf16
+  // thread: token m = tid / 16, columns n .. n + 3 (E % 8 == 0: n < E implies n + 3 < E)
+  const int m = tid >> 4, cq = tid & 15;
+  const int64_t n = n0 + 4 * cq;
+  const bool live = m < M && n < E;
+  // what does not depend on t goes out first: the first four split
+  // partials and the weight-side factor of the block row (B[j][n0 + c]
+  // forward, A[n0 + c][j] backward), so that these loads overlap the t reads
+  const rsrc_t rpt = make_rsrc(sa.part, clamp_bytes((int64_t)S * M * E * 4));
+  u32x4 pv[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+    pv[s] = bload16_dev(rpt, opaque_u32(live && s < S ? (uint32_t)((((int64_t)s * M + m) * E + n) * 4) : LRQ_OOB));
+  const rsrc_t rb = make_rsrc(a.lw, TS > 0 ? clamp_bytes((int64_t)r * E * 2) : 0u);
+  uint32_t bv[16];  // rp * 64 entries over 256 threads
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const int i = tid + q * SK_NT, j = i / 64, c = i % 64;
+    const bool ok = j < r && n0 + c < E;
+    const uint32_t off = BWD ? (uint32_t)(((n0 + c) * r + j) * 2) : (uint32_t)(((int64_t)j * E + n0 + c) * 2);
+    bv[q] = bload2(rb, opaque_u32(ok ? off : LRQ_OOB));
+  }
+  // t (u) [16][rp] as published: this thread's entries i = tid + 256 q,
+  // stamped with the launch's epoch
+  const rsrc_t rtf = make_rsrc(sa.tpart + (int64_t)TS * 16 * rp, TS > 0 ? clamp_bytes((int64_t)16 * rp * 8) : 0u);
+  u32x2 tv[4];
+  auto load_t = [&]() {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int i = tid + q * SK_NT;
+      tv[q] = bload8_dev(rtf, opaque_u32(i < 16 * rp ? (uint32_t)(i * 8) : LRQ_OOB));
+    }
+  };
+  load_t();
+  if (TS > 0) {
+    const uint32_t want = stamp(__hip_atomic_load(sa.cnt + SK_EPOCH, __ATOMIC_RELAXED, XSCOPE));
+    // not all published yet: read all of this thread's entries again
+    for (uint32_t polls = 0;; ++polls) {
+      bool ok = true;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) ok = ok && (tid + q * SK_NT >= 16 * rp || tv[q][1] == want);
+      if (ok) break;
+      if (polls == SK_MAX_POLLS) {
+        __hip_atomic_store(sa.cnt + SK_FAIL, 1u, __ATOMIC_RELAXED, XSCOPE);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+      load_t();
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int i = tid + q * SK_NT;
+      if (i < 16 * rp) tt[(i / rp) * 64 + i % rp] = __uint_as_float(tv[q][0]);
+    }
+#pragma unroll
+    for (int q = 0; q < 16; ++q)
+      if (tid + q * SK_NT < rp * 64) bs[tid + q * SK_NT] = (uint16_t)bv[q];
+  }
+  __syncthreads();
+  if (live) {
+    float base[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) base[e] += __uint_as_float(pv[s][e]);
+    for (int s0 = 4; s0 < S; s0 += 4) {  // splits past the first four, in order, four loads issued together
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        pv[s] = bload16_dev(rpt, opaque_u32(s0 + s < S ? (uint32_t)((((int64_t)(s0 + s) * M + m) * E + n) * 4) : LRQ_OOB));
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) base[e] += __uint_as_float(pv[s][e]);
+    }
+    float l[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < (TS > 0 ? rp : 0); ++j) {  // t and the factor rows exist only with t slices
+      const float tv = tt[m * 64 + j];
+      const u32x2 bv = *reinterpret_cast<const u32x2*>(bs + j * 64 + 4 * cq);
+      l[0] = __builtin_fmaf(tv, __uint_as_float(bv[0] << 16), l[0]);
+      l[1] = __builtin_fmaf(tv, __uint_as_float(bv[0] & 0xffff0000u), l[1]);
+      l[2] = __builtin_fmaf(tv, __uint_as_float(bv[1] << 16), l[2]);
+      l[3] = __builtin_fmaf(tv, __uint_as_float(bv[1] & 0xffff0000u), l[3]);
+    }
+    float sc[4] = {1.0f, 1.0f, 1.0f, 1.0f}, bias[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (!BWD && FMT == LRQ_FMT_FP8) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sc[e] = a.wscale[a.per_channel ? n + e : 0];
+    }
+    if (!BWD && a.bias) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bias[e] = a.bias[n + e];
+    }
+    u32x2 o;
+    o[0] = pack_bf16x2(base[0] * sc[0] + l[0] + bias[0], base[1] * sc[1] + l[1] + bias[1]);
+    o[1] = pack_bf16x2(base[2] * sc[2] + l[2] + bias[2], base[3] * sc[3] + l[3] + bias[3]);
+    *reinterpret_cast<u32x2*>(a.out + (int64_t)m * E + n) = o;
+  }
+}
+
 
 // MQ (int4 forward, groups of 64 or more, so one group per 64-wide block):
 // the matrix-core operand is the stored nibble u = q + 8 as the exact bf16
@@ -57,11 +210,13 @@ struct SkArgs {
 // is multiplied into fresh accumulators, and the block's partial is scaled
 // in f32: s * (sum x (128 + u) - 136 sum x) = s * sum x q. The block sums of
 // x come from one more matrix-core step against ones.
-template <int FMT, bool BWD, bool MQ>
-__global__ void __launch_bounds__(SK_NT) k_sk_part(SkArgs sa) {
+// TSTEPS: 32-wide k steps per wavefront of a t (u) slice (1, 2 or 4)
+template <int FMT, bool BWD, bool MQ, int TSTEPS>
+__global__ void __launch_bounds__(SK_NT) k_sk(SkArgs sa) {
   constexpr bool I4 = FMT == LRQ_FMT_INT4;
   // cross-wavefront reduction buffer: [4 wavefronts][64 columns][16 tokens]
   __shared__ __attribute__((aligned(16))) float xs[4 * 64 * 16];
+  __shared__ int last;  // this workgroup was the last of its block row (t: of the t slices)
   const GemmArgs& a = sa.g;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -75,19 +230,18 @@ __global__ void __launch_bounds__(SK_NT) k_sk_part(SkArgs sa) {
     // (backward: of dy[m, n] B[j, n], for u)
     const int ts = blockIdx.x, rp = a.rp, r = a.r;
     const int64_t kt0 = (int64_t)ts * sa.p.KT, kt1 = kt0 + sa.p.KT < K ? kt0 + sa.p.KT : K;
-    const int nsteps = (int)((kt1 - kt0 + 31) / 32);  // <= 4 * SK_TSTEPS
+    const int nsteps = (int)((kt1 - kt0 + 31) / 32);
     const rsrc_t rx = make_rsrc(a.act, clamp_bytes(M * K * 2));
     const rsrc_t ra = make_rsrc(sa.A, clamp_bytes(K * r * 2));
     f32x4 acc[4];
 #pragma unroll
     for (int jt = 0; jt < 4; ++jt) acc[jt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-    // one k step per phase: each issues all its loads (out-of-range ones
-    // read zero) before its matrix-core steps, in few enough registers that
-    // the streaming workgroups keep their occupancy
-    u32x4 xf[SK_TSTEPS];
-    uint32_t bw[SK_TSTEPS][4][4];
+    // every load of the slice (at most 4 * TSTEPS steps) is issued at once
+    // (out-of-range ones read zero), then the matrix-core steps run as they land
+    u32x4 xf[TSTEPS];
+    uint32_t bw[TSTEPS][4][4];
 #pragma unroll
-    for (int i = 0; i < SK_TSTEPS; ++i) {
+    for (int i = 0; i < TSTEPS; ++i) {
       {
         const int st = wv + (SK_NT / 64) * i;
         const int64_t k = kt0 + (int64_t)st * 32 + kq * 8;
@@ -112,15 +266,17 @@ __global__ void __launch_bounds__(SK_NT) k_sk_part(SkArgs sa) {
           }
         }
       }
-      // every column tile runs (tiles past rp multiply zeros): a matrix-core
-      // result read in a block other than the one that wrote it has come
-      // back stale here, so the steps stay branch-free
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // every column tile runs (tiles past rp multiply zeros): a matrix-core
+    // result read in a block other than the one that wrote it has come back
+    // stale here, so the steps stay branch-free
+#pragma unroll
+    for (int i = 0; i < TSTEPS; ++i)
 #pragma unroll
       for (int jt = 0; jt < 4; ++jt)
         acc[jt] = mfma16(as_bf16x8(xf[i]), as_bf16x8((u32x4){bw[i][jt][0], bw[i][jt][1], bw[i][jt][2], bw[i][jt][3]}),
                          acc[jt]);
-      __builtin_amdgcn_sched_barrier(0);
-    }
     // reduce the four wavefronts; C element v of lane l: token 4*(l/16) + v, column l%16
     float* tred = xs;  // [4][16][64]
 #pragma unroll
@@ -133,7 +289,44 @@ __global__ void __launch_bounds__(SK_NT) k_sk_part(SkArgs sa) {
       float v = 0.0f;
 #pragma unroll
       for (int w2 = 0; w2 < SK_NT / 64; ++w2) v += tred[(w2 * 16 + m) * 64 + j];
-      sa.tpart[((int64_t)ts * 16 + m) * rp + j] = v;
+      store_dev(sa.tpart + ((int64_t)ts * 16 + m) * rp + j, v);
+    }
+    // counted done once every store of the workgroup is acknowledged at
+    // device scope; the last slice's workgroup sums the slices in order (two
+    // entries per thread, every slice's loads issued at once), rounds t to
+    // bf16 and publishes it, stamped with the launch's epoch
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) last = add_dev(sa.cnt + SK_TCNT) + 1 == (uint32_t)TS;
+    __syncthreads();
+    if (!last) return;
+    const rsrc_t rtp = make_rsrc(sa.tpart, clamp_bytes((int64_t)TS * 16 * rp * 4));
+    uint64_t* tfin = reinterpret_cast<uint64_t*>(sa.tpart + (int64_t)TS * 16 * rp);
+    // the epoch cannot advance before this workgroup publishes t: every
+    // epilogue of the launch waits for it
+    const uint32_t mark = stamp(__hip_atomic_load(sa.cnt + SK_EPOCH, __ATOMIC_RELAXED, XSCOPE));
+    // two entries per thread and pass (rp % 16 == 0: both in one token row)
+    for (int e0 = 2 * tid; e0 < 16 * rp; e0 += 2 * SK_NT) {
+      float v[2] = {0.0f, 0.0f};
+      for (int q0 = 0; q0 < TS; q0 += SK_TMAX) {  // slices in order
+        u32x2 part[SK_TMAX];
+#pragma unroll
+        for (int q = 0; q < SK_TMAX; ++q)
+          part[q] = bload8_dev(rtp, opaque_u32(q0 + q < TS ? (uint32_t)(((q0 + q) * 16 * rp + e0) * 4) : LRQ_OOB));
+#pragma unroll
+        for (int q = 0; q < SK_TMAX; ++q) {
+          v[0] += __uint_as_float(part[q][0]);
+          v[1] += __uint_as_float(part[q][1]);
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int i = e0 + e, m = i / rp, j = i % rp;
+        const uint32_t hb = pack_bf16x2(sa.scaling * v[e], 0.0f) & 0xffffu;  // t (u) as the caller sees it
+        // value and stamp in one 8-byte store: a reader sees both or neither
+        __hip_atomic_store(tfin + i, ((uint64_t)mark << 32) | (hb << 16), __ATOMIC_RELAXED, XSCOPE);
+        if (sa.t_out && m < M && (BWD || j < r)) sa.t_out[(int64_t)m * (BWD ? rp : r) + j] = (uint16_t)hb;
+      }
     }
     return;
   }
@@ -295,161 +488,26 @@ __global__ void __launch_bounds__(SK_NT) k_sk_part(SkArgs sa) {
       float v = 0.0f;
 #pragma unroll
       for (int w2 = 0; w2 < 4; ++w2) v += red[((w2 * 4 + rt) * 16 + m) * 16 + c];
-      if (n < E) sa.part[((int64_t)s * M + m) * E + n] = v;
+      if (n < E) store_dev(sa.part + ((int64_t)s * M + m) * E + n, v);
     }
   }
-}
-
-// y[m, n] = bf16(sc[n] * sum_s part[s][m][n] + sum_j t[m, j] B[j, n] + bias[n]).
-// Every workgroup first reduces t = bf16(scale * sum_ts tpart[ts]) into LDS.
-// Backward: dx[m, k] = bf16(sum_s part[s][m][k] + sum_j u[m, j] A[k, j]) with
-// u = bf16(scaling * sum_ts tpart[ts]) (t_out gets u [m, rp]) and A = a.lw
-// [k, r] (no scale: the transposed weight's scales are applied per value,
-// no bias).
-// A thread owns two adjacent columns and four tokens. Every load is a
-// buffer load whose out-of-range offsets read zero, so none sits behind a
-// branch and all of a thread's loads issue together.
-template <int FMT, bool BWD>
-__global__ void __launch_bounds__(SK_NT) k_sk_epi(SkArgs sa, float scaling, uint16_t* t_out) {
-  const GemmArgs& a = sa.g;
-  const int tid = threadIdx.x;
-  const int64_t M = a.m, E = a.e;
-  const int rp = a.rp, r = a.r, S = sa.p.S, TS = sa.p.TS;
-  __shared__ __attribute__((aligned(16))) float tt[16][64];
-  const int64_t n = (int64_t)blockIdx.x * 128 + 2 * (tid & 63);  // E % 8 == 0: n < E implies n + 1 < E
-  const int mg = tid >> 6;                                        // tokens 4 mg .. 4 mg + 3
-  const bool live = n < E && 4 * mg < M;
-  // this thread's loads go out first, so that they share one memory round
-  // trip with the reduction of t below (dead threads' offsets read zero)
-  const rsrc_t rb = make_rsrc(a.lw, clamp_bytes((int64_t)r * E * 2));
-  const rsrc_t rpt = make_rsrc(sa.part, clamp_bytes((int64_t)S * M * E * 4));
-  const rsrc_t rbias = make_rsrc(a.bias, a.bias ? clamp_bytes(E * 4) : 0u);
-  // bp[j]: the weight-side factor at columns n (low half) and n + 1 (high)
-  uint32_t bp[64];
-  if (BWD) {
-    // A[n][j] and A[n + 1][j] from A [k, r]: rows of 16-byte runs when r is
-    // a multiple of 8 and A is 16-byte aligned, else value by value
-    if ((r & 7) == 0 && (reinterpret_cast<uintptr_t>(a.lw) & 15) == 0) {
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const bool ok = live && q * 8 < r;
-        const u32x4 v0 = bload16(rb, opaque_u32(ok ? (uint32_t)((n * r + q * 8) * 2) : LRQ_OOB));
-        const u32x4 v1 = bload16(rb, opaque_u32(ok ? (uint32_t)(((n + 1) * r + q * 8) * 2) : LRQ_OOB));
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          bp[q * 8 + 2 * e] = __builtin_amdgcn_perm(v1[e], v0[e], 0x05040100u);
-          bp[q * 8 + 2 * e + 1] = __builtin_amdgcn_perm(v1[e], v0[e], 0x07060302u);
-        }
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 64; ++j) {
-        const bool ok = live && j < r;
-        const uint32_t lo = bload2(rb, opaque_u32(ok ? (uint32_t)((n * r + j) * 2) : LRQ_OOB));
-        const uint32_t hi = bload2(rb, opaque_u32(ok ? (uint32_t)(((n + 1) * r + j) * 2) : LRQ_OOB));
-        bp[j] = lo | (hi << 16);
-      }
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < 64; ++j)
-      bp[j] = bload4(rb, opaque_u32(live && j < r ? (uint32_t)(((int64_t)j * E + n) * 2) : LRQ_OOB));
-  }
-  u32x2 pv[4][8];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int m = 4 * mg + i;
-#pragma unroll
-    for (int s = 0; s < 8; ++s)
-      pv[i][s] = bload8(rpt, opaque_u32((live && s < S && m < M) ? (uint32_t)((((int64_t)s * M + m) * E + n) * 4)
-                                                                   : LRQ_OOB));
-  }
-  float sc0 = 1.0f, sc1 = 1.0f;
-  if (!BWD && FMT == LRQ_FMT_FP8) {
-    const rsrc_t rsc = make_rsrc(a.wscale, clamp_bytes((a.per_channel ? E : 1) * 4));
-    const uint32_t c0 = a.per_channel ? (uint32_t)(n * 4) : 0u;
-    sc0 = bloadf(rsc, opaque_u32(live ? c0 : LRQ_OOB));
-    sc1 = bloadf(rsc, opaque_u32(live ? c0 + (a.per_channel ? 4u : 0u) : LRQ_OOB));
-  }
-  const u32x2 bias = bload8(rbias, opaque_u32(live ? (uint32_t)(n * 4) : LRQ_OOB));
-
-  const rsrc_t rtp = make_rsrc(sa.tpart, clamp_bytes((int64_t)TS * 16 * rp * 4));
-  // two outputs per thread and pass (entries i and i + SK_NT of [16][rp]),
-  // slices in order, 16 loads of each issued together per batch
-  for (int i0 = tid; i0 < 16 * rp; i0 += 2 * SK_NT) {
-    float v[2] = {0.0f, 0.0f};
-    for (int q0 = 0; q0 < TS; q0 += 16) {
-      float part[2][16];
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-          const int i = i0 + h * SK_NT;
-          part[h][q] = bloadf(rtp, opaque_u32((q0 + q < TS && i < 16 * rp) ? (uint32_t)(((q0 + q) * 16 * rp + i) * 4)
-                                                                           : LRQ_OOB));
-        }
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int q = 0; q < 16; ++q) v[h] += part[h][q];
-    }
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int i = i0 + h * SK_NT;
-      if (i >= 16 * rp) break;
-      const int m = i / rp, j = i % rp;
-      const uint32_t hb = pack_bf16x2(scaling * v[h], 0.0f) & 0xffffu;  // t (u) as the caller sees it
-      tt[m][j] = __uint_as_float(hb << 16);
-      // t [m, r]; u [m, rp] (columns >= r zero), dA's factor
-      if (blockIdx.x == 0 && t_out && m < M && (BWD || j < r)) t_out[(int64_t)m * (BWD ? rp : r) + j] = (uint16_t)hb;
-    }
+  // arrive once every store of the workgroup is acknowledged at device scope;
+  // the last of the block row's S splits runs its epilogue, once t is in
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) {
+    last = add_dev(sa.cnt + nb) + 1 == (uint32_t)S;
+    if (last) zero_dev(sa.cnt + nb);
   }
   __syncthreads();
-  if (!live) return;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int m = 4 * mg + i;
-    if (m >= M) break;
-    float base0 = 0.0f, base1 = 0.0f;
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      base0 += __uint_as_float(pv[i][s][0]);
-      base1 += __uint_as_float(pv[i][s][1]);
-    }
-    // splits past the first eight, in order, eight loads issued together
-    for (int s0 = 8; s0 < S; s0 += 8) {
-      u32x2 pw[8];
-#pragma unroll
-      for (int s = 0; s < 8; ++s)
-        pw[s] = bload8(rpt, opaque_u32(s0 + s < S ? (uint32_t)((((int64_t)(s0 + s) * M + m) * E + n) * 4) : LRQ_OOB));
-#pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        base0 += __uint_as_float(pw[s][0]);
-        base1 += __uint_as_float(pw[s][1]);
-      }
-    }
-    float l0 = 0.0f, l1 = 0.0f;
-#pragma unroll
-    for (int jc = 0; jc < 4; ++jc) {
-      if (jc * 16 < rp) {  // rank chunks of 16 (rp is a multiple of 16)
-        float4 tv[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) tv[q] = *reinterpret_cast<const float4*>(&tt[m][jc * 16 + 4 * q]);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float t4[4] = {tv[q].x, tv[q].y, tv[q].z, tv[q].w};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t bv = bp[jc * 16 + 4 * q + e];
-            l0 = __builtin_fmaf(t4[e], __uint_as_float(bv << 16), l0);
-            l1 = __builtin_fmaf(t4[e], __uint_as_float(bv & 0xffff0000u), l1);
-          }
-        }
-      }
-    }
-    const uint32_t o = pack_bf16x2(base0 * sc0 + l0 + __uint_as_float(bias[0]),
-                                   base1 * sc1 + l1 + __uint_as_float(bias[1]));
-    *reinterpret_cast<uint32_t*>(a.out + (int64_t)m * E + n) = o;
+  if (!last) return;
+  sk_epilogue<FMT, BWD>(sa, nb, xs);
+  // the last epilogue of the launch resets the t and epilogue counters and
+  // advances the epoch (every read of t, and of the epoch, is over by then)
+  if (tid == 0 && add_dev(sa.cnt + SK_DCNT) + 1 == (uint32_t)((E + 63) / 64)) {
+    zero_dev(sa.cnt + SK_TCNT);
+    zero_dev(sa.cnt + SK_DCNT);
+    add_dev(sa.cnt + SK_EPOCH);
   }
 }
 
@@ -471,61 +529,55 @@ SkinnyPlan skinny_plan(int64_t n, int64_t k, int rp, int num_cus) {
   if (S < 1) S = 1;
   p.KS = (int)((KB + S - 1) / S);
   p.S = (int)((KB + p.KS - 1) / p.KS);  // every split holds at least one block
-  // t: slices of at most 256 k (multiples of 32)
+  // t: slices of 128, 256 or 512 k (one, two or four 32-wide steps per
+  // wavefront), the smallest that keeps the slices at 32 or fewer
   if (rp > 0) {
-    const int64_t kmax = 32 * 4 * SK_TSTEPS;
-    int64_t TS = (k + kmax - 1) / kmax;
-    if (TS < 1) TS = 1;
-    p.KT = ((k + TS - 1) / TS + 31) / 32 * 32;
+    int64_t steps = 1;
+    while (steps < 4 && (k + 128 * steps - 1) / (128 * steps) > SK_TMAX) steps *= 2;
+    p.KT = 128 * steps;
     p.TS = (int)((k + p.KT - 1) / p.KT);
+    if (p.TS < 1) p.TS = 1;
   }
   return p;
 }
 
 size_t skinny_ws_bytes(const SkinnyPlan& p, int64_t m, int64_t n, int rp) {
-  const size_t part = (size_t)p.S * m * n * 4, tp = (size_t)p.TS * 16 * rp * 4;
+  const size_t part = (size_t)p.S * m * n * 4, tp = (size_t)(p.TS + 2) * 16 * rp * 4;
   return (part + 255) / 256 * 256 + tp + 256;
 }
 
-hipError_t launch_skinny_part(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, const uint16_t* A,
-                              const SkinnyPlan& p, float* part, float* tpart) {
-  if (a.m <= 0 || a.m > 16 || p.S < 1 || p.KS < 1 || p.KS > SK_MAXKS) return hipErrorInvalidValue;
-  SkArgs sa{a, A, p, part, tpart};
-  if (a.rp == 0 || !A) sa.p.TS = 0;
+hipError_t launch_skinny(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, const uint16_t* A,
+                         const SkinnyPlan& p, float* part, float* tpart, uint32_t* cnt, float scaling,
+                         uint16_t* t_out) {
   const int64_t NB = (a.e + 63) / 64;
+  if (a.m <= 0 || a.m > 16 || p.S < 1 || p.KS < 1 || p.KS > SK_MAXKS || !cnt || NB > SK_MAX_NB)
+    return hipErrorInvalidValue;
+  SkArgs sa{a, A, p, part, tpart, cnt, scaling, t_out};
+  if (a.rp == 0 || !A) sa.p.TS = 0;
   const unsigned grid = (unsigned)(NB * p.S + sa.p.TS);
-  if (fmt == LRQ_FMT_INT4) {
-    if (bwd)
-      hipLaunchKernelGGL((k_sk_part<LRQ_FMT_INT4, true, false>), dim3(grid), dim3(SK_NT), 0, st, sa);
-    else if (a.gshift >= 6)
-      hipLaunchKernelGGL((k_sk_part<LRQ_FMT_INT4, false, true>), dim3(grid), dim3(SK_NT), 0, st, sa);
-    else
-      hipLaunchKernelGGL((k_sk_part<LRQ_FMT_INT4, false, false>), dim3(grid), dim3(SK_NT), 0, st, sa);
-  } else {
-    if (bwd)
-      hipLaunchKernelGGL((k_sk_part<LRQ_FMT_FP8, true, false>), dim3(grid), dim3(SK_NT), 0, st, sa);
-    else
-      hipLaunchKernelGGL((k_sk_part<LRQ_FMT_FP8, false, false>), dim3(grid), dim3(SK_NT), 0, st, sa);
+  // 32-wide steps per wavefront of a t slice (skinny_plan; 0 without t)
+  const int steps = (int)(p.KT / 128);
+#define SK_LAUNCH(F, B, Q)                                                                             \
+  switch (steps) {                                                                                     \
+    case 4: case 3: hipLaunchKernelGGL((k_sk<F, B, Q, 4>), dim3(grid), dim3(SK_NT), 0, st, sa); break; \
+    case 2: hipLaunchKernelGGL((k_sk<F, B, Q, 2>), dim3(grid), dim3(SK_NT), 0, st, sa); break;       \
+    default: hipLaunchKernelGGL((k_sk<F, B, Q, 1>), dim3(grid), dim3(SK_NT), 0, st, sa); break;      \
   }
-  return hipGetLastError();
-}
-
-hipError_t launch_skinny_epi(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, const SkinnyPlan& p,
-                             const float* part, const float* tpart, float scaling, uint16_t* t_out) {
-  if (a.m <= 0 || a.m > 16) return hipErrorInvalidValue;
-  SkArgs sa{a, nullptr, p, const_cast<float*>(part), const_cast<float*>(tpart)};
-  if (a.rp == 0 || !tpart) sa.p.TS = 0;
-  const unsigned grid = (unsigned)((a.e + 127) / 128);
   if (fmt == LRQ_FMT_INT4) {
-    if (bwd)
-      hipLaunchKernelGGL((k_sk_epi<LRQ_FMT_INT4, true>), dim3(grid), dim3(SK_NT), 0, st, sa, scaling, t_out);
-    else
-      hipLaunchKernelGGL((k_sk_epi<LRQ_FMT_INT4, false>), dim3(grid), dim3(SK_NT), 0, st, sa, scaling, t_out);
+    if (bwd) {
+      SK_LAUNCH(LRQ_FMT_INT4, true, false)
+    } else if (a.gshift >= 6) {
+      SK_LAUNCH(LRQ_FMT_INT4, false, true)
+    } else {
+      SK_LAUNCH(LRQ_FMT_INT4, false, false)
+    }
   } else {
-    if (bwd)
-      hipLaunchKernelGGL((k_sk_epi<LRQ_FMT_FP8, true>), dim3(grid), dim3(SK_NT), 0, st, sa, scaling, t_out);
-    else
-      hipLaunchKernelGGL((k_sk_epi<LRQ_FMT_FP8, false>), dim3(grid), dim3(SK_NT), 0, st, sa, scaling, t_out);
+    if (bwd) {
+      SK_LAUNCH(LRQ_FMT_FP8, true, false)
+    } else {
+      SK_LAUNCH(LRQ_FMT_FP8, false, false)
+    }
   }
+#undef SK_LAUNCH
   return hipGetLastError();
 }

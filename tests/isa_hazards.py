@@ -6,9 +6,10 @@ must put enough independent instructions (or s_nop) in between. On gfx950
 the required distance for a read or write by a VALU, LDS, VMEM or
 accumulator-move instruction, and for a SrcA/SrcB read by another MFMA, is
 passes + 4 wait states (8 for v_mfma_f32_16x16x32_bf16, 4 passes; 12 for
-v_mfma_f32_32x32x16_bf16, 8 passes). An MFMA that accumulates into exactly
-the previous one's destination (SrcC = vDst, the chained accumulation) is
-the one access that needs none.
+v_mfma_f32_32x32x16_bf16, 8 passes). An MFMA whose SrcC is exactly the
+earlier MFMA's destination (full overlap: the chained accumulation, whatever
+its own destination) is the one access that needs none; a partial overlap
+of SrcC, or any overlap of SrcA/SrcB, is checked like the rest.
 
 This module compiles HIP sources to assembly (hipcc --cuda-device-only -S),
 splits the kernels into instructions and basic blocks, and walks every path
@@ -191,9 +192,12 @@ def check_kernel(k: Kernel) -> tuple:
             if touched:
                 ok = False
                 if nxt.mnem.startswith("v_mfma"):
-                    # chained accumulation: SrcC and vDst exactly the earlier vDst
+                    # chained accumulation: SrcC exactly the earlier vDst, which
+                    # the new vDst may overwrite in place or not at all
                     src_ab = _regs(nxt.ops[1]) | _regs(nxt.ops[2])
-                    ok = not (src_ab & dst) and _regs(nxt.ops[3]) == dst and _regs(nxt.ops[0]) == dst
+                    new_dst = _regs(nxt.ops[0])
+                    ok = (not (src_ab & dst) and _regs(nxt.ops[3]) == dst
+                          and (new_dst == dst or not (new_dst & dst)))
                 if not ok:
                     out.append(Violation(k.name, i, ins.text, j, nxt.text, dist, need))
                 continue  # stop on this path at the first access

@@ -94,3 +94,25 @@ def test_skinny_zero_b_is_bitwise_no_op(cuda):
     xd = to_dev(x, cuda)
     y, _ = D.lora_fwd(xd, wq, to_dev(a, cuda), torch.zeros(r, N, dtype=torch.bfloat16, device=cuda), 1.0)
     assert torch.equal(y, D.quant_matmul_t(xd, wq))
+
+
+def test_few_token_counters_leave_no_failure_flag(cuda):
+    """The single-launch few-token kernels finish through arrival counters
+    and a bounded wait for the t slices; after forward and backward calls at
+    m <= 16 (with and without LoRA) and a repeat of each, lrq_sync reports no
+    timed-out wait, and the repeat reproduces the first result bit for bit
+    (the counters were left at zero)."""
+    M, K, N, r = 9, 3072, 4096, 32
+    w, x, a, b, dy = case_inputs(M, K, N, r, seed=5, b_sigma=0.05)
+    wq, _ = _weight(w, "int4", 64, cuda)
+    xd, ad, bd, dyd = to_dev(x, cuda), to_dev(a, cuda), to_dev(b, cuda), to_dev(dy, cuda)
+    outs = []
+    for _ in range(2):
+        y, t = D.lora_fwd(xd, wq, ad, bd, 0.5)
+        dx, da, db = D.lora_bwd(xd, dyd, wq, ad, bd, 0.5, t)
+        base = D.quant_matmul_t(xd, wq)
+        gx = D.quant_matmul_t_bwd(dyd, wq)
+        outs.append([v.clone() for v in (y, t, dx, da, db, base, gx)])
+    D.context().call("lrq_sync")
+    for u, v in zip(*outs):
+        assert torch.equal(u, v)

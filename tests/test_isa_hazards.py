@@ -50,6 +50,17 @@ def test_checker_follows_a_branch_join():
     assert n == 1 and len(v) == 1 and v[0].distance == 3 and v[0].insn.startswith("ds_write_b32")
 
 
+def test_checker_allows_a_chain_into_other_registers_but_not_a_partial_srcc():
+    ks = _listing("\tv_mfma_f32_16x16x32_bf16 a[4:7], v[6:9], v[10:13], a[12:15]\n"
+                  "\tv_mfma_f32_16x16x32_bf16 a[0:3], v[14:17], v[18:21], a[4:7]\n")
+    v, n = H.check_kernel(ks[0])
+    assert n == 2 and not v
+    ks = _listing("\tv_mfma_f32_16x16x32_bf16 a[4:7], v[6:9], v[10:13], a[12:15]\n"
+                  "\tv_mfma_f32_16x16x32_bf16 a[0:3], v[14:17], v[18:21], a[2:5]\n")
+    v, n = H.check_kernel(ks[0])
+    assert len(v) == 1 and v[0].distance == 0
+
+
 def test_checker_allows_chained_accumulation():
     ks = _listing("\tv_mfma_f32_16x16x32_bf16 v[2:5], v[6:9], v[10:13], v[2:5]\n"
                   "\tv_mfma_f32_16x16x32_bf16 v[2:5], v[14:17], v[18:21], v[2:5]\n\ts_nop 7\n"

@@ -67,6 +67,7 @@ def test_noalloc_rejects_a_shape_beyond_its_scratch(cuda):
     wq, xb, ab, bb = _case(cuda, M, K, N, r, "int4", 5)
     y = torch.empty((M, N), dtype=torch.bfloat16, device=cuda)
     t = torch.empty((M, r), dtype=torch.bfloat16, device=cuda)
-    with pytest.raises(L.LrqError, match="more than its fixed 33554432"):
+    # the array's first 64 KiB hold the few-token kernels' arrival counters
+    with pytest.raises(L.LrqError, match=f"more than its fixed {(32 << 20) - (64 << 10)}"):
         D.lora_fwd_noalloc(xb, wq, ab, bb, 1.0, y, t)
     assert L.LRQ_NOALLOC_SCRATCH_BYTES == 32 << 20
