@@ -58,9 +58,8 @@ static int init_scratch(int device) {
 
 namespace {
 
-const char* kNames[KID_COUNT] = {"quantize_int4", "quantize_fp8", "dequant", "fwd_main", "bwd_dx",
-                                 "lora_t",        "lora_u",       "lora_da", "lora_db",  "lora_reduce",
-                                 "block",         "lora_dadb"};
+const char* kNames[KID_COUNT] = {"quantize_int4", "quantize_fp8", "dequant", "fwd_main", "bwd_dx", "lora_t",
+                                 "lora_u",        "lora_da",      "lora_db", "block",    "lora_dadb"};
 
 int fail(lrq_ctx* c, int code, const char* fmt, ...) {
   if (c) {
@@ -216,7 +215,8 @@ LoraWs lora_layout(char* base, int64_t m, int64_t n, int64_t k, int rp, bool fwd
 
 // Shape limit of the LoRA kernels: 32-bit buffer offsets over one slice.
 int check_lora_shapes(lrq_ctx* c, int64_t m, int64_t n, int64_t k, int rp) {
-  const LoraPlan pa = lora_plan_tn(m, k, rp), pb = lora_plan_tn(m, n, rp);
+  // the widest slices are those of the two jobs launched together
+  const LoraPlan pa = lora_plan_tn(m, k, rp, n), pb = lora_plan_tn(m, n, rp, k);
   const int64_t span = std::max(std::max(16 * std::max(n, k), (pa.per + 256) * k), (pb.per + 256) * n) * 2;
   if (span >= (int64_t)1 << 31)
     return fail(c, LRQ_EUNSUPPORTED, "LoRA shape m=%lld n=%lld k=%lld exceeds 2 GiB per slice",
@@ -549,13 +549,12 @@ static int fwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t 
     LoraWs lw = lora_layout(ws, m, w->n, w->k, rp, true);
     // t = s . x . A   (bf16 [m, rp] for the fused step, [m, r] for the caller)
     const LoraPlan pt = lora_plan_nt(m, w->k, rp);
+    // fp8: B^T divided by the weight scale (the GEMM scales base + LoRA)
+    const bool f8 = w->format == LRQ_FMT_FP8;
+    const NtFinish fin{cnt,  scaling, (int)r, lw.tp,  t_out, b, w->n, 0,
+                       lw.fr, f8 ? w->scales : nullptr, (f8 && w->per_channel) ? 1 : 0};
     LRQ_TRY(run(c, KID_LORA_T, "lora_t", [&] {
-      hipError_t e = launch_lora_nt(c->stream, x, a, false, r, (int)r, m, w->k, rp, pt, lw.pn);
-      if (e != hipSuccess) return e;
-      // fp8: B^T divided by the weight scale (the GEMM scales base + LoRA)
-      const bool f8 = w->format == LRQ_FMT_FP8;
-      return launch_nt_reduce(c->stream, lw.pn, pt.splits, m, rp, (int)r, scaling, lw.tp, t_out, b, w->n, false,
-                              lw.fr, f8 ? w->scales : nullptr, f8 && w->per_channel);
+      return launch_lora_nt(c->stream, x, a, false, r, (int)r, m, w->k, rp, pt, lw.pn, fin);
     }));
     ga.lact = lw.tp;
     ga.lw = lw.fr;
@@ -660,11 +659,9 @@ static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const ui
       // u = s . dy . B^T   (bf16 [m, rp]: the dx epilogue operand and dA's factor)
       const LoraPlan pu = lora_plan_nt(m, w->n, rp);
       LRQ_TRY(run(c, KID_LORA_U, "lora_u", [&] {
-        hipError_t e = launch_lora_nt(c->stream, dy, b, true, w->n, (int)r, m, w->n, rp, pu, ws.pn);
-        if (e != hipSuccess) return e;
         // and A [k, r] padded to [k, rp]: the dx GEMM's weight-side LoRA rows
-        return launch_nt_reduce(c->stream, ws.pn, pu.splits, m, rp, (int)r, scaling, ws.up, nullptr, a, w->k,
-                                true, ws.fr);
+        const NtFinish fin{c->cnt, scaling, (int)r, ws.up, nullptr, a, w->k, 1, ws.fr, nullptr, 0};
+        return launch_lora_nt(c->stream, dy, b, true, w->n, (int)r, m, w->n, rp, pu, ws.pn, fin);
       }));
       ga.lact = ws.up;
       ga.lw = ws.fr;
@@ -672,27 +669,19 @@ static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const ui
       if (dx) LRQ_TRY(run(c, KID_BWD_DX, "bwd_dx", [&] { return launch_bwd(c->stream, w->format, ga); }));
     }
     // dA = x^T . u -> f32 [k, r] and dB = t^T . dy -> f32 [r, n]: token-slice
-    // partials in one launch (dB's longer workgroups dispatched first), then
-    // one reduction launch for both
-    // (a job of one token slice writes its result directly, unreduced)
+    // partials of both in one launch (dB's longer workgroups dispatched
+    // first), each column tile finished by its last slice
     TnSpec specs[2];
-    TnJob jobs[2];
-    int nj = 0, nr = 0;
-    if (db) {
-      const LoraPlan pb = lora_plan_tn(m, w->n, rp);
-      specs[nj++] = TnSpec{dy, t, r, m, w->n, (int)r, pb, ws.pb, db, 1, w->n};
-      if (pb.splits > 1) jobs[nr++] = TnJob{ws.pb, w->n, rp, (int)r, pb.splits, db, 1, w->n};
-    }
-    if (da) {
-      const LoraPlan pa = lora_plan_tn(m, w->k, rp);
-      specs[nj++] = TnSpec{x, ws.up, rp, m, w->k, (int)r, pa, ws.pa, da, r, 1};
-      if (pa.splits > 1) jobs[nr++] = TnJob{ws.pa, w->k, rp, (int)r, pa.splits, da, r, 1};
-    }
+    int nj = 0;
+    // (planned together when both run: fewer, longer slices than either
+    // alone, so the partials reserved for the single-job plans suffice)
+    const int64_t ob = da ? w->k : 0, oa = db ? w->n : 0;
+    if (db) specs[nj++] = TnSpec{dy, t, r, m, w->n, (int)r, lora_plan_tn(m, w->n, rp, ob), ws.pb, db, 1, w->n};
+    if (da) specs[nj++] = TnSpec{x, ws.up, rp, m, w->k, (int)r, lora_plan_tn(m, w->k, rp, oa), ws.pa, da, r, 1};
     if (nj) {
       const int kid = nj == 2 ? KID_LORA_DADB : (db ? KID_LORA_DB : KID_LORA_DA);
-      LRQ_TRY(run(c, kid, kNames[kid], [&] { return launch_lora_tn(c->stream, specs, nj, rp); }));
+      LRQ_TRY(run(c, kid, kNames[kid], [&] { return launch_lora_tn(c->stream, specs, nj, rp, c->cnt); }));
     }
-    if (nr) LRQ_TRY(run(c, KID_LORA_RED, "lora_reduce", [&] { return launch_tn_reduce(c->stream, jobs, nr); }));
     return LRQ_OK;
   }
   if (!dx) return LRQ_OK;

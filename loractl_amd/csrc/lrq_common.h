@@ -121,6 +121,23 @@ LRQ_DEV f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+// A zero accumulator of its own, already in accumulator registers. When many
+// loop-carried accumulators start from one shared constant zero, the register
+// allocator rotates them through other registers on every iteration (dozens
+// of v_accvgpr moves per trip, and a loop back edge on which the compiler
+// left one read short of its MFMA wait states); a separate opaque zero per
+// accumulator keeps every MFMA in place.
+LRQ_DEV f32x4 acc_zero4() {
+  f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+  asm volatile("" : "+a"(z));
+  return z;
+}
+LRQ_DEV f32x16 acc_zero16() {
+  f32x16 z = {};
+  asm volatile("" : "+a"(z));
+  return z;
+}
+
 LRQ_DEV bf16x8 as_bf16x8(const u32x4& v) { return __builtin_bit_cast(bf16x8, v); }
 
 LRQ_DEV u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }

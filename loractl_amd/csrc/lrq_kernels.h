@@ -102,24 +102,40 @@ struct LoraPlan {
   int splits;
 };
 LoraPlan lora_plan_nt(int64_t M, int64_t C, int rp);
-LoraPlan lora_plan_tn(int64_t M, int64_t C, int rp);
-// partial[s][m][j] = sum over slice s of p[m, c] * q(j, c) (f32) for j < rp,
-// q(j, c) = q[j * ldq + c] when qrow (B [r, n]), else q[c * ldq + j] (A
-// [k, r]); entries j >= R read as zero. plan.splits * M * rp floats.
-hipError_t launch_lora_nt(hipStream_t st, const uint16_t* p, const uint16_t* q, bool qrow, int64_t ldq,
-                          int R, int64_t M, int64_t C, int rp, const LoraPlan& plan, float* partial);
-// out = bf16(s * sum_s partial[s]) as [M, rp] (columns >= r zero) and/or [M, r];
-// with fr set, also the fused GEMM's weight-side LoRA rows fr [N, rp]
+LoraPlan lora_plan_tn(int64_t M, int64_t C, int rp, int64_t other_c = 0);
+// out = bf16(s * sum over slices of p[m, c] * q(j, c)) as [M, rp] (columns
+// >= r zero) and/or [M, r], with q(j, c) = q[j * ldq + c] when qrow (B [r, n]),
+// else q[c * ldq + j] (A [k, r]); entries j >= R read as zero. One launch:
+// the slices write f32 partials (plan.splits * M * rp floats) and the last
+// slice of each 128-token tile sums them in slice order; cnt holds
+// plan.tiles <= LRQ_CNT_WORDS counters, zero on entry and exit. With fr set,
+// the launch also writes the fused GEMM's weight-side LoRA rows fr [N, rp]
 // (columns >= r zero): B^T from B [r, N], or (b_rows) A [N, r] itself,
-// divided by bdiv[n] (bdiv_rows) or bdiv[0] when bdiv is set (an fp8 weight scale).
-hipError_t launch_nt_reduce(hipStream_t st, const float* partial, int splits, int64_t M, int rp, int r, float s,
-                            uint16_t* out, uint16_t* out_user, const uint16_t* B = nullptr, int64_t N = 0,
-                            bool b_rows = false, uint16_t* fr = nullptr, const float* bdiv = nullptr,
-                            bool bdiv_rows = false);
-// partial[s][c][j] = sum over slice s of p[m, c] * q[m * ldq + j] (f32) for
-// c < C, j < rp (columns j >= R of q read as zero); plan.splits * C * rp
-// floats. One or two such jobs per launch (the first job's workgroups are
-// dispatched first).
+// divided by bdiv[n] (bdiv_rows) or bdiv[0] when bdiv is set (an fp8 weight
+// scale).
+struct NtFinish {
+  uint32_t* cnt;
+  float s;
+  int r;
+  uint16_t* out;       // [M, rp] or null
+  uint16_t* out_user;  // [M, r] or null
+  const uint16_t* B;
+  int64_t N;
+  int b_rows;
+  uint16_t* fr;        // or null
+  const float* bdiv;
+  int bdiv_rows;
+};
+hipError_t launch_lora_nt(hipStream_t st, const uint16_t* p, const uint16_t* q, bool qrow, int64_t ldq,
+                          int R, int64_t M, int64_t C, int rp, const LoraPlan& plan, float* partial,
+                          const NtFinish& fin);
+// out[c * sc + j * sj] = sum over tokens of p[m, c] * q[m * ldq + j] (f32)
+// for c < C, j < R (columns j >= R of q read as zero). One or two such jobs
+// per launch (the first job's workgroups are dispatched first). Token slices
+// write f32 partials (plan.splits * C * rp floats; a single slice writes out
+// directly) and the last slice of each 128-column tile sums them in slice
+// order; cnt holds the jobs' column tiles together (<= LRQ_CNT_WORDS)
+// counters, zero on entry and exit.
 struct TnSpec {
   const uint16_t* p;
   const uint16_t* q;
@@ -127,19 +143,10 @@ struct TnSpec {
   int R;
   LoraPlan plan;
   float* partial;
-  float* out;       // the result out[c * sc + j * sj], written directly when plan.splits == 1
-  int64_t sc, sj;
-};
-hipError_t launch_lora_tn(hipStream_t st, const TnSpec* jobs, int njobs, int rp);
-// out[c * sc + j * sj] = sum_s partial[s][c][j] (slice order) for c < C, j < R.
-struct TnJob {
-  const float* partial;
-  int64_t C;
-  int rp, R, splits;
   float* out;
   int64_t sc, sj;
 };
-hipError_t launch_tn_reduce(hipStream_t st, const TnJob* jobs, int njobs);
+hipError_t launch_lora_tn(hipStream_t st, const TnSpec* jobs, int njobs, int rp, uint32_t* cnt);
 
 // kernel ids for the profiler (lrq_profile_*)
 enum {
@@ -152,7 +159,6 @@ enum {
   KID_LORA_U,
   KID_LORA_DA,
   KID_LORA_DB,
-  KID_LORA_RED,
   KID_BLOCK,
   KID_LORA_DADB,
   KID_COUNT

@@ -14,15 +14,20 @@
 //     factor slice (B rows as stored, or A transposed in registers) is
 //     staged once in LDS and shared by the 8 wavefronts, each of which
 //     streams its own 16 token rows (64-byte runs per row and load). Slices
-//     write f32 partials; a small kernel sums them in slice order and writes
-//     the bf16 result.
+//     write f32 partials and count themselves done per token tile; the last
+//     slice of a tile sums them in slice order and writes the bf16 result
+//     (in the same launch, as the few-token kernel finishes a block row:
+//     device-scope stores acknowledged before the count, device-scope
+//     loads). Every workgroup also copies its share of the fused GEMM's
+//     weight-side factor rows (B^T or A, padded to rp).
 //   tn (dA, dB): the reduction runs over tokens, which are strided in p.
 //     Each lane loads an 8 (tokens) x 8 (columns) block with eight 16-byte
 //     loads and transposes it in registers (byte permutes), so every load is
 //     a contiguous 256-byte run per 16 lanes; the token-major factor (u or t)
 //     is transposed once into LDS. Workgroups own 128 columns and a token
-//     slice and write f32 partials; one small kernel sums the slices of both
-//     reductions in slice order.
+//     slice and write f32 partials; the last slice of a column tile sums the
+//     slices in order and writes the result, in the same launch (both
+//     reductions in one launch).
 //
 // Nothing depends on timing: every sum has a fixed order, and no workgroup
 // waits for another.
@@ -57,7 +62,14 @@ struct NtArgs {
   int R;               // valid factor rank entries (the rest read as zero)
   int64_t c_per;       // columns per slice (multiple of 32)
   float* partial;      // [splits][M][rp] f32
+  NtFinish f;
 };
+
+// device-scope (sc1) accesses of the partials the last slice reads
+LRQ_DEV void store_dev(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+LRQ_DEV u32x4 bload16_dev(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 16); }
+LRQ_DEV uint32_t add_dev(uint32_t* c) { return __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+LRQ_DEV void zero_dev(uint32_t* c) { __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 
 constexpr int NQ_BYTES = 100 * 1024;  // factor slice in LDS
 
@@ -186,51 +198,109 @@ __global__ void __launch_bounds__(LNT) k_lora_nt(NtArgs a) {
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int64_t m = m0 + 4 * g + v;
-      if (m < a.M) part[m * RP + jt * 16 + l16] = acc[jt][v];
+      if (m < a.M) store_dev(part + m * RP + jt * 16 + l16, acc[jt][v]);
     }
-}
 
-// out[m, j] = bf16(s * sum over splits (in order) of partial[sp][m][j]); as
-// [M, rp] (columns >= r zero) and/or [M, r]. Threads past M * rp write the
-// weight-side LoRA rows fr [N, rp] (columns >= r zero) when fr is set, as
-// the fused GEMM's LoRA step reads them: B^T from B [r, N] (forward), or A
-// [N, r] row for row (b_rows, backward). With bdiv, each value is divided by
-// bdiv[n] (bdiv_rows) or bdiv[0] and rounded to bf16: the forward multiplies
-// its accumulators (base + LoRA) by the fp8 weight scale, so the LoRA factor
-// arrives pre-divided by it.
-__global__ void __launch_bounds__(256) k_nt_reduce(const float* __restrict__ partial, int splits, int64_t M,
-                                                   int rp, int r, float s, uint16_t* __restrict__ out,
-                                                   uint16_t* __restrict__ out_user, const uint16_t* __restrict__ B,
-                                                   int64_t N, int b_rows, uint16_t* __restrict__ fr,
-                                                   const float* __restrict__ bdiv, int bdiv_rows) {
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= M * rp) {
-    const int64_t i2 = idx - M * rp;
-    if (!fr || i2 >= N * rp) return;
-    const int64_t n = i2 / rp;
-    const int j = (int)(i2 % rp);
-    uint16_t v = j < r ? B[b_rows ? n * r + j : (int64_t)j * N + n] : (uint16_t)0;
-    if (bdiv && j < r) {
-      const float d = bdiv[bdiv_rows ? n : 0];
-      v = f32_to_bf16_bits(__builtin_bit_cast(float, (uint32_t)v << 16) / d);
+  // count this slice done once its partial stores are acknowledged
+  const NtFinish& f = a.f;
+  __shared__ int last;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) {
+    last = add_dev(f.cnt + blockIdx.x) + 1 == gridDim.y;
+    if (last) zero_dev(f.cnt + blockIdx.x);
+  }
+  __syncthreads();
+
+  // this workgroup's share of the weight-side factor rows fr [N, rp]
+  // (columns >= r zero): B^T from B [r, N], or (b_rows) A [N, r] row for row,
+  // divided by bdiv[n] (bdiv_rows) or bdiv[0] when set (an fp8 weight scale).
+  // Nothing in this launch reads them, so they are not part of the count.
+  if (f.fr) {
+    const int64_t nwg = (int64_t)gridDim.x * gridDim.y, wg = (int64_t)blockIdx.y * gridDim.x + blockIdx.x;
+    if (!f.b_rows && (f.N & 7) == 0) {
+      // B^T as 8 (n) x 8 (j) blocks: eight 16-byte row loads of B, transposed
+      // in registers, eight 16-byte stores
+      constexpr int JB = RP / 8;
+      for (int64_t bi = wg * LNT + tid; bi < f.N / 8 * JB; bi += nwg * LNT) {
+        const int j0 = (int)(bi % JB) * 8;
+        const int64_t n0 = bi / JB * 8;
+        u32x4 v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = j0 + i < f.r ? ld16(f.B + (int64_t)(j0 + i) * f.N + n0) : zero4();
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          u32x4 cv = column8(v, e);
+          if (f.bdiv) {
+            const float d = f.bdiv[f.bdiv_rows ? n0 + e : 0];
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+              const uint32_t lo = j0 + 2 * h < f.r ? f32_to_bf16_bits(bf16_lo(cv[h]) / d) : 0u;
+              const uint32_t hi = j0 + 2 * h + 1 < f.r ? f32_to_bf16_bits(bf16_hi(cv[h]) / d) : 0u;
+              cv[h] = lo | (hi << 16);
+            }
+          }
+          st16(f.fr + (n0 + e) * RP + j0, cv);
+        }
+      }
+    } else {
+      for (int64_t i2 = wg * LNT + tid; i2 < f.N * RP; i2 += nwg * LNT) {
+        const int64_t n = i2 / RP;
+        const int j = (int)(i2 % RP);
+        uint16_t v = j < f.r ? f.B[f.b_rows ? n * f.r + j : (int64_t)j * f.N + n] : (uint16_t)0;
+        if (f.bdiv && j < f.r) {
+          const float d = f.bdiv[f.bdiv_rows ? n : 0];
+          v = f32_to_bf16_bits(__builtin_bit_cast(float, (uint32_t)v << 16) / d);
+        }
+        f.fr[i2] = v;
+      }
     }
-    fr[i2] = v;
-    return;
   }
-  const int64_t m = idx / rp;
-  const int j = (int)(idx % rp);
-  const int64_t stride = M * rp;
-  float sum = 0.0f;
-  for (int s0 = 0; s0 < splits; s0 += 16) {
-    float v[16];
+  if (!last) return;
+
+  // the last slice of the token tile sums the slices in order: each thread
+  // owns NE entries of four, and every load of a batch of SB slices is
+  // issued before the first sum (one memory round trip per batch)
+  constexpr int NE = 128 * RP / 4 / LNT, SB = 16 / NE;
+  const int64_t t0 = (int64_t)blockIdx.x * 128;
+  const int splits = (int)gridDim.y;
+  const rsrc_t rp_ = make_rsrc(a.partial, clamp_bytes((int64_t)splits * a.M * RP * 4));
+  float v[NE][4] = {};
+  for (int s0 = 0; s0 < splits; s0 += SB) {
+    u32x4 pv[NE][SB];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) v[i] = (s0 + i < splits) ? partial[(s0 + i) * stride + idx] : 0.0f;
+    for (int k = 0; k < NE; ++k) {
+      const int q4 = tid + k * LNT;
+      const int64_t m = t0 + (q4 * 4) / RP;
+      const int j = (q4 * 4) % RP;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) sum += v[i];
+      for (int u = 0; u < SB; ++u)
+        pv[k][u] = bload16_dev(rp_, opaque_u32(s0 + u < splits && m < a.M
+                                                   ? (uint32_t)((((int64_t)(s0 + u) * a.M + m) * RP + j) * 4)
+                                                   : LRQ_OOB));
+    }
+#pragma unroll
+    for (int k = 0; k < NE; ++k)
+#pragma unroll
+      for (int u = 0; u < SB; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[k][e] += __uint_as_float(pv[k][u][e]);
   }
-  const uint16_t h = f32_to_bf16_bits(j < r ? sum * s : 0.0f);
-  if (out) out[idx] = h;
-  if (out_user && j < r) out_user[m * r + j] = h;
+#pragma unroll
+  for (int k = 0; k < NE; ++k) {
+    const int q4 = tid + k * LNT;
+    const int64_t m = t0 + (q4 * 4) / RP;
+    const int j = (q4 * 4) % RP;
+    if (m >= a.M) continue;
+    uint16_t h[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) h[e] = f32_to_bf16_bits(j + e < f.r ? v[k][e] * f.s : 0.0f);
+    if (f.out) *reinterpret_cast<u32x2*>(f.out + m * RP + j) = (u32x2){h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16)};
+    if (f.out_user)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (j + e < f.r) f.out_user[m * f.r + j + e] = h[e];
+  }
 }
 
 // ------------------------------------------------------------------ tn
@@ -242,8 +312,10 @@ struct TnArgs {
   int64_t m_per;       // tokens per slice (multiple of 128)
   float* partial;      // [splits][C][rp]
   int tiles, blocks;   // column tiles of 128, tiles x slices
-  float* out;          // one slice: the result out[c * sc + j * sj] (j < R) instead of partial
+  float* out;          // the result out[c * sc + j * sj] (j < R)
   int64_t sc, sj;
+  int splits;          // token slices; one slice writes out directly
+  uint32_t* cnt;       // [tiles] arrival counters, zero on entry and exit
 };
 
 // partial[split][c][j] = sum over the split's tokens of p[m, c] * q[m, j],
@@ -252,7 +324,7 @@ struct TnArgs {
 // wavefront w takes tokens [128 it + 32 w, +32) of every 128-token chunk.
 constexpr int TW = 4;            // wavefronts per tn workgroup
 constexpr int TNT = 64 * TW;
-constexpr int TQ_BYTES = 64 * 1024;  // factor slice in LDS (later reused for the combine)
+constexpr int TQ_BYTES = 72 * 1024;  // factor slice in LDS (later reused for the combine); two per CU
 
 template <int NJT>
 __global__ void __launch_bounds__(TNT) k_lora_tn(TnArgs j0, TnArgs j1) {
@@ -282,7 +354,7 @@ __global__ void __launch_bounds__(TNT) k_lora_tn(TnArgs j0, TnArgs j1) {
 #pragma unroll
   for (int q = 0; q < 8; ++q)
 #pragma unroll
-    for (int jt = 0; jt < NJT; ++jt) acc[q][jt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    for (int jt = 0; jt < NJT; ++jt) acc[q][jt] = acc_zero4();
 
   const int64_t nchunks = (toks + 127) / 128;
   u32x4 pv[2][8];
@@ -368,46 +440,63 @@ __global__ void __launch_bounds__(TNT) k_lora_tn(TnArgs j0, TnArgs j1) {
 #pragma unroll
       for (int w = 0; w < TW; ++w) sum += red[(w * 128 + cl) * 16 + jl];
       if (c0 + cl < C) {
-        if (a.out) {
+        if (a.splits == 1) {
           if (jt * 16 + jl < a.R) a.out[(c0 + cl) * a.sc + (int64_t)(jt * 16 + jl) * a.sj] = sum;
         } else {
-          part[(c0 + cl) * RP + jt * 16 + jl] = sum;
+          store_dev(part + (c0 + cl) * RP + jt * 16 + jl, sum);
         }
       }
     }
     __syncthreads();
   }
-}
-
-// out[c * sc + j * sj] = sum over splits (in order) of partial[s][c][j], for
-// one or two reductions in one launch.
-struct TnReduce {
-  const float* partial;
-  int64_t C;
-  int rp, R, splits;
-  float* out;
-  int64_t sc, sj;
-  int64_t blocks;
-};
-
-__global__ void __launch_bounds__(256) k_tn_reduce(TnReduce j0, TnReduce j1) {
-  const bool second = blockIdx.x >= j0.blocks;
-  const TnReduce& t = second ? j1 : j0;
-  const int64_t idx = (int64_t)(blockIdx.x - (second ? j0.blocks : 0)) * 256 + threadIdx.x;
-  const int64_t c = idx / t.R;
-  const int j = (int)(idx % t.R);
-  if (c >= t.C) return;
-  const float* src = t.partial + c * t.rp + j;
-  const int64_t stride = t.C * t.rp;
-  float sum = 0.0f;
-  for (int s0 = 0; s0 < t.splits; s0 += 8) {
-    float v[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = (s0 + i < t.splits) ? src[(s0 + i) * stride] : 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) sum += v[i];
+  if (a.splits == 1) return;
+  // count this slice done once its partial stores are acknowledged; the last
+  // slice of the column tile sums the slices in order, four entries a thread
+  __shared__ int last;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  const int tile = bid % a.tiles;
+  if (tid == 0) {
+    last = add_dev(a.cnt + tile) + 1 == (uint32_t)a.splits;
+    if (last) zero_dev(a.cnt + tile);
   }
-  t.out[c * t.sc + (int64_t)j * t.sj] = sum;
+  __syncthreads();
+  if (!last) return;
+  // each thread owns NE entries of four; every load of a batch of SB slices
+  // is issued before the first sum (one memory round trip per batch)
+  constexpr int NE = 128 * RP / 4 / TNT, SB = 16 / NE;
+  const rsrc_t rp_ = make_rsrc(a.partial, clamp_bytes((int64_t)a.splits * C * RP * 4));
+  float v[NE][4] = {};
+  for (int s0 = 0; s0 < a.splits; s0 += SB) {  // slices in order
+    u32x4 pv[NE][SB];
+#pragma unroll
+    for (int k = 0; k < NE; ++k) {
+      const int q4 = tid + k * TNT;
+      const int64_t c = c0 + (q4 * 4) / RP;
+      const int j = (q4 * 4) % RP;
+#pragma unroll
+      for (int u = 0; u < SB; ++u)
+        pv[k][u] = bload16_dev(rp_, opaque_u32(s0 + u < a.splits && c < C
+                                                   ? (uint32_t)((((int64_t)(s0 + u) * C + c) * RP + j) * 4)
+                                                   : LRQ_OOB));
+    }
+#pragma unroll
+    for (int k = 0; k < NE; ++k)
+#pragma unroll
+      for (int u = 0; u < SB; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[k][e] += __uint_as_float(pv[k][u][e]);
+  }
+#pragma unroll
+  for (int k = 0; k < NE; ++k) {
+    const int q4 = tid + k * TNT;
+    const int64_t c = c0 + (q4 * 4) / RP;
+    const int j = (q4 * 4) % RP;
+    if (c >= C) continue;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (j + e < a.R) a.out[c * a.sc + (int64_t)(j + e) * a.sj] = v[k][e];
+  }
 }
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -431,13 +520,15 @@ LoraPlan lora_plan_nt(int64_t M, int64_t C, int rp) {
   return p;
 }
 
-// tn: token slices (multiples of 128) so that column tiles x slices fill at
-// most the 512 workgroup slots (two resident per CU): a partial second round
-// would cost a whole slice's time. Within the LDS factor slice.
-LoraPlan lora_plan_tn(int64_t M, int64_t C, int rp) {
+// tn: token slices (multiples of 128) so that the column tiles of every job
+// in the launch (this job's C and other_c, 0 when it runs alone) times the
+// slices fill at most the 512 workgroup slots (two resident per CU): a
+// partial second round would cost a whole slice's time. Within the LDS
+// factor slice.
+LoraPlan lora_plan_tn(int64_t M, int64_t C, int rp, int64_t other_c) {
   LoraPlan p{};
   const int64_t tiles = cdiv(C, 128);
-  const int64_t want = std::max<int64_t>(1, 512 / tiles);
+  const int64_t want = std::max<int64_t>(1, 512 / (tiles + cdiv(other_c, 128)));
   int64_t per = 128 * cdiv(cdiv(M > 0 ? M : 1, want), 128);
   const int64_t cap = ((TQ_BYTES / 2) / rp - 8) / 128 * 128;
   if (per > cap) per = cap;
@@ -449,9 +540,11 @@ LoraPlan lora_plan_tn(int64_t M, int64_t C, int rp) {
 }
 
 hipError_t launch_lora_nt(hipStream_t st, const uint16_t* p, const uint16_t* q, bool qrow, int64_t ldq,
-                          int R, int64_t M, int64_t C, int rp, const LoraPlan& plan, float* partial) {
+                          int R, int64_t M, int64_t C, int rp, const LoraPlan& plan, float* partial,
+                          const NtFinish& fin) {
   if (M == 0) return hipSuccess;
-  NtArgs a{p, q, M, C, ldq, R, plan.per, partial};
+  if (!fin.cnt || plan.tiles > LRQ_CNT_WORDS) return hipErrorInvalidValue;
+  NtArgs a{p, q, M, C, ldq, R, plan.per, partial, fin};
   const dim3 grid((unsigned)plan.tiles, (unsigned)plan.splits);
   switch ((qrow ? 4 : 0) + rp / 16 - 1) {
     case 0: hipLaunchKernelGGL((k_lora_nt<1, false>), grid, dim3(LNT), 0, st, a); break;
@@ -467,26 +560,19 @@ hipError_t launch_lora_nt(hipStream_t st, const uint16_t* p, const uint16_t* q, 
   return hipGetLastError();
 }
 
-hipError_t launch_nt_reduce(hipStream_t st, const float* partial, int splits, int64_t M, int rp, int r, float s,
-                            uint16_t* out, uint16_t* out_user, const uint16_t* B, int64_t N, bool b_rows,
-                            uint16_t* fr, const float* bdiv, bool bdiv_rows) {
-  const int64_t total = M * rp + (fr ? N * rp : 0);
-  if (total == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_nt_reduce, dim3((unsigned)cdiv(total, 256)), dim3(256), 0, st, partial, splits, M, rp, r,
-                     s, out, out_user, B, N, b_rows ? 1 : 0, fr, bdiv, bdiv_rows ? 1 : 0);
-  return hipGetLastError();
-}
-
-hipError_t launch_lora_tn(hipStream_t st, const TnSpec* jobs, int njobs, int rp) {
+hipError_t launch_lora_tn(hipStream_t st, const TnSpec* jobs, int njobs, int rp, uint32_t* cnt) {
   TnArgs t[2] = {};
-  int64_t total = 0;
+  int64_t total = 0, ntiles = 0;
   for (int i = 0; i < njobs && i < 2; ++i) {
     const TnSpec& j = jobs[i];
     const int64_t blocks = j.C > 0 ? j.plan.tiles * j.plan.splits : 0;
+    // each job's column tiles count on their own counters
     t[i] = TnArgs{j.p,      j.q, j.M, j.C, j.ldq, j.R, j.plan.per, j.partial, (int)j.plan.tiles, (int)blocks,
-                  j.plan.splits == 1 ? j.out : nullptr, j.sc, j.sj};
+                  j.out,    j.sc, j.sj, j.plan.splits, cnt + ntiles};
     total += blocks;
+    ntiles += j.plan.tiles;
   }
+  if (!cnt || ntiles > LRQ_CNT_WORDS) return hipErrorInvalidValue;
   if (total == 0) return hipSuccess;
   const dim3 grid((unsigned)total);
   switch (rp / 16) {
@@ -496,18 +582,5 @@ hipError_t launch_lora_tn(hipStream_t st, const TnSpec* jobs, int njobs, int rp)
     case 4: hipLaunchKernelGGL(k_lora_tn<4>, grid, dim3(TNT), 0, st, t[0], t[1]); break;
     default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
-}
-
-hipError_t launch_tn_reduce(hipStream_t st, const TnJob* jobs, int njobs) {
-  TnReduce t[2] = {};
-  int64_t total = 0;
-  for (int i = 0; i < njobs && i < 2; ++i) {
-    const TnJob& j = jobs[i];
-    t[i] = TnReduce{j.partial, j.C, j.rp, j.R, j.splits, j.out, j.sc, j.sj, cdiv(j.C * j.R, 256)};
-    total += t[i].blocks;
-  }
-  if (total == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_tn_reduce, dim3((unsigned)total), dim3(256), 0, st, t[0], t[1]);
   return hipGetLastError();
 }
