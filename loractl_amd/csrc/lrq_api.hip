@@ -205,7 +205,7 @@ LoraWs lora_layout(char* base, int64_t m, int64_t n, int64_t k, int rp, bool fwd
   w.fr = s.take<uint16_t>((fwd_only ? n : std::max(n, k)) * rp);
   const int64_t nt = fwd_only ? lora_plan_nt(m, k, rp).splits
                               : std::max((int64_t)lora_plan_nt(m, k, rp).splits, (int64_t)lora_plan_nt(m, n, rp).splits);
-  w.pn = s.take<float>(std::max(nt * m * rp, (int64_t)1));
+  w.pn = s.take<float>(std::max(nt * round_up(m, 128) * rp, (int64_t)1));
   w.pa = s.take<float>(fwd_only ? 0 : (int64_t)lora_plan_tn(m, k, rp).splits * k * rp);
   w.pb = s.take<float>(fwd_only ? 0 : (int64_t)lora_plan_tn(m, n, rp).splits * n * rp);
   w.gp = s.take<float>(std::max(fwd_only ? gemm_split_floats(m, n, k) : gemm_part_floats(m, n, k), (int64_t)1));

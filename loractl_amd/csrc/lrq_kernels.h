@@ -106,9 +106,10 @@ LoraPlan lora_plan_tn(int64_t M, int64_t C, int rp, int64_t other_c = 0);
 // out = bf16(s * sum over slices of p[m, c] * q(j, c)) as [M, rp] (columns
 // >= r zero) and/or [M, r], with q(j, c) = q[j * ldq + c] when qrow (B [r, n]),
 // else q[c * ldq + j] (A [k, r]); entries j >= R read as zero. One launch:
-// the slices write f32 partials (plan.splits * M * rp floats) and the last
-// slice of each 128-token tile sums them in slice order; cnt holds
-// plan.tiles <= LRQ_CNT_WORDS counters, zero on entry and exit. With fr set,
+// the slices write f32 partials (plan.splits * round_up(M, 128) * rp floats)
+// and the last slice to finish each 16-token group sums them in slice order;
+// cnt holds 8 * plan.tiles <= SK_MAX_NB counters, zero on entry and exit.
+// With fr set,
 // the launch also writes the fused GEMM's weight-side LoRA rows fr [N, rp]
 // (columns >= r zero): B^T from B [r, N], or (b_rows) A [N, r] itself,
 // divided by bdiv[n] (bdiv_rows) or bdiv[0] when bdiv is set (an fp8 weight
@@ -133,9 +134,9 @@ hipError_t launch_lora_nt(hipStream_t st, const uint16_t* p, const uint16_t* q, 
 // for c < C, j < R (columns j >= R of q read as zero). One or two such jobs
 // per launch (the first job's workgroups are dispatched first). Token slices
 // write f32 partials (plan.splits * C * rp floats; a single slice writes out
-// directly) and the last slice of each 128-column tile sums them in slice
-// order; cnt holds the jobs' column tiles together (<= LRQ_CNT_WORDS)
-// counters, zero on entry and exit.
+// directly) and the last slice to finish each 32-column group sums them in
+// slice order; cnt holds 4 counters per 128-column tile of the jobs together
+// (<= SK_MAX_NB), zero on entry and exit.
 struct TnSpec {
   const uint16_t* p;
   const uint16_t* q;

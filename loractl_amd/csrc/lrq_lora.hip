@@ -67,6 +67,7 @@ struct NtArgs {
 
 // device-scope (sc1) accesses of the partials the last slice reads
 LRQ_DEV void store_dev(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+LRQ_DEV void store16_dev(rsrc_t r, uint32_t off, const u32x4& v) { __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, 16); }
 LRQ_DEV u32x4 bload16_dev(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 16); }
 LRQ_DEV uint32_t add_dev(uint32_t* c) { return __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 LRQ_DEV void zero_dev(uint32_t* c) { __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
@@ -124,6 +125,57 @@ LRQ_DEV void stage_factor(const NtArgs& a, int64_t c_lo, int64_t c_hi, int width
       uint16_t v = 0;
       if (j < a.R && cc < cols) v = QROW ? a.q[(int64_t)j * a.ldq + c_lo + cc] : a.q[(c_lo + cc) * a.ldq + j];
       sQ[j * SQ + cc] = v;
+    }
+  }
+}
+
+// The weight-side factor rows fr [N, rp] of the fused GEMM's LoRA epilogue
+// (columns >= r zero): B^T from B [r, N], or (b_rows) A [N, r] row for row,
+// divided by bdiv[n] (bdiv_rows) or bdiv[0] when set (an fp8 weight scale).
+// Workgroup wg of nwg copies an equal contiguous share (so that no workgroup
+// carries much of it); nothing in the launch reads them.
+template <int RP>
+LRQ_DEV void copy_factor_rows(const NtFinish& f, int64_t wg, int64_t nwg, int nthreads) {
+  const int tid = threadIdx.x;
+  if (!f.b_rows && (f.N & 7) == 0) {
+    // B^T as 8 (n) x 8 (j) blocks: eight 16-byte row loads of B, transposed
+    // in registers, eight 16-byte stores
+    constexpr int JB = RP / 8;
+    const int64_t total = f.N / 8 * JB, share = (total + nwg - 1) / nwg;
+    const int64_t hi = min(total, (wg + 1) * share);
+    for (int64_t bi = wg * share + tid; bi < hi; bi += nthreads) {
+      const int j0 = (int)(bi % JB) * 8;
+      const int64_t n0 = bi / JB * 8;
+      u32x4 v[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = j0 + i < f.r ? ld16(f.B + (int64_t)(j0 + i) * f.N + n0) : zero4();
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        u32x4 cv = column8(v, e);
+        if (f.bdiv) {
+          const float d = f.bdiv[f.bdiv_rows ? n0 + e : 0];
+#pragma unroll
+          for (int h = 0; h < 4; ++h) {
+            const uint32_t lo = j0 + 2 * h < f.r ? f32_to_bf16_bits(bf16_lo(cv[h]) / d) : 0u;
+            const uint32_t hi = j0 + 2 * h + 1 < f.r ? f32_to_bf16_bits(bf16_hi(cv[h]) / d) : 0u;
+            cv[h] = lo | (hi << 16);
+          }
+        }
+        st16(f.fr + (n0 + e) * RP + j0, cv);
+      }
+    }
+  } else {
+    const int64_t total = f.N * RP, share = (total + nwg - 1) / nwg;
+    const int64_t hi = min(total, (wg + 1) * share);
+    for (int64_t i2 = wg * share + tid; i2 < hi; i2 += nthreads) {
+      const int64_t n = i2 / RP;
+      const int j = (int)(i2 % RP);
+      uint16_t v = j < f.r ? f.B[f.b_rows ? n * f.r + j : (int64_t)j * f.N + n] : (uint16_t)0;
+      if (f.bdiv && j < f.r) {
+        const float d = f.bdiv[f.bdiv_rows ? n : 0];
+        v = f32_to_bf16_bits(__builtin_bit_cast(float, (uint32_t)v << 16) / d);
+      }
+      f.fr[i2] = v;
     }
   }
 }
@@ -191,116 +243,57 @@ __global__ void __launch_bounds__(LNT) k_lora_nt(NtArgs a) {
     }
   }
 
-  // accumulator: token 4g+v of the wavefront's 16, rank column 16jt + l16
-  float* part = a.partial + (int64_t)split * a.M * RP;
-#pragma unroll
-  for (int jt = 0; jt < NJT; ++jt)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int64_t m = m0 + 4 * g + v;
-      if (m < a.M) store_dev(part + m * RP + jt * 16 + l16, acc[jt][v]);
-    }
-
-  // count this slice done once its partial stores are acknowledged
+  // this wavefront's partial, in the accumulator's own layout (lane l's
+  // f32x4 of rank tile jt: token 4g+v of the wavefront's 16, rank column
+  // 16jt + l16), one 16-byte store per tile, in slot (split, wavefront)
   const NtFinish& f = a.f;
-  __shared__ int last;
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (tid == 0) {
-    last = add_dev(f.cnt + blockIdx.x) + 1 == gridDim.y;
-    if (last) zero_dev(f.cnt + blockIdx.x);
-  }
-  __syncthreads();
-
-  // this workgroup's share of the weight-side factor rows fr [N, rp]
-  // (columns >= r zero): B^T from B [r, N], or (b_rows) A [N, r] row for row,
-  // divided by bdiv[n] (bdiv_rows) or bdiv[0] when set (an fp8 weight scale).
-  // Nothing in this launch reads them, so they are not part of the count.
-  if (f.fr) {
-    const int64_t nwg = (int64_t)gridDim.x * gridDim.y, wg = (int64_t)blockIdx.y * gridDim.x + blockIdx.x;
-    if (!f.b_rows && (f.N & 7) == 0) {
-      // B^T as 8 (n) x 8 (j) blocks: eight 16-byte row loads of B, transposed
-      // in registers, eight 16-byte stores
-      constexpr int JB = RP / 8;
-      for (int64_t bi = wg * LNT + tid; bi < f.N / 8 * JB; bi += nwg * LNT) {
-        const int j0 = (int)(bi % JB) * 8;
-        const int64_t n0 = bi / JB * 8;
-        u32x4 v[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = j0 + i < f.r ? ld16(f.B + (int64_t)(j0 + i) * f.N + n0) : zero4();
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          u32x4 cv = column8(v, e);
-          if (f.bdiv) {
-            const float d = f.bdiv[f.bdiv_rows ? n0 + e : 0];
-#pragma unroll
-            for (int h = 0; h < 4; ++h) {
-              const uint32_t lo = j0 + 2 * h < f.r ? f32_to_bf16_bits(bf16_lo(cv[h]) / d) : 0u;
-              const uint32_t hi = j0 + 2 * h + 1 < f.r ? f32_to_bf16_bits(bf16_hi(cv[h]) / d) : 0u;
-              cv[h] = lo | (hi << 16);
-            }
-          }
-          st16(f.fr + (n0 + e) * RP + j0, cv);
-        }
-      }
-    } else {
-      for (int64_t i2 = wg * LNT + tid; i2 < f.N * RP; i2 += nwg * LNT) {
-        const int64_t n = i2 / RP;
-        const int j = (int)(i2 % RP);
-        uint16_t v = j < f.r ? f.B[f.b_rows ? n * f.r + j : (int64_t)j * f.N + n] : (uint16_t)0;
-        if (f.bdiv && j < f.r) {
-          const float d = f.bdiv[f.bdiv_rows ? n : 0];
-          v = f32_to_bf16_bits(__builtin_bit_cast(float, (uint32_t)v << 16) / d);
-        }
-        f.fr[i2] = v;
-      }
-    }
-  }
-  if (!last) return;
-
-  // the last slice of the token tile sums the slices in order: each thread
-  // owns NE entries of four, and every load of a batch of SB slices is
-  // issued before the first sum (one memory round trip per batch)
-  constexpr int NE = 128 * RP / 4 / LNT, SB = 16 / NE;
-  const int64_t t0 = (int64_t)blockIdx.x * 128;
   const int splits = (int)gridDim.y;
-  const rsrc_t rp_ = make_rsrc(a.partial, clamp_bytes((int64_t)splits * a.M * RP * 4));
-  float v[NE][4] = {};
-  for (int s0 = 0; s0 < splits; s0 += SB) {
-    u32x4 pv[NE][SB];
+  const int64_t nwv = (int64_t)gridDim.x * LW, slot = (int64_t)blockIdx.x * LW + wv;
+  const rsrc_t rpart = make_rsrc(a.partial, clamp_bytes((int64_t)splits * nwv * RP * 64));
+  auto poff = [&](int64_t sp, int jt) { return (uint32_t)((((sp * nwv + slot) * NJT + jt) * 64 + lane) * 16); };
 #pragma unroll
-    for (int k = 0; k < NE; ++k) {
-      const int q4 = tid + k * LNT;
-      const int64_t m = t0 + (q4 * 4) / RP;
-      const int j = (q4 * 4) % RP;
+  for (int jt = 0; jt < NJT; ++jt) store16_dev(rpart, poff(split, jt), __builtin_bit_cast(u32x4, acc[jt]));
+
+  // count these 16 tokens done in this slice once the stores are
+  // acknowledged (wavefront by wavefront: no barrier); the last wavefront
+  // to arrive sums the slices in order, every load of a batch of SB slices
+  // issued before the first sum
+  __builtin_amdgcn_s_waitcnt(0);
+  uint32_t old = 0;
+  if (lane == 0) old = add_dev(f.cnt + slot);
+  const bool last = __builtin_amdgcn_readfirstlane(old) + 1 == (uint32_t)splits;
+  if (last) {
+    if (lane == 0) zero_dev(f.cnt + slot);
+    constexpr int SB = 16 / NJT;
+    f32x4 sum[NJT];
 #pragma unroll
-      for (int u = 0; u < SB; ++u)
-        pv[k][u] = bload16_dev(rp_, opaque_u32(s0 + u < splits && m < a.M
-                                                   ? (uint32_t)((((int64_t)(s0 + u) * a.M + m) * RP + j) * 4)
-                                                   : LRQ_OOB));
+    for (int jt = 0; jt < NJT; ++jt) sum[jt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s0 = 0; s0 < splits; s0 += SB) {
+      u32x4 pv[NJT][SB];
+#pragma unroll
+      for (int jt = 0; jt < NJT; ++jt)
+#pragma unroll
+        for (int u = 0; u < SB; ++u) pv[jt][u] = bload16_dev(rpart, opaque_u32(s0 + u < splits ? poff(s0 + u, jt) : LRQ_OOB));
+#pragma unroll
+      for (int jt = 0; jt < NJT; ++jt)
+#pragma unroll
+        for (int u = 0; u < SB; ++u) sum[jt] += __builtin_bit_cast(f32x4, pv[jt][u]);
     }
 #pragma unroll
-    for (int k = 0; k < NE; ++k)
+    for (int jt = 0; jt < NJT; ++jt)
 #pragma unroll
-      for (int u = 0; u < SB; ++u)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[k][e] += __uint_as_float(pv[k][u][e]);
+      for (int v = 0; v < 4; ++v) {
+        const int64_t m = m0 + 4 * g + v;
+        const int j = 16 * jt + l16;
+        if (m >= a.M) continue;
+        const uint16_t h = f32_to_bf16_bits(j < f.r ? sum[jt][v] * f.s : 0.0f);
+        if (f.out) f.out[m * RP + j] = h;
+        if (f.out_user && j < f.r) f.out_user[m * f.r + j] = h;
+      }
   }
-#pragma unroll
-  for (int k = 0; k < NE; ++k) {
-    const int q4 = tid + k * LNT;
-    const int64_t m = t0 + (q4 * 4) / RP;
-    const int j = (q4 * 4) % RP;
-    if (m >= a.M) continue;
-    uint16_t h[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) h[e] = f32_to_bf16_bits(j + e < f.r ? v[k][e] * f.s : 0.0f);
-    if (f.out) *reinterpret_cast<u32x2*>(f.out + m * RP + j) = (u32x2){h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16)};
-    if (f.out_user)
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (j + e < f.r) f.out_user[m * f.r + j + e] = h[e];
-  }
+
+  if (f.fr)
+    copy_factor_rows<RP>(f, (int64_t)blockIdx.y * gridDim.x + blockIdx.x, (int64_t)gridDim.x * gridDim.y, LNT);
 }
 
 // ------------------------------------------------------------------ tn
@@ -315,7 +308,7 @@ struct TnArgs {
   float* out;          // the result out[c * sc + j * sj] (j < R)
   int64_t sc, sj;
   int splits;          // token slices; one slice writes out directly
-  uint32_t* cnt;       // [tiles] arrival counters, zero on entry and exit
+  uint32_t* cnt;       // [tiles][TW] arrival counters, zero on entry and exit
 };
 
 // partial[split][c][j] = sum over the split's tokens of p[m, c] * q[m, j],
@@ -421,59 +414,70 @@ __global__ void __launch_bounds__(TNT) k_lora_tn(TnArgs j0, TnArgs j1) {
   if (it < nchunks) compute(0, it);
   __syncthreads();  // the factor slice's LDS becomes the combine buffer
 
-  // combine the wavefronts (fixed order), one 16-wide rank tile per round;
-  // accumulator row 4g+v of MFMA q is column c0 + 8*(4g+v) + q
-  float* part = a.partial + (int64_t)split * C * RP;
+  // combine the wavefronts (fixed order); accumulator row 4g+v of MFMA q is
+  // column c0 + 8*(4g+v) + q. All rank tiles go through LDS at once when
+  // they fit (rank <= 32), else one 16-wide tile per round; each thread then
+  // sums four consecutive rank entries of a column and stores them together.
+  const rsrc_t rpart = make_rsrc(a.partial + (int64_t)split * C * RP, clamp_bytes(C * RP * 4));
+  constexpr int RT = (TW * 128 * RP * 4 <= TQ_BYTES) ? NJT : 1;  // rank tiles per round
+  constexpr int RW = 16 * RT;                                    // rank entries per round
 #pragma unroll
-  for (int jt = 0; jt < NJT; ++jt) {
+  for (int jr = 0; jr < NJT; jr += RT) {
 #pragma unroll
-    for (int q = 0; q < 8; ++q)
+    for (int jt = 0; jt < RT; ++jt)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int cl = 8 * (4 * g + v) + q;
-        red[(wv * 128 + cl) * 16 + l16] = acc[q][jt][v];
-      }
+      for (int q = 0; q < 8; ++q)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int cl = 8 * (4 * g + v) + q;
+          red[(wv * 128 + cl) * RW + jt * 16 + l16] = acc[q][jr + jt][v];
+        }
     __syncthreads();
-    for (int id = tid; id < 128 * 16; id += TNT) {
-      const int cl = id / 16, jl = id % 16;
-      float sum = 0.0f;
+    // wavefront w sums columns [32w, 32w + 32): PL items of four per lane
+    constexpr int PL = RW / 8;
 #pragma unroll
-      for (int w = 0; w < TW; ++w) sum += red[(w * 128 + cl) * 16 + jl];
+    for (int k = 0; k < PL; ++k) {
+      const int id = wv * 64 * PL + k * 64 + lane;
+      const int cl = id / (RW / 4), jl = (id % (RW / 4)) * 4;
+      f32x4 sum = *reinterpret_cast<const f32x4*>(red + cl * RW + jl);
+#pragma unroll
+      for (int w = 1; w < TW; ++w) sum += *reinterpret_cast<const f32x4*>(red + (w * 128 + cl) * RW + jl);
+      const int j = jr * 16 + jl;
       if (c0 + cl < C) {
         if (a.splits == 1) {
-          if (jt * 16 + jl < a.R) a.out[(c0 + cl) * a.sc + (int64_t)(jt * 16 + jl) * a.sj] = sum;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (j + e < a.R) a.out[(c0 + cl) * a.sc + (int64_t)(j + e) * a.sj] = sum[e];
         } else {
-          store_dev(part + (c0 + cl) * RP + jt * 16 + jl, sum);
+          store16_dev(rpart, (uint32_t)(((c0 + cl) * RP + j) * 4), __builtin_bit_cast(u32x4, sum));
         }
       }
     }
     __syncthreads();
   }
   if (a.splits == 1) return;
-  // count this slice done once its partial stores are acknowledged; the last
-  // slice of the column tile sums the slices in order, four entries a thread
-  __shared__ int last;
+  // count this wavefront's 32 columns done in this slice once its stores are
+  // acknowledged (no barrier); the last wavefront to arrive sums the slices
+  // in order, NE entries of four per lane, every load of a batch of SB
+  // slices issued before the first sum
   __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  const int tile = bid % a.tiles;
-  if (tid == 0) {
-    last = add_dev(a.cnt + tile) + 1 == (uint32_t)a.splits;
-    if (last) zero_dev(a.cnt + tile);
-  }
-  __syncthreads();
-  if (!last) return;
-  // each thread owns NE entries of four; every load of a batch of SB slices
-  // is issued before the first sum (one memory round trip per batch)
-  constexpr int NE = 128 * RP / 4 / TNT, SB = 16 / NE;
+  uint32_t* const ctr = a.cnt + (bid % a.tiles) * TW + wv;
+  uint32_t old = 0;
+  if (lane == 0) old = add_dev(ctr);
+  if (__builtin_amdgcn_readfirstlane(old) + 1 != (uint32_t)a.splits) return;
+  if (lane == 0) zero_dev(ctr);
+  constexpr int NE = 32 * RP / 4 / 64, SB = 16 / NE;
   const rsrc_t rp_ = make_rsrc(a.partial, clamp_bytes((int64_t)a.splits * C * RP * 4));
-  float v[NE][4] = {};
+  f32x4 v[NE];
+#pragma unroll
+  for (int k = 0; k < NE; ++k) v[k] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
   for (int s0 = 0; s0 < a.splits; s0 += SB) {  // slices in order
     u32x4 pv[NE][SB];
 #pragma unroll
     for (int k = 0; k < NE; ++k) {
-      const int q4 = tid + k * TNT;
-      const int64_t c = c0 + (q4 * 4) / RP;
-      const int j = (q4 * 4) % RP;
+      const int e = k * 64 + lane;
+      const int64_t c = c0 + 32 * wv + e / (RP / 4);
+      const int j = (e % (RP / 4)) * 4;
 #pragma unroll
       for (int u = 0; u < SB; ++u)
         pv[k][u] = bload16_dev(rp_, opaque_u32(s0 + u < a.splits && c < C
@@ -483,19 +487,17 @@ __global__ void __launch_bounds__(TNT) k_lora_tn(TnArgs j0, TnArgs j1) {
 #pragma unroll
     for (int k = 0; k < NE; ++k)
 #pragma unroll
-      for (int u = 0; u < SB; ++u)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[k][e] += __uint_as_float(pv[k][u][e]);
+      for (int u = 0; u < SB; ++u) v[k] += __builtin_bit_cast(f32x4, pv[k][u]);
   }
 #pragma unroll
   for (int k = 0; k < NE; ++k) {
-    const int q4 = tid + k * TNT;
-    const int64_t c = c0 + (q4 * 4) / RP;
-    const int j = (q4 * 4) % RP;
+    const int e = k * 64 + lane;
+    const int64_t c = c0 + 32 * wv + e / (RP / 4);
+    const int j = (e % (RP / 4)) * 4;
     if (c >= C) continue;
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      if (j + e < a.R) a.out[c * a.sc + (int64_t)(j + e) * a.sj] = v[k][e];
+    for (int q = 0; q < 4; ++q)
+      if (j + q < a.R) a.out[c * a.sc + (int64_t)(j + q) * a.sj] = v[k][q];
   }
 }
 
@@ -543,7 +545,7 @@ hipError_t launch_lora_nt(hipStream_t st, const uint16_t* p, const uint16_t* q, 
                           int R, int64_t M, int64_t C, int rp, const LoraPlan& plan, float* partial,
                           const NtFinish& fin) {
   if (M == 0) return hipSuccess;
-  if (!fin.cnt || plan.tiles > LRQ_CNT_WORDS) return hipErrorInvalidValue;
+  if (!fin.cnt || plan.tiles * LW > SK_MAX_NB) return hipErrorInvalidValue;
   NtArgs a{p, q, M, C, ldq, R, plan.per, partial, fin};
   const dim3 grid((unsigned)plan.tiles, (unsigned)plan.splits);
   switch ((qrow ? 4 : 0) + rp / 16 - 1) {
@@ -568,11 +570,11 @@ hipError_t launch_lora_tn(hipStream_t st, const TnSpec* jobs, int njobs, int rp,
     const int64_t blocks = j.C > 0 ? j.plan.tiles * j.plan.splits : 0;
     // each job's column tiles count on their own counters
     t[i] = TnArgs{j.p,      j.q, j.M, j.C, j.ldq, j.R, j.plan.per, j.partial, (int)j.plan.tiles, (int)blocks,
-                  j.out,    j.sc, j.sj, j.plan.splits, cnt + ntiles};
+                  j.out,    j.sc, j.sj, j.plan.splits, cnt + ntiles * TW};
     total += blocks;
     ntiles += j.plan.tiles;
   }
-  if (!cnt || ntiles > LRQ_CNT_WORDS) return hipErrorInvalidValue;
+  if (!cnt || ntiles * TW > SK_MAX_NB) return hipErrorInvalidValue;
   if (total == 0) return hipSuccess;
   const dim3 grid((unsigned)total);
   switch (rp / 16) {
