@@ -132,11 +132,6 @@ LRQ_DEV f32x4 acc_zero4() {
   asm volatile("" : "+a"(z));
   return z;
 }
-LRQ_DEV f32x16 acc_zero16() {
-  f32x16 z = {};
-  asm volatile("" : "+a"(z));
-  return z;
-}
 
 LRQ_DEV bf16x8 as_bf16x8(const u32x4& v) { return __builtin_bit_cast(bf16x8, v); }
 

@@ -302,7 +302,9 @@ k_gemm(GemmArgs a, int tiles_m, int ntiles) {
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int j = 0; j < MJ; ++j) acc[i][j] = acc_zero16();
+      for (int j = 0; j < MJ; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
   };
 
   uint16_t* const bufs[2] = {sX0, sX1};
