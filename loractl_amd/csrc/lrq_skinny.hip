@@ -204,6 +204,271 @@ LRQ_DEV void sk_epilogue(const SkArgs& sa, int64_t nb, float* lds) {
 }
 
 
+// t partial of slice blockIdx.x (< TS): tpart[ts][m][j] = sum over the slice
+// of x[m, k] A[k, j] (backward: of dy[m, n] B[j, n], for u); the last slice
+// to finish sums the slices in order and publishes t stamped with the
+// launch's epoch. `xs` is the kernel's LDS buffer (4096 floats), `last` a
+// shared flag.
+template <bool BWD, int TSTEPS, int NT = SK_NT>
+LRQ_DEV void sk_t_slices(const SkArgs& sa, float* xs, int& last) {
+  const GemmArgs& a = sa.g;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c16 = lane & 15, kq = lane >> 4;
+  const int64_t M = a.m, K = a.l;
+  const int TS = sa.p.TS;
+  // ---------------- t partial: tpart[ts][m][j] = sum over the slice of x[m, k] A[k, j]
+  // (backward: of dy[m, n] B[j, n], for u)
+  const int ts = blockIdx.x, rp = a.rp, r = a.r;
+  const int64_t kt0 = (int64_t)ts * sa.p.KT, kt1 = kt0 + sa.p.KT < K ? kt0 + sa.p.KT : K;
+  const int nsteps = (int)((kt1 - kt0 + 31) / 32);
+  const rsrc_t rx = make_rsrc(a.act, clamp_bytes(M * K * 2));
+  const rsrc_t ra = make_rsrc(sa.A, clamp_bytes(K * r * 2));
+  f32x4 acc[4];
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt) acc[jt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+  // every load of the slice (at most 4 * TSTEPS steps) is issued at once
+  // (out-of-range ones read zero), then the matrix-core steps run as they land
+  u32x4 xf[TSTEPS];
+  uint32_t bw[TSTEPS][4][4];
+#pragma unroll
+  for (int i = 0; i < TSTEPS; ++i) {
+    {
+      const int st = wv + (NT / 64) * i;
+      const int64_t k = kt0 + (int64_t)st * 32 + kq * 8;
+      const bool kok = st < nsteps && k < kt1;  // K % 8 == 0 and slices are multiples of 32
+      xf[i] = bload16(rx, opaque_u32(kok ? (uint32_t)(((int64_t)c16 * K + k) * 2) : LRQ_OOB));
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) {
+        const int j = jt * 16 + c16;
+        const bool ok = kok && j < r;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          if (BWD) {
+            // B[j][k + 2q], B[j][k + 2q + 1] (one dword: the depth is a multiple of 8)
+            bw[i][jt][q] = bload4(ra, opaque_u32(ok ? (uint32_t)(((int64_t)j * K + k + 2 * q) * 2) : LRQ_OOB));
+          } else {
+            // A[k + 2q][j], A[k + 2q + 1][j]
+            const uint32_t off = (uint32_t)(((k + 2 * q) * r + j) * 2);
+            const uint32_t lo = bload2(ra, opaque_u32(ok ? off : LRQ_OOB));
+            const uint32_t hi = bload2(ra, opaque_u32(ok ? off + (uint32_t)(2 * r) : LRQ_OOB));
+            bw[i][jt][q] = lo | (hi << 16);
+          }
+        }
+      }
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // every column tile runs (tiles past rp multiply zeros): a matrix-core
+  // result read in a block other than the one that wrote it has come back
+  // stale here, so the steps stay branch-free
+#pragma unroll
+  for (int i = 0; i < TSTEPS; ++i)
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt)
+      acc[jt] = mfma16(as_bf16x8(xf[i]), as_bf16x8((u32x4){bw[i][jt][0], bw[i][jt][1], bw[i][jt][2], bw[i][jt][3]}),
+                       acc[jt]);
+  // reduce the four wavefronts; C element v of lane l: token 4*(l/16) + v, column l%16
+  float* tred = xs;  // [NT / 64][16][64]
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) tred[(wv * 16 + 4 * kq + v) * 64 + jt * 16 + c16] = acc[jt][v];
+  __syncthreads();
+  for (int i = tid; i < 16 * rp; i += NT) {
+    const int m = i / rp, j = i % rp;
+    float v = 0.0f;
+#pragma unroll
+    for (int w2 = 0; w2 < NT / 64; ++w2) v += tred[(w2 * 16 + m) * 64 + j];
+    store_dev(sa.tpart + ((int64_t)ts * 16 + m) * rp + j, v);
+  }
+  // counted done once every store of the workgroup is acknowledged at
+  // device scope; the last slice's workgroup sums the slices in order (two
+  // entries per thread, every slice's loads issued at once), rounds t to
+  // bf16 and publishes it, stamped with the launch's epoch
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) last = add_dev(sa.cnt + SK_TCNT) + 1 == (uint32_t)TS;
+  __syncthreads();
+  if (!last) return;
+  const rsrc_t rtp = make_rsrc(sa.tpart, clamp_bytes((int64_t)TS * 16 * rp * 4));
+  uint64_t* tfin = reinterpret_cast<uint64_t*>(sa.tpart + (int64_t)TS * 16 * rp);
+  // the epoch cannot advance before this workgroup publishes t: every
+  // epilogue of the launch waits for it
+  const uint32_t mark = stamp(__hip_atomic_load(sa.cnt + SK_EPOCH, __ATOMIC_RELAXED, XSCOPE));
+  // two entries per thread and pass (rp % 16 == 0: both in one token row)
+  for (int e0 = 2 * tid; e0 < 16 * rp; e0 += 2 * NT) {
+    float v[2] = {0.0f, 0.0f};
+    for (int q0 = 0; q0 < TS; q0 += SK_TMAX) {  // slices in order
+      u32x2 part[SK_TMAX];
+#pragma unroll
+      for (int q = 0; q < SK_TMAX; ++q)
+        part[q] = bload8_dev(rtp, opaque_u32(q0 + q < TS ? (uint32_t)(((q0 + q) * 16 * rp + e0) * 4) : LRQ_OOB));
+#pragma unroll
+      for (int q = 0; q < SK_TMAX; ++q) {
+        v[0] += __uint_as_float(part[q][0]);
+        v[1] += __uint_as_float(part[q][1]);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int i = e0 + e, m = i / rp, j = i % rp;
+      const uint32_t hb = pack_bf16x2(sa.scaling * v[e], 0.0f) & 0xffffu;  // t (u) as the caller sees it
+      // value and stamp in one 8-byte store: a reader sees both or neither
+      __hip_atomic_store(tfin + i, ((uint64_t)mark << 32) | (hb << 16), __ATOMIC_RELAXED, XSCOPE);
+      if (sa.t_out && m < M && (BWD || j < r)) sa.t_out[(int64_t)m * (BWD ? rp : r) + j] = (uint16_t)hb;
+    }
+  }
+}
+
+// The loads of one wavefront's run of reduction blocks [kb0, kb0 + nkb)
+// (at most WB; the rest read zeros) for row tiles rt0 .. rt0 + RTN - 1 (16
+// weight rows each) of block row nb, all issued at once in block order: the
+// x fragments, then the row tiles' packed words (and int4 scales); block b
+// is consumed once its loads are in.
+template <int FMT, bool BWD, int WB, int RTN>
+struct SkRun {
+  static constexpr bool I4 = FMT == LRQ_FMT_INT4;
+  u32x4 xf[WB][2];
+  u32x2 w4[I4 ? WB : 1][RTN];
+  u32x2 w8[I4 ? 1 : WB][RTN][2];
+  float sc[(I4 || BWD) ? WB : 1][RTN];  // forward int4: per row tile; backward: lane c16's depth (fp8: [b][0])
+};
+
+template <int FMT, bool BWD, int WB, int RTN>
+LRQ_DEV void sk_load(const GemmArgs& a, SkRun<FMT, BWD, WB, RTN>& R, int64_t nb, int rt0, int kb0, int nkb) {
+  constexpr bool I4 = FMT == LRQ_FMT_INT4;
+  const int lane = threadIdx.x & 63, c16 = lane & 15, kq = lane >> 4;
+  const int64_t M = a.m, K = a.l, E = a.e;
+  const int64_t KB = (K + 63) / 64;
+  constexpr uint32_t blkb = I4 ? 2048u : 4096u;
+  constexpr uint32_t rowb = I4 ? 32u : 64u;
+  const rsrc_t rw = make_rsrc(a.wdata + nb * KB * blkb, clamp_bytes(KB * (int64_t)blkb));
+  const int64_t Gp = I4 ? ((KB * 64) >> a.gshift) : 0;
+  // forward: int4 group scales of the block row ([NB][Gp][64]); backward: the
+  // per-depth scales (int4 the transposed table ST [KGt][64 KB], fp8 the
+  // channel scales [depth] or one scalar)
+  const int64_t NP = KB * 64;
+  const int64_t KGt = (BWD && I4) ? (((E + 63) / 64 * 64 + (1 << a.gshift) - 1) >> a.gshift) : 0;
+  const rsrc_t rs = BWD ? (I4 ? make_rsrc(a.wscale, clamp_bytes(KGt * NP * 4))
+                              : make_rsrc(a.wscale, a.per_channel ? clamp_bytes(K * 4) : 0u))
+                        : (I4 ? make_rsrc(a.wscale + nb * Gp * 64, clamp_bytes(Gp * 64 * 4)) : make_rsrc(a.wscale, 4u));
+  const float s0add = (BWD && !I4 && !a.per_channel) ? a.wscale[0] : 0.0f;
+  const rsrc_t rx = make_rsrc(a.act, clamp_bytes(M * K * 2));
+  const uint32_t woff = (uint32_t)c16 * rowb + (uint32_t)kq * (I4 ? 8u : 16u);
+  const uint32_t xoff = (uint32_t)(((int64_t)c16 * K + kq * 16) * 2);
+#pragma unroll
+  for (int b = 0; b < WB; ++b) {
+    const bool ok = b < nkb;
+    const uint32_t kb = (uint32_t)(kb0 + b);
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int64_t k = (int64_t)kb * 64 + kq * 16 + jj * 8;
+      const bool xok = ok && k < K;  // K % 8 == 0
+      R.xf[b][jj] = bload16(rx, opaque_u32(xok ? xoff + (uint32_t)(((int64_t)kb * 64 + jj * 8) * 2) : LRQ_OOB));
+    }
+    // backward: lane (kq, c16) holds the scale of depth 64 kb + 16 kq + c16,
+    // which the 16 lanes of its DPP row (one kq) broadcast among themselves
+    const uint32_t dpos = kb * 64u + (uint32_t)(kq * 16 + c16);
+    if (BWD && !I4) R.sc[b][0] = bloadf(rs, opaque_u32(ok ? dpos * 4u : LRQ_OOB)) + s0add;
+#pragma unroll
+    for (int rt = 0; rt < RTN; ++rt) {
+      const int rg = rt0 + rt;  // row tile within the 64-row block row
+      const uint32_t wo = kb * blkb + (uint32_t)(rg * 16) * rowb + woff;
+      if constexpr (I4) {
+        R.w4[b][rt] = bload8(rw, opaque_u32(ok ? wo : LRQ_OOB));
+        if (BWD) {
+          // group of output rows 64 nb + 16 rg .. +16 (groups are >= 32 and aligned)
+          const uint32_t kg = (uint32_t)((nb * 64 + rg * 16) >> a.gshift);
+          R.sc[b][rt] = bloadf(rs, opaque_u32(ok ? (uint32_t)((kg * NP + dpos) * 4) : LRQ_OOB));
+        } else {
+          const uint32_t j = (kb * 64u + (uint32_t)kq * 16u) >> a.gshift;
+          R.sc[b][rt] = bloadf(rs, opaque_u32(ok ? (j * 64u + (uint32_t)(rg * 16 + c16)) * 4u : LRQ_OOB));
+        }
+      } else {
+        const u32x4 v = bload16(rw, opaque_u32(ok ? wo : LRQ_OOB));
+        R.w8[b][rt][0] = (u32x2){v[0], v[1]};
+        R.w8[b][rt][1] = (u32x2){v[2], v[3]};
+      }
+    }
+  }
+}
+
+// The matrix-core steps of a run, block by block into acc[RTN] (C element v
+// of lane l: token 4*(l/16) + v, weight row 16 rt + l%16 of the run's tiles).
+template <int FMT, bool BWD, bool MQ, int WB, int RTN>
+LRQ_DEV void sk_math(const GemmArgs& a, const SkRun<FMT, BWD, WB, RTN>& R, f32x4 (&acc)[RTN]) {
+  constexpr bool I4 = FMT == LRQ_FMT_INT4;
+#pragma unroll
+  for (int rt = 0; rt < RTN; ++rt) acc[rt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int b = 0; b < WB; ++b) {
+    // blocks past this wavefront's run hold zeros: the steps stay
+    // unconditional (a matrix-core result read in another block than the
+    // one that wrote it has come back stale)
+    if constexpr (MQ) {
+      const u32x4 ones = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+      f32x4 xsum = {0.0f, 0.0f, 0.0f, 0.0f};
+      u32x4 xp[2];
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const u32x4 v = R.xf[b][jj];
+        xsum = mfma16(as_bf16x8(v), as_bf16x8(ones), xsum);
+        // k order 0 4 1 5 2 6 3 7, as the weight pairs below
+        xp[jj] = (u32x4){__builtin_amdgcn_perm(v[2], v[0], 0x05040100u), __builtin_amdgcn_perm(v[2], v[0], 0x07060302u),
+                         __builtin_amdgcn_perm(v[3], v[1], 0x05040100u), __builtin_amdgcn_perm(v[3], v[1], 0x07060302u)};
+      }
+#pragma unroll
+      for (int rt = 0; rt < RTN; ++rt) {
+        f32x4 ab = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+          const uint32_t d = R.w4[b][rt][jj];
+          // (u_e, u_e+4) as bf16 (128 + u) pairs
+          const u32x4 wb = {(d & 0x000f000fu) | 0x43004300u, ((d >> 4) & 0x000f000fu) | 0x43004300u,
+                            ((d >> 8) & 0x000f000fu) | 0x43004300u, ((d >> 12) & 0x000f000fu) | 0x43004300u};
+          ab = mfma16(as_bf16x8(xp[jj]), as_bf16x8(wb), ab);
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          acc[rt][v] = __builtin_fmaf(R.sc[b][rt], __builtin_fmaf(-136.0f, xsum[v], ab[v]), acc[rt][v]);
+      }
+      continue;
+    }
+#pragma unroll
+    for (int rt = 0; rt < RTN; ++rt) {
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        u32x4 wb;
+        if constexpr (BWD) {
+          // transposed section: value e is q (a sign-extended nibble, or the
+          // e4m3 value) times the scale of its depth 16 kq + 8 jj + e, then bf16
+          float f[8];
+          if (I4) {
+            const uint32_t d = R.w4[b][rt][jj];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) f[e] = (float)((int)(d << (28 - 4 * e)) >> 28);
+          } else {
+            fp8x4_to_f32(R.w8[b][rt][jj][0], f);
+            fp8x4_to_f32(R.w8[b][rt][jj][1], f + 4);
+          }
+          const float S = R.sc[b][I4 ? rt : 0];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) f[e] = row_bcast_n(S, 8 * jj + e) * f[e];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) wb[q] = pack_bf16x2(f[2 * q], f[2 * q + 1]);
+        } else if constexpr (I4) {
+          wb = dequant8_int4_bf16(R.w4[b][rt][jj], R.sc[b][rt], a.nib);
+        } else {
+          const u32x2 p0 = fp8x4_to_bf16(R.w8[b][rt][jj][0]), p1 = fp8x4_to_bf16(R.w8[b][rt][jj][1]);
+          wb = (u32x4){p0[0], p0[1], p1[0], p1[1]};
+        }
+        acc[rt] = mfma16(as_bf16x8(R.xf[b][jj]), as_bf16x8(wb), acc[rt]);
+      }
+    }
+  }
+}
+
 // MQ (int4 forward, groups of 64 or more, so one group per 64-wide block):
 // the matrix-core operand is the stored nibble u = q + 8 as the exact bf16
 // value 128 + u (bits 0x4300 | u, two bit operations per pair), each block
@@ -226,108 +491,7 @@ __global__ void __launch_bounds__(SK_NT) k_sk(SkArgs sa) {
   const int TS = sa.p.TS;
 
   if ((int)blockIdx.x < TS) {
-    // ---------------- t partial: tpart[ts][m][j] = sum over the slice of x[m, k] A[k, j]
-    // (backward: of dy[m, n] B[j, n], for u)
-    const int ts = blockIdx.x, rp = a.rp, r = a.r;
-    const int64_t kt0 = (int64_t)ts * sa.p.KT, kt1 = kt0 + sa.p.KT < K ? kt0 + sa.p.KT : K;
-    const int nsteps = (int)((kt1 - kt0 + 31) / 32);
-    const rsrc_t rx = make_rsrc(a.act, clamp_bytes(M * K * 2));
-    const rsrc_t ra = make_rsrc(sa.A, clamp_bytes(K * r * 2));
-    f32x4 acc[4];
-#pragma unroll
-    for (int jt = 0; jt < 4; ++jt) acc[jt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-    // every load of the slice (at most 4 * TSTEPS steps) is issued at once
-    // (out-of-range ones read zero), then the matrix-core steps run as they land
-    u32x4 xf[TSTEPS];
-    uint32_t bw[TSTEPS][4][4];
-#pragma unroll
-    for (int i = 0; i < TSTEPS; ++i) {
-      {
-        const int st = wv + (SK_NT / 64) * i;
-        const int64_t k = kt0 + (int64_t)st * 32 + kq * 8;
-        const bool kok = st < nsteps && k < kt1;  // K % 8 == 0 and slices are multiples of 32
-        xf[i] = bload16(rx, opaque_u32(kok ? (uint32_t)(((int64_t)c16 * K + k) * 2) : LRQ_OOB));
-#pragma unroll
-        for (int jt = 0; jt < 4; ++jt) {
-          const int j = jt * 16 + c16;
-          const bool ok = kok && j < r;
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            if (BWD) {
-              // B[j][k + 2q], B[j][k + 2q + 1] (one dword: the depth is a multiple of 8)
-              bw[i][jt][q] = bload4(ra, opaque_u32(ok ? (uint32_t)(((int64_t)j * K + k + 2 * q) * 2) : LRQ_OOB));
-            } else {
-              // A[k + 2q][j], A[k + 2q + 1][j]
-              const uint32_t off = (uint32_t)(((k + 2 * q) * r + j) * 2);
-              const uint32_t lo = bload2(ra, opaque_u32(ok ? off : LRQ_OOB));
-              const uint32_t hi = bload2(ra, opaque_u32(ok ? off + (uint32_t)(2 * r) : LRQ_OOB));
-              bw[i][jt][q] = lo | (hi << 16);
-            }
-          }
-        }
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    // every column tile runs (tiles past rp multiply zeros): a matrix-core
-    // result read in a block other than the one that wrote it has come back
-    // stale here, so the steps stay branch-free
-#pragma unroll
-    for (int i = 0; i < TSTEPS; ++i)
-#pragma unroll
-      for (int jt = 0; jt < 4; ++jt)
-        acc[jt] = mfma16(as_bf16x8(xf[i]), as_bf16x8((u32x4){bw[i][jt][0], bw[i][jt][1], bw[i][jt][2], bw[i][jt][3]}),
-                         acc[jt]);
-    // reduce the four wavefronts; C element v of lane l: token 4*(l/16) + v, column l%16
-    float* tred = xs;  // [4][16][64]
-#pragma unroll
-    for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) tred[(wv * 16 + 4 * kq + v) * 64 + jt * 16 + c16] = acc[jt][v];
-    __syncthreads();
-    for (int i = tid; i < 16 * rp; i += SK_NT) {
-      const int m = i / rp, j = i % rp;
-      float v = 0.0f;
-#pragma unroll
-      for (int w2 = 0; w2 < SK_NT / 64; ++w2) v += tred[(w2 * 16 + m) * 64 + j];
-      store_dev(sa.tpart + ((int64_t)ts * 16 + m) * rp + j, v);
-    }
-    // counted done once every store of the workgroup is acknowledged at
-    // device scope; the last slice's workgroup sums the slices in order (two
-    // entries per thread, every slice's loads issued at once), rounds t to
-    // bf16 and publishes it, stamped with the launch's epoch
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (tid == 0) last = add_dev(sa.cnt + SK_TCNT) + 1 == (uint32_t)TS;
-    __syncthreads();
-    if (!last) return;
-    const rsrc_t rtp = make_rsrc(sa.tpart, clamp_bytes((int64_t)TS * 16 * rp * 4));
-    uint64_t* tfin = reinterpret_cast<uint64_t*>(sa.tpart + (int64_t)TS * 16 * rp);
-    // the epoch cannot advance before this workgroup publishes t: every
-    // epilogue of the launch waits for it
-    const uint32_t mark = stamp(__hip_atomic_load(sa.cnt + SK_EPOCH, __ATOMIC_RELAXED, XSCOPE));
-    // two entries per thread and pass (rp % 16 == 0: both in one token row)
-    for (int e0 = 2 * tid; e0 < 16 * rp; e0 += 2 * SK_NT) {
-      float v[2] = {0.0f, 0.0f};
-      for (int q0 = 0; q0 < TS; q0 += SK_TMAX) {  // slices in order
-        u32x2 part[SK_TMAX];
-#pragma unroll
-        for (int q = 0; q < SK_TMAX; ++q)
-          part[q] = bload8_dev(rtp, opaque_u32(q0 + q < TS ? (uint32_t)(((q0 + q) * 16 * rp + e0) * 4) : LRQ_OOB));
-#pragma unroll
-        for (int q = 0; q < SK_TMAX; ++q) {
-          v[0] += __uint_as_float(part[q][0]);
-          v[1] += __uint_as_float(part[q][1]);
-        }
-      }
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const int i = e0 + e, m = i / rp, j = i % rp;
-        const uint32_t hb = pack_bf16x2(sa.scaling * v[e], 0.0f) & 0xffffu;  // t (u) as the caller sees it
-        // value and stamp in one 8-byte store: a reader sees both or neither
-        __hip_atomic_store(tfin + i, ((uint64_t)mark << 32) | (hb << 16), __ATOMIC_RELAXED, XSCOPE);
-        if (sa.t_out && m < M && (BWD || j < r)) sa.t_out[(int64_t)m * (BWD ? rp : r) + j] = (uint16_t)hb;
-      }
-    }
+    sk_t_slices<BWD, TSTEPS>(sa, xs, last);
     return;
   }
 
@@ -342,135 +506,14 @@ __global__ void __launch_bounds__(SK_NT) k_sk(SkArgs sa) {
   const int nks = (int)(KB - kbs < KS ? KB - kbs : KS);  // blocks of this split (>= 1)
   const int kb0 = kbs + (nks * wv) / 4, nkb = kbs + (nks * (wv + 1)) / 4 - kb0;  // this wavefront's run
 
-  constexpr uint32_t blkb = I4 ? 2048u : 4096u;
-  constexpr uint32_t rowb = I4 ? 32u : 64u;
-  const rsrc_t rw = make_rsrc(a.wdata + nb * KB * blkb, clamp_bytes(KB * (int64_t)blkb));
-  const int64_t Gp = I4 ? ((KB * 64) >> a.gshift) : 0;
-  // forward: int4 group scales of the block row ([NB][Gp][64]); backward: the
-  // per-depth scales (int4 the transposed table ST [KGt][64 KB], fp8 the
-  // channel scales [depth] or one scalar)
-  const int64_t NP = KB * 64;
-  const int64_t KGt = (BWD && I4) ? (((E + 63) / 64 * 64 + (1 << a.gshift) - 1) >> a.gshift) : 0;
-  const rsrc_t rs = BWD ? (I4 ? make_rsrc(a.wscale, clamp_bytes(KGt * NP * 4))
-                              : make_rsrc(a.wscale, a.per_channel ? clamp_bytes(K * 4) : 0u))
-                        : (I4 ? make_rsrc(a.wscale + nb * Gp * 64, clamp_bytes(Gp * 64 * 4)) : make_rsrc(a.wscale, 4u));
-  const float s0add = (BWD && !I4 && !a.per_channel) ? a.wscale[0] : 0.0f;
-  const rsrc_t rx = make_rsrc(a.act, clamp_bytes(M * K * 2));
-  const uint32_t woff = (uint32_t)c16 * rowb + (uint32_t)kq * (I4 ? 8u : 16u);
-  const uint32_t xoff = (uint32_t)(((int64_t)c16 * K + kq * 16) * 2);
-
-  // all loads in block order: x fragments, then the four row tiles' packed
-  // words (and int4 scales); block b is consumed once its loads are in
-  u32x4 xf[SK_WB][2];
-  u32x2 w4[I4 ? SK_WB : 1][4];
-  u32x2 w8[I4 ? 1 : SK_WB][4][2];
-  float sc[(I4 || BWD) ? SK_WB : 1][4];  // forward int4: per row tile; backward: lane c16's depth (fp8: [b][0])
-#pragma unroll
-  for (int b = 0; b < SK_WB; ++b) {
-    const bool ok = b < nkb;
-    const uint32_t kb = (uint32_t)(kb0 + b);
-#pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-      const int64_t k = (int64_t)kb * 64 + kq * 16 + jj * 8;
-      const bool xok = ok && k < K;  // K % 8 == 0
-      xf[b][jj] = bload16(rx, opaque_u32(xok ? xoff + (uint32_t)(((int64_t)kb * 64 + jj * 8) * 2) : LRQ_OOB));
-    }
-    // backward: lane (kq, c16) holds the scale of depth 64 kb + 16 kq + c16,
-    // which the 16 lanes of its DPP row (one kq) broadcast among themselves
-    const uint32_t dpos = kb * 64u + (uint32_t)(kq * 16 + c16);
-    if (BWD && !I4) sc[b][0] = bloadf(rs, opaque_u32(ok ? dpos * 4u : LRQ_OOB)) + s0add;
-#pragma unroll
-    for (int rt = 0; rt < 4; ++rt) {
-      const uint32_t wo = kb * blkb + (uint32_t)(rt * 16) * rowb + woff;
-      if constexpr (I4) {
-        w4[b][rt] = bload8(rw, opaque_u32(ok ? wo : LRQ_OOB));
-        if (BWD) {
-          // group of output rows 64 nb + 16 rt .. +16 (groups are >= 32 and aligned)
-          const uint32_t kg = (uint32_t)((nb * 64 + rt * 16) >> a.gshift);
-          sc[b][rt] = bloadf(rs, opaque_u32(ok ? (uint32_t)((kg * NP + dpos) * 4) : LRQ_OOB));
-        } else {
-          const uint32_t j = (kb * 64u + (uint32_t)kq * 16u) >> a.gshift;
-          sc[b][rt] = bloadf(rs, opaque_u32(ok ? (j * 64u + (uint32_t)(rt * 16 + c16)) * 4u : LRQ_OOB));
-        }
-      } else {
-        const u32x4 v = bload16(rw, opaque_u32(ok ? wo : LRQ_OOB));
-        w8[b][rt][0] = (u32x2){v[0], v[1]};
-        w8[b][rt][1] = (u32x2){v[2], v[3]};
-      }
-    }
-  }
+  SkRun<FMT, BWD, SK_WB, 4> R;
+  sk_load<FMT, BWD, SK_WB, 4>(a, R, nb, 0, kb0, nkb);
 
   // keep every load ahead of the math (the scheduler would otherwise trade
   // loads in flight for registers)
   __builtin_amdgcn_sched_barrier(0);
   f32x4 acc[4];
-#pragma unroll
-  for (int rt = 0; rt < 4; ++rt) acc[rt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-  for (int b = 0; b < SK_WB; ++b) {
-    // blocks past this wavefront's run hold zeros: the steps stay
-    // unconditional (a matrix-core result read in another block than the
-    // one that wrote it has come back stale)
-    if constexpr (MQ) {
-      const u32x4 ones = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
-      f32x4 xsum = {0.0f, 0.0f, 0.0f, 0.0f};
-      u32x4 xp[2];
-#pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        const u32x4 v = xf[b][jj];
-        xsum = mfma16(as_bf16x8(v), as_bf16x8(ones), xsum);
-        // k order 0 4 1 5 2 6 3 7, as the weight pairs below
-        xp[jj] = (u32x4){__builtin_amdgcn_perm(v[2], v[0], 0x05040100u), __builtin_amdgcn_perm(v[2], v[0], 0x07060302u),
-                         __builtin_amdgcn_perm(v[3], v[1], 0x05040100u), __builtin_amdgcn_perm(v[3], v[1], 0x07060302u)};
-      }
-#pragma unroll
-      for (int rt = 0; rt < 4; ++rt) {
-        f32x4 ab = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj) {
-          const uint32_t d = w4[b][rt][jj];
-          // (u_e, u_e+4) as bf16 (128 + u) pairs
-          const u32x4 wb = {(d & 0x000f000fu) | 0x43004300u, ((d >> 4) & 0x000f000fu) | 0x43004300u,
-                            ((d >> 8) & 0x000f000fu) | 0x43004300u, ((d >> 12) & 0x000f000fu) | 0x43004300u};
-          ab = mfma16(as_bf16x8(xp[jj]), as_bf16x8(wb), ab);
-        }
-#pragma unroll
-        for (int v = 0; v < 4; ++v) acc[rt][v] = __builtin_fmaf(sc[b][rt], __builtin_fmaf(-136.0f, xsum[v], ab[v]), acc[rt][v]);
-      }
-      continue;
-    }
-#pragma unroll
-    for (int rt = 0; rt < 4; ++rt) {
-#pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        u32x4 wb;
-        if constexpr (BWD) {
-          // transposed section: value e is q (a sign-extended nibble, or the
-          // e4m3 value) times the scale of its depth 16 kq + 8 jj + e, then bf16
-          float f[8];
-          if (I4) {
-            const uint32_t d = w4[b][rt][jj];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) f[e] = (float)((int)(d << (28 - 4 * e)) >> 28);
-          } else {
-            fp8x4_to_f32(w8[b][rt][jj][0], f);
-            fp8x4_to_f32(w8[b][rt][jj][1], f + 4);
-          }
-          const float S = sc[b][I4 ? rt : 0];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) f[e] = row_bcast_n(S, 8 * jj + e) * f[e];
-#pragma unroll
-          for (int q = 0; q < 4; ++q) wb[q] = pack_bf16x2(f[2 * q], f[2 * q + 1]);
-        } else if constexpr (I4) {
-          wb = dequant8_int4_bf16(w4[b][rt][jj], sc[b][rt], a.nib);
-        } else {
-          const u32x2 p0 = fp8x4_to_bf16(w8[b][rt][jj][0]), p1 = fp8x4_to_bf16(w8[b][rt][jj][1]);
-          wb = (u32x4){p0[0], p0[1], p1[0], p1[1]};
-        }
-        acc[rt] = mfma16(as_bf16x8(xf[b][jj]), as_bf16x8(wb), acc[rt]);
-      }
-    }
-  }
+  sk_math<FMT, BWD, MQ, SK_WB, 4>(a, R, acc);
   // reduce the four runs: C element v of lane l is token 4*(l/16) + v,
   // weight row 16 rt + l%16
   float* red = xs;  // [4 runs][4 rt][16 tokens][16 rows]
@@ -505,6 +548,191 @@ __global__ void __launch_bounds__(SK_NT) k_sk(SkArgs sa) {
   // the last epilogue of the launch resets the t and epilogue counters and
   // advances the epoch (every read of t, and of the epoch, is over by then)
   if (tid == 0 && add_dev(sa.cnt + SK_DCNT) + 1 == (uint32_t)((E + 63) / 64)) {
+    zero_dev(sa.cnt + SK_TCNT);
+    zero_dev(sa.cnt + SK_DCNT);
+    add_dev(sa.cnt + SK_EPOCH);
+  }
+}
+
+// ---------------------------------------------------------------- full depth
+// Forward with d_in <= 4 * SKF_WB * 64: a workgroup owns 16 RT weight rows (RT
+// of the four 16-row tiles of a 64-row block row) over the whole reduction. Its four wavefronts take
+// consecutive runs of the blocks (every load of a run issued at once, as in
+// k_sk), meet in LDS and the workgroup finishes its rows itself:
+//   y[m, n] = bf16(sc[n] * base[m, n] + sum_j t[m, j] B[j, n] + bias[n])
+// so no split partial, counter or finishing epilogue sits between the weight
+// stream and y. t comes from the same t workgroups and stamped publication
+// as in k_sk (dispatched first, waiting on nothing).
+constexpr int SKF_WB = 12;  // blocks per run of four wavefronts (d_in <= 3072); NT / 64 runs share them
+constexpr int SKF_RT = 4;   // 16-row tiles per workgroup
+constexpr int SKF_NT = 512; // threads per workgroup
+
+// The epilogue of the 16 RT rows n0 ..: `red` holds the runs' sums
+// [NT / 64][RT tiles][16 tokens][16 rows], then (with t) the LoRA term in the
+// same layout. Thread (tid < 256): token m = tid / 16, column pairs cq + 16 h.
+template <int FMT, int RT, int NT>
+LRQ_DEV void skf_epilogue(const SkArgs& sa, int64_t n0, const float* red) {
+  constexpr int NP = 8 * RT;                 // column pairs
+  constexpr int NW = NT / 64;                // runs
+  constexpr int PH = NP > 16 ? NP / 16 : 1;  // pairs per thread
+  const GemmArgs& a = sa.g;
+  const int tid = threadIdx.x;
+  const int64_t M = a.m, E = a.e;
+  const bool lora = sa.p.TS > 0;
+  if (tid >= 256) return;
+  const int m = tid >> 4, cq = tid & 15;
+#pragma unroll
+  for (int h = 0; h < PH; ++h) {
+    const int pc = cq + 16 * h;  // column pair: row tile pc / 8
+    const int64_t n = n0 + 2 * pc;
+    if (!(m < M && pc < NP && n < E)) continue;  // E % 8 == 0: n < E implies n + 1 < E
+    float base[2], l[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int cl = 2 * pc + e, rt = cl >> 4, c = cl & 15;
+      float v = 0.0f;
+#pragma unroll
+      for (int w2 = 0; w2 < NW; ++w2) v += red[((w2 * RT + rt) * 16 + m) * 16 + c];
+      base[e] = v;
+      l[e] = lora ? red[((NW * RT + rt) * 16 + m) * 16 + c] : 0.0f;
+    }
+    float sc[2] = {1.0f, 1.0f}, bias[2] = {0.0f, 0.0f};
+    if (FMT == LRQ_FMT_FP8) {
+#pragma unroll
+      for (int e = 0; e < 2; ++e) sc[e] = a.wscale[a.per_channel ? n + e : 0];
+    }
+    if (a.bias) {
+#pragma unroll
+      for (int e = 0; e < 2; ++e) bias[e] = a.bias[n + e];
+    }
+    *reinterpret_cast<uint32_t*>(a.out + (int64_t)m * E + n) =
+        pack_bf16x2(base[0] * sc[0] + l[0] + bias[0], base[1] * sc[1] + l[1] + bias[1]);
+  }
+}
+
+template <int FMT, bool MQ, int TSTEPS, int RT, int NT>
+__global__ void __launch_bounds__(NT) k_skf(SkArgs sa) {
+  constexpr int NP = 8 * RT;   // column pairs of the workgroup's rows
+  constexpr int NW = NT / 64;  // runs
+  // LDS: the runs' sums and the LoRA term [NW + 1][RT][16][16], then the
+  // factor slice B[j][rows] as column pairs [64][NP]; the t slices use the
+  // first NW * 1024 floats
+  constexpr int RED = (NW + 1) * RT * 16 * 16, XS = RED + 64 * NP;
+  __shared__ __attribute__((aligned(16))) float xs[XS > NW * 1024 ? XS : NW * 1024];
+  __shared__ int last;
+  const GemmArgs& a = sa.g;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c16 = lane & 15, kq = lane >> 4;
+  const int64_t K = a.l, E = a.e;
+  const int64_t KB = (K + 63) / 64;
+  const int TS = sa.p.TS, rp = a.rp;
+  if ((int)blockIdx.x < TS) {
+    sk_t_slices<false, TSTEPS, NT>(sa, xs, last);
+    return;
+  }
+  const int64_t hb = (int64_t)blockIdx.x - TS;  // this workgroup's rows: tiles RT (hb % (4 / RT)) .. of block row nb
+  const int64_t nb = hb / (4 / RT);
+  const int rt0 = (int)(hb % (4 / RT)) * RT;
+  const int64_t n0 = hb * 16 * RT;
+  const int kb0 = (int)((KB * wv) / NW), nkb = (int)((KB * (wv + 1)) / NW) - kb0;
+
+  // the factor slice B[j][n0 ..] as column pairs (4-byte loads), out ahead of
+  // the weight stream: entry i = tid + NT q is (j = i / NP, pair i % NP)
+  constexpr int NBQ = (64 * NP + NT - 1) / NT;
+  uint32_t bq[NBQ];
+  {
+    const rsrc_t rb = make_rsrc(a.lw, TS > 0 ? clamp_bytes((int64_t)a.r * E * 2) : 0u);
+#pragma unroll
+    for (int q = 0; q < NBQ; ++q) {
+      const int i = tid + q * NT, j = i / NP, pc = i % NP;
+      const int64_t nn = n0 + 2 * pc;
+      const bool ok = j < a.r && nn < E;
+      bq[q] = bload4(rb, opaque_u32(ok ? (uint32_t)(((int64_t)j * E + nn) * 2) : LRQ_OOB));
+    }
+  }
+  constexpr int WB = (SKF_WB * 4 + NW - 1) / NW;  // blocks per run, at most
+  SkRun<FMT, false, WB, RT> R;
+  sk_load<FMT, false, WB, RT>(a, R, nb, rt0, kb0, nkb);
+  // keep every load ahead of the rest
+  __builtin_amdgcn_sched_barrier(0);
+  uint32_t* bsl = reinterpret_cast<uint32_t*>(xs + RED);
+#pragma unroll
+  for (int q = 0; q < NBQ; ++q)
+    if (tid + q * NT < 64 * NP) bsl[tid + q * NT] = bq[q];
+  __syncthreads();  // (the factor slice only waits for its own loads, issued first)
+  f32x4 acc[RT];
+  sk_math<FMT, false, MQ, WB, RT>(a, R, acc);
+  float* red = xs;
+  if (TS > 0 && wv == 0) {
+    // the first run to finish adds t . B for the workgroup's rows, a
+    // rank-wide matrix-core step per row tile, while the others still
+    // stream: t in the A role (lane (c16, kq): t[c16][32 ks + 8 kq ..]) as
+    // published, every entry stamped with the launch's epoch
+    const uint32_t want = stamp(__hip_atomic_load(sa.cnt + SK_EPOCH, __ATOMIC_RELAXED, XSCOPE));
+    const rsrc_t rtf = make_rsrc(sa.tpart + (int64_t)TS * 16 * rp, clamp_bytes((int64_t)16 * rp * 8));
+    u32x2 tv[2][8];
+    auto load_t = [&]() {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int j = 32 * ks + 8 * kq + e;
+          tv[ks][e] = bload8_dev(rtf, opaque_u32(j < rp ? (uint32_t)((c16 * rp + j) * 8) : LRQ_OOB));
+        }
+    };
+    load_t();
+    for (uint32_t polls = 0;; ++polls) {
+      bool ok = true;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ok = ok && (32 * ks + 8 * kq + e >= rp || tv[ks][e][1] == want);
+      if (__all(ok)) break;
+      if (polls == SK_MAX_POLLS) {
+        __hip_atomic_store(sa.cnt + SK_FAIL, 1u, __ATOMIC_RELAXED, XSCOPE);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+      load_t();
+    }
+    // B in the B role (lane (c16, kq): B[32 ks + 8 kq ..][row 16 rt + c16])
+    // from the staged slice; rank steps past rp multiply zeros
+    f32x4 lacc[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) lacc[rt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    const uint16_t* bsh = reinterpret_cast<const uint16_t*>(bsl);  // [64 j][2 NP] bf16
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      u32x4 ta;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) ta[q] = (tv[ks][2 * q][0] >> 16) | (tv[ks][2 * q + 1][0] & 0xffff0000u);
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        u32x4 bb;
+        const int col = 16 * rt + c16;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int j = 32 * ks + 8 * kq + 2 * q;
+          bb[q] = (uint32_t)bsh[j * 2 * NP + col] | ((uint32_t)bsh[(j + 1) * 2 * NP + col] << 16);
+        }
+        lacc[rt] = mfma16(as_bf16x8(ta), as_bf16x8(bb), lacc[rt]);
+      }
+    }
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) red[((NW * RT + rt) * 16 + 4 * kq + v) * 16 + c16] = lacc[rt][v];
+  }
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) red[((wv * RT + rt) * 16 + 4 * kq + v) * 16 + c16] = acc[rt][v];
+  __syncthreads();
+  skf_epilogue<FMT, RT, NT>(sa, n0, red);
+  // the last workgroup of the launch resets the t and epilogue counters and
+  // advances the epoch (every read of t, and of the epoch, is over by then)
+  if (tid == 0 && add_dev(sa.cnt + SK_DCNT) + 1 == (uint32_t)((E + 16 * RT - 1) / (16 * RT))) {
     zero_dev(sa.cnt + SK_TCNT);
     zero_dev(sa.cnt + SK_DCNT);
     add_dev(sa.cnt + SK_EPOCH);
@@ -554,9 +782,30 @@ hipError_t launch_skinny(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, c
     return hipErrorInvalidValue;
   SkArgs sa{a, A, p, part, tpart, cnt, scaling, t_out};
   if (a.rp == 0 || !A) sa.p.TS = 0;
-  const unsigned grid = (unsigned)(NB * p.S + sa.p.TS);
   // 32-wide steps per wavefront of a t slice (skinny_plan; 0 without t)
   const int steps = (int)(p.KT / 128);
+  if (!bwd && (a.l + 63) / 64 <= 4 * SKF_WB) {
+    // the whole reduction fits one workgroup's runs: 32-row workgroups, no splits
+    const unsigned gridf = (unsigned)((a.e + 16 * SKF_RT - 1) / (16 * SKF_RT) + sa.p.TS);
+#define SKF_LAUNCH(F, Q)                                                                                 \
+  switch (steps) {                                                                                       \
+    case 4: case 3: hipLaunchKernelGGL((k_skf<F, Q, 4, SKF_RT, SKF_NT>), dim3(gridf), dim3(SKF_NT), 0, st, sa); break; \
+    case 2: hipLaunchKernelGGL((k_skf<F, Q, 2, SKF_RT, SKF_NT>), dim3(gridf), dim3(SKF_NT), 0, st, sa); break;         \
+    default: hipLaunchKernelGGL((k_skf<F, Q, 1, SKF_RT, SKF_NT>), dim3(gridf), dim3(SKF_NT), 0, st, sa); break;        \
+  }
+    if (fmt == LRQ_FMT_INT4) {
+      if (a.gshift >= 6) {
+        SKF_LAUNCH(LRQ_FMT_INT4, true)
+      } else {
+        SKF_LAUNCH(LRQ_FMT_INT4, false)
+      }
+    } else {
+      SKF_LAUNCH(LRQ_FMT_FP8, false)
+    }
+#undef SKF_LAUNCH
+    return hipGetLastError();
+  }
+  const unsigned grid = (unsigned)(NB * p.S + sa.p.TS);
 #define SK_LAUNCH(F, B, Q)                                                                             \
   switch (steps) {                                                                                     \
     case 4: case 3: hipLaunchKernelGGL((k_sk<F, B, Q, 4>), dim3(grid), dim3(SK_NT), 0, st, sa); break; \

@@ -30,7 +30,8 @@ FORMATS = [("int4", 32, True), ("int4", 64, True), ("int4", 128, True), ("fp8", 
 
 
 @pytest.mark.parametrize("M", [1, 7, 16])
-@pytest.mark.parametrize("K,N", [(96, 72), (1088, 520), (3072, 264)])
+# d_in <= 3072: full-depth workgroups; 4160: reduction splits with partials
+@pytest.mark.parametrize("K,N", [(96, 72), (1088, 520), (3072, 264), (4160, 136)])
 @pytest.mark.parametrize("fmt,g,pc", FORMATS)
 def test_skinny_base_and_lora(cuda, M, K, N, fmt, g, pc):
     if fmt == "int4" and K % g:
