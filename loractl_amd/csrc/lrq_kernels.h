@@ -76,6 +76,7 @@ struct SkinnyPlan {
   int S, KS;  // reduction splits of the base, 64-wide blocks per split
   int TS;     // k slices of t (0 without LoRA)
   int64_t KT; // k per t slice (a multiple of 32)
+  int full;   // a forward may run whole-depth workgroups (k_skf) instead of splits
 };
 // arrival counters at the start of every workspace (zeroed when allocated):
 // block rows at [0, SK_MAX_NB), then, one 128-byte line each, the count of

@@ -766,6 +766,15 @@ SkinnyPlan skinny_plan(int64_t n, int64_t k, int rp, int num_cus) {
     p.TS = (int)((k + p.KT - 1) / p.KT);
     if (p.TS < 1) p.TS = 1;
   }
+  // whole-depth workgroups (k_skf, forward only) when the depth fits a
+  // workgroup's runs and its workgroups are many (>= 128) yet fit the CUs in
+  // one round with the t slices. Measured per shape at m = 16 (graph
+  // replay over rotated weights, us, k_skf against splits): 3072 -> 12288
+  // 12.7 / 13.4, 3072 -> 9216 11.9 / 12.6, 2560 -> 9728 11.9 / 12.4; but
+  // 2560 -> 4096 10.8 / 10.8, 2560 -> 1024 9.9 / 9.0, 3072 -> 18432 (288
+  // workgroups) 20.6 / 16.3.
+  const int64_t nwf = (n + 16 * SKF_RT - 1) / (16 * SKF_RT);  // k_skf workgroups
+  p.full = KB <= 4 * SKF_WB && nwf >= 128 && nwf + p.TS <= num_cus;
   return p;
 }
 
@@ -784,8 +793,8 @@ hipError_t launch_skinny(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, c
   if (a.rp == 0 || !A) sa.p.TS = 0;
   // 32-wide steps per wavefront of a t slice (skinny_plan; 0 without t)
   const int steps = (int)(p.KT / 128);
-  if (!bwd && (a.l + 63) / 64 <= 4 * SKF_WB) {
-    // the whole reduction fits one workgroup's runs: 32-row workgroups, no splits
+  if (!bwd && p.full) {
+    // whole-depth workgroups, no splits (skinny_plan)
     const unsigned gridf = (unsigned)((a.e + 16 * SKF_RT - 1) / (16 * SKF_RT) + sa.p.TS);
 #define SKF_LAUNCH(F, Q)                                                                                 \
   switch (steps) {                                                                                       \

@@ -31,6 +31,7 @@ PATHS = [
     ("few-token m=5", 5, 512, 768),
     ("few-token m=16", 16, 3072, 3072),
     ("few-token split forward m=9", 9, 4160, 520),
+    ("few-token whole-depth forward m=16", 16, 3072, 8192),
     ("split-depth r192", 256, 3072, 3072),
     ("tiled r192 fwd / split bwd", 4096, 256, 3072),
     ("tiled r256", 4096, 4096, 4096),

@@ -30,8 +30,9 @@ FORMATS = [("int4", 32, True), ("int4", 64, True), ("int4", 128, True), ("fp8", 
 
 
 @pytest.mark.parametrize("M", [1, 7, 16])
-# d_in <= 3072: full-depth workgroups; 4160: reduction splits with partials
-@pytest.mark.parametrize("K,N", [(96, 72), (1088, 520), (3072, 264), (4160, 136)])
+# reduction splits with partials, except (1088, 8192): 128 whole-depth
+# workgroups (skinny_plan's rule)
+@pytest.mark.parametrize("K,N", [(96, 72), (1088, 520), (3072, 264), (4160, 136), (1088, 8192)])
 @pytest.mark.parametrize("fmt,g,pc", FORMATS)
 def test_skinny_base_and_lora(cuda, M, K, N, fmt, g, pc):
     if fmt == "int4" and K % g:
@@ -49,8 +50,9 @@ def test_skinny_base_and_lora(cuda, M, K, N, fmt, g, pc):
 
 
 @pytest.mark.parametrize("r", [1, 16, 33, 64])
-def test_skinny_ranks_and_bias(cuda, r):
-    M, K, N, g = 9, 640, 200, 64
+@pytest.mark.parametrize("N", [200, 8192])  # splits; whole-depth workgroups
+def test_skinny_ranks_and_bias(cuda, r, N):
+    M, K, g = 9, 640, 64
     w, x, a, b, _ = case_inputs(M, K, N, r, seed=r, b_sigma=0.05)
     wq, wdq = _weight(w, "int4", g, cuda)
     bias = np.linspace(-1, 1, N).astype(np.float32)
