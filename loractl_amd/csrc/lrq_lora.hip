@@ -506,14 +506,16 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 }  // namespace
 
 // nt: 128-token tiles x column slices (multiples of 32) so that the grid is
-// ~256 workgroups (one per CU, 8 wavefronts each), in at most 32 slices (a
-// few tokens gain nothing from more workgroups, and the reduction reads
-// every slice); a slice wider than the LDS factor slice holds (nt_cap) is
-// staged and streamed in sub-slices.
+// up to ~256 workgroups (one per CU, 8 wavefronts each), in at most 8 slices:
+// each slice costs the finishing wavefronts a load, and short slices stream
+// too little to hide their staging (3072 -> 3072 at M = 1024: t 17.8 -> 11.4
+// us and u 16.7 -> 11.1 us going from 32 slices to 8; 16 gave 12.6 and 12.3);
+// a slice wider than the LDS factor slice holds (nt_cap) is staged and
+// streamed in sub-slices.
 LoraPlan lora_plan_nt(int64_t M, int64_t C, int rp) {
   LoraPlan p{};
   const int64_t tiles = cdiv(M > 0 ? M : 1, 128);
-  const int64_t want = std::min<int64_t>(32, cdiv(256, tiles));
+  const int64_t want = std::min<int64_t>(8, cdiv(256, tiles));
   int64_t per = 32 * cdiv(cdiv(C, want), 32);
   if (per < 32) per = 32;
   p.per = per;
