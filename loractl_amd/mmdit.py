@@ -81,20 +81,20 @@ def timestep_embedding(t: torch.Tensor, dim: int, max_period: float = 10000.0) -
     return torch.cat([torch.cos(args), torch.sin(args)], dim=-1)
 
 
-def rope_tables(L: int, dim: int, device, theta: float = 10000.0):
-    """cos/sin [L, dim] (pairs (2j, 2j+1) share a frequency), f32."""
+def rope_tables(L: int, dim: int, device, theta: float = 10000.0) -> torch.Tensor:
+    """cos + i sin [L, dim / 2] complex64: pair (2j, 2j+1) turns by
+    position * theta^(-2j / dim)."""
     inv = 1.0 / theta ** (torch.arange(0, dim, 2, dtype=torch.float32, device=device) / dim)
     ang = torch.arange(L, dtype=torch.float32, device=device)[:, None] * inv[None]
-    cos = torch.repeat_interleave(torch.cos(ang), 2, dim=-1)
-    sin = torch.repeat_interleave(torch.sin(ang), 2, dim=-1)
-    return cos, sin
+    return torch.polar(torch.ones_like(ang), ang)
 
 
-def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
-    """Rotate (x_2j, x_2j+1) pairs; x [H, L, D] bf16, tables [L, D] f32."""
-    xf = x.float()
-    x2 = torch.stack((-xf[..., 1::2], xf[..., 0::2]), dim=-1).flatten(-2)
-    return (xf * cos + x2 * sin).to(x.dtype)
+def apply_rope(x: torch.Tensor, freqs: torch.Tensor) -> torch.Tensor:
+    """Rotate (x_2j, x_2j+1) pairs as complex numbers x_2j + i x_2j+1 times
+    cos + i sin: (x_2j cos - x_2j+1 sin, x_2j sin + x_2j+1 cos), in f32;
+    x [H, L, D] bf16."""
+    xc = torch.view_as_complex(x.float().unflatten(-1, (-1, 2)))
+    return torch.view_as_real(xc * freqs).flatten(-2).to(x.dtype)
 
 
 @dataclass
@@ -104,7 +104,7 @@ class Capture:
 
     block_inputs: List[Tuple[torch.Tensor, torch.Tensor]] = field(default_factory=list)
     vec: Optional[torch.Tensor] = None
-    rope: Optional[Tuple[torch.Tensor, torch.Tensor]] = None
+    rope: Optional[torch.Tensor] = None
     x_img: Optional[torch.Tensor] = None
     x_txt: Optional[torch.Tensor] = None
 
@@ -164,34 +164,30 @@ class Mmdit:
         p = f"blocks.{i}"
         site = self.site_fn
         cvec = F.silu(vec)
-        mods, qs, ks, vs = {}, [], [], []
+        mods, qkvs = {}, []
         for s, x in (("txt", x_txt), ("img", x_img)):  # text tokens first in the joint sequence
             m = site(adapters, f"{p}.{s}.mod", self.bases[f"{p}.{s}.mod"], cvec)
             mods[s] = m.chunk(6, dim=-1)
             sh1, sc1 = mods[s][0], mods[s][1]
-            h = F.layer_norm(x, (H,), eps=1e-6) * (1 + sc1) + sh1
-            qkv = site(adapters, f"{p}.{s}.qkv", self.bases[f"{p}.{s}.qkv"], h)
-            q, k, v = qkv.view(-1, 3, nh, hd).permute(1, 2, 0, 3).unbind(0)  # [nh, L, hd] each
-            qs.append(F.rms_norm(q, (hd,), eps=1e-6))
-            ks.append(F.rms_norm(k, (hd,), eps=1e-6))
-            vs.append(v)
-        cos, sin = rope
-        q = apply_rope(torch.cat(qs, dim=1), cos, sin)
-        k = apply_rope(torch.cat(ks, dim=1), cos, sin)
-        v = torch.cat(vs, dim=1)
+            h = torch.addcmul(sh1, F.layer_norm(x, (H,), eps=1e-6), 1 + sc1)
+            qkvs.append(site(adapters, f"{p}.{s}.qkv", self.bases[f"{p}.{s}.qkv"], h))
+        # the joint sequence as one [L, 3H] tensor, split into [nh, L, hd]
+        # views; per-head RMSNorm and RoPE run once over both streams
+        q, k, v = torch.cat(qkvs, dim=0).view(-1, 3, nh, hd).permute(1, 2, 0, 3).unbind(0)
+        q = apply_rope(F.rms_norm(q, (hd,), eps=1e-6), rope)
+        k = apply_rope(F.rms_norm(k, (hd,), eps=1e-6), rope)
         with torch.nn.attention.sdpa_kernel([torch.nn.attention.SDPBackend.EFFICIENT_ATTENTION]):
-            o = F.scaled_dot_product_attention(q.unsqueeze(0).contiguous(), k.unsqueeze(0).contiguous(),
-                                               v.unsqueeze(0).contiguous())
+            o = F.scaled_dot_product_attention(q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0).contiguous())
         o = o[0].transpose(0, 1).reshape(-1, H)  # [L, H]
         lt = x_txt.shape[0]
         outs = {}
         for s, x, oo in (("txt", x_txt, o[:lt]), ("img", x_img, o[lt:])):
             _, _, g1, sh2, sc2, g2 = mods[s]
-            x = x + g1 * site(adapters, f"{p}.{s}.out", self.bases[f"{p}.{s}.out"], oo.contiguous())
-            h2 = F.layer_norm(x, (H,), eps=1e-6) * (1 + sc2) + sh2
+            x = torch.addcmul(x, g1, site(adapters, f"{p}.{s}.out", self.bases[f"{p}.{s}.out"], oo))
+            h2 = torch.addcmul(sh2, F.layer_norm(x, (H,), eps=1e-6), 1 + sc2)
             up = site(adapters, f"{p}.{s}.up", self.bases[f"{p}.{s}.up"], h2)
-            x = x + g2 * site(adapters, f"{p}.{s}.down", self.bases[f"{p}.{s}.down"],
-                              F.gelu(up, approximate="tanh"))
+            x = torch.addcmul(x, g2, site(adapters, f"{p}.{s}.down", self.bases[f"{p}.{s}.down"],
+                                          F.gelu(up, approximate="tanh")))
             outs[s] = x
         return outs["img"], outs["txt"]
 
