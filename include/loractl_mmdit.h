@@ -1,0 +1,58 @@
+/*
+ * loractl_mmdit.h — C ABI of libloractl_mmdit.so, the attention-input
+ * kernels of the double-stream MMDiT step driver on MI355X (gfx950).
+ *
+ * These sit beside the quantized LoRA linear (loractl_rocm.h), between a
+ * block's QKV linears and its attention. They replace, per block, the
+ * reference's head split, QK-norm and RoPE on q and k
+ * (crates/loractl-core/src/mmdit.rs:599-619: ZRmsNorm forward
+ * :307-330 with its frozen zero-initialised gain, so gain 1, and the
+ * consecutive-pair rotation apply_rope :385-399), done on the joint
+ * text-then-image token sequence, with the gradient of the same map.
+ *
+ * Conventions (as loractl_rocm.h): device pointers owned by the caller,
+ * 16-byte aligned, row-major; bf16 as uint16_t bits; stream-ordered and
+ * asynchronous on `stream` (a hipStream_t, NULL for the default stream);
+ * 0 on success or a negative LRQ-style code (-1 invalid argument, -3 HIP
+ * launch error), message in lmd_last_error(). Nothing is allocated.
+ *
+ * Shapes: h = heads * head_dim, head_dim 64 or 128, L = l_txt + l_img.
+ *   qkv_txt [l_txt, 3h], qkv_img [l_img, 3h]: the QKV linears' outputs,
+ *     each row [q | k | v], each part head-major [heads, head_dim].
+ *   cos, sin f32 [L, head_dim / 2]: pair j of a token's head turns by the
+ *     angle whose cosine and sine these hold.
+ *   q, k, v bf16 [L, heads, head_dim]: text tokens first.
+ *   rstd f32 [2, L, heads]: 1 / sqrt(mean(x^2) + eps) of each q and k head.
+ */
+#ifndef LORACTL_MMDIT_H
+#define LORACTL_MMDIT_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Message of the last failed call on this host thread ("" if none). */
+const char* lmd_last_error(void);
+
+/* q = rope(x_q * rstd_q), k = rope(x_k * rstd_k), v = x_v, per head, in f32,
+ * rounded once to bf16 (mmdit.rs:599-619 for one token sequence). */
+int lmd_attn_prep_fwd(const uint16_t* qkv_txt, int64_t l_txt, const uint16_t* qkv_img, int64_t l_img,
+                      int heads, int head_dim, const float* cos, const float* sin, float eps,
+                      uint16_t* q, uint16_t* k, uint16_t* v, float* rstd, void* stream);
+
+/* Gradient of lmd_attn_prep_fwd: from dq, dk, dv [L, heads, head_dim], the
+ * forward's inputs and its rstd, writes d qkv_txt [l_txt, 3h] and
+ * d qkv_img [l_img, 3h]. With g = rope^-1(dq) per head and n = rstd * x:
+ * dx = rstd * (g - n * sum(g * n) / head_dim). */
+int lmd_attn_prep_bwd(const uint16_t* dq, const uint16_t* dk, const uint16_t* dv, const uint16_t* qkv_txt,
+                      int64_t l_txt, const uint16_t* qkv_img, int64_t l_img, int heads, int head_dim,
+                      const float* cos, const float* sin, const float* rstd, uint16_t* dqkv_txt,
+                      uint16_t* dqkv_img, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LORACTL_MMDIT_H */

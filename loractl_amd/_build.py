@@ -1,4 +1,6 @@
-"""In-tree build of libloractl_rocm.so (hipcc, gfx950 only).
+"""In-tree build of libloractl_rocm.so (the quantized LoRA linear) and
+libloractl_mmdit.so (the MMDiT driver's attention-input kernels), hipcc,
+gfx950 only.
 
 The library is built next to this file so that it travels with the source
 tree; nothing is installed into site-packages.
@@ -16,6 +18,8 @@ INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libloractl_rocm.so")
 SOURCES = ["lrq_quant.hip", "lrq_gemm.hip", "lrq_skinny.hip", "lrq_lora.hip", "lrq_api.hip"]
+MMDIT_LIB = os.path.join(HERE, "libloractl_mmdit.so")
+MMDIT_SOURCES = ["mmdit_attn_prep.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 FLAGS = [
@@ -38,19 +42,25 @@ def _compile(src: str) -> str:
     return out
 
 
-def build(verbose: bool = False) -> str:
-    """Compile every HIP source for gfx950 and link libloractl_rocm.so."""
-    os.makedirs(OBJ, exist_ok=True)
-    with ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
-        objs = list(ex.map(_compile, SOURCES))
-    tmp = LIB + ".tmp"
+def _link(lib: str, objs) -> None:
+    tmp = lib + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
-        raise RuntimeError(f"link failed:\n{r.stderr}")
-    os.replace(tmp, LIB)
+        raise RuntimeError(f"link failed for {os.path.basename(lib)}:\n{r.stderr}")
+    os.replace(tmp, lib)
+
+
+def build(verbose: bool = False) -> str:
+    """Compile every HIP source for gfx950 and link both libraries."""
+    os.makedirs(OBJ, exist_ok=True)
+    srcs = SOURCES + MMDIT_SOURCES
+    with ThreadPoolExecutor(max_workers=len(srcs)) as ex:
+        objs = list(ex.map(_compile, srcs))
+    _link(LIB, objs[:len(SOURCES)])
+    _link(MMDIT_LIB, objs[len(SOURCES):])
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB} and {MMDIT_LIB}")
     return LIB
 
 

@@ -18,6 +18,7 @@
 
 from __future__ import annotations
 
+import contextlib
 import re
 from dataclasses import dataclass, field
 from typing import List, Optional, Sequence
@@ -69,6 +70,20 @@ class LoraAdapters(torch.nn.Module):
     def apply(self, path: str, x: torch.Tensor, base_out: torch.Tensor) -> torch.Tensor:
         delta = self.get(path)
         return base_out + delta(x) if delta is not None else base_out
+
+    @contextlib.contextmanager
+    def cached_factors(self):
+        """Inside the block each delta's bf16 factor copies (the fused op's
+        operands) are made on first use and reused, for passes whose factors
+        do not change between them (a step's capture and replay). Changing a
+        factor inside the block is not seen by the fused sites."""
+        for d in self.deltas:
+            d.bf16_cache = []
+        try:
+            yield self
+        finally:
+            for d in self.deltas:
+                d.bf16_cache = None
 
 
 def build_adapters(sites: Sequence[LoraSite], cfg: LoraConfig, device=None) -> LoraAdapters:

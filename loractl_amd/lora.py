@@ -37,6 +37,7 @@ class LoraDelta(torch.nn.Module):
         self.scaling = float(alpha) / rank
         self.dropout_prob = float(dropout_prob)
         self.rank = rank
+        self.bf16_cache = None  # a list while LoraAdapters.cached_factors() is open
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         """The plain (unfused) delta, for sites whose base is not quantized."""
@@ -47,10 +48,14 @@ class LoraDelta(torch.nn.Module):
 
 class _QuantLoraFn(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x2: torch.Tensor, a: torch.Tensor, b: torch.Tensor, wq: D.PackedWeight, scaling: float):
+    def forward(ctx, x2: torch.Tensor, a: torch.Tensor, b: torch.Tensor, wq: D.PackedWeight, scaling: float,
+                factors=None):
         xb = x2.to(torch.bfloat16).contiguous()
-        ab = a.detach().to(torch.bfloat16).contiguous()
-        bb = b.detach().to(torch.bfloat16).contiguous()
+        if factors is None:
+            ab = a.detach().to(torch.bfloat16).contiguous()
+            bb = b.detach().to(torch.bfloat16).contiguous()
+        else:
+            ab, bb = factors
         y, t = D.lora_fwd(xb, wq, ab, bb, scaling)
         ctx.save_for_backward(xb, ab, bb, t)
         ctx.wq = wq
@@ -66,7 +71,7 @@ class _QuantLoraFn(torch.autograd.Function):
         dx, da, db = D.lora_bwd(xb, dyb, ctx.wq, ab, bb, ctx.scaling, t, need_dx, need_da, need_db)
         xd, ad, bd = ctx.dtypes
         return (dx.to(xd) if dx is not None else None, da.to(ad) if da is not None else None,
-                db.to(bd) if db is not None else None, None, None)
+                db.to(bd) if db is not None else None, None, None, None)
 
 
 def quant_lora_linear(x: torch.Tensor, wq: D.PackedWeight, delta: LoraDelta,
@@ -79,5 +84,8 @@ def quant_lora_linear(x: torch.Tensor, wq: D.PackedWeight, delta: LoraDelta,
     lead = x.shape[:-1]
     x2 = x.reshape(-1, x.shape[-1])
     w = wq if bias is None else wq.with_bias(bias.float().contiguous())
-    y = _QuantLoraFn.apply(x2, delta.lora_a, delta.lora_b, w, delta.scaling)
+    cache = getattr(delta, "bf16_cache", None)
+    if cache is not None and not cache:
+        cache.extend(p.detach().to(torch.bfloat16).contiguous() for p in (delta.lora_a, delta.lora_b))
+    y = _QuantLoraFn.apply(x2, delta.lora_a, delta.lora_b, w, delta.scaling, tuple(cache) if cache else None)
     return y.reshape(*lead, wq.n)

@@ -22,10 +22,12 @@ sites and the step structure carry over:
 - the flow-matching target follows ``flow.rs``: ``x_t = (1 - t) x0 + t eps``,
   target ``v = eps - x0`` (t = 0 is data), loss ``mean((pred - v)^2)``.
 
-Around the fused sites everything is PyTorch-ROCm (LayerNorm, modulation,
-per-head RMSNorm of q and k, RoPE, SDPA attention on its memory-efficient
-backend, GELU, the frozen bf16 embedders and head): those are outside the
-quantized-linear path. The modulation (adaLN) linears take the conditioning
+Between the QKV linears and attention, one HIP kernel (``attn_prep``) splits
+heads, RMS-normalises q and k per head (the reference's ``ZRmsNorm`` with its
+frozen zero gain, eps 1e-5) and applies RoPE over the joint text-then-image
+sequence. The rest around the fused sites is PyTorch-ROCm (LayerNorm,
+modulation, SDPA attention on its memory-efficient backend, GELU, the frozen
+bf16 embedders and head): those are outside the quantized-linear path. The modulation (adaLN) linears take the conditioning
 vector, one row per batch element, as in FLUX.
 """
 
@@ -40,6 +42,7 @@ import torch.nn.functional as F
 
 from . import device as D
 from .adapters import LoraAdapters, QuantLinear, site
+from .attn_prep import attn_prep, rope_tables
 from .lora import LoraDelta
 
 STREAMS = ("img", "txt")
@@ -81,22 +84,6 @@ def timestep_embedding(t: torch.Tensor, dim: int, max_period: float = 10000.0) -
     return torch.cat([torch.cos(args), torch.sin(args)], dim=-1)
 
 
-def rope_tables(L: int, dim: int, device, theta: float = 10000.0) -> torch.Tensor:
-    """cos + i sin [L, dim / 2] complex64: pair (2j, 2j+1) turns by
-    position * theta^(-2j / dim)."""
-    inv = 1.0 / theta ** (torch.arange(0, dim, 2, dtype=torch.float32, device=device) / dim)
-    ang = torch.arange(L, dtype=torch.float32, device=device)[:, None] * inv[None]
-    return torch.polar(torch.ones_like(ang), ang)
-
-
-def apply_rope(x: torch.Tensor, freqs: torch.Tensor) -> torch.Tensor:
-    """Rotate (x_2j, x_2j+1) pairs as complex numbers x_2j + i x_2j+1 times
-    cos + i sin: (x_2j cos - x_2j+1 sin, x_2j sin + x_2j+1 cos), in f32;
-    x [H, L, D] bf16."""
-    xc = torch.view_as_complex(x.float().unflatten(-1, (-1, 2)))
-    return torch.view_as_real(xc * freqs).flatten(-2).to(x.dtype)
-
-
 @dataclass
 class Capture:
     """What the capture forward keeps (``mmdit.rs:1474-1507``): each block's
@@ -104,7 +91,7 @@ class Capture:
 
     block_inputs: List[Tuple[torch.Tensor, torch.Tensor]] = field(default_factory=list)
     vec: Optional[torch.Tensor] = None
-    rope: Optional[torch.Tensor] = None
+    rope: Optional[Tuple[torch.Tensor, torch.Tensor]] = None
     x_img: Optional[torch.Tensor] = None
     x_txt: Optional[torch.Tensor] = None
 
@@ -171,13 +158,11 @@ class Mmdit:
             sh1, sc1 = mods[s][0], mods[s][1]
             h = torch.addcmul(sh1, F.layer_norm(x, (H,), eps=1e-6), 1 + sc1)
             qkvs.append(site(adapters, f"{p}.{s}.qkv", self.bases[f"{p}.{s}.qkv"], h))
-        # the joint sequence as one [L, 3H] tensor, split into [nh, L, hd]
-        # views; per-head RMSNorm and RoPE run once over both streams
-        q, k, v = torch.cat(qkvs, dim=0).view(-1, 3, nh, hd).permute(1, 2, 0, 3).unbind(0)
-        q = apply_rope(F.rms_norm(q, (hd,), eps=1e-6), rope)
-        k = apply_rope(F.rms_norm(k, (hd,), eps=1e-6), rope)
+        # q, k, v [L, nh, hd] over the joint sequence, q and k RMS-normalised
+        # per head and rotated (one kernel over both streams' rows)
+        q, k, v = attn_prep(qkvs[0], qkvs[1], rope, nh)
         with torch.nn.attention.sdpa_kernel([torch.nn.attention.SDPBackend.EFFICIENT_ATTENTION]):
-            o = F.scaled_dot_product_attention(q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0).contiguous())
+            o = F.scaled_dot_product_attention(*(t.unsqueeze(0).transpose(1, 2) for t in (q, k, v)))
         o = o[0].transpose(0, 1).reshape(-1, H)  # [L, H]
         lt = x_txt.shape[0]
         outs = {}
@@ -269,6 +254,11 @@ def checkpointed_step(model: Mmdit, adapters: LoraAdapters, batch, loss_scale: f
     """One block-checkpointed step (``block_ckpt.rs:103-207``): capture, head
     graph, reverse per-block replay. Returns the unscaled loss; adapter
     gradients accumulate on the deltas' ``.grad`` (scaled by ``loss_scale``)."""
+    with adapters.cached_factors():  # the factors stay fixed through capture and replay
+        return _checkpointed_step(model, adapters, batch, loss_scale)
+
+
+def _checkpointed_step(model: Mmdit, adapters: LoraAdapters, batch, loss_scale: float) -> float:
     img, txt, t, target = batch
     cap = model.forward_capture(img, txt, t, adapters)
     # head graph: trunk output re-tracked, loss scale folded into the seed once

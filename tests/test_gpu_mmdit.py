@@ -11,6 +11,7 @@ import torch
 
 import oracle as O
 from loractl_amd import device as D
+from loractl_amd.attn_prep import attn_prep, rope_tables
 from loractl_amd.mmdit import (Mmdit, MmditConfig, build_mmdit_adapters, checkpointed_step, flow_batch,
                                monolithic_step)
 
@@ -103,3 +104,66 @@ def test_adamw_on_adapters_lowers_the_loss(cuda):
     # B starts at zero (lora.rs:123-137), so the first step only moves B
     assert losses[-1] < losses[0] * 0.97, losses
     assert all(b < a for a, b in zip(losses, losses[1:])), losses
+
+
+def _prep_reference(qkv_txt, qkv_img, cos, sin, heads, eps):
+    """The reference's head split, ZRmsNorm (gain 1) and consecutive-pair
+    RoPE (mmdit.rs:307-330, :385-399) in f64 on the joint sequence."""
+    x = torch.cat([qkv_txt, qkv_img]).double()
+    L, h = x.shape[0], x.shape[1] // 3
+    hd = h // heads
+    q, k, v = x.view(L, 3, heads, hd).unbind(1)
+    c, s = cos.double()[:, None, :], sin.double()[:, None, :]
+
+    def norm_rope(t):
+        t = t / torch.sqrt(t.pow(2).mean(-1, keepdim=True) + eps)
+        x0, x1 = t[..., 0::2], t[..., 1::2]
+        return torch.stack((c * x0 - s * x1, s * x0 + c * x1), dim=-1).reshape(L, heads, hd)
+
+    return norm_rope(q), norm_rope(k), v
+
+
+@pytest.mark.parametrize("lt,li,heads,hd", [(37, 91, 4, 128), (5, 128, 3, 64), (0, 64, 2, 128), (16, 0, 2, 64)])
+def test_attn_prep_matches_reference(cuda, lt, li, heads, hd):
+    """q, k, v and the gradient of the fused attention-input kernel against
+    the f64 reference and its autograd, on ragged streams (one may be
+    empty). Forward: within bf16 rounding of the reference; v bit-exact.
+    Backward: within bf16 rounding plus 1e-4 of the largest entry."""
+    g = torch.Generator(device=cuda).manual_seed(lt * 1000 + li + hd)
+    h = heads * hd
+    # per-head scales far from 1 so the normalisation matters
+    scale = torch.rand(1, 3 * h, device=cuda, generator=g) * 4 + 0.1
+    qt = (torch.randn(lt, 3 * h, device=cuda, generator=g) * scale).to(torch.bfloat16)
+    qi = (torch.randn(li, 3 * h, device=cuda, generator=g) * scale).to(torch.bfloat16)
+    cos, sin = rope_tables(lt + li, hd, cuda)
+    eps = 1e-5
+    qt.requires_grad_(True)
+    qi.requires_grad_(True)
+    q, k, v = attn_prep(qt, qi, (cos, sin), heads, eps)
+    ref = _prep_reference(qt.detach(), qi.detach(), cos, sin, heads, eps)
+    for got, want in zip((q, k), ref[:2]):
+        err = (got.double() - want).abs()
+        assert bool((err <= want.abs() * 2.0 ** -8 + 1e-6).all()), err.max().item()
+    assert torch.equal(v, ref[2].to(torch.bfloat16))
+    dq, dk, dv = (torch.randn(lt + li, heads, hd, device=cuda, generator=g).to(torch.bfloat16) for _ in range(3))
+    torch.autograd.backward([q, k, v], [dq, dk, dv])
+    xt = qt.detach().double().requires_grad_(True)
+    xi = qi.detach().double().requires_grad_(True)
+    rq, rk, rv = _prep_reference(xt, xi, cos, sin, heads, eps)
+    torch.autograd.backward([rq, rk, rv], [dq.double(), dk.double(), dv.double()])
+    for got, want in ((qt.grad, xt.grad), (qi.grad, xi.grad)):
+        if want.numel() == 0:
+            continue
+        err = (got.double() - want).abs()
+        tol = want.abs() * 2.0 ** -8 + 1e-4 * want.abs().max()
+        assert bool((err <= tol).all()), (err - tol).max().item()
+
+
+def test_rope_tables_closed_form(cuda):
+    """Position 0 turns nothing; pair 0 turns by the position in radians; the
+    last pair of head_dim 128 by p * 10000^(-126/128)."""
+    cos, sin = rope_tables(4096, 128, cuda)
+    assert torch.equal(cos[0], torch.ones(64, device=cuda)) and torch.equal(sin[0], torch.zeros(64, device=cuda))
+    p = torch.arange(4096, dtype=torch.float64)
+    assert torch.allclose(cos[:, 0].double().cpu(), torch.cos(p), atol=1e-7)
+    assert torch.allclose(sin[:, 63].double().cpu(), torch.sin(p * 10000.0 ** (-126 / 128)), atol=1e-7)

@@ -132,6 +132,25 @@ def test_c_abi_library_exports_every_declared_symbol():
     assert "fwd_main" in names and "bwd_dx" in names
 
 
+def test_mmdit_library_exports_what_its_header_declares():
+    """libloractl_mmdit.so (the MMDiT driver's attention-input kernels) loads
+    without a GPU and exports exactly include/loractl_mmdit.h's functions,
+    each bound in attn_prep.SIGNATURES; invalid shapes are refused before
+    any launch."""
+    from loractl_amd import attn_prep
+
+    txt = open(os.path.join(ROOT, "include", "loractl_mmdit.h")).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    declared = set(re.findall(r"\b(lmd_[a-z0-9_]+)\s*\(", txt))
+    assert declared == set(attn_prep.SIGNATURES)
+    lib = attn_prep.load()
+    for name in declared:
+        assert hasattr(lib, name), name
+    # head_dim 96 is not supported: refused with a message, no device work
+    rc = lib.lmd_attn_prep_fwd(None, 0, None, 4, 2, 96, None, None, 1e-5, None, None, None, None, None)
+    assert rc == -1 and b"head_dim" in lib.lmd_last_error()
+
+
 def test_c_abi_rejects_null_context():
     lib = _lib.load()
     assert lib.lrq_sync(None) == _lib.LRQ_EINVAL
