@@ -793,7 +793,7 @@ def mmdit_measure(args, dev, steps, warmup, with_cpu=True):
     batch = flow_batch(cfg, img_tokens, txt_tokens, dev, seed=2)
     params = [p for d in ad.deltas for p in (d.lora_a, d.lora_b)]
     # burn's AdamWConfig defaults (beta 0.9/0.999, eps 1e-5); the trainer's weight decay default 0
-    opt = torch.optim.AdamW(params, lr=1e-4, eps=1e-5, weight_decay=0.0)
+    opt = torch.optim.AdamW(params, lr=1e-4, eps=1e-5, weight_decay=0.0, fused=True)
     for (M, (K, N)) in [(m, kn) for m in MMDIT_TOKENS for kn in cfg.site_shapes().values()]:
         D.reserve(M, N, K, cfg.rank)
     losses = []

@@ -73,12 +73,16 @@ class LoraAdapters(torch.nn.Module):
 
     @contextlib.contextmanager
     def cached_factors(self):
-        """Inside the block each delta's bf16 factor copies (the fused op's
-        operands) are made on first use and reused, for passes whose factors
-        do not change between them (a step's capture and replay). Changing a
-        factor inside the block is not seen by the fused sites."""
-        for d in self.deltas:
-            d.bf16_cache = []
+        """Inside the block the fused sites use bf16 copies of every delta's
+        factors, made once on entry, for passes whose factors do not change
+        between them (a step's capture and replay). Changing a factor inside
+        the block is not seen by the fused sites."""
+        params = [p for d in self.deltas for p in (d.lora_a, d.lora_b)]
+        casts = [torch.empty(p.shape, dtype=torch.bfloat16, device=p.device) for p in params]
+        with torch.no_grad():
+            torch._foreach_copy_(casts, params)  # all factors in a few multi-tensor launches
+        for i, d in enumerate(self.deltas):
+            d.bf16_cache = casts[2 * i:2 * i + 2]
         try:
             yield self
         finally:

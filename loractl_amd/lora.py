@@ -37,7 +37,7 @@ class LoraDelta(torch.nn.Module):
         self.scaling = float(alpha) / rank
         self.dropout_prob = float(dropout_prob)
         self.rank = rank
-        self.bf16_cache = None  # a list while LoraAdapters.cached_factors() is open
+        self.bf16_cache = None  # [A, B] in bf16 while LoraAdapters.cached_factors() is open
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         """The plain (unfused) delta, for sites whose base is not quantized."""
@@ -84,8 +84,6 @@ def quant_lora_linear(x: torch.Tensor, wq: D.PackedWeight, delta: LoraDelta,
     lead = x.shape[:-1]
     x2 = x.reshape(-1, x.shape[-1])
     w = wq if bias is None else wq.with_bias(bias.float().contiguous())
-    cache = getattr(delta, "bf16_cache", None)
-    if cache is not None and not cache:
-        cache.extend(p.detach().to(torch.bfloat16).contiguous() for p in (delta.lora_a, delta.lora_b))
+    cache = getattr(delta, "bf16_cache", None)  # (A, B) in bf16 inside LoraAdapters.cached_factors()
     y = _QuantLoraFn.apply(x2, delta.lora_a, delta.lora_b, w, delta.scaling, tuple(cache) if cache else None)
     return y.reshape(*lead, wq.n)
