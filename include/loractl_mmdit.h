@@ -1,10 +1,11 @@
 /*
  * loractl_mmdit.h — C ABI of libloractl_mmdit.so, the attention-input
- * kernels of the double-stream MMDiT step driver on MI355X (gfx950).
+ * and modulation kernels of the double-stream MMDiT step driver on MI355X
+ * (gfx950).
  *
- * These sit beside the quantized LoRA linear (loractl_rocm.h), between a
- * block's QKV linears and its attention. They replace, per block, the
- * reference's head split, QK-norm and RoPE on q and k
+ * These sit beside the quantized LoRA linear (loractl_rocm.h). The first
+ * pair runs between a block's QKV linears and its attention and replaces,
+ * per block, the reference's head split, QK-norm and RoPE on q and k
  * (crates/loractl-core/src/mmdit.rs:599-619: ZRmsNorm forward
  * :307-330 with its frozen zero-initialised gain, so gain 1, and the
  * consecutive-pair rotation apply_rope :385-399), done on the joint
@@ -50,6 +51,33 @@ int lmd_attn_prep_bwd(const uint16_t* dq, const uint16_t* dk, const uint16_t* dv
                       int64_t l_txt, const uint16_t* qkv_img, int64_t l_img, int heads, int head_dim,
                       const float* cos, const float* sin, const float* rstd, uint16_t* dqkv_txt,
                       uint16_t* dqkv_img, void* stream);
+
+/* Modulated RMSNorm of a block's stream (mmdit.rs:857-870: the prenorm and
+ * postnorm ZRmsNorm, gain 1, then (scale + 1) * norm + shift), per row of
+ * x [rows, h] with scale, shift [h] bf16:
+ *   out = (scale + 1) * x / sqrt(mean(x^2) + eps) + shift, in f32, one rounding;
+ * rstd f32 [rows] = 1 / sqrt(mean(x^2) + eps) for the gradient. h <= 4096,
+ * h % 8 == 0. */
+int lmd_modnorm_fwd(const uint16_t* x, int64_t rows, int h, const uint16_t* scale, const uint16_t* shift,
+                    float eps, uint16_t* out, float* rstd, void* stream);
+
+/* Number of partial rows the column sums of the two gradients below use for
+ * `rows` rows: their `part` workspace is f32 [groups][2][h] (modnorm) or
+ * [groups][h] (gated residual). */
+int64_t lmd_colsum_groups(int64_t rows);
+
+/* Gradient of lmd_modnorm_fwd: dx [rows, h] and the vector gradients
+ * dscale = sum over rows of dh * n, dshift = sum of dh (bf16 [h]), each
+ * summed in a fixed order (bitwise reproducible). With n = rstd * x and
+ * g = dh * (scale + 1): dx = rstd * (g - n * mean(g * n)). */
+int lmd_modnorm_bwd(const uint16_t* dh, const uint16_t* x, int64_t rows, int h, const uint16_t* scale,
+                    const float* rstd, uint16_t* dx, uint16_t* dscale, uint16_t* dshift, float* part, void* stream);
+
+/* Gradient of the gated residual y = x + gate * o (mmdit.rs:860-869) in o and
+ * gate: d_o = dy * gate [rows, h], dgate = sum over rows of dy * o (bf16
+ * [h], fixed order). The gradient in x is dy itself. */
+int lmd_gated_residual_bwd(const uint16_t* dy, const uint16_t* o, int64_t rows, int h, const uint16_t* gate,
+                           uint16_t* d_o, uint16_t* dgate, float* part, void* stream);
 
 #ifdef __cplusplus
 }

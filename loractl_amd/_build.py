@@ -19,7 +19,7 @@ OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libloractl_rocm.so")
 SOURCES = ["lrq_quant.hip", "lrq_gemm.hip", "lrq_skinny.hip", "lrq_lora.hip", "lrq_api.hip"]
 MMDIT_LIB = os.path.join(HERE, "libloractl_mmdit.so")
-MMDIT_SOURCES = ["mmdit_attn_prep.hip"]
+MMDIT_SOURCES = ["mmdit_attn_prep.hip", "mmdit_modulate.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 FLAGS = [

@@ -17,6 +17,9 @@
 
 #include "loractl_mmdit.h"
 
+// the message of the last failed call on this thread, for every lmd_ entry point
+__attribute__((visibility("hidden"))) thread_local std::string lmd_err_msg;
+
 namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -146,10 +149,8 @@ __global__ __launch_bounds__(256) void k_attn_prep_bwd(PrepArgs a) {
   st16(drow + 2 * h + c * 8, gv);
 }
 
-thread_local std::string g_err;
-
 int fail(int code, const char* what) {
-  g_err = what;
+  lmd_err_msg = what;
   return code;
 }
 
@@ -188,7 +189,7 @@ int launch(K kern, const PrepArgs& a, void* stream) {
 
 }  // namespace
 
-extern "C" const char* lmd_last_error(void) { return g_err.c_str(); }
+extern "C" const char* lmd_last_error(void) { return lmd_err_msg.c_str(); }
 
 extern "C" int lmd_attn_prep_fwd(const uint16_t* qkv_txt, int64_t l_txt, const uint16_t* qkv_img, int64_t l_img,
                                  int heads, int head_dim, const float* cos, const float* sin, float eps,
@@ -203,7 +204,7 @@ extern "C" int lmd_attn_prep_fwd(const uint16_t* qkv_txt, int64_t l_txt, const u
   a.out[1] = k;
   a.out[2] = v;
   a.rstd = rstd;
-  g_err.clear();
+  lmd_err_msg.clear();
   return head_dim == 128 ? launch(k_attn_prep_fwd<16>, a, stream) : launch(k_attn_prep_fwd<8>, a, stream);
 }
 
@@ -223,6 +224,6 @@ extern "C" int lmd_attn_prep_bwd(const uint16_t* dq, const uint16_t* dk, const u
   a.rstd = const_cast<float*>(rstd);
   a.dqkv[0] = dqkv_txt;
   a.dqkv[1] = dqkv_img;
-  g_err.clear();
+  lmd_err_msg.clear();
   return head_dim == 128 ? launch(k_attn_prep_bwd<16>, a, stream) : launch(k_attn_prep_bwd<8>, a, stream);
 }

@@ -22,12 +22,15 @@ sites and the step structure carry over:
 - the flow-matching target follows ``flow.rs``: ``x_t = (1 - t) x0 + t eps``,
   target ``v = eps - x0`` (t = 0 is data), loss ``mean((pred - v)^2)``.
 
-Between the QKV linears and attention, one HIP kernel (``attn_prep``) splits
-heads, RMS-normalises q and k per head (the reference's ``ZRmsNorm`` with its
-frozen zero gain, eps 1e-5) and applies RoPE over the joint text-then-image
-sequence. The rest around the fused sites is PyTorch-ROCm (LayerNorm,
-modulation, SDPA attention on its memory-efficient backend, GELU, the frozen
-bf16 embedders and head): those are outside the quantized-linear path. The modulation (adaLN) linears take the conditioning
+Each stream's pre- and post-attention norms are the reference block's
+modulated norm, ``(scale + 1) * ZRmsNorm(x) + shift`` (``mmdit.rs:857-870``,
+the norm's gain its frozen zero parameter + 1), and its residuals are gated,
+``x + gate * branch``; both run as HIP kernels (``modnorm``,
+``gated_residual``), as does the attention input (``attn_prep``: head split,
+per-head RMSNorm of q and k, RoPE over the joint text-then-image sequence).
+The rest around the fused sites is PyTorch-ROCm (SDPA attention on its
+memory-efficient backend, GELU, the frozen bf16 embedders and head linears):
+outside the quantized-linear path. The modulation (adaLN) linears take the conditioning
 vector, one row per batch element, as in FLUX.
 """
 
@@ -42,7 +45,7 @@ import torch.nn.functional as F
 
 from . import device as D
 from .adapters import LoraAdapters, QuantLinear, site
-from .attn_prep import attn_prep, rope_tables
+from .mmdit_ops import attn_prep, modnorm, gated_residual, rope_tables
 from .lora import LoraDelta
 
 STREAMS = ("img", "txt")
@@ -139,9 +142,10 @@ class Mmdit:
         return self._linear(img, self.img_in), self._linear(txt, self.txt_in)
 
     def head(self, x_img: torch.Tensor, vec: torch.Tensor) -> torch.Tensor:
-        shift, scale = self._linear(F.silu(vec), self.final_mod).chunk(2, dim=-1)
-        h = F.layer_norm(x_img, (self.cfg.hidden,), eps=1e-6) * (1 + scale) + shift
-        return self._linear(h, self.final)
+        """The output head (``mmdit.rs:885-887``): modulated norm, then the
+        linear back to patches."""
+        scale, shift = self._linear(F.silu(vec), self.final_mod).chunk(2, dim=-1)
+        return self._linear(modnorm(x_img, scale.contiguous(), shift.contiguous()), self.final)
 
     def block(self, i: int, x_img: torch.Tensor, x_txt: torch.Tensor, vec: torch.Tensor, rope,
               adapters: Optional[LoraAdapters]):
@@ -156,7 +160,7 @@ class Mmdit:
             m = site(adapters, f"{p}.{s}.mod", self.bases[f"{p}.{s}.mod"], cvec)
             mods[s] = m.chunk(6, dim=-1)
             sh1, sc1 = mods[s][0], mods[s][1]
-            h = torch.addcmul(sh1, F.layer_norm(x, (H,), eps=1e-6), 1 + sc1)
+            h = modnorm(x, sc1, sh1)
             qkvs.append(site(adapters, f"{p}.{s}.qkv", self.bases[f"{p}.{s}.qkv"], h))
         # q, k, v [L, nh, hd] over the joint sequence, q and k RMS-normalised
         # per head and rotated (one kernel over both streams' rows)
@@ -168,11 +172,11 @@ class Mmdit:
         outs = {}
         for s, x, oo in (("txt", x_txt, o[:lt]), ("img", x_img, o[lt:])):
             _, _, g1, sh2, sc2, g2 = mods[s]
-            x = torch.addcmul(x, g1, site(adapters, f"{p}.{s}.out", self.bases[f"{p}.{s}.out"], oo))
-            h2 = torch.addcmul(sh2, F.layer_norm(x, (H,), eps=1e-6), 1 + sc2)
+            x = gated_residual(x, g1, site(adapters, f"{p}.{s}.out", self.bases[f"{p}.{s}.out"], oo))
+            h2 = modnorm(x, sc2, sh2)
             up = site(adapters, f"{p}.{s}.up", self.bases[f"{p}.{s}.up"], h2)
-            x = torch.addcmul(x, g2, site(adapters, f"{p}.{s}.down", self.bases[f"{p}.{s}.down"],
-                                          F.gelu(up, approximate="tanh")))
+            x = gated_residual(x, g2, site(adapters, f"{p}.{s}.down", self.bases[f"{p}.{s}.down"],
+                                           F.gelu(up, approximate="tanh")))
             outs[s] = x
         return outs["img"], outs["txt"]
 

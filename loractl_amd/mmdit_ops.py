@@ -1,4 +1,6 @@
-"""Attention inputs of a double-stream block, through libloractl_mmdit.so.
+"""The double-stream block's glue kernels, through libloractl_mmdit.so:
+attention inputs (``attn_prep``), the modulated RMSNorm (``modnorm``) and the
+gated residual's gradient (``gated_residual``).
 
 ``attn_prep(qkv_txt, qkv_img, rope, heads)`` takes the two streams' QKV
 linear outputs (``[l, 3h]`` rows ``[q | k | v]``) and returns q, k, v as
@@ -24,6 +26,10 @@ LIB_PATH = os.path.join(_HERE, "libloractl_mmdit.so")
 _vp, _i64, _i32, _f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
 SIGNATURES = {
     "lmd_last_error": ([], ctypes.c_char_p),
+    "lmd_colsum_groups": ([_i64], _i64),
+    "lmd_modnorm_fwd": ([_vp, _i64, _i32, _vp, _vp, _f32, _vp, _vp, _vp], _i32),
+    "lmd_modnorm_bwd": ([_vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp], _i32),
+    "lmd_gated_residual_bwd": ([_vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp], _i32),
     "lmd_attn_prep_fwd": ([_vp, _i64, _vp, _i64, _i32, _i32, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _vp], _i32),
     "lmd_attn_prep_bwd": ([_vp, _vp, _vp, _vp, _i64, _vp, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp], _i32),
 }
@@ -111,3 +117,79 @@ def attn_prep(qkv_txt: torch.Tensor, qkv_img: torch.Tensor, rope: Tuple[torch.Te
     streams' QKV rows, differentiable in both."""
     cos, sin = rope
     return _AttnPrep.apply(qkv_txt, qkv_img, cos, sin, heads, eps)
+
+
+def _rows(x: torch.Tensor, vec: torch.Tensor, what: str):
+    h = x.shape[-1]
+    if x.dtype != torch.bfloat16 or vec.dtype != torch.bfloat16 or not x.is_cuda:
+        raise ValueError(f"{what}: bf16 tensors on the GPU expected")
+    if vec.numel() != h or not vec.is_contiguous():
+        raise ValueError(f"{what}: the vector must be one contiguous row of {h}")
+    return x.reshape(-1, h).contiguous(), h
+
+
+class _ModNorm(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, scale, shift, eps: float):
+        x2, h = _rows(x, scale, "modnorm")
+        if shift.numel() != h or shift.dtype != torch.bfloat16 or not shift.is_contiguous():
+            raise ValueError("modnorm: shift must be one contiguous bf16 row")
+        rows = x2.shape[0]
+        out = torch.empty_like(x2)
+        rstd = torch.empty(rows, device=x2.device, dtype=torch.float32)
+        _check(load().lmd_modnorm_fwd(x2.data_ptr(), rows, h, scale.data_ptr(), shift.data_ptr(), eps,
+                                      out.data_ptr(), rstd.data_ptr(), _stream(x2.device)), "lmd_modnorm_fwd")
+        ctx.save_for_backward(x2, scale, rstd)
+        ctx.shapes = (x.shape, scale.shape, shift.shape)
+        return out.view(x.shape)
+
+    @staticmethod
+    def backward(ctx, dh):
+        x2, scale, rstd = ctx.saved_tensors
+        rows, h = x2.shape
+        dh2 = dh.to(torch.bfloat16).reshape(rows, h).contiguous()
+        dx = torch.empty_like(x2)
+        dscale = torch.empty(h, device=x2.device, dtype=torch.bfloat16)
+        dshift = torch.empty_like(dscale)
+        part = torch.empty(load().lmd_colsum_groups(rows) * 2 * h, device=x2.device, dtype=torch.float32)
+        _check(load().lmd_modnorm_bwd(dh2.data_ptr(), x2.data_ptr(), rows, h, scale.data_ptr(), rstd.data_ptr(),
+                                      dx.data_ptr(), dscale.data_ptr(), dshift.data_ptr(), part.data_ptr(),
+                                      _stream(x2.device)), "lmd_modnorm_bwd")
+        xs, ss, hs = ctx.shapes
+        return dx.view(xs), dscale.view(ss), dshift.view(hs), None
+
+
+class _GatedResidual(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, gate, o):
+        o2, h = _rows(o, gate, "gated_residual")
+        ctx.save_for_backward(o2, gate)
+        ctx.shapes = (o.shape, gate.shape)
+        return torch.addcmul(x, gate, o)
+
+    @staticmethod
+    def backward(ctx, dy):
+        o2, gate = ctx.saved_tensors
+        rows, h = o2.shape
+        dy2 = dy.to(torch.bfloat16).reshape(rows, h).contiguous()
+        do = torch.empty_like(o2)
+        dgate = torch.empty(h, device=o2.device, dtype=torch.bfloat16)
+        part = torch.empty(load().lmd_colsum_groups(rows) * h, device=o2.device, dtype=torch.float32)
+        _check(load().lmd_gated_residual_bwd(dy2.data_ptr(), o2.data_ptr(), rows, h, gate.data_ptr(), do.data_ptr(),
+                                             dgate.data_ptr(), part.data_ptr(), _stream(o2.device)),
+               "lmd_gated_residual_bwd")
+        os_, gs = ctx.shapes
+        return dy, dgate.view(gs), do.view(os_)
+
+
+def modnorm(x: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor, eps: float = 1e-5) -> torch.Tensor:
+    """``(scale + 1) * x / sqrt(mean(x^2) + eps) + shift`` per row of x
+    (``mmdit.rs:857-870``: ZRmsNorm with its frozen zero gain, then the
+    block's pre/post modulation), differentiable in x, scale and shift."""
+    return _ModNorm.apply(x, scale, shift, eps)
+
+
+def gated_residual(x: torch.Tensor, gate: torch.Tensor, o: torch.Tensor) -> torch.Tensor:
+    """``x + gate * o`` (``mmdit.rs:860-869``), gate one row broadcast over
+    the rows of o; the gradient in gate and o is one kernel."""
+    return _GatedResidual.apply(x, gate, o)

@@ -135,15 +135,15 @@ def test_c_abi_library_exports_every_declared_symbol():
 def test_mmdit_library_exports_what_its_header_declares():
     """libloractl_mmdit.so (the MMDiT driver's attention-input kernels) loads
     without a GPU and exports exactly include/loractl_mmdit.h's functions,
-    each bound in attn_prep.SIGNATURES; invalid shapes are refused before
+    each bound in mmdit_ops.SIGNATURES; invalid shapes are refused before
     any launch."""
-    from loractl_amd import attn_prep
+    from loractl_amd import mmdit_ops
 
     txt = open(os.path.join(ROOT, "include", "loractl_mmdit.h")).read()
     txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
     declared = set(re.findall(r"\b(lmd_[a-z0-9_]+)\s*\(", txt))
-    assert declared == set(attn_prep.SIGNATURES)
-    lib = attn_prep.load()
+    assert declared == set(mmdit_ops.SIGNATURES)
+    lib = mmdit_ops.load()
     for name in declared:
         assert hasattr(lib, name), name
     # head_dim 96 is not supported: refused with a message, no device work
