@@ -35,7 +35,7 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 #define LMD_DEV __device__ __forceinline__
 
 constexpr int MAX_CPL = 8;  // 16-byte chunks per lane: h <= 4096
-constexpr int GROUPS = 128; // partial rows of a column sum, at most
+constexpr int GROUPS = 256; // partial rows of a column sum, at most (one wavefront per SIMD)
 
 LMD_DEV uint32_t pack2(float lo, float hi) {
   const f32x2_t v = {lo, hi};
@@ -230,15 +230,46 @@ __global__ __launch_bounds__(256) void k_gated_res_bwd(ModArgs a) {
   group_partials<CPL, 1>(a, acc, red);
 }
 
-// out_k[c] = bf16(sum over groups, in order, of part[g][k][c])
+// out_k[c] = bf16(sum over groups of part[g][k][c]), in a fixed order: a
+// workgroup owns 64 four-column quads of the nsum * h sums; thread (quarter
+// u, quad q) sums groups u * gq .. in order, loads issued 16 at a time, and
+// the four quarters are added in order through LDS.
 __global__ __launch_bounds__(256) void k_colsum(ModArgs a, int groups, int nsum) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= nsum * a.h) return;
-  const int k = i / a.h, c = i - k * a.h;
-  float s = 0.0f;
-  for (int g = 0; g < groups; ++g) s += a.part[((int64_t)g * nsum + k) * a.h + c];
-  const uint16_t b = __builtin_bit_cast(uint16_t, (__bf16)s);
-  (k == 0 ? a.vout0 : a.vout1)[c] = b;
+  __shared__ float4 lds[4][64];
+  const int q = threadIdx.x & 63, u = threadIdx.x >> 6;
+  const int quad = blockIdx.x * 64 + q, nq = nsum * a.h / 4;
+  const int gq = (groups + 3) / 4, g0 = u * gq, g1 = g0 + gq < groups ? g0 + gq : groups;
+  const float4* part = reinterpret_cast<const float4*>(a.part);
+  float4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (quad < nq) {
+    for (int g = g0; g < g1; g += 16) {
+      float4 v[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) v[i] = g + i < g1 ? part[(int64_t)(g + i) * nq + quad] : (float4){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        s.x += v[i].x;
+        s.y += v[i].y;
+        s.z += v[i].z;
+        s.w += v[i].w;
+      }
+    }
+  }
+  lds[u][q] = s;
+  __syncthreads();
+  if (u != 0 || quad >= nq) return;
+  float t[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    t[0] += lds[w][q].x;
+    t[1] += lds[w][q].y;
+    t[2] += lds[w][q].z;
+    t[3] += lds[w][q].w;
+  }
+  const int i = quad * 4, k = i / a.h, c = i - k * a.h;  // h % 8 == 0: the quad stays in one sum
+  uint16_t* out = (k == 0 ? a.vout0 : a.vout1) + c;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) out[e] = __builtin_bit_cast(uint16_t, (__bf16)t[e]);
 }
 
 int fail(int code, const char* what) {
@@ -330,7 +361,7 @@ extern "C" int lmd_modnorm_bwd(const uint16_t* dh, const uint16_t* x, int64_t ro
   const int groups = (int)lmd_colsum_groups(rows);
   LMD_CPL_SWITCH(k_modnorm_bwd, dim3(groups), 2 * h * sizeof(float))
   if (int rc = launched()) return rc;
-  hipLaunchKernelGGL(k_colsum, dim3((2 * h + 255) / 256), dim3(256), 0, (hipStream_t)stream, a, groups, 2);
+  hipLaunchKernelGGL(k_colsum, dim3((2 * h / 4 + 63) / 64), dim3(256), 0, (hipStream_t)stream, a, groups, 2);
   return launched();
 }
 
@@ -353,6 +384,6 @@ extern "C" int lmd_gated_residual_bwd(const uint16_t* dy, const uint16_t* o, int
   const int groups = (int)lmd_colsum_groups(rows);
   LMD_CPL_SWITCH(k_gated_res_bwd, dim3(groups), h * sizeof(float))
   if (int rc = launched()) return rc;
-  hipLaunchKernelGGL(k_colsum, dim3((h + 255) / 256), dim3(256), 0, (hipStream_t)stream, a, groups, 1);
+  hipLaunchKernelGGL(k_colsum, dim3((h / 4 + 63) / 64), dim3(256), 0, (hipStream_t)stream, a, groups, 1);
   return launched();
 }
