@@ -101,6 +101,7 @@ struct LoraPlan {
   int64_t tiles;
   int64_t per;
   int splits;
+  int lw;  // nt: wavefronts (16 tokens each) per workgroup, 4 or 8
 };
 LoraPlan lora_plan_nt(int64_t M, int64_t C, int rp);
 LoraPlan lora_plan_tn(int64_t M, int64_t C, int rp, int64_t other_c = 0);

@@ -38,8 +38,7 @@
 
 namespace {
 
-constexpr int LW = 8;          // wavefronts per workgroup
-constexpr int LNT = 64 * LW;   // threads per workgroup
+constexpr int LW = 8;          // nt: wavefronts per workgroup, at most (LoraPlan.lw: 4 or 8)
 
 // Transpose-pack: the 16-bit element `e` (0..7) of eight 8-element rows into
 // one 8-element vector (rows in order).
@@ -181,11 +180,12 @@ LRQ_DEV void copy_factor_rows(const NtFinish& f, int64_t wg, int64_t nwg, int nt
 }
 
 // partial[split][m][j] = sum over the slice's columns of p[m, c] * q(j, c).
-// A workgroup owns 128 tokens (16 per wavefront) and one column slice; the
-// factor slice is staged once in LDS and shared by the 8 wavefronts, which
-// each stream their own 16 token rows through a ring of D loads.
-template <int NJT, bool QROW>
-__global__ void __launch_bounds__(LNT) k_lora_nt(NtArgs a) {
+// A workgroup owns 16 LWT tokens (16 per wavefront) and one column slice;
+// the factor slice is staged once in LDS and shared by the LWT wavefronts,
+// which each stream their own 16 token rows through a ring of D loads.
+template <int NJT, bool QROW, int LWT>
+__global__ void __launch_bounds__(64 * LWT) k_lora_nt(NtArgs a) {
+  constexpr int LNT = 64 * LWT;
   constexpr int RP = 16 * NJT;
   __shared__ __attribute__((aligned(16))) uint16_t sQ[NQ_BYTES / 2];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -199,7 +199,7 @@ __global__ void __launch_bounds__(LNT) k_lora_nt(NtArgs a) {
   const int sub = (int)min(a.c_per, (int64_t)nt_cap(RP));
   const int SQ = nt_stride(sub);
 
-  const int64_t m0 = (int64_t)blockIdx.x * 128 + wv * 16;  // this wavefront's tokens
+  const int64_t m0 = (int64_t)blockIdx.x * (16 * LWT) + wv * 16;  // this wavefront's tokens
   const int64_t rows = max((int64_t)0, min((int64_t)16, a.M - m0));
   const rsrc_t rpv = make_rsrc(a.p + min(m0, a.M) * C, clamp_bytes(rows * C * 2));
   const uint32_t roff = (uint32_t)(l16 * C * 2);
@@ -248,7 +248,7 @@ __global__ void __launch_bounds__(LNT) k_lora_nt(NtArgs a) {
   // 16jt + l16), one 16-byte store per tile, in slot (split, wavefront)
   const NtFinish& f = a.f;
   const int splits = (int)gridDim.y;
-  const int64_t nwv = (int64_t)gridDim.x * LW, slot = (int64_t)blockIdx.x * LW + wv;
+  const int64_t nwv = (int64_t)gridDim.x * LWT, slot = (int64_t)blockIdx.x * LWT + wv;
   const rsrc_t rpart = make_rsrc(a.partial, clamp_bytes((int64_t)splits * nwv * RP * 64));
   auto poff = [&](int64_t sp, int jt) { return (uint32_t)((((sp * nwv + slot) * NJT + jt) * 64 + lane) * 16); };
 #pragma unroll
@@ -514,7 +514,13 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // streamed in sub-slices.
 LoraPlan lora_plan_nt(int64_t M, int64_t C, int rp) {
   LoraPlan p{};
-  const int64_t tiles = cdiv(M > 0 ? M : 1, 128);
+  // 64-token workgroups when 128-token ones cannot give 256 workgroups with
+  // at most 8 slices (fewer than 4096 tokens): more CUs stream (3072 -> 3072
+  // at M = 1024: t 11.4 -> 10.5 us, u 11.1 -> 9.7 us); at 4096 tokens the
+  // 128-token workgroups share each staged factor slice among more
+  // wavefronts (u 24.8 -> 23.8 us)
+  p.lw = cdiv(M > 0 ? M : 1, 128) * 8 < 256 ? 4 : 8;
+  const int64_t tiles = cdiv(M > 0 ? M : 1, 16 * p.lw);
   const int64_t want = std::min<int64_t>(8, cdiv(256, tiles));
   int64_t per = 32 * cdiv(cdiv(C, want), 32);
   if (per < 32) per = 32;
@@ -547,20 +553,26 @@ hipError_t launch_lora_nt(hipStream_t st, const uint16_t* p, const uint16_t* q, 
                           int R, int64_t M, int64_t C, int rp, const LoraPlan& plan, float* partial,
                           const NtFinish& fin) {
   if (M == 0) return hipSuccess;
-  if (!fin.cnt || plan.tiles * LW > SK_MAX_NB) return hipErrorInvalidValue;
+  if (!fin.cnt || plan.tiles * plan.lw > SK_MAX_NB || (plan.lw != 4 && plan.lw != 8)) return hipErrorInvalidValue;
   NtArgs a{p, q, M, C, ldq, R, plan.per, partial, fin};
   const dim3 grid((unsigned)plan.tiles, (unsigned)plan.splits);
+#define LRQ_NT(NJT, QR)                                                                   \
+  if (plan.lw == 8)                                                                       \
+    hipLaunchKernelGGL((k_lora_nt<NJT, QR, 8>), grid, dim3(512), 0, st, a);               \
+  else                                                                                    \
+    hipLaunchKernelGGL((k_lora_nt<NJT, QR, 4>), grid, dim3(256), 0, st, a)
   switch ((qrow ? 4 : 0) + rp / 16 - 1) {
-    case 0: hipLaunchKernelGGL((k_lora_nt<1, false>), grid, dim3(LNT), 0, st, a); break;
-    case 1: hipLaunchKernelGGL((k_lora_nt<2, false>), grid, dim3(LNT), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((k_lora_nt<3, false>), grid, dim3(LNT), 0, st, a); break;
-    case 3: hipLaunchKernelGGL((k_lora_nt<4, false>), grid, dim3(LNT), 0, st, a); break;
-    case 4: hipLaunchKernelGGL((k_lora_nt<1, true>), grid, dim3(LNT), 0, st, a); break;
-    case 5: hipLaunchKernelGGL((k_lora_nt<2, true>), grid, dim3(LNT), 0, st, a); break;
-    case 6: hipLaunchKernelGGL((k_lora_nt<3, true>), grid, dim3(LNT), 0, st, a); break;
-    case 7: hipLaunchKernelGGL((k_lora_nt<4, true>), grid, dim3(LNT), 0, st, a); break;
+    case 0: LRQ_NT(1, false); break;
+    case 1: LRQ_NT(2, false); break;
+    case 2: LRQ_NT(3, false); break;
+    case 3: LRQ_NT(4, false); break;
+    case 4: LRQ_NT(1, true); break;
+    case 5: LRQ_NT(2, true); break;
+    case 6: LRQ_NT(3, true); break;
+    case 7: LRQ_NT(4, true); break;
     default: return hipErrorInvalidValue;
   }
+#undef LRQ_NT
   return hipGetLastError();
 }
 
