@@ -38,6 +38,7 @@ pub mod ffi {
 
     pub const LRQ_FMT_INT4: i32 = 1;
     pub const LRQ_FMT_FP8: i32 = 2;
+    pub const LRQ_FMT_INT8: i32 = 3;
     pub const LRQ_LAYOUT_ROWS: i32 = 0;
     pub const LRQ_LAYOUT_BLOCKED: i32 = 1;
 
@@ -79,6 +80,15 @@ pub mod ffi {
             k: i64,
             group: i64,
             packed: *mut u8,
+            scales: *mut f32,
+        ) -> c_int;
+        pub fn lrq_quantize_int8(
+            ctx: *mut lrq_ctx,
+            w: *const f32,
+            n: i64,
+            k: i64,
+            group: i64,
+            q: *mut i8,
             scales: *mut f32,
         ) -> c_int;
         pub fn lrq_quantize_fp8(
@@ -217,6 +227,8 @@ pub enum Format {
     Int4 { group: i32 },
     /// e4m3fn bytes with one f32 scale per output row, or one for the tensor.
     Fp8 { per_channel: bool },
+    /// int8 bytes `q` (two's complement) with one f32 scale per `group` inputs of a row.
+    Int8 { group: i32 },
 }
 
 /// A frozen weight in device memory, file layout `[d_out = n, d_in = k]`
@@ -238,6 +250,7 @@ impl Weight {
         let (format, group, per_channel) = match self.format {
             Format::Int4 { group } => (ffi::LRQ_FMT_INT4, group, 0),
             Format::Fp8 { per_channel } => (ffi::LRQ_FMT_FP8, 0, per_channel as i32),
+            Format::Int8 { group } => (ffi::LRQ_FMT_INT8, group, 0),
         };
         ffi::lrq_weight {
             format,
@@ -333,6 +346,21 @@ impl Context {
         self.check(rc, "lrq_quantize_int4")
     }
 
+    /// The same at Q8S (`quant.rs:156-162`): f32 `[n, k]` -> int8 `q [n, k]`
+    /// + scales `[n, k/group]`, row layout.
+    pub fn quantize_int8(
+        &mut self,
+        w: DevPtr,
+        n: i64,
+        k: i64,
+        group: i64,
+        q: DevPtr,
+        scales: DevPtr,
+    ) -> anyhow::Result<()> {
+        let rc = unsafe { ffi::lrq_quantize_int8(self.raw, w.c(), n, k, group, q.m() as *mut i8, scales.m()) };
+        self.check(rc, "lrq_quantize_int8")
+    }
+
     /// An fp8 checkpoint tensor (e4m3fn bytes and its scale) re-quantized
     /// to int4 on the device (the load pass of `diffusion_trainer.rs:1143-1169`
     /// without the f32 copy).
@@ -372,7 +400,7 @@ impl Context {
         let rc = unsafe { ffi::lrq_weight_block(self.raw, &d, data_out.m(), scales_out.m()) };
         self.check(rc, "lrq_weight_block")?;
         let scales = match rows.format {
-            Format::Int4 { .. } => scales_out,
+            Format::Int4 { .. } | Format::Int8 { .. } => scales_out,
             Format::Fp8 { .. } => rows.scales,
         };
         Ok(Weight { data: data_out, scales, blocked: true, ..*rows })

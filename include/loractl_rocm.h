@@ -9,7 +9,8 @@
  *   - site() = BaseLinear::forward + LoraAdapters::apply
  *     (src/mmdit.rs:483-536, src/adapters.rs:75-85, src/lora.rs:199-203)
  *       -> lrq_lora_fwd / lrq_lora_bwd (the fused drop-in: base + delta)
- *   - quantize_linear_weight (src/quant.rs:74-82) -> lrq_quantize_int4
+ *   - quantize_linear_weight (src/quant.rs:74-82) -> lrq_quantize_int4 (Q4S)
+ *     and lrq_quantize_int8 (Q8S, the Quant::Int8 knob, src/quant.rs:156-162)
  *   - dequantize to f32 (src/quant.rs:232, :250) -> lrq_dequant
  *   - e4m3fn LUT decode * scale (src/fp8.rs:39-56, :279-329) -> lrq_dequant
  *     on an LRQ_FMT_FP8 weight
@@ -44,16 +45,17 @@
  *   lrq_weight_block: 64 (n) x 64 (k) blocks contiguous in memory, block
  *   (nb, kb) at (nb * KB + kb) * block bytes with KB = ceil(k / 64); inside a
  *   block the rows keep the row-layout byte order (int4: 32 bytes per row,
- *   fp8: 64). int4 scales become [NB][Gp][64] (NB = ceil(n/64),
- *   Gp = 64*KB/group); fp8 scales are unchanged. Padding rows/columns hold
- *   q = 0 with scale 0 (int4) or byte 0 (fp8). A transposed section of the
- *   same byte size follows, read by the input-gradient kernel (its reduction
- *   runs along n): the same blocking applied to W^T [k, n] (block (kb, nb)
- *   at (kb * NB + nb) * block bytes, rows along k), int4 nibbles holding q
- *   in two's complement, and for int4 a second scale table ST [KGt][NB*64]
- *   (KGt = ceil(64*KB/group), ST[kg][n] = scale of row n, group kg) after
- *   the [NB][Gp][64] one. The blocked weight thus takes twice the packed
- *   bytes (38 MB for an int4 12288 x 3072 weight).
+ *   fp8 and int8: 64). int4 and int8 scales become [NB][Gp][64]
+ *   (NB = ceil(n/64), Gp = 64*KB/group); fp8 scales are unchanged. Padding
+ *   rows/columns hold q = 0 with scale 0 (int4, int8) or byte 0 (fp8). A
+ *   transposed section of the same byte size follows, read by the
+ *   input-gradient kernel (its reduction runs along n): the same blocking
+ *   applied to W^T [k, n] (block (kb, nb) at (kb * NB + nb) * block bytes,
+ *   rows along k), int4 nibbles holding q in two's complement (int8 bytes as
+ *   in the row layout), and for int4 and int8 a second scale table
+ *   ST [KGt][NB*64] (KGt = ceil(64*KB/group), ST[kg][n] = scale of row n,
+ *   group kg) after the [NB][Gp][64] one. The blocked weight thus takes
+ *   twice the packed bytes (38 MB for an int4 12288 x 3072 weight).
  *   LoRA factors in burn layout: A = [k, r] (d_in x rank), B = [r, n].
  */
 #ifndef LORACTL_ROCM_H
@@ -75,19 +77,19 @@ enum {
   LRQ_ENOMEM = -4        /* device allocation for the workspace failed */
 };
 
-enum { LRQ_FMT_INT4 = 1, LRQ_FMT_FP8 = 2 };
+enum { LRQ_FMT_INT4 = 1, LRQ_FMT_FP8 = 2, LRQ_FMT_INT8 = 3 };
 enum { LRQ_LAYOUT_ROWS = 0, LRQ_LAYOUT_BLOCKED = 1 };
 
 typedef struct lrq_ctx lrq_ctx;
 
 /* A frozen base weight: plain pointers and sizes, no ownership. */
 typedef struct lrq_weight {
-  int32_t format;       /* LRQ_FMT_INT4 or LRQ_FMT_FP8 */
-  int32_t group;        /* int4: block size along k, a power of two >= 32 dividing k */
+  int32_t format;       /* LRQ_FMT_INT4, LRQ_FMT_FP8 or LRQ_FMT_INT8 */
+  int32_t group;        /* int4, int8: block size along k, a power of two >= 32 dividing k */
   int64_t n;            /* d_out */
   int64_t k;            /* d_in (a multiple of 32) */
-  const void* data;     /* device: packed int4 [n, k/2] or fp8 bytes [n, k] */
-  const float* scales;  /* device: int4 [n, k/group]; fp8 [n] or [1] */
+  const void* data;     /* device: packed int4 [n, k/2], fp8 bytes [n, k] or int8 [n, k] */
+  const float* scales;  /* device: int4, int8 [n, k/group]; fp8 [n] or [1] */
   int32_t per_channel;  /* fp8: 1 when scales has n entries, 0 for one scalar */
   int32_t layout;       /* LRQ_LAYOUT_ROWS or LRQ_LAYOUT_BLOCKED */
   const float* bias;    /* device f32 [n] or NULL (src/mmdit.rs:426-427) */
@@ -115,6 +117,12 @@ int lrq_reserve(lrq_ctx* ctx, int64_t m, int64_t n, int64_t k, int64_t r);
  * closed form scale = absmax/7, q = clamp(round_half_away(w/scale), -7, 7). */
 int lrq_quantize_int4(lrq_ctx* ctx, const float* w, int64_t n, int64_t k, int64_t group,
                       uint8_t* packed, float* scales);
+
+/* The same at Q8S (src/quant.rs:156-162 maps Quant::Int8 to it): w f32 [n, k]
+ * -> int8 q [n, k] + scales [n, k/group], scale = absmax/127,
+ * q = clamp(round_half_away(w/scale), -127, 127). */
+int lrq_quantize_int8(lrq_ctx* ctx, const float* w, int64_t n, int64_t k, int64_t group,
+                      int8_t* q, float* scales);
 
 /* fp8 repack (reference/fp8_reference.py:83-91): scale = max(amax/448, 1e-12)
  * per tensor or per output row, byte = RNE e4m3fn of w/scale, saturating to
@@ -148,7 +156,8 @@ int lrq_weight_block(lrq_ctx* ctx, const lrq_weight* rows, uint8_t* data_out, fl
 int lrq_dequant(lrq_ctx* ctx, const lrq_weight* w, float* out);
 
 /* The bf16 GEMM operand the fused kernels feed to the matrix cores:
- * bf16_rne(dequant) for int4; the exact e4m3fn value (no scale) for fp8. */
+ * bf16_rne(dequant) for int4 and int8; the exact e4m3fn value (no scale)
+ * for fp8. */
 int lrq_dequant_bf16(lrq_ctx* ctx, const lrq_weight* w, uint16_t* out);
 
 /* QuantBackend::quant_matmul_t (src/quant.rs:172-178): y[m, n] = x[m, k] .

@@ -19,6 +19,7 @@ LRQ_EHIP = -3
 LRQ_ENOMEM = -4
 LRQ_FMT_INT4 = 1
 LRQ_FMT_FP8 = 2
+LRQ_FMT_INT8 = 3
 LRQ_LAYOUT_ROWS = 0
 LRQ_LAYOUT_BLOCKED = 1
 LRQ_NOALLOC_SCRATCH_BYTES = 32 << 20
@@ -69,6 +70,7 @@ SIGNATURES = {
     "lrq_last_error": (ctypes.c_char_p, [_vp]),
     "lrq_reserve": (_i32, [_vp, _i64, _i64, _i64, _i64]),
     "lrq_quantize_int4": (_i32, [_vp, _vp, _i64, _i64, _i64, _vp, _vp]),
+    "lrq_quantize_int8": (_i32, [_vp, _vp, _i64, _i64, _i64, _vp, _vp]),
     "lrq_quantize_fp8": (_i32, [_vp, _vp, _i64, _i64, _i32, _vp, _vp]),
     "lrq_requantize_fp8_int4": (_i32, [_vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp, _vp]),
     "lrq_weight_blocked_size": (_i32, [_i32, _i64, _i64, _i64, ctypes.POINTER(_i64), ctypes.POINTER(_i64)]),

@@ -59,7 +59,8 @@ static int init_scratch(int device) {
 namespace {
 
 const char* kNames[KID_COUNT] = {"quantize_int4", "quantize_fp8", "dequant", "fwd_main", "bwd_dx", "lora_t",
-                                 "lora_u",        "lora_da",      "lora_db", "block",    "lora_dadb"};
+                                 "lora_u",        "lora_da",      "lora_db", "block",    "lora_dadb",
+                                 "quantize_int8"};
 
 int fail(lrq_ctx* c, int code, const char* fmt, ...) {
   if (c) {
@@ -226,14 +227,14 @@ int check_lora_shapes(lrq_ctx* c, int64_t m, int64_t n, int64_t k, int rp) {
 
 int check_weight(lrq_ctx* c, const lrq_weight* w, bool gemm) {
   if (!w) return fail(c, LRQ_EINVAL, "weight descriptor is NULL");
-  if (w->format != LRQ_FMT_INT4 && w->format != LRQ_FMT_FP8)
-    return fail(c, LRQ_EINVAL, "weight format %d is neither LRQ_FMT_INT4 nor LRQ_FMT_FP8", w->format);
+  if (w->format != LRQ_FMT_INT4 && w->format != LRQ_FMT_FP8 && w->format != LRQ_FMT_INT8)
+    return fail(c, LRQ_EINVAL, "weight format %d is not LRQ_FMT_INT4, LRQ_FMT_FP8 or LRQ_FMT_INT8", w->format);
   if (w->n < 0 || w->k < 0) return fail(c, LRQ_EINVAL, "negative weight shape [%lld, %lld]",
                                         (long long)w->n, (long long)w->k);
   if (w->k % 32 != 0)
     return fail(c, LRQ_EINVAL, "linear weight [%lld, %lld]: the input dim must be a multiple of 32",
                 (long long)w->n, (long long)w->k);
-  if (w->format == LRQ_FMT_INT4) {
+  if (w->format != LRQ_FMT_FP8) {
     if (w->group < 32 || (w->group & (w->group - 1)) != 0 || w->k % w->group != 0)
       return fail(c, LRQ_EINVAL,
                   "linear weight [%lld, %lld]: the input dim must be a multiple of the quant block "
@@ -382,6 +383,22 @@ int lrq_quantize_int4(lrq_ctx* c, const float* w, int64_t n, int64_t k, int64_t 
              [&] { return launch_quantize_int4(c->stream, w, n, k, (int)group, packed, scales); });
 }
 
+int lrq_quantize_int8(lrq_ctx* c, const float* w, int64_t n, int64_t k, int64_t group, int8_t* q,
+                      float* scales) {
+  LRQ_TRY(begin(c));
+  if (n < 0 || k < 0) return fail(c, LRQ_EINVAL, "negative shape");
+  if (group < 32 || group > 2048 || (group & (group - 1)) != 0)
+    return fail(c, LRQ_EINVAL, "quant block %lld must be a power of two in [32, 2048]", (long long)group);
+  if (k % group != 0)
+    return fail(c, LRQ_EINVAL,
+                "linear weight [%lld, %lld]: the input dim must be a multiple of the quant block (%lld)",
+                (long long)n, (long long)k, (long long)group);
+  if (n * k > 0 && (!w || !q || !scales)) return fail(c, LRQ_EINVAL, "int8 quantize: NULL pointer");
+  if (!aligned16(w) || !aligned16(q)) return fail(c, LRQ_EINVAL, "w and q must be 16-byte aligned");
+  return run(c, KID_QUANT_INT8, "quantize_int8",
+             [&] { return launch_quantize_int8(c->stream, w, n, k, (int)group, q, scales); });
+}
+
 int lrq_requantize_fp8_int4(lrq_ctx* c, const uint8_t* bytes, const float* scale, int per_channel, int64_t n,
                             int64_t k, int64_t group, uint8_t* packed, float* scales) {
   LRQ_TRY(begin(c));
@@ -415,10 +432,12 @@ int lrq_quantize_fp8(lrq_ctx* c, const float* w, int64_t n, int64_t k, int per_c
 
 int lrq_weight_blocked_size(int format, int64_t n, int64_t k, int64_t group, int64_t* data_bytes,
                             int64_t* scale_count) {
-  if ((format != LRQ_FMT_INT4 && format != LRQ_FMT_FP8) || n < 0 || k < 0 || !data_bytes || !scale_count)
+  if ((format != LRQ_FMT_INT4 && format != LRQ_FMT_FP8 && format != LRQ_FMT_INT8) || n < 0 || k < 0 ||
+      !data_bytes || !scale_count)
     return LRQ_EINVAL;
-  if (format == LRQ_FMT_INT4 && (group < 32 || (group & (group - 1)) != 0 || k % group != 0)) return LRQ_EINVAL;
-  blocked_sizes(format, n, k, format == LRQ_FMT_INT4 ? group : 64, data_bytes, scale_count);
+  const bool gs = format != LRQ_FMT_FP8;  // group scales
+  if (gs && (group < 32 || (group & (group - 1)) != 0 || k % group != 0)) return LRQ_EINVAL;
+  blocked_sizes(format, n, k, gs ? group : 64, data_bytes, scale_count);
   return LRQ_OK;
 }
 
@@ -426,10 +445,10 @@ int lrq_weight_block(lrq_ctx* c, const lrq_weight* w, uint8_t* data_out, float* 
   LRQ_TRY(begin(c));
   LRQ_TRY(check_weight(c, w, false));
   if (w->layout != LRQ_LAYOUT_ROWS) return fail(c, LRQ_EINVAL, "lrq_weight_block takes a LRQ_LAYOUT_ROWS weight");
-  if (w->format == LRQ_FMT_INT4 && ((w->group & (w->group - 1)) != 0))
-    return fail(c, LRQ_EINVAL, "int4 block %d must be a power of two", w->group);
+  if (w->format != LRQ_FMT_FP8 && ((w->group & (w->group - 1)) != 0))
+    return fail(c, LRQ_EINVAL, "quant block %d must be a power of two", w->group);
   if (!aligned16(data_out)) return fail(c, LRQ_EINVAL, "data_out must be 16-byte aligned");
-  if (w->format == LRQ_FMT_INT4 && !scales_out) return fail(c, LRQ_EINVAL, "scales_out is NULL");
+  if (w->format != LRQ_FMT_FP8 && !scales_out) return fail(c, LRQ_EINVAL, "scales_out is NULL");
   return run(c, KID_BLOCK, "weight_block", [&] { return launch_block(c->stream, w, data_out, scales_out); });
 }
 
@@ -455,7 +474,7 @@ static GemmArgs gemm_args(const lrq_weight* w, bool bwd, const uint16_t* act, in
   g.e = bwd ? w->k : w->n;
   g.wk = w->k;
   // forward: the row section of the blocked layout; backward: the transposed
-  // section (and, int4, its scale table) that follows it
+  // section (and, int4 and int8, its scale table) that follows it
   int64_t db = 0, sc = 0;
   if (bwd) blocked_sections(w->format, w->n, w->k, w->group, &db, &sc);
   g.wdata = reinterpret_cast<const uint8_t*>(w->data) + db;

@@ -1,4 +1,4 @@
-// Shared device helpers for the gfx950 kernels: bf16 packing, int4/fp8
+// Shared device helpers for the gfx950 kernels: bf16 packing, int4/int8/fp8
 // decode, and the matrix-core (MFMA) fragment layouts used by every GEMM.
 #pragma once
 #include <hip/hip_runtime.h>
@@ -61,6 +61,38 @@ LRQ_DEV u32x4 dequant8_int4_bf16(uint32_t w, float s, uint32_t nib = 0x0f0f0f0fu
   o[2] = pack_bf16x2(f[4], f[5]);
   o[3] = pack_bf16x2(f[6], f[7]);
   return o;
+}
+
+// ---------------------------------------------------------------- int8
+// Two dwords hold 8 two's-complement bytes (k = 0..7 of a run, byte j of
+// dword d is k = 4d + j). Flipping the sign bits gives u = q + 128, and
+// fma(u, s, -128s) == RN((u - 128) * s) == RN(q * s) (-128s is exact): the
+// f32 product bit for bit, with one byte convert and one fma per value.
+LRQ_DEV void dequant8_int8_f32(u32x2 w, float s, float f[8]) {
+  const float nb = -128.0f * s;
+#pragma unroll
+  for (int d = 0; d < 2; ++d) {
+    const uint32_t u = w[d] ^ 0x80808080u;
+    f[4 * d] = __builtin_fmaf((float)(u & 0xffu), s, nb);
+    f[4 * d + 1] = __builtin_fmaf((float)((u >> 8) & 0xffu), s, nb);
+    f[4 * d + 2] = __builtin_fmaf((float)((u >> 16) & 0xffu), s, nb);
+    f[4 * d + 3] = __builtin_fmaf((float)(u >> 24), s, nb);
+  }
+}
+
+LRQ_DEV u32x4 dequant8_int8_bf16(u32x2 w, float s) {
+  float f[8];
+  dequant8_int8_f32(w, s, f);
+  u32x4 o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = pack_bf16x2(f[2 * i], f[2 * i + 1]);
+  return o;
+}
+
+// Four two's-complement bytes -> their integer values as f32 (exact).
+LRQ_DEV void int8x4_to_f32(uint32_t w, float f[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) f[j] = (float)((int)(w << (24 - 8 * j)) >> 24);
 }
 
 // ---------------------------------------------------------------- fp8 e4m3fn
@@ -215,12 +247,12 @@ LRQ_DEV u32x4 zero4() { return (u32x4){0u, 0u, 0u, 0u}; }
 typedef __attribute__((address_space(3))) void lds_void;
 
 // Blocked-layout sizes (lrq_quant.hip writes the layout): data bytes and
-// int4 scale count.
+// group-scale count (int4, int8; none for fp8).
 LRQ_DEV void blocked_sizes_dev(int fmt, int64_t n, int64_t k, int64_t* data_bytes, int64_t* nscales,
                                int gshift) {
   const int64_t NB = (n + 63) / 64, KB = (k + 63) / 64;
   *data_bytes = NB * KB * 64 * (fmt == LRQ_FMT_INT4 ? 32 : 64);
-  *nscales = (fmt == LRQ_FMT_INT4) ? NB * ((KB * 64) >> gshift) * 64 : 0;
+  *nscales = (fmt != LRQ_FMT_FP8) ? NB * ((KB * 64) >> gshift) * 64 : 0;
 }
 
 // 8 consecutive bf16 (16 bytes) from global with a validity predicate.

@@ -103,10 +103,12 @@ template <bool BWD, int FMT, bool R192, bool SPLIT>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 k_gemm(GemmArgs a, int tiles_m, int ntiles) {
   constexpr bool I4 = FMT == LRQ_FMT_INT4;
+  constexpr bool I8 = FMT == LRQ_FMT_INT8;
+  constexpr bool GS = I4 || I8;         // group scales (int4, int8) or channel scales (fp8)
   constexpr int WV = I4 ? 1 : 2;        // 16-byte packed loads per row tile per step
   constexpr int RA = R192 ? 192 : 256;  // rows per tile
   constexpr int MJ1 = R192 ? 4 : MJ;    // token tiles of row tile 1
-  constexpr int NSC = I4 ? 2 : 1;       // backward scale registers: per row tile (int4) or shared (fp8)
+  constexpr int NSC = GS ? 2 : 1;       // backward scale registers: per row tile (int4, int8) or shared (fp8)
   __shared__ __attribute__((aligned(16))) uint16_t sX0[XBUF];
   __shared__ __attribute__((aligned(16))) uint16_t sX1[XBUF];
   // epilogue region: the tile's LoRA operands (token rows, then weight-side
@@ -134,7 +136,7 @@ k_gemm(GemmArgs a, int tiles_m, int ntiles) {
   const int64_t KB = (K + 63) / 64;
   constexpr uint32_t blkb = I4 ? 2048u : 4096u;  // bytes per 64x64 block
   constexpr uint32_t rowb = I4 ? 32u : 64u;      // bytes per block row
-  const uint32_t Gp = (I4 && !BWD) ? (uint32_t)((KB * 64) >> a.gshift) : 0u;
+  const uint32_t Gp = (GS && !BWD) ? (uint32_t)((KB * 64) >> a.gshift) : 0u;
   int64_t wbytes, nsc;
   blocked_sizes_dev(FMT, E, K, &wbytes, &nsc, a.gshift);
   const int nk = (int)KB;
@@ -142,16 +144,16 @@ k_gemm(GemmArgs a, int tiles_m, int ntiles) {
   // one split range (a multiple of NBUF; the last range may run past nk)
   const int nkp = SPLIT ? a.spl : (nk + NBUF - 1) / NBUF * NBUF;
 
-  // backward scales: int4 ST [KGt][64*KB] (row n = depth, group kg of the
-  // output row k); fp8 the channel scales [n] or one scalar
+  // backward scales: int4 and int8 ST [KGt][64*KB] (row n = depth, group kg
+  // of the output row k); fp8 the channel scales [n] or one scalar
   const int64_t NP = KB * 64;
-  const int64_t KGt = (BWD && I4) ? (((E + 63) / 64 * 64 + (1 << a.gshift) - 1) >> a.gshift) : 0;
-  const bool pc = !I4 && a.per_channel;
-  const rsrc_t rbs = BWD ? (I4 ? make_rsrc(a.wscale, clamp_bytes(KGt * NP * 4))
+  const int64_t KGt = (BWD && GS) ? (((E + 63) / 64 * 64 + (1 << a.gshift) - 1) >> a.gshift) : 0;
+  const bool pc = !GS && a.per_channel;
+  const rsrc_t rbs = BWD ? (GS ? make_rsrc(a.wscale, clamp_bytes(KGt * NP * 4))
                                : make_rsrc(a.wscale, pc ? clamp_bytes(K * 4) : 0u))
                          : make_rsrc(a.wscale, 0u);
   // fp8 with one scalar scale: the per-channel loads read zeros, plus this
-  const float s0add = (BWD && !I4 && !pc) ? a.wscale[0] : 0.0f;
+  const float s0add = (BWD && !GS && !pc) ? a.wscale[0] : 0.0f;
 
   // sources of virtual unit v (zero-size resources when v is past the grid);
   // the S ranges of a tile are consecutive units
@@ -173,10 +175,10 @@ k_gemm(GemmArgs a, int tiles_m, int ntiles) {
     // block row of the resource base: the wavefront's own (RA = 256) or the tile's first
     const int64_t nb = t.e0 / 64 + (R192 ? 0 : w);
     t.wd = make_rsrc(a.wdata + nb * KB * blkb, ok ? clamp_bytes(wbytes - nb * KB * blkb) : 0u);
-    t.ws = make_rsrc(a.wscale + ((I4 && !BWD) ? nb * Gp * 64 : 0),
-                     (I4 && !BWD && ok) ? clamp_bytes((nsc - nb * Gp * 64) * 4) : 0u);
-    t.sk0 = (BWD && I4) ? (uint32_t)(((t.e0 + ro0) >> a.gshift) * NP * 4) : 0u;
-    t.sk1 = (BWD && I4) ? (uint32_t)(((t.e0 + ro1) >> a.gshift) * NP * 4) : 0u;
+    t.ws = make_rsrc(a.wscale + ((GS && !BWD) ? nb * Gp * 64 : 0),
+                     (GS && !BWD && ok) ? clamp_bytes((nsc - nb * Gp * 64) * 4) : 0u);
+    t.sk0 = (BWD && GS) ? (uint32_t)(((t.e0 + ro0) >> a.gshift) * NP * 4) : 0u;
+    t.sk1 = (BWD && GS) ? (uint32_t)(((t.e0 + ro1) >> a.gshift) * NP * 4) : 0u;
     return t;
   };
 
@@ -224,8 +226,8 @@ k_gemm(GemmArgs a, int tiles_m, int ntiles) {
   };
 
   // ---------------- weight: offsets from the resource's block row: the
-  // lane's part (row l32 of a row tile, lane group g's 16 (int4) or 32 (fp8)
-  // bytes; int4 scale of row l32) plus a wavefront-uniform part per row tile
+  // lane's part (row l32 of a row tile, lane group g's 16 (int4) or 32 (fp8,
+  // int8) bytes; group scale of row l32) plus a wavefront-uniform part per row tile
   // (a constant for RA = 256, so it folds into the loads' immediates)
   const uint32_t woff = (uint32_t)l32 * rowb + (uint32_t)g * (I4 ? 16u : 32u);
   const uint32_t soff = (uint32_t)l32 * 4u;
@@ -234,7 +236,7 @@ k_gemm(GemmArgs a, int tiles_m, int ntiles) {
     const int ro = i ? ro1 : ro0;
     return (uint32_t)(ro >> 6) * (uint32_t)KB * blkb + (uint32_t)(ro & 63) * rowb;
   };
-  auto srow = [&](int i) -> uint32_t {  // uniform int4 scale offset of row tile i
+  auto srow = [&](int i) -> uint32_t {  // uniform group-scale offset of row tile i
     if (!R192) return (uint32_t)i * 128u;
     const int ro = i ? ro1 : ro0;
     return ((uint32_t)(ro >> 6) * Gp * 64u + (uint32_t)(ro & 63)) * 4u;
@@ -242,7 +244,7 @@ k_gemm(GemmArgs a, int tiles_m, int ntiles) {
   // backward: lane l of a 16-lane row holds the scale of depth 32g + 16p + l%16
   const uint32_t bsoff = (uint32_t)(32 * g + (lane & 15)) * 4u;
   u32x4 wp[NBUF][2 * WV];   // packed weight bytes per register set
-  float wsc[NBUF][2];       // forward int4 group scales per register set
+  float wsc[NBUF][2];       // forward int4 / int8 group scales per register set
   float bsc[NBUF][NSC][2];  // backward per-depth scales, two halves of a step
   auto load_w = [&](int set, const TileSrc& t, int kt) {
     // steps past the tile's last one read zeros (bytes and scales)
@@ -251,7 +253,7 @@ k_gemm(GemmArgs a, int tiles_m, int ntiles) {
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int h = 0; h < WV; ++h) wp[set][i * WV + h] = bload16(t.wd, kb + woff + wrow(i) + 16u * h);
-    if (!BWD && I4) {
+    if (!BWD && GS) {
       const uint32_t j = ((uint32_t)kt * 64u + (uint32_t)g * 32u) >> a.gshift;
       const uint32_t so = opaque_u32(kt < nk ? (j * 64u) * 4u : LRQ_OOB);
 #pragma unroll
@@ -259,7 +261,7 @@ k_gemm(GemmArgs a, int tiles_m, int ntiles) {
     }
     if (BWD) {
       const uint32_t sb = opaque_u32(kt < nk ? (uint32_t)kt * 256u + bsoff : LRQ_OOB);
-      if (I4) {
+      if (GS) {
         bsc[set][0][0] = bloadf(rbs, sb + t.sk0);
         bsc[set][0][1] = bloadf(rbs, sb + t.sk0 + 64u);
         bsc[set][NSC - 1][0] = bloadf(rbs, sb + t.sk1);
@@ -275,15 +277,20 @@ k_gemm(GemmArgs a, int tiles_m, int ntiles) {
     if (!BWD) {
       if (I4) return as_bf16x8(dequant8_int4_bf16(wp[set][i][kk], wsc[set][i], a.nib));
       const u32x4 v = wp[set][i * WV + (kk >> 1)];
+      if (I8) return as_bf16x8(dequant8_int8_bf16((u32x2){v[2 * (kk & 1)], v[2 * (kk & 1) + 1]}, wsc[set][i]));
       const u32x2 lo = fp8x4_to_bf16(v[2 * (kk & 1)]), hi = fp8x4_to_bf16(v[2 * (kk & 1) + 1]);
       return as_bf16x8((u32x4){lo[0], lo[1], hi[0], hi[1]});
     }
     float f[8];
-    const float S = bsc[set][I4 ? i : 0][kk >> 1];
+    const float S = bsc[set][GS ? i : 0][kk >> 1];
     if (I4) {
       const uint32_t d = wp[set][i][kk];
 #pragma unroll
       for (int e = 0; e < 8; ++e) f[e] = (float)((int)(d << (28 - 4 * e)) >> 28);
+    } else if (I8) {
+      const u32x4 v = wp[set][i * WV + (kk >> 1)];
+      int8x4_to_f32(v[2 * (kk & 1)], f);
+      int8x4_to_f32(v[2 * (kk & 1) + 1], f + 4);
     } else {
       const u32x4 v = wp[set][i * WV + (kk >> 1)];
       fp8x4_to_f32(v[2 * (kk & 1)], f);
@@ -417,7 +424,7 @@ k_gemm(GemmArgs a, int tiles_m, int ntiles) {
     // its sE slice (16-byte chunk c of row r at c ^ swz(r)), then back out in
     // row segments, 8 rows per store
     uint16_t* sO = sE + w * 128 * 64;
-    const float s0 = (!BWD && !I4 && !pc) ? a.wscale[0] : 1.0f;
+    const float s0 = (!BWD && !GS && !pc) ? a.wscale[0] : 1.0f;
     // output rows of this tile: a resource from row m0, so rows past M fall
     // outside it
     const rsrc_t ry = make_rsrc(a.out + m0 * E, clamp_bytes((M - m0) * E * 2));
@@ -444,7 +451,7 @@ k_gemm(GemmArgs a, int tiles_m, int ntiles) {
             // forward fp8: the per-output-channel scale factors out of the
             // depth reduction (the LoRA operand bt arrives divided by it);
             // per-channel scales of columns past E are zero (not stored)
-            const f32x4 sv = (BWD || I4) ? (f32x4){1.f, 1.f, 1.f, 1.f}
+            const f32x4 sv = (BWD || GS) ? (f32x4){1.f, 1.f, 1.f, 1.f}
                                          : (pc ? *reinterpret_cast<const f32x4*>(sAux + 256 + ro + 8 * vg + 4 * g)
                                                : (f32x4){s0, s0, s0, s0});
             const f32x16& c = acc[i][4 * h + jj];
@@ -637,6 +644,8 @@ template <bool BWD, bool SPLIT>
 hipError_t run_fmt(hipStream_t st, int fmt, bool r192, const GemmArgs& a) {
   if (fmt == LRQ_FMT_INT4)
     return r192 ? run<BWD, LRQ_FMT_INT4, true, SPLIT>(st, a) : run<BWD, LRQ_FMT_INT4, false, SPLIT>(st, a);
+  if (fmt == LRQ_FMT_INT8)
+    return r192 ? run<BWD, LRQ_FMT_INT8, true, SPLIT>(st, a) : run<BWD, LRQ_FMT_INT8, false, SPLIT>(st, a);
   return r192 ? run<BWD, LRQ_FMT_FP8, true, SPLIT>(st, a) : run<BWD, LRQ_FMT_FP8, false, SPLIT>(st, a);
 }
 

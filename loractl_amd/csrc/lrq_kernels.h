@@ -8,6 +8,9 @@
 // lrq_quant.hip
 hipError_t launch_quantize_int4(hipStream_t st, const float* w, int64_t n, int64_t k, int g,
                                 uint8_t* packed, float* scales);
+// Q8S: int8 q [n, k] + scales [n, k/g]
+hipError_t launch_quantize_int8(hipStream_t st, const float* w, int64_t n, int64_t k, int g, int8_t* q,
+                                float* scales);
 // the same from e4m3fn bytes [n, k] and their scalar (per_channel 0) or
 // per-row f32 scale: int4 of the f32 values LUT[byte] * scale
 hipError_t launch_requantize_fp8_int4(hipStream_t st, const uint8_t* bytes, const float* scale, int per_channel,
@@ -164,5 +167,6 @@ enum {
   KID_LORA_DB,
   KID_BLOCK,
   KID_LORA_DADB,
+  KID_QUANT_INT8,
   KID_COUNT
 };

@@ -1,5 +1,5 @@
-// Weight-format kernels: int4 block quantization (src/quant.rs:74-82 closed
-// form), fp8 e4m3fn repack (reference/fp8_reference.py:83-91), and the
+// Weight-format kernels: int4 and int8 block quantization (src/quant.rs:74-82
+// closed form), fp8 e4m3fn repack (reference/fp8_reference.py:83-91), and the
 // dequantize kernels that expose the f32 values (src/quant.rs:232,
 // src/fp8.rs:306-318) and the bf16 matrix-core operands.
 //
@@ -8,7 +8,8 @@
 #include "lrq_common.h"
 #include "lrq_kernels.h"
 
-// ------------------------------------------------------------------ int4 quantize
+// ------------------------------------------------------------------ int4 / int8 quantize
+// QMAX 7: Q4S, packed nibbles q + 8; QMAX 127: Q8S, int8 bytes (src/quant.rs:156-162).
 // One thread per (row, 32-value half-block); a block of `group` values is
 // covered by group/32 consecutive threads that reduce absmax with lane
 // shuffles (group/32 <= 64 lanes, a power of two or not: a plain loop over
@@ -17,8 +18,8 @@
 // and each value is LUT[byte] * scale in f32 first (src/fp8.rs:306-318), the
 // reference's f32 snapshot of an fp8 checkpoint tensor, which its load pass
 // then quantizes (src/diffusion_trainer.rs:1143-1169); no f32 copy is kept.
-template <bool FP8>
-__global__ void __launch_bounds__(256) k_quantize_int4(const void* __restrict__ wv, const float* __restrict__ fsc,
+template <bool FP8, int QMAX>
+__global__ void __launch_bounds__(256) k_quantize(const void* __restrict__ wv, const float* __restrict__ fsc,
                                                        int per_channel, int64_t n, int64_t k, int g,
                                                        uint8_t* __restrict__ packed, float* __restrict__ scales) {
   const int64_t runs_per_row = k / 32;
@@ -64,26 +65,30 @@ __global__ void __launch_bounds__(256) k_quantize_int4(const void* __restrict__ 
     for (int j = 0; j < rpb; ++j) m = fmaxf(m, __shfl(amax, first + j, 64));
     amax = m;
   }
-  const float s = amax / 7.0f;  // correctly rounded f32 division
+  const float s = amax / (float)QMAX;  // correctly rounded f32 division
   if (run % rpb == 0) scales[row * (k / g) + run / rpb] = s;
-  uint32_t out[4];
+  int q[32];
 #pragma unroll
-  for (int d = 0; d < 4; ++d) {
-    uint32_t word = 0;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      int q = 0;
-      if (s != 0.0f) {
-        float r = roundf(v[d * 8 + j] / s);  // half away from zero
-        r = fminf(fmaxf(r, -7.0f), 7.0f);
-        q = (int)r;
-      }
-      word |= (uint32_t)(q + 8) << (4 * j);
+  for (int i = 0; i < 32; ++i) {
+    q[i] = 0;
+    if (s != 0.0f) {
+      float r = roundf(v[i] / s);  // half away from zero
+      r = fminf(fmaxf(r, -(float)QMAX), (float)QMAX);
+      q[i] = (int)r;
     }
-    out[d] = word;
   }
-  u32x4 o = {out[0], out[1], out[2], out[3]};
-  st16(packed + row * (k / 2) + run * 16, o);
+  if constexpr (QMAX == 7) {
+    u32x4 o = zero4();
+#pragma unroll
+    for (int i = 0; i < 32; ++i) o[i >> 3] |= (uint32_t)(q[i] + 8) << (4 * (i & 7));
+    st16(packed + row * (k / 2) + run * 16, o);
+  } else {
+    u32x4 o[2] = {zero4(), zero4()};
+#pragma unroll
+    for (int i = 0; i < 32; ++i) o[i >> 4][(i >> 2) & 3] |= ((uint32_t)q[i] & 0xffu) << (8 * (i & 3));
+    st16(packed + row * k + run * 32, o[0]);
+    st16(packed + row * k + run * 32 + 16, o[1]);
+  }
 }
 
 // ------------------------------------------------------------------ fp8 quantize
@@ -163,10 +168,11 @@ __global__ void __launch_bounds__(256) k_fp8_encode(const float* __restrict__ w,
 
 // ------------------------------------------------------------------ blocked layout
 // The fused GEMMs read the frozen weight in 64 (n) x 64 (k) blocks that are
-// contiguous in memory (int4: 64 rows x 32 bytes; fp8: 64 rows x 64 bytes),
-// block (nb, kb) at (nb * KB + kb) * block bytes, KB = ceil(k / 64); int4
-// scales as [NB][Gp][64] (Gp = 64*KB / group). Rows past n and columns past
-// k are padding: int4 nibbles 8 (q = 0) with scale 0, fp8 bytes 0. A second,
+// contiguous in memory (int4: 64 rows x 32 bytes; fp8, int8: 64 rows x 64
+// bytes), block (nb, kb) at (nb * KB + kb) * block bytes, KB = ceil(k / 64);
+// int4 and int8 scales as [NB][Gp][64] (Gp = 64*KB / group). Rows past n and
+// columns past k are padding: int4 nibbles 8 (q = 0) with scale 0, int8 and
+// fp8 bytes 0 (int8 with scale 0). A second,
 // transposed section of the same size follows (k_block_data_t).
 LRQ_DEV int64_t blk_data_off(int fmt, int64_t n, int64_t k, int64_t KB) {
   const int64_t rb = (fmt == LRQ_FMT_INT4) ? 32 : 64;  // bytes per block row
@@ -210,7 +216,8 @@ __global__ void __launch_bounds__(256) k_block_scales(const float* __restrict__ 
 // block (kb, nb) at (kb * NB + nb) * block bytes, block row r = k. int4: 32
 // bytes per row, byte c holding n = 2c in its low nibble and 2c+1 in its high
 // nibble, each nibble q in two's complement (the kernel sign-extends it);
-// fp8: 64 bytes per row. Padding is q = 0 (int4) or byte 0 (fp8). One thread
+// fp8 and int8: 64 bytes per row, bytes as in the row layout. Padding is
+// q = 0 (int4) or byte 0 (fp8, int8). One thread
 // per 16 output bytes (32 or 16 values of one k row, gathered from as many
 // rows of the row layout).
 __global__ void __launch_bounds__(256) k_block_data_t(const uint8_t* __restrict__ src, int64_t n, int64_t k,
@@ -244,7 +251,7 @@ __global__ void __launch_bounds__(256) k_block_data_t(const uint8_t* __restrict_
   st16(dst + tid * 16, v);
 }
 
-// int4 scales of the transposed section: ST [KGt][NB*64], ST[kg][n] = scale
+// int4 and int8 scales of the transposed section: ST [KGt][NB*64], ST[kg][n] = scale
 // of row n, group kg (zero for padding rows and groups).
 __global__ void __launch_bounds__(256) k_block_scales_t(const float* __restrict__ src, int64_t n, int64_t G,
                                                         int64_t KGt, int64_t NP, float* __restrict__ dst) {
@@ -284,6 +291,33 @@ __global__ void __launch_bounds__(256) k_dequant_int4(const uint8_t* __restrict_
   }
 }
 
+// int8 -> f32 (bit-exact q*s) or bf16 operand; one thread per 8-value run.
+template <bool BF16>
+__global__ void __launch_bounds__(256) k_dequant_int8(const uint8_t* __restrict__ data,
+                                                      const float* __restrict__ scales, int64_t n,
+                                                      int64_t k, int g, int blocked, void* __restrict__ out) {
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t runs = n * (k / 8);
+  if (tid >= runs) return;
+  const int64_t row = tid / (k / 8);
+  const int64_t kk = (tid % (k / 8)) * 8;
+  const int64_t KB = (k + 63) / 64;
+  const int64_t Gp = KB * 64 / g;
+  const int64_t doff = blocked ? blk_data_off(LRQ_FMT_INT8, row, kk, KB) : row * k + kk;
+  const int64_t soff = blocked ? (((row >> 6) * Gp + kk / g) * 64 + (row & 63)) : row * (k / g) + kk / g;
+  const u32x2 word = *reinterpret_cast<const u32x2*>(data + doff);
+  const float s = scales[soff];
+  if (BF16) {
+    st16(reinterpret_cast<uint16_t*>(out) + row * k + kk, dequant8_int8_bf16(word, s));
+  } else {
+    float f[8];
+    dequant8_int8_f32(word, s, f);
+    float* o = reinterpret_cast<float*>(out) + row * k + kk;
+    *reinterpret_cast<f32x4*>(o) = (f32x4){f[0], f[1], f[2], f[3]};
+    *reinterpret_cast<f32x4*>(o + 4) = (f32x4){f[4], f[5], f[6], f[7]};
+  }
+}
+
 // fp8 -> f32 (LUT value * scale, one f32 rounding) or the unscaled bf16 operand.
 template <bool BF16>
 __global__ void __launch_bounds__(256) k_dequant_fp8(const uint8_t* __restrict__ bytes,
@@ -316,8 +350,17 @@ hipError_t launch_quantize_int4(hipStream_t st, const float* w, int64_t n, int64
                                 uint8_t* packed, float* scales) {
   const int64_t items = n * (k / 32);
   if (items == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_quantize_int4<false>, dim3(blocks_for(items, 256)), dim3(256), 0, st, w, nullptr, 0, n, k,
+  hipLaunchKernelGGL((k_quantize<false, 7>), dim3(blocks_for(items, 256)), dim3(256), 0, st, w, nullptr, 0, n, k,
                      g, packed, scales);
+  return hipGetLastError();
+}
+
+hipError_t launch_quantize_int8(hipStream_t st, const float* w, int64_t n, int64_t k, int g, int8_t* q,
+                                float* scales) {
+  const int64_t items = n * (k / 32);
+  if (items == 0) return hipSuccess;
+  hipLaunchKernelGGL((k_quantize<false, 127>), dim3(blocks_for(items, 256)), dim3(256), 0, st, w, nullptr, 0, n, k,
+                     g, reinterpret_cast<uint8_t*>(q), scales);
   return hipGetLastError();
 }
 
@@ -325,7 +368,7 @@ hipError_t launch_requantize_fp8_int4(hipStream_t st, const uint8_t* bytes, cons
                                       int64_t n, int64_t k, int g, uint8_t* packed, float* scales) {
   const int64_t items = n * (k / 32);
   if (items == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_quantize_int4<true>, dim3(blocks_for(items, 256)), dim3(256), 0, st, bytes, scale,
+  hipLaunchKernelGGL((k_quantize<true, 7>), dim3(blocks_for(items, 256)), dim3(256), 0, st, bytes, scale,
                      per_channel, n, k, g, packed, scales);
   return hipGetLastError();
 }
@@ -354,6 +397,14 @@ hipError_t launch_dequant(hipStream_t st, const lrq_weight* w, void* out, bool b
     else
       hipLaunchKernelGGL(k_dequant_int4<false>, dim3(blocks_for(runs, 256)), dim3(256), 0, st, d,
                          w->scales, n, k, w->group, blocked, out);
+  } else if (w->format == LRQ_FMT_INT8) {
+    const int64_t runs = n * (k / 8);
+    if (bf16)
+      hipLaunchKernelGGL(k_dequant_int8<true>, dim3(blocks_for(runs, 256)), dim3(256), 0, st, d,
+                         w->scales, n, k, w->group, blocked, out);
+    else
+      hipLaunchKernelGGL(k_dequant_int8<false>, dim3(blocks_for(runs, 256)), dim3(256), 0, st, d,
+                         w->scales, n, k, w->group, blocked, out);
   } else {
     const int64_t quads = n * k / 4;
     if (bf16)
@@ -369,11 +420,11 @@ hipError_t launch_dequant(hipStream_t st, const lrq_weight* w, void* out, bool b
 void blocked_sections(int fmt, int64_t n, int64_t k, int64_t group, int64_t* data_bytes, int64_t* scale_count) {
   const int64_t NB = (n + 63) / 64, KB = (k + 63) / 64;
   *data_bytes = NB * KB * 64 * (fmt == LRQ_FMT_INT4 ? 32 : 64);
-  *scale_count = (fmt == LRQ_FMT_INT4) ? NB * (KB * 64 / group) * 64 : 0;
+  *scale_count = (fmt != LRQ_FMT_FP8) ? NB * (KB * 64 / group) * 64 : 0;
 }
 
 int64_t blocked_t_scale_count(int fmt, int64_t n, int64_t k, int64_t group) {
-  if (fmt != LRQ_FMT_INT4) return 0;
+  if (fmt == LRQ_FMT_FP8) return 0;
   const int64_t NB = (n + 63) / 64, KB = (k + 63) / 64;
   return (KB * 64 + group - 1) / group * NB * 64;
 }
@@ -396,7 +447,7 @@ hipError_t launch_block(hipStream_t st, const lrq_weight* w, uint8_t* data, floa
                      data);
   hipLaunchKernelGGL(k_block_data_t, dim3(blocks_for(db / 16, 256)), dim3(256), 0, st, src, n, k, w->format, NB,
                      KB, data + db);
-  if (w->format == LRQ_FMT_INT4 && sc > 0) {
+  if (w->format != LRQ_FMT_FP8 && sc > 0) {
     hipLaunchKernelGGL(k_block_scales, dim3(blocks_for(sc, 256)), dim3(256), 0, st, w->scales, n,
                        k / w->group, NB, KB * 64 / w->group, scales);
     const int64_t st_count = blocked_t_scale_count(w->format, n, k, w->group);

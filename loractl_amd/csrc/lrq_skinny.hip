@@ -47,8 +47,9 @@
 //
 // int4 with groups of 64 or more multiplies the integer q exactly and
 // applies the group scale in f32 per 64-wide block (see MQ below), which is
-// the oracle's f32 dequantization; groups of 32 and fp8 use the large-m
-// kernel's operand (bf16(q s), exact e4m3). No atomic touches a result and
+// the oracle's f32 dequantization; groups of 32, int8 and fp8 use the
+// large-m kernel's operand (bf16(q s), exact e4m3). int8 loads like fp8 (16
+// bytes of one row tile per lane) and scales like int4. No atomic touches a result and
 // every sum has a fixed order: results are bitwise reproducible.
 
 #include "lrq_common.h"
@@ -340,11 +341,13 @@ LRQ_DEV void sk_t_slices(const SkArgs& sa, float* xs, int& last) {
 template <int FMT, bool BWD, int WB, int RTN>
 struct SkRun {
   static constexpr bool I4 = FMT == LRQ_FMT_INT4;
+  static constexpr bool GS = FMT != LRQ_FMT_FP8;  // group scales
   static_assert(!I4 || RTN % 2 == 0, "int4 row tiles are loaded in pairs");
   u32x4 xf[WB][2];
   u32x4 w4[I4 ? WB : 1][I4 ? RTN / 2 : 1];  // tile pairs as loaded
   u32x2 w8[I4 ? 1 : WB][RTN][2];
-  float sc[(I4 || BWD) ? WB : 1][RTN];  // forward int4: per row tile; backward: lane c16's depth (fp8: [b][0])
+  // forward int4 / int8: per row tile; backward: lane c16's depth (fp8: [b][0])
+  float sc[(GS || BWD) ? WB : 1][RTN];
 };
 
 // first depth (within a 64-wide block) of lane group kq's 16 values
@@ -367,25 +370,26 @@ LRQ_DEV void sk_int4_pair(const u32x4& v, u32x2& t0, u32x2& t1) {
 template <int FMT, bool BWD, int WB, int RTN>
 LRQ_DEV void sk_load(const GemmArgs& a, SkRun<FMT, BWD, WB, RTN>& R, int64_t nb, int rt0, int kb0, int nkb) {
   constexpr bool I4 = FMT == LRQ_FMT_INT4;
+  constexpr bool GS = FMT != LRQ_FMT_FP8;
   const int lane = threadIdx.x & 63, c16 = lane & 15, kq = lane >> 4;
   const int64_t M = a.m, K = a.l, E = a.e;
   const int64_t KB = (K + 63) / 64;
   constexpr uint32_t blkb = I4 ? 2048u : 4096u;
   constexpr uint32_t rowb = I4 ? 32u : 64u;
   const rsrc_t rw = make_rsrc(a.wdata + nb * KB * blkb, clamp_bytes(KB * (int64_t)blkb));
-  const int64_t Gp = I4 ? ((KB * 64) >> a.gshift) : 0;
-  // forward: int4 group scales of the block row ([NB][Gp][64]); backward: the
-  // per-depth scales (int4 the transposed table ST [KGt][64 KB], fp8 the
-  // channel scales [depth] or one scalar)
+  const int64_t Gp = GS ? ((KB * 64) >> a.gshift) : 0;
+  // forward: int4 / int8 group scales of the block row ([NB][Gp][64]);
+  // backward: the per-depth scales (int4 / int8 the transposed table
+  // ST [KGt][64 KB], fp8 the channel scales [depth] or one scalar)
   const int64_t NP = KB * 64;
-  const int64_t KGt = (BWD && I4) ? (((E + 63) / 64 * 64 + (1 << a.gshift) - 1) >> a.gshift) : 0;
-  const rsrc_t rs = BWD ? (I4 ? make_rsrc(a.wscale, clamp_bytes(KGt * NP * 4))
+  const int64_t KGt = (BWD && GS) ? (((E + 63) / 64 * 64 + (1 << a.gshift) - 1) >> a.gshift) : 0;
+  const rsrc_t rs = BWD ? (GS ? make_rsrc(a.wscale, clamp_bytes(KGt * NP * 4))
                               : make_rsrc(a.wscale, a.per_channel ? clamp_bytes(K * 4) : 0u))
-                        : (I4 ? make_rsrc(a.wscale + nb * Gp * 64, clamp_bytes(Gp * 64 * 4)) : make_rsrc(a.wscale, 4u));
-  const float s0add = (BWD && !I4 && !a.per_channel) ? a.wscale[0] : 0.0f;
+                        : (GS ? make_rsrc(a.wscale + nb * Gp * 64, clamp_bytes(Gp * 64 * 4)) : make_rsrc(a.wscale, 4u));
+  const float s0add = (BWD && !GS && !a.per_channel) ? a.wscale[0] : 0.0f;
   const rsrc_t rx = make_rsrc(a.act, clamp_bytes(M * K * 2));
   const int kd = sk_depth<FMT>(kq);
-  // fp8: 16 bytes of row c16 per tile; int4: 16 bytes of row c16 of tile
+  // fp8, int8: 16 bytes of row c16 per tile; int4: 16 bytes of row c16 of tile
   // lane / 32 of the pair, depth half (lane / 16) % 2
   const uint32_t woff = I4 ? (uint32_t)((lane >> 5) * 16 + c16) * rowb + (uint32_t)((lane >> 4) & 1) * 16u
                            : (uint32_t)c16 * rowb + (uint32_t)kq * 16u;
@@ -403,13 +407,19 @@ LRQ_DEV void sk_load(const GemmArgs& a, SkRun<FMT, BWD, WB, RTN>& R, int64_t nb,
     // backward: lane (kq, c16) holds the scale of depth 64 kb + kd + c16,
     // which the 16 lanes of its DPP row (one kq) broadcast among themselves
     const uint32_t dpos = kb * 64u + (uint32_t)(kd + c16);
-    if (BWD && !I4) R.sc[b][0] = bloadf(rs, opaque_u32(ok ? dpos * 4u : LRQ_OOB)) + s0add;
+    if (BWD && !GS) R.sc[b][0] = bloadf(rs, opaque_u32(ok ? dpos * 4u : LRQ_OOB)) + s0add;
 #pragma unroll
     for (int rt = 0; rt < RTN; ++rt) {
       const int rg = rt0 + rt;  // row tile within the 64-row block row
       const uint32_t wo = kb * blkb + (uint32_t)(rg * 16) * rowb + woff;
       if constexpr (I4) {
         if (rt % 2 == 0) R.w4[b][rt / 2] = bload16(rw, opaque_u32(ok ? wo : LRQ_OOB));
+      } else {
+        const u32x4 v = bload16(rw, opaque_u32(ok ? wo : LRQ_OOB));
+        R.w8[b][rt][0] = (u32x2){v[0], v[1]};
+        R.w8[b][rt][1] = (u32x2){v[2], v[3]};
+      }
+      if constexpr (GS) {
         if (BWD) {
           // group of output rows 64 nb + 16 rg .. +16 (groups are >= 32 and aligned)
           const uint32_t kg = (uint32_t)((nb * 64 + rg * 16) >> a.gshift);
@@ -418,10 +428,6 @@ LRQ_DEV void sk_load(const GemmArgs& a, SkRun<FMT, BWD, WB, RTN>& R, int64_t nb,
           const uint32_t j = (kb * 64u + (uint32_t)kd) >> a.gshift;
           R.sc[b][rt] = bloadf(rs, opaque_u32(ok ? (j * 64u + (uint32_t)(rg * 16 + c16)) * 4u : LRQ_OOB));
         }
-      } else {
-        const u32x4 v = bload16(rw, opaque_u32(ok ? wo : LRQ_OOB));
-        R.w8[b][rt][0] = (u32x2){v[0], v[1]};
-        R.w8[b][rt][1] = (u32x2){v[2], v[3]};
       }
     }
   }
@@ -432,6 +438,7 @@ LRQ_DEV void sk_load(const GemmArgs& a, SkRun<FMT, BWD, WB, RTN>& R, int64_t nb,
 template <int FMT, bool BWD, bool MQ, int WB, int RTN>
 LRQ_DEV void sk_math(const GemmArgs& a, const SkRun<FMT, BWD, WB, RTN>& R, f32x4 (&acc)[RTN]) {
   constexpr bool I4 = FMT == LRQ_FMT_INT4;
+  constexpr bool I8 = FMT == LRQ_FMT_INT8;
 #pragma unroll
   for (int rt = 0; rt < RTN; ++rt) acc[rt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -485,24 +492,30 @@ LRQ_DEV void sk_math(const GemmArgs& a, const SkRun<FMT, BWD, WB, RTN>& R, f32x4
       for (int jj = 0; jj < 2; ++jj) {
         u32x4 wb;
         if constexpr (BWD) {
-          // transposed section: value e is q (a sign-extended nibble, or the
-          // e4m3 value) times the scale of its depth kd + 8 jj + e, then bf16
+          // transposed section: value e is q (a sign-extended nibble or
+          // byte, or the e4m3 value) times the scale of its depth
+          // kd + 8 jj + e, then bf16
           float f[8];
           if (I4) {
             const uint32_t d = w4[rt][jj];
 #pragma unroll
             for (int e = 0; e < 8; ++e) f[e] = (float)((int)(d << (28 - 4 * e)) >> 28);
+          } else if (I8) {
+            int8x4_to_f32(R.w8[b][rt][jj][0], f);
+            int8x4_to_f32(R.w8[b][rt][jj][1], f + 4);
           } else {
             fp8x4_to_f32(R.w8[b][rt][jj][0], f);
             fp8x4_to_f32(R.w8[b][rt][jj][1], f + 4);
           }
-          const float S = R.sc[b][I4 ? rt : 0];
+          const float S = R.sc[b][(I4 || I8) ? rt : 0];
 #pragma unroll
           for (int e = 0; e < 8; ++e) f[e] = row_bcast_n(S, 8 * jj + e) * f[e];
 #pragma unroll
           for (int q = 0; q < 4; ++q) wb[q] = pack_bf16x2(f[2 * q], f[2 * q + 1]);
         } else if constexpr (I4) {
           wb = dequant8_int4_bf16(w4[rt][jj], R.sc[b][rt], a.nib);
+        } else if constexpr (I8) {
+          wb = dequant8_int8_bf16(R.w8[b][rt][jj], R.sc[b][rt]);
         } else {
           const u32x2 p0 = fp8x4_to_bf16(R.w8[b][rt][jj][0]), p1 = fp8x4_to_bf16(R.w8[b][rt][jj][1]);
           wb = (u32x4){p0[0], p0[1], p1[0], p1[1]};
@@ -852,6 +865,8 @@ hipError_t launch_skinny(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, c
       } else {
         SKF_LAUNCH(LRQ_FMT_INT4, false)
       }
+    } else if (fmt == LRQ_FMT_INT8) {
+      SKF_LAUNCH(LRQ_FMT_INT8, false)
     } else {
       SKF_LAUNCH(LRQ_FMT_FP8, false)
     }
@@ -872,6 +887,12 @@ hipError_t launch_skinny(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, c
       SK_LAUNCH(LRQ_FMT_INT4, false, true)
     } else {
       SK_LAUNCH(LRQ_FMT_INT4, false, false)
+    }
+  } else if (fmt == LRQ_FMT_INT8) {
+    if (bwd) {
+      SK_LAUNCH(LRQ_FMT_INT8, true, false)
+    } else {
+      SK_LAUNCH(LRQ_FMT_INT8, false, false)
     }
   } else {
     if (bwd) {

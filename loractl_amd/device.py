@@ -98,8 +98,9 @@ class PackedWeight:
     """A frozen base weight in device memory, file layout [d_out, d_in].
 
     int4: ``data`` uint8 [n, k/2] (nibbles q+8, low nibble = even k) and
-    ``scales`` f32 [n, k/group]. fp8: ``data`` uint8 e4m3fn [n, k] and
-    ``scales`` f32 [n] (per_channel) or [1]. ``bias`` optional f32 [n].
+    ``scales`` f32 [n, k/group]. int8: ``data`` int8 [n, k] and ``scales``
+    f32 [n, k/group]. fp8: ``data`` uint8 e4m3fn [n, k] and ``scales`` f32
+    [n] (per_channel) or [1]. ``bias`` optional f32 [n].
     """
 
     fmt: int
@@ -158,11 +159,12 @@ def block(w: PackedWeight) -> PackedWeight:
     ctx = context(w.device.index)
     db = ctypes.c_int64()
     ns = ctypes.c_int64()
-    rc = ctx.lib.lrq_weight_blocked_size(w.fmt, w.n, w.k, w.group if w.fmt == L.LRQ_FMT_INT4 else 64,
+    grouped = w.fmt != L.LRQ_FMT_FP8
+    rc = ctx.lib.lrq_weight_blocked_size(w.fmt, w.n, w.k, w.group if grouped else 64,
                                          ctypes.byref(db), ctypes.byref(ns))
     ctx.check(rc, "lrq_weight_blocked_size")
     data = torch.empty((db.value,), dtype=torch.uint8, device=w.device)
-    if w.fmt == L.LRQ_FMT_INT4:
+    if grouped:
         scales = torch.empty((ns.value,), dtype=torch.float32, device=w.device)
     else:
         scales = w.scales
@@ -180,6 +182,18 @@ def quantize_int4(w: torch.Tensor, group: int) -> PackedWeight:
     scales = torch.empty((n, max(k // group, 0) if group > 0 else 0), dtype=torch.float32, device=w.device)
     ctx.call("lrq_quantize_int4", _ptr(w), n, k, group, _ptr(packed), _ptr(scales))
     return PackedWeight(L.LRQ_FMT_INT4, n, k, packed, scales, group=group)
+
+
+def quantize_int8(w: torch.Tensor, group: int) -> PackedWeight:
+    """quantize_linear_weight at Q8S (src/quant.rs:74-82 with the Int8 value of
+    src/quant.rs:156-162) on the GPU: int8 q [n, k] and f32 scales [n, k/group]."""
+    _need(w, torch.float32, "w")
+    n, k = w.shape
+    ctx = context(w.device.index)
+    q = torch.empty((n, k), dtype=torch.int8, device=w.device)
+    scales = torch.empty((n, max(k // group, 0) if group > 0 else 0), dtype=torch.float32, device=w.device)
+    ctx.call("lrq_quantize_int8", _ptr(w), n, k, group, _ptr(q), _ptr(scales))
+    return PackedWeight(L.LRQ_FMT_INT8, n, k, q, scales, group=group)
 
 
 def requantize_fp8_int4(w: PackedWeight, group: int) -> PackedWeight:

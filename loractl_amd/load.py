@@ -134,16 +134,18 @@ def load_fp8_checkpoint(path: str, device: Union[str, torch.device], quant: Opti
     """Load a scaled-fp8 checkpoint onto ``device``.
 
     Each 2-D fp8 weight becomes a ``PackedWeight``: e4m3fn as stored
-    (``quant=None``) or int4 at Q4S with ``group`` (``quant="int4"``; the
+    (``quant=None``), int4 at Q4S with ``group`` (``quant="int4"``; the
     reference's load pass always uses QUANT_BLOCK = 32), re-quantized on the
-    device from the bytes. A weight whose input dim is not a multiple of 32
+    device from the bytes, or int8 at Q8S (``quant="int8"``), quantized from
+    the weight's f32 values on the device (one f32 copy of one weight at a
+    time, as the reference's pass holds on the host). A weight whose input dim is not a multiple of 32
     stays plain, as the reference keeps such sites (src/mmdit.rs:1266-1280),
     and so does one whose output dim is not a multiple of 8, which the fused
     kernels cannot write: both come back as their f32 values. A caller-chosen
     group that does not divide an aligned weight's input dim raises.
     Pass-through tensors keep their dtype; dropped keys are absent."""
-    if quant not in (None, "int4"):
-        raise ValueError(f"quant must be None or 'int4', got {quant!r}")
+    if quant not in (None, "int4", "int8"):
+        raise ValueError(f"quant must be None, 'int4' or 'int8', got {quant!r}")
     ck = classify_fp8_checkpoint(path)
     from safetensors import safe_open
 
@@ -154,14 +156,18 @@ def load_fp8_checkpoint(path: str, device: Union[str, torch.device], quant: Opti
             data = f.get_tensor(name).view(torch.uint8).to(device)
             scale = f.get_tensor(f"{name}_scale").to(device)
             aligned = data.dim() == 2 and fused_aligned(data.shape[0], data.shape[1])
-            if aligned and quant == "int4":
+            if aligned and quant is not None:
                 _check_group(name, data.shape[1], group)
             if not aligned:
                 vals = data.view(torch.float8_e4m3fn).float()
                 out[name] = vals * (scale.reshape(-1, *([1] * (vals.dim() - 1))) if ck.fp8[name] else scale.reshape(()))
                 continue
             w = F.fp8_weight(name, data, scale)
-            out[name] = D.requantize_fp8_int4(w, group) if quant == "int4" else w
+            if quant == "int4":
+                w = D.requantize_fp8_int4(w, group)
+            elif quant == "int8":
+                w = D.quantize_int8(D.dequant(w), group)
+            out[name] = w
         for name in ck.plain:
             out[name] = f.get_tensor(name).to(device)
     return out
@@ -184,12 +190,14 @@ class QuantLoadReport:
 
 
 def load_quant_checkpoint(path: str, device: Union[str, torch.device], base_paths: List[str],
-                          group: int = QUANT_BLOCK, chunk_bytes: int = DEFAULT_DEQUANT_CHUNK_MIB << 20):
+                          group: int = QUANT_BLOCK, chunk_bytes: int = DEFAULT_DEQUANT_CHUNK_MIB << 20,
+                          value=None):
     """The quant pass of ``load_quant_module`` (src/diffusion_trainer.rs:1094-1267)
     for a plain (bf16/f32/f16) or scaled-fp8 safetensors checkpoint, on the
     device: for each frozen-base site in ``base_paths`` (in order), its
     ``<path>.weight`` (file layout ``[d_out, d_in]``) is read, moved to the
-    device, widened to f32 and quantized to int4 at Q4S as the row chunks
+    device, widened to f32 and quantized at ``value`` (a ``QuantValue``:
+    Q4S int4 by default, or Q8S int8) as the row chunks
     ``dequant_chunk_rows`` prescribes, one tensor at a time; the f32 copy is
     dropped before the next site. fp8 checkpoints (detected from the header)
     go through ``load_fp8_checkpoint``'s device requantization instead, with
@@ -206,11 +214,12 @@ def load_quant_checkpoint(path: str, device: Union[str, torch.device], base_path
     from .quant import QuantValue, quantize_linear_weight_chunked
 
     device = torch.device(device)
+    value = QuantValue.Q4S if value is None else value
     report = QuantLoadReport()
     quantized = {}
     fp8 = is_fp8_checkpoint(path)
     if fp8:
-        rest = load_fp8_checkpoint(path, device, quant="int4", group=group)
+        rest = load_fp8_checkpoint(path, device, quant="int8" if value is QuantValue.Q8S else "int4", group=group)
         keys = set(rest)
     else:
         keys = set(_header(path))
@@ -237,7 +246,7 @@ def load_quant_checkpoint(path: str, device: Union[str, torch.device], base_path
                 _check_group(wkey, t.shape[1], group)
                 w32 = t.to(device).float()
                 del t
-                chunks = quantize_linear_weight_chunked(w32, QuantValue.Q4S, chunk_bytes, group)
+                chunks = quantize_linear_weight_chunked(w32, value, chunk_bytes, group)
                 del w32
             if len(chunks) > 1:
                 report.chunked_sites += 1

@@ -18,8 +18,8 @@ Same names, argument meaning and error behaviour as the reference:
   ``grad_x = grad . dequant(wq)`` and no weight gradient.
 
 The compute runs in libloractl_rocm.so on the GPU; there is no CPU path.
-``Q8S`` (int8) is a known value that this backend does not implement: it
-raises at run time instead of falling back.
+Both values of the knob are built: ``Q4S`` (int4, packed nibbles) and
+``Q8S`` (int8 bytes), each with f32 block scales.
 """
 
 from __future__ import annotations
@@ -85,12 +85,17 @@ def quantize_linear_weight(weight: torch.Tensor, value: QuantValue = QuantValue.
     """Quantize one file-layout ``[d_out, d_in]`` f32 weight on the GPU."""
     d_out, d_in = weight.shape
     _check_block(d_out, d_in, group)
-    if value is QuantValue.Q8S:
-        raise NotImplementedError("compute.backend rocm implements Q4S (int4) and fp8 bases; Q8S is not built")
     if group & (group - 1):
         raise ValueError(f"compute.backend rocm needs a power-of-two quant block, got {group}")
     # quantize in the interchange row layout, keep the blocked layout the fused kernels read
-    return D.block(D.quantize_int4(weight.float().contiguous(), group))
+    return D.block(_quantize(weight.float().contiguous(), value, group))
+
+
+def _quantize(w32: torch.Tensor, value: QuantValue, group: int) -> D.PackedWeight:
+    """One f32 ``[d_out, d_in]`` weight at ``value`` in the row layout."""
+    if value is QuantValue.Q8S:
+        return D.quantize_int8(w32, group)
+    return D.quantize_int4(w32, group)
 
 
 def dequant_chunk_rows(d_out: int, d_in: int, chunk_bytes: int) -> List[int]:
@@ -109,12 +114,10 @@ def quantize_linear_weight_chunked(weight: torch.Tensor, value: QuantValue = Qua
     """Row chunks in the interchange row layout (QuantLinear joins and blocks them)."""
     d_out, d_in = weight.shape
     _check_block(d_out, d_in, group)
-    if value is QuantValue.Q8S:
-        raise NotImplementedError("compute.backend rocm implements Q4S (int4) and fp8 bases; Q8S is not built")
     rows = dequant_chunk_rows(d_out, d_in, chunk_bytes)
     out, start = [], 0
     for r in rows:
-        out.append(D.quantize_int4(weight[start:start + r].float().contiguous(), group))
+        out.append(_quantize(weight[start:start + r].float().contiguous(), value, group))
         start += r
     return out
 

@@ -45,6 +45,29 @@ def test_chunked_quant_linear_equals_whole(cuda):
     assert chunked.forward(x).shape == (2, 7, 96)
 
 
+def test_q8s_chunked_quant_linear_equals_whole(cuda):
+    """The Quant::Int8 knob (quant.rs:156-162) through QuantLinear: int8 row
+    chunks join to the whole weight bit for bit, and the forward and input
+    gradient equal the oracle's on the int8 dequantization."""
+    torch.manual_seed(2)
+    w = torch.randn(96, 128, device=cuda) * 0.1
+    whole = QuantLinear([quantize_linear_weight(w, QuantValue.Q8S, 32)])
+    chunked = QuantLinear(quantize_linear_weight_chunked(w, QuantValue.Q8S, 128 * 4 * 40, 32))
+    q, sc = O.quantize(w.cpu().numpy(), 32, 127)
+    wdq = O.dequant_q(q, sc, 32)
+    assert np.array_equal(whole.dequantized_weight().cpu().numpy(), wdq)
+    assert torch.equal(chunked.dequantized_weight(), whole.dequantized_weight())
+    x = (torch.randn(3, 5, 128, device=cuda) * 0.5).to(torch.bfloat16).requires_grad_(True)
+    y = chunked.forward(x)
+    assert torch.equal(y, whole.forward(x))
+    dy = torch.randn_like(y)
+    y.backward(dy)
+    xr = x.detach().float().reshape(-1, 128).cpu().numpy()
+    check("y", y.reshape(-1, 96), O.linear_fwd(xr, wdq)[0])
+    check("grad_x", x.grad.reshape(-1, 128), O.linear_bwd(xr, wdq, None, None, 1.0,
+                                                          dy.float().reshape(-1, 96).cpu().numpy())[0])
+
+
 def test_site_fused_matches_two_step_semantics(cuda):
     """site() with a quantized base and a delta (fused) equals base + delta
     computed from the oracle, and routes gradients to x, A and B only."""

@@ -1,5 +1,6 @@
 """Bit-exact parity of the GPU weight-format kernels with the CPU oracle:
-int4 quantize/pack/dequant and fp8 e4m3fn encode/decode."""
+int4 quantize/pack/dequant, int8 quantize/dequant and fp8 e4m3fn
+encode/decode."""
 
 import json
 import os
@@ -47,6 +48,39 @@ def test_int4_reference_golden_on_gpu(cuda):
     w = np.array(g["w"], np.float32)
     wq = D.quantize_int4(torch.from_numpy(w).to(cuda), 32)
     assert np.array_equal(D.dequant(wq).cpu().numpy(), np.array(g["dq"], np.float32))
+
+
+@pytest.mark.parametrize("N,K,g", [(8, 64, 32), (40, 96, 32), (128, 512, 64), (72, 1024, 128), (3, 2048, 2048)])
+def test_quantize_int8_bit_exact(cuda, N, K, g):
+    """Q8S (qmax 127): q and scales equal the oracle's quantizer byte for byte
+    (ties, all-zero blocks), and so do dequant and the bf16 operand."""
+    w = _int4_case(N, K, g, seed=3 * N + K)
+    if N > 2 and K >= 64:
+        w[2, 6:10] = [127.0, 1.5, -1.5, 63.5]  # exact .5 ties once the block's scale is 1
+    wq = D.quantize_int8(torch.from_numpy(w).to(cuda), g)
+    q_ref, s_ref = O.quantize(w, g, 127)
+    assert wq.data.dtype == torch.int8
+    assert np.array_equal(wq.data.cpu().numpy(), q_ref)
+    assert np.array_equal(wq.scales.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+    dq_ref = O.dequant_q(q_ref, s_ref, g)
+    assert np.array_equal(D.dequant(wq).cpu().numpy().view(np.uint32), dq_ref.view(np.uint32))
+    bf = D.dequant_bf16(wq).view(torch.int16).cpu().numpy().view(np.uint16)
+    assert np.array_equal(bf, O.bf16_bits(dq_ref))
+
+
+def test_int8_reference_golden_on_gpu(cuda):
+    """quant_int8_golden.json dequantized on the GPU equals the torch golden."""
+    g = json.load(open(os.path.join(GOLD, "quant_int8_golden.json")))
+    w = np.array(g["w"], np.float32)
+    wq = D.quantize_int8(torch.from_numpy(w).to(cuda), g["block"])
+    assert np.array_equal(D.dequant(wq).cpu().numpy(), np.array(g["dq"], np.float32))
+
+
+def test_quantize_int8_rejects_bad_blocks(cuda):
+    with pytest.raises(LrqError, match="LRQ_EINVAL"):
+        D.quantize_int8(torch.zeros(4, 96, device=cuda), 64)
+    with pytest.raises(LrqError, match="LRQ_EINVAL"):
+        D.quantize_int8(torch.zeros(4, 96, device=cuda), 48)
 
 
 def test_quantize_int4_rejects_bad_blocks(cuda):
@@ -110,14 +144,16 @@ def test_fp8_dequant_golden_on_gpu(cuda, case):
 
 
 @pytest.mark.parametrize("fmt,N,K,g", [("int4", 72, 96, 32), ("int4", 130, 256, 64), ("int4", 64, 512, 128),
-                                       ("fp8", 40, 96, 0), ("fp8", 200, 320, 0)])
+                                       ("fp8", 40, 96, 0), ("fp8", 200, 320, 0),
+                                       ("int8", 72, 96, 32), ("int8", 130, 256, 64)])
 def test_blocked_layout_roundtrip(cuda, fmt, N, K, g):
     """The blocked device layout dequantizes bit-identically to the row layout
     (padding rows and columns included), and places bytes where the layout
     definition says (spot-checked against the row layout)."""
     w = (rng(N * K).standard_normal((N, K)) * 0.3).astype(np.float32)
     t = torch.from_numpy(w).to(cuda)
-    rows = D.quantize_int4(t, g) if fmt == "int4" else D.quantize_fp8(t, True)
+    rows = {"int4": lambda: D.quantize_int4(t, g), "int8": lambda: D.quantize_int8(t, g),
+            "fp8": lambda: D.quantize_fp8(t, True)}[fmt]()
     blk = D.block(rows)
     assert blk.blocked and not rows.blocked
     a = D.dequant(rows).cpu().numpy()
@@ -127,7 +163,7 @@ def test_blocked_layout_roundtrip(cuda, fmt, N, K, g):
     # layout spot checks: row n, byte j of the row layout sits at block (n/64, k/64)
     KB = (K + 63) // 64
     rb = 32 if fmt == "int4" else 64
-    src = rows.data.cpu().numpy()
+    src = rows.data.view(torch.uint8).cpu().numpy()
     dst = blk.data.cpu().numpy()
     for n_, kk in [(0, 0), (N - 1, K - 8), (N // 2, K // 2)]:
         kk -= kk % (2 if fmt == "int4" else 1)
@@ -150,7 +186,7 @@ def test_blocked_layout_roundtrip(cuda, fmt, N, K, g):
     if N % 64:  # padding depth columns of the last block column are zero (N is even here)
         last = dst[t0 + (NB - 1) * 64 * rb:t0 + NB * 64 * rb].reshape(64, rb)
         assert not last[:, ((N % 64) // 2 if fmt == "int4" else N % 64):].any()
-    if fmt == "int4":
+    if fmt != "fp8":
         Gp = KB * 64 // g
         allsc = blk.scales.cpu().numpy()
         sc = allsc[:NB * Gp * 64].reshape(NB, Gp, 64)

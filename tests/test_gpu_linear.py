@@ -26,13 +26,26 @@ def _weight(w, fmt, g, dev, per_channel=True):
         wq = D.quantize_int4(t, g)
         p, s = O.quantize_int4_packed(w, g)
         return wq, O.dequant_int4(p, s, w.shape[1], g)
+    if fmt == "int8":
+        wq = D.quantize_int8(t, g)
+        q, s = O.quantize(w, g, 127)
+        return wq, O.dequant_q(q, s, g)
     wq = D.quantize_fp8(t, per_channel)
     b, s = O.fp8_quantize(w, per_channel)
     return wq, O.fp8_dequant(b, s)
 
 
+def _quantize(w, fmt, group, per_channel=True):
+    """A device weight of ``fmt`` from an f32 device tensor (int4 / int8 at ``group``)."""
+    if fmt == "int4":
+        return D.quantize_int4(w, group)
+    if fmt == "int8":
+        return D.quantize_int8(w, group)
+    return D.quantize_fp8(w, per_channel)
+
+
 @pytest.mark.parametrize("M,K,N,g", SHAPES)
-@pytest.mark.parametrize("fmt", ["int4", "fp8"])
+@pytest.mark.parametrize("fmt", ["int4", "fp8", "int8"])
 def test_quant_matmul_t_and_bwd(cuda, fmt, M, K, N, g):
     w, x, _, _, dy = case_inputs(M, K, N, 0, seed=M + N)
     wq, wdq = _weight(w, fmt, g, cuda)
@@ -44,13 +57,15 @@ def test_quant_matmul_t_and_bwd(cuda, fmt, M, K, N, g):
     check(f"{fmt} dx", dx, dx_ref)
 
 
-def test_quant_matmul_t_reference_golden(cuda):
-    """quant_int4_golden.json: y = x . dq^T on the GPU within bf16 rounding."""
+@pytest.mark.parametrize("fmt", ["int4", "int8"])
+def test_quant_matmul_t_reference_golden(cuda, fmt):
+    """quant_int4_golden.json / quant_int8_golden.json: y = x . dq^T on the GPU
+    within bf16 rounding."""
     import json, os
-    g = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "quant_int4_golden.json")))
+    g = json.load(open(os.path.join(os.path.dirname(__file__), "golden", f"quant_{fmt}_golden.json")))
     w = np.array(g["w"], np.float32)
     x = np.array(g["x"], np.float32)
-    wq = D.quantize_int4(torch.from_numpy(w).to(cuda), 32)
+    wq = _quantize(torch.from_numpy(w).to(cuda), fmt, 32)
     y = D.quant_matmul_t(to_dev(x, cuda), wq)
     check("golden y", y, np.array(g["y"], np.float32))
 
@@ -83,6 +98,57 @@ def test_lora_fwd_bwd_int4(cuda, M, K, N, g, r):
              + 1e-4 * np.abs(y_ref).max())
     assert (err <= bound).all(), f"y-base: worst excess {(err - bound).max():.3e}"
     assert np.abs(lora_ref).max() > 1e-2 * np.abs(y_ref).max()  # the case exercises a visible LoRA term
+
+
+def test_reduced_precision_accuracy_gates(cuda):
+    """tests/reduced_precision_accuracy.rs:44-62, :105-155 on the fused
+    forward: y = x . dq(w)^T against x . w^T with the unquantized f32 weight,
+    on the reference's golden w [8, 64] and x [4, 64] (block 32). int8 and
+    int4 each stay within the reference's calibrated band (d <= max(2 d_bar,
+    1e-3) and d <= ceil, d the peak-normalized deviation) and are not
+    no-ops, and on the same inputs int4 moves the output more than 4x as
+    much as int8. x enters as bf16 (the kernels' activation type) on both
+    sides; y leaves as bf16, whose rounding the bands absorb."""
+    import json, os
+    from loractl_amd.accuracy import RelGate, rel_deviation
+
+    gates = {"int8": RelGate(5.8e-3, 1e-3, 2.5e-2), "int4": RelGate(9.4e-2, 1e-3, 2.0e-1)}
+
+    def deviation(fmt, golden):
+        g = json.load(open(os.path.join(os.path.dirname(__file__), "golden", golden)))
+        w = np.array(g["w"], np.float32)
+        xb = to_dev(np.array(g["x"], np.float32), cuda)
+        ref = xb.float().cpu().numpy().astype(np.float64) @ w.astype(np.float64).T
+        y = D.quant_matmul_t(xb, _quantize(torch.from_numpy(w).to(cuda), fmt, 32))
+        return rel_deviation(y.float().cpu().numpy(), ref)
+
+    for fmt in ("int8", "int4"):
+        d = deviation(fmt, f"quant_{fmt}_golden.json")
+        assert d > 0.0, f"{fmt}: quantization was a no-op"
+        gates[fmt].apply(d).expect_pass(f"{fmt} forward")
+    d8 = deviation("int8", "quant_int8_golden.json")
+    d4 = deviation("int4", "quant_int8_golden.json")
+    assert d4 > 4.0 * d8, f"int4 must be markedly coarser than int8: int4 {d4:e} vs int8 {d8:e}"
+
+
+@pytest.mark.parametrize("M,K,N,g", [SHAPES[0], SHAPES[2], SHAPES[3], SHAPES[6]])
+def test_lora_fwd_bwd_int8(cuda, M, K, N, g):
+    """The int8 (Q8S) base through the fused forward and backward, few-token
+    and large-tile paths, against the oracle on its dequantized weight."""
+    r = 16
+    w, x, a, b, dy = case_inputs(M, K, N, r, seed=5 * M + N)
+    wq, wdq = _weight(w, "int8", g, cuda)
+    s = 16.0 / r
+    xd, ad, bd = to_dev(x, cuda), to_dev(a, cuda), to_dev(b, cuda)
+    y, t = D.lora_fwd(xd, wq, ad, bd, s)
+    dx, da, db = D.lora_bwd(xd, to_dev(dy, cuda), wq, ad, bd, s, t)
+    y_ref, t_ref = O.linear_fwd(x, wdq, a, b, s)
+    dx_ref, da_ref, db_ref = O.linear_bwd(x, wdq, a, b, s, dy)
+    check("t", t, t_ref)
+    check("y", y, y_ref)
+    check("dx", dx, dx_ref)
+    check("dA", da, da_ref)
+    check("dB", db, db_ref)
 
 
 @pytest.mark.parametrize("r", [1, 3, 8, 17, 64])
@@ -129,7 +195,7 @@ def test_bias_epilogue(cuda):
     check("y+bias", y, y_ref)
 
 
-@pytest.mark.parametrize("fmt,per_channel", [("int4", True), ("fp8", True), ("fp8", False)])
+@pytest.mark.parametrize("fmt,per_channel", [("int4", True), ("fp8", True), ("fp8", False), ("int8", True)])
 def test_split_depth_bias_and_scales(cuda, fmt, per_channel):
     """Few output tiles (M = 200, d_out = 3072): the depth is split into
     ranges whose f32 partials a reduction sums; the bias and the forward fp8
@@ -137,7 +203,7 @@ def test_split_depth_bias_and_scales(cuda, fmt, per_channel):
     M, K, N, r = 200, 3072, 3072, 16
     g = torch.Generator(device=cuda).manual_seed(7)
     w = torch.randn(N, K, device=cuda, generator=g) * 0.02
-    wq = D.quantize_int4(w, 64) if fmt == "int4" else D.quantize_fp8(w, per_channel)
+    wq = _quantize(w, fmt, 64, per_channel)
     bias = torch.randn(N, device=cuda, generator=g) * 0.1
     wq = wq.with_bias(bias)
     wdq = D.dequant(wq)
@@ -156,7 +222,7 @@ def test_split_depth_bias_and_scales(cuda, fmt, per_channel):
 
 @pytest.mark.parametrize("M,r", [(1, 17), (3, 32), (16, 17), (16, 64)])
 @pytest.mark.parametrize("fmt,per_channel,group", [("int4", True, 32), ("int4", True, 128), ("fp8", True, 0),
-                                                   ("fp8", False, 0)])
+                                                   ("fp8", False, 0), ("int8", True, 32), ("int8", True, 128)])
 def test_few_token_input_gradient(cuda, M, r, fmt, per_channel, group):
     """m <= 16: the input gradient streams the transposed section once in
     depth splits (d_out = 2056, ragged past 32 blocks of 64); the transposed
@@ -166,7 +232,7 @@ def test_few_token_input_gradient(cuda, M, r, fmt, per_channel, group):
     K, N = 1024, 2056
     g = torch.Generator(device=cuda).manual_seed(11 + M + r)
     w = torch.randn(N, K, device=cuda, generator=g) * 0.02
-    wq = D.quantize_int4(w, group) if fmt == "int4" else D.quantize_fp8(w, per_channel)
+    wq = _quantize(w, fmt, group, per_channel)
     wdq = D.dequant(wq)
     x = torch.randn(M, K, device=cuda, generator=g).to(torch.bfloat16)
     a = ((torch.rand(K, r, device=cuda, generator=g) * 2 - 1) / K ** 0.5).to(torch.bfloat16)
@@ -233,13 +299,18 @@ def test_shape_errors_are_loud(cuda):
                                          (256, 3072, 12288, 32, "fp8"), (300, 3008, 12280, 16, "int4"),
                                          # few tokens with a deep d_in (Qwen MLP down): more than 16 t
                                          # slices and 8 reduction splits in the few-token epilogue
-                                         (16, 9728, 2560, 16, "int4"), (5, 9728, 2560, 16, "fp8")])
+                                         (16, 9728, 2560, 16, "int4"), (5, 9728, 2560, 16, "fp8"),
+                                         # the int8 base on the same paths: large tiles, ragged edges,
+                                         # 192-row tiles, split depth, few tokens
+                                         (4096, 3072, 12288, 32, "int8"), (4000, 12224, 3064, 16, "int8"),
+                                         (300, 3008, 12280, 16, "int8"), (16, 3072, 12288, 32, "int8"),
+                                         (5, 9728, 2560, 16, "int8")])
 def test_baseline_shapes_against_torch_fp32(cuda, M, K, N, r, fmt):
     """The benchmark configurations at full size: the fused kernels vs torch fp32 GEMMs over the
     same bf16 inputs and the (bit-exact) dequantized weight."""
     g = torch.Generator(device=cuda).manual_seed(M + N)
     w = torch.randn(N, K, device=cuda, generator=g) * 0.02
-    wq = D.quantize_int4(w, 64) if fmt == "int4" else D.quantize_fp8(w, True)
+    wq = _quantize(w, fmt, 64)
     wdq = D.dequant(wq)
     x = torch.randn(M, K, device=cuda, generator=g).to(torch.bfloat16)
     a = ((torch.rand(K, r, device=cuda, generator=g) * 2 - 1) / K ** 0.5).to(torch.bfloat16)

@@ -98,6 +98,13 @@ def test_load_fp8_checkpoint_end_to_end(cuda, tmp_path):
     y4 = D.quant_matmul_t(xb, q4["blk.w.weight"])
     check("y fp8", y8, O.linear_fwd(xr, wd)[0])
     check("y int4", y4, O.linear_fwd(xr, O.dequant_int4(p_ref, s_ref, k, 64))[0])
+    # int8 (Q8S) from the same snapshot: bit-exact q and scales, and the fused forward
+    q8 = load_fp8_checkpoint(path, cuda, quant="int8", group=64)
+    q_ref, s8_ref = O.quantize(wd, 64, 127)
+    assert np.array_equal(q8["blk.w.weight"].data.cpu().numpy(), q_ref)
+    assert np.array_equal(q8["blk.w.weight"].scales.cpu().numpy(), s8_ref)
+    assert torch.equal(q8["blk.odd.weight"].cpu(), torch.tensor(WEIGHT_5X3).reshape(5, 3) * 2.0)
+    check("y int8", D.quant_matmul_t(xb, q8["blk.w.weight"]), O.linear_fwd(xr, O.dequant_q(q_ref, s8_ref, 64))[0])
 
 
 def test_fp8_load_default_block_and_alignment(cuda, tmp_path):
@@ -151,6 +158,14 @@ def test_load_quant_checkpoint_plain(cuda, tmp_path):
     assert torch.equal(rest["s.c.weight"].cpu(), torch.from_numpy(w_c))
     with pytest.raises(ValueError, match="quantized base site s.d has no s.d.weight"):
         load_quant_checkpoint(path, cuda, ["s.a", "s.d"])
+    # the same pass at Q8S (the Quant::Int8 knob): bit-exact int8 of the f32 values, same chunks
+    from loractl_amd.quant import QuantValue
+    q8, _, rep8 = load_quant_checkpoint(path, cuda, ["s.a", "s.b", "s.c"], chunk_bytes=96 * 128 * 4 // 3,
+                                        value=QuantValue.Q8S)
+    assert (rep8.quantized, rep8.left_plain, rep8.total_chunks) == (2, 1, 3)
+    for p_, w_ in (("s.a", w_a), ("s.b", wb32)):
+        qq, sc = O.quantize(w_, 32, 127)
+        assert np.array_equal(q8[p_].dequantized_weight().cpu().numpy(), O.dequant_q(qq, sc, 32)), p_
 
 
 def test_quantize_field_orientation(cuda):

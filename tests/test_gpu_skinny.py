@@ -20,13 +20,18 @@ def _weight(w, fmt, g, dev, per_channel=True):
         wq = D.quantize_int4(t, g)
         p, s = O.quantize_int4_packed(w, g)
         return wq, O.dequant_int4(p, s, w.shape[1], g)
+    if fmt == "int8":
+        wq = D.quantize_int8(t, g)
+        q, s = O.quantize(w, g, 127)
+        return wq, O.dequant_q(q, s, g)
     wq = D.quantize_fp8(t, per_channel)
     b, s = O.fp8_quantize(w, per_channel)
     return wq, O.fp8_dequant(b, s)
 
 
 # (fmt, group, per_channel): int4 blocks smaller, equal and larger than the 64-wide step
-FORMATS = [("int4", 32, True), ("int4", 64, True), ("int4", 128, True), ("fp8", 0, True), ("fp8", 0, False)]
+FORMATS = [("int4", 32, True), ("int4", 64, True), ("int4", 128, True), ("fp8", 0, True), ("fp8", 0, False),
+           ("int8", 32, True), ("int8", 128, True)]
 
 
 @pytest.mark.parametrize("M", [1, 7, 16])
@@ -35,8 +40,8 @@ FORMATS = [("int4", 32, True), ("int4", 64, True), ("int4", 128, True), ("fp8", 
 @pytest.mark.parametrize("K,N", [(96, 72), (1088, 520), (3072, 264), (4160, 136), (1088, 8192)])
 @pytest.mark.parametrize("fmt,g,pc", FORMATS)
 def test_skinny_base_and_lora(cuda, M, K, N, fmt, g, pc):
-    if fmt == "int4" and K % g:
-        pytest.skip("int4 blocks must divide d_in")
+    if fmt != "fp8" and K % g:
+        pytest.skip("int4 and int8 blocks must divide d_in")
     r = 17
     w, x, a, b, _ = case_inputs(M, K, N, r, seed=11 * M + K + N, b_sigma=0.05)
     wq, wdq = _weight(w, fmt, g, cuda, pc)
@@ -62,14 +67,14 @@ def test_skinny_ranks_and_bias(cuda, r, N):
     check("y", y, y_ref)
 
 
-@pytest.mark.parametrize("fmt", ["int4", "fp8"])
+@pytest.mark.parametrize("fmt", ["int4", "fp8", "int8"])
 def test_skinny_matches_large_m_kernel(cuda, fmt):
     """Rows 0..15 of a 300-token call (large-m kernel) against the same 16
     tokens alone (few-token kernel). The large-m kernel multiplies bf16(q s);
     the few-token int4 kernel (groups >= 64) multiplies q exactly and scales
     in f32, so the two differ by at most the weight's bf16 rounding (half
     an ulp, 2^-8 relative per weight, int4 only: fp8 values are exact in
-    bf16), the rounding of both outputs and of t to bf16, and f32
+    bf16 and both int8 kernels multiply bf16(q s)), the rounding of both outputs and of t to bf16, and f32
     summation order."""
     M, K, N, r = 300, 1024, 328, 32
     w, x, a, b, _ = case_inputs(M, K, N, r, seed=21)

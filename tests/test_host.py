@@ -40,7 +40,8 @@ def test_quant_knob_and_block_guard():
     # non-divisible input dim fails before any device work (quant.rs:76-80)
     with pytest.raises(AssertionError, match="multiple of the quant block"):
         quantize_linear_weight(torch.zeros(4, 33), QuantValue.Q4S, 32)
-    with pytest.raises(NotImplementedError):
+    # Q8S is built, and like Q4S it has no CPU path: a host tensor raises
+    with pytest.raises(ValueError, match="no CPU fallback"):
         quantize_linear_weight(torch.zeros(4, 64), QuantValue.Q8S, 32)
 
 

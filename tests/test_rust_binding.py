@@ -26,6 +26,7 @@ C2RUST = {
     "const float*": "*const f32",
     "double*": "*mut f64",
     "int64_t*": "*mut i64",
+    "int8_t*": "*mut i8",
     "uint8_t*": "*mut u8",
     "const uint8_t*": "*const u8",
     "uint16_t*": "*mut u16",
