@@ -19,6 +19,9 @@ around each of its launches on the launch stream. `cpu_baseline` times the
 reference's CPU algorithm (the oracle's f32 dequant + f32 GEMMs) on a
 bounded token sample of the same layer.
 
+`--workload ns8` is the north-star layer over an int8 (Q8S) group-64 base,
+`--workload c2` over a per-channel fp8 base: the same step and metric.
+
 `--workload requant` measures the on-device load path: an fp8 checkpoint
 tensor of the same layer (e4m3fn bytes and per-row f32 scales, [12288,
 3072]) re-quantized to int4-g64 by one kernel; `value` is GB/s of fp8 bytes
@@ -44,7 +47,9 @@ WORKLOADS = {
     "ns": (4096, 3072, 12288, 32, 32.0, "int4", 64),
     "c1": (1024, 3072, 3072, 16, 16.0, "int4", 64),
     "c2": (4096, 3072, 12288, 32, 32.0, "fp8", 0),
+    "ns8": (4096, 3072, 12288, 32, 32.0, "int8", 64),  # the north-star layer over an int8 (Q8S) base
     "skinny": (16, 3072, 12288, 32, 32.0, "int4", 64),  # forward only, HBM-bound
+    "skinny8": (16, 3072, 12288, 32, 32.0, "int8", 64),  # the same over an int8 (Q8S) base
     "requant": (0, 3072, 12288, 0, 0.0, "fp8", 64),  # fp8 checkpoint tensor -> int4, load time
     "c3": None,  # one synthetic MMDiT double-stream block's linear set (C3_SITES), image + text stream
     "c5": None,  # a Qwen3-style 28-layer decoder's linears (C5_LAYER), M swept over C5_M
@@ -164,7 +169,7 @@ def main():
 
     torch.cuda.set_device(0)
     dev = torch.device("cuda:0")
-    if args.workload == "skinny":
+    if args.workload in ("skinny", "skinny8"):
         return bench_skinny(args, dev)
     if args.workload == "requant":
         return bench_requant(args, dev)
@@ -178,7 +183,8 @@ def main():
     s = alpha / r
     w, x, a, b, dy = make_inputs(M, K, N, r)
     wt = torch.from_numpy(w).to(dev)
-    wq = D.quantize_int4(wt, group) if fmt == "int4" else D.quantize_fp8(wt, True)
+    wq = {"int4": lambda: D.quantize_int4(wt, group), "int8": lambda: D.quantize_int8(wt, group),
+          "fp8": lambda: D.quantize_fp8(wt, True)}[fmt]()
     del wt
     # the interchange (row) layout, for the CPU baseline: the first fused
     # call re-lays the weight into the blocked layout in place
@@ -259,7 +265,7 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (seeded PCG64; W~N(0,0.02) quantized on device, X,dY~N(0,1), A~U(+-1/sqrt(K)), B~N(0,1e-3))",
         "config": {
-            "workload": f"{fmt}{'-g' + str(group) if fmt == 'int4' else '-per-channel'} frozen Linear {K}->{N} "
+            "workload": f"{fmt}{'-per-channel' if fmt == 'fp8' else '-g' + str(group)} frozen Linear {K}->{N} "
                         f"+ LoRA r={r} alpha={alpha:g}, M={M} tokens, forward+backward (y, dx, dA, dB)",
             "M": M, "K": K, "N": N, "rank": r, "group": group, "format": fmt,
             "parallelism": "single-gpu",
@@ -284,7 +290,7 @@ def main():
     print(json.dumps(out), flush=True)
 
 
-def skinny_measure(args, dev, with_cpu=True, steps=100):
+def skinny_measure(args, dev, with_cpu=True, steps=100, workload="skinny"):
     """The few-token forward of the north-star layer (M=16): GB/s with the
     packed weight rotated past the Infinity Cache and ``steps`` forwards
     replayed from a HIP graph; per-kernel times from the library's events;
@@ -296,10 +302,12 @@ def skinny_measure(args, dev, with_cpu=True, steps=100):
     from loractl_amd import _lib as L
     from loractl_amd import device as D
 
-    M, K, N, r, alpha, fmt, group = WORKLOADS["skinny"]
+    M, K, N, r, alpha, fmt, group = WORKLOADS[workload]
     s = alpha / r
     w, x, a, b, _ = make_inputs(M, K, N, r)
-    wq = D.quantize_int4(torch.from_numpy(w).to(dev), group)
+    wt = torch.from_numpy(w).to(dev)
+    wq = D.quantize_int8(wt, group) if fmt == "int8" else D.quantize_int4(wt, group)
+    del wt
     wq_rows = (wq.data.cpu().numpy(), wq.scales.cpu().numpy()) if with_cpu else None
     wb = D.compute_weight(wq)
     # the row section of the blocked layout, the part the few-token kernel
@@ -346,7 +354,7 @@ def skinny_measure(args, dev, with_cpu=True, steps=100):
 
     ms_total, ratio, warm_ms = warm_and_time(run, 4, 2)
     ms_fwd = ms_total / (4 * n_graph)
-    wb_alg = N * K / 2 + 4 * N * K / group  # W_B (packed int4 + f32 group scales)
+    wb_alg = N * K * (1 if fmt == "int8" else 0.5) + 4 * N * K / group  # W_B (packed q + f32 group scales)
     bytes_fwd = wb_alg + 2 * M * K + 2 * M * N + 4 * r * (K + N)
     value = bytes_fwd / (ms_fwd * 1e-3) / 1e9
 
@@ -378,23 +386,23 @@ def skinny_measure(args, dev, with_cpu=True, steps=100):
         "peak": PEAK_HBM_GBS,
         "unit": "GB/s",
         "frac": round(achieved / PEAK_HBM_GBS, 4),
-        "traffic": load_traffic("fwd_main", "skinny"),
+        "traffic": load_traffic("fwd_main", workload),
         "bytes_per_launch": k_bytes,
         "avg_launch_us": round(launch_us, 3),
         "launch_time_from": "graph replay per forward (one launch)" if one_launch else "per-launch events",
     }
     cpu = None
     if with_cpu:
-        cpu = cpu_baseline_fwd(wq_rows, x, a, b, M, K, N, r, s, group, args.cpu_seconds, bytes_fwd)
+        cpu = cpu_baseline_fwd(wq_rows, x, a, b, M, K, N, r, s, group, args.cpu_seconds, bytes_fwd, fmt)
     return {
-        "metric": "int4-base LoRA linear skinny-M forward GB/s",
+        "metric": f"{fmt}-base LoRA linear skinny-M forward GB/s",
         "value": round(value, 1),
         "unit": "GB/s",
         "us_per_forward": round(ms_fwd * 1e3, 3),
         "pct_of_hbm_peak": round(100.0 * value / PEAK_HBM_GBS, 2),
         "bytes_per_forward": bytes_fwd,
         "sanity_x2_ratio": round(ratio, 3),
-        "workload": f"int4-g{group} frozen Linear {K}->{N} + LoRA r={r} alpha={alpha:g}, M={M} tokens, "
+        "workload": f"{fmt}-g{group} frozen Linear {K}->{N} + LoRA r={r} alpha={alpha:g}, M={M} tokens, "
                     f"forward (y, t); packed weight rotated over {ncopy} copies "
                     f"({ncopy * wbytes / 2**20:.0f} MiB), {n_graph} forwards replayed from a HIP graph",
         "kernels_us": {k: round(v, 3) for k, v in kernels.items()},
@@ -404,8 +412,8 @@ def skinny_measure(args, dev, with_cpu=True, steps=100):
 
 
 def bench_skinny(args, dev):
-    M, K, N, r, alpha, fmt, group = WORKLOADS["skinny"]
-    m = skinny_measure(args, dev, with_cpu=not args.no_cpu_baseline, steps=args.steps)
+    M, K, N, r, alpha, fmt, group = WORKLOADS[args.workload]
+    m = skinny_measure(args, dev, with_cpu=not args.no_cpu_baseline, steps=args.steps, workload=args.workload)
     out = {
         "metric": m["metric"],
         "value": m["value"],
@@ -923,13 +931,19 @@ def bench_mmdit(args, dev):
     print(json.dumps(out), flush=True)
 
 
-def cpu_baseline_fwd(wq_rows, x, a, b, M, K, N, r, s, group, budget_s, bytes_fwd):
+def cpu_baseline_fwd(wq_rows, x, a, b, M, K, N, r, s, group, budget_s, bytes_fwd, fmt="int4"):
     """The reference's CPU forward (f32 dequant of the whole weight, f32
     GEMMs) on the whole few-token workload, on this host's cores;
-    ``wq_rows`` is the (packed, scales) row layout."""
+    ``wq_rows`` is the (packed or int8 q, scales) row layout."""
+    import numpy as np
+
     import oracle as O
 
-    st = O.CpuFwdInt4(wq_rows[0], wq_rows[1], group, x, a, b, s)
+    if fmt == "int8":
+        st = O.CpuStepInt8(wq_rows[0], wq_rows[1], group, x, a, b, s, np.zeros((M, N), np.float32))
+        st.run = st.forward  # forward only
+    else:
+        st = O.CpuFwdInt4(wq_rows[0], wq_rows[1], group, x, a, b, s)
     t0 = time.perf_counter()
     threads = st.run()
     first = time.perf_counter() - t0
@@ -943,7 +957,7 @@ def cpu_baseline_fwd(wq_rows, x, a, b, M, K, N, r, s, group, budget_s, bytes_fwd
         "unit": "GB/s",
         "cores": int(threads),
         "kind": "port",
-        "sample": f"the whole workload (M={M}, {K}->{N} r={r} int4-g{group}), forward, {reps} reps of {dt:.4f} s "
+        "sample": f"the whole workload (M={M}, {K}->{N} r={r} {fmt}-g{group}), forward, {reps} reps of {dt:.4f} s "
                   f"(f32 dequant of the full weight + f32 GEMMs, OpenMP)",
     }
 
@@ -960,6 +974,9 @@ def cpu_baseline(wq_rows, x, a, b, dy, M, K, N, r, s, group, fmt, budget_s):
     if fmt == "int4":
         st = O.CpuStepInt4(wq_rows[0], wq_rows[1], group, x, a, b, s, dy)
         what = "f32 dequant of the full weight per forward and per backward (OpenMP), then f32 GEMMs"
+    elif fmt == "int8":
+        st = O.CpuStepInt8(wq_rows[0], wq_rows[1], group, x, a, b, s, dy)
+        what = "f32 dequant of the full int8 weight per forward and per backward (OpenMP), then f32 GEMMs"
     else:
         st = O.CpuStepF32(O.fp8_dequant(wq_rows[0], wq_rows[1]), x, a, b, s, dy)
         what = "f32 weight decoded once at load, f32 GEMMs"
@@ -975,7 +992,7 @@ def cpu_baseline(wq_rows, x, a, b, dy, M, K, N, r, s, group, fmt, budget_s):
         "unit": "TFLOP/s",
         "cores": O.blas_threads(),
         "kind": "port",
-        "sample": f"the whole step (M={M}, {K}->{N} r={r} {fmt}{'-g' + str(group) if fmt == 'int4' else ''}), fwd+bwd, "
+        "sample": f"the whole step (M={M}, {K}->{N} r={r} {fmt}{'' if fmt == 'fp8' else '-g' + str(group)}), fwd+bwd, "
                   f"{reps} steps of {dt:.3f} s: {what} in {O.blas_info()}",
     }
 

@@ -71,6 +71,8 @@ def lib():
         L.lrq_o_linear_bwd.argtypes = [vp, vp, vp, vp, ctypes.c_double, vp, _i64, _i64, _i64, _i64, vp, vp, vp]
         L.lrq_o_cpu_dequant_int4.restype = ctypes.c_int
         L.lrq_o_cpu_dequant_int4.argtypes = [vp, vp, _i64, _i64, _i64, vp]
+        L.lrq_o_cpu_dequant_int8.restype = ctypes.c_int
+        L.lrq_o_cpu_dequant_int8.argtypes = [vp, vp, _i64, _i64, _i64, vp]
         _lib = L
     return _lib
 
@@ -324,6 +326,20 @@ class CpuStepInt4(CpuFwdInt4):
         self.dA = self.X.T @ self.U
         self.dB = self.T.T @ self.dY
         return th
+
+
+class CpuStepInt8(CpuStepInt4):
+    """The same step over an int8 (Q8S) weight: q int8 [N, K] and scales
+    [N, K/g], dequantized to f32 on every forward and every backward
+    (lrq_o_cpu_dequant_int8, OpenMP)."""
+
+    def __init__(self, q, scales, group, X, A, B, s, dY):
+        super().__init__(np.zeros((1, 1), np.uint8), scales, group, X, A, B, s, dY)
+        self.q = _c(q, np.int8)
+
+    def dequant(self) -> int:
+        return lib().lrq_o_cpu_dequant_int8(_ptr(self.q), _ptr(self.scales), self.g, self.N, self.K,
+                                            _ptr(self.Wdq))
 
 
 class CpuStepF32(CpuStepInt4):

@@ -366,3 +366,21 @@ EXPORT int lrq_o_cpu_dequant_int4(const uint8_t* packed, const float* scales, in
   return 1;
 #endif
 }
+
+/* The same for an int8 (Q8S) weight: Wdq[N,K] = q * scale in f32 from q [N,K]
+ * and scales [N, K/g], OpenMP over rows. Returns the number of threads used. */
+EXPORT int lrq_o_cpu_dequant_int8(const int8_t* q, const float* scales, int64_t g, int64_t N, int64_t K,
+                                  float* Wdq) {
+#pragma omp parallel for schedule(static)
+  for (int64_t n = 0; n < N; ++n) {
+    const int8_t* row = q + n * K;
+    const float* sc = scales + n * (K / g);
+    float* out = Wdq + n * K;
+    for (int64_t k = 0; k < K; ++k) out[k] = (float)row[k] * sc[k / g];
+  }
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}

@@ -280,6 +280,28 @@ def test_cpu_baseline_step_matches_oracle():
         assert O.rel_deviation(got, ref) < 1e-5
 
 
+def test_cpu_baseline_int8_step_matches_oracle():
+    """The int8 CPU baseline: its per-pass dequant is bit-identical to the
+    pinned q * s (lrq_o_dequant_q, held to quant_int8_golden.json), and the
+    step computes the f64 oracle's fwd+bwd."""
+    rng = np.random.Generator(np.random.PCG64(4))
+    M, K, N, r, g = 48, 128, 80, 8, 32
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    q, s = O.quantize(w, g, 127)
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    A = rng.uniform(-0.1, 0.1, (K, r)).astype(np.float32)
+    B = (rng.standard_normal((r, N)) * 1e-2).astype(np.float32)
+    dY = rng.standard_normal((M, N)).astype(np.float32)
+    st = O.CpuStepInt8(q, s, g, X, A, B, 0.5, dY)
+    st.run()
+    wdq = O.dequant_q(q, s, g)
+    assert np.array_equal(st.Wdq.view(np.uint32), wdq.view(np.uint32))
+    Y, T = O.linear_fwd(X, wdq, A, B, 0.5)
+    dX, dA, dB = O.linear_bwd(X, wdq, A, B, 0.5, dY)
+    for got, ref in ((st.Y, Y), (st.dX, dX), (st.dA, dA), (st.dB, dB), (st.T, T)):
+        assert O.rel_deviation(got, ref) < 1e-5
+
+
 def test_cpu_baseline_forward_matches_oracle():
     """The timed few-token CPU baseline (forward only) computes the oracle's forward."""
     rng = np.random.Generator(np.random.PCG64(3))
