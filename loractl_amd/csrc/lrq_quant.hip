@@ -67,15 +67,30 @@ __global__ void __launch_bounds__(256) k_quantize(const void* __restrict__ wv, c
   }
   const float s = amax / (float)QMAX;  // correctly rounded f32 division
   if (run % rpb == 0) scales[row * (k / g) + run / rpb] = s;
+  // q = clamp(round_half_away(RN(v / s))). The quotient RN(v / s) is formed
+  // without a division per value: with y = RN(1 / s), q0 = RN(v y) and the
+  // exact remainder r = v - q0 s (one fma), RN(q0 + r y) == RN(v / s)
+  // (Markstein: y within half an ulp of 1/s and q0 within one ulp of v/s,
+  // no underflow). r stays normal for s >= 2^-80; smaller scales divide.
   int q[32];
+  auto to_int = [](float t) {
+    const float r = fminf(fmaxf(roundf(t), -(float)QMAX), (float)QMAX);  // half away from zero
+    return (int)r;
+  };
+  if (s >= 0x1p-80f) {
+    const float y = 1.0f / s;
 #pragma unroll
-  for (int i = 0; i < 32; ++i) {
-    q[i] = 0;
-    if (s != 0.0f) {
-      float r = roundf(v[i] / s);  // half away from zero
-      r = fminf(fmaxf(r, -(float)QMAX), (float)QMAX);
-      q[i] = (int)r;
+    for (int i = 0; i < 32; ++i) {
+      const float q0 = v[i] * y;
+      const float rem = __builtin_fmaf(-q0, s, v[i]);
+      q[i] = to_int(__builtin_fmaf(rem, y, q0));
     }
+  } else if (s != 0.0f) {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) q[i] = to_int(v[i] / s);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) q[i] = 0;
   }
   if constexpr (QMAX == 7) {
     u32x4 o = zero4();

@@ -179,3 +179,25 @@ def test_dropout_above_zero_is_refused():
     big = LoraDelta(64, 32, 65, 65.0)
     with pytest.raises(ValueError, match="rank <= 64"):
         quant_lora_linear(torch.zeros(2, 64), None, big)
+
+
+def test_quantizer_quotient_without_division(tmp_path):
+    """The quantizer kernels (lrq_quant.hip k_quantize) form RN(v / s) as
+    fma(r, y, q0) with y = RN(1/s), q0 = RN(v y), r = fma(-q0, s, v), not by
+    a division per value. tests/quotient_check.c restates that sequence in C
+    and holds it to the correctly rounded division over the kernels' domain
+    (every f32 near each rounding threshold, random values, 4000 scales):
+    the quotient is equal, and so is its half-away rounding. The GPU tests
+    hold the kernels themselves bit-exact against the oracle's division."""
+    import shutil
+    import subprocess
+
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("no C compiler")
+    exe = str(tmp_path / "quotient_check")
+    src = os.path.join(os.path.dirname(__file__), "quotient_check.c")
+    subprocess.run([gcc, "-O2", "-ffp-contract=off", "-o", exe, src, "-lm"], check=True)
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert " 0 differ" in r.stdout and " 0 round differently" in r.stdout
