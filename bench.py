@@ -77,6 +77,9 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-skinny", action="store_true", help="leave the skinny-M sub-object out of the ns line")
     p.add_argument("--no-mmdit", action="store_true", help="leave the MMDiT step sub-object out of the ns line")
+    p.add_argument("--mmdit-full-replay", action="store_true",
+                   help="MMDiT step: replay each block whole (attention forward included) instead of reusing the "
+                        "capture's attention output")
     return p.parse_args()
 
 
@@ -806,9 +809,11 @@ def mmdit_measure(args, dev, steps, warmup, with_cpu=True):
         D.reserve(M, N, K, cfg.rank)
     losses = []
 
+    keep = not getattr(args, "mmdit_full_replay", False)
+
     def step():
         opt.zero_grad(set_to_none=True)
-        losses.append(checkpointed_step(model, ad, batch))
+        losses.append(checkpointed_step(model, ad, batch, keep_attention=keep))
         opt.step()
 
     def run(n):
@@ -840,6 +845,8 @@ def mmdit_measure(args, dev, steps, warmup, with_cpu=True):
         "ms_per_step": round(ms_step, 2),
         "tflops": round(fl["total"] / (ms_step * 1e-3) / 1e12, 2),
         "flop_model": {k: fl[k] for k in ("proj", "attn", "lora", "total")},
+        "checkpointing": "per block; the capture's attention output and log-sum-exp kept for the replay"
+                         if keep else "per block, whole-block replay",
         "sanity_x2_ratio": round(ratio, 3),
         "warm_ms": round(warm_ms, 1),
         "setup_s": round(setup_s, 1),

@@ -18,7 +18,11 @@ sites and the step structure carry over:
   loss and the trunk cotangent (the loss scale folded in once), then each
   block is replayed last to first on its own graph, seeded by the incoming
   cotangent, its adapter gradients accumulating on the deltas' parameters;
-  the per-site cost is two fused forwards and one fused backward;
+  the per-site cost is two fused forwards and one fused backward. The
+  capture may also keep each block's attention output and log-sum-exp
+  (``keep_attention``, about 29 MB per block at 4608 tokens): the replay
+  then recomputes q, k and v (its backward needs them) but not the
+  attention forward, and the gradients are those of the full replay;
 - the flow-matching target follows ``flow.rs``: ``x_t = (1 - t) x0 + t eps``,
   target ``v = eps - x0`` (t = 0 is data), loss ``mean((pred - v)^2)``.
 
@@ -28,8 +32,8 @@ the norm's gain its frozen zero parameter + 1), and its residuals are gated,
 ``x + gate * branch``; both run as HIP kernels (``modnorm``,
 ``gated_residual``), as does the attention input (``attn_prep``: head split,
 per-head RMSNorm of q and k, RoPE over the joint text-then-image sequence).
-The rest around the fused sites is PyTorch-ROCm (SDPA attention on its
-memory-efficient backend, GELU, the frozen bf16 embedders and head linears):
+The rest around the fused sites is PyTorch-ROCm (attention through torch's
+memory-efficient kernels, GELU, the frozen bf16 embedders and head linears):
 outside the quantized-linear path. The modulation (adaLN) linears take the conditioning
 vector, one row per batch element, as in FLUX.
 """
@@ -50,6 +54,39 @@ from .lora import LoraDelta
 
 STREAMS = ("img", "txt")
 SITE_NAMES = ("mod", "qkv", "out", "up", "down")
+
+
+class _Attention(torch.autograd.Function):
+    """softmax(q k^T / sqrt(d)) v over the joint sequence with torch's
+    memory-efficient attention kernels (``aten::_efficient_attention_forward``
+    and ``_backward``) on [1, L, heads, d], the layout they take and the one
+    ``attn_prep`` writes. ``kept`` is (out, log-sum-exp) of an earlier forward
+    of the same q, k, v, which the call returns instead of running the
+    forward again; ``keep`` (a list) receives them from a forward that runs."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, kept, keep):
+        grad = any(ctx.needs_input_grad[:3])
+        if kept is None:
+            out, lse = torch.ops.aten._efficient_attention_forward(q, k, v, None, None, None, None, None, 0.0, 0,
+                                                                    grad or keep is not None)[:2]
+            if keep is not None:
+                keep.append((out, lse))
+        else:
+            out, lse = kept
+        if grad:
+            ctx.save_for_backward(q, k, v, out, lse)
+        return out.detach()
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, out, lse = ctx.saved_tensors
+        # no dropout: the philox state is not read
+        zero = torch.zeros((), dtype=torch.int64)
+        dq, dk, dv, _ = torch.ops.aten._efficient_attention_backward(
+            dout.contiguous(), q, k, v, None, out, None, None, q.shape[1], k.shape[1], lse, 0.0, zero, zero, 0,
+            False)
+        return dq, dk, dv, None, None
 
 
 @dataclass
@@ -95,6 +132,7 @@ class Capture:
     block_inputs: List[Tuple[torch.Tensor, torch.Tensor]] = field(default_factory=list)
     vec: Optional[torch.Tensor] = None
     rope: Optional[Tuple[torch.Tensor, torch.Tensor]] = None
+    attention: list = field(default_factory=list)  # per block (out, log-sum-exp), when kept
     x_img: Optional[torch.Tensor] = None
     x_txt: Optional[torch.Tensor] = None
 
@@ -148,8 +186,10 @@ class Mmdit:
         return self._linear(modnorm(x_img, scale.contiguous(), shift.contiguous()), self.final)
 
     def block(self, i: int, x_img: torch.Tensor, x_txt: torch.Tensor, vec: torch.Tensor, rope,
-              adapters: Optional[LoraAdapters]):
-        """One double-stream block on [L_img, H] and [L_txt, H] bf16 streams."""
+              adapters: Optional[LoraAdapters], kept=None, keep: Optional[list] = None):
+        """One double-stream block on [L_img, H] and [L_txt, H] bf16 streams
+        (``kept`` / ``keep``: the attention output and log-sum-exp to reuse, or
+        a list to append them to; see ``_Attention``)."""
         cfg = self.cfg
         H, nh, hd = cfg.hidden, cfg.heads, cfg.head_dim
         p = f"blocks.{i}"
@@ -165,9 +205,8 @@ class Mmdit:
         # q, k, v [L, nh, hd] over the joint sequence, q and k RMS-normalised
         # per head and rotated (one kernel over both streams' rows)
         q, k, v = attn_prep(qkvs[0], qkvs[1], rope, nh)
-        with torch.nn.attention.sdpa_kernel([torch.nn.attention.SDPBackend.EFFICIENT_ATTENTION]):
-            o = F.scaled_dot_product_attention(*(t.unsqueeze(0).transpose(1, 2) for t in (q, k, v)))
-        o = o[0].transpose(0, 1).reshape(-1, H)  # [L, H]
+        o = _Attention.apply(q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0), kept, keep)
+        o = o.reshape(-1, H)  # [L, H]
         lt = x_txt.shape[0]
         outs = {}
         for s, x, oo in (("txt", x_txt, o[:lt]), ("img", x_img, o[lt:])):
@@ -196,14 +235,16 @@ class Mmdit:
         return self.head(x_img, vec)
 
     @torch.no_grad()
-    def forward_capture(self, img, txt, t, adapters) -> Capture:
+    def forward_capture(self, img, txt, t, adapters, keep_attention: bool = False) -> Capture:
         """Pre-trunk and trunk with no graph, keeping each block's inputs
-        (``mmdit.rs:1474-1507``)."""
+        (``mmdit.rs:1474-1507``) and, with ``keep_attention``, each block's
+        attention output and log-sum-exp."""
         x_img, x_txt, vec, rope = self.prepare(img, txt, t)
         cap = Capture(vec=vec, rope=rope)
+        keep = cap.attention if keep_attention else None
         for i in range(self.cfg.layers):
             cap.block_inputs.append((x_img, x_txt))
-            x_img, x_txt = self.block(i, x_img, x_txt, vec, rope, adapters)
+            x_img, x_txt = self.block(i, x_img, x_txt, vec, rope, adapters, keep=keep)
         cap.x_img, cap.x_txt = x_img, x_txt
         return cap
 
@@ -254,17 +295,22 @@ def monolithic_step(model: Mmdit, adapters: LoraAdapters, batch, loss_scale: flo
     return float(loss.item())
 
 
-def checkpointed_step(model: Mmdit, adapters: LoraAdapters, batch, loss_scale: float = 1.0) -> float:
+def checkpointed_step(model: Mmdit, adapters: LoraAdapters, batch, loss_scale: float = 1.0,
+                      keep_attention: bool = True) -> float:
     """One block-checkpointed step (``block_ckpt.rs:103-207``): capture, head
     graph, reverse per-block replay. Returns the unscaled loss; adapter
-    gradients accumulate on the deltas' ``.grad`` (scaled by ``loss_scale``)."""
+    gradients accumulate on the deltas' ``.grad`` (scaled by ``loss_scale``).
+    ``keep_attention`` keeps each block's attention output and log-sum-exp
+    from the capture for its replay (``keep_attention=False`` replays the
+    whole block, as the reference does)."""
     with adapters.cached_factors():  # the factors stay fixed through capture and replay
-        return _checkpointed_step(model, adapters, batch, loss_scale)
+        return _checkpointed_step(model, adapters, batch, loss_scale, keep_attention)
 
 
-def _checkpointed_step(model: Mmdit, adapters: LoraAdapters, batch, loss_scale: float) -> float:
+def _checkpointed_step(model: Mmdit, adapters: LoraAdapters, batch, loss_scale: float,
+                       keep_attention: bool) -> float:
     img, txt, t, target = batch
-    cap = model.forward_capture(img, txt, t, adapters)
+    cap = model.forward_capture(img, txt, t, adapters, keep_attention)
     # head graph: trunk output re-tracked, loss scale folded into the seed once
     x_img = cap.x_img.detach().requires_grad_()
     loss = flow_loss(model.head(x_img, cap.vec), target)
@@ -275,10 +321,13 @@ def _checkpointed_step(model: Mmdit, adapters: LoraAdapters, batch, loss_scale: 
     # reverse sweep, one standalone graph per block
     for i in reversed(range(model.cfg.layers)):
         xi, xt = (v.detach().requires_grad_() for v in cap.block_inputs[i])
-        oi, ot = model.block(i, xi, xt, cap.vec, cap.rope, adapters)
+        kept = cap.attention[i] if keep_attention else None
+        oi, ot = model.block(i, xi, xt, cap.vec, cap.rope, adapters, kept=kept)
         torch.autograd.backward([oi, ot], [g_img, g_txt])
         g_img, g_txt = xi.grad, xt.grad
         cap.block_inputs[i] = None  # this block's inputs are done
+        if keep_attention:
+            cap.attention[i] = None
     return float(loss.item())
 
 

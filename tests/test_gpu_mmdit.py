@@ -10,6 +10,7 @@ import pytest
 import torch
 
 import oracle as O
+from gpu_helpers import check
 from loractl_amd import device as D
 from loractl_amd.mmdit_ops import attn_prep, gated_residual, modnorm, rope_tables
 from loractl_amd.mmdit import (Mmdit, MmditConfig, build_mmdit_adapters, checkpointed_step, flow_batch,
@@ -64,6 +65,55 @@ def test_checkpointed_step_matches_monolithic(cuda):
         ref = a.cpu().numpy()
         got = b.cpu().numpy()
         assert O.rel_deviation(got, ref) <= 1e-3 and O.cosine(got, ref) >= 0.99999, path
+
+
+def test_kept_attention_matches_full_replay(cuda):
+    """keep_attention (the capture's attention output and log-sum-exp reused
+    by the replay) gives the full replay's loss and, up to the attention
+    backward's atomic reduction order, its gradients."""
+    model = Mmdit(CFG, cuda, seed=3)
+    ad = build_mmdit_adapters(CFG, cuda, seed=4, b_std=0.02)
+    batch = flow_batch(CFG, IMG, TXT, cuda, seed=5)
+    loss_f = checkpointed_step(model, ad, batch, keep_attention=False)
+    gf = _grads(ad)
+    _zero(ad)
+    loss_k = checkpointed_step(model, ad, batch, keep_attention=True)
+    gk = _grads(ad)
+    assert loss_k == loss_f
+    for path_i, (a, b) in enumerate(zip(gf, gk)):
+        path = CFG.site_paths()[path_i // 2]
+        assert (a is None) == (b is None), path
+        if a is None or not a.abs().max() > 0:
+            continue
+        got, ref = b.cpu().numpy(), a.cpu().numpy()
+        assert O.rel_deviation(got, ref) <= 1e-3 and O.cosine(got, ref) >= 0.99999, path
+
+
+@pytest.mark.parametrize("L,heads,hd", [(160, 4, 128), (96, 2, 64)])
+def test_attention_matches_fp32_reference(cuda, L, heads, hd):
+    """The block's attention (torch's memory-efficient kernels called on
+    [1, L, heads, d]) against softmax(q k^T / sqrt(d)) v in fp32 with fp32
+    autograd: output and dq, dk, dv within bf16 rounding, and a kept
+    (output, log-sum-exp) pair gives the same output and gradients."""
+    from loractl_amd.mmdit import _Attention
+
+    g = torch.Generator(device=cuda).manual_seed(L + hd)
+    q, k, v = (torch.randn(1, L, heads, hd, device=cuda, generator=g).to(torch.bfloat16) for _ in range(3))
+    do = torch.randn(1, L, heads, hd, device=cuda, generator=g).to(torch.bfloat16)
+    qf, kf, vf = (t.float().detach().requires_grad_() for t in (q, k, v))
+    s = torch.einsum("blhd,bmhd->bhlm", qf, kf) / hd ** 0.5
+    of = torch.einsum("bhlm,bmhd->blhd", s.softmax(-1), vf)
+    of.backward(do.float())
+    keep = []
+    with torch.no_grad():
+        _Attention.apply(q, k, v, None, keep)
+    for kept in (None, keep[0]):
+        qq, kk, vv = (t.detach().requires_grad_() for t in (q, k, v))
+        o = _Attention.apply(qq, kk, vv, kept, None)
+        o.backward(do)
+        check("o", o, of.detach().cpu().numpy())
+        for name, got, ref in (("dq", qq.grad, qf.grad), ("dk", kk.grad, kf.grad), ("dv", vv.grad, vf.grad)):
+            check(name, got, ref.cpu().numpy())
 
 
 def test_fused_sites_match_fp32_dequantized_reference(cuda):
