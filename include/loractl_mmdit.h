@@ -11,6 +11,9 @@
  * consecutive-pair rotation apply_rope :385-399), done on the joint
  * text-then-image token sequence, with the gradient of the same map.
  *
+ * The rest are the block's elementwise glue: modulated norms, gated
+ * residuals and the MLP's GELU, forward and gradient.
+ *
  * Conventions (as loractl_rocm.h): device pointers owned by the caller,
  * 16-byte aligned, row-major; bf16 as uint16_t bits; stream-ordered and
  * asynchronous on `stream` (a hipStream_t, NULL for the default stream);
@@ -78,6 +81,20 @@ int lmd_modnorm_bwd(const uint16_t* dh, const uint16_t* x, int64_t rows, int h, 
  * [h], fixed order). The gradient in x is dy itself. */
 int lmd_gated_residual_bwd(const uint16_t* dy, const uint16_t* o, int64_t rows, int h, const uint16_t* gate,
                            uint16_t* d_o, uint16_t* dgate, float* part, void* stream);
+
+/* The gated residual itself: y = x + gate * o (mmdit.rs:860-869), x, o, y
+ * [rows, h], gate bf16 [h]; f32 fma, one rounding. */
+int lmd_gated_residual_fwd(const uint16_t* x, const uint16_t* o, int64_t rows, int h, const uint16_t* gate,
+                           uint16_t* y, void* stream);
+
+/* The driver's MLP activation (FLUX-style blocks; the reference's own
+ * single-stream block uses SwiGLU): g = gelu_tanh(u) =
+ * u (1 + tanh(sqrt(2/pi) (u + 0.044715 u^3))) / 2 elementwise over n bf16
+ * values (n % 8 == 0), computed in f32 as u * sigmoid(2 z). */
+int lmd_gelu_tanh_fwd(const uint16_t* u, int64_t n, uint16_t* g, void* stream);
+
+/* Its gradient: du = dg * d gelu_tanh(u) / du. */
+int lmd_gelu_tanh_bwd(const uint16_t* dg, const uint16_t* u, int64_t n, uint16_t* du, void* stream);
 
 #ifdef __cplusplus
 }

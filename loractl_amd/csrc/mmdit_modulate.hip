@@ -1,12 +1,14 @@
-// Modulated RMSNorm and gated residual of a double-stream MMDiT block, the
-// elementwise glue around its fused linears:
+// Modulated RMSNorm, gated residual and the MLP's GELU of a double-stream
+// MMDiT block, the elementwise glue around its fused linears:
 //
 //   h = (scale + 1) * x / sqrt(mean(x^2) + eps) + shift      (per row of x)
 //   y = x + gate * o
+//   g = gelu_tanh(u) = u / (1 + exp(-2 c (u + 0.044715 u^3))), c = sqrt(2/pi)
 //
 // with scale, shift and gate one [h] vector per block (the modulation
-// linear's output). Forward of the norm and the gradients of both are HIP
-// kernels here; the residual's forward is one torch addcmul.
+// linear's output). Forwards and gradients are HIP kernels here. The
+// residual's forward and GELU are flat streams of 16-byte chunks (y: 6
+// bytes per element; GELU 4, its gradient 6).
 //
 // A row is one wavefront: lane l takes the 16-byte chunks l, l + 64, ... of
 // the row, so the row's sum is a 64-lane reduction and every load and store
@@ -272,6 +274,73 @@ __global__ __launch_bounds__(256) void k_colsum(ModArgs a, int groups, int nsum)
   for (int e = 0; e < 4; ++e) out[e] = __builtin_bit_cast(uint16_t, (__bf16)t[e]);
 }
 
+// y = x + gate * o over rows x h, one thread per 16-byte chunk
+__global__ __launch_bounds__(256) void k_gated_res_fwd(const uint16_t* __restrict__ x,
+                                                       const uint16_t* __restrict__ o,
+                                                       const uint16_t* __restrict__ gate, int64_t chunks, int cpr,
+                                                       uint16_t* __restrict__ y) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= chunks) return;
+  const int c = (int)(i % cpr);
+  float xv[8], ov[8], gv[8];
+  unpack8(ld16(x + i * 8), xv);
+  unpack8(ld16(o + i * 8), ov);
+  unpack8(ld16(gate + c * 8), gv);
+  u32x4 r;
+#pragma unroll
+  for (int p = 0; p < 4; ++p)
+    r[p] = pack2(__builtin_fmaf(gv[2 * p], ov[2 * p], xv[2 * p]), __builtin_fmaf(gv[2 * p + 1], ov[2 * p + 1], xv[2 * p + 1]));
+  st16(y + i * 8, r);
+}
+
+constexpr float GELU_C = 0.7978845608028654f;  // sqrt(2 / pi)
+constexpr float GELU_K = 0.044715f;
+
+// sigmoid(2 c (u + k u^3)) = (1 + tanh(c (u + k u^3))) / 2, and its argument's
+// derivative in u
+LMD_DEV float gelu_gate(float u, float* dz) {
+  const float u2 = fminf(u * u, 1e30f);  // |u| past 1e15: z and z' stay ordered, no inf * 0 below
+  const float z = GELU_C * __builtin_fmaf(GELU_K * u2, u, u);
+  if (dz) *dz = GELU_C * __builtin_fmaf(3.0f * GELU_K, u2, 1.0f);
+  return __builtin_amdgcn_rcpf(1.0f + __expf(-2.0f * z));
+}
+
+// g = u * sigmoid(2z), one thread per 16-byte chunk
+__global__ __launch_bounds__(256) void k_gelu_fwd(const uint16_t* __restrict__ u, int64_t chunks,
+                                                  uint16_t* __restrict__ g) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= chunks) return;
+  float f[8];
+  unpack8(ld16(u + i * 8), f);
+  u32x4 r;
+#pragma unroll
+  for (int p = 0; p < 4; ++p)
+    r[p] = pack2(f[2 * p] * gelu_gate(f[2 * p], nullptr), f[2 * p + 1] * gelu_gate(f[2 * p + 1], nullptr));
+  st16(g + i * 8, r);
+}
+
+// du = dg * (s + 2 u s (1 - s) z'), s = sigmoid(2z): the derivative of
+// u * (1 + tanh z) / 2 with 1 - tanh^2 z = 4 s (1 - s)
+__global__ __launch_bounds__(256) void k_gelu_bwd(const uint16_t* __restrict__ dg, const uint16_t* __restrict__ u,
+                                                  int64_t chunks, uint16_t* __restrict__ du) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= chunks) return;
+  float f[8], d[8], o[8];
+  unpack8(ld16(u + i * 8), f);
+  unpack8(ld16(dg + i * 8), d);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float dz;
+    const float sg = gelu_gate(f[e], &dz);
+    const float w = sg * (1.0f - sg);  // 0 once the sigmoid saturates, before u scales it
+    o[e] = d[e] * __builtin_fmaf(2.0f * (w * f[e]), dz, sg);
+  }
+  u32x4 r;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) r[p] = pack2(o[2 * p], o[2 * p + 1]);
+  st16(du + i * 8, r);
+}
+
 int fail(int code, const char* what) {
   lmd_err_msg = what;
   return code;
@@ -385,5 +454,42 @@ extern "C" int lmd_gated_residual_bwd(const uint16_t* dy, const uint16_t* o, int
   LMD_CPL_SWITCH(k_gated_res_bwd, dim3(groups), h * sizeof(float))
   if (int rc = launched()) return rc;
   hipLaunchKernelGGL(k_colsum, dim3((h / 4 + 63) / 64), dim3(256), 0, (hipStream_t)stream, a, groups, 1);
+  return launched();
+}
+
+extern "C" int lmd_gated_residual_fwd(const uint16_t* x, const uint16_t* o, int64_t rows, int h, const uint16_t* gate,
+                                      uint16_t* y, void* stream) {
+  if (int rc = check_common(rows, h, o, gate)) return rc;
+  if (!x || !y) return fail(-1, "null pointer");
+  if (!al16(x) || !al16(y)) return fail(-1, "x and y must be 16-byte aligned");
+  const int64_t chunks = rows * (h / 8);
+  if ((chunks + 255) / 256 > 0x7fffffff) return fail(-1, "too many rows");
+  lmd_err_msg.clear();
+  hipLaunchKernelGGL(k_gated_res_fwd, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, (hipStream_t)stream, x, o,
+                     gate, chunks, h / 8, y);
+  return launched();
+}
+
+extern "C" int lmd_gelu_tanh_fwd(const uint16_t* u, int64_t n, uint16_t* g, void* stream) {
+  if (n <= 0 || n % 8) return fail(-1, "n must be a positive multiple of 8");
+  if (!u || !g) return fail(-1, "null pointer");
+  if (!al16(u) || !al16(g)) return fail(-1, "u and g must be 16-byte aligned");
+  const int64_t chunks = n / 8;
+  if ((chunks + 255) / 256 > 0x7fffffff) return fail(-1, "too many elements");
+  lmd_err_msg.clear();
+  hipLaunchKernelGGL(k_gelu_fwd, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, (hipStream_t)stream, u, chunks,
+                     g);
+  return launched();
+}
+
+extern "C" int lmd_gelu_tanh_bwd(const uint16_t* dg, const uint16_t* u, int64_t n, uint16_t* du, void* stream) {
+  if (n <= 0 || n % 8) return fail(-1, "n must be a positive multiple of 8");
+  if (!dg || !u || !du) return fail(-1, "null pointer");
+  if (!al16(dg) || !al16(u) || !al16(du)) return fail(-1, "dg, u and du must be 16-byte aligned");
+  const int64_t chunks = n / 8;
+  if ((chunks + 255) / 256 > 0x7fffffff) return fail(-1, "too many elements");
+  lmd_err_msg.clear();
+  hipLaunchKernelGGL(k_gelu_bwd, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, (hipStream_t)stream, dg, u,
+                     chunks, du);
   return launched();
 }

@@ -30,12 +30,13 @@ Each stream's pre- and post-attention norms are the reference block's
 modulated norm, ``(scale + 1) * ZRmsNorm(x) + shift`` (``mmdit.rs:857-870``,
 the norm's gain its frozen zero parameter + 1), and its residuals are gated,
 ``x + gate * branch``; both run as HIP kernels (``modnorm``,
-``gated_residual``), as does the attention input (``attn_prep``: head split,
-per-head RMSNorm of q and k, RoPE over the joint text-then-image sequence).
-The rest around the fused sites is PyTorch-ROCm (attention through torch's
-memory-efficient kernels, GELU, the frozen bf16 embedders and head linears):
-outside the quantized-linear path. The modulation (adaLN) linears take the conditioning
-vector, one row per batch element, as in FLUX.
+``gated_residual``), as do the MLP's GELU (``gelu_tanh``) and the attention
+input (``attn_prep``: head split, per-head RMSNorm of q and k, RoPE over
+the joint text-then-image sequence). The rest around the fused sites is
+PyTorch-ROCm (attention through torch's memory-efficient kernels, the
+frozen bf16 embedders and head linears): outside the quantized-linear path.
+The modulation (adaLN) linears take the conditioning vector, one row per
+batch element, as in FLUX.
 """
 
 from __future__ import annotations
@@ -49,7 +50,7 @@ import torch.nn.functional as F
 
 from . import device as D
 from .adapters import LoraAdapters, QuantLinear, site
-from .mmdit_ops import attn_prep, modnorm, gated_residual, rope_tables
+from .mmdit_ops import attn_prep, gated_residual, gelu_tanh, modnorm, rope_tables
 from .lora import LoraDelta
 
 STREAMS = ("img", "txt")
@@ -215,7 +216,7 @@ class Mmdit:
             h2 = modnorm(x, sc2, sh2)
             up = site(adapters, f"{p}.{s}.up", self.bases[f"{p}.{s}.up"], h2)
             x = gated_residual(x, g2, site(adapters, f"{p}.{s}.down", self.bases[f"{p}.{s}.down"],
-                                           F.gelu(up, approximate="tanh")))
+                                           gelu_tanh(up)))
             outs[s] = x
         return outs["img"], outs["txt"]
 

@@ -30,6 +30,9 @@ SIGNATURES = {
     "lmd_modnorm_fwd": ([_vp, _i64, _i32, _vp, _vp, _f32, _vp, _vp, _vp], _i32),
     "lmd_modnorm_bwd": ([_vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp], _i32),
     "lmd_gated_residual_bwd": ([_vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp], _i32),
+    "lmd_gated_residual_fwd": ([_vp, _vp, _i64, _i32, _vp, _vp, _vp], _i32),
+    "lmd_gelu_tanh_fwd": ([_vp, _i64, _vp, _vp], _i32),
+    "lmd_gelu_tanh_bwd": ([_vp, _vp, _i64, _vp, _vp], _i32),
     "lmd_attn_prep_fwd": ([_vp, _i64, _vp, _i64, _i32, _i32, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _vp], _i32),
     "lmd_attn_prep_bwd": ([_vp, _vp, _vp, _vp, _i64, _vp, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp], _i32),
 }
@@ -163,9 +166,16 @@ class _GatedResidual(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, gate, o):
         o2, h = _rows(o, gate, "gated_residual")
+        if x.shape != o.shape or x.dtype != torch.bfloat16:
+            raise ValueError("gated_residual: x must be bf16 with the shape of o")
+        x2 = x.reshape(-1, h).contiguous()
+        rows = o2.shape[0]
+        y = torch.empty_like(x2)
+        _check(load().lmd_gated_residual_fwd(x2.data_ptr(), o2.data_ptr(), rows, h, gate.data_ptr(), y.data_ptr(),
+                                             _stream(o2.device)), "lmd_gated_residual_fwd")
         ctx.save_for_backward(o2, gate)
         ctx.shapes = (o.shape, gate.shape)
-        return torch.addcmul(x, gate, o)
+        return y.view(x.shape)
 
     @staticmethod
     def backward(ctx, dy):
@@ -182,6 +192,35 @@ class _GatedResidual(torch.autograd.Function):
         return dy, dgate.view(gs), do.view(os_)
 
 
+class _GeluTanh(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, u):
+        if u.dtype != torch.bfloat16 or not u.is_cuda or u.numel() % 8:
+            raise ValueError("gelu_tanh: a bf16 GPU tensor of a multiple of 8 elements expected")
+        u2 = u.contiguous()
+        g = torch.empty_like(u2)
+        _check(load().lmd_gelu_tanh_fwd(u2.data_ptr(), u2.numel(), g.data_ptr(), _stream(u2.device)),
+               "lmd_gelu_tanh_fwd")
+        ctx.save_for_backward(u2)
+        return g
+
+    @staticmethod
+    def backward(ctx, dg):
+        (u,) = ctx.saved_tensors
+        dg2 = dg.to(torch.bfloat16).contiguous()
+        du = torch.empty_like(u)
+        _check(load().lmd_gelu_tanh_bwd(dg2.data_ptr(), u.data_ptr(), u.numel(), du.data_ptr(), _stream(u.device)),
+               "lmd_gelu_tanh_bwd")
+        return du
+
+
+def gelu_tanh(u: torch.Tensor) -> torch.Tensor:
+    """``u (1 + tanh(sqrt(2/pi) (u + 0.044715 u^3))) / 2``, the MLP activation
+    of the FLUX-style blocks (``F.gelu(u, approximate="tanh")``), in f32 with
+    one rounding; forward and gradient are one kernel each."""
+    return _GeluTanh.apply(u)
+
+
 def modnorm(x: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor, eps: float = 1e-5) -> torch.Tensor:
     """``(scale + 1) * x / sqrt(mean(x^2) + eps) + shift`` per row of x
     (``mmdit.rs:857-870``: ZRmsNorm with its frozen zero gain, then the
@@ -191,5 +230,6 @@ def modnorm(x: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor, eps: floa
 
 def gated_residual(x: torch.Tensor, gate: torch.Tensor, o: torch.Tensor) -> torch.Tensor:
     """``x + gate * o`` (``mmdit.rs:860-869``), gate one row broadcast over
-    the rows of o; the gradient in gate and o is one kernel."""
+    the rows of o; the forward is one kernel, the gradient in gate and o
+    another."""
     return _GatedResidual.apply(x, gate, o)

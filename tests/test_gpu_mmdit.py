@@ -12,7 +12,7 @@ import torch
 import oracle as O
 from gpu_helpers import check
 from loractl_amd import device as D
-from loractl_amd.mmdit_ops import attn_prep, gated_residual, modnorm, rope_tables
+from loractl_amd.mmdit_ops import attn_prep, gated_residual, gelu_tanh, modnorm, rope_tables
 from loractl_amd.mmdit import (Mmdit, MmditConfig, build_mmdit_adapters, checkpointed_step, flow_batch,
                                monolithic_step)
 
@@ -276,3 +276,35 @@ def test_modnorm_and_gated_residual_match_reference(cuda, rows, h):
     for a, b in zip([hh, dx, dsc, dsh, y, dgt, do], [*(lambda r: [r[0], *r[1]])(norm_grads()),
                                                    *(lambda r: [r[0], r[1][1], r[1][2]])(res_grads())]):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("n", [64, 4096 * 24, 512 * 12288])
+def test_gelu_tanh_matches_reference(cuda, n):
+    """The MLP's GELU (forward and gradient kernels) against the f64 formula
+    u (1 + tanh(sqrt(2/pi) (u + 0.044715 u^3))) / 2 and its autograd within
+    bf16 rounding, against torch's F.gelu(approximate="tanh") on the same
+    bf16 input within one bf16 ulp (plus 1e-5 where torch's f32 1 + tanh(z)
+    cancels, u below about -4; the kernel's u * sigmoid(2z) does not), and
+    at zeros and saturation (finite, exact limits)."""
+    import torch.nn.functional as F
+
+    g = torch.Generator(device=cuda).manual_seed(n)
+    u = (torch.randn(n, device=cuda, generator=g) * 3).to(torch.bfloat16)
+    dg = torch.randn(n, device=cuda, generator=g).to(torch.bfloat16)
+    ul = u.clone().requires_grad_(True)
+    out = gelu_tanh(ul)
+    out.backward(dg)
+    ud = u.double().requires_grad_(True)
+    ref = 0.5 * ud * (1 + torch.tanh((2 / np.pi) ** 0.5 * (ud + 0.044715 * ud ** 3)))
+    ref.backward(dg.double())
+    _close(out, ref.detach(), 2.0 ** -8, 1e-6)
+    _close(ul.grad, ud.grad, 2.0 ** -8, 1e-4)
+    tg = F.gelu(u.float(), approximate="tanh").to(torch.bfloat16).float()
+    assert bool(((out.float() - tg).abs() <= 2.0 ** -7 * tg.abs() + 1e-5).all())
+    ext = torch.tensor([0.0, -0.0, 30.0, -30.0, 1e20, -1e20, 3e38, -3e38], device=cuda).to(torch.bfloat16)
+    e = ext.clone().requires_grad_(True)
+    o = gelu_tanh(e)
+    o.backward(torch.ones_like(e))
+    assert torch.equal(o.float().cpu(), torch.tensor([0.0, 0.0, 30.0, 0.0, 0.0, 0.0, 0.0, 0.0]) +
+                       torch.where(ext.float().cpu() > 1e19, ext.float().cpu(), torch.zeros(8)))
+    assert torch.equal(e.grad.float().cpu(), torch.tensor([0.5, 0.5, 1.0, 0.0, 1.0, 0.0, 1.0, 0.0]))
