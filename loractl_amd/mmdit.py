@@ -297,13 +297,14 @@ def monolithic_step(model: Mmdit, adapters: LoraAdapters, batch, loss_scale: flo
 
 
 def checkpointed_step(model: Mmdit, adapters: LoraAdapters, batch, loss_scale: float = 1.0,
-                      keep_attention: bool = True) -> float:
+                      keep_attention: bool = False) -> float:
     """One block-checkpointed step (``block_ckpt.rs:103-207``): capture, head
-    graph, reverse per-block replay. Returns the unscaled loss; adapter
-    gradients accumulate on the deltas' ``.grad`` (scaled by ``loss_scale``).
-    ``keep_attention`` keeps each block's attention output and log-sum-exp
-    from the capture for its replay (``keep_attention=False`` replays the
-    whole block, as the reference does)."""
+    graph, reverse per-block replay of the whole block, as the reference
+    does. Returns the unscaled loss; adapter gradients accumulate on the
+    deltas' ``.grad`` (scaled by ``loss_scale``). ``keep_attention=True``
+    instead keeps each block's attention output and log-sum-exp from the
+    capture for its replay (memory for time: the replay skips the attention
+    forward; the gradients are the same)."""
     with adapters.cached_factors():  # the factors stay fixed through capture and replay
         return _checkpointed_step(model, adapters, batch, loss_scale, keep_attention)
 
