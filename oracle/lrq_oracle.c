@@ -29,10 +29,14 @@
  *   linear fwd/bwd: quant golden y (1e-5), lora_toy.json (20 SGD steps), and
  *     finite-difference gradients on tiny shapes.
  *
+ *   cpu_baseline dequant (lrq_o_cpu_dequant_int4 / _int8): bit-identical to
+ *     dequant_int4 / dequant_q above (test_cpu_baseline_*_matches_oracle).
+ *
  * Numbers: f32 storage, f64 accumulation for the parity oracle; the
- * cpu_baseline dequant (lrq_o_cpu_dequant_int4) follows the reference's own
- * CPU algorithm: materialize the f32 dequantized weight, then f32 GEMMs
- * (those run in numpy's cache-blocked SGEMM; oracle/__init__.py).
+ * cpu_baseline dequant (lrq_o_cpu_dequant_int4, lrq_o_cpu_dequant_int8)
+ * follows the reference's own CPU algorithm: materialize the f32
+ * dequantized weight, then f32 GEMMs (those run in numpy's cache-blocked
+ * SGEMM; oracle/__init__.py).
  */
 #include <math.h>
 #include <stdint.h>

@@ -274,6 +274,7 @@ def test_cpu_baseline_step_matches_oracle():
     st = O.CpuStepInt4(p, s, g, X, A, B, 1.0, dY)
     st.run()
     wdq = O.dequant_int4(p, s, K, g)
+    assert np.array_equal(st.Wdq.view(np.uint32), wdq.view(np.uint32))  # the per-pass dequant, bit for bit
     Y, T = O.linear_fwd(X, wdq, A, B, 1.0)
     dX, dA, dB = O.linear_bwd(X, wdq, A, B, 1.0, dY)
     for got, ref in ((st.Y, Y), (st.dX, dX), (st.dA, dA), (st.dB, dB), (st.T, T)):
