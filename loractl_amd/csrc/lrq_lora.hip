@@ -506,7 +506,8 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 }  // namespace
 
 // nt: 128-token tiles x column slices (multiples of 32) so that the grid is
-// up to ~256 workgroups (one per CU, 8 wavefronts each), in at most 8 slices:
+// up to ~256 workgroups (one per CU, 8 wavefronts each), in at most 8 slices
+// (more for very few tokens, below):
 // each slice costs the finishing wavefronts a load, and short slices stream
 // too little to hide their staging (3072 -> 3072 at M = 1024: t 17.8 -> 11.4
 // us and u 16.7 -> 11.1 us going from 32 slices to 8; 16 gave 12.6 and 12.3);
@@ -521,7 +522,13 @@ LoraPlan lora_plan_nt(int64_t M, int64_t C, int rp) {
   // wavefronts (u 24.8 -> 23.8 us)
   p.lw = cdiv(M > 0 ? M : 1, 128) * 8 < 256 ? 4 : 8;
   const int64_t tiles = cdiv(M > 0 ? M : 1, 16 * p.lw);
-  const int64_t want = std::min<int64_t>(8, cdiv(256, tiles));
+  // slices: at most 8, but 32 for one or two token tiles and 16 for up to
+  // four, where 8 slices leave most CUs idle (u = s dy B^T, us, 8 / 16 /
+  // 32 / 64 slices: M = 1, 18432 columns 28.2 / 18.2 / 13.5 / 15.3; M = 64,
+  // 9216 columns 26.2 / 17.0 / 13.0 / 15.0; M = 256, 9728 columns t + u
+  // 25.5 / 24.0 / 28.5 / 38.7)
+  const int64_t cap = tiles <= 2 ? 32 : (tiles <= 4 ? 16 : 8);
+  const int64_t want = std::min<int64_t>(cap, cdiv(256, tiles));
   int64_t per = 32 * cdiv(cdiv(C, want), 32);
   if (per < 32) per = 32;
   p.per = per;
