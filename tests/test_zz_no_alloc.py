@@ -18,7 +18,8 @@ pytestmark = pytest.mark.gpu
 def _case(cuda, M, K, N, r, fmt, seed):
     w, x, a, b, _ = case_inputs(M, K, N, r, seed=seed)
     wt = torch.from_numpy(w).to(cuda)
-    wq = D.quantize_int4(wt, 64) if fmt == "int4" else D.quantize_fp8(wt, True)
+    wq = {"int4": lambda: D.quantize_int4(wt, 64), "int8": lambda: D.quantize_int8(wt, 64),
+          "fp8": lambda: D.quantize_fp8(wt, True)}[fmt]()
     wq = D.compute_weight(wq)
     return wq, to_dev(x, cuda), to_dev(a[:, :r], cuda), to_dev(b[:r], cuda)
 
@@ -33,7 +34,7 @@ def _both(cuda, wq, xb, ab, bb, s):
     return (y0, t0), (y1, t1)
 
 
-@pytest.mark.parametrize("fmt", ["int4", "fp8"])
+@pytest.mark.parametrize("fmt", ["int4", "fp8", "int8"])
 def test_noalloc_matches_lora_fwd_twice(cuda, fmt):
     """Two calls in a row, the second smaller, through each path (large-m
     GEMM with the LoRA side kernels; few-token stream), each bit-identical
