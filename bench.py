@@ -605,8 +605,8 @@ class LinearSet:
         return {"fwd_main": f, "bwd_dx": b}
 
     def bytes(self, group=64):
-        """Algorithmic HBM bytes per step (SURVEY 8(d) model): packed weight,
-        activations and factors, forward plus backward."""
+        """Algorithmic HBM bytes per step: packed int4 weight and its group
+        scales, activations and factors, forward plus backward."""
         tot = 0.0
         for (M, K, N, r, *_r) in self.sites:
             wb = N * K / 2 + 4 * N * K / group
