@@ -43,6 +43,7 @@ pub mod ffi {
     pub const LRQ_LAYOUT_BLOCKED: i32 = 1;
 
     pub const LRQ_NOALLOC_SCRATCH_BYTES: u32 = 32 << 20;
+    pub const LRQ_MAX_LORA_TOKENS: i64 = 259456;
 
     /// Opaque context (a device, a stream, a workspace).
     #[repr(C)]
@@ -190,6 +191,7 @@ pub mod ffi {
             total_ms: *mut f64,
             launches: *mut i64,
         ) -> c_int;
+        pub fn lrq_debug_force_wait_timeout(on: c_int) -> c_int;
     }
 }
 

@@ -31,7 +31,11 @@
  *     be used concurrently. Hot calls allocate only when the context's
  *     workspace must grow (pre-size it with lrq_reserve); while the stream
  *     is being captured into a graph they return LRQ_EINVAL instead of
- *     growing it.
+ *     growing it. Once a call has been captured on a context, a later
+ *     growth (lrq_reserve or a hot call with a larger shape) keeps the old
+ *     workspace allocated until lrq_destroy, so graphs captured earlier
+ *     stay valid; replays of one graph, and eager calls on the same
+ *     context, are ordered by the stream like any other calls.
  *
  * Weight layouts (file layout [d_out = n, d_in = k], as QuantLinear keeps it,
  * src/mmdit.rs:413-444):
@@ -105,8 +109,20 @@ int lrq_destroy(lrq_ctx* ctx);
 
 /* Run subsequent calls on `stream` (a hipStream_t; NULL is the null stream). */
 int lrq_set_stream(lrq_ctx* ctx, void* stream);
+
+/* Wait for the context's stream, then report a failure the few-token
+ * kernels (m <= 16) flagged on the device: an epilogue whose bounded wait
+ * for t (u) ran out, which also writes NaN to the outputs it owns. A
+ * reported failure returns LRQ_EHIP once; the call then waits for the whole
+ * device, clears the flag and resets the arrival counters (the context's
+ * and the device's no-alloc scratch), so later calls start clean. */
 int lrq_sync(lrq_ctx* ctx);
 const char* lrq_last_error(const lrq_ctx* ctx);
+
+/* Tokens per call of the LoRA calls (lrq_lora_fwd, lrq_lora_bwd) for m > 16:
+ * the t and u kernels keep one arrival counter per 16 tokens. A larger m
+ * returns LRQ_EUNSUPPORTED; split the batch. */
+#define LRQ_MAX_LORA_TOKENS 259456
 
 /* Pre-size the workspace for calls with up to m tokens, n outputs, k inputs
  * and rank r, so that later hot calls do not allocate. */
@@ -215,6 +231,14 @@ int lrq_profile_reset(lrq_ctx* ctx);
 int lrq_profile_count(void);
 const char* lrq_profile_name(int kid);
 int lrq_profile_read(lrq_ctx* ctx, int kid, double* total_ms, int64_t* launches);
+
+/* Test hook, no counterpart in the reference: with on != 0, later
+ * few-token launches (in this process) give their epilogues' bounded wait
+ * for t a stamp that is never published and a cap of 16 polls, so every
+ * such epilogue gives up, as a lost t would make it: the kernels still end,
+ * the outputs are NaN and lrq_sync reports the flag. on = 0 restores the
+ * normal wait. For tests of the failure path only. */
+int lrq_debug_force_wait_timeout(int on);
 
 #ifdef __cplusplus
 }

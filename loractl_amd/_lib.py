@@ -22,6 +22,7 @@ LRQ_FMT_FP8 = 2
 LRQ_FMT_INT8 = 3
 LRQ_LAYOUT_ROWS = 0
 LRQ_LAYOUT_BLOCKED = 1
+LRQ_MAX_LORA_TOKENS = 259456  # include/loractl_rocm.h: tokens per LoRA call (m > 16)
 LRQ_NOALLOC_SCRATCH_BYTES = 32 << 20
 
 _ERRNAMES = {
@@ -87,6 +88,7 @@ SIGNATURES = {
     "lrq_profile_count": (_i32, []),
     "lrq_profile_name": (ctypes.c_char_p, [_i32]),
     "lrq_profile_read": (_i32, [_vp, _i32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i64)]),
+    "lrq_debug_force_wait_timeout": (_i32, [_i32]),
 }
 
 _lib = None

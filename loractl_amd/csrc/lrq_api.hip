@@ -23,6 +23,11 @@ struct lrq_ctx {
   uint32_t* cnt = nullptr;    // LRQ_CNT_WORDS arrival counters of the few-token kernels
   char* ws = nullptr;         // ws_alloc + LRQ_CNT_BYTES
   size_t ws_bytes = 0;
+  // set once a call has run while the stream was being captured: from then
+  // on a growing workspace keeps the old allocations (a captured graph may
+  // still point at them) until lrq_destroy
+  bool captured = false;
+  std::vector<char*> retired;
   char err[512] = {0};
   bool prof = false;
   struct Rec {
@@ -158,7 +163,14 @@ int ensure_ws(lrq_ctx* c, size_t bytes) {
   // stream-ordered users of the old buffer must finish before it goes
   e = hipStreamSynchronize(c->stream);
   if (e != hipSuccess) return hip_fail(c, e, "hipStreamSynchronize");
-  if (c->ws_alloc) (void)hipFree(c->ws_alloc);
+  if (c->ws_alloc) {
+    // a graph captured on this context may still replay kernels that read
+    // and write the old allocation: keep it until lrq_destroy
+    if (c->captured)
+      c->retired.push_back(c->ws_alloc);
+    else
+      (void)hipFree(c->ws_alloc);
+  }
   c->ws_alloc = c->ws = nullptr;
   c->cnt = nullptr;
   c->ws_bytes = 0;
@@ -222,6 +234,12 @@ int check_lora_shapes(lrq_ctx* c, int64_t m, int64_t n, int64_t k, int rp) {
   if (span >= (int64_t)1 << 31)
     return fail(c, LRQ_EUNSUPPORTED, "LoRA shape m=%lld n=%lld k=%lld exceeds 2 GiB per slice",
                 (long long)m, (long long)n, (long long)k);
+  // t and u keep one arrival counter per 16 tokens in the counter area
+  if (m > LRQ_MAX_LORA_TOKENS)
+    return fail(c, LRQ_EUNSUPPORTED,
+                "LoRA call with m=%lld tokens: the t and u kernels take at most %lld tokens per call (split the "
+                "batch)",
+                (long long)m, (long long)LRQ_MAX_LORA_TOKENS);
   return LRQ_OK;
 }
 
@@ -259,6 +277,17 @@ int begin(lrq_ctx* c) {
   c->err[0] = 0;
   hipError_t e = hipSetDevice(c->device);
   if (e != hipSuccess) return hip_fail(c, e, "hipSetDevice");
+  return LRQ_OK;
+}
+
+// Note whether the context's stream is being captured (the hot calls ask
+// once per call): a captured graph keeps the workspace's address.
+int note_capture(lrq_ctx* c) {
+  if (c->captured) return LRQ_OK;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  const hipError_t e = hipStreamIsCapturing(c->stream, &cap);
+  if (e != hipSuccess) return hip_fail(c, e, "hipStreamIsCapturing");
+  if (cap != hipStreamCaptureStatusNone) c->captured = true;
   return LRQ_OK;
 }
 
@@ -308,6 +337,7 @@ int lrq_destroy(lrq_ctx* c) {
   }
   for (auto e : c->pool) (void)hipEventDestroy(e);
   if (c->ws_alloc) (void)hipFree(c->ws_alloc);
+  for (char* p : c->retired) (void)hipFree(p);
   delete c;
   return LRQ_OK;
 }
@@ -315,6 +345,23 @@ int lrq_destroy(lrq_ctx* c) {
 int lrq_set_stream(lrq_ctx* c, void* stream) {
   LRQ_TRY(begin(c));
   c->stream = reinterpret_cast<hipStream_t>(stream);  // NULL: the device's null stream
+  return LRQ_OK;
+}
+
+// Reset a counter area after a reported failure, with no kernel running on
+// the device: every counter and the flag to zero, the epoch moved past every
+// stamp already published (a late t slice of the failed launch may have
+// stamped its publication with the epoch of that time), so no stale entry
+// matches the next launch's stamp.
+static int reset_counters(lrq_ctx* c, uint32_t* cnt) {
+  uint32_t ep = 0;
+  hipError_t e = hipMemcpy(&ep, cnt + SK_EPOCH, sizeof(ep), hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return hip_fail(c, e, "hipMemcpy");
+  e = hipMemset(cnt, 0, LRQ_CNT_BYTES);
+  if (e != hipSuccess) return hip_fail(c, e, "hipMemset");
+  ep += 2;
+  e = hipMemcpy(cnt + SK_EPOCH, &ep, sizeof(ep), hipMemcpyHostToDevice);
+  if (e != hipSuccess) return hip_fail(c, e, "hipMemcpy");
   return LRQ_OK;
 }
 
@@ -329,14 +376,29 @@ int lrq_sync(lrq_ctx* c) {
     std::lock_guard<std::mutex> lk(g_scratch_mu);
     scratch = g_scratch[c->device];
   }
-  const uint32_t* counters[2] = {c->cnt, reinterpret_cast<const uint32_t*>(scratch)};
-  for (const uint32_t* cnt : counters) {
+  uint32_t* counters[2] = {c->cnt, reinterpret_cast<uint32_t*>(scratch)};
+  bool failed = false;
+  for (uint32_t* cnt : counters) {
     if (!cnt) continue;
     uint32_t flag = 0;
     e = hipMemcpy(&flag, cnt + SK_FAIL, sizeof(flag), hipMemcpyDeviceToHost);
     if (e != hipSuccess) return hip_fail(c, e, "hipMemcpy");
-    if (flag) return fail(c, LRQ_EHIP, "a few-token kernel timed out waiting for its t slices; its outputs are invalid");
+    failed = failed || flag != 0;
   }
+  if (!failed) return LRQ_OK;
+  // the late workgroups of the failed launch, and any other stream's use of
+  // the scratch array, end before the counters are rewritten
+  e = hipDeviceSynchronize();
+  if (e != hipSuccess) return hip_fail(c, e, "hipDeviceSynchronize");
+  for (uint32_t* cnt : counters)
+    if (cnt) LRQ_TRY(reset_counters(c, cnt));
+  return fail(c, LRQ_EHIP,
+              "a few-token kernel gave up waiting for its t (u) slices: the outputs it wrote are NaN; the flag "
+              "is cleared and the counters reset");
+}
+
+int lrq_debug_force_wait_timeout(int on) {
+  set_force_wait_timeout(on != 0);
   return LRQ_OK;
 }
 
@@ -532,6 +594,7 @@ static int acquire_ws(lrq_ctx* c, WsSource* src, size_t bytes, char** out, uint3
 static int fwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t m, const uint16_t* a,
                     const uint16_t* b, int64_t r, float scaling, uint16_t* y, uint16_t* t_out, WsSource* src) {
   LRQ_TRY(begin(c));
+  LRQ_TRY(note_capture(c));
   LRQ_TRY(check_gemm(c, w, m));
   if (!aligned16(x) || !aligned16(y)) return fail(c, LRQ_EINVAL, "x and y must be 16-byte aligned");
   const bool lora = a != nullptr && b != nullptr && r > 0;
@@ -646,6 +709,7 @@ static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const ui
                     const uint16_t* a, const uint16_t* b, int64_t r, float scaling, const uint16_t* t,
                     uint16_t* dx, float* da, float* db) {
   LRQ_TRY(begin(c));
+  LRQ_TRY(note_capture(c));
   LRQ_TRY(check_gemm(c, w, m));
   if (!aligned16(dy)) return fail(c, LRQ_EINVAL, "dy must be 16-byte aligned");
   if (dx && !aligned16(dx)) return fail(c, LRQ_EINVAL, "dx must be 16-byte aligned");

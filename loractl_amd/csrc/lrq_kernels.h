@@ -91,7 +91,12 @@ constexpr size_t LRQ_CNT_BYTES = (size_t)LRQ_CNT_WORDS * 4;
 constexpr int64_t SK_MAX_NB = LRQ_CNT_WORDS - 160;
 constexpr int64_t SK_TCNT = LRQ_CNT_WORDS - 128, SK_EPOCH = LRQ_CNT_WORDS - 96, SK_DCNT = LRQ_CNT_WORDS - 64,
                   SK_FAIL = LRQ_CNT_WORDS - 32;
+static_assert(LRQ_MAX_LORA_TOKENS <= (SK_MAX_NB - 8) * 16,
+              "the t and u kernels keep one arrival counter per 16 tokens");
 SkinnyPlan skinny_plan(int64_t n, int64_t k, int rp, int num_cus);
+// test hook (lrq_debug_force_wait_timeout): later launches wait for a stamp
+// that is never published, 16 polls at most
+void set_force_wait_timeout(bool on);
 size_t skinny_ws_bytes(const SkinnyPlan& p, int64_t m, int64_t n, int rp);
 hipError_t launch_skinny(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, const uint16_t* A,
                          const SkinnyPlan& p, float* part, float* tpart, uint32_t* cnt, float scaling,

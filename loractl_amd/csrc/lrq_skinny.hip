@@ -71,6 +71,8 @@ struct SkArgs {
   uint32_t* cnt;      // [ceil(n / 64)] arrival counters, zero on entry and exit
   float scaling;
   uint16_t* t_out;    // t [m, r] (backward: u [m, rp]), or null
+  uint32_t max_polls; // cap of an epilogue's polls for t (SK_MAX_POLLS)
+  uint32_t skew;      // added to the awaited stamp: 0 (a test hook sets it to force the timeout)
 };
 
 // device-scope accesses of the cross-workgroup data: stores written through
@@ -88,6 +90,9 @@ LRQ_DEV u32x2 bload8_dev(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_b
 LRQ_DEV uint32_t stamp(uint32_t ep) { return ep + 1 == 0 ? 1u : ep + 1; }
 
 constexpr uint32_t SK_MAX_POLLS = 1u << 22;  // about 0.2 s of s_sleep 2
+// what an epilogue takes for t after its wait ran out: NaN as an f32 and as
+// both bf16 halves, so the outputs it writes are NaN, not stale
+constexpr uint32_t SK_NAN2 = 0x7fc07fc0u;
 
 LRQ_DEV uint32_t add_dev(uint32_t* c) { return __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, XSCOPE); }
 LRQ_DEV void zero_dev(uint32_t* c) { __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, XSCOPE); }
@@ -141,15 +146,17 @@ LRQ_DEV void sk_epilogue(const SkArgs& sa, int64_t nb, float* lds) {
   };
   load_t();
   if (TS > 0) {
-    const uint32_t want = stamp(__hip_atomic_load(sa.cnt + SK_EPOCH, __ATOMIC_RELAXED, XSCOPE));
+    const uint32_t want = stamp(__hip_atomic_load(sa.cnt + SK_EPOCH, __ATOMIC_RELAXED, XSCOPE)) + sa.skew;
     // not all published yet: read all of this thread's entries again
     for (uint32_t polls = 0;; ++polls) {
       bool ok = true;
 #pragma unroll
       for (int q = 0; q < 4; ++q) ok = ok && (tid + q * SK_NT >= 16 * rp || tv[q][1] == want);
       if (ok) break;
-      if (polls == SK_MAX_POLLS) {
+      if (polls == sa.max_polls) {
         __hip_atomic_store(sa.cnt + SK_FAIL, 1u, __ATOMIC_RELAXED, XSCOPE);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) tv[q][0] = SK_NAN2;
         break;
       }
       __builtin_amdgcn_s_sleep(2);
@@ -726,7 +733,7 @@ __global__ void __launch_bounds__(NT) k_skf(SkArgs sa) {
     // rank-wide matrix-core step per row tile, while the others still
     // stream: t in the A role (lane (c16, kq): t[c16][32 ks + 8 kq ..]) as
     // published, every entry stamped with the launch's epoch
-    const uint32_t want = stamp(__hip_atomic_load(sa.cnt + SK_EPOCH, __ATOMIC_RELAXED, XSCOPE));
+    const uint32_t want = stamp(__hip_atomic_load(sa.cnt + SK_EPOCH, __ATOMIC_RELAXED, XSCOPE)) + sa.skew;
     const rsrc_t rtf = make_rsrc(sa.tpart + (int64_t)TS * 16 * rp, clamp_bytes((int64_t)16 * rp * 8));
     u32x2 tv[2][8];
     auto load_t = [&]() {
@@ -746,8 +753,12 @@ __global__ void __launch_bounds__(NT) k_skf(SkArgs sa) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) ok = ok && (32 * ks + 8 * kq + e >= rp || tv[ks][e][1] == want);
       if (__all(ok)) break;
-      if (polls == SK_MAX_POLLS) {
+      if (polls == sa.max_polls) {
         __hip_atomic_store(sa.cnt + SK_FAIL, 1u, __ATOMIC_RELAXED, XSCOPE);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) tv[ks][e][0] = SK_NAN2;
         break;
       }
       __builtin_amdgcn_s_sleep(2);
@@ -798,6 +809,9 @@ __global__ void __launch_bounds__(NT) k_skf(SkArgs sa) {
 
 }  // namespace
 
+bool g_force_wait_timeout = false;
+void set_force_wait_timeout(bool on) { g_force_wait_timeout = on; }
+
 SkinnyPlan skinny_plan(int64_t n, int64_t k, int rp, int num_cus) {
   SkinnyPlan p{};
   const int64_t KB = (k + 63) / 64, NB = (n + 63) / 64;
@@ -846,7 +860,11 @@ hipError_t launch_skinny(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, c
   const int64_t NB = (a.e + 63) / 64;
   if (a.m <= 0 || a.m > 16 || p.S < 1 || p.KS < 1 || p.KS > SK_MAXKS || !cnt || NB > SK_MAX_NB)
     return hipErrorInvalidValue;
-  SkArgs sa{a, A, p, part, tpart, cnt, scaling, t_out};
+  SkArgs sa{a, A, p, part, tpart, cnt, scaling, t_out, SK_MAX_POLLS, 0u};
+  if (g_force_wait_timeout) {
+    sa.max_polls = 16;
+    sa.skew = 0x40000000u;  // a stamp no launch publishes
+  }
   if (a.rp == 0 || !A) sa.p.TS = 0;
   // 32-wide steps per wavefront of a t slice (skinny_plan; 0 without t)
   const int steps = (int)(p.KT / 128);

@@ -356,6 +356,21 @@ def profile_read(device: Optional[int] = None) -> dict:
     return out
 
 
+def sync(device: Optional[int] = None):
+    """Wait for torch's current stream and raise ``LrqError`` if a few-token
+    kernel flagged a failure on the device since the last check (an
+    epilogue whose bounded wait for t or u ran out; it wrote NaN outputs).
+    The library clears the flag and resets its counters when it reports it.
+    A training step calls this once, after reading its loss."""
+    context(device).call("lrq_sync")
+
+
+def debug_force_wait_timeout(on: bool):
+    """Test hook: make later few-token launches give up their wait for t
+    (the failure path ``sync`` reports). Never on in a real run."""
+    L.load().lrq_debug_force_wait_timeout(int(on))
+
+
 def reserve(m: int, n: int, k: int, r: int, device: Optional[int] = None):
     ctx = context(device)
     ctx.call("lrq_reserve", m, n, k, r)

@@ -79,7 +79,9 @@ def export_adapters(adapters: LoraAdapters, path: str, metadata: Optional[Dict[s
     header = None
     if metadata:
         ss = {k: str(v) for k, v in metadata.items() if k.startswith("ss_")}
-        model_hash, legacy_hash = sd_webui_hashes(save(out, metadata=ss or None))
+        # an empty ss_* subset still serializes an (empty) metadata map, as the
+        # reference passes Some(map) to the serializer (src/export.rs:330-336)
+        model_hash, legacy_hash = sd_webui_hashes(save(out, metadata=ss))
         header = {k: str(v) for k, v in metadata.items()}
         header["sshs_model_hash"] = model_hash
         header["sshs_legacy_hash"] = legacy_hash

@@ -196,56 +196,75 @@ def load_quant_checkpoint(path: str, device: Union[str, torch.device], base_path
     for a plain (bf16/f32/f16) or scaled-fp8 safetensors checkpoint, on the
     device: for each frozen-base site in ``base_paths`` (in order), its
     ``<path>.weight`` (file layout ``[d_out, d_in]``) is read, moved to the
-    device, widened to f32 and quantized at ``value`` (a ``QuantValue``:
-    Q4S int4 by default, or Q8S int8) as the row chunks
-    ``dequant_chunk_rows`` prescribes, one tensor at a time; the f32 copy is
-    dropped before the next site. fp8 checkpoints (detected from the header)
-    go through ``load_fp8_checkpoint``'s device requantization instead, with
-    no f32 copy. A site whose weight is not block-aligned (``fused_aligned``)
+    device and quantized at ``value`` (a ``QuantValue``: Q4S int4 by default,
+    or Q8S int8) as the row chunks ``dequant_chunk_rows`` prescribes, one
+    tensor at a time. A plain weight is widened to f32 first (one f32 copy of
+    one chunk's rows at a time). An fp8 weight is quantized from its f32
+    values ``LUT[byte] * scale`` (src/fp8.rs:306-318): at Q4S straight from
+    the bytes by ``lrq_requantize_fp8_int4`` (no f32 copy), at Q8S through
+    the device's f32 decode of the chunk. A base site that an fp8 file
+    stores in another float dtype is quantized from its f32 values like a
+    plain one. A site whose weight is not block-aligned (``fused_aligned``)
     is left plain: its weight stays in the returned rest, as the reference
     leaves it to the applier. A site missing from the checkpoint raises.
 
+    Everything else goes to the rest as the reference's snapshots give it to
+    the applier (src/diffusion_trainer.rs:1106-1112, :1141-1170): fp8
+    tensors that are not base sites as their f32 values, other tensors with
+    their dtype; dropped fp8 keys are absent.
+
     Returns ``(quantized, rest, report)``: ``{path: QuantLinear}`` (with the
     site's ``<path>.bias`` as its bias when present), every other tensor by
-    key (dropped fp8 keys absent), and the accounting."""
+    key, and the accounting."""
     from safetensors import safe_open
 
     from .adapters import QuantLinear
-    from .quant import QuantValue, quantize_linear_weight_chunked
+    from .quant import QuantValue, dequant_chunk_rows, quantize_linear_weight_chunked
 
     device = torch.device(device)
     value = QuantValue.Q4S if value is None else value
     report = QuantLoadReport()
     quantized = {}
-    fp8 = is_fp8_checkpoint(path)
-    if fp8:
-        rest = load_fp8_checkpoint(path, device, quant="int8" if value is QuantValue.Q8S else "int4", group=group)
-        keys = set(rest)
-    else:
-        keys = set(_header(path))
-        rest = {}
+    ck = classify_fp8_checkpoint(path) if is_fp8_checkpoint(path) else None
+    keys = (set(ck.fp8) | set(ck.plain)) if ck is not None else set(_header(path))
+    rest = {}
     with safe_open(path, framework="pt") as f:
+
+        def fp8_values(key: str) -> torch.Tensor:
+            """The f32 snapshot of an fp8 tensor: LUT[byte] * scale."""
+            data = f.get_tensor(key).view(torch.uint8).to(device)
+            scale = f.get_tensor(f"{key}_scale").to(device)
+            vals = data.view(torch.float8_e4m3fn).float()
+            if ck.fp8[key]:
+                return vals * scale.reshape(-1, *([1] * (vals.dim() - 1)))
+            return vals * scale.reshape(())
+
         for p in base_paths:
             wkey = f"{p}.weight"
             if wkey not in keys:
                 raise ValueError(f"quantized base site {p} has no {wkey} in the checkpoint {path}")
-            if fp8:
-                w = rest[wkey]
-                if not isinstance(w, D.PackedWeight):  # left plain (unaligned)
-                    report.left_plain += 1
-                    report.plain_sites.append(p)
-                    continue
-                del rest[wkey]
-                chunks = [w]
+            shape = f.get_slice(wkey).get_shape()
+            if len(shape) != 2 or not fused_aligned(shape[0], shape[1]):
+                report.left_plain += 1
+                report.plain_sites.append(p)
+                continue
+            _check_group(wkey, shape[1], group)
+            if ck is not None and wkey in ck.fp8:
+                data = f.get_tensor(wkey).view(torch.uint8).to(device)
+                scale = f.get_tensor(f"{wkey}_scale").to(device).reshape(-1)
+                per_channel = ck.fp8[wkey]
+                chunks, start = [], 0
+                for rows in dequant_chunk_rows(shape[0], shape[1], chunk_bytes):
+                    w8 = F.fp8_weight(wkey, data[start:start + rows],
+                                      scale[start:start + rows] if per_channel else scale)
+                    if value is QuantValue.Q8S:
+                        chunks.append(D.quantize_int8(D.dequant(w8), group))
+                    else:
+                        chunks.append(D.requantize_fp8_int4(w8, group))
+                    start += rows
+                del data, scale
             else:
-                t = f.get_tensor(wkey)
-                if t.dim() != 2 or not fused_aligned(t.shape[0], t.shape[1]):
-                    report.left_plain += 1
-                    report.plain_sites.append(p)
-                    continue
-                _check_group(wkey, t.shape[1], group)
-                w32 = t.to(device).float()
-                del t
+                w32 = f.get_tensor(wkey).to(device).float()
                 chunks = quantize_linear_weight_chunked(w32, value, chunk_bytes, group)
                 del w32
             if len(chunks) > 1:
@@ -254,12 +273,11 @@ def load_quant_checkpoint(path: str, device: Union[str, torch.device], base_path
             bkey = f"{p}.bias"
             bias = None
             if bkey in keys:
-                bias = rest.pop(bkey) if fp8 else f.get_tensor(bkey).to(device)
+                bias = fp8_values(bkey) if (ck is not None and bkey in ck.fp8) else f.get_tensor(bkey).to(device)
                 bias = bias.float()
             quantized[p] = QuantLinear(chunks, bias)
             report.quantized += 1
-        if not fp8:
-            taken = {f"{p}.weight" for p in quantized} | {f"{p}.bias" for p in quantized}
-            for k in sorted(keys - taken):
-                rest[k] = f.get_tensor(k).to(device)
+        taken = {f"{p}.weight" for p in quantized} | {f"{p}.bias" for p in quantized}
+        for k in sorted(keys - taken):
+            rest[k] = fp8_values(k) if (ck is not None and k in ck.fp8) else f.get_tensor(k).to(device)
     return quantized, rest, report

@@ -293,7 +293,9 @@ def monolithic_step(model: Mmdit, adapters: LoraAdapters, batch, loss_scale: flo
     img, txt, t, target = batch
     loss = flow_loss(model.forward(img, txt, t, adapters), target)
     (loss * loss_scale).backward()
-    return float(loss.item())
+    value = float(loss.item())
+    D.sync()  # a few-token kernel's device-side failure flag, once per step
+    return value
 
 
 def checkpointed_step(model: Mmdit, adapters: LoraAdapters, batch, loss_scale: float = 1.0,
@@ -330,7 +332,9 @@ def _checkpointed_step(model: Mmdit, adapters: LoraAdapters, batch, loss_scale: 
         cap.block_inputs[i] = None  # this block's inputs are done
         if keep_attention:
             cap.attention[i] = None
-    return float(loss.item())
+    value = float(loss.item())
+    D.sync()  # a few-token kernel's device-side failure flag, once per step
+    return value
 
 
 def mmdit_step_flops(cfg: MmditConfig, img_tokens: int, txt_tokens: int, batch: int = 1,

@@ -176,3 +176,28 @@ def test_rank_change_is_a_shape_mismatch(tmp_path):
     export_adapters(_set(rank=4), p)
     with pytest.raises(ValueError, match="did lora.rank change"):
         import_adapters(_set(rank=8, alpha=16.0), p)
+
+
+def test_legacy_hash_without_ss_metadata(tmp_path):
+    """Metadata with no ss_* key still hashes a serialization that carries a
+    metadata map, an empty one: the reference hands the serializer
+    Some(map) whenever metadata is given (src/export.rs:330-336), which
+    writes '"__metadata__":{}' into the header. Above 1 MiB that header
+    length moves the 64 KiB the legacy hash reads, so it differs from the
+    hash of a buffer without the map."""
+    torch.manual_seed(5)
+    big = LoraAdapters([LoraDelta(4096, 4096, 64, 64.0)], ["blocks.0.attn.wq"])
+    with torch.no_grad():
+        big.deltas[0].lora_b.normal_()
+    p = str(tmp_path / "nometa.safetensors")
+    export_adapters(big, p, {"modelspec.title": "z"})
+    with_map = save(kohya_tensors(big), metadata={})
+    without = save(kohya_tensors(big), metadata=None)
+    n = struct.unpack("<Q", with_map[:8])[0]
+    assert b'"__metadata__":{}' in with_map[8:8 + n]
+    assert len(with_map) > 0x110000
+    with safe_open(p, framework="pt") as f:
+        meta = f.metadata()
+    assert meta["sshs_legacy_hash"] == hashlib.sha256(with_map[0x100000:0x110000]).hexdigest()[:8]
+    assert meta["sshs_legacy_hash"] != sd_webui_hashes(without)[1]
+    assert meta["sshs_model_hash"] == hashlib.sha256(_data_region(open(p, "rb").read())).hexdigest()

@@ -1,0 +1,112 @@
+"""Failure handling of the C ABI on the GPU, each condition forced from the
+host so that every kernel still ends normally:
+
+- a few-token epilogue whose bounded wait for t (u) runs out (the test hook
+  makes it wait for a stamp that is never published, 16 polls): the
+  outputs it owns are NaN, lrq_sync reports the flag once, then clears it
+  and resets the counters, and the next calls are exact again;
+- a LoRA call past LRQ_MAX_LORA_TOKENS is refused before any launch, and
+  one at the limit runs;
+- a workspace that grows after a graph was captured on the context keeps
+  the old allocation: the graph replays bit-identically to the eager call."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from gpu_helpers import case_inputs, check, to_dev
+from loractl_amd import _lib as L
+from loractl_amd import device as D
+
+pytestmark = pytest.mark.gpu
+
+
+def _weight(cuda, w, group=64):
+    return D.compute_weight(D.quantize_int4(torch.from_numpy(w).to(cuda), group))
+
+
+@pytest.mark.parametrize("K,N", [(3072, 12288), (1024, 4096)], ids=["whole-depth", "splits"])
+def test_few_token_wait_timeout_is_reported_and_cleared(cuda, K, N):
+    M, r = 4, 16
+    w, x, a, b, dy = case_inputs(M, K, N, r, seed=7)
+    wq = _weight(cuda, w)
+    xd, ad, bd, dyd = (to_dev(v, cuda) for v in (x, a, b, dy))
+    y0, t0 = D.lora_fwd(xd, wq, ad, bd, 1.0)
+    dx0, da0, db0 = D.lora_bwd(xd, dyd, wq, ad, bd, 1.0, t0)
+    D.sync()
+    D.debug_force_wait_timeout(True)
+    try:
+        print(f"forced timeout K={K} N={N}: forward", flush=True)
+        y1, _ = D.lora_fwd(xd, wq, ad, bd, 1.0)
+        print(f"forced timeout K={K} N={N}: backward", flush=True)
+        dx1, _, _ = D.lora_bwd(xd, dyd, wq, ad, bd, 1.0, t0)
+    finally:
+        D.debug_force_wait_timeout(False)
+    with pytest.raises(L.LrqError, match="gave up waiting"):
+        D.sync()
+    assert bool(torch.isnan(y1.float()).all()) and bool(torch.isnan(dx1.float()).all())
+    D.sync()  # reported once: the flag is clear
+    # the counters were reset: the same calls are bit-identical to the first
+    y2, t2 = D.lora_fwd(xd, wq, ad, bd, 1.0)
+    dx2, da2, db2 = D.lora_bwd(xd, dyd, wq, ad, bd, 1.0, t2)
+    D.sync()
+    for first, again in ((y0, y2), (t0, t2), (dx0, dx2), (da0, da2), (db0, db2)):
+        assert torch.equal(first, again)
+
+
+def test_lora_token_limit(cuda):
+    K, N, r = 64, 64, 4
+    rng = np.random.Generator(np.random.PCG64(3))
+    wq = _weight(cuda, (rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    a = to_dev(rng.uniform(-0.1, 0.1, (K, r)).astype(np.float32), cuda)
+    b = to_dev((rng.standard_normal((r, N)) * 0.01).astype(np.float32), cuda)
+    lim = L.LRQ_MAX_LORA_TOKENS
+    x = torch.randn(lim + 16, K, device=cuda).to(torch.bfloat16)
+    with pytest.raises(L.LrqError, match="at most 259456 tokens"):
+        D.lora_fwd(x, wq, a, b, 1.0)
+    with pytest.raises(L.LrqError, match="at most 259456 tokens"):
+        D.lora_bwd(x, x, wq, a, b, 1.0, torch.zeros(lim + 16, r, device=cuda, dtype=torch.bfloat16))
+    xl = x[:lim].contiguous()
+    y, t = D.lora_fwd(xl, wq, a, b, 1.0)
+    torch.cuda.synchronize()
+    rows = np.array([0, 1, lim // 2, lim - 2, lim - 1])
+    ri = torch.from_numpy(rows).to(cuda)
+    y_ref, t_ref = O.linear_fwd(xl[ri].float().cpu().numpy(), D.dequant(wq).cpu().numpy(),
+                                a.float().cpu().numpy(), b.float().cpu().numpy(), 1.0)
+    check("y", y[ri], y_ref)
+    check("t", t[ri], t_ref)
+
+
+def test_workspace_growth_keeps_captured_graphs_valid(cuda):
+    M, K, N, r = 300, 1024, 2048, 32
+    w, x, a, b, _ = case_inputs(M, K, N, r, seed=11)
+    wq = _weight(cuda, w)
+    xd, ad, bd = (to_dev(v, cuda) for v in (x, a, b))
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=cuda)
+    t = torch.empty((M, r), dtype=torch.bfloat16, device=cuda)
+    with torch.cuda.stream(stream):
+        D.reserve(M, N, K, r)
+        y_eager, t_eager = D.lora_fwd(xd, wq, ad, bd, 1.0)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            D.lora_fwd(xd, wq, ad, bd, 1.0, y=y, t=t)
+    torch.cuda.synchronize()
+    big = (8192, 12288, 3072, 64)
+    for i in range(3):
+        y.zero_()
+        t.zero_()
+        if i == 1:
+            # the context of the capture stream grows its workspace: the
+            # graph still points at the old one, which must stay allocated
+            with torch.cuda.stream(stream):
+                D.reserve(*big)
+                # eager work in the grown workspace between the replays
+                D.lora_fwd(xd, wq, ad, bd, 1.0)
+            torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, y_eager) and torch.equal(t, t_eager), f"replay {i}"

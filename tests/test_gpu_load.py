@@ -168,6 +168,52 @@ def test_load_quant_checkpoint_plain(cuda, tmp_path):
         assert np.array_equal(q8[p_].dequantized_weight().cpu().numpy(), O.dequant_q(qq, sc, 32)), p_
 
 
+@pytest.mark.parametrize("q8", [False, True], ids=["q4s", "q8s"])
+def test_load_quant_checkpoint_fp8(cuda, tmp_path, q8):
+    """Quantize-on-load for a scaled-fp8 checkpoint (src/diffusion_trainer.rs:1106-1170):
+    only the base sites are quantized, from their f32 values LUT[byte] * scale
+    (an fp8 base) or widened floats (a base the file stores in bf16), in row
+    chunks under the threshold; an fp8 tensor that is not a base site (a
+    modulation linear) and an fp8 bias reach the rest as their f32 values,
+    other tensors keep their dtype, and the sidecars are consumed."""
+    from loractl_amd.load import load_quant_checkpoint
+    from loractl_amd.quant import QuantValue
+
+    b_a, s_a = _fp8_case(96, 128, True, seed=31)     # fp8 base, per-channel scale
+    b_m, s_m = _fp8_case(64, 128, False, seed=32)    # fp8, not a base site
+    b_bias, s_bias = _fp8_case(96, 1, False, seed=33)
+    rng = np.random.Generator(np.random.PCG64(34))
+    w_b = (rng.standard_normal((40, 64)) * 0.02).astype(np.float32)  # base site stored as bf16
+    norm = np.ones(8, np.float32)
+    path = str(tmp_path / "fp8.safetensors")
+    save_file({"s.a.weight": torch.from_numpy(b_a).view(torch.float8_e4m3fn),
+               "s.a.weight_scale": torch.from_numpy(s_a),
+               "s.a.bias": torch.from_numpy(b_bias.reshape(96)).view(torch.float8_e4m3fn),
+               "s.a.bias_scale": torch.from_numpy(s_bias),
+               "mod.weight": torch.from_numpy(b_m).view(torch.float8_e4m3fn),
+               "mod.weight_scale": torch.from_numpy(s_m),
+               "s.b.weight": torch.from_numpy(w_b).to(torch.bfloat16),
+               "norm.scale": torch.from_numpy(norm)}, path)
+    value = QuantValue.Q8S if q8 else QuantValue.Q4S
+    q, rest, rep = load_quant_checkpoint(path, cuda, ["s.a", "s.b"], chunk_bytes=96 * 128 * 4 // 3, value=value)
+    assert (rep.quantized, rep.left_plain, rep.chunked_sites, rep.total_chunks) == (2, 0, 1, 3)
+    assert q["s.a"].chunk_rows == [32, 32, 32]
+    assert sorted(rest) == ["mod.weight", "norm.scale"]
+    assert rest["mod.weight"].dtype == torch.float32
+    assert np.array_equal(rest["mod.weight"].cpu().numpy(), O.fp8_dequant(b_m, s_m))
+    assert rest["norm.scale"].dtype == torch.float32
+    assert np.array_equal(q["s.a"].bias.cpu().numpy(), O.fp8_dequant(b_bias, s_bias).reshape(96))
+    wb32 = torch.from_numpy(w_b).to(torch.bfloat16).float().numpy()
+    for p_, w_ in (("s.a", O.fp8_dequant(b_a, s_a)), ("s.b", wb32)):
+        if q8:
+            qq, sc = O.quantize(w_, 32, 127)
+            ref = O.dequant_q(qq, sc, 32)
+        else:
+            pk, sc = O.quantize_int4_packed(w_, 32)
+            ref = O.dequant_int4(pk, sc, w_.shape[1], 32)
+        assert np.array_equal(q[p_].dequantized_weight().cpu().numpy(), ref), p_
+
+
 def test_quantize_field_orientation(cuda):
     """quantize_field (src/mmdit.rs:1266-1280): a burn-layout [d_in, d_out]
     weight is transposed to file layout, then quantized; the forward equals

@@ -108,6 +108,7 @@ def test_constants_match():
     cvals["LRQ_ABI_VERSION"] = int(re.search(r"#define LRQ_ABI_VERSION (\d+)", h).group(1))
     m = re.search(r"#define LRQ_NOALLOC_SCRATCH_BYTES \((\d+)u << (\d+)\)", h)
     cvals["LRQ_NOALLOC_SCRATCH_BYTES"] = int(m.group(1)) << int(m.group(2))
+    cvals["LRQ_MAX_LORA_TOKENS"] = int(re.search(r"#define LRQ_MAX_LORA_TOKENS (\d+)", h).group(1))
     for name, v in cvals.items():
         rm = re.search(rf"pub const {name}: \w+ = (-?\d+)(?: << (\d+))?;", rs)
         assert rm, f"{name} missing from the Rust binding"
