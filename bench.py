@@ -13,11 +13,26 @@ layer, forward only, HBM-bound): `value` is algorithmic GB/s,
 W_B + 2MK + 2MN + 4r(K+N) bytes per forward, with the packed weight rotated
 over more than 256 MB of distinct copies so the Infinity Cache cannot serve
 it, and the forwards replayed from a HIP graph so host launch overhead is
-not in the timed region. `roofline` is for the dominant kernel, with
-its average launch time taken from HIP events that the library records
-around each of its launches on the launch stream. `cpu_baseline` times the
-reference's CPU algorithm (the oracle's f32 dequant + f32 GEMMs) on a
-bounded token sample of the same layer.
+not in the timed region. `roofline` is for the dominant kernel: its
+algorithmic work per launch over its launch time. That time is the
+kernel's in-step cost: HIP graphs of 10 steps, with and without one more
+launch of the step's own launch of that kernel per step
+(lrq_profile_relaunch, same arguments and outputs), replayed in
+alternation; for the one-launch few-token forward it is the
+graph-replayed forward itself. `kernels_us` holds every kernel of the
+step measured that way, `kernels_us_isolated` each kernel repeated alone
+back to back (a sustained repeat runs a few percent slower under the
+power limit), and `kernels_us_events` the library's per-launch event
+brackets (each adds a few microseconds of markers). `ceiling` holds what the box
+delivers: torch.matmul's bf16 GEMM (hipBLASLt) at the layer's forward
+and input-gradient shapes, and a streaming read of the packed weight.
+`cpu_baseline` times the reference's CPU algorithm (the oracle's f32
+dequant + f32 GEMMs) on a bounded token sample of the same layer.
+
+The default line also carries `c1` (the 3072 -> 3072 r16 layer at
+M=1024, the same measurement) and `c5` (the Qwen3-style decoder's 196
+linears at M=16 and M=256, one step replayed from a HIP graph), and
+`mmdit` (the C4 training step).
 
 `--workload ns8` is the north-star layer over an int8 (Q8S) group-64 base,
 `--workload c2` over a per-channel fp8 base: the same step and metric.
@@ -77,6 +92,7 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-skinny", action="store_true", help="leave the skinny-M sub-object out of the ns line")
     p.add_argument("--no-mmdit", action="store_true", help="leave the MMDiT step sub-object out of the ns line")
+    p.add_argument("--no-extra", action="store_true", help="leave the C1 and C5 sub-objects out of the ns line")
     p.add_argument("--no-mmdit-kept", action="store_true",
                    help="MMDiT step: leave out the second measurement, with the capture's attention output kept "
                         "for the replay")
@@ -165,10 +181,7 @@ def main():
         print(f"bench.py measures one GPU: every box of this build has one MI355X and the path is "
               f"single-device; --gpus {args.gpus} is not supported (run with --gpus 1).", file=sys.stderr)
         sys.exit(2)
-    import numpy as np
     import torch
-
-    from loractl_amd import device as D
 
     torch.cuda.set_device(0)
     dev = torch.device("cuda:0")
@@ -182,7 +195,198 @@ def main():
         return bench_c5(args, dev)
     if args.workload == "mmdit":
         return bench_mmdit(args, dev)
-    M, K, N, r, alpha, fmt, group = WORKLOADS[args.workload]
+    out, ceilings_for = site_measure(args, dev, args.workload, with_cpu=not args.no_cpu_baseline,
+                                     ceilings=args.workload == "ns")
+    if args.workload == "ns" and not args.no_skinny:
+        # the north star's second bar, the few-token forward of the same layer
+        out["skinny"] = skinny_measure(args, dev, with_cpu=not args.no_cpu_baseline)
+        read = out.get("ceiling", {}).get("stream_read_packed_weight")
+        if read:
+            r = out["skinny"]["roofline"]
+            r["measured_ceiling"] = read["gbs"]
+            r["frac_of_measured"] = round(r["achieved"] / read["gbs"], 4)
+    if args.workload == "ns" and not args.no_extra:
+        # the mid-size configurations, timed by the driver too: C1, and C5
+        # at the few-token and mid token counts
+        torch.cuda.empty_cache()
+        out["c1"] = site_measure(args, dev, "c1", with_cpu=False)[0]
+        torch.cuda.empty_cache()
+        out["c5"] = c5_measure(args, dev, (16, 256), with_cpu=False)
+    if args.workload == "ns" and not args.no_mmdit:
+        # the metric's second half: MMDiT train steps/s (C4)
+        torch.cuda.empty_cache()
+        out["mmdit"] = mmdit_measure(args, dev, steps=min(args.steps, 5), warmup=min(args.warmup, 2),
+                                     with_cpu=not args.no_cpu_baseline)
+    print(json.dumps(out), flush=True)
+
+
+RELAUNCH_REPS = 20  # back-to-back repeats of one kernel per graph
+RELAUNCH_ROUNDS = 5
+
+
+def isolated_kernel_us(kernels, reps=RELAUNCH_REPS, rounds=RELAUNCH_ROUNDS):
+    """GPU microseconds per launch of each of ``kernels`` (profiler names)
+    alone: the library repeats its last launch of that kernel with the same
+    arguments (lrq_profile_relaunch), ``reps`` times back to back in one HIP
+    graph, which is replayed ``rounds`` times between events on the replay
+    stream. No per-launch markers sit between the repeats."""
+    import torch
+
+    from loractl_amd import device as D
+
+    ctx = D.context()
+    side = torch.cuda.Stream()
+    out = {}
+    for k in kernels:
+        side.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            D.profile_relaunch(k, reps, ctx=ctx, on_stream=side)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(rounds):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        out[k] = e0.elapsed_time(e1) * 1e3 / (rounds * reps)
+        del graph
+    return out
+
+
+FWD_KERNELS = ("lora_t", "fwd_main")
+
+
+def in_step_kernel_us(fwd, bwd, kernels, reserve, n_steps=10, rounds=10):
+    """Each kernel's cost inside the step, in microseconds per launch: HIP
+    graphs of ``n_steps`` steps (``fwd`` then ``bwd``), one plain and one per
+    kernel in which that kernel's step launch is repeated once more right
+    after its pass (lrq_profile_relaunch: same arguments, same outputs),
+    replayed in alternation ``rounds`` times; the extra time per step is the
+    kernel's duration among the step's other kernels (so under the step's
+    power state, not a sustained repeat's). Returns (per kernel, step us)."""
+    import torch
+
+    from loractl_amd import device as D
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graphs = {}
+    with torch.cuda.stream(side):
+        reserve()
+        fwd()
+        bwd()
+        torch.cuda.synchronize()
+        for k in [None] + list(kernels):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=side):
+                for _ in range(n_steps):
+                    fwd()
+                    if k in FWD_KERNELS:
+                        D.profile_relaunch(k, 1)
+                    bwd()
+                    if k is not None and k not in FWD_KERNELS:
+                        D.profile_relaunch(k, 1)
+            graphs[k] = g
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    for g in graphs.values():
+        g.replay()
+    torch.cuda.synchronize()
+    total = {k: 0.0 for k in graphs}
+    for _ in range(rounds):
+        for k, g in graphs.items():
+            e0.record()
+            g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            total[k] += e0.elapsed_time(e1)
+    per = {k: 1e3 * v / (rounds * n_steps) for k, v in total.items()}
+    del graphs
+    return {k: per[k] - per[None] for k in kernels}, per[None]
+
+
+def measure_ceilings(M, K, N, weights, row_bytes):
+    """What the part delivers on this box, for the fractions of the bench
+    line: the bf16 GEMM of the vendor library (torch.matmul, hipBLASLt) at
+    the forward shape x[M,K] . W^T and the input-gradient shape dy[M,N] . W,
+    no dequantization; and a streaming read of the packed weight's row
+    section (``row_bytes`` of each of ``weights``, rotated past the Infinity
+    Cache) by the library's probe (16-byte loads, every byte once)."""
+    import torch
+
+    g = torch.Generator(device="cuda").manual_seed(9)
+    w = (torch.randn(N, K, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    wt = w.t().contiguous()
+    x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+    dy = torch.randn(M, N, device="cuda", generator=g).to(torch.bfloat16)
+
+    def timed(fn, n=20):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        best = float("inf")
+        for _ in range(3):
+            e0.record()
+            for _ in range(n):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            best = min(best, e0.elapsed_time(e1) * 1e3 / n)
+        return best
+
+    fwd_us = timed(lambda: torch.matmul(x, wt))
+    dx_us = timed(lambda: torch.matmul(dy, w))
+    del w, wt, x, dy
+    from loractl_amd import device as D
+
+    views = [wb.data[:row_bytes] for wb in weights]
+    n = len(views)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    reads = 100
+    with torch.cuda.stream(side):
+        D.probe_stream_read(views[0])
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            for i in range(reads):
+                D.probe_stream_read(views[i % n])
+    torch.cuda.synchronize()
+    read_us = timed(lambda: graph.replay(), n=4) / reads
+    fl = 2.0 * M * N * K
+    return {
+        "gemm_bf16_hipblaslt": {"fwd_us": round(fwd_us, 2), "fwd_tflops": round(fl / (fwd_us * 1e-6) / 1e12, 1),
+                                "dx_us": round(dx_us, 2), "dx_tflops": round(fl / (dx_us * 1e-6) / 1e12, 1),
+                                "shape": f"x[{M},{K}] . W^T[{K},{N}] and dy[{M},{N}] . W[{N},{K}], bf16, torch.matmul"},
+        "stream_read_packed_weight": {"us": round(read_us, 3), "bytes": row_bytes,
+                                      "gbs": round(row_bytes / (read_us * 1e-6) / 1e9, 1),
+                                      "how": f"lrq_probe_stream_read over the blocked weight's row section, "
+                                             f"rotated over {n} copies, {reads} reads replayed from a HIP graph"},
+    }
+
+
+def site_measure(args, dev, workload, with_cpu=True, ceilings=False):
+    """One fused site of ``workload`` (ns, ns8, c1, c2): the step y, t =
+    fwd(x); dx, dA, dB = bwd(dy) timed over host-launched steps; every
+    kernel's in-step cost from graph differentials (``kernels_us``), its
+    time alone (``kernels_us_isolated``) and its event brackets
+    (``kernels_us_events``); the roofline of the dominant kernel from its
+    in-step cost; measured ceilings when asked. Returns (line, None)."""
+    import math
+
+    import torch
+
+    from loractl_amd import _lib as L
+    from loractl_amd import device as D
+
+    M, K, N, r, alpha, fmt, group = WORKLOADS[workload]
     s = alpha / r
     w, x, a, b, dy = make_inputs(M, K, N, r)
     wt = torch.from_numpy(w).to(dev)
@@ -191,7 +395,7 @@ def main():
     del wt
     # the interchange (row) layout, for the CPU baseline: the first fused
     # call re-lays the weight into the blocked layout in place
-    wq_rows = (wq.data.cpu().numpy(), wq.scales.cpu().numpy()) if not args.no_cpu_baseline else None
+    wq_rows = (wq.data.cpu().numpy(), wq.scales.cpu().numpy()) if with_cpu else None
     xb = torch.from_numpy(x).to(dev).to(torch.bfloat16)
     ab = torch.from_numpy(a).to(dev).to(torch.bfloat16)
     bb = torch.from_numpy(b).to(dev).to(torch.bfloat16)
@@ -222,22 +426,21 @@ def main():
     F = flops_step(M, K, N, r)
     value = F / (ms_step * 1e-3) / 1e12
 
-    # per-kernel launch times from the library's HIP events; the GPU first
-    # spins so that every profiled launch is queued behind it (the events
-    # then bracket GPU time only, not host enqueue gaps)
-    D.profile_reset()
-    D.profile_enable(True)
-    torch.cuda._sleep(GPU_SPIN_CYCLES)
-    for _ in range(args.steps):
-        step()
+    # which kernels a step launches, and their event-bracketed times (the GPU
+    # first spins so that every profiled launch is queued behind it)
+    prof = profile_kernels(run, args.steps)
+    events = {k: 1e3 * ms / n for k, (ms, n) in prof.items()}
+    # each kernel's cost inside the step (graph differential), and alone
+    # (back-to-back repeats of its step launch)
+    in_step, graph_step_us = in_step_kernel_us(lambda: D.lora_fwd(xb, wq, ab, bb, s, y=y, t=t),
+                                               lambda: D.lora_bwd(xb, dyb, wq, ab, bb, s, t, out=(dx, da, db)),
+                                               list(prof), lambda: D.reserve(M, N, K, r))
+    step()
     torch.cuda.synchronize()
-    prof = D.profile_read()
-    D.profile_enable(False)
-    kernels = {k: {"avg_us": 1e3 * ms / n, "launches": n} for k, (ms, n) in prof.items() if n}
+    iso = isolated_kernel_us(list(prof))
     per_kernel_flops = {"fwd_main": 2.0 * M * N * (K + r), "bwd_dx": 2.0 * M * K * (N + r)}
-    dom = max(("fwd_main", "bwd_dx"), key=lambda k: prof[k][0])
-    dom_us = kernels[dom]["avg_us"]
-    achieved = per_kernel_flops[dom] / (dom_us * 1e-6) / 1e12
+    dom = max(("fwd_main", "bwd_dx"), key=lambda k: in_step[k])
+    achieved = per_kernel_flops[dom] / (in_step[dom] * 1e-6) / 1e12
     roofline = {
         "kernel": dom,
         "bound": "mfma",
@@ -245,15 +448,14 @@ def main():
         "peak": PEAK_BF16_TFLOPS,
         "unit": "TFLOP/s",
         "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-        "traffic": load_traffic(dom, args.workload),
+        "traffic": load_traffic(dom, workload),
         "flops_per_launch": per_kernel_flops[dom],
-        "avg_launch_us": round(dom_us, 2),
+        "avg_launch_us": round(in_step[dom], 2),
+        "launch_time_from": "in-step cost: HIP graphs of 10 steps with and without one more launch of the "
+                            "step's own " + dom + " per step, replayed in alternation",
+        "isolated_us": round(iso[dom], 2),
+        "achieved_isolated": round(per_kernel_flops[dom] / (iso[dom] * 1e-6) / 1e12, 2),
     }
-
-    cpu = None
-    if not args.no_cpu_baseline:
-        cpu = cpu_baseline(wq_rows, x, a, b, dy, M, K, N, r, s, group, fmt, args.cpu_seconds)
-
     out = {
         "metric": f"{fmt}-base LoRA linear fwd+bwd TFLOP/s",
         "value": round(value, 2),
@@ -277,20 +479,30 @@ def main():
         "flops_per_step": F,
         "sanity_x2_ratio": round(ratio, 3),
         "warm_ms": round(warm_ms, 1),
-        "kernels_us": {k: round(v["avg_us"], 2) for k, v in kernels.items()},
+        "kernels_us": {k: round(v, 2) for k, v in in_step.items()},
+        "kernels_us_sum": round(sum(in_step.values()), 2),
+        "graph_step_us": round(graph_step_us, 2),
+        "kernels_us_isolated": {k: round(v, 2) for k, v in iso.items()},
+        "kernels_us_events": {k: round(v, 2) for k, v in events.items()},
         "roofline": roofline,
-        "cpu_baseline": cpu,
+        "cpu_baseline": None,
     }
-    if args.workload == "ns" and not args.no_skinny:
-        # the north star's second bar, the few-token forward of the same layer
-        out["skinny"] = skinny_measure(args, dev, with_cpu=not args.no_cpu_baseline)
-    if args.workload == "ns" and not args.no_mmdit:
-        # the metric's second half: MMDiT train steps/s (C4)
-        del wq, xb, ab, bb, dyb, y, t, dx, da, db
-        torch.cuda.empty_cache()
-        out["mmdit"] = mmdit_measure(args, dev, steps=min(args.steps, 5), warmup=min(args.warmup, 2),
-                                     with_cpu=not args.no_cpu_baseline)
-    print(json.dumps(out), flush=True)
+    if ceilings:
+        NB, KB = (N + 63) // 64, (K + 63) // 64
+        row_bytes = wq.data.numel() // 2
+        ncopy = max(2, math.ceil(1.15 * INFINITY_CACHE_BYTES / row_bytes))
+        copies = [wq] + [D.PackedWeight(wq.fmt, wq.n, wq.k, wq.data.clone(), wq.scales, wq.group, wq.per_channel,
+                                        None, L.LRQ_LAYOUT_BLOCKED) for _ in range(ncopy - 1)]
+        ceil_ = measure_ceilings(M, K, N, copies, row_bytes)
+        del copies
+        out["ceiling"] = ceil_
+        key = "fwd_tflops" if dom == "fwd_main" else "dx_tflops"
+        roofline["measured_ceiling"] = ceil_["gemm_bf16_hipblaslt"][key]
+        roofline["frac_of_measured"] = round(achieved / ceil_["gemm_bf16_hipblaslt"][key], 4)
+    if with_cpu:
+        out["cpu_baseline"] = cpu_baseline(wq_rows, x, a, b, dy, M, K, N, r, s, group, fmt, args.cpu_seconds)
+    del wq, xb, ab, bb, dyb, y, t, dx, da, db
+    return out, None
 
 
 def skinny_measure(args, dev, with_cpu=True, steps=100, workload="skinny"):
@@ -648,7 +860,9 @@ def mfma_roofline(prof, kflops, steps):
     achieved = kflops[dom] * steps / (ms * 1e-3) / 1e12
     return {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
-            "flops_per_launch": kflops[dom] * steps / n, "avg_launch_us": round(1e3 * ms / n, 2)}
+            "flops_per_launch": kflops[dom] * steps / n, "avg_launch_us": round(1e3 * ms / n, 2),
+            "launch_time_from": "per-launch HIP event brackets averaged over every site's launches (each "
+                                "bracket adds a few microseconds of markers)"}
 
 
 def cpu_baseline_set(rows, sites, group, budget_s, scale=1.0, what=""):
@@ -724,18 +938,21 @@ def bench_c3(args, dev):
     }), flush=True)
 
 
-def bench_c5(args, dev):
-    """C5: the linears of a Qwen3-style 28-layer decoder (q/k/v/o/gate/up/down,
-    int4 g64, LoRA r=16), forward + backward per step, at each M of the
-    sweep. Every layer has its own weights (3.2 GB blocked, past the
-    Infinity Cache), so the few-token end streams HBM."""
+def c5_measure(args, dev, Ms, with_cpu=True):
+    """C5 at each token count of ``Ms``: the linears of a Qwen3-style 28-layer
+    decoder (q/k/v/o/gate/up/down, int4 g64, LoRA r=16), forward + backward
+    of every site per step, one step replayed from a HIP graph. Every layer
+    has its own weights (3.2 GB blocked, past the Infinity Cache), so the
+    few-token end streams HBM. The roofline object is the whole step's (196
+    sites, both passes, many kernels): algorithmic flops (m >= 256, MFMA
+    bound) or bytes (m <= 16, HBM bound) per step over the step time; the
+    per-kernel figures are event-bracketed launch averages over all sites."""
     import torch
 
     sweep = {}
-    cpu = None
-    for M in C5_M:
+    for M in Ms:
         sites = [(M, K, N, 16, 16.0) for _layer in range(C5_LAYERS) for (K, N) in C5_LAYER]
-        keep = len(C5_LAYER) if (not args.no_cpu_baseline) else 0
+        keep = len(C5_LAYER) if with_cpu else 0
         ls = LinearSet(dev, sites, seed=5, keep_rows=keep)
         ls.run(1)
         torch.cuda.synchronize()
@@ -750,23 +967,32 @@ def bench_c5(args, dev):
         entry = {"ms_per_step": round(ms_step, 4), "tflops": round(F / (ms_step * 1e-3) / 1e12, 2),
                  "gbs": round(B / (ms_step * 1e-3) / 1e9, 1), "flops_per_step": F, "bytes_per_step": B,
                  "sanity_x2_ratio": round(ratio, 3),
-                 "kernels_us": {k: round(1e3 * v[0] / v[1], 2) for k, v in prof.items()}}
+                 "kernels_us_events": {k: round(1e3 * v[0] / v[1], 2) for k, v in prof.items()},
+                 "launches_per_step": {k: round(v[1] / steps, 2) for k, v in prof.items()}}
         if M >= 256:
-            entry["roofline"] = mfma_roofline(prof, ls.kernel_flops(), steps)
+            achieved = F / (ms_step * 1e-3) / 1e12
+            entry["roofline"] = {"kernel": "whole step (196 sites, forward and backward)", "bound": "mfma",
+                                 "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                                 "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                                 "flops_per_step": F, "time_from": "graph replay of the whole step"}
         else:
-            total_ms = sum(v[0] for v in prof.values()) / steps
-            achieved = B / (total_ms * 1e-3) / 1e9
-            entry["roofline"] = {"kernel": "all (stream of 196 weights, both passes)", "bound": "hbm",
+            achieved = B / (ms_step * 1e-3) / 1e9
+            entry["roofline"] = {"kernel": "whole step (196 weights streamed by both passes)", "bound": "hbm",
                                  "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                                  "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
-                                 "bytes_per_step": B}
-        if not args.no_cpu_baseline:
-            c = cpu_baseline_set(ls.rows, sites[:len(C5_LAYER)], 64, args.cpu_seconds / len(C5_M),
+                                 "bytes_per_step": B, "time_from": "graph replay of the whole step"}
+        if with_cpu:
+            c = cpu_baseline_set(ls.rows, sites[:len(C5_LAYER)], 64, args.cpu_seconds / len(Ms),
                                  scale=C5_LAYERS, what=f"1 of {C5_LAYERS} layers at M={M}, ")
             entry["cpu_baseline"] = {k: v for k, v in c.items() if k != "_seconds_per_step"}
         sweep[str(M)] = entry
         del ls
         torch.cuda.empty_cache()
+    return sweep
+
+
+def bench_c5(args, dev):
+    sweep = c5_measure(args, dev, C5_M, with_cpu=not args.no_cpu_baseline)
     head = sweep[str(C5_M[-1])]
     print(json.dumps({
         "metric": "int4-base LoRA linear set fwd+bwd TFLOP/s (C5: Qwen3-style decoder linears, M sweep)",

@@ -10,7 +10,15 @@ use std::env;
 use std::path::{Path, PathBuf};
 use std::process::Command;
 
-const SOURCES: [&str; 5] = ["lrq_quant.hip", "lrq_gemm.hip", "lrq_skinny.hip", "lrq_lora.hip", "lrq_api.hip"];
+const SOURCES: [&str; 7] = [
+    "lrq_quant.hip",
+    "lrq_gemm.hip",
+    "lrq_gemm_mid.hip",
+    "lrq_skinny.hip",
+    "lrq_lora.hip",
+    "lrq_api.hip",
+    "lrq_probe.hip",
+];
 
 fn main() {
     let manifest = PathBuf::from(env::var("CARGO_MANIFEST_DIR").expect("cargo sets CARGO_MANIFEST_DIR"));

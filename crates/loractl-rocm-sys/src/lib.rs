@@ -191,7 +191,10 @@ pub mod ffi {
             total_ms: *mut f64,
             launches: *mut i64,
         ) -> c_int;
+        pub fn lrq_profile_relaunch(ctx: *mut lrq_ctx, kid: c_int, n: c_int) -> c_int;
+        pub fn lrq_probe_stream_read(ctx: *mut lrq_ctx, data: *const c_void, bytes: i64) -> c_int;
         pub fn lrq_debug_force_wait_timeout(on: c_int) -> c_int;
+        pub fn lrq_debug_gemm_path(path: c_int) -> c_int;
     }
 }
 

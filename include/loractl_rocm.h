@@ -232,6 +232,26 @@ int lrq_profile_count(void);
 const char* lrq_profile_name(int kid);
 int lrq_profile_read(lrq_ctx* ctx, int kid, double* total_ms, int64_t* launches);
 
+/* Repeat, n times, the context's last launch of kernel `kid` among the
+ * fused calls' kernels (fwd_main, bwd_dx, lora_t, lora_u, lora_da, lora_db,
+ * lora_dadb), with the same arguments and buffers, on the context's stream,
+ * so that one kernel can be timed alone (a graph of back-to-back repeats).
+ * The buffers of that launch must still be allocated; a workspace growth
+ * forgets the kept launches. A repeat writes the same outputs again while
+ * the buffers it reads hold what they held at the launch: the workspace is
+ * shared by the passes (the backward reuses the forward's slot of the B^T
+ * rows for A), so a forward kernel repeated after a backward reads other
+ * values (same work, other results). */
+int lrq_profile_relaunch(lrq_ctx* ctx, int kid, int n);
+
+/* Measurement probe, no counterpart in the reference: read `bytes` (a
+ * multiple of 16, 16-byte aligned) of device memory once, as a plain
+ * streaming read with 16-byte loads (its per-workgroup checksums go to the
+ * workspace). Timed by the caller, it is the box's measured read rate for a
+ * buffer of that size, the ceiling beside the HBM peak for the few-token
+ * kernels. */
+int lrq_probe_stream_read(lrq_ctx* ctx, const void* data, int64_t bytes);
+
 /* Test hook, no counterpart in the reference: with on != 0, later
  * few-token launches (in this process) give their epilogues' bounded wait
  * for t a stamp that is never published and a cap of 16 polls, so every
@@ -239,6 +259,14 @@ int lrq_profile_read(lrq_ctx* ctx, int kid, double* total_ms, int64_t* launches)
  * the outputs are NaN and lrq_sync reports the flag. on = 0 restores the
  * normal wait. For tests of the failure path only. */
 int lrq_debug_force_wait_timeout(int on);
+
+/* Tuning and test hook, no counterpart in the reference: which kernel the
+ * fused products of m > 16 tokens take in this process. 0 (the default) the
+ * planned one; 1 the 256-token tiles (split in depth when too few); 2 and 3
+ * the 64-row tiles of 64 or 128 tokens over the whole depth. Every path
+ * computes the same products; a workspace sized by lrq_reserve under one
+ * setting grows on the next hot call if another needs more. */
+int lrq_debug_gemm_path(int path);
 
 #ifdef __cplusplus
 }

@@ -17,7 +17,7 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libloractl_rocm.so")
-SOURCES = ["lrq_quant.hip", "lrq_gemm.hip", "lrq_skinny.hip", "lrq_lora.hip", "lrq_api.hip"]
+SOURCES = ["lrq_quant.hip", "lrq_gemm.hip", "lrq_gemm_mid.hip", "lrq_skinny.hip", "lrq_lora.hip", "lrq_api.hip", "lrq_probe.hip"]
 MMDIT_LIB = os.path.join(HERE, "libloractl_mmdit.so")
 MMDIT_SOURCES = ["mmdit_attn_prep.hip", "mmdit_modulate.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -88,7 +88,10 @@ SIGNATURES = {
     "lrq_profile_count": (_i32, []),
     "lrq_profile_name": (ctypes.c_char_p, [_i32]),
     "lrq_profile_read": (_i32, [_vp, _i32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i64)]),
+    "lrq_profile_relaunch": (_i32, [_vp, _i32, _i32]),
+    "lrq_probe_stream_read": (_i32, [_vp, _vp, _i64]),
     "lrq_debug_force_wait_timeout": (_i32, [_i32]),
+    "lrq_debug_gemm_path": (_i32, [_i32]),
 }
 
 _lib = None

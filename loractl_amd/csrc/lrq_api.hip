@@ -8,6 +8,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <algorithm>
+#include <functional>
 #include <mutex>
 #include <new>
 #include <vector>
@@ -38,6 +39,9 @@ struct lrq_ctx {
   std::vector<hipEvent_t> pool;
   double total_ms[KID_COUNT] = {0};
   int64_t launches[KID_COUNT] = {0};
+  // the last launch of each hot kernel with its arguments, for
+  // lrq_profile_relaunch (timing one kernel alone)
+  std::function<hipError_t()> last[KID_COUNT];
 };
 
 // The workspace of lrq_lora_fwd_noalloc: a file-scope device array, one
@@ -120,6 +124,15 @@ int run(lrq_ctx* c, int kid, const char* what, F&& f) {
   return LRQ_OK;
 }
 
+// A launch of the fused calls: run it, and keep it (arguments by value) so
+// that lrq_profile_relaunch can repeat exactly this launch.
+template <class F>
+int run_hot(lrq_ctx* c, int kid, const char* what, F f) {
+  const int rc = run(c, kid, what, f);
+  if (rc == LRQ_OK) c->last[kid] = f;
+  return rc;
+}
+
 int flush_profile(lrq_ctx* c) {
   for (auto& r : c->pending) {
     hipError_t e = hipEventSynchronize(r.b);
@@ -163,6 +176,8 @@ int ensure_ws(lrq_ctx* c, size_t bytes) {
   // stream-ordered users of the old buffer must finish before it goes
   e = hipStreamSynchronize(c->stream);
   if (e != hipSuccess) return hip_fail(c, e, "hipStreamSynchronize");
+  // launches kept for lrq_profile_relaunch point into the old workspace
+  for (auto& f : c->last) f = nullptr;
   if (c->ws_alloc) {
     // a graph captured on this context may still replay kernels that read
     // and write the old allocation: keep it until lrq_destroy
@@ -397,6 +412,22 @@ int lrq_sync(lrq_ctx* c) {
               "is cleared and the counters reset");
 }
 
+int lrq_probe_stream_read(lrq_ctx* c, const void* data, int64_t bytes) {
+  LRQ_TRY(begin(c));
+  if (bytes < 0 || bytes % 16 != 0 || (bytes > 0 && !data) || !aligned16(data))
+    return fail(c, LRQ_EINVAL, "the probe reads a 16-byte aligned buffer of a multiple of 16 bytes");
+  LRQ_TRY(ensure_ws(c, (size_t)probe_read_grid(bytes) * 4));
+  uint32_t* out = reinterpret_cast<uint32_t*>(c->ws);
+  const hipError_t e = launch_stream_read(c->stream, data, bytes, out);
+  return e == hipSuccess ? LRQ_OK : hip_fail(c, e, "stream_read");
+}
+
+int lrq_debug_gemm_path(int path) {
+  if (path < 0 || path > 3) return LRQ_EINVAL;
+  set_gemm_path(path);
+  return LRQ_OK;
+}
+
 int lrq_debug_force_wait_timeout(int on) {
   set_force_wait_timeout(on != 0);
   return LRQ_OK;
@@ -597,6 +628,8 @@ static int fwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t 
   LRQ_TRY(note_capture(c));
   LRQ_TRY(check_gemm(c, w, m));
   if (!aligned16(x) || !aligned16(y)) return fail(c, LRQ_EINVAL, "x and y must be 16-byte aligned");
+  const int fmt = w->format;
+  const int64_t wk = w->k;
   const bool lora = a != nullptr && b != nullptr && r > 0;
   GemmArgs ga = gemm_args(w, false, x, m, y);
   if (lora) {
@@ -619,9 +652,10 @@ static int fwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t 
       ga.r = (int)r;
       ga.rp = rp;
     }
-    return run(c, KID_FWD_MAIN, "fwd_main", [&] {
-      return launch_skinny(c->stream, w->format, false, ga, lora ? a : nullptr, p, part, tpart, cnt, scaling,
-                           lora ? t_out : nullptr);
+    const uint16_t* ta = lora ? a : nullptr;
+    uint16_t* tt = lora ? t_out : nullptr;
+    return run_hot(c, KID_FWD_MAIN, "fwd_main", [=] {
+      return launch_skinny(c->stream, fmt, false, ga, ta, p, part, tpart, cnt, scaling, tt);
     });
   }
   if (lora) {
@@ -635,8 +669,9 @@ static int fwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t 
     const bool f8 = w->format == LRQ_FMT_FP8;
     const NtFinish fin{cnt,  scaling, (int)r, lw.tp,  t_out, b, w->n, 0,
                        lw.fr, f8 ? w->scales : nullptr, (f8 && w->per_channel) ? 1 : 0};
-    LRQ_TRY(run(c, KID_LORA_T, "lora_t", [&] {
-      return launch_lora_nt(c->stream, x, a, false, r, (int)r, m, w->k, rp, pt, lw.pn, fin);
+    float* pn = lw.pn;
+    LRQ_TRY(run_hot(c, KID_LORA_T, "lora_t", [=] {
+      return launch_lora_nt(c->stream, x, a, false, r, (int)r, m, wk, rp, pt, pn, fin);
     }));
     ga.lact = lw.tp;
     ga.lw = lw.fr;
@@ -650,7 +685,7 @@ static int fwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t 
       ga.part = reinterpret_cast<float*>(ws);
     }
   }
-  return run(c, KID_FWD_MAIN, "fwd_main", [&] { return launch_fwd(c->stream, w->format, ga); });
+  return run_hot(c, KID_FWD_MAIN, "fwd_main", [=] { return launch_fwd(c->stream, fmt, ga); });
 }
 
 int lrq_quant_matmul_t(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t m, uint16_t* y) {
@@ -691,12 +726,13 @@ int lrq_lora_fwd_noalloc(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int
 
 // The input gradient: the few-token path for m <= 16 (partials at `skpart`),
 // else the fused GEMM.
-static hipError_t launch_dx(lrq_ctx* c, const lrq_weight* w, const GemmArgs& ga, int64_t m, float* skpart) {
+static hipError_t launch_dx(lrq_ctx* c, int fmt, int64_t wn, int64_t wk, const GemmArgs& ga, int64_t m,
+                            float* skpart) {
   if (m >= 1 && m <= 16) {
-    const SkinnyPlan p = skinny_plan(w->k, w->n, 0, get_num_cus());
-    return launch_skinny(c->stream, w->format, true, ga, nullptr, p, skpart, nullptr, c->cnt, 1.0f, nullptr);
+    const SkinnyPlan p = skinny_plan(wk, wn, 0, get_num_cus());
+    return launch_skinny(c->stream, fmt, true, ga, nullptr, p, skpart, nullptr, c->cnt, 1.0f, nullptr);
   }
-  return launch_bwd(c->stream, w->format, ga);
+  return launch_bwd(c->stream, fmt, ga);
 }
 
 // workspace bytes of the few-token input gradient's partials (0 for m > 16)
@@ -712,6 +748,8 @@ static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const ui
   LRQ_TRY(note_capture(c));
   LRQ_TRY(check_gemm(c, w, m));
   if (!aligned16(dy)) return fail(c, LRQ_EINVAL, "dy must be 16-byte aligned");
+  const int fmt = w->format;
+  const int64_t wn = w->n, wk = w->k;
   if (dx && !aligned16(dx)) return fail(c, LRQ_EINVAL, "dx must be 16-byte aligned");
   const bool lora = a != nullptr && b != nullptr && r > 0;
   GemmArgs ga = gemm_args(w, true, dy, m, dx);
@@ -735,26 +773,28 @@ static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const ui
       float* part = reinterpret_cast<float*>(c->ws + lbytes);
       float* tpart = part + round_up((int64_t)sp.S * m * w->k, 64);
       ga.lw = a;
-      LRQ_TRY(run(c, KID_BWD_DX, "bwd_dx", [&] {
-        return launch_skinny(c->stream, w->format, true, ga, b, sp, part, tpart, c->cnt, scaling, ws.up);
+      uint16_t* up = ws.up;
+      LRQ_TRY(run_hot(c, KID_BWD_DX, "bwd_dx", [=] {
+        return launch_skinny(c->stream, fmt, true, ga, b, sp, part, tpart, c->cnt, scaling, up);
       }));
     } else {
       // u = s . dy . B^T   (bf16 [m, rp]: the dx epilogue operand and dA's factor)
       const LoraPlan pu = lora_plan_nt(m, w->n, rp);
-      LRQ_TRY(run(c, KID_LORA_U, "lora_u", [&] {
+      const LoraWs wsv = ws;
+      LRQ_TRY(run_hot(c, KID_LORA_U, "lora_u", [=] {
         // and A [k, r] padded to [k, rp]: the dx GEMM's weight-side LoRA rows
-        const NtFinish fin{c->cnt, scaling, (int)r, ws.up, nullptr, a, w->k, 1, ws.fr, nullptr, 0};
-        return launch_lora_nt(c->stream, dy, b, true, w->n, (int)r, m, w->n, rp, pu, ws.pn, fin);
+        const NtFinish fin{c->cnt, scaling, (int)r, wsv.up, nullptr, a, wk, 1, wsv.fr, nullptr, 0};
+        return launch_lora_nt(c->stream, dy, b, true, wn, (int)r, m, wn, rp, pu, wsv.pn, fin);
       }));
       ga.lact = ws.up;
       ga.lw = ws.fr;
       ga.part = ws.gp;
-      if (dx) LRQ_TRY(run(c, KID_BWD_DX, "bwd_dx", [&] { return launch_bwd(c->stream, w->format, ga); }));
+      if (dx) LRQ_TRY(run_hot(c, KID_BWD_DX, "bwd_dx", [=] { return launch_bwd(c->stream, fmt, ga); }));
     }
     // dA = x^T . u -> f32 [k, r] and dB = t^T . dy -> f32 [r, n]: token-slice
     // partials of both in one launch (dB's longer workgroups dispatched
     // first), each column tile finished by its last slice
-    TnSpec specs[2];
+    TnSpec specs[2] = {};
     int nj = 0;
     // (planned together when both run: fewer, longer slices than either
     // alone, so the partials reserved for the single-job plans suffice)
@@ -763,7 +803,11 @@ static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const ui
     if (da) specs[nj++] = TnSpec{x, ws.up, rp, m, w->k, (int)r, lora_plan_tn(m, w->k, rp, oa), ws.pa, da, r, 1};
     if (nj) {
       const int kid = nj == 2 ? KID_LORA_DADB : (db ? KID_LORA_DB : KID_LORA_DA);
-      LRQ_TRY(run(c, kid, kNames[kid], [&] { return launch_lora_tn(c->stream, specs, nj, rp, c->cnt); }));
+      const TnSpec s0 = specs[0], s1 = specs[1];
+      LRQ_TRY(run_hot(c, kid, kNames[kid], [=] {
+        const TnSpec sp[2] = {s0, s1};
+        return launch_lora_tn(c->stream, sp, nj, rp, c->cnt);
+      }));
     }
     return LRQ_OK;
   }
@@ -772,7 +816,7 @@ static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const ui
   LRQ_TRY(ensure_ws(c, std::max((size_t)pf * 4, skinny_dx_bytes(w, m))));
   if (pf > 0) ga.part = reinterpret_cast<float*>(c->ws);
   float* skpart = reinterpret_cast<float*>(c->ws);
-  return run(c, KID_BWD_DX, "bwd_dx", [&] { return launch_dx(c, w, ga, m, skpart); });
+  return run_hot(c, KID_BWD_DX, "bwd_dx", [=] { return launch_dx(c, fmt, wn, wk, ga, m, skpart); });
 }
 
 int lrq_quant_matmul_t_bwd(lrq_ctx* c, const lrq_weight* w, const uint16_t* dy, int64_t m, uint16_t* dx) {
@@ -806,6 +850,17 @@ int lrq_profile_reset(lrq_ctx* c) {
 }
 
 int lrq_profile_count(void) { return KID_COUNT; }
+
+int lrq_profile_relaunch(lrq_ctx* c, int kid, int n) {
+  LRQ_TRY(begin(c));
+  if (kid < 0 || kid >= KID_COUNT || n < 0) return fail(c, LRQ_EINVAL, "kernel id %d or count %d out of range", kid, n);
+  if (!c->last[kid]) return fail(c, LRQ_EINVAL, "no launch of kernel %s on this context to repeat", kNames[kid]);
+  for (int i = 0; i < n; ++i) {
+    const hipError_t e = c->last[kid]();
+    if (e != hipSuccess) return hip_fail(c, e, kNames[kid]);
+  }
+  return LRQ_OK;
+}
 
 const char* lrq_profile_name(int kid) { return (kid >= 0 && kid < KID_COUNT) ? kNames[kid] : ""; }
 

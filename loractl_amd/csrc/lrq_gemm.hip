@@ -649,9 +649,64 @@ hipError_t run_fmt(hipStream_t st, int fmt, bool r192, const GemmArgs& a) {
   return r192 ? run<BWD, LRQ_FMT_FP8, true, SPLIT>(st, a) : run<BWD, LRQ_FMT_FP8, false, SPLIT>(st, a);
 }
 
+// Which GEMM kernel a shape takes: the 256-token tiles above (split in
+// depth when they are too few), or lrq_gemm_mid.hip's 64-row tiles of 64 or
+// 128 tokens over the whole depth, two workgroups per CU. The choice is the
+// smaller modelled time, in microseconds, with constants measured on MI355X
+// (fwd and input gradient of the C1, C3, C5 and north-star shapes, every
+// path forced in turn):
+//   - a 256 x 256 x 64 step of the large tiles takes 1.86 us (0.8 of that
+//     for 192-row tiles); a split shape adds its f32 partials, written and
+//     read once at about 4 TB/s, and the reduction launch;
+//   - a 64-wide depth block of a mid tile takes MID_T1 us when its
+//     workgroup has the CU to itself and MID_T2 us each when two share it
+//     (64 tokens: 0.342 / 0.423, 128 tokens: 0.441 / 0.696); the tiles are
+//     dealt over the CUs, two at a time.
+constexpr double LARGE_STEP_US = 1.86;
+constexpr double MID_T1[2] = {0.342, 0.441}, MID_T2[2] = {0.423, 0.696};
+int g_gemm_path = 0;  // lrq_debug_gemm_path: 0 planned, 1 large tiles, 2 mid 64 tokens, 3 mid 128 tokens
+
+double large_us(int64_t m, int64_t e, int64_t depth) {
+  const SplitPlan p = plan_split(m, e, depth);
+  const int64_t cus = get_num_cus();
+  const int64_t RA = p.r192 ? 192 : 256;
+  const int64_t tiles = (m + RB - 1) / RB * ((e + RA - 1) / RA);
+  const double f = p.r192 ? 0.8 : 1.0;
+  if (p.S <= 1) return (double)((tiles + cus - 1) / cus) * (double)((depth + 63) / 64) * LARGE_STEP_US * f + 3.0;
+  const double part = 4.0 * (double)p.S * (double)m * (double)e;
+  return (double)p.spl * LARGE_STEP_US * f + 2.0 * part / 4.0e6 + 8.0;
+}
+
+double mid_us(int64_t m, int64_t e, int64_t depth, int tt) {
+  const int64_t T = 16 * tt, cus = get_num_cus();
+  const int64_t tiles = (m + T - 1) / T * ((e + 63) / 64);
+  const int64_t n = (tiles + cus - 1) / cus, nb = (depth + 63) / 64;
+  const int i = tt == 8 ? 1 : 0;
+  return (double)nb * ((double)(n / 2) * MID_T2[i] + (double)(n % 2) * MID_T1[i]) + 2.0;
+}
+
+int mid_plan(int64_t m, int64_t e, int64_t depth) {
+  if (m <= 0 || e <= 0) return 0;
+  if (g_gemm_path == 1) return 0;
+  if (g_gemm_path == 2) return 4;
+  if (g_gemm_path == 3) return 8;
+  double best = large_us(m, e, depth);
+  int tt = 0;
+  for (int cand : {4, 8}) {
+    const double t = mid_us(m, e, depth, cand);
+    if (t < best) {
+      best = t;
+      tt = cand;
+    }
+  }
+  return tt;
+}
+
 template <bool BWD>
 hipError_t dispatch(hipStream_t st, int fmt, const GemmArgs& a) {
   if (a.m == 0 || a.e == 0) return hipSuccess;
+  const int tt = mid_plan(a.m, a.e, a.l);
+  if (tt) return launch_mid(st, fmt, BWD, a, tt);
   const SplitPlan p = plan_split(a.m, a.e, a.l);
   if (p.S <= 1) return run_fmt<BWD, false>(st, fmt, p.r192, a);
   if (!a.part) return hipErrorInvalidValue;
@@ -677,7 +732,10 @@ int get_num_cus() { return g_num_cus_; }
 hipError_t launch_fwd(hipStream_t st, int fmt, const GemmArgs& a) { return dispatch<false>(st, fmt, a); }
 int64_t gemm_split_floats(int64_t m, int64_t e, int64_t depth) {
   if (m <= 0 || e <= 0) return 0;
+  if (mid_plan(m, e, depth)) return 0;  // the mid kernel keeps no partials
   const SplitPlan p = plan_split(m, e, depth);
   return p.S > 1 ? (int64_t)p.S * m * e : 0;
 }
 hipError_t launch_bwd(hipStream_t st, int fmt, const GemmArgs& a) { return dispatch<true>(st, fmt, a); }
+int gemm_mid_tokens(int64_t m, int64_t e, int64_t depth) { return 16 * mid_plan(m, e, depth); }
+void set_gemm_path(int path) { g_gemm_path = path; }

@@ -1,0 +1,363 @@
+// The two GEMMs of the quantized LoRA linear for mid token counts (the
+// token count that leaves the 256 x 256 tiles of lrq_gemm.hip too few to
+// fill the CUs), without splitting the depth:
+//
+//   forward   y[m, n]  = x[m, k]  . bf16(dq(w))[n, k]^T (+bias) + t[m, :] . B[:, n]
+//   backward  dx[m, k] = dy[m, n] . bf16(dq(w))[n, k]            + u[m, :] . A[k, :]^T
+//
+// (src/quant.rs:175-176 and :229-233; the LoRA terms of src/lora.rs:199-203
+// with t, u and the weight-side factor rows prepared by the LoRA side
+// kernels, as for the large tiles.)
+//
+// "Rows" are the output columns (n forward, k backward), "depth" the
+// reduction index. A tile is 64 rows x T tokens (T = 16 TT: 64 or 128) over
+// the whole depth, one workgroup of four wavefronts, two workgroups per CU:
+//   - wavefront w owns rows 16w .. 16w+15 of the tile for all T tokens, so
+//     each weight element is dequantized once per tile and each dequantized
+//     fragment feeds TT matrix-core steps (v_mfma_f32_16x16x32_bf16, weight
+//     rows in the A role, tokens in the B role);
+//   - weight: per 64-wide depth step a lane loads the packed bytes of its
+//     row (l & 15) for depths 16 (l >> 4) .. +16 from the blocked layout
+//     (int4 8 bytes, fp8 and int8 16): the 16 rows x 64 depth of a
+//     wavefront are one contiguous 512- or 1024-byte run. Sub-step kk of a
+//     step takes depths 16 (l >> 4) + 8 kk .. +8 in the MFMA's k slots
+//     8 (l >> 4) .. +8, and the activation fragments follow the same order.
+//     Forward: fma(u, s, -8s) = q s exactly (int4), the int8 analogue, or
+//     the exact e4m3 value (its channel scale multiplies the accumulators in
+//     the epilogue), then bf16. Backward (the transposed section): each of a
+//     lane's values has its own depth's scale; lane l of each 16-lane row
+//     loads the scale of depth 16 (l >> 4) + (l & 15) and a DPP row
+//     broadcast hands it to the lanes that need it: bf16(q s) again;
+//   - activations: the T x 64 slice of a step is copied global -> LDS by
+//     buffer loads with an LDS destination (16-byte chunk c of row r stored
+//     at chunk c ^ ((r >> 1) & 7)), four stages in flight, each in its own
+//     LDS array so that the compiler's waits track them apart; one barrier
+//     per step;
+//   - epilogue: the LoRA term as rank-wide matrix-core steps (the tile's
+//     token-side rows t or u and weight-side rows B^T or A from the
+//     workspace), the forward fp8 channel scales and the bias, bf16 stores;
+//   - tile order: the tiles are cut into groups of up to eight token tiles
+//     by all row tiles, token tile fastest, and each XCD (own L2) takes a
+//     contiguous range, so an XCD's tiles share a few token tiles of the
+//     activations and a band of weight rows.
+// Edges: rows past M, E and the depth read zeros (buffer-resource bounds),
+// the depth runs in whole rounds of four steps (the tail reads zeros), and
+// outputs past M or E are not stored.
+
+#include "lrq_common.h"
+#include "lrq_kernels.h"
+
+namespace {
+
+constexpr int MD = 64;    // depth per step (one 64 x 64 weight block)
+constexpr int MR = 64;    // rows per tile: four wavefronts of 16
+constexpr int MST = 4;    // pipeline stages
+
+// LDS chunk swizzle: rows r and r + 1 share a chunk order, so the 16 rows a
+// quarter-wavefront reads at one logical chunk cover all 64 banks
+LRQ_DEV int mswz(int r) { return (r >> 1) & 7; }
+
+template <bool BWD, int FMT, int TT, int SD>
+__global__ void __launch_bounds__(256, 2) k_mid(GemmArgs a, int tiles_m, int tiles_e, int group_m) {
+  constexpr bool I4 = FMT == LRQ_FMT_INT4;
+  constexpr bool I8 = FMT == LRQ_FMT_INT8;
+  constexpr bool GS = I4 || I8;                    // group scales (int4, int8) or channel scales (fp8)
+  constexpr int T = 16 * TT;                       // tokens per tile
+  constexpr int XB = T * MD * SD;                  // bf16 per stage: SD sub-tiles [T][64]
+  constexpr int XL = T / 32;                       // activation copies per wavefront per step
+  constexpr uint32_t blkb = I4 ? 2048u : 4096u;    // bytes per 64 x 64 block
+  constexpr uint32_t rowb = I4 ? 32u : 64u;        // bytes per block row
+  __shared__ __attribute__((aligned(16))) uint16_t sx0[XB];
+  __shared__ __attribute__((aligned(16))) uint16_t sx1[XB];
+  __shared__ __attribute__((aligned(16))) uint16_t sx2[XB];
+  __shared__ __attribute__((aligned(16))) uint16_t sx3[XB];
+
+  const int ntiles = tiles_m * tiles_e;
+  const int lt = xcd_remap((int)blockIdx.x, ntiles);
+  const int per = group_m * tiles_e;
+  const int grp = lt / per, within = lt % per;
+  const int gm = min(group_m, tiles_m - grp * group_m);
+  const int tm = grp * group_m + within % gm, te = within / gm;
+  const int64_t M = a.m, D = a.l, E = a.e;
+  const int64_t m0 = (int64_t)tm * T, e0 = (int64_t)te * MR;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q = lane >> 4, l16 = lane & 15;
+  const int64_t KB = (D + 63) / 64;
+  const int nk = (int)KB;
+  // stages of SD blocks, in whole rounds of MST stages
+  const int nsp = ((nk + SD - 1) / SD + MST - 1) / MST * MST;
+
+  // ---- weight: the tile's block row (64 rows = the tile), wavefront w's 16.
+  // Each resource ends where this block row's data ends, so a step past the
+  // depth reads zeros without a per-lane select.
+  const int64_t rb = e0 / 64;
+  const rsrc_t rw = make_rsrc(a.wdata + rb * KB * blkb, clamp_bytes(KB * blkb));
+  const uint32_t woff = (uint32_t)(16 * w + l16) * rowb + (uint32_t)q * (I4 ? 8u : 16u);
+  // forward int4 / int8: group scales [NB][Gp][64], this block row's slab;
+  // lane quarter q's group at step kt is (64 kt + 16 q) >> gshift: the
+  // step's first group, plus q / 2 for groups of 32
+  const uint32_t Gp = (uint32_t)((KB * 64) >> a.gshift);
+  // backward int4 / int8: ST [KGt][64 KB], row kg = output row >> gshift
+  // (uniform over the wavefront's 16 rows: groups are 32 or more); lane l
+  // of each 16-lane row loads the scale of depth 16 (l >> 4) + (l & 15).
+  // backward fp8: the channel scale of each depth [n], or a scalar.
+  const bool pc = !GS && a.per_channel;
+  const int64_t NP = KB * 64;
+  rsrc_t rs;
+  uint32_t sbase = 0;
+  if (!BWD) {
+    rs = make_rsrc(a.wscale + (GS ? rb * Gp * 64 : 0), GS ? clamp_bytes((int64_t)Gp * 64 * 4) : 0u);
+    sbase = (uint32_t)(16 * w + l16) * 4u + (a.gshift == 5 ? (uint32_t)(q >> 1) * 256u : 0u);
+  } else if (GS) {
+    rs = make_rsrc(a.wscale + ((e0 + 16 * w) >> a.gshift) * NP, clamp_bytes(NP * 4));
+    sbase = (uint32_t)((16 * q + l16) * 4);
+  } else {
+    rs = make_rsrc(a.wscale, pc ? clamp_bytes(D * 4) : 0u);
+    sbase = (uint32_t)((16 * q + l16) * 4);
+  }
+  const float s0add = (BWD && !GS && !pc) ? a.wscale[0] : 0.0f;
+
+  // ---- activations: wavefront w copies token rows w T/4 .. +T/4; lane l of
+  // copy c lands at row w T/4 + 8c + l/8, physical chunk l%8, fetching
+  // logical chunk (l%8) ^ mswz(row) = (l%8) ^ ((4c' + l/16) & 7), c' the
+  // row's 8-row group (its parity decides the pattern). A chunk at or past
+  // the depth reads zeros: lim = D - 8 lc bounds the step's start (it also
+  // ends the steps past the last block).
+  const rsrc_t rx = make_rsrc(a.act + (m0 < M ? m0 : 0) * D, m0 < M ? clamp_bytes((M - m0) * D * 2) : 0u);
+  const int xr0 = w * (T / 4);
+  const int lc0 = (lane & 7) ^ ((lane >> 4) & 7), lc1 = (lane & 7) ^ (((lane >> 4) + 4) & 7);
+  const uint32_t xo0 = (uint32_t)(((xr0 + (lane >> 3)) * D + lc0 * 8) * 2);
+  const uint32_t xo1 = (uint32_t)(((xr0 + (lane >> 3)) * D + lc1 * 8) * 2);
+  const int lim0 = (int)D - 8 * lc0, lim1 = (int)D - 8 * lc1;
+  auto dma = [&](uint16_t* buf, int kt) {
+    const int k0 = kt * MD;
+    const bool ok0 = k0 < lim0, ok1 = k0 < lim1;
+    const uint32_t ko = (uint32_t)(k0 * 2);
+    __attribute__((address_space(3))) char* base =
+        (__attribute__((address_space(3))) char*)(lds_void*)(buf + xr0 * MD);
+    const uint32_t o0 = opaque_u32(xo0) + ko, o1 = opaque_u32(xo1) + ko;
+#pragma unroll
+    for (int c = 0; c < XL; ++c) {
+      // the row group of copy c is xr0/8 + c: xr0/8 is even (T/4 is a
+      // multiple of 16), so its parity is c's
+      const bool ok = (c & 1) ? ok1 : ok0;
+      const uint32_t off = opaque_u32(ok ? ((c & 1) ? o1 : o0) + (uint32_t)(c * 8 * D * 2) : LRQ_OOB);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void*)(base + c * 8 * MD * 2), 16, off, 0, 0, 0);
+    }
+  };
+  // B-role fragment of token tile j, sub-step kk: row 16j + l16, logical
+  // chunk 2q + kk at physical chunk (2q + kk) ^ mswz(l16) (mswz(16j + l16) =
+  // mswz(l16)); the tile offset is an immediate of the LDS read
+  uint32_t xf[2];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk)
+    xf[kk] = opaque_u32((uint32_t)((l16 * MD + (((2 * q + kk) ^ mswz(l16)) * 8)) * 2));
+  auto xfrag = [&](const uint16_t* buf, int j, int kk) -> bf16x8 {
+    return as_bf16x8(ld16(reinterpret_cast<const char*>(buf) + xf[kk] + (uint32_t)(j * 16 * MD * 2)));
+  };
+
+  // ---- weights: per stage and block the packed bytes and one scale, in
+  // register sets; loaded one stage ahead of the activations, so a step can
+  // dequantize the next stage while its matrix-core steps run
+  u32x4 wv[MST][SD];
+  float sv[MST][SD];
+  auto load_w = [&](int set, int st) {
+#pragma unroll
+    for (int d = 0; d < SD; ++d) {
+      const uint32_t kt = (uint32_t)(st * SD + d);
+      if (I4) {
+        const u32x2 v = bload8(rw, opaque_u32(woff + kt * blkb));
+        wv[set][d] = (u32x4){v[0], v[1], 0u, 0u};
+      } else {
+        wv[set][d] = bload16(rw, opaque_u32(woff + kt * blkb));
+      }
+      const uint32_t so = !BWD ? ((kt * 64u) >> a.gshift) * 256u : kt * 256u;
+      sv[set][d] = bloadf(rs, opaque_u32(sbase + so));
+    }
+  };
+  // A-role fragment of block d, sub-step kk from register set `set`
+  auto wfrag = [&](int set, int d, int kk) -> bf16x8 {
+    const u32x4 v = wv[set][d];
+    const float sc = sv[set][d];
+    if (!BWD) {
+      if (I4) return as_bf16x8(dequant8_int4_bf16(v[kk], sc, a.nib));
+      if (I8) return as_bf16x8(dequant8_int8_bf16((u32x2){v[2 * kk], v[2 * kk + 1]}, sc));
+      const u32x2 lo = fp8x4_to_bf16(v[2 * kk]), hi = fp8x4_to_bf16(v[2 * kk + 1]);
+      return as_bf16x8((u32x4){lo[0], lo[1], hi[0], hi[1]});
+    }
+    float f[8];
+    if (I4) {
+      const uint32_t dw = v[kk];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[e] = (float)((int)(dw << (28 - 4 * e)) >> 28);
+    } else if (I8) {
+      int8x4_to_f32(v[2 * kk], f);
+      int8x4_to_f32(v[2 * kk + 1], f + 4);
+    } else {
+      fp8x4_to_f32(v[2 * kk], f);
+      fp8x4_to_f32(v[2 * kk + 1], f + 4);
+    }
+    const float S = sc + s0add;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = row_bcast_n(S, 8 * kk + e) * f[e];
+    u32x4 o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = pack_bf16x2(f[2 * i], f[2 * i + 1]);
+    return as_bf16x8(o);
+  };
+
+  f32x4 acc[TT];
+#pragma unroll
+  for (int j = 0; j < TT; ++j) acc[j] = acc_zero4();
+
+  uint16_t* const bufs[MST] = {sx0, sx1, sx2, sx3};
+  // A fragments of the current and the next stage
+  bf16x8 fa[2][SD][2];
+  // per-lane memory instructions of one stage: per block the activation
+  // copies, the weight bytes and the scale
+  constexpr int NST = SD * (XL + 2);
+  // Stage st: activations in bufs[st % MST] (issued MST - 1 stages ahead),
+  // weights in register set st % MST (MST stages ahead), A fragments in
+  // fa[st % 2] (dequantized during stage st - 1).
+  auto step = [&](const int b, const int st) {
+    // nothing of one step moves into another
+    __builtin_amdgcn_sched_barrier(0);
+    // stage st's copies and stage st + 1's weights have landed (issued in
+    // that order, then MST - 2 more stages); the newer ones may be in flight
+    __builtin_amdgcn_s_waitcnt((((MST - 2) * NST) & 0xf) | ((((MST - 2) * NST) >> 4) << 14) | 0xf70);
+    // a barrier without a memory fence: a fence would wait for every copy
+    // in flight (the newer stages too). Each wavefront's own wait above
+    // covers its copies of this stage, and the fragment reads of the last
+    // step were consumed by its matrix-core steps before this point.
+    __builtin_amdgcn_s_barrier();
+    // every wavefront is done with the buffer of stage st - 1: refill it;
+    // register set b (stage st's weights, dequantized last step) takes
+    // stage st + MST's
+    const int nb = (b + MST - 1) % MST;
+#pragma unroll
+    for (int d = 0; d < SD; ++d) dma(bufs[nb] + d * T * MD, (st + MST - 1) * SD + d);
+    load_w(b, st + MST);
+    __builtin_amdgcn_sched_barrier(0);
+    const int cur = b & 1, nxt = cur ^ 1;
+#pragma unroll
+    for (int d = 0; d < SD; ++d)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+        for (int j = 0; j < TT; ++j) acc[j] = mfma16(fa[cur][d][kk], xfrag(bufs[b] + d * T * MD, j, kk), acc[j]);
+        // the next stage's fragment, between this stage's matrix-core steps
+        fa[nxt][d][kk] = wfrag((b + 1) % MST, d, kk);
+      }
+  };
+
+  // prologue: stage 0's weights, then stages 0 .. MST-2 of activations
+  // each followed by the next stage's weights; stage 0 dequantized
+  load_w(0, 0);
+#pragma unroll
+  for (int s = 0; s < MST - 1; ++s) {
+#pragma unroll
+    for (int d = 0; d < SD; ++d) dma(bufs[s] + d * T * MD, s * SD + d);
+    load_w(s + 1, s + 1);
+  }
+  __builtin_amdgcn_s_waitcnt((((MST - 1) * NST) & 0xf) | ((((MST - 1) * NST) >> 4) << 14) | 0xf70);
+#pragma unroll
+  for (int d = 0; d < SD; ++d)
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) fa[0][d][kk] = wfrag(0, d, kk);
+  for (int st = 0; st < nsp; st += MST) {
+#pragma unroll
+    for (int b = 0; b < MST; ++b) step(b, st + b);
+  }
+  // the look-ahead copies past the depth read nothing (out of range), but
+  // they are still in flight: drain them before LDS is released
+  __builtin_amdgcn_s_waitcnt(0);
+
+  // ---- epilogue
+  const int rp = a.rp;
+  if (rp > 0) {
+    // LoRA: A role = weight-side rows e0 + 16w + l16 (B^T forward, A
+    // backward, [E][rp]), B role = token rows m0 + 16j + l16 (t or u,
+    // [M][rp]); rank slots 32 ks + 8q .. +8, zero past rp
+    const rsrc_t rfr = make_rsrc(a.lw + (e0 + 16 * w) * rp,
+                                 e0 + 16 * w < E ? clamp_bytes((E - e0 - 16 * w) * rp * 2) : 0u);
+    const rsrc_t rt = make_rsrc(a.lact + (m0 < M ? m0 : 0) * rp, m0 < M ? clamp_bytes((M - m0) * rp * 2) : 0u);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      if (ks * 32 < rp) {
+        const bool ok = 32 * ks + 8 * q < rp;
+        const bf16x8 la = as_bf16x8(bload16(rfr, opaque_u32(ok ? (uint32_t)((l16 * rp + 32 * ks + 8 * q) * 2) : LRQ_OOB)));
+#pragma unroll
+        for (int j = 0; j < TT; ++j) {
+          const bf16x8 lb = as_bf16x8(
+              bload16(rt, opaque_u32(ok ? (uint32_t)(((16 * j + l16) * rp + 32 * ks + 8 * q) * 2) : LRQ_OOB)));
+          acc[j] = mfma16(la, lb, acc[j]);
+        }
+      }
+    }
+  }
+  // lane: output rows (columns of y / dx) n = e0 + 16w + 4q + v, v = 0..3,
+  // token m0 + 16j + l16
+  const int64_t n = e0 + 16 * w + 4 * q;
+  const bool nok = n < E;  // E % 8 == 0: the four are in or out together
+  f32x4 sc = {1.f, 1.f, 1.f, 1.f}, bv = {0.f, 0.f, 0.f, 0.f};
+  if (!BWD) {
+    if (!GS) {
+      if (pc) {
+        const rsrc_t rsc = make_rsrc(a.wscale, clamp_bytes(E * 4));
+        const u32x4 s4 = bload16(rsc, opaque_u32(nok ? (uint32_t)(n * 4) : LRQ_OOB));
+        sc = (f32x4){__uint_as_float(s4[0]), __uint_as_float(s4[1]), __uint_as_float(s4[2]), __uint_as_float(s4[3])};
+      } else {
+        const float s0 = a.wscale[0];
+        sc = (f32x4){s0, s0, s0, s0};
+      }
+    }
+    if (a.bias) {
+      const rsrc_t rbi = make_rsrc(a.bias, clamp_bytes(E * 4));
+      const u32x4 b4 = bload16(rbi, opaque_u32(nok ? (uint32_t)(n * 4) : LRQ_OOB));
+      bv = (f32x4){__uint_as_float(b4[0]), __uint_as_float(b4[1]), __uint_as_float(b4[2]), __uint_as_float(b4[3])};
+    }
+  }
+  const rsrc_t ry = make_rsrc(a.out + (m0 < M ? m0 : 0) * E, m0 < M ? clamp_bytes((M - m0) * E * 2) : 0u);
+#pragma unroll
+  for (int j = 0; j < TT; ++j) {
+    const f32x4 c = acc[j];
+    u32x2 o;
+    o[0] = pack_bf16x2(__builtin_fmaf(c[0], sc[0], bv[0]), __builtin_fmaf(c[1], sc[1], bv[1]));
+    o[1] = pack_bf16x2(__builtin_fmaf(c[2], sc[2], bv[2]), __builtin_fmaf(c[3], sc[3], bv[3]));
+    const uint32_t off = nok ? (uint32_t)(((16 * j + l16) * E + n) * 2) : LRQ_OOB;
+    __builtin_amdgcn_raw_buffer_store_b64(o, ry, opaque_u32(off), 0, 0);
+  }
+}
+
+template <bool BWD, int FMT>
+hipError_t run_mid(hipStream_t st, const GemmArgs& a, int tt) {
+  const int T = 16 * tt;
+  const int tiles_m = (int)((a.m + T - 1) / T);
+  const int tiles_e = (int)((a.e + MR - 1) / MR);
+  const int group_m = tiles_m < 8 ? tiles_m : 8;
+  const int ntiles = tiles_m * tiles_e;
+  // two 64-wide blocks per stage with 64-token tiles, one with 128: 64 KiB
+  // of LDS either way, two workgroups per CU
+  if (tt == 8)
+    hipLaunchKernelGGL((k_mid<BWD, FMT, 8, 1>), dim3(ntiles), dim3(256), 0, st, a, tiles_m, tiles_e, group_m);
+  else
+    hipLaunchKernelGGL((k_mid<BWD, FMT, 4, 2>), dim3(ntiles), dim3(256), 0, st, a, tiles_m, tiles_e, group_m);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_mid(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, int tt) {
+  if (a.m <= 0 || a.e <= 0) return hipSuccess;
+  if (tt != 4 && tt != 8) return hipErrorInvalidValue;
+  if (a.rp > 64) return hipErrorInvalidValue;
+  // 32-bit buffer offsets: one tile's activation rows and outputs, the depth
+  // run of the weight's block row
+  if ((int64_t)16 * tt * a.l * 2 >= ((int64_t)1 << 31) || (int64_t)16 * tt * a.e * 2 >= ((int64_t)1 << 31))
+    return hipErrorInvalidValue;
+  if (fmt == LRQ_FMT_INT4) return bwd ? run_mid<true, LRQ_FMT_INT4>(st, a, tt) : run_mid<false, LRQ_FMT_INT4>(st, a, tt);
+  if (fmt == LRQ_FMT_INT8) return bwd ? run_mid<true, LRQ_FMT_INT8>(st, a, tt) : run_mid<false, LRQ_FMT_INT8>(st, a, tt);
+  return bwd ? run_mid<true, LRQ_FMT_FP8>(st, a, tt) : run_mid<false, LRQ_FMT_FP8>(st, a, tt);
+}

@@ -60,6 +60,14 @@ hipError_t launch_fwd(hipStream_t st, int fmt, const GemmArgs& a);
 hipError_t launch_bwd(hipStream_t st, int fmt, const GemmArgs& a);
 int64_t gemm_split_floats(int64_t m, int64_t e, int64_t depth);
 int get_num_cus();
+// lrq_gemm_mid.hip: the same products on 64-row tiles of 16 tt tokens (tt 4
+// or 8) over the whole depth, no partials; lrq_gemm.hip's launchers take it
+// when it is modelled faster (gemm_mid_tokens: its tile's tokens, or 0)
+hipError_t launch_mid(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, int tt);
+int gemm_mid_tokens(int64_t m, int64_t e, int64_t depth);
+// tuning and test hook (lrq_debug_gemm_path): 0 planned, 1 large tiles,
+// 2 mid tiles of 64 tokens, 3 of 128
+void set_gemm_path(int path);
 
 // lrq_skinny.hip: the forward for m <= 16 in one launch. Split workgroups
 // stream the packed weight once and write f32 partials of x . W^T per
@@ -158,6 +166,11 @@ struct TnSpec {
   int64_t sc, sj;
 };
 hipError_t launch_lora_tn(hipStream_t st, const TnSpec* jobs, int njobs, int rp, uint32_t* cnt);
+
+// lrq_probe.hip: a streaming read of `bytes` (a multiple of 16) with one
+// 32-bit value per workgroup to out (probe_read_grid(bytes) of them)
+int probe_read_grid(int64_t bytes);
+hipError_t launch_stream_read(hipStream_t st, const void* data, int64_t bytes, uint32_t* out);
 
 // kernel ids for the profiler (lrq_profile_*)
 enum {

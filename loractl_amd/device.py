@@ -371,6 +371,44 @@ def debug_force_wait_timeout(on: bool):
     L.load().lrq_debug_force_wait_timeout(int(on))
 
 
+GEMM_PATHS = {"planned": 0, "large": 1, "mid64": 2, "mid128": 3}
+
+
+def debug_gemm_path(path: str):
+    """Tuning and test hook: force the kernel the fused products of m > 16
+    tokens take in this process ("planned", "large": the 256-token tiles,
+    split in depth when too few, "mid64" / "mid128": 64-row tiles of 64 or
+    128 tokens over the whole depth). Every path computes the same products."""
+    L.load().lrq_debug_gemm_path(GEMM_PATHS[path])
+
+
+def probe_stream_read(t: torch.Tensor):
+    """Read every byte of the contiguous device tensor ``t`` once (a plain
+    streaming read, for timing the box's read rate)."""
+    if not t.is_cuda or not t.is_contiguous():
+        raise ValueError("probe_stream_read takes a contiguous GPU tensor")
+    context(t.device.index).call("lrq_probe_stream_read", _ptr(t), t.numel() * t.element_size())
+
+
+def profile_relaunch(kernel: str, n: int, ctx: Optional[Context] = None, on_stream=None):
+    """Repeat the last launch of ``kernel`` (a profiler name such as
+    "fwd_main" or "bwd_dx") on ``ctx`` (default: the current stream's
+    context) ``n`` times with the same arguments, to time that kernel alone.
+    ``on_stream`` (a torch stream) issues the repeats there instead of on the
+    context's stream, e.g. to capture them into a graph."""
+    ctx = ctx if ctx is not None else context()
+    names = [ctx.lib.lrq_profile_name(i).decode() for i in range(ctx.lib.lrq_profile_count())]
+    kid = names.index(kernel)
+    with ctx.lock:
+        if on_stream is not None:
+            ctx.call("lrq_set_stream", ctypes.c_void_p(on_stream.cuda_stream))
+        try:
+            ctx.call("lrq_profile_relaunch", kid, n)
+        finally:
+            if on_stream is not None:
+                ctx.call("lrq_set_stream", ctypes.c_void_p(ctx.stream))
+
+
 def reserve(m: int, n: int, k: int, r: int, device: Optional[int] = None):
     ctx = context(device)
     ctx.call("lrq_reserve", m, n, k, r)

@@ -1,5 +1,7 @@
 """Seeded inputs and comparisons shared by the GPU parity tests."""
 
+import contextlib
+
 import numpy as np
 import torch
 
@@ -34,3 +36,16 @@ def check(name, got, ref, tol_rel=TOL_REL, tol_cos=TOL_COS):
     cos = O.cosine(g, ref) if np.abs(ref).max() > 0 else (1.0 if not np.abs(g).max() else 0.0)
     assert rel <= tol_rel and cos >= tol_cos, f"{name}: rel_dev={rel:.3e} cos={cos:.6f}"
     return rel, cos
+
+
+@contextlib.contextmanager
+def gemm_path(path):
+    """Run the block with the fused products of m > 16 tokens forced onto one
+    kernel path ("planned", "large", "mid64", "mid128")."""
+    from loractl_amd import device as D
+
+    D.debug_gemm_path(path)
+    try:
+        yield
+    finally:
+        D.debug_gemm_path("planned")

@@ -110,3 +110,36 @@ def test_workspace_growth_keeps_captured_graphs_valid(cuda):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(y, y_eager) and torch.equal(t, t_eager), f"replay {i}"
+
+
+def test_profile_relaunch_repeats_the_step_launch(cuda):
+    """lrq_profile_relaunch repeats a context's last launch of one kernel with
+    its arguments: while the buffers it reads (the workspace included) hold
+    what they held, the outputs it writes come back bit for bit; a kernel
+    never launched on the context is refused."""
+    M, K, N, r = 300, 1024, 2048, 16
+    w, x, a, b, dy = case_inputs(M, K, N, r, seed=13)
+    wq = _weight(cuda, w)
+    xd, ad, bd, dyd = (to_dev(v, cuda) for v in (x, a, b, dy))
+    y, t = D.lora_fwd(xd, wq, ad, bd, 1.0)
+    torch.cuda.synchronize()
+    y_ref = y.clone()
+    y.zero_()
+    D.profile_relaunch("fwd_main", 2)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_ref)
+    # the backward reuses the workspace slot of the forward's B^T rows for A
+    dx, da, db = D.lora_bwd(xd, dyd, wq, ad, bd, 1.0, t)
+    torch.cuda.synchronize()
+    ref = [v.clone() for v in (dx, da, db)]
+    for v in (dx, da, db):
+        v.zero_()
+    for k in ("bwd_dx", "lora_dadb"):
+        D.profile_relaunch(k, 2)
+    torch.cuda.synchronize()
+    for got, want in zip((dx, da, db), ref):
+        assert torch.equal(got, want)
+    other = torch.cuda.Stream()
+    with torch.cuda.stream(other):
+        with pytest.raises(L.LrqError, match="no launch of kernel fwd_main"):
+            D.profile_relaunch("fwd_main", 1)

@@ -9,7 +9,7 @@ import pytest
 import torch
 
 import oracle as O
-from gpu_helpers import case_inputs, check, to_dev
+from gpu_helpers import case_inputs, check, gemm_path, to_dev
 from loractl_amd import device as D
 from loractl_amd._lib import LrqError
 
@@ -195,11 +195,14 @@ def test_bias_epilogue(cuda):
     check("y+bias", y, y_ref)
 
 
+@pytest.mark.parametrize("path", ["large", "mid64", "mid128"])
 @pytest.mark.parametrize("fmt,per_channel", [("int4", True), ("fp8", True), ("fp8", False), ("int8", True)])
-def test_split_depth_bias_and_scales(cuda, fmt, per_channel):
-    """Few output tiles (M = 200, d_out = 3072): the depth is split into
-    ranges whose f32 partials a reduction sums; the bias and the forward fp8
-    channel scales (or the scalar) are applied there, once."""
+def test_split_depth_bias_and_scales(cuda, fmt, per_channel, path):
+    """Few output tiles (M = 200, d_out = 3072). On the large tiles the depth
+    is split into ranges whose f32 partials a reduction sums, and the bias
+    and the forward fp8 channel scales (or the scalar) are applied there,
+    once; the mid-size tiles run the whole depth and apply them in their
+    epilogue."""
     M, K, N, r = 200, 3072, 3072, 16
     g = torch.Generator(device=cuda).manual_seed(7)
     w = torch.randn(N, K, device=cuda, generator=g) * 0.02
@@ -211,8 +214,9 @@ def test_split_depth_bias_and_scales(cuda, fmt, per_channel):
     a = ((torch.rand(K, r, device=cuda, generator=g) * 2 - 1) / K ** 0.5).to(torch.bfloat16)
     b = (torch.randn(r, N, device=cuda, generator=g) * 1e-2).to(torch.bfloat16)
     dy = torch.randn(M, N, device=cuda, generator=g).to(torch.bfloat16)
-    y, t = D.lora_fwd(x, wq, a, b, 0.5)
-    dx, _, _ = D.lora_bwd(x, dy, wq, a, b, 0.5, t)
+    with gemm_path(path):
+        y, t = D.lora_fwd(x, wq, a, b, 0.5)
+        dx, _, _ = D.lora_bwd(x, dy, wq, a, b, 0.5, t)
     xf, af, bf, dyf = x.float(), a.float(), b.float(), dy.float()
     y_ref = xf @ wdq.t() + 0.5 * (xf @ af) @ bf + bias
     dx_ref = dyf @ wdq + 0.5 * (dyf @ bf.t()) @ af.t()
@@ -327,3 +331,39 @@ def test_baseline_shapes_against_torch_fp32(cuda, M, K, N, r, fmt):
     db_ref = t_ref.t() @ dyf
     for name, got, ref in (("y", y, y_ref), ("dx", dx, dx_ref), ("dA", da, da_ref), ("dB", db, db_ref)):
         check(name, got, ref.cpu().numpy())
+
+
+# m > 16: ragged token counts (not a multiple of 64 or 128), K % 64 == 32,
+# d_out not a multiple of 64, groups 32 to 128
+PATH_SHAPES = [(37, 96, 72, 32), (130, 192, 520, 64), (300, 320, 264, 64), (513, 512, 392, 128)]
+
+
+@pytest.mark.parametrize("path", ["large", "mid64", "mid128"])
+@pytest.mark.parametrize("fmt,per_channel", [("int4", True), ("int8", True), ("fp8", True), ("fp8", False)])
+@pytest.mark.parametrize("M,K,N,g", PATH_SHAPES)
+def test_gemm_paths_against_oracle(cuda, M, K, N, g, fmt, per_channel, path):
+    """Every kernel path of m > 16 (the 256-token tiles, split in depth where
+    they are few, and the 64-row tiles of 64 or 128 tokens) on the same
+    inputs: y (with bias), t, dx, dA and dB of the fused site, and the plain
+    product and its input gradient, against the f64 oracle."""
+    r = 33
+    w, x, a, b, dy = case_inputs(M, K, N, r, seed=7 * M + N + g)
+    wq, wdq = _weight(w, fmt, g, cuda, per_channel)
+    bias = np.linspace(-0.5, 0.5, N).astype(np.float32)
+    wb = wq.with_bias(torch.from_numpy(bias).to(cuda))
+    s = 0.75
+    xd, ad, bd, dyd = to_dev(x, cuda), to_dev(a, cuda), to_dev(b, cuda), to_dev(dy, cuda)
+    with gemm_path(path):
+        y, t = D.lora_fwd(xd, wb, ad, bd, s)
+        dx, da, db = D.lora_bwd(xd, dyd, wb, ad, bd, s, t)
+        y0 = D.quant_matmul_t(xd, wq)
+        dx0 = D.quant_matmul_t_bwd(dyd, wq)
+    y_ref, t_ref = O.linear_fwd(x, wdq, a, b, s, bias=bias)
+    dx_ref, da_ref, db_ref = O.linear_bwd(x, wdq, a, b, s, dy)
+    check("y", y, y_ref)
+    check("t", t, t_ref)
+    check("dx", dx, dx_ref)
+    check("dA", da, da_ref)
+    check("dB", db, db_ref)
+    check("y base", y0, O.linear_fwd(x, wdq)[0])
+    check("dx base", dx0, O.linear_bwd(x, wdq, None, None, 1.0, dy)[0])

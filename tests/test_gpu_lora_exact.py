@@ -9,32 +9,36 @@ matrix-core step was skipped, or an accumulator element read before its
 last step landed, changes the elements that chunk contributes to, and the
 test checks that the last chunk contributes to a large share of them.
 
-Each shape selects one kernel path of the library (256 CUs): the few-token
-kernels (m <= 16), the split-depth GEMM with 192-row tiles (m = 256), and
-the tiled GEMM with 192-row and 256-row tiles (m = 4096), forward and
-backward. Ranks 16, 32, 33, 48 and 64 cover one to four rank chunks and a
-padded chunk.
+Each case selects one kernel path of the library (256 CUs): the few-token
+kernels (m <= 16), the split-depth GEMM with 192-row tiles (m = 256, forced
+onto the large tiles), the tiled GEMM with 192-row and 256-row tiles
+(m = 4096), and the mid-size tiles of 64 and 128 tokens (forced, with a
+ragged token count), forward and backward. Ranks 16, 32, 33, 48 and 64
+cover one to four rank chunks and a padded chunk.
 """
 
 import numpy as np
 import pytest
 import torch
 
+from gpu_helpers import gemm_path
 from loractl_amd import _lib as L
 from loractl_amd import device as D
 
 pytestmark = pytest.mark.gpu
 
 SCALING = 0.5
-# (label, M, K, N)
+# (label, M, K, N, GEMM path)
 PATHS = [
-    ("few-token m=5", 5, 512, 768),
-    ("few-token m=16", 16, 3072, 3072),
-    ("few-token split forward m=9", 9, 4160, 520),
-    ("few-token whole-depth forward m=16", 16, 3072, 8192),
-    ("split-depth r192", 256, 3072, 3072),
-    ("tiled r192 fwd / split bwd", 4096, 256, 3072),
-    ("tiled r256", 4096, 4096, 4096),
+    ("few-token m=5", 5, 512, 768, "planned"),
+    ("few-token m=16", 16, 3072, 3072, "planned"),
+    ("few-token split forward m=9", 9, 4160, 520, "planned"),
+    ("few-token whole-depth forward m=16", 16, 3072, 8192, "planned"),
+    ("split-depth r192", 256, 3072, 3072, "large"),
+    ("tiled r192 fwd / split bwd", 4096, 256, 3072, "large"),
+    ("tiled r256", 4096, 4096, 4096, "large"),
+    ("mid 64-token tiles", 300, 3072, 3064, "mid64"),
+    ("mid 128-token tiles", 300, 1088, 1032, "mid128"),
 ]
 RANKS = [16, 32, 33, 48, 64]
 
@@ -74,9 +78,9 @@ def _exact(name, got, ref):
 
 @pytest.mark.parametrize("fmt", ["int4", "fp8"])
 @pytest.mark.parametrize("r", RANKS)
-@pytest.mark.parametrize("label,M,K,N", PATHS, ids=[p[0] for p in PATHS])
-def test_lora_exact_per_rank_chunk(cuda, label, M, K, N, r, fmt):
-    print(f"[exact] {label} M={M} K={K} N={N} r={r} {fmt}", flush=True)
+@pytest.mark.parametrize("label,M,K,N,path", PATHS, ids=[p[0] for p in PATHS])
+def test_lora_exact_per_rank_chunk(cuda, label, M, K, N, path, r, fmt):
+    print(f"[exact] {label} M={M} K={K} N={N} r={r} {fmt} {path}", flush=True)
     cf = _closed_form(M, K, N, r)
     # the test's power: the last rank chunk (16 wide, possibly padded)
     # changes a large share of the outputs, so skipping its step cannot go unseen
@@ -90,9 +94,10 @@ def test_lora_exact_per_rank_chunk(cuda, label, M, K, N, r, fmt):
     a = torch.from_numpy(cf["A"]).to(cuda).to(torch.bfloat16).contiguous()
     b = torch.from_numpy(cf["B"]).to(cuda).to(torch.bfloat16).contiguous()
     wq = _weight(fmt, N, K, cuda)
-    y, t = D.lora_fwd(x, wq, a, b, SCALING)
-    dx, da, db = D.lora_bwd(x, dy, wq, a, b, SCALING, t)
-    torch.cuda.synchronize()
+    with gemm_path(path):
+        y, t = D.lora_fwd(x, wq, a, b, SCALING)
+        dx, da, db = D.lora_bwd(x, dy, wq, a, b, SCALING, t)
+        torch.cuda.synchronize()
     _exact("t", t, cf["t"])
     _exact("y", y, cf["y"])
     _exact("dx", dx, cf["dx"])

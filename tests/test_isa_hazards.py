@@ -15,7 +15,7 @@ import isa_hazards as H
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CSRC = os.path.join(ROOT, "loractl_amd", "csrc")
-MFMA_SOURCES = ["lrq_gemm.hip", "lrq_skinny.hip", "lrq_lora.hip"]
+MFMA_SOURCES = ["lrq_gemm.hip", "lrq_gemm_mid.hip", "lrq_skinny.hip", "lrq_lora.hip"]
 
 _HEAD = "\t.text\n\t.globl k\n\t.type k,@function\nk:\n"
 _TAIL = "\ts_endpgm\n.Lfunc_end0:\n"
