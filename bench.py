@@ -93,6 +93,10 @@ def parse():
     p.add_argument("--no-skinny", action="store_true", help="leave the skinny-M sub-object out of the ns line")
     p.add_argument("--no-mmdit", action="store_true", help="leave the MMDiT step sub-object out of the ns line")
     p.add_argument("--no-extra", action="store_true", help="leave the C1 and C5 sub-objects out of the ns line")
+    p.add_argument("--profile-run", action="store_true",
+                   help="no timing: run --steps steps of the workload (c5: at M=16 and 256) after one warm step, "
+                        "plus one 256 MiB streaming-read probe (a known byte count for the traffic counters), for "
+                        "rocprofv3 --pmc; prints one JSON line naming what ran")
     p.add_argument("--no-mmdit-kept", action="store_true",
                    help="MMDiT step: leave out the second measurement, with the capture's attention output kept "
                         "for the replay")
@@ -185,6 +189,8 @@ def main():
 
     torch.cuda.set_device(0)
     dev = torch.device("cuda:0")
+    if args.profile_run:
+        return profile_run(args, dev)
     if args.workload in ("skinny", "skinny8"):
         return bench_skinny(args, dev)
     if args.workload == "requant":
@@ -218,6 +224,69 @@ def main():
         out["mmdit"] = mmdit_measure(args, dev, steps=min(args.steps, 5), warmup=min(args.warmup, 2),
                                      with_cpu=not args.no_cpu_baseline)
     print(json.dumps(out), flush=True)
+
+
+PROBE_BYTES = 256 << 20
+
+
+def profile_run(args, dev):
+    """The kernels of one workload for a counter run, untimed: one warm step,
+    then ``--steps`` steps (the site workloads: host-launched fwd + bwd; c5:
+    every site at M = 16, then at M = 256; skinny: the few-token forward
+    over the rotated weight copies), then one streaming read of PROBE_BYTES
+    by lrq_probe_stream_read, whose byte count calibrates FETCH_SIZE."""
+    import math
+
+    import torch
+
+    from loractl_amd import _lib as L
+    from loractl_amd import device as D
+
+    w = args.workload
+    if w in ("ns", "ns8", "c1", "c2", "skinny", "skinny8"):
+        M, K, N, r, alpha, fmt, group = WORKLOADS[w]
+        s = alpha / r
+        wf, x, a, b, dy = make_inputs(M, K, N, r)
+        wt = torch.from_numpy(wf).to(dev)
+        wq = {"int4": lambda: D.quantize_int4(wt, group), "int8": lambda: D.quantize_int8(wt, group),
+              "fp8": lambda: D.quantize_fp8(wt, True)}[fmt]()
+        del wt
+        wq = D.compute_weight(wq)
+        xb, ab, bb, dyb = (torch.from_numpy(v).to(dev).to(torch.bfloat16) for v in (x, a, b, dy))
+        D.reserve(M, N, K, r)
+        if w.startswith("skinny"):
+            row_bytes = wq.data.numel() // 2
+            ncopy = max(2, math.ceil(1.15 * INFINITY_CACHE_BYTES / row_bytes))
+            copies = [wq] + [D.PackedWeight(wq.fmt, wq.n, wq.k, wq.data.clone(), wq.scales.clone(), wq.group,
+                                            wq.per_channel, None, L.LRQ_LAYOUT_BLOCKED) for _ in range(ncopy - 1)]
+
+            def step(i):
+                D.lora_fwd(xb, copies[i % ncopy], ab, bb, s)
+        else:
+            def step(i):
+                _, t = D.lora_fwd(xb, wq, ab, bb, s)
+                D.lora_bwd(xb, dyb, wq, ab, bb, s, t)
+        for i in range(1 + args.steps):
+            step(i)
+        torch.cuda.synchronize()
+        ran = f"{w}: {1 + args.steps} steps"
+    elif w == "c5":
+        ran = []
+        for M in (16, 256):
+            sites = [(M, K, N, 16, 16.0) for _layer in range(C5_LAYERS) for (K, N) in C5_LAYER]
+            ls = LinearSet(dev, sites, seed=5)
+            ls.run(1 + args.steps)
+            torch.cuda.synchronize()
+            ran.append(f"c5 M={M}: {1 + args.steps} steps")
+            del ls
+            torch.cuda.empty_cache()
+        ran = "; ".join(ran)
+    else:
+        raise SystemExit(f"--profile-run covers ns, ns8, c1, c2, c5, skinny, skinny8, not {w}")
+    buf = torch.empty(PROBE_BYTES, dtype=torch.uint8, device=dev)
+    D.probe_stream_read(buf)
+    torch.cuda.synchronize()
+    print(json.dumps({"profile_run": ran, "probe_stream_read_bytes": PROBE_BYTES}), flush=True)
 
 
 RELAUNCH_REPS = 20  # back-to-back repeats of one kernel per graph

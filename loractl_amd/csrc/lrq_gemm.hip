@@ -663,8 +663,12 @@ hipError_t run_fmt(hipStream_t st, int fmt, bool r192, const GemmArgs& a) {
 //     (64 tokens: 0.342 / 0.423, 128 tokens: 0.441 / 0.696); the tiles are
 //     dealt over the CUs, two at a time.
 constexpr double LARGE_STEP_US = 1.86;
-constexpr double MID_T1[2] = {0.342, 0.441}, MID_T2[2] = {0.423, 0.696};
-int g_gemm_path = 0;  // lrq_debug_gemm_path: 0 planned, 1 large tiles, 2 mid 64 tokens, 3 mid 128 tokens
+// per variant MID_64, MID_128: tile tokens, block us alone and shared, and
+// a fixed cost per round of tiles
+constexpr int MID_T[3] = {0, 64, 128};
+constexpr double MID_T1[3] = {0, 0.342, 0.441}, MID_T2[3] = {0, 0.423, 0.696};
+constexpr double MID_FIX[3] = {0, 2.0, 2.0};
+int g_gemm_path = 0;  // lrq_debug_gemm_path: 0 planned, 1 large tiles, 2 + (variant - 1) a mid variant
 
 double large_us(int64_t m, int64_t e, int64_t depth) {
   const SplitPlan p = plan_split(m, e, depth);
@@ -677,36 +681,36 @@ double large_us(int64_t m, int64_t e, int64_t depth) {
   return (double)p.spl * LARGE_STEP_US * f + 2.0 * part / 4.0e6 + 8.0;
 }
 
-double mid_us(int64_t m, int64_t e, int64_t depth, int tt) {
-  const int64_t T = 16 * tt, cus = get_num_cus();
+double mid_us(int64_t m, int64_t e, int64_t depth, int v) {
+  const int64_t T = MID_T[v], cus = get_num_cus();
   const int64_t tiles = (m + T - 1) / T * ((e + 63) / 64);
   const int64_t n = (tiles + cus - 1) / cus, nb = (depth + 63) / 64;
-  const int i = tt == 8 ? 1 : 0;
-  return (double)nb * ((double)(n / 2) * MID_T2[i] + (double)(n % 2) * MID_T1[i]) + 2.0;
+  return (double)nb * ((double)(n / 2) * MID_T2[v] + (double)(n % 2) * MID_T1[v]) +
+         MID_FIX[v] * (double)((n + 1) / 2);
 }
 
+// MID_NONE (the large tiles) or the mid variant a shape takes
 int mid_plan(int64_t m, int64_t e, int64_t depth) {
-  if (m <= 0 || e <= 0) return 0;
-  if (g_gemm_path == 1) return 0;
-  if (g_gemm_path == 2) return 4;
-  if (g_gemm_path == 3) return 8;
+  if (m <= 0 || e <= 0) return MID_NONE;
+  if (g_gemm_path == 1) return MID_NONE;
+  if (g_gemm_path >= 2) return g_gemm_path - 1;
   double best = large_us(m, e, depth);
-  int tt = 0;
-  for (int cand : {4, 8}) {
-    const double t = mid_us(m, e, depth, cand);
+  int pick = MID_NONE;
+  for (int v : {MID_64, MID_128}) {
+    const double t = mid_us(m, e, depth, v);
     if (t < best) {
       best = t;
-      tt = cand;
+      pick = v;
     }
   }
-  return tt;
+  return pick;
 }
 
 template <bool BWD>
 hipError_t dispatch(hipStream_t st, int fmt, const GemmArgs& a) {
   if (a.m == 0 || a.e == 0) return hipSuccess;
-  const int tt = mid_plan(a.m, a.e, a.l);
-  if (tt) return launch_mid(st, fmt, BWD, a, tt);
+  const int mv = mid_plan(a.m, a.e, a.l);
+  if (mv != MID_NONE) return launch_mid(st, fmt, BWD, a, mv);
   const SplitPlan p = plan_split(a.m, a.e, a.l);
   if (p.S <= 1) return run_fmt<BWD, false>(st, fmt, p.r192, a);
   if (!a.part) return hipErrorInvalidValue;
@@ -737,5 +741,5 @@ int64_t gemm_split_floats(int64_t m, int64_t e, int64_t depth) {
   return p.S > 1 ? (int64_t)p.S * m * e : 0;
 }
 hipError_t launch_bwd(hipStream_t st, int fmt, const GemmArgs& a) { return dispatch<true>(st, fmt, a); }
-int gemm_mid_tokens(int64_t m, int64_t e, int64_t depth) { return 16 * mid_plan(m, e, depth); }
+int gemm_mid_tokens(int64_t m, int64_t e, int64_t depth) { return MID_T[mid_plan(m, e, depth)]; }
 void set_gemm_path(int path) { g_gemm_path = path; }

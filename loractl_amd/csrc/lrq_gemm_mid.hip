@@ -332,15 +332,15 @@ __global__ void __launch_bounds__(256, 2) k_mid(GemmArgs a, int tiles_m, int til
 }
 
 template <bool BWD, int FMT>
-hipError_t run_mid(hipStream_t st, const GemmArgs& a, int tt) {
-  const int T = 16 * tt;
+hipError_t run_mid(hipStream_t st, const GemmArgs& a, int variant) {
+  const int T = variant == MID_64 ? 64 : 128;
   const int tiles_m = (int)((a.m + T - 1) / T);
   const int tiles_e = (int)((a.e + MR - 1) / MR);
   const int group_m = tiles_m < 8 ? tiles_m : 8;
   const int ntiles = tiles_m * tiles_e;
-  // two 64-wide blocks per stage with 64-token tiles, one with 128: 64 KiB
-  // of LDS either way, two workgroups per CU
-  if (tt == 8)
+  // k_mid: two 64-wide blocks per stage with 64-token tiles, one with 128;
+  // 64 KiB of LDS in every variant, two workgroups per CU
+  if (variant == MID_128)
     hipLaunchKernelGGL((k_mid<BWD, FMT, 8, 1>), dim3(ntiles), dim3(256), 0, st, a, tiles_m, tiles_e, group_m);
   else
     hipLaunchKernelGGL((k_mid<BWD, FMT, 4, 2>), dim3(ntiles), dim3(256), 0, st, a, tiles_m, tiles_e, group_m);
@@ -349,15 +349,17 @@ hipError_t run_mid(hipStream_t st, const GemmArgs& a, int tt) {
 
 }  // namespace
 
-hipError_t launch_mid(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, int tt) {
+hipError_t launch_mid(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, int variant) {
   if (a.m <= 0 || a.e <= 0) return hipSuccess;
-  if (tt != 4 && tt != 8) return hipErrorInvalidValue;
-  if (a.rp > 64) return hipErrorInvalidValue;
+  if (variant != MID_64 && variant != MID_128) return hipErrorInvalidValue;
+  if (a.rp > 64 || a.rp % 16 != 0) return hipErrorInvalidValue;
   // 32-bit buffer offsets: one tile's activation rows and outputs, the depth
   // run of the weight's block row
-  if ((int64_t)16 * tt * a.l * 2 >= ((int64_t)1 << 31) || (int64_t)16 * tt * a.e * 2 >= ((int64_t)1 << 31))
+  if ((int64_t)128 * a.l * 2 >= ((int64_t)1 << 31) || (int64_t)128 * a.e * 2 >= ((int64_t)1 << 31))
     return hipErrorInvalidValue;
-  if (fmt == LRQ_FMT_INT4) return bwd ? run_mid<true, LRQ_FMT_INT4>(st, a, tt) : run_mid<false, LRQ_FMT_INT4>(st, a, tt);
-  if (fmt == LRQ_FMT_INT8) return bwd ? run_mid<true, LRQ_FMT_INT8>(st, a, tt) : run_mid<false, LRQ_FMT_INT8>(st, a, tt);
-  return bwd ? run_mid<true, LRQ_FMT_FP8>(st, a, tt) : run_mid<false, LRQ_FMT_FP8>(st, a, tt);
+  if (fmt == LRQ_FMT_INT4)
+    return bwd ? run_mid<true, LRQ_FMT_INT4>(st, a, variant) : run_mid<false, LRQ_FMT_INT4>(st, a, variant);
+  if (fmt == LRQ_FMT_INT8)
+    return bwd ? run_mid<true, LRQ_FMT_INT8>(st, a, variant) : run_mid<false, LRQ_FMT_INT8>(st, a, variant);
+  return bwd ? run_mid<true, LRQ_FMT_FP8>(st, a, variant) : run_mid<false, LRQ_FMT_FP8>(st, a, variant);
 }

@@ -60,13 +60,15 @@ hipError_t launch_fwd(hipStream_t st, int fmt, const GemmArgs& a);
 hipError_t launch_bwd(hipStream_t st, int fmt, const GemmArgs& a);
 int64_t gemm_split_floats(int64_t m, int64_t e, int64_t depth);
 int get_num_cus();
-// lrq_gemm_mid.hip: the same products on 64-row tiles of 16 tt tokens (tt 4
-// or 8) over the whole depth, no partials; lrq_gemm.hip's launchers take it
-// when it is modelled faster (gemm_mid_tokens: its tile's tokens, or 0)
-hipError_t launch_mid(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, int tt);
+// lrq_gemm_mid.hip: the same products on 64-row tiles of 64 or 128 tokens
+// over the whole depth, 16 rows per wavefront, no partials (MID_64,
+// MID_128); lrq_gemm.hip's launchers take one when it is modelled faster
+// (gemm_mid_tokens: its tile's tokens, or 0)
+enum { MID_NONE = 0, MID_64 = 1, MID_128 = 2 };
+hipError_t launch_mid(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, int variant);
 int gemm_mid_tokens(int64_t m, int64_t e, int64_t depth);
 // tuning and test hook (lrq_debug_gemm_path): 0 planned, 1 large tiles,
-// 2 mid tiles of 64 tokens, 3 of 128
+// 2 MID_64, 3 MID_128
 void set_gemm_path(int path);
 
 // lrq_skinny.hip: the forward for m <= 16 in one launch. Split workgroups
