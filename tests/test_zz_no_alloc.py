@@ -8,7 +8,7 @@ import pytest
 import torch
 
 import oracle as O
-from gpu_helpers import case_inputs, to_dev
+from gpu_helpers import case_inputs, gemm_path, to_dev
 from loractl_amd import _lib as L
 from loractl_amd import device as D
 
@@ -62,13 +62,19 @@ def test_noalloc_against_the_oracle(cuda):
 
 
 def test_noalloc_rejects_a_shape_beyond_its_scratch(cuda):
-    """256 tokens of a 3072 -> 12288 layer split the GEMM depth into ranges
-    whose f32 partials (about 50-60 MB) exceed the 32 MiB scratch array."""
+    """256 tokens of a 3072 -> 12288 layer on the large tiles split the GEMM
+    depth into ranges whose f32 partials (about 50-60 MB) exceed the 32 MiB
+    scratch array; the planned path (the 128-token tiles, no partials) runs
+    the same shape in the array, bit-identical to lrq_lora_fwd."""
     M, K, N, r = 256, 3072, 12288, 32
     wq, xb, ab, bb = _case(cuda, M, K, N, r, "int4", 5)
     y = torch.empty((M, N), dtype=torch.bfloat16, device=cuda)
     t = torch.empty((M, r), dtype=torch.bfloat16, device=cuda)
     # the array's first 64 KiB hold the few-token kernels' arrival counters
-    with pytest.raises(L.LrqError, match=f"more than its fixed {(32 << 20) - (64 << 10)}"):
-        D.lora_fwd_noalloc(xb, wq, ab, bb, 1.0, y, t)
+    with gemm_path("large"):
+        with pytest.raises(L.LrqError, match=f"more than its fixed {(32 << 20) - (64 << 10)}"):
+            D.lora_fwd_noalloc(xb, wq, ab, bb, 1.0, y, t)
     assert L.LRQ_NOALLOC_SCRATCH_BYTES == 32 << 20
+    (y0, t0), (y1, t1) = _both(cuda, wq, xb, ab, bb, 1.0)
+    assert torch.equal(y0.view(torch.int16), y1.view(torch.int16))
+    assert torch.equal(t0.view(torch.int16), t1.view(torch.int16))
