@@ -215,6 +215,12 @@ pub fn code_name(rc: i32) -> &'static str {
 #[derive(Debug, Clone, Copy, PartialEq, Eq)]
 pub struct DevPtr(pub *mut c_void);
 
+// A device address is a number to the host: it is never dereferenced here,
+// so moving or sharing it across threads is sound (autodiff keeps weight
+// descriptors in backward state, which must be Send).
+unsafe impl Send for DevPtr {}
+unsafe impl Sync for DevPtr {}
+
 impl DevPtr {
     pub const NULL: DevPtr = DevPtr(std::ptr::null_mut());
     fn c<T>(self) -> *const T {

@@ -141,13 +141,80 @@ def test_patch_wires_the_backend_at_the_reference_seams():
         "crates/loractl-core/src/quant.rs",
         "crates/loractl-core/src/rocm.rs",
     }
-    added = "\n".join(l[1:] for l in p.splitlines() if l.startswith("+") and not l.startswith("+++"))
+    added = _added(p)
     for needle in ("    Rocm,", '"rocm" | "hip" => Ok(Self::Rocm)', "BackendKind::Ndarray | BackendKind::Cuda | BackendKind::Rocm",
-                   "(BackendKind::Rocm, p) if p != Precision::Bf16", "BackendKind::Rocm => dispatch_checkpointing",
-                   "B::fused_lora_site(x.clone(), q, delta)", 'rocm = ["burn/rocm", "dep:loractl-rocm-sys"]',
-                   "fn fused_lora_site", "impl<B: Backend> Backward<B, 3> for FusedLoraSite"):
+                   "(BackendKind::Rocm, p) if p != Precision::F32", "dispatch_checkpointing::<Rocm>(",
+                   "B::fused_quant_site(x.clone(), q, Some(delta))", "B::fused_quant_site(x.clone(), q, None)",
+                   'rocm = ["burn/rocm", "dep:loractl-rocm-sys"]', "fn fused_quant_site",
+                   "impl QuantBackend for burn::backend::Rocm", "impl<B: Backend> Backward<B, 3> for FusedLoraSite",
+                   "impl<B: Backend> Backward<B, 1> for QuantSite"):
         assert needle in added, needle
     # the rocm module calls the binding, and only through functions it declares
     rust = _rust_externs()
     for call in re.findall(r"ctx\.(\w+)\(", added):
         assert f"lrq_{call}" in rust or call in ("block",), call
+
+
+def _added(p, path=None):
+    """The added lines of the patch, of one file if `path` is given."""
+    if path is not None:
+        p = p[p.index(f"+++ b/{path}"):]
+        end = p.find("\ndiff ", 1)
+        p = p if end < 0 else p[:end]
+    return "\n".join(l[1:] for l in p.splitlines() if l.startswith("+") and not l.startswith("+++"))
+
+
+def _removed(p):
+    return "\n".join(l[1:] for l in p.splitlines() if l.startswith("-") and not l.startswith("---"))
+
+
+def test_patch_keeps_the_adapters_f32():
+    """The reference trains the adapters (and their AdamW moments) in f32
+    whenever the base is quantized (diffusion_trainer.rs:395-401). The patch
+    keeps that guard, runs the model on Rocm's default f32 element, rounds
+    only the site's operands to bf16, and registers the kernels' f32 dA and
+    dB without a cast."""
+    p = open(PATCH).read()
+    assert "if config.compute.precision != Precision::F32 {" not in _removed(p)
+    added = _added(p)
+    assert "burn::tensor::bf16" not in _added(p, "crates/loractl-core/src/diffusion_trainer.rs")
+    assert "Precision::Bf16" not in added
+    rocm = _added(p, "crates/loractl-core/src/rocm.rs")
+    # operands rounded at the site: x, A and B (and dy in the backward)
+    assert "cast::<B>(xp, FloatDType::BF16)" in rocm and "cast::<B>(xp.primitive.clone(), FloatDType::BF16)" in rocm
+    assert "(cast::<B>(a, FloatDType::BF16), cast::<B>(b, FloatDType::BF16)" in rocm
+    assert rocm.count("cast::<B>(grads.consume::<B>(&ops.node), FloatDType::BF16)") == 2
+    # the kernels write f32 dA [k, r] and dB [r, n]; both are registered as they are
+    assert "Shape::new([k, st.r as usize]), &device, FloatDType::F32" in rocm
+    assert "Shape::new([st.r as usize, n]), &device, FloatDType::F32" in rocm
+    bwd = rocm[rocm.index("if let (Some(node), Some(g)) = (px, dx)"):]
+    bwd = bwd[:bwd.index("\n    }\n}")]
+    assert "grads.register::<B>(node.id, cast::<B>(g, FloatDType::F32));" in bwd      # dx widened to f32
+    assert bwd.count("grads.register::<B>(node.id, g);") == 2                         # dA, dB as they are
+    assert "FloatDType::BF16" not in bwd
+    # y and dx come back widened to the model's f32
+    assert rocm.count("cast::<B>(y, FloatDType::F32)") == 3
+
+
+def test_patch_keeps_one_copy_of_each_quantized_weight():
+    """At load, a site the library packs keeps only the library's blocked
+    copy: the load pass stores the placeholder register_quant_site returns
+    and skips burn's own quantization of the same values; every forward of
+    a quantized site (with or without a delta) goes through the library."""
+    p = open(PATCH).read()
+    trainer = p[p.index("+++ b/crates/loractl-core/src/diffusion_trainer.rs"):]
+    hunk = trainer[trainer.index("register_quant_site"):]
+    hunk = hunk[:hunk.index("\n@@") if "\n@@" in hunk else len(hunk)]
+    reg, quant = hunk.index("register_quant_site"), hunk.index("quantize_linear_weight_chunked")
+    between = hunk[:quant]
+    assert "q.weight = vec![placeholder];" in between and "continue;" in between and reg < quant
+    assert "Err(data) => data," in between
+    # no second registration after burn's chunks are built
+    assert _added(p).count("crate::rocm::register_quant_site") == 1
+    rocm = _added(p, "crates/loractl-core/src/rocm.rs")
+    assert "-> Result<Param<Tensor<B, 2>>, TensorData>" in rocm
+    assert "Param::from_tensor(Tensor::<B, 2>::zeros([1, 1], device))" in rocm
+    # the base-only forward (BaseLinear::forward's quant arm) routes to the library too
+    mm = _added(p, "crates/loractl-core/src/mmdit.rs")
+    assert "B::fused_quant_site(x.clone(), q, None)" in mm
+    assert "ctx.quant_matmul_t(" in rocm and "ctx.quant_matmul_t_bwd(" in rocm
