@@ -774,9 +774,14 @@ static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const ui
       float* tpart = part + round_up((int64_t)sp.S * m * w->k, 64);
       ga.lw = a;
       uint16_t* up = ws.up;
+      // and dA = x^T . u, dB = t^T . dy in the same launch: dB by the split
+      // workgroups (nothing to wait for), dA by each block row's epilogue
+      // once u is in
+      const SkGrads gr{da ? x : nullptr, db ? t : nullptr, da, db};
       LRQ_TRY(run_hot(c, KID_BWD_DX, "bwd_dx", [=] {
-        return launch_skinny(c->stream, fmt, true, ga, b, sp, part, tpart, c->cnt, scaling, up);
+        return launch_skinny(c->stream, fmt, true, ga, b, sp, part, tpart, c->cnt, scaling, up, gr);
       }));
+      return LRQ_OK;
     } else {
       // u = s . dy . B^T   (bf16 [m, rp]: the dx epilogue operand and dA's factor)
       const LoraPlan pu = lora_plan_nt(m, w->n, rp);

@@ -108,9 +108,18 @@ SkinnyPlan skinny_plan(int64_t n, int64_t k, int rp, int num_cus);
 // that is never published, 16 polls at most
 void set_force_wait_timeout(bool on);
 size_t skinny_ws_bytes(const SkinnyPlan& p, int64_t m, int64_t n, int rp);
+// The backward's LoRA factor gradients, folded into its launch (null: not
+// formed): dA = x^T . u (f32 [k, r]) from the forward input x [m, k] and
+// dB = t^T . dy (f32 [r, n]) from the forward's t [m, r].
+struct SkGrads {
+  const uint16_t* x;
+  const uint16_t* t;
+  float* da;
+  float* db;
+};
 hipError_t launch_skinny(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, const uint16_t* A,
                          const SkinnyPlan& p, float* part, float* tpart, uint32_t* cnt, float scaling,
-                         uint16_t* t_out);
+                         uint16_t* t_out, const SkGrads& gr = SkGrads{});
 
 // lrq_lora.hip
 // A split of a LoRA reduction: `tiles` output tiles x `splits` slices of

@@ -73,6 +73,7 @@ struct SkArgs {
   uint16_t* t_out;    // t [m, r] (backward: u [m, rp]), or null
   uint32_t max_polls; // cap of an epilogue's polls for t (SK_MAX_POLLS)
   uint32_t skew;      // added to the awaited stamp: 0 (a test hook sets it to force the timeout)
+  SkGrads gr;         // backward: the LoRA factors' gradients folded into the launch (null: skipped)
 };
 
 // device-scope accesses of the cross-workgroup data: stores written through
@@ -97,6 +98,23 @@ constexpr uint32_t SK_NAN2 = 0x7fc07fc0u;
 LRQ_DEV uint32_t add_dev(uint32_t* c) { return __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, XSCOPE); }
 LRQ_DEV void zero_dev(uint32_t* c) { __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, XSCOPE); }
 
+
+LRQ_DEV void bstore4(rsrc_t r, uint32_t off, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, off, 0, 0);
+}
+
+// One matrix-core step over the tokens, C[i][j] = sum_m P[i][m] Q[j][m], with
+// both operands staged token-minor in LDS as bf16 ([row][16 tokens]): lane
+// (c16, kq) takes tokens 8 kq .. + 8 of row c16 (kq < 2; tokens 16 .. 31 are
+// zero). C element v of lane (c16, kq): row i = 4 kq + v of the P tile,
+// column j = c16 of the Q tile.
+LRQ_DEV f32x4 sk_token_step(const uint16_t* p_rows, const uint16_t* q_rows) {
+  const int lane = threadIdx.x & 63, c16 = lane & 15, kq = lane >> 4;
+  const u32x4 z = {0u, 0u, 0u, 0u};
+  const u32x4 pa = kq < 2 ? *reinterpret_cast<const u32x4*>(p_rows + c16 * 16 + 8 * kq) : z;
+  const u32x4 qb = kq < 2 ? *reinterpret_cast<const u32x4*>(q_rows + c16 * 16 + 8 * kq) : z;
+  return mfma16(as_bf16x8(pa), as_bf16x8(qb), (f32x4){0.0f, 0.0f, 0.0f, 0.0f});
+}
 
 // The epilogue of block row nb (output columns 64 nb .. +64), run by the last
 // workgroup to arrive there (all 256 threads, uniform control flow):
@@ -145,6 +163,14 @@ LRQ_DEV void sk_epilogue(const SkArgs& sa, int64_t nb, float* lds) {
     }
   };
   load_t();
+  // backward with dA: the x tile [16 tokens][64 columns n0 ..] of this block
+  // row (dA rows n0 .. n0 + 63), loaded with the rest (x is [m, E])
+  const bool fold_da = BWD && sa.gr.da != nullptr && TS > 0;
+  u32x2 xv = {0u, 0u};
+  if (fold_da) {
+    const rsrc_t rx = make_rsrc(sa.gr.x, clamp_bytes(M * E * 2));
+    xv = bload8(rx, opaque_u32(live ? (uint32_t)((m * E + n) * 2) : LRQ_OOB));
+  }
   if (TS > 0) {
     const uint32_t want = stamp(__hip_atomic_load(sa.cnt + SK_EPOCH, __ATOMIC_RELAXED, XSCOPE)) + sa.skew;
     // not all published yet: read all of this thread's entries again
@@ -170,6 +196,19 @@ LRQ_DEV void sk_epilogue(const SkArgs& sa, int64_t nb, float* lds) {
 #pragma unroll
     for (int q = 0; q < 16; ++q)
       if (tid + q * SK_NT < rp * 64) bs[tid + q * SK_NT] = (uint16_t)bv[q];
+    if (fold_da) {
+      // x and u token-minor for the dA step: xT [64 columns][16 tokens],
+      // uT [64 ranks][16 tokens] (bf16, after tt and bs)
+      uint16_t* xT = reinterpret_cast<uint16_t*>(lds + 3 * 1024);
+      uint16_t* uT = xT + 64 * 16;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xT[(4 * cq + e) * 16 + m] = (uint16_t)(xv[e >> 1] >> (16 * (e & 1)));
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int i = tid + q * SK_NT;
+        if (i < 16 * rp) uT[(i % rp) * 16 + i / rp] = (uint16_t)(tv[q][0] >> 16);
+      }
+    }
   }
   __syncthreads();
   if (live) {
@@ -209,6 +248,78 @@ LRQ_DEV void sk_epilogue(const SkArgs& sa, int64_t nb, float* lds) {
     o[0] = pack_bf16x2(base[0] * sc[0] + l[0] + bias[0], base[1] * sc[1] + l[1] + bias[1]);
     o[1] = pack_bf16x2(base[2] * sc[2] + l[2] + bias[2], base[3] * sc[3] + l[3] + bias[3]);
     *reinterpret_cast<u32x2*>(a.out + (int64_t)m * E + n) = o;
+  }
+  if (fold_da) {
+    // dA[n0 + i][j] = sum_m x[m][n0 + i] u[m][j] (f32): wave w takes rows
+    // 16 w .. + 16 of the block row, one matrix-core step per rank tile
+    // (ranks past rp read entries never written and are not stored)
+    const uint16_t* xT = reinterpret_cast<const uint16_t*>(lds + 3 * 1024);
+    const uint16_t* uT = xT + 64 * 16;
+    const int w = tid >> 6, kq = (tid & 63) >> 4, c16 = tid & 15;
+    const rsrc_t rda = make_rsrc(sa.gr.da, clamp_bytes(E * r * 4));
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) {
+      const f32x4 c = sk_token_step(xT + w * 256, uT + jt * 256);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int64_t row = n0 + 16 * w + 4 * kq + v;
+        const int j = 16 * jt + c16;
+        const bool ok = row < E && j < r && j < rp;
+        bstore4(rda, opaque_u32(ok ? (uint32_t)((row * r + j) * 4) : LRQ_OOB), c[v]);
+      }
+    }
+  }
+}
+
+// Backward with dB: dB[j][c] = sum_m t[m][j] dy[m][c] (f32 [r, n]) over the
+// depth slice [kt0, kt1) of dy that a u slice has just read, straight from
+// its fragments: xf[i] holds dy[c16][kt0 + 32 st + 8 kq ..] (st = wave + 4 i).
+// Each column has one owner and nothing waits for it. The slice's dy goes
+// to LDS token-minor (dyT [KT columns][16 tokens]) and t likewise (tT [64
+// ranks][16 tokens]); each wave then takes every fourth 16-column tile, all
+// four rank tiles. `lds` holds 128 * TSTEPS * 16 + 1024 bf16; `tq` is this
+// thread's four entries of t (bf16 in the low half), i = tid + 256 q as
+// (token i / 64, rank i % 64).
+template <int TSTEPS>
+LRQ_DEV void sk_fold_db(const SkArgs& sa, int64_t kt0, int64_t kt1, const u32x4 (&xf)[TSTEPS],
+                        const uint32_t (&tq)[4], uint16_t* lds) {
+  static_assert(TSTEPS >= 1 && TSTEPS <= 4, "a u slice of four 32-wide steps per wavefront at most");
+  const GemmArgs& a = sa.g;
+  const int tid = threadIdx.x, lane = tid & 63, c16 = lane & 15, kq = lane >> 4;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t N = a.l;  // the depth of the backward is the weight's n
+  const int r = a.r;
+  constexpr int KT = 128 * TSTEPS;
+  uint16_t* dyT = lds;            // [KT][16]
+  uint16_t* tT = lds + KT * 16;   // [64][16]
+  __syncthreads();  // the slice's reads of the LDS buffer are over
+#pragma unroll
+  for (int i = 0; i < TSTEPS; ++i) {
+    const int cl = (wv + 4 * i) * 32 + 8 * kq;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dyT[(cl + e) * 16 + c16] = (uint16_t)(xf[i][e >> 1] >> (16 * (e & 1)));
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int i = tid + q * SK_NT;
+    tT[(i & 63) * 16 + (i >> 6)] = (uint16_t)tq[q];
+  }
+  __syncthreads();
+  const rsrc_t rdb = make_rsrc(sa.gr.db, clamp_bytes((int64_t)r * N * 4));
+#pragma unroll
+  for (int h = 0; h < 2 * TSTEPS; ++h) {
+    const int ct = wv + 4 * h;  // column tile (16 columns) of the slice
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) {
+      const f32x4 c = sk_token_step(tT + jt * 256, dyT + ct * 256);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int j = 16 * jt + 4 * kq + v;
+        const int64_t col = kt0 + 16 * ct + c16;
+        const bool ok = j < r && col < kt1;
+        bstore4(rdb, opaque_u32(ok ? (uint32_t)(((int64_t)j * N + col) * 4) : LRQ_OOB), c[v]);
+      }
+    }
   }
 }
 
@@ -267,6 +378,17 @@ LRQ_DEV void sk_t_slices(const SkArgs& sa, float* xs, int& last) {
       }
     }
   }
+  // backward with dB: this thread's entries of t (bf16 [m, r]) for the fold,
+  // out with the slice's loads
+  uint32_t tq[4] = {0u, 0u, 0u, 0u};
+  if (BWD && sa.gr.db) {
+    const rsrc_t rt = make_rsrc(sa.gr.t, clamp_bytes(M * r * 2));
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int i = tid + q * SK_NT, mm = i >> 6, j = i & 63;
+      tq[q] = bload2(rt, opaque_u32(mm < M && j < r ? (uint32_t)((mm * r + j) * 2) : LRQ_OOB));
+    }
+  }
   __builtin_amdgcn_sched_barrier(0);
   // every column tile runs (tiles past rp multiply zeros): a matrix-core
   // result read in a block other than the one that wrote it has come back
@@ -299,7 +421,14 @@ LRQ_DEV void sk_t_slices(const SkArgs& sa, float* xs, int& last) {
   __syncthreads();
   if (tid == 0) last = add_dev(sa.cnt + SK_TCNT) + 1 == (uint32_t)TS;
   __syncthreads();
-  if (!last) return;
+  // backward with dB: this slice's columns of dB, once the slice is counted
+  // (the last slice publishes u first)
+  if (!last) {
+    if constexpr (BWD && NT == SK_NT) {
+      if (sa.gr.db) sk_fold_db<TSTEPS>(sa, kt0, kt1, xf, tq, reinterpret_cast<uint16_t*>(xs));
+    }
+    return;
+  }
   const rsrc_t rtp = make_rsrc(sa.tpart, clamp_bytes((int64_t)TS * 16 * rp * 4));
   uint64_t* tfin = reinterpret_cast<uint64_t*>(sa.tpart + (int64_t)TS * 16 * rp);
   // the epoch cannot advance before this workgroup publishes t: every
@@ -327,6 +456,9 @@ LRQ_DEV void sk_t_slices(const SkArgs& sa, float* xs, int& last) {
       __hip_atomic_store(tfin + i, ((uint64_t)mark << 32) | (hb << 16), __ATOMIC_RELAXED, XSCOPE);
       if (sa.t_out && m < M && (BWD || j < r)) sa.t_out[(int64_t)m * (BWD ? rp : r) + j] = (uint16_t)hb;
     }
+  }
+  if constexpr (BWD && NT == SK_NT) {
+    if (sa.gr.db) sk_fold_db<TSTEPS>(sa, kt0, kt1, xf, tq, reinterpret_cast<uint16_t*>(xs));
   }
 }
 
@@ -544,7 +676,9 @@ template <int FMT, bool BWD, bool MQ, int TSTEPS>
 __global__ void __launch_bounds__(SK_NT) k_sk(SkArgs sa) {
   constexpr bool I4 = FMT == LRQ_FMT_INT4;
   // cross-wavefront reduction buffer: [4 wavefronts][64 columns][16 tokens]
-  __shared__ __attribute__((aligned(16))) float xs[4 * 64 * 16];
+  // (backward with dB: the u slices then stage dy and t there, 128 TSTEPS * 16
+  // + 1024 bf16)
+  __shared__ __attribute__((aligned(16))) float xs[4 * 64 * 16 + 512];
   __shared__ int last;  // this workgroup was the last of its block row (t: of the t slices)
   const GemmArgs& a = sa.g;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -856,11 +990,13 @@ size_t skinny_ws_bytes(const SkinnyPlan& p, int64_t m, int64_t n, int rp) {
 
 hipError_t launch_skinny(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, const uint16_t* A,
                          const SkinnyPlan& p, float* part, float* tpart, uint32_t* cnt, float scaling,
-                         uint16_t* t_out) {
+                         uint16_t* t_out, const SkGrads& gr) {
   const int64_t NB = (a.e + 63) / 64;
   if (a.m <= 0 || a.m > 16 || p.S < 1 || p.KS < 1 || p.KS > SK_MAXKS || !cnt || NB > SK_MAX_NB)
     return hipErrorInvalidValue;
-  SkArgs sa{a, A, p, part, tpart, cnt, scaling, t_out, SK_MAX_POLLS, 0u};
+  if (!bwd && (gr.da || gr.db)) return hipErrorInvalidValue;
+  if ((gr.da && !gr.x) || (gr.db && !gr.t) || ((gr.da || gr.db) && (a.rp == 0 || !A))) return hipErrorInvalidValue;
+  SkArgs sa{a, A, p, part, tpart, cnt, scaling, t_out, SK_MAX_POLLS, 0u, gr};
   if (g_force_wait_timeout) {
     sa.max_polls = 16;
     sa.skew = 0x40000000u;  // a stamp no launch publishes
