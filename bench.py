@@ -69,6 +69,7 @@ WORKLOADS = {
     "c3": None,  # one synthetic MMDiT double-stream block's linear set (C3_SITES), image + text stream
     "c5": None,  # a Qwen3-style 28-layer decoder's linears (C5_LAYER), M swept over C5_M
     "mmdit": None,  # C4: the block-checkpointed synthetic MMDiT training step (loractl_amd.mmdit)
+    "fewfit": None,  # few-token (M=16) forward and backward time against weight bytes over FEWFIT_SHAPES
 }
 MMDIT_TOKENS = (4096, 512)  # image tokens (64x64 latent, 2x2 patches), text tokens
 # C3: (d_in, d_out) of QKV, attn-out, MLP up, MLP down, adaLN-mod; int4 g64, r=32, alpha=32
@@ -201,6 +202,9 @@ def main():
         return bench_c5(args, dev)
     if args.workload == "mmdit":
         return bench_mmdit(args, dev)
+    if args.workload == "fewfit":
+        print(json.dumps(few_token_fit(dev)), flush=True)
+        return None
     out, ceilings_for = site_measure(args, dev, args.workload, with_cpu=not args.no_cpu_baseline,
                                      ceilings=args.workload == "ns")
     if args.workload == "ns" and not args.no_skinny:
@@ -218,12 +222,104 @@ def main():
         out["c1"] = site_measure(args, dev, "c1", with_cpu=False)[0]
         torch.cuda.empty_cache()
         out["c5"] = c5_measure(args, dev, (16, 256), with_cpu=False)
+        torch.cuda.empty_cache()
+        out["few_token_fit"] = few_token_fit(dev)
     if args.workload == "ns" and not args.no_mmdit:
         # the metric's second half: MMDiT train steps/s (C4)
         torch.cuda.empty_cache()
         out["mmdit"] = mmdit_measure(args, dev, steps=min(args.steps, 5), warmup=min(args.warmup, 2),
                                      with_cpu=not args.no_cpu_baseline)
     print(json.dumps(out), flush=True)
+
+
+# (K, N, r) of the few-token fit: C5's projections and the north-star layer
+FEWFIT_SHAPES = ((2560, 1024, 16), (2560, 4096, 16), (4096, 2560, 16), (2560, 9728, 16), (9728, 2560, 16),
+                 (3072, 12288, 32))
+
+
+def few_token_fit(dev, M=16, reps=60):
+    """Graph-replay time of one few-token (M=16, int4 g64) forward (y, t) and
+    one backward (dx, dA, dB: one launch each) per shape, with the packed
+    weight rotated past the Infinity Cache, against the bytes the launch
+    must move; then the least-squares line time = intercept + slope * MB
+    over the shapes. The intercept is the per-launch cost that does not
+    depend on the weight (launch, the t / u publication, the epilogue
+    hand-off); 1 / slope is the marginal streaming rate."""
+    import math
+
+    import numpy as np
+    import torch
+
+    from loractl_amd import _lib as L
+    from loractl_amd import device as D
+
+    rows = []
+    for K, N, r in FEWFIT_SHAPES:
+        g = np.random.Generator(np.random.PCG64(K * 7 + N))
+        wq = D.quantize_int4(torch.from_numpy((g.standard_normal((N, K)) * 0.02).astype(np.float32)).to(dev), 64)
+        wb = D.compute_weight(wq)
+        del wq
+        NB, KB = (N + 63) // 64, (K + 63) // 64
+        data_b, scale_b = N * K // 2, 4 * NB * KB * 64  # one section of the blocked layout and its scales
+        ncopy = max(2, math.ceil(1.15 * INFINITY_CACHE_BYTES / (data_b + scale_b)))
+        copies = [wb] + [D.PackedWeight(wb.fmt, wb.n, wb.k, wb.data.clone(), wb.scales.clone(), wb.group,
+                                        wb.per_channel, None, L.LRQ_LAYOUT_BLOCKED) for _ in range(ncopy - 1)]
+        x = torch.from_numpy(g.standard_normal((M, K)).astype(np.float32)).to(dev).to(torch.bfloat16)
+        dy = torch.from_numpy(g.standard_normal((M, N)).astype(np.float32)).to(dev).to(torch.bfloat16)
+        a = torch.from_numpy(g.uniform(-1 / math.sqrt(K), 1 / math.sqrt(K), (K, r)).astype(np.float32)).to(dev).to(
+            torch.bfloat16)
+        b = torch.from_numpy((g.standard_normal((r, N)) * 1e-3).astype(np.float32)).to(dev).to(torch.bfloat16)
+        s = 1.0
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        out = {}
+        with torch.cuda.stream(stream):
+            D.reserve(M, N, K, r)
+            y, t = D.lora_fwd(x, wb, a, b, s)
+            dx, da, db = D.lora_bwd(x, dy, wb, a, b, s, t)
+            torch.cuda.synchronize()
+            for name, call in (("fwd", lambda i: D.lora_fwd(x, copies[i % ncopy], a, b, s, y=y, t=t)),
+                               ("bwd", lambda i: D.lora_bwd(x, dy, copies[i % ncopy], a, b, s, t,
+                                                            out=(dx, da, db)))):
+                call(0)
+                torch.cuda.synchronize()
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, stream=stream):
+                    for i in range(reps):
+                        call(i)
+                graph.replay()
+                torch.cuda.synchronize()
+                best = float("inf")
+                for _ in range(5):
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record(stream)
+                    graph.replay()
+                    e1.record(stream)
+                    torch.cuda.synchronize()
+                    best = min(best, e0.elapsed_time(e1) * 1000.0 / reps)
+                out[name] = best
+                del graph
+        # bytes a launch must move: the weight section and its scales, the
+        # activations and factors read, the outputs written
+        fwd_b = data_b + scale_b + 2 * M * K + 2 * K * r + 2 * r * N + 2 * M * N + 2 * M * r
+        bwd_b = data_b + scale_b + 2 * M * N + 2 * r * N + 2 * K * r + 2 * M * K + 2 * M * r + 2 * M * K \
+            + 4 * K * r + 4 * r * N
+        rows.append({"K": K, "N": N, "r": r, "fwd_us": round(out["fwd"], 2), "bwd_us": round(out["bwd"], 2),
+                     "fwd_mb": round(fwd_b / 1e6, 3), "bwd_mb": round(bwd_b / 1e6, 3)})
+        del copies, wb
+        torch.cuda.empty_cache()
+
+    def fit(xs, ys):
+        A = np.stack([np.ones(len(xs)), np.asarray(xs)], axis=1)
+        (c0, c1), *_ = np.linalg.lstsq(A, np.asarray(ys), rcond=None)
+        return {"intercept_us": round(float(c0), 2), "us_per_mb": round(float(c1), 4),
+                "marginal_tbs": round(1.0 / float(c1), 2) if c1 > 0 else None}
+
+    return {"workload": f"few-token int4-g64 LoRA linear, M={M}, one launch per pass (forward y, t; backward "
+                        "dx, dA, dB), packed weight rotated past the Infinity Cache, graph replay",
+            "shapes": rows,
+            "fwd_fit": fit([r_["fwd_mb"] for r_ in rows], [r_["fwd_us"] for r_ in rows]),
+            "bwd_fit": fit([r_["bwd_mb"] for r_ in rows], [r_["bwd_us"] for r_ in rows])}
 
 
 PROBE_BYTES = 256 << 20
