@@ -506,7 +506,7 @@ LRQ_DEV void sk_int4_pair(const u32x4& v, u32x2& t0, u32x2& t1) {
   t1 = (u32x2){s0[1], s1[1]};
 }
 
-template <int FMT, bool BWD, int WB, int RTN>
+template <int FMT, bool BWD, int WB, int RTN, bool ONEG = false>
 LRQ_DEV void sk_load(const GemmArgs& a, SkRun<FMT, BWD, WB, RTN>& R, int64_t nb, int rt0, int kb0, int nkb) {
   constexpr bool I4 = FMT == LRQ_FMT_INT4;
   constexpr bool GS = FMT != LRQ_FMT_FP8;
@@ -560,9 +560,11 @@ LRQ_DEV void sk_load(const GemmArgs& a, SkRun<FMT, BWD, WB, RTN>& R, int64_t nb,
       }
       if constexpr (GS) {
         if (BWD) {
-          // group of output rows 64 nb + 16 rg .. +16 (groups are >= 32 and aligned)
+          // group of output rows 64 nb + 16 rg .. +16 (groups are >= 32 and
+          // aligned); with groups of 64 or more (ONEG) one for all the row
+          // tiles, loaded once
           const uint32_t kg = (uint32_t)((nb * 64 + rg * 16) >> a.gshift);
-          R.sc[b][rt] = bloadf(rs, opaque_u32(ok ? (uint32_t)((kg * NP + dpos) * 4) : LRQ_OOB));
+          if (!ONEG || rt == 0) R.sc[b][rt] = bloadf(rs, opaque_u32(ok ? (uint32_t)((kg * NP + dpos) * 4) : LRQ_OOB));
         } else {
           const uint32_t j = (kb * 64u + (uint32_t)kd) >> a.gshift;
           R.sc[b][rt] = bloadf(rs, opaque_u32(ok ? (j * 64u + (uint32_t)(rg * 16 + c16)) * 4u : LRQ_OOB));
@@ -590,7 +592,7 @@ LRQ_DEV void sk_math(const GemmArgs& a, const SkRun<FMT, BWD, WB, RTN>& R, f32x4
 #pragma unroll
       for (int p = 0; p < RTN / 2; ++p) sk_int4_pair(R.w4[b][p], w4[2 * p], w4[2 * p + 1]);
     }
-    if constexpr (MQ) {
+    if constexpr (MQ && !BWD) {
       const u32x4 ones = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
       f32x4 xsum = {0.0f, 0.0f, 0.0f, 0.0f};
       u32x4 xp[2];
@@ -646,7 +648,7 @@ LRQ_DEV void sk_math(const GemmArgs& a, const SkRun<FMT, BWD, WB, RTN>& R, f32x4
             fp8x4_to_f32(R.w8[b][rt][jj][0], f);
             fp8x4_to_f32(R.w8[b][rt][jj][1], f + 4);
           }
-          const float S = R.sc[b][(I4 || I8) ? rt : 0];
+          const float S = R.sc[b][(I4 || I8) && !MQ ? rt : 0];
 #pragma unroll
           for (int e = 0; e < 8; ++e) f[e] = row_bcast_n(S, 8 * jj + e) * f[e];
 #pragma unroll
@@ -671,6 +673,9 @@ LRQ_DEV void sk_math(const GemmArgs& a, const SkRun<FMT, BWD, WB, RTN>& R, f32x4
 // is multiplied into fresh accumulators, and the block's partial is scaled
 // in f32: s * (sum x (128 + u) - 136 sum x) = s * sum x q. The block sums of
 // x come from one more matrix-core step against ones.
+// MQ in the backward (int4 or int8, groups of 64 or more): one scale group
+// over a block row's 64 output rows, so its per-depth scales are loaded
+// once for the four row tiles.
 // TSTEPS: 32-wide k steps per wavefront of a t (u) slice (1, 2 or 4)
 template <int FMT, bool BWD, bool MQ, int TSTEPS>
 __global__ void __launch_bounds__(SK_NT) k_sk(SkArgs sa) {
@@ -705,7 +710,7 @@ __global__ void __launch_bounds__(SK_NT) k_sk(SkArgs sa) {
   const int kb0 = kbs + (nks * wv) / 4, nkb = kbs + (nks * (wv + 1)) / 4 - kb0;  // this wavefront's run
 
   SkRun<FMT, BWD, SK_WB, 4> R;
-  sk_load<FMT, BWD, SK_WB, 4>(a, R, nb, 0, kb0, nkb);
+  sk_load<FMT, BWD, SK_WB, 4, BWD && MQ>(a, R, nb, 0, kb0, nkb);
 
   // keep every load ahead of the math (the scheduler would otherwise trade
   // loads in flight for registers)
@@ -1036,7 +1041,11 @@ hipError_t launch_skinny(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, c
   }
   if (fmt == LRQ_FMT_INT4) {
     if (bwd) {
-      SK_LAUNCH(LRQ_FMT_INT4, true, false)
+      if (a.gshift >= 6) {
+        SK_LAUNCH(LRQ_FMT_INT4, true, true)
+      } else {
+        SK_LAUNCH(LRQ_FMT_INT4, true, false)
+      }
     } else if (a.gshift >= 6) {
       SK_LAUNCH(LRQ_FMT_INT4, false, true)
     } else {
@@ -1044,7 +1053,11 @@ hipError_t launch_skinny(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, c
     }
   } else if (fmt == LRQ_FMT_INT8) {
     if (bwd) {
-      SK_LAUNCH(LRQ_FMT_INT8, true, false)
+      if (a.gshift >= 6) {
+        SK_LAUNCH(LRQ_FMT_INT8, true, true)
+      } else {
+        SK_LAUNCH(LRQ_FMT_INT8, true, false)
+      }
     } else {
       SK_LAUNCH(LRQ_FMT_INT8, false, false)
     }
