@@ -61,6 +61,10 @@ constexpr int SK_NT = 256;     // threads per workgroup (4 wavefronts)
 constexpr int SK_MAXKS = 16;   // reduction blocks per split, at most
 constexpr int SK_TMAX = 32;    // t (u) slices, at most, while a slice needs no more than 4 steps per wavefront
 constexpr int SK_WB = SK_MAXKS / 4;  // blocks per wavefront run, at most
+// floats of k_sk's LDS buffer: the cross-wavefront reduction [4][64][16],
+// or a t slice's A^T (rank 32 by 512 depths, rank 64 by 256), or a u
+// slice's dy and t for the folded dB
+constexpr int SK_LDSF = 8704;
 
 struct SkArgs {
   GemmArgs g;
@@ -329,7 +333,7 @@ LRQ_DEV void sk_fold_db(const SkArgs& sa, int64_t kt0, int64_t kt1, const u32x4 
 // to finish sums the slices in order and publishes t stamped with the
 // launch's epoch. `xs` is the kernel's LDS buffer (4096 floats), `last` a
 // shared flag.
-template <bool BWD, int TSTEPS, int NT = SK_NT>
+template <bool BWD, int TSTEPS, int NT, int LDSF>
 LRQ_DEV void sk_t_slices(const SkArgs& sa, float* xs, int& last) {
   const GemmArgs& a = sa.g;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -349,25 +353,54 @@ LRQ_DEV void sk_t_slices(const SkArgs& sa, float* xs, int& last) {
   for (int jt = 0; jt < 4; ++jt) acc[jt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
   // every load of the slice (at most 4 * TSTEPS steps) is issued at once
   // (out-of-range ones read zero), then the matrix-core steps run as they land
+  // The factor operand, lane (c16, kq) of rank tile jt: rank 16 jt + c16 at
+  // depths k .. k + 7. Backward: B [r, n] rows as stored, one 16-byte load.
+  // Forward: A [k, r] is rank-contiguous, so (when the rank is a multiple of
+  // 8 and the slice's A^T fits the LDS buffer) the slice's rows come in as
+  // 16-byte runs, go to LDS transposed (aT [rp][KT + 8] bf16, the padding
+  // spreads a read's 16 rows over the banks) and are read back as 16-byte
+  // runs; otherwise as 2-byte pairs.
+  constexpr int KT = 128 * TSTEPS, AST = KT + 8;
+  const bool staged = !BWD && (r & 7) == 0 && rp * AST * 2 <= LDSF * 4;
   u32x4 xf[TSTEPS];
-  uint32_t bw[TSTEPS][4][4];
+  u32x4 bw[TSTEPS][4];
+  // (depth, 8-rank run) pairs per thread, at most: the largest rank (a
+  // multiple of 16, at most 64) whose A^T fits the buffer
+  constexpr int RPMAX = ((LDSF * 4) / (2 * AST)) / 16 * 16 < 64 ? ((LDSF * 4) / (2 * AST)) / 16 * 16 : 64;
+  constexpr int AQ = (KT * (RPMAX / 8) + NT - 1) / NT;
+  u32x4 av[AQ > 0 ? AQ : 1];
 #pragma unroll
   for (int i = 0; i < TSTEPS; ++i) {
-    {
+    const int st = wv + (NT / 64) * i;
+    const int64_t k = kt0 + (int64_t)st * 32 + kq * 8;
+    const bool kok = st < nsteps && k < kt1;  // K % 8 == 0 and slices are multiples of 32
+    xf[i] = bload16(rx, opaque_u32(kok ? (uint32_t)(((int64_t)c16 * K + k) * 2) : LRQ_OOB));
+  }
+  if (staged) {
+    // pair i = tid + NT q: depth i / (rp / 8) of the slice, ranks 8 (i % (rp / 8)) ..
+    const int jb = rp >> 3;
+#pragma unroll
+    for (int q = 0; q < AQ; ++q) {
+      const int i = tid + NT * q, kk = i / jb, j0 = (i % jb) * 8;
+      const bool ok = kk < KT && kt0 + kk < kt1 && j0 < r;
+      av[q] = bload16(ra, opaque_u32(ok ? (uint32_t)(((kt0 + kk) * r + j0) * 2) : LRQ_OOB));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < TSTEPS; ++i) {
       const int st = wv + (NT / 64) * i;
       const int64_t k = kt0 + (int64_t)st * 32 + kq * 8;
-      const bool kok = st < nsteps && k < kt1;  // K % 8 == 0 and slices are multiples of 32
-      xf[i] = bload16(rx, opaque_u32(kok ? (uint32_t)(((int64_t)c16 * K + k) * 2) : LRQ_OOB));
+      const bool kok = st < nsteps && k < kt1;
 #pragma unroll
       for (int jt = 0; jt < 4; ++jt) {
         const int j = jt * 16 + c16;
         const bool ok = kok && j < r;
+        if (BWD) {
+          // B[j][k .. k + 7]: 16 bytes (the depth is a multiple of 8)
+          bw[i][jt] = bload16(ra, opaque_u32(ok ? (uint32_t)(((int64_t)j * K + k) * 2) : LRQ_OOB));
+        } else {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          if (BWD) {
-            // B[j][k + 2q], B[j][k + 2q + 1] (one dword: the depth is a multiple of 8)
-            bw[i][jt][q] = bload4(ra, opaque_u32(ok ? (uint32_t)(((int64_t)j * K + k + 2 * q) * 2) : LRQ_OOB));
-          } else {
+          for (int q = 0; q < 4; ++q) {
             // A[k + 2q][j], A[k + 2q + 1][j]
             const uint32_t off = (uint32_t)(((k + 2 * q) * r + j) * 2);
             const uint32_t lo = bload2(ra, opaque_u32(ok ? off : LRQ_OOB));
@@ -390,16 +423,41 @@ LRQ_DEV void sk_t_slices(const SkArgs& sa, float* xs, int& last) {
     }
   }
   __builtin_amdgcn_sched_barrier(0);
+  if (staged) {
+    // A^T of the slice into LDS (every entry of ranks < rp and depths < KT
+    // written, zeros outside A), then each lane's runs out of it
+    uint16_t* aT = reinterpret_cast<uint16_t*>(xs);
+    const int jb = rp >> 3;
+#pragma unroll
+    for (int q = 0; q < AQ; ++q) {
+      const int i = tid + NT * q, kk = i / jb, j0 = (i % jb) * 8;
+      if (kk < KT) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) aT[(j0 + e) * AST + kk] = (uint16_t)(av[q][e >> 1] >> (16 * (e & 1)));
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < TSTEPS; ++i) {
+      const int st = wv + (NT / 64) * i;
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) {
+        const int j = jt * 16 + c16;
+        // (steps past the slice, which 512-thread workgroups have, read zeros:
+        // their x is zero, and zero times a stale NaN would not be)
+        bw[i][jt] = j < rp && st * 32 < KT ? *reinterpret_cast<const u32x4*>(aT + j * AST + st * 32 + kq * 8) : zero4();
+      }
+    }
+  }
   // every column tile runs (tiles past rp multiply zeros): a matrix-core
   // result read in a block other than the one that wrote it has come back
   // stale here, so the steps stay branch-free
 #pragma unroll
   for (int i = 0; i < TSTEPS; ++i)
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt)
-      acc[jt] = mfma16(as_bf16x8(xf[i]), as_bf16x8((u32x4){bw[i][jt][0], bw[i][jt][1], bw[i][jt][2], bw[i][jt][3]}),
-                       acc[jt]);
+    for (int jt = 0; jt < 4; ++jt) acc[jt] = mfma16(as_bf16x8(xf[i]), as_bf16x8(bw[i][jt]), acc[jt]);
   // reduce the four wavefronts; C element v of lane l: token 4*(l/16) + v, column l%16
+  if (staged) __syncthreads();  // every read of aT is over
   float* tred = xs;  // [NT / 64][16][64]
 #pragma unroll
   for (int jt = 0; jt < 4; ++jt)
@@ -683,7 +741,7 @@ __global__ void __launch_bounds__(SK_NT) k_sk(SkArgs sa) {
   // cross-wavefront reduction buffer: [4 wavefronts][64 columns][16 tokens]
   // (backward with dB: the u slices then stage dy and t there, 128 TSTEPS * 16
   // + 1024 bf16)
-  __shared__ __attribute__((aligned(16))) float xs[4 * 64 * 16 + 512];
+  __shared__ __attribute__((aligned(16))) float xs[SK_LDSF];
   __shared__ int last;  // this workgroup was the last of its block row (t: of the t slices)
   const GemmArgs& a = sa.g;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -694,7 +752,7 @@ __global__ void __launch_bounds__(SK_NT) k_sk(SkArgs sa) {
   const int TS = sa.p.TS;
 
   if ((int)blockIdx.x < TS) {
-    sk_t_slices<BWD, TSTEPS>(sa, xs, last);
+    sk_t_slices<BWD, TSTEPS, SK_NT, SK_LDSF>(sa, xs, last);
     return;
   }
 
@@ -831,7 +889,7 @@ __global__ void __launch_bounds__(NT) k_skf(SkArgs sa) {
   const int64_t KB = (K + 63) / 64;
   const int TS = sa.p.TS, rp = a.rp;
   if ((int)blockIdx.x < TS) {
-    sk_t_slices<false, TSTEPS, NT>(sa, xs, last);
+    sk_t_slices<false, TSTEPS, NT, (XS > NW * 1024 ? XS : NW * 1024)>(sa, xs, last);
     return;
   }
   const int64_t hb = (int64_t)blockIdx.x - TS;  // this workgroup's rows: tiles RT (hb % (4 / RT)) .. of block row nb
