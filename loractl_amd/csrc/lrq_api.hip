@@ -661,6 +661,26 @@ static int fwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t 
   if (lora) {
     const int rp = (int)round_up(r, 16);
     LRQ_TRY(check_lora_shapes(c, m, w->n, w->k, rp));
+    // mid-size tiles at rank 8 or 16: t is formed in the same launch by
+    // workgroups ahead of the tiles (no side launch)
+    const int64_t G = (m + 63) / 64, fs = (w->k + MID_FOLD_KT - 1) / MID_FOLD_KT;
+    if ((r == 8 || r == 16) && gemm_mid_tokens(m, w->n, w->k) > 0 && aligned16(a) && t_out && aligned16(t_out) &&
+        2 * G <= SK_MAX_NB) {
+      LRQ_TRY(acquire_ws(c, src, (size_t)fs * G * 64 * 16 * 4, &ws, &cnt));
+      ga.fold = force_wait_timeout() ? -1 : 1;
+      ga.fold_slices = (int)fs;
+      ga.fold_wgs = (int)round_up(fs * G, 8);
+      ga.fpart = reinterpret_cast<float*>(ws);
+      ga.fcnt = cnt;
+      ga.lact = a;
+      ga.lw = b;
+      ga.fscale = scaling;
+      ga.fout = t_out;
+      ga.fout_ld = (int)r;
+      ga.r = (int)r;
+      ga.rp = rp;
+      return run_hot(c, KID_FWD_MAIN, "fwd_main", [=] { return launch_fwd(c->stream, fmt, ga); });
+    }
     LRQ_TRY(acquire_ws(c, src, lora_layout(nullptr, m, w->n, w->k, rp, true).bytes, &ws, &cnt));
     LoraWs lw = lora_layout(ws, m, w->n, w->k, rp, true);
     // t = s . x . A   (bf16 [m, rp] for the fused step, [m, r] for the caller)
@@ -763,7 +783,14 @@ static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const ui
     const bool few = dx && m >= 1 && m <= 16;
     const SkinnyPlan sp = skinny_plan(w->k, w->n, rp, get_num_cus());
     const size_t lbytes = lora_layout(nullptr, m, w->n, w->k, rp).bytes;
-    LRQ_TRY(ensure_ws(c, lbytes + (few ? skinny_ws_bytes(sp, m, w->k, rp) : 0)));
+    // mid-size tiles at rank 8 or 16: u is formed in the input gradient's
+    // launch by workgroups ahead of the tiles (partials after the LoRA
+    // workspace)
+    const int64_t G = (m + 63) / 64, fs = (w->n + MID_FOLD_KT - 1) / MID_FOLD_KT;
+    const bool fold = !few && dx && (r == 8 || r == 16) && gemm_mid_tokens(m, w->k, w->n) > 0 && aligned16(a) &&
+                      2 * G <= SK_MAX_NB;
+    const size_t fbytes = fold ? (size_t)fs * G * 64 * 16 * 4 : 0;
+    LRQ_TRY(ensure_ws(c, lbytes + (few ? skinny_ws_bytes(sp, m, w->k, rp) : fbytes)));
     LoraWs ws = lora_layout(c->ws, m, w->n, w->k, rp);
     ga.r = (int)r;
     ga.rp = rp;
@@ -782,6 +809,19 @@ static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const ui
         return launch_skinny(c->stream, fmt, true, ga, b, sp, part, tpart, c->cnt, scaling, up, gr);
       }));
       return LRQ_OK;
+    } else if (fold) {
+      // u (stored to the workspace for dA) from the fold's workgroups
+      ga.fold = force_wait_timeout() ? -1 : 1;
+      ga.fold_slices = (int)fs;
+      ga.fold_wgs = (int)round_up(fs * G, 8);
+      ga.fpart = reinterpret_cast<float*>(c->ws + lbytes);
+      ga.fcnt = c->cnt;
+      ga.lact = b;
+      ga.lw = a;
+      ga.fscale = scaling;
+      ga.fout = ws.up;
+      ga.fout_ld = rp;
+      LRQ_TRY(run_hot(c, KID_BWD_DX, "bwd_dx", [=] { return launch_bwd(c->stream, fmt, ga); }));
     } else {
       // u = s . dy . B^T   (bf16 [m, rp]: the dx epilogue operand and dA's factor)
       const LoraPlan pu = lora_plan_nt(m, w->n, rp);

@@ -36,6 +36,19 @@
 //   - epilogue: the LoRA term as rank-wide matrix-core steps (the tile's
 //     token-side rows t or u and weight-side rows B^T or A from the
 //     workspace), the forward fp8 channel scales and the bias, bf16 stores;
+//   - FOLD (rank 8 or 16): the token-side rows are formed in the same
+//     launch, so no side launch precedes it. The first workgroups of the
+//     grid (dispatched first, on the CU slots the tiles leave free) each
+//     take 64 tokens and a depth slice of 384: t = x . A (or u = dy . B^T)
+//     as matrix-core steps, factor rows in the A role; f32 partials at
+//     device scope, the last slice of a group sums them in order, stores
+//     bf16(s . sum) (t for the caller, u for dA) and publishes the group's
+//     ready flag stamped with the launch's epoch. A tile waits for its
+//     groups' flags before its LoRA step (bounded: it never waits for a
+//     workgroup that is not running, and a wait that runs out flags a
+//     failure and uses NaN). The weight-side rows come from the raw factor
+//     (B across its rows, divided by an fp8 weight scale; A's rows). The
+//     last tile to finish clears the flags and advances the epoch;
 //   - tile order: the tiles are cut into groups of up to eight token tiles
 //     by all row tiles, token tile fastest, and each XCD (own L2) takes a
 //     contiguous range, so an XCD's tiles share a few token tiles of the
@@ -49,6 +62,20 @@
 
 namespace {
 
+// device-scope accesses of the fold's cross-workgroup data (written through
+// and read past the per-XCD L2s), as in lrq_skinny.hip
+constexpr int MXSCOPE = __HIP_MEMORY_SCOPE_AGENT;
+LRQ_DEV uint32_t madd_dev(uint32_t* c) { return __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, MXSCOPE); }
+LRQ_DEV void mzero_dev(uint32_t* c) { __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, MXSCOPE); }
+LRQ_DEV uint32_t mload_dev(const uint32_t* c) { return __hip_atomic_load(c, __ATOMIC_RELAXED, MXSCOPE); }
+LRQ_DEV u32x4 mbload16_dev(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 16); }
+LRQ_DEV void mstore16_dev(rsrc_t r, uint32_t off, const u32x4& v) { __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, 16); }
+LRQ_DEV void mstore8_dev(rsrc_t r, uint32_t off, const u32x2& v) { __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, 16); }
+LRQ_DEV uint32_t mstamp(uint32_t ep) { return ep + 1 == 0 ? 1u : ep + 1; }
+constexpr uint32_t MID_MAX_POLLS = 1u << 22;  // about 0.2 s of s_sleep 2
+// the fold's counters: per 64-token group the slices' arrivals at [0, G)
+// and the ready flags at [G, 2 G)
+
 constexpr int MD = 64;    // depth per step (one 64 x 64 weight block)
 constexpr int MR = 64;    // rows per tile: four wavefronts of 16
 constexpr int MST = 4;    // pipeline stages
@@ -57,7 +84,95 @@ constexpr int MST = 4;    // pipeline stages
 // quarter-wavefront reads at one logical chunk cover all 64 banks
 LRQ_DEV int mswz(int r) { return (r >> 1) & 7; }
 
-template <bool BWD, int FMT, int TT, int SD>
+// FOLD: workgroup fw of the factor workgroups: 64-token group fw / fold_slices,
+// depth slice fw % fold_slices. Wavefront w takes tokens 16 w .. + 16 of the
+// group; each of its lanes loads the group's token row 16 w + (l & 15) at
+// depths 32 ss + 8 (l >> 4) .. + 8 of the slice (every load of the slice at
+// once) and the factor fragment of the same depths for rank l & 15:
+// forward A's rows staged transposed in LDS (aT [16][FKT + 8]), backward B's
+// rows read directly. `lds` holds 16 (FKT + 8) bf16. `want` is the
+// launch's stamp.
+template <bool BWD>
+LRQ_DEV void mid_fold_slice(const GemmArgs& a, int fw, uint16_t* lds, uint32_t want) {
+  constexpr int FKT = MID_FOLD_KT, NSS = FKT / 32, AST = FKT + 8;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c16 = lane & 15, kq = lane >> 4;
+  const int fs = a.fold_slices, g = fw / fs, sl = fw % fs;
+  const int64_t M = a.m, D = a.l, Mp = (M + 63) / 64 * 64;
+  const int r = a.r;
+  const int64_t k0 = (int64_t)sl * FKT, k1 = k0 + FKT < D ? k0 + FKT : D;
+  const int64_t tok = (int64_t)g * 64 + 16 * w + c16;
+  const rsrc_t rx = make_rsrc(a.act, clamp_bytes(M * D * 2));
+  const rsrc_t rf = make_rsrc(a.lact, clamp_bytes(D * r * 2));
+  u32x4 xf[NSS], bf[NSS];
+#pragma unroll
+  for (int ss = 0; ss < NSS; ++ss) {
+    const int64_t k = k0 + 32 * ss + 8 * kq;
+    xf[ss] = bload16(rx, opaque_u32(tok < M && k < k1 ? (uint32_t)((tok * D + k) * 2) : LRQ_OOB));
+    if (BWD) bf[ss] = bload16(rf, opaque_u32(c16 < r && k < k1 ? (uint32_t)(((int64_t)c16 * D + k) * 2) : LRQ_OOB));
+  }
+  if (!BWD) {
+    // A [D][r] rows of the slice, 8 ranks per 16-byte run: pair i = tid +
+    // 256 q is depth i / 2, ranks 8 (i % 2) ..; zeros past the rank or depth
+    constexpr int AQ = 2 * FKT / 256;
+    u32x4 av[AQ];
+#pragma unroll
+    for (int qq = 0; qq < AQ; ++qq) {
+      const int i = tid + 256 * qq, dd = i >> 1, j0 = 8 * (i & 1);
+      av[qq] = bload16(rf, opaque_u32(k0 + dd < k1 && j0 < r ? (uint32_t)(((k0 + dd) * r + j0) * 2) : LRQ_OOB));
+    }
+#pragma unroll
+    for (int qq = 0; qq < AQ; ++qq) {
+      const int i = tid + 256 * qq, dd = i >> 1, j0 = 8 * (i & 1);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) lds[(j0 + e) * AST + dd] = (uint16_t)(av[qq][e >> 1] >> (16 * (e & 1)));
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ss = 0; ss < NSS; ++ss) bf[ss] = *reinterpret_cast<const u32x4*>(lds + c16 * AST + 32 * ss + 8 * kq);
+  }
+  // C element v of lane (c16, kq): rank 4 kq + v, token 16 w + c16
+  f32x4 acc = acc_zero4();
+#pragma unroll
+  for (int ss = 0; ss < NSS; ++ss) acc = mfma16(as_bf16x8(bf[ss]), as_bf16x8(xf[ss]), acc);
+  const rsrc_t rp = make_rsrc(a.fpart, clamp_bytes((int64_t)fs * Mp * 16 * 4));
+  mstore16_dev(rp, opaque_u32((uint32_t)((((int64_t)sl * Mp + tok) * 16 + 4 * kq) * 4)), __builtin_bit_cast(u32x4, acc));
+  // counted once the partial is acknowledged; the last slice of the group
+  // sums the slices in order, stores the factor and publishes the flag
+  __builtin_amdgcn_s_waitcnt(0);
+  __shared__ int last;
+  __syncthreads();
+  const int64_t G = (M + 63) / 64;
+  if (tid == 0) {
+    last = madd_dev(a.fcnt + g) + 1 == (uint32_t)fs;
+    if (last) mzero_dev(a.fcnt + g);
+  }
+  __syncthreads();
+  if (!last) return;
+  // thread: token g 64 + tid / 4, ranks 4 (tid % 4) ..
+  const int64_t tk = (int64_t)g * 64 + (tid >> 2);
+  const int rq = 4 * (tid & 3);
+  f32x4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int s0 = 0; s0 < fs; s0 += 8) {
+    u32x4 pv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      pv[u] = mbload16_dev(rp, opaque_u32(s0 + u < fs ? (uint32_t)((((int64_t)(s0 + u) * Mp + tk) * 16 + rq) * 4) : LRQ_OOB));
+#pragma unroll
+    for (int u = 0; u < 8; ++u) sum += __builtin_bit_cast(f32x4, pv[u]);
+  }
+  if (a.fout && tk < M && rq < a.fout_ld) {
+    const rsrc_t ro = make_rsrc(a.fout, clamp_bytes(M * a.fout_ld * 2));
+    const u32x2 o = {pack_bf16x2(a.fscale * sum[0], a.fscale * sum[1]), pack_bf16x2(a.fscale * sum[2], a.fscale * sum[3])};
+    mstore8_dev(ro, opaque_u32((uint32_t)((tk * a.fout_ld + rq) * 2)), o);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) __hip_atomic_store(a.fcnt + G + g, want, __ATOMIC_RELAXED, MXSCOPE);
+}
+
+template <bool BWD, int FMT, int TT, int SD, bool FOLD>
 __global__ void __launch_bounds__(256, 2) k_mid(GemmArgs a, int tiles_m, int tiles_e, int group_m) {
   constexpr bool I4 = FMT == LRQ_FMT_INT4;
   constexpr bool I8 = FMT == LRQ_FMT_INT8;
@@ -73,7 +188,20 @@ __global__ void __launch_bounds__(256, 2) k_mid(GemmArgs a, int tiles_m, int til
   __shared__ __attribute__((aligned(16))) uint16_t sx3[XB];
 
   const int ntiles = tiles_m * tiles_e;
-  const int lt = xcd_remap((int)blockIdx.x, ntiles);
+  // FOLD: the launch's stamp, and the factor workgroups ahead of the tiles
+  // (the test hook, a.fold < 0, makes the tiles wait for a stamp no
+  // launch publishes)
+  uint32_t want = 0;
+  if (FOLD) {
+    const uint32_t stamp = mstamp(mload_dev(a.fcnt + SK_EPOCH));
+    if ((int)blockIdx.x < a.fold_wgs) {
+      if ((int)blockIdx.x < a.fold_slices * (int)((a.m + 63) / 64)) mid_fold_slice<BWD>(a, (int)blockIdx.x, sx0, stamp);
+      return;
+    }
+    want = stamp + (a.fold < 0 ? 0x40000000u : 0u);
+  }
+  const int vb = FOLD ? (int)blockIdx.x - a.fold_wgs : (int)blockIdx.x;
+  const int lt = xcd_remap(vb, ntiles);
   const int per = group_m * tiles_e;
   const int grp = lt / per, within = lt % per;
   const int gm = min(group_m, tiles_m - grp * group_m);
@@ -252,6 +380,28 @@ __global__ void __launch_bounds__(256, 2) k_mid(GemmArgs a, int tiles_m, int til
       }
   };
 
+  // FOLD: the weight-side factor rows of the LoRA step, fetched first (row
+  // e0 + 16w + l16; ranks 8q .. + 8, q < 2): forward B [r][E] across its
+  // rows, backward A [E][r] as stored
+  const int64_t frow = e0 + 16 * w + l16;
+  u32x4 fla = zero4();
+  if (FOLD) {
+    const int fr_r = a.r;
+    if (!BWD) {
+      const rsrc_t rb = make_rsrc(a.lw, clamp_bytes((int64_t)fr_r * E * 2));
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const int j = 8 * q + e;
+        const uint32_t lo = bload2(rb, opaque_u32(q < 2 && j < fr_r && frow < E ? (uint32_t)((j * E + frow) * 2) : LRQ_OOB));
+        const uint32_t hi =
+            bload2(rb, opaque_u32(q < 2 && j + 1 < fr_r && frow < E ? (uint32_t)(((j + 1) * E + frow) * 2) : LRQ_OOB));
+        fla[e >> 1] = lo | (hi << 16);
+      }
+    } else {
+      const rsrc_t ra = make_rsrc(a.lw, clamp_bytes(E * fr_r * 2));
+      fla = bload16(ra, opaque_u32(q < 2 && 8 * q < fr_r && frow < E ? (uint32_t)((frow * fr_r + 8 * q) * 2) : LRQ_OOB));
+    }
+  }
   // prologue: stage 0's weights, then stages 0 .. MST-2 of activations
   // each followed by the next stage's weights; stage 0 dequantized
   load_w(0, 0);
@@ -276,7 +426,47 @@ __global__ void __launch_bounds__(256, 2) k_mid(GemmArgs a, int tiles_m, int til
 
   // ---- epilogue
   const int rp = a.rp;
-  if (rp > 0) {
+  if (FOLD) {
+    // wait for the token-side factor of the tile's 64-token groups (lane
+    // i < T / 64 of wavefront 0 polls group m0 / 64 + i), bounded
+    __shared__ int fold_bad;
+    const int64_t G = (M + 63) / 64;
+    if (w == 0) {
+      const int64_t gi = m0 / 64 + lane;
+      const bool mine = lane < T / 64 && gi < G;
+      uint32_t polls = 0;
+      const uint32_t cap = a.fold < 0 ? 16u : MID_MAX_POLLS;  // the test hook: 16 polls
+      bool ok = !mine || mload_dev(a.fcnt + G + gi) == want;
+      while (!__all(ok) && polls < cap) {
+        __builtin_amdgcn_s_sleep(2);
+        ++polls;
+        ok = !mine || mload_dev(a.fcnt + G + gi) == want;
+      }
+      if (lane == 0) {
+        fold_bad = __all(ok) ? 0 : 1;
+        if (!__all(ok)) __hip_atomic_store(a.fcnt + SK_FAIL, 1u, __ATOMIC_RELAXED, MXSCOPE);
+      }
+    }
+    __syncthreads();
+    // the LoRA step: weight-side rows (A role) from the prefetched factor,
+    // the tile's factor rows (B role) read past the L2s; forward fp8 rows
+    // divided by the weight scale the epilogue multiplies by
+    u32x4 la = fla;
+    if (!BWD && !GS) {
+      const float dv = a.per_channel ? (frow < E ? a.wscale[frow] : 1.0f) : a.wscale[0];
+#pragma unroll
+      for (int h = 0; h < 4; ++h)
+        la[h] = (uint32_t)f32_to_bf16_bits(bf16_lo(la[h]) / dv) | ((uint32_t)f32_to_bf16_bits(bf16_hi(la[h]) / dv) << 16);
+    }
+    const rsrc_t rfo = make_rsrc(a.fout + (m0 < M ? m0 : 0) * a.fout_ld, m0 < M ? clamp_bytes((M - m0) * a.fout_ld * 2) : 0u);
+    const bool bad = fold_bad != 0;
+#pragma unroll
+    for (int j = 0; j < TT; ++j) {
+      u32x4 lb = mbload16_dev(rfo, opaque_u32(q < 2 && 8 * q < a.fout_ld ? (uint32_t)(((16 * j + l16) * a.fout_ld + 8 * q) * 2) : LRQ_OOB));
+      if (bad) lb = (u32x4){0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u};
+      acc[j] = mfma16(as_bf16x8(la), as_bf16x8(lb), acc[j]);
+    }
+  } else if (rp > 0) {
     // LoRA: A role = weight-side rows e0 + 16w + l16 (B^T forward, A
     // backward, [E][rp]), B role = token rows m0 + 16j + l16 (t or u,
     // [M][rp]); rank slots 32 ks + 8q .. +8, zero past rp
@@ -329,6 +519,22 @@ __global__ void __launch_bounds__(256, 2) k_mid(GemmArgs a, int tiles_m, int til
     const uint32_t off = nok ? (uint32_t)(((16 * j + l16) * E + n) * 2) : LRQ_OOB;
     __builtin_amdgcn_raw_buffer_store_b64(o, ry, opaque_u32(off), 0, 0);
   }
+  if (FOLD) {
+    // the last tile of the launch (every read of a flag is over by then)
+    // clears the flags and advances the epoch
+    __shared__ int fin;
+    __syncthreads();
+    if (tid == 0) fin = madd_dev(a.fcnt + SK_DCNT) + 1 == (uint32_t)ntiles;
+    __syncthreads();
+    if (fin) {
+      const int64_t G = (M + 63) / 64;
+      for (int64_t i = tid; i < G; i += 256) mzero_dev(a.fcnt + G + i);
+      if (tid == 0) {
+        mzero_dev(a.fcnt + SK_DCNT);
+        madd_dev(a.fcnt + SK_EPOCH);
+      }
+    }
+  }
 }
 
 template <bool BWD, int FMT>
@@ -339,11 +545,19 @@ hipError_t run_mid(hipStream_t st, const GemmArgs& a, int variant) {
   const int group_m = tiles_m < 8 ? tiles_m : 8;
   const int ntiles = tiles_m * tiles_e;
   // k_mid: two 64-wide blocks per stage with 64-token tiles, one with 128;
-  // 64 KiB of LDS in every variant, two workgroups per CU
-  if (variant == MID_128)
-    hipLaunchKernelGGL((k_mid<BWD, FMT, 8, 1>), dim3(ntiles), dim3(256), 0, st, a, tiles_m, tiles_e, group_m);
-  else
-    hipLaunchKernelGGL((k_mid<BWD, FMT, 4, 2>), dim3(ntiles), dim3(256), 0, st, a, tiles_m, tiles_e, group_m);
+  // 64 KiB of LDS in every variant, two workgroups per CU; with the fold,
+  // its workgroups first
+  if (a.fold) {
+    const unsigned grid = (unsigned)(ntiles + a.fold_wgs);
+    if (variant == MID_128)
+      hipLaunchKernelGGL((k_mid<BWD, FMT, 8, 1, true>), dim3(grid), dim3(256), 0, st, a, tiles_m, tiles_e, group_m);
+    else
+      hipLaunchKernelGGL((k_mid<BWD, FMT, 4, 2, true>), dim3(grid), dim3(256), 0, st, a, tiles_m, tiles_e, group_m);
+  } else if (variant == MID_128) {
+    hipLaunchKernelGGL((k_mid<BWD, FMT, 8, 1, false>), dim3(ntiles), dim3(256), 0, st, a, tiles_m, tiles_e, group_m);
+  } else {
+    hipLaunchKernelGGL((k_mid<BWD, FMT, 4, 2, false>), dim3(ntiles), dim3(256), 0, st, a, tiles_m, tiles_e, group_m);
+  }
   return hipGetLastError();
 }
 
@@ -353,6 +567,18 @@ hipError_t launch_mid(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, int 
   if (a.m <= 0 || a.e <= 0) return hipSuccess;
   if (variant != MID_64 && variant != MID_128) return hipErrorInvalidValue;
   if (a.rp > 64 || a.rp % 16 != 0) return hipErrorInvalidValue;
+  // the fold: rank 8 or 16, both raw factors, its output, partials and
+  // counters (groups' arrivals and flags within the counter area), and
+  // enough factor workgroups, whole groups of eight
+  if (a.fold) {
+    const int64_t G = (a.m + 63) / 64;
+    if (a.rp != 16 || (a.r != 8 && a.r != 16) || !a.lact || !a.lw || !a.fout || a.fout_ld % 8 != 0 ||
+        a.fout_ld < a.r || !a.fpart || !a.fcnt || 2 * G > SK_MAX_NB || a.fold_wgs % 8 != 0 ||
+        a.fold_slices != (int)((a.l + MID_FOLD_KT - 1) / MID_FOLD_KT) || a.fold_wgs < a.fold_slices * G ||
+        a.m * a.l * 2 >= ((int64_t)1 << 32) || a.m * a.fout_ld * 2 >= ((int64_t)1 << 32) ||
+        (int64_t)a.fold_slices * G * 64 * 16 * 4 >= ((int64_t)1 << 32))
+      return hipErrorInvalidValue;
+  }
   // 32-bit buffer offsets: one tile's activation rows and outputs, the depth
   // run of the weight's block row
   if ((int64_t)128 * a.l * 2 >= ((int64_t)1 << 31) || (int64_t)128 * a.e * 2 >= ((int64_t)1 << 31))

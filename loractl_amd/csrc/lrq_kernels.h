@@ -47,6 +47,22 @@ struct GemmArgs {
   uint16_t* out;         // [m, e]
   float* part;           // lrq_gemm.hip split-depth partials [S][m][e] (gemm_split_floats), or null
   int splits, spl;       // set by lrq_gemm.hip: depth ranges and steps per range
+  // lrq_gemm_mid.hip with the token-side LoRA factor formed in the same
+  // launch (fold != 0, rank 8 or 16): the first fold_wgs workgroups (a
+  // multiple of 8) form bf16(fscale . act . F) for 64-token groups over
+  // fold_slices depth slices of MID_FOLD_KT (F = lact: forward A [l, r],
+  // backward B [r, l]), sum the slices in order, store it to fout
+  // [m][fout_ld] and publish a stamped ready flag per group; the tiles read
+  // it after the flag. lw is then the raw weight-side factor (forward B
+  // [r, e], backward A [e, r]). fpart holds the slices' f32 partials
+  // [fold_slices][round_up(m, 64)][16]; fcnt is the counter area (zero on
+  // entry and exit; the epoch only grows).
+  int fold, fold_wgs, fold_slices;
+  float fscale;
+  uint16_t* fout;
+  int fout_ld;
+  float* fpart;
+  uint32_t* fcnt;
 };
 
 // lrq_gemm.hip: the forward for m > 16 and the input gradient, weight
@@ -67,6 +83,8 @@ int get_num_cus();
 enum { MID_NONE = 0, MID_64 = 1, MID_128 = 2 };
 hipError_t launch_mid(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, int variant);
 int gemm_mid_tokens(int64_t m, int64_t e, int64_t depth);
+// depth per slice of the folded factor's workgroups (GemmArgs.fold)
+constexpr int MID_FOLD_KT = 384;
 // tuning and test hook (lrq_debug_gemm_path): 0 planned, 1 large tiles,
 // 2 MID_64, 3 MID_128
 void set_gemm_path(int path);
@@ -107,6 +125,7 @@ SkinnyPlan skinny_plan(int64_t n, int64_t k, int rp, int num_cus);
 // test hook (lrq_debug_force_wait_timeout): later launches wait for a stamp
 // that is never published, 16 polls at most
 void set_force_wait_timeout(bool on);
+bool force_wait_timeout();
 size_t skinny_ws_bytes(const SkinnyPlan& p, int64_t m, int64_t n, int rp);
 // The backward's LoRA factor gradients, folded into its launch (null: not
 // formed): dA = x^T . u (f32 [k, r]) from the forward input x [m, k] and

@@ -1008,6 +1008,7 @@ __global__ void __launch_bounds__(NT) k_skf(SkArgs sa) {
 
 bool g_force_wait_timeout = false;
 void set_force_wait_timeout(bool on) { g_force_wait_timeout = on; }
+bool force_wait_timeout() { return g_force_wait_timeout; }
 
 SkinnyPlan skinny_plan(int64_t n, int64_t k, int rp, int num_cus) {
   SkinnyPlan p{};

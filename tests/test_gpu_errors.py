@@ -1,9 +1,9 @@
 """Failure handling of the C ABI on the GPU, each condition forced from the
 host so that every kernel still ends normally:
 
-- a few-token epilogue whose bounded wait for t (u) runs out (the test hook
-  makes it wait for a stamp that is never published, 16 polls): the
-  outputs it owns are NaN, lrq_sync reports the flag once, then clears it
+- a few-token epilogue, or a mid-size tile of rank 16, whose bounded wait
+  for t (u) runs out (the test hook makes it wait for a stamp that is never
+  published, 16 polls): the outputs it owns are NaN, lrq_sync reports the flag once, then clears it
   and resets the counters, and the next calls are exact again;
 - a LoRA call past LRQ_MAX_LORA_TOKENS is refused before any launch, and
   one at the limit runs;
@@ -26,23 +26,29 @@ def _weight(cuda, w, group=64):
     return D.compute_weight(D.quantize_int4(torch.from_numpy(w).to(cuda), group))
 
 
-@pytest.mark.parametrize("K,N", [(3072, 12288), (1024, 4096)], ids=["whole-depth", "splits"])
-def test_few_token_wait_timeout_is_reported_and_cleared(cuda, K, N):
-    M, r = 4, 16
+@pytest.mark.parametrize(
+    "M,K,N,path",
+    [(4, 3072, 12288, "planned"), (4, 1024, 4096, "planned"), (192, 1024, 1536, "mid64"), (256, 1152, 1024, "mid128")],
+    ids=["whole-depth", "splits", "mid64-fold", "mid128-fold"],
+)
+def test_few_token_wait_timeout_is_reported_and_cleared(cuda, M, K, N, path):
+    r = 16
     w, x, a, b, dy = case_inputs(M, K, N, r, seed=7)
     wq = _weight(cuda, w)
     xd, ad, bd, dyd = (to_dev(v, cuda) for v in (x, a, b, dy))
     y0, t0 = D.lora_fwd(xd, wq, ad, bd, 1.0)
     dx0, da0, db0 = D.lora_bwd(xd, dyd, wq, ad, bd, 1.0, t0)
     D.sync()
+    D.debug_gemm_path(path)
     D.debug_force_wait_timeout(True)
     try:
-        print(f"forced timeout K={K} N={N}: forward", flush=True)
+        print(f"forced timeout M={M} K={K} N={N} {path}: forward", flush=True)
         y1, _ = D.lora_fwd(xd, wq, ad, bd, 1.0)
-        print(f"forced timeout K={K} N={N}: backward", flush=True)
+        print(f"forced timeout M={M} K={K} N={N} {path}: backward", flush=True)
         dx1, _, _ = D.lora_bwd(xd, dyd, wq, ad, bd, 1.0, t0)
     finally:
         D.debug_force_wait_timeout(False)
+        D.debug_gemm_path("planned")
     with pytest.raises(L.LrqError, match="gave up waiting"):
         D.sync()
     assert bool(torch.isnan(y1.float()).all()) and bool(torch.isnan(dx1.float()).all())
