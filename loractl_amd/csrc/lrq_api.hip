@@ -133,6 +133,20 @@ int run_hot(lrq_ctx* c, int kid, const char* what, F f) {
   return rc;
 }
 
+// A forward (backward) call forgets the recorded launches of every kernel
+// its pass may launch, so that lrq_profile_relaunch repeats only launches of
+// the pass's latest call: a kernel that call did not launch (the shape took
+// another path) has none to repeat, rather than one whose buffers may be
+// gone.
+void forget_pass(lrq_ctx* c, bool bwd) {
+  static const int fwd_k[] = {KID_FWD_MAIN, KID_LORA_T};
+  static const int bwd_k[] = {KID_BWD_DX, KID_LORA_U, KID_LORA_DA, KID_LORA_DB, KID_LORA_DADB};
+  if (bwd)
+    for (int k : bwd_k) c->last[k] = nullptr;
+  else
+    for (int k : fwd_k) c->last[k] = nullptr;
+}
+
 int flush_profile(lrq_ctx* c) {
   for (auto& r : c->pending) {
     hipError_t e = hipEventSynchronize(r.b);
@@ -579,6 +593,7 @@ static GemmArgs gemm_args(const lrq_weight* w, bool bwd, const uint16_t* act, in
   g.nib = 0x0f0f0f0fu;
   g.bias = bwd ? nullptr : w->bias;
   g.out = out;
+  g.tn_da = -1;
   return g;
 }
 
@@ -628,6 +643,7 @@ static int fwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t 
   LRQ_TRY(note_capture(c));
   LRQ_TRY(check_gemm(c, w, m));
   if (!aligned16(x) || !aligned16(y)) return fail(c, LRQ_EINVAL, "x and y must be 16-byte aligned");
+  forget_pass(c, false);
   const int fmt = w->format;
   const int64_t wk = w->k;
   const bool lora = a != nullptr && b != nullptr && r > 0;
@@ -768,6 +784,7 @@ static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const ui
   LRQ_TRY(note_capture(c));
   LRQ_TRY(check_gemm(c, w, m));
   if (!aligned16(dy)) return fail(c, LRQ_EINVAL, "dy must be 16-byte aligned");
+  forget_pass(c, true);
   const int fmt = w->format;
   const int64_t wn = w->n, wk = w->k;
   if (dx && !aligned16(dx)) return fail(c, LRQ_EINVAL, "dx must be 16-byte aligned");
@@ -789,7 +806,16 @@ static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const ui
     const int64_t G = (m + 63) / 64, fs = (w->n + MID_FOLD_KT - 1) / MID_FOLD_KT;
     const bool fold = !few && dx && (r == 8 || r == 16) && gemm_mid_tokens(m, w->k, w->n) > 0 && aligned16(a) &&
                       2 * G <= SK_MAX_NB;
-    const size_t fbytes = fold ? (size_t)fs * G * 64 * 16 * 4 : 0;
+    // and the weight gradients by workgroups after its tiles, in token
+    // slices that fit its LDS (their counters after the fold's, partials
+    // after u's)
+    const LoraPlan tpb = fold ? mid_tn_plan(m, w->n, rp) : LoraPlan{}, tpa = fold ? mid_tn_plan(m, w->k, rp) : LoraPlan{};
+    const int64_t tb_floats = (db && tpb.splits > 1) ? (int64_t)tpb.splits * w->n * rp : 0;
+    const int64_t ta_floats = (da && tpa.splits > 1) ? (int64_t)tpa.splits * w->k * rp : 0;
+    const bool fold_tn = fold && (da || db) && tpb.splits > 0 && tpa.splits > 0 &&
+                         2 * G + TN_WAVES * ((db ? tpb.tiles : 0) + (da ? tpa.tiles : 0)) <= SK_MAX_NB;
+    const int64_t fp_floats = round_up(fs * G * 64 * 16, 64);
+    const size_t fbytes = fold ? (size_t)(fp_floats + (fold_tn ? tb_floats + ta_floats : 0)) * 4 : 0;
     LRQ_TRY(ensure_ws(c, lbytes + (few ? skinny_ws_bytes(sp, m, w->k, rp) : fbytes)));
     LoraWs ws = lora_layout(c->ws, m, w->n, w->k, rp);
     ga.r = (int)r;
@@ -821,7 +847,24 @@ static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const ui
       ga.fscale = scaling;
       ga.fout = ws.up;
       ga.fout_ld = rp;
+      if (fold_tn) {
+        // dB = t^T . dy first (nothing to wait for), then dA = x^T . u
+        float* tpart = ga.fpart + fp_floats;
+        uint32_t* tcnt = c->cnt + 2 * G;
+        int nj = 0;
+        if (db) {
+          ga.tj[nj++] = tn_args(TnSpec{dy, t, r, m, w->n, (int)r, tpb, tpart, db, 1, w->n}, tcnt);
+          tpart += tb_floats;
+          tcnt += TN_WAVES * tpb.tiles;
+        }
+        if (da) {
+          ga.tn_da = nj;
+          ga.tj[nj++] = tn_args(TnSpec{x, ws.up, rp, m, w->k, (int)r, tpa, tpart, da, r, 1}, tcnt);
+        }
+        ga.tn_blocks = ga.tj[0].blocks + ga.tj[1].blocks;
+      }
       LRQ_TRY(run_hot(c, KID_BWD_DX, "bwd_dx", [=] { return launch_bwd(c->stream, fmt, ga); }));
+      if (fold_tn) return LRQ_OK;
     } else {
       // u = s . dy . B^T   (bf16 [m, rp]: the dx epilogue operand and dA's factor)
       const LoraPlan pu = lora_plan_nt(m, w->n, rp);

@@ -59,6 +59,7 @@
 
 #include "lrq_common.h"
 #include "lrq_kernels.h"
+#include "lrq_tn.h"
 
 namespace {
 
@@ -172,6 +173,66 @@ LRQ_DEV void mid_fold_slice(const GemmArgs& a, int fw, uint16_t* lds, uint32_t w
   if (tid == 0) __hip_atomic_store(a.fcnt + G + g, want, __ATOMIC_RELAXED, MXSCOPE);
 }
 
+// FOLD: a reader of the ready flags is done with them (a tile after its
+// LoRA step, a dA block after its wait). The last of the launch's `readers`
+// clears the flags and advances the epoch. Every thread of the workgroup
+// calls it.
+LRQ_DEV void mid_flags_done(const GemmArgs& a, int readers) {
+  __shared__ int fin;
+  __syncthreads();
+  if (threadIdx.x == 0) fin = madd_dev(a.fcnt + SK_DCNT) + 1 == (uint32_t)readers;
+  __syncthreads();
+  if (fin) {
+    const int64_t G = (a.m + 63) / 64;
+    for (int64_t i = threadIdx.x; i < G; i += 256) mzero_dev(a.fcnt + G + i);
+    if (threadIdx.x == 0) {
+      mzero_dev(a.fcnt + SK_DCNT);
+      madd_dev(a.fcnt + SK_EPOCH);
+    }
+  }
+}
+
+// FOLD backward: weight-gradient block tb of the launch's tn jobs (after the
+// tiles). A dA block first waits (bounded, as the tiles do) for the ready
+// flags of the 64-token groups of its token slice, then reads u at device
+// scope; a wait that runs out flags the failure and makes its sums NaN.
+// The factor slice goes to sq, the combine buffer to sr (16 KiB each).
+LRQ_DEV void mid_tn(const GemmArgs& a, int tb, uint32_t want, int readers, uint16_t* sq, uint16_t* sr) {
+  const bool second = tb >= a.tj[0].blocks;
+  const int ji = second ? 1 : 0;
+  const TnArgs& j = a.tj[ji];
+  const int bid = tb - (second ? a.tj[0].blocks : 0);
+  if (ji != a.tn_da) {
+    tn_block<1, MID_TN_LDS, MID_TN_LDS, false>(j, bid, sq, reinterpret_cast<float*>(sr), false);
+    return;
+  }
+  __shared__ int bad;
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    const int64_t G = (a.m + 63) / 64;
+    const int64_t m_lo = (int64_t)(bid / j.tiles) * j.m_per;
+    const int64_t m_hi = min(j.M, m_lo + j.m_per);
+    const int64_t gi = m_lo / 64 + lane;
+    const bool mine = gi < (m_hi + 63) / 64 && gi < G;
+    uint32_t polls = 0;
+    const uint32_t cap = a.fold < 0 ? 16u : MID_MAX_POLLS;  // the test hook: 16 polls
+    bool ok = !mine || mload_dev(a.fcnt + G + gi) == want;
+    while (!__all(ok) && polls < cap) {
+      __builtin_amdgcn_s_sleep(2);
+      ++polls;
+      ok = !mine || mload_dev(a.fcnt + G + gi) == want;
+    }
+    if (lane == 0) {
+      bad = __all(ok) ? 0 : 1;
+      if (!__all(ok)) __hip_atomic_store(a.fcnt + SK_FAIL, 1u, __ATOMIC_RELAXED, MXSCOPE);
+    }
+  }
+  __syncthreads();
+  const bool poison = bad != 0;
+  mid_flags_done(a, readers);
+  tn_block<1, MID_TN_LDS, MID_TN_LDS, true>(j, bid, sq, reinterpret_cast<float*>(sr), poison);
+}
+
 template <bool BWD, int FMT, int TT, int SD, bool FOLD>
 __global__ void __launch_bounds__(256, 2) k_mid(GemmArgs a, int tiles_m, int tiles_e, int group_m) {
   constexpr bool I4 = FMT == LRQ_FMT_INT4;
@@ -199,6 +260,14 @@ __global__ void __launch_bounds__(256, 2) k_mid(GemmArgs a, int tiles_m, int til
       return;
     }
     want = stamp + (a.fold < 0 ? 0x40000000u : 0u);
+    if constexpr (BWD) {
+      if ((int)blockIdx.x >= a.fold_wgs + ntiles) {
+        static_assert(MID_TN_LDS <= XB * 2, "a weight-gradient block's LDS fits one stage buffer");
+        const int nda = a.tn_da >= 0 ? a.tj[a.tn_da].blocks : 0;
+        mid_tn(a, (int)blockIdx.x - a.fold_wgs - ntiles, want, ntiles + nda, sx0, sx1);
+        return;
+      }
+    }
   }
   const int vb = FOLD ? (int)blockIdx.x - a.fold_wgs : (int)blockIdx.x;
   const int lt = xcd_remap(vb, ntiles);
@@ -519,22 +588,7 @@ __global__ void __launch_bounds__(256, 2) k_mid(GemmArgs a, int tiles_m, int til
     const uint32_t off = nok ? (uint32_t)(((16 * j + l16) * E + n) * 2) : LRQ_OOB;
     __builtin_amdgcn_raw_buffer_store_b64(o, ry, opaque_u32(off), 0, 0);
   }
-  if (FOLD) {
-    // the last tile of the launch (every read of a flag is over by then)
-    // clears the flags and advances the epoch
-    __shared__ int fin;
-    __syncthreads();
-    if (tid == 0) fin = madd_dev(a.fcnt + SK_DCNT) + 1 == (uint32_t)ntiles;
-    __syncthreads();
-    if (fin) {
-      const int64_t G = (M + 63) / 64;
-      for (int64_t i = tid; i < G; i += 256) mzero_dev(a.fcnt + G + i);
-      if (tid == 0) {
-        mzero_dev(a.fcnt + SK_DCNT);
-        madd_dev(a.fcnt + SK_EPOCH);
-      }
-    }
-  }
+  if (FOLD) mid_flags_done(a, ntiles + ((BWD && a.tn_da >= 0) ? a.tj[a.tn_da].blocks : 0));
 }
 
 template <bool BWD, int FMT>
@@ -548,7 +602,7 @@ hipError_t run_mid(hipStream_t st, const GemmArgs& a, int variant) {
   // 64 KiB of LDS in every variant, two workgroups per CU; with the fold,
   // its workgroups first
   if (a.fold) {
-    const unsigned grid = (unsigned)(ntiles + a.fold_wgs);
+    const unsigned grid = (unsigned)(ntiles + a.fold_wgs + (BWD ? a.tn_blocks : 0));
     if (variant == MID_128)
       hipLaunchKernelGGL((k_mid<BWD, FMT, 8, 1, true>), dim3(grid), dim3(256), 0, st, a, tiles_m, tiles_e, group_m);
     else
@@ -578,6 +632,31 @@ hipError_t launch_mid(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, int 
         a.m * a.l * 2 >= ((int64_t)1 << 32) || a.m * a.fout_ld * 2 >= ((int64_t)1 << 32) ||
         (int64_t)a.fold_slices * G * 64 * 16 * 4 >= ((int64_t)1 << 32))
       return hipErrorInvalidValue;
+    // the weight gradients' jobs after the tiles (backward): each a whole
+    // plan of token slices that fit MID_TN_LDS, over all the launch's
+    // tokens, with its counters past the fold's and apart from the other's
+    if (a.tn_blocks != 0) {
+      if (!bwd || a.tn_blocks < 0 || a.tj[0].blocks + a.tj[1].blocks != a.tn_blocks || a.tn_da < -1 ||
+          a.tn_da > 1 || (a.tn_da >= 0 && a.tj[a.tn_da].blocks == 0))
+        return hipErrorInvalidValue;
+      const uint32_t* lo = a.fcnt + 2 * G;
+      for (int i = 0; i < 2; ++i) {
+        const TnArgs& j = a.tj[i];
+        if (j.blocks == 0) continue;
+        if (j.C <= 0 || j.tiles != (j.C + 127) / 128 || j.splits < 1 || j.blocks != j.tiles * j.splits ||
+            j.m_per <= 0 || j.m_per % 128 != 0 || 16 * (j.m_per + 8) * 2 > MID_TN_LDS || j.M != a.m ||
+            (int64_t)j.splits * j.m_per < j.M || (int64_t)(j.splits - 1) * j.m_per >= j.M || !j.p || !j.q ||
+            !j.out || j.R < 1 || j.R > 16 || j.ldq < j.R || (j.splits > 1 && !j.partial) || !j.cnt ||
+            j.cnt < lo || j.cnt + TN_WAVES * j.tiles > a.fcnt + SK_MAX_NB ||
+            j.m_per * j.C * 2 >= ((int64_t)1 << 31) || (int64_t)j.splits * j.C * 16 * 4 >= ((int64_t)1 << 32))
+          return hipErrorInvalidValue;
+        if (i == a.tn_da && (j.ldq % 8 != 0 || (reinterpret_cast<uintptr_t>(j.q) & 15) != 0))
+          return hipErrorInvalidValue;
+        lo = j.cnt + TN_WAVES * j.tiles;
+      }
+    }
+  } else if (a.tn_blocks != 0) {
+    return hipErrorInvalidValue;
   }
   // 32-bit buffer offsets: one tile's activation rows and outputs, the depth
   // run of the weight's block row

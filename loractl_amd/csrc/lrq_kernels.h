@@ -31,6 +31,23 @@ hipError_t launch_block(hipStream_t st, const lrq_weight* w, uint8_t* data, floa
 //   backward (lrq_gemm.hip): act = dy [m, n], l = n, e = k; lact = u [m, rp];
 //            lw = A [k, rp]
 // The weight is a section of the blocked layout (wk = k).
+// One tn job as its workgroups see it (lrq_tn.h): TN_WAVES wavefronts per
+// workgroup, 128 columns x a token slice each.
+constexpr int TN_WAVES = 4;
+struct TnArgs {
+  const uint16_t* p;   // [M, C] bf16
+  const uint16_t* q;   // [M, ldq] bf16, columns j < R
+  int64_t M, C, ldq;
+  int R;
+  int64_t m_per;       // tokens per slice (multiple of 128)
+  float* partial;      // [splits][C][rp]
+  int tiles, blocks;   // column tiles of 128, tiles x slices
+  float* out;          // the result out[c * sc + j * sj] (j < R)
+  int64_t sc, sj;
+  int splits;          // token slices; one slice writes out directly
+  uint32_t* cnt;       // [tiles][TN_WAVES] arrival counters, zero on entry and exit
+};
+
 struct GemmArgs {
   const uint16_t* act;
   int64_t m, l, e, wk;
@@ -63,6 +80,14 @@ struct GemmArgs {
   int fout_ld;
   float* fpart;
   uint32_t* fcnt;
+  // The backward with the fold also runs the weight gradients' token
+  // reductions (dB = t^T dy, dA = x^T u; lrq_tn.h) in tn_blocks workgroups
+  // after the tiles: job tj[0]'s blocks, then tj[1]'s. Job tn_da (or none,
+  // -1) is dA: its blocks wait for the ready flags of their token slice's
+  // groups and read u at device scope. Plans from mid_tn_plan; counters in
+  // the counter area past the fold's [0, 2 G).
+  TnArgs tj[2];
+  int tn_blocks, tn_da;
 };
 
 // lrq_gemm.hip: the forward for m > 16 and the input gradient, weight
@@ -85,6 +110,9 @@ hipError_t launch_mid(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, int 
 int gemm_mid_tokens(int64_t m, int64_t e, int64_t depth);
 // depth per slice of the folded factor's workgroups (GemmArgs.fold)
 constexpr int MID_FOLD_KT = 384;
+// the token slices of a weight-gradient job run inside the mid-size
+// backward: the factor slice takes at most 16 KiB of LDS (rank 16)
+constexpr int MID_TN_LDS = 16384;
 // tuning and test hook (lrq_debug_gemm_path): 0 planned, 1 large tiles,
 // 2 MID_64, 3 MID_128
 void set_gemm_path(int path);
@@ -151,6 +179,9 @@ struct LoraPlan {
 };
 LoraPlan lora_plan_nt(int64_t M, int64_t C, int rp);
 LoraPlan lora_plan_tn(int64_t M, int64_t C, int rp, int64_t other_c = 0);
+// tn slices that fit the mid-size backward's LDS (MID_TN_LDS for the factor
+// slice): as few token slices as that allows
+LoraPlan mid_tn_plan(int64_t M, int64_t C, int rp);
 // out = bf16(s * sum over slices of p[m, c] * q(j, c)) as [M, rp] (columns
 // >= r zero) and/or [M, r], with q(j, c) = q[j * ldq + c] when qrow (B [r, n]),
 // else q[c * ldq + j] (A [k, r]); entries j >= R read as zero. One launch:
@@ -196,6 +227,8 @@ struct TnSpec {
   int64_t sc, sj;
 };
 hipError_t launch_lora_tn(hipStream_t st, const TnSpec* jobs, int njobs, int rp, uint32_t* cnt);
+// The job's workgroup arguments, its counters at cnt.
+TnArgs tn_args(const TnSpec& j, uint32_t* cnt);
 
 // lrq_probe.hip: a streaming read of `bytes` (a multiple of 16) with one
 // 32-bit value per workgroup to out (probe_read_grid(bytes) of them)

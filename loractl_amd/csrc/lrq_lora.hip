@@ -35,23 +35,11 @@
 
 #include "lrq_common.h"
 #include "lrq_kernels.h"
+#include "lrq_tn.h"
 
 namespace {
 
 constexpr int LW = 8;          // nt: wavefronts per workgroup, at most (LoraPlan.lw: 4 or 8)
-
-// Transpose-pack: the 16-bit element `e` (0..7) of eight 8-element rows into
-// one 8-element vector (rows in order).
-LRQ_DEV u32x4 column8(const u32x4 (&v)[8], int e) {
-  const int d = e >> 1;
-  const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-  u32x4 o;
-  o[0] = __builtin_amdgcn_perm(v[1][d], v[0][d], sel);
-  o[1] = __builtin_amdgcn_perm(v[3][d], v[2][d], sel);
-  o[2] = __builtin_amdgcn_perm(v[5][d], v[4][d], sel);
-  o[3] = __builtin_amdgcn_perm(v[7][d], v[6][d], sel);
-  return o;
-}
 
 // ------------------------------------------------------------------ nt
 struct NtArgs {
@@ -63,13 +51,6 @@ struct NtArgs {
   float* partial;      // [splits][M][rp] f32
   NtFinish f;
 };
-
-// device-scope (sc1) accesses of the partials the last slice reads
-LRQ_DEV void store_dev(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-LRQ_DEV void store16_dev(rsrc_t r, uint32_t off, const u32x4& v) { __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, 16); }
-LRQ_DEV u32x4 bload16_dev(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 16); }
-LRQ_DEV uint32_t add_dev(uint32_t* c) { return __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-LRQ_DEV void zero_dev(uint32_t* c) { __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 
 constexpr int NQ_BYTES = 100 * 1024;  // factor slice in LDS
 
@@ -297,208 +278,15 @@ __global__ void __launch_bounds__(64 * LWT) k_lora_nt(NtArgs a) {
 }
 
 // ------------------------------------------------------------------ tn
-struct TnArgs {
-  const uint16_t* p;   // [M, C] bf16
-  const uint16_t* q;   // [M, ldq] bf16, columns j < R
-  int64_t M, C, ldq;
-  int R;
-  int64_t m_per;       // tokens per slice (multiple of 128)
-  float* partial;      // [splits][C][rp]
-  int tiles, blocks;   // column tiles of 128, tiles x slices
-  float* out;          // the result out[c * sc + j * sj] (j < R)
-  int64_t sc, sj;
-  int splits;          // token slices; one slice writes out directly
-  uint32_t* cnt;       // [tiles][TW] arrival counters, zero on entry and exit
-};
-
-// partial[split][c][j] = sum over the split's tokens of p[m, c] * q[m, j],
-// for one or two jobs in one launch (the first j0.blocks workgroups run job
-// 0). A workgroup (4 wavefronts) owns 128 columns and one token slice;
-// wavefront w takes tokens [128 it + 32 w, +32) of every 128-token chunk.
-constexpr int TW = 4;            // wavefronts per tn workgroup
-constexpr int TNT = 64 * TW;
+// One or two jobs per launch (the first j0.blocks workgroups run job 0).
 constexpr int TQ_BYTES = 72 * 1024;  // factor slice in LDS (later reused for the combine); two per CU
 
 template <int NJT>
 __global__ void __launch_bounds__(TNT) k_lora_tn(TnArgs j0, TnArgs j1) {
-  constexpr int RP = 16 * NJT;
-  static_assert(TW * 128 * 16 * 4 <= TQ_BYTES, "combine buffer fits the factor slice");
   __shared__ __attribute__((aligned(16))) uint16_t sQ[TQ_BYTES / 2];
-  float* const red = reinterpret_cast<float*>(sQ);
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool second = (int)blockIdx.x >= j0.blocks;
-  const TnArgs a = second ? j1 : j0;
-  const int bid = (int)blockIdx.x - (second ? j0.blocks : 0);
-  const int64_t c0 = (int64_t)(bid % a.tiles) * 128;
-  const int split = bid / a.tiles;
-  const int64_t m_lo = split * a.m_per;
-  const int64_t m_hi = min(a.M, m_lo + a.m_per);
-  const int64_t C = a.C;
-  const int l16 = lane & 15, g = lane >> 4;
-  const int64_t toks = m_hi - m_lo;
-
-  const int SQ = (int)a.m_per + 8;
-  const rsrc_t rpv = make_rsrc(a.p + m_lo * C, clamp_bytes(toks * C * 2));
-  const int64_t col = c0 + l16 * 8;
-  const uint32_t coff = (col < C) ? (uint32_t)(col * 2) : LRQ_OOB;
-
-  f32x4 acc[8][NJT];
-#pragma unroll
-  for (int q = 0; q < 8; ++q)
-#pragma unroll
-    for (int jt = 0; jt < NJT; ++jt) acc[q][jt] = acc_zero4();
-
-  const int64_t nchunks = (toks + 127) / 128;
-  u32x4 pv[2][8];
-  auto load = [&](int set, int64_t it) {
-    const int64_t mrow = it * 128 + wv * 32 + g * 8;  // slice-relative token of row 0
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t off = opaque_u32(coff + (uint32_t)((mrow + i) * C * 2));
-      pv[set][i] = bload16(rpv, off);
-    }
-  };
-  auto compute = [&](int set, int64_t it) {
-    const int64_t mrow = it * 128 + wv * 32 + g * 8;
-    bf16x8 fq[NJT];
-#pragma unroll
-    for (int jt = 0; jt < NJT; ++jt) fq[jt] = as_bf16x8(ld16(sQ + (jt * 16 + l16) * SQ + mrow));
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const bf16x8 fa = as_bf16x8(column8(pv[set], q));
-#pragma unroll
-      for (int jt = 0; jt < NJT; ++jt) acc[q][jt] = mfma16(fa, fq[jt], acc[q][jt]);
-    }
-  };
-
-  load(0, 0);  // overlaps the factor staging
-  // factor slice q [m_lo, m_hi) x R -> LDS as [j][m - m_lo] (stride SQ):
-  // 8 (tokens) x 8 (j) blocks, loaded as rows and transposed in registers
-  if ((a.ldq & 7) == 0) {
-    const rsrc_t rq = make_rsrc(a.q + m_lo * a.ldq, clamp_bytes(toks * a.ldq * 2));
-    const int jb = RP / 8;
-    for (int blk = tid; blk < jb * (int)(a.m_per / 8); blk += TNT) {
-      const int j0 = (blk % jb) * 8, mm = (blk / jb) * 8;
-      u32x4 v[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint32_t off = opaque_u32(j0 < a.ldq ? (uint32_t)(((mm + i) * a.ldq + j0) * 2) : LRQ_OOB);
-        v[i] = bload16(rq, off);
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        u32x4 cv = column8(v, e);
-        if (j0 + e >= a.R) cv = (u32x4){0u, 0u, 0u, 0u};
-        *reinterpret_cast<u32x4*>(sQ + (j0 + e) * SQ + mm) = cv;
-      }
-    }
-  } else {
-    for (int64_t id = tid; id < (int64_t)RP * a.m_per; id += TNT) {
-      const int j = (int)(id % RP);
-      const int64_t mm = id / RP;
-      uint16_t v = 0;
-      if (j < a.R && mm < toks) v = a.q[(m_lo + mm) * a.ldq + j];
-      sQ[j * SQ + mm] = v;
-    }
-  }
-  __syncthreads();
-
-  int64_t it = 0;
-  for (; it + 1 < nchunks; it += 2) {
-    load(1, it + 1);
-    compute(0, it);
-    load(0, it + 2);
-    compute(1, it + 1);
-  }
-  if (it < nchunks) compute(0, it);
-  __syncthreads();  // the factor slice's LDS becomes the combine buffer
-
-  // combine the wavefronts (fixed order); accumulator row 4g+v of MFMA q is
-  // column c0 + 8*(4g+v) + q. All rank tiles go through LDS at once when
-  // they fit (rank <= 32), else one 16-wide tile per round; each thread then
-  // sums four consecutive rank entries of a column and stores them together.
-  const rsrc_t rpart = make_rsrc(a.partial + (int64_t)split * C * RP, clamp_bytes(C * RP * 4));
-  constexpr int RT = (TW * 128 * RP * 4 <= TQ_BYTES) ? NJT : 1;  // rank tiles per round
-  constexpr int RW = 16 * RT;                                    // rank entries per round
-#pragma unroll
-  for (int jr = 0; jr < NJT; jr += RT) {
-#pragma unroll
-    for (int jt = 0; jt < RT; ++jt)
-#pragma unroll
-      for (int q = 0; q < 8; ++q)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int cl = 8 * (4 * g + v) + q;
-          red[(wv * 128 + cl) * RW + jt * 16 + l16] = acc[q][jr + jt][v];
-        }
-    __syncthreads();
-    // wavefront w sums columns [32w, 32w + 32): PL items of four per lane
-    constexpr int PL = RW / 8;
-#pragma unroll
-    for (int k = 0; k < PL; ++k) {
-      const int id = wv * 64 * PL + k * 64 + lane;
-      const int cl = id / (RW / 4), jl = (id % (RW / 4)) * 4;
-      f32x4 sum = *reinterpret_cast<const f32x4*>(red + cl * RW + jl);
-#pragma unroll
-      for (int w = 1; w < TW; ++w) sum += *reinterpret_cast<const f32x4*>(red + (w * 128 + cl) * RW + jl);
-      const int j = jr * 16 + jl;
-      if (c0 + cl < C) {
-        if (a.splits == 1) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (j + e < a.R) a.out[(c0 + cl) * a.sc + (int64_t)(j + e) * a.sj] = sum[e];
-        } else {
-          store16_dev(rpart, (uint32_t)(((c0 + cl) * RP + j) * 4), __builtin_bit_cast(u32x4, sum));
-        }
-      }
-    }
-    __syncthreads();
-  }
-  if (a.splits == 1) return;
-  // count this wavefront's 32 columns done in this slice once its stores are
-  // acknowledged (no barrier); the last wavefront to arrive sums the slices
-  // in order, NE entries of four per lane, every load of a batch of SB
-  // slices issued before the first sum
-  __builtin_amdgcn_s_waitcnt(0);
-  uint32_t* const ctr = a.cnt + (bid % a.tiles) * TW + wv;
-  uint32_t old = 0;
-  if (lane == 0) old = add_dev(ctr);
-  if (__builtin_amdgcn_readfirstlane(old) + 1 != (uint32_t)a.splits) return;
-  if (lane == 0) zero_dev(ctr);
-  constexpr int NE = 32 * RP / 4 / 64, SB = 16 / NE;
-  const rsrc_t rp_ = make_rsrc(a.partial, clamp_bytes((int64_t)a.splits * C * RP * 4));
-  f32x4 v[NE];
-#pragma unroll
-  for (int k = 0; k < NE; ++k) v[k] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-  for (int s0 = 0; s0 < a.splits; s0 += SB) {  // slices in order
-    u32x4 pv[NE][SB];
-#pragma unroll
-    for (int k = 0; k < NE; ++k) {
-      const int e = k * 64 + lane;
-      const int64_t c = c0 + 32 * wv + e / (RP / 4);
-      const int j = (e % (RP / 4)) * 4;
-#pragma unroll
-      for (int u = 0; u < SB; ++u)
-        pv[k][u] = bload16_dev(rp_, opaque_u32(s0 + u < a.splits && c < C
-                                                   ? (uint32_t)((((int64_t)(s0 + u) * C + c) * RP + j) * 4)
-                                                   : LRQ_OOB));
-    }
-#pragma unroll
-    for (int k = 0; k < NE; ++k)
-#pragma unroll
-      for (int u = 0; u < SB; ++u) v[k] += __builtin_bit_cast(f32x4, pv[k][u]);
-  }
-#pragma unroll
-  for (int k = 0; k < NE; ++k) {
-    const int e = k * 64 + lane;
-    const int64_t c = c0 + 32 * wv + e / (RP / 4);
-    const int j = (e % (RP / 4)) * 4;
-    if (c >= C) continue;
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      if (j + q < a.R) a.out[c * a.sc + (int64_t)(j + q) * a.sj] = v[k][q];
-  }
+  tn_block<NJT, TQ_BYTES, TQ_BYTES, false>(second ? j1 : j0, (int)blockIdx.x - (second ? j0.blocks : 0), sQ,
+                                           reinterpret_cast<float*>(sQ), false);
 }
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -556,6 +344,18 @@ LoraPlan lora_plan_tn(int64_t M, int64_t C, int rp, int64_t other_c) {
   return p;
 }
 
+LoraPlan mid_tn_plan(int64_t M, int64_t C, int rp) {
+  LoraPlan p{};
+  const int64_t cap = rp > 0 ? ((MID_TN_LDS / 2) / rp - 8) / 128 * 128 : 0;
+  if (cap < 128) return p;  // no slice fits (ranks past 16 do not run there)
+  const int64_t m = M > 0 ? M : 1;
+  const int64_t S = cdiv(m, cap);
+  p.per = 128 * cdiv(cdiv(m, S), 128);
+  p.splits = (int)cdiv(m, p.per);
+  p.tiles = cdiv(C, 128);
+  return p;
+}
+
 hipError_t launch_lora_nt(hipStream_t st, const uint16_t* p, const uint16_t* q, bool qrow, int64_t ldq,
                           int R, int64_t M, int64_t C, int rp, const LoraPlan& plan, float* partial,
                           const NtFinish& fin) {
@@ -583,6 +383,12 @@ hipError_t launch_lora_nt(hipStream_t st, const uint16_t* p, const uint16_t* q, 
   return hipGetLastError();
 }
 
+TnArgs tn_args(const TnSpec& j, uint32_t* cnt) {
+  const int64_t blocks = j.C > 0 ? j.plan.tiles * j.plan.splits : 0;
+  return TnArgs{j.p,   j.q,  j.M,  j.C,           j.ldq, j.R, j.plan.per, j.partial, (int)j.plan.tiles, (int)blocks,
+                j.out, j.sc, j.sj, j.plan.splits, cnt};
+}
+
 hipError_t launch_lora_tn(hipStream_t st, const TnSpec* jobs, int njobs, int rp, uint32_t* cnt) {
   TnArgs t[2] = {};
   int64_t total = 0, ntiles = 0;
@@ -590,8 +396,7 @@ hipError_t launch_lora_tn(hipStream_t st, const TnSpec* jobs, int njobs, int rp,
     const TnSpec& j = jobs[i];
     const int64_t blocks = j.C > 0 ? j.plan.tiles * j.plan.splits : 0;
     // each job's column tiles count on their own counters
-    t[i] = TnArgs{j.p,      j.q, j.M, j.C, j.ldq, j.R, j.plan.per, j.partial, (int)j.plan.tiles, (int)blocks,
-                  j.out,    j.sc, j.sj, j.plan.splits, cnt + ntiles * TW};
+    t[i] = tn_args(j, cnt + ntiles * TW);
     total += blocks;
     ntiles += j.plan.tiles;
   }

@@ -45,13 +45,15 @@ def test_few_token_wait_timeout_is_reported_and_cleared(cuda, M, K, N, path):
         print(f"forced timeout M={M} K={K} N={N} {path}: forward", flush=True)
         y1, _ = D.lora_fwd(xd, wq, ad, bd, 1.0)
         print(f"forced timeout M={M} K={K} N={N} {path}: backward", flush=True)
-        dx1, _, _ = D.lora_bwd(xd, dyd, wq, ad, bd, 1.0, t0)
+        dx1, da1, _ = D.lora_bwd(xd, dyd, wq, ad, bd, 1.0, t0)
     finally:
         D.debug_force_wait_timeout(False)
         D.debug_gemm_path("planned")
     with pytest.raises(L.LrqError, match="gave up waiting"):
         D.sync()
     assert bool(torch.isnan(y1.float()).all()) and bool(torch.isnan(dx1.float()).all())
+    if path != "planned":  # dA from the same launch, after its own wait for u
+        assert bool(torch.isnan(da1).all())
     D.sync()  # reported once: the flag is clear
     # the counters were reset: the same calls are bit-identical to the first
     y2, t2 = D.lora_fwd(xd, wq, ad, bd, 1.0)
@@ -118,33 +120,54 @@ def test_workspace_growth_keeps_captured_graphs_valid(cuda):
         assert torch.equal(y, y_eager) and torch.equal(t, t_eager), f"replay {i}"
 
 
-def test_profile_relaunch_repeats_the_step_launch(cuda):
+# the kernels each pass launches on the 256-token tiles and on the mid-size
+# tiles (which form t, u, dA and dB in the GEMM's own launch)
+RELAUNCH_PATHS = {
+    "large": (("lora_t", "fwd_main"), ("lora_u", "bwd_dx", "lora_dadb")),
+    "mid128": (("fwd_main",), ("bwd_dx",)),
+}
+
+
+@pytest.mark.parametrize("path", sorted(RELAUNCH_PATHS))
+def test_profile_relaunch_repeats_the_step_launch(cuda, path):
     """lrq_profile_relaunch repeats a context's last launch of one kernel with
     its arguments: while the buffers it reads (the workspace included) hold
-    what they held, the outputs it writes come back bit for bit; a kernel
-    never launched on the context is refused."""
+    what they held, the outputs it writes come back bit for bit. A kernel
+    the pass's latest call did not launch, or one never launched on the
+    context, is refused."""
     M, K, N, r = 300, 1024, 2048, 16
+    fwd_k, bwd_k = RELAUNCH_PATHS[path]
     w, x, a, b, dy = case_inputs(M, K, N, r, seed=13)
     wq = _weight(cuda, w)
     xd, ad, bd, dyd = (to_dev(v, cuda) for v in (x, a, b, dy))
-    y, t = D.lora_fwd(xd, wq, ad, bd, 1.0)
-    torch.cuda.synchronize()
-    y_ref = y.clone()
-    y.zero_()
-    D.profile_relaunch("fwd_main", 2)
-    torch.cuda.synchronize()
-    assert torch.equal(y, y_ref)
-    # the backward reuses the workspace slot of the forward's B^T rows for A
-    dx, da, db = D.lora_bwd(xd, dyd, wq, ad, bd, 1.0, t)
-    torch.cuda.synchronize()
-    ref = [v.clone() for v in (dx, da, db)]
-    for v in (dx, da, db):
-        v.zero_()
-    for k in ("bwd_dx", "lora_dadb"):
-        D.profile_relaunch(k, 2)
-    torch.cuda.synchronize()
-    for got, want in zip((dx, da, db), ref):
-        assert torch.equal(got, want)
+    D.debug_gemm_path(path)
+    try:
+        y, t = D.lora_fwd(xd, wq, ad, bd, 1.0)
+        torch.cuda.synchronize()
+        y_ref, t_ref = y.clone(), t.clone()
+        y.zero_()
+        D.profile_relaunch("fwd_main", 2)
+        torch.cuda.synchronize()
+        assert torch.equal(y, y_ref) and torch.equal(t, t_ref)
+        for k in {"lora_t", "fwd_main"} - set(fwd_k):
+            with pytest.raises(L.LrqError, match=f"no launch of kernel {k}"):
+                D.profile_relaunch(k, 1)
+        # the backward reuses the workspace slot of the forward's B^T rows for A
+        dx, da, db = D.lora_bwd(xd, dyd, wq, ad, bd, 1.0, t)
+        torch.cuda.synchronize()
+        ref = [v.clone() for v in (dx, da, db)]
+        for v in (dx, da, db):
+            v.zero_()
+        for k in bwd_k:
+            D.profile_relaunch(k, 2)
+        torch.cuda.synchronize()
+        for got, want in zip((dx, da, db), ref):
+            assert torch.equal(got, want)
+        for k in {"lora_u", "bwd_dx", "lora_dadb"} - set(bwd_k):
+            with pytest.raises(L.LrqError, match=f"no launch of kernel {k}"):
+                D.profile_relaunch(k, 1)
+    finally:
+        D.debug_gemm_path("planned")
     other = torch.cuda.Stream()
     with torch.cuda.stream(other):
         with pytest.raises(L.LrqError, match="no launch of kernel fwd_main"):
