@@ -237,7 +237,11 @@ int lrq_profile_read(lrq_ctx* ctx, int kid, double* total_ms, int64_t* launches)
  * lora_dadb), with the same arguments and buffers, on the context's stream,
  * so that one kernel can be timed alone (a graph of back-to-back repeats).
  * The buffers of that launch must still be allocated; a workspace growth
- * forgets the kept launches. A repeat writes the same outputs again while
+ * forgets the kept launches, and each forward (backward) call forgets those
+ * of the kernels its pass may launch, so only the pass's latest call's
+ * launches repeat (a kernel that call did not launch is refused with
+ * LRQ_EINVAL: at ranks 8 and 16 on the mid-size tiles, one bwd_dx launch
+ * also forms u, dA and dB). A repeat writes the same outputs again while
  * the buffers it reads hold what they held at the launch: the workspace is
  * shared by the passes (the backward reuses the forward's slot of the B^T
  * rows for A), so a forward kernel repeated after a backward reads other
