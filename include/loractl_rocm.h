@@ -267,8 +267,9 @@ int lrq_debug_force_wait_timeout(int on);
 /* Tuning and test hook, no counterpart in the reference: which kernel the
  * fused products of m > 16 tokens take in this process. 0 (the default) the
  * planned one; 1 the 256-token tiles (split in depth when too few); 2 and 3
- * the 64-row tiles of 64 or 128 tokens over the whole depth. Every path
- * computes the same products; a workspace sized by lrq_reserve under one
+ * the 64-row tiles of 64 or 128 tokens (depth ranges as planned); 4 and 5
+ * the same tiles with at least two depth ranges wherever the depth has two
+ * whole rounds of their pipeline. Every path computes the same products; a workspace sized by lrq_reserve under one
  * setting grows on the next hot call if another needs more. */
 int lrq_debug_gemm_path(int path);
 

@@ -437,7 +437,7 @@ int lrq_probe_stream_read(lrq_ctx* c, const void* data, int64_t bytes) {
 }
 
 int lrq_debug_gemm_path(int path) {
-  if (path < 0 || path > 3) return LRQ_EINVAL;
+  if (path < 0 || path > 5) return LRQ_EINVAL;
   set_gemm_path(path);
   return LRQ_OK;
 }
@@ -449,6 +449,21 @@ int lrq_debug_force_wait_timeout(int on) {
 
 const char* lrq_last_error(const lrq_ctx* c) { return c ? c->err : "null context"; }
 
+// Workspace floats of the mid-size passes at ranks 8 and 16 that form the
+// LoRA factors in their own launch: the factor's slice partials, then the
+// tiles' depth-range partials, then (backward) dB's and dA's token-slice
+// partials (both jobs counted).
+static int64_t fold_fwd_floats(int64_t m, int64_t n, int64_t k) {
+  const int64_t G = (m + 63) / 64, fs = (k + MID_FOLD_KT - 1) / MID_FOLD_KT;
+  return round_up(fs * G * 64 * 16, 64) + mid_split_plan(m, n, k).floats;
+}
+static int64_t fold_bwd_floats(int64_t m, int64_t n, int64_t k, int rp) {
+  const int64_t G = (m + 63) / 64, fs = (n + MID_FOLD_KT - 1) / MID_FOLD_KT;
+  const LoraPlan tpb = mid_tn_plan(m, n, rp), tpa = mid_tn_plan(m, k, rp);
+  return round_up(fs * G * 64 * 16, 64) + round_up(mid_split_plan(m, k, n).floats, 64) +
+         (tpb.splits > 1 ? (int64_t)tpb.splits * n * rp : 0) + (tpa.splits > 1 ? (int64_t)tpa.splits * k * rp : 0);
+}
+
 int lrq_reserve(lrq_ctx* c, int64_t m, int64_t n, int64_t k, int64_t r) {
   LRQ_TRY(begin(c));
   if (m < 0 || n < 0 || k < 0 || r < 0 || r > 64) return fail(c, LRQ_EINVAL, "bad reserve shape");
@@ -456,10 +471,10 @@ int lrq_reserve(lrq_ctx* c, int64_t m, int64_t n, int64_t k, int64_t r) {
   size_t need = lora_layout(nullptr, m, n, k, rp).bytes;
   // the fused GEMMs' split partials are not monotonic in the token count
   // (fewer tiles, more depth ranges): their largest size over m' <= m, which
-  // peaks at a whole number of 256-token tiles
+  // peaks at a whole number of 64-token tiles
   const int64_t gp_m = gemm_part_floats(m, n, k);
   int64_t gp_max = gp_m;
-  for (int64_t mm = 256; mm < m; mm += 256) gp_max = std::max(gp_max, gemm_part_floats(mm, n, k));
+  for (int64_t mm = 64; mm < m; mm += 64) gp_max = std::max(gp_max, gemm_part_floats(mm, n, k));
   need += (size_t)(gp_max - gp_m) * 4;
   if (m >= 1) {  // the few-token forward, at up to 16 tokens
     const size_t sk = skinny_ws_bytes(skinny_plan(n, k, rp, get_num_cus()), m < 16 ? m : 16, n, rp);
@@ -469,6 +484,16 @@ int lrq_reserve(lrq_ctx* c, int64_t m, int64_t n, int64_t k, int64_t r) {
     const size_t skd = lora_layout(nullptr, mm, n, k, rp).bytes +
                        skinny_ws_bytes(skinny_plan(k, n, rp, get_num_cus()), mm, k, rp);
     if (skd > need) need = skd;
+  }
+  if ((r == 8 || r == 16) && m > 16) {
+    // the one-launch mid-size passes, at every token count up to m
+    const size_t lb = lora_layout(nullptr, m, n, k, rp).bytes;
+    for (int64_t mm = 64;; mm += 64) {
+      const int64_t mt = mm < m ? mm : m;
+      need = std::max(need, (size_t)fold_fwd_floats(mt, n, k) * 4);
+      need = std::max(need, lb + (size_t)fold_bwd_floats(mt, n, k, rp) * 4);
+      if (mt == m) break;
+    }
   }
   const size_t fp8_need = (size_t)round_up(n * 4, 256);
   if (fp8_need > need) need = fp8_need;
@@ -680,14 +705,20 @@ static int fwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t 
     // mid-size tiles at rank 8 or 16: t is formed in the same launch by
     // workgroups ahead of the tiles (no side launch)
     const int64_t G = (m + 63) / 64, fs = (w->k + MID_FOLD_KT - 1) / MID_FOLD_KT;
+    // (and the tiles' depth ranges, if any: partials after t's, counters
+    // after the fold's)
+    const MidSplit ms = mid_split_plan(m, w->n, w->k);
     if ((r == 8 || r == 16) && gemm_mid_tokens(m, w->n, w->k) > 0 && aligned16(a) && t_out && aligned16(t_out) &&
-        2 * G <= SK_MAX_NB) {
-      LRQ_TRY(acquire_ws(c, src, (size_t)fs * G * 64 * 16 * 4, &ws, &cnt));
+        2 * G + ms.tiles <= SK_MAX_NB) {
+      const int64_t fp = round_up(fs * G * 64 * 16, 64);
+      LRQ_TRY(acquire_ws(c, src, (size_t)(fp + ms.floats) * 4, &ws, &cnt));
       ga.fold = force_wait_timeout() ? -1 : 1;
       ga.fold_slices = (int)fs;
       ga.fold_wgs = (int)round_up(fs * G, 8);
       ga.fpart = reinterpret_cast<float*>(ws);
       ga.fcnt = cnt;
+      ga.part = ms.floats > 0 ? ga.fpart + fp : nullptr;
+      ga.mcnt = cnt + 2 * G;
       ga.lact = a;
       ga.lw = b;
       ga.fscale = scaling;
@@ -714,11 +745,13 @@ static int fwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t 
     ga.r = (int)r;
     ga.rp = rp;
     ga.part = lw.gp;
+    ga.mcnt = cnt;
   } else {
     const int64_t pf = gemm_split_floats(m, w->n, w->k);
     if (pf > 0) {
       LRQ_TRY(acquire_ws(c, src, (size_t)pf * 4, &ws, &cnt));
       ga.part = reinterpret_cast<float*>(ws);
+      ga.mcnt = cnt;
     }
   }
   return run_hot(c, KID_FWD_MAIN, "fwd_main", [=] { return launch_fwd(c->stream, fmt, ga); });
@@ -805,17 +838,20 @@ static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const ui
     // workspace)
     const int64_t G = (m + 63) / 64, fs = (w->n + MID_FOLD_KT - 1) / MID_FOLD_KT;
     const bool fold = !few && dx && (r == 8 || r == 16) && gemm_mid_tokens(m, w->k, w->n) > 0 && aligned16(a) &&
-                      2 * G <= SK_MAX_NB;
+                      2 * G + mid_split_plan(m, w->k, w->n).tiles <= SK_MAX_NB;
     // and the weight gradients by workgroups after its tiles, in token
     // slices that fit its LDS (their counters after the fold's, partials
     // after u's)
     const LoraPlan tpb = fold ? mid_tn_plan(m, w->n, rp) : LoraPlan{}, tpa = fold ? mid_tn_plan(m, w->k, rp) : LoraPlan{};
     const int64_t tb_floats = (db && tpb.splits > 1) ? (int64_t)tpb.splits * w->n * rp : 0;
     const int64_t ta_floats = (da && tpa.splits > 1) ? (int64_t)tpa.splits * w->k * rp : 0;
+    // the tiles' depth ranges, if any (their partials and counters first)
+    const MidSplit ms = fold ? mid_split_plan(m, w->k, w->n) : MidSplit{1, 0, 0, 0};
     const bool fold_tn = fold && (da || db) && tpb.splits > 0 && tpa.splits > 0 &&
-                         2 * G + TN_WAVES * ((db ? tpb.tiles : 0) + (da ? tpa.tiles : 0)) <= SK_MAX_NB;
+                         2 * G + ms.tiles + TN_WAVES * ((db ? tpb.tiles : 0) + (da ? tpa.tiles : 0)) <= SK_MAX_NB;
     const int64_t fp_floats = round_up(fs * G * 64 * 16, 64);
-    const size_t fbytes = fold ? (size_t)(fp_floats + (fold_tn ? tb_floats + ta_floats : 0)) * 4 : 0;
+    const int64_t ms_floats = round_up(ms.floats, 64);
+    const size_t fbytes = fold ? (size_t)(fp_floats + ms_floats + (fold_tn ? tb_floats + ta_floats : 0)) * 4 : 0;
     LRQ_TRY(ensure_ws(c, lbytes + (few ? skinny_ws_bytes(sp, m, w->k, rp) : fbytes)));
     LoraWs ws = lora_layout(c->ws, m, w->n, w->k, rp);
     ga.r = (int)r;
@@ -847,10 +883,12 @@ static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const ui
       ga.fscale = scaling;
       ga.fout = ws.up;
       ga.fout_ld = rp;
+      ga.part = ms.floats > 0 ? ga.fpart + fp_floats : nullptr;
+      ga.mcnt = c->cnt + 2 * G;
       if (fold_tn) {
         // dB = t^T . dy first (nothing to wait for), then dA = x^T . u
-        float* tpart = ga.fpart + fp_floats;
-        uint32_t* tcnt = c->cnt + 2 * G;
+        float* tpart = ga.fpart + fp_floats + ms_floats;
+        uint32_t* tcnt = c->cnt + 2 * G + ms.tiles;
         int nj = 0;
         if (db) {
           ga.tj[nj++] = tn_args(TnSpec{dy, t, r, m, w->n, (int)r, tpb, tpart, db, 1, w->n}, tcnt);
@@ -877,6 +915,7 @@ static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const ui
       ga.lact = ws.up;
       ga.lw = ws.fr;
       ga.part = ws.gp;
+      ga.mcnt = c->cnt;
       if (dx) LRQ_TRY(run_hot(c, KID_BWD_DX, "bwd_dx", [=] { return launch_bwd(c->stream, fmt, ga); }));
     }
     // dA = x^T . u -> f32 [k, r] and dB = t^T . dy -> f32 [r, n]: token-slice
@@ -902,7 +941,10 @@ static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const ui
   if (!dx) return LRQ_OK;
   const int64_t pf = (m >= 1 && m <= 16) ? 0 : gemm_split_floats(m, w->k, w->n);
   LRQ_TRY(ensure_ws(c, std::max((size_t)pf * 4, skinny_dx_bytes(w, m))));
-  if (pf > 0) ga.part = reinterpret_cast<float*>(c->ws);
+  if (pf > 0) {
+    ga.part = reinterpret_cast<float*>(c->ws);
+    ga.mcnt = c->cnt;
+  }
   float* skpart = reinterpret_cast<float*>(c->ws);
   return run_hot(c, KID_BWD_DX, "bwd_dx", [=] { return launch_dx(c, fmt, wn, wk, ga, m, skpart); });
 }

@@ -661,14 +661,23 @@ hipError_t run_fmt(hipStream_t st, int fmt, bool r192, const GemmArgs& a) {
 //   - a 64-wide depth block of a mid tile takes MID_T1 us when its
 //     workgroup has the CU to itself and MID_T2 us each when two share it
 //     (64 tokens: 0.342 / 0.423, 128 tokens: 0.441 / 0.696); the tiles are
-//     dealt over the CUs, two at a time.
+//     dealt over the CUs, two at a time;
+//   - a mid tile may split its depth into S <= MID_MAX_SPLIT ranges (one
+//     workgroup each, whole rounds of MID_MST stages) when its tiles leave
+//     CUs idle; the ranges' accumulators meet in the launch, about
+//     MID_FINISH_US more, and S > 1 must model at least a tenth faster.
 constexpr double LARGE_STEP_US = 1.86;
 // per variant MID_64, MID_128: tile tokens, block us alone and shared, and
 // a fixed cost per round of tiles
 constexpr int MID_T[3] = {0, 64, 128};
 constexpr double MID_T1[3] = {0, 0.342, 0.441}, MID_T2[3] = {0, 0.423, 0.696};
 constexpr double MID_FIX[3] = {0, 2.0, 2.0};
-int g_gemm_path = 0;  // lrq_debug_gemm_path: 0 planned, 1 large tiles, 2 + (variant - 1) a mid variant
+constexpr int MID_SD[3] = {0, 2, 1};  // 64-deep blocks per pipeline stage
+constexpr double MID_FINISH_US = 3.0;
+// lrq_debug_gemm_path: 0 planned, 1 large tiles, 2 + (variant - 1) a mid
+// variant, 4 + (variant - 1) a mid variant with at least two depth ranges
+// where the depth has them
+int g_gemm_path = 0;
 
 double large_us(int64_t m, int64_t e, int64_t depth) {
   const SplitPlan p = plan_split(m, e, depth);
@@ -681,36 +690,78 @@ double large_us(int64_t m, int64_t e, int64_t depth) {
   return (double)p.spl * LARGE_STEP_US * f + 2.0 * part / 4.0e6 + 8.0;
 }
 
-double mid_us(int64_t m, int64_t e, int64_t depth, int v) {
-  const int64_t T = MID_T[v], cus = get_num_cus();
-  const int64_t tiles = (m + T - 1) / T * ((e + 63) / 64);
-  const int64_t n = (tiles + cus - 1) / cus, nb = (depth + 63) / 64;
-  return (double)nb * ((double)(n / 2) * MID_T2[v] + (double)(n % 2) * MID_T1[v]) +
-         MID_FIX[v] * (double)((n + 1) / 2);
+// stages per range (whole rounds) for S ranges of a depth, and the ranges
+// that gives
+int mid_spl(int64_t depth, int v, int S) {
+  const int64_t nst = ((depth + 63) / 64 + MID_SD[v] - 1) / MID_SD[v];
+  return (int)(((nst + S - 1) / S + MID_MST - 1) / MID_MST * MID_MST);
+}
+int mid_ranges(int64_t depth, int v, int S) {
+  const int64_t nst = ((depth + 63) / 64 + MID_SD[v] - 1) / MID_SD[v];
+  const int spl = mid_spl(depth, v, S);
+  return (int)((nst + spl - 1) / spl);
 }
 
-// MID_NONE (the large tiles) or the mid variant a shape takes
-int mid_plan(int64_t m, int64_t e, int64_t depth) {
-  if (m <= 0 || e <= 0) return MID_NONE;
-  if (g_gemm_path == 1) return MID_NONE;
-  if (g_gemm_path >= 2) return g_gemm_path - 1;
-  double best = large_us(m, e, depth);
-  int pick = MID_NONE;
+double mid_us(int64_t m, int64_t e, int64_t depth, int v, int S = 1) {
+  const int64_t T = MID_T[v], cus = get_num_cus();
+  const int64_t tiles = (m + T - 1) / T * ((e + 63) / 64) * S;
+  const int64_t n = (tiles + cus - 1) / cus;
+  const int64_t nb = S > 1 ? std::min<int64_t>((int64_t)mid_spl(depth, v, S) * MID_SD[v], (depth + 63) / 64)
+                           : (depth + 63) / 64;
+  return (double)nb * ((double)(n / 2) * MID_T2[v] + (double)(n % 2) * MID_T1[v]) +
+         MID_FIX[v] * (double)((n + 1) / 2) + (S > 1 ? MID_FINISH_US : 0.0);
+}
+
+struct MidChoice {
+  int v, S, spl;
+  double us;
+};
+
+// the best number of depth ranges for variant v (forced: at least two
+// where the depth has them)
+MidChoice mid_best_split(int64_t m, int64_t e, int64_t depth, int v, bool force_split) {
+  MidChoice best{v, 1, 0, mid_us(m, e, depth, v, 1)};
+  MidChoice alt{v, 1, 0, 1e30};
+  for (int S = 2; S <= MID_MAX_SPLIT; ++S) {
+    const int R = mid_ranges(depth, v, S);
+    if (R < 2 || R != S) continue;  // (S that rounding turns into fewer ranges are covered by those)
+    const double t = mid_us(m, e, depth, v, S);
+    if (t < alt.us) alt = MidChoice{v, S, mid_spl(depth, v, S), t};
+  }
+  if (alt.S > 1 && (force_split || alt.us < 0.9 * best.us)) return alt;
+  return best;
+}
+
+// the mid variant and its depth ranges a shape takes (v = MID_NONE: the
+// large tiles)
+MidChoice mid_choice(int64_t m, int64_t e, int64_t depth) {
+  const MidChoice none{MID_NONE, 1, 0, 0.0};
+  if (m <= 0 || e <= 0 || g_gemm_path == 1) return none;
+  if (g_gemm_path >= 2) return mid_best_split(m, e, depth, (g_gemm_path - 2) % 2 + 1, g_gemm_path >= 4);
+  MidChoice pick = none;
+  pick.us = large_us(m, e, depth);
   for (int v : {MID_64, MID_128}) {
-    const double t = mid_us(m, e, depth, v);
-    if (t < best) {
-      best = t;
-      pick = v;
-    }
+    const MidChoice c = mid_best_split(m, e, depth, v, false);
+    if (c.us < pick.us) pick = c;
   }
   return pick;
 }
 
+// MID_NONE (the large tiles) or the mid variant a shape takes
+int mid_plan(int64_t m, int64_t e, int64_t depth) { return mid_choice(m, e, depth).v; }
+
 template <bool BWD>
 hipError_t dispatch(hipStream_t st, int fmt, const GemmArgs& a) {
   if (a.m == 0 || a.e == 0) return hipSuccess;
-  const int mv = mid_plan(a.m, a.e, a.l);
-  if (mv != MID_NONE) return launch_mid(st, fmt, BWD, a, mv);
+  const MidChoice mc = mid_choice(a.m, a.e, a.l);
+  if (mc.v != MID_NONE) {
+    if (mc.S <= 1) return launch_mid(st, fmt, BWD, a, mc.v);
+    if (!a.part || !a.mcnt) return hipErrorInvalidValue;
+    GemmArgs b = a;
+    b.msplit = mc.S;
+    b.mspl = mc.spl;
+    return launch_mid(st, fmt, BWD, b, mc.v);
+  }
   const SplitPlan p = plan_split(a.m, a.e, a.l);
   if (p.S <= 1) return run_fmt<BWD, false>(st, fmt, p.r192, a);
   if (!a.part) return hipErrorInvalidValue;
@@ -734,9 +785,16 @@ void set_num_cus(int n) { g_num_cus_ = n > 0 ? n : 256; }
 int get_num_cus() { return g_num_cus_; }
 
 hipError_t launch_fwd(hipStream_t st, int fmt, const GemmArgs& a) { return dispatch<false>(st, fmt, a); }
+MidSplit mid_split_plan(int64_t m, int64_t e, int64_t depth) {
+  const MidChoice mc = mid_choice(m, e, depth);
+  if (mc.v == MID_NONE || mc.S <= 1) return MidSplit{1, 0, 0, 0};
+  const int64_t T = MID_T[mc.v], tiles = (m + T - 1) / T * ((e + 63) / 64);
+  return MidSplit{mc.S, mc.spl, tiles, (int64_t)mc.S * tiles * T * 64};
+}
+
 int64_t gemm_split_floats(int64_t m, int64_t e, int64_t depth) {
   if (m <= 0 || e <= 0) return 0;
-  if (mid_plan(m, e, depth)) return 0;  // the mid kernel keeps no partials
+  if (mid_plan(m, e, depth)) return mid_split_plan(m, e, depth).floats;  // the mid tiles' depth ranges
   const SplitPlan p = plan_split(m, e, depth);
   return p.S > 1 ? (int64_t)p.S * m * e : 0;
 }

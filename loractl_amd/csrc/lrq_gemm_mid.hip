@@ -79,7 +79,7 @@ constexpr uint32_t MID_MAX_POLLS = 1u << 22;  // about 0.2 s of s_sleep 2
 
 constexpr int MD = 64;    // depth per step (one 64 x 64 weight block)
 constexpr int MR = 64;    // rows per tile: four wavefronts of 16
-constexpr int MST = 4;    // pipeline stages
+constexpr int MST = MID_MST;  // pipeline stages
 
 // LDS chunk swizzle: rows r and r + 1 share a chunk order, so the 16 rows a
 // quarter-wavefront reads at one logical chunk cover all 64 banks
@@ -249,6 +249,10 @@ __global__ void __launch_bounds__(256, 2) k_mid(GemmArgs a, int tiles_m, int til
   __shared__ __attribute__((aligned(16))) uint16_t sx3[XB];
 
   const int ntiles = tiles_m * tiles_e;
+  // depth ranges per tile (msplit > 1: the tile's ranges are consecutive
+  // units, the last to finish sums them; see the epilogue)
+  const int S = a.msplit > 1 ? a.msplit : 1;
+  const int nunits = ntiles * S;
   // FOLD: the launch's stamp, and the factor workgroups ahead of the tiles
   // (the test hook, a.fold < 0, makes the tiles wait for a stamp no
   // launch publishes)
@@ -261,16 +265,17 @@ __global__ void __launch_bounds__(256, 2) k_mid(GemmArgs a, int tiles_m, int til
     }
     want = stamp + (a.fold < 0 ? 0x40000000u : 0u);
     if constexpr (BWD) {
-      if ((int)blockIdx.x >= a.fold_wgs + ntiles) {
+      if ((int)blockIdx.x >= a.fold_wgs + nunits) {
         static_assert(MID_TN_LDS <= XB * 2, "a weight-gradient block's LDS fits one stage buffer");
         const int nda = a.tn_da >= 0 ? a.tj[a.tn_da].blocks : 0;
-        mid_tn(a, (int)blockIdx.x - a.fold_wgs - ntiles, want, ntiles + nda, sx0, sx1);
+        mid_tn(a, (int)blockIdx.x - a.fold_wgs - nunits, want, ntiles + nda, sx0, sx1);
         return;
       }
     }
   }
   const int vb = FOLD ? (int)blockIdx.x - a.fold_wgs : (int)blockIdx.x;
-  const int lt = xcd_remap(vb, ntiles);
+  const int lu = xcd_remap(vb, nunits);
+  const int lt = lu / S, sp = lu % S;
   const int per = group_m * tiles_e;
   const int grp = lt / per, within = lt % per;
   const int gm = min(group_m, tiles_m - grp * group_m);
@@ -283,8 +288,12 @@ __global__ void __launch_bounds__(256, 2) k_mid(GemmArgs a, int tiles_m, int til
   const int q = lane >> 4, l16 = lane & 15;
   const int64_t KB = (D + 63) / 64;
   const int nk = (int)KB;
-  // stages of SD blocks, in whole rounds of MST stages
-  const int nsp = ((nk + SD - 1) / SD + MST - 1) / MST * MST;
+  // stages of SD blocks, in whole rounds of MST stages: the whole depth, or
+  // range sp's a.mspl stages (a multiple of MST) from stage s0, the last
+  // range rounded up past the depth (which reads zeros)
+  const int nst = (nk + SD - 1) / SD;
+  const int s0 = S > 1 ? sp * a.mspl : 0;
+  const int nsp = (S > 1 && sp < S - 1) ? a.mspl : (nst - s0 + MST - 1) / MST * MST;
 
   // ---- weight: the tile's block row (64 rows = the tile), wavefront w's 16.
   // Each resource ends where this block row's data ends, so a step past the
@@ -329,7 +338,7 @@ __global__ void __launch_bounds__(256, 2) k_mid(GemmArgs a, int tiles_m, int til
   const uint32_t xo1 = (uint32_t)(((xr0 + (lane >> 3)) * D + lc1 * 8) * 2);
   const int lim0 = (int)D - 8 * lc0, lim1 = (int)D - 8 * lc1;
   auto dma = [&](uint16_t* buf, int kt) {
-    const int k0 = kt * MD;
+    const int k0 = (kt + s0 * SD) * MD;
     const bool ok0 = k0 < lim0, ok1 = k0 < lim1;
     const uint32_t ko = (uint32_t)(k0 * 2);
     __attribute__((address_space(3))) char* base =
@@ -363,7 +372,7 @@ __global__ void __launch_bounds__(256, 2) k_mid(GemmArgs a, int tiles_m, int til
   auto load_w = [&](int set, int st) {
 #pragma unroll
     for (int d = 0; d < SD; ++d) {
-      const uint32_t kt = (uint32_t)(st * SD + d);
+      const uint32_t kt = (uint32_t)((st + s0) * SD + d);
       if (I4) {
         const u32x2 v = bload8(rw, opaque_u32(woff + kt * blkb));
         wv[set][d] = (u32x4){v[0], v[1], 0u, 0u};
@@ -493,6 +502,41 @@ __global__ void __launch_bounds__(256, 2) k_mid(GemmArgs a, int tiles_m, int til
   // they are still in flight: drain them before LDS is released
   __builtin_amdgcn_s_waitcnt(0);
 
+  // ---- depth ranges: every range stores its accumulators (f32, in their
+  // own layout: unit (lt, range), token tile j, thread) at device scope and
+  // counts itself at its tile once they are acknowledged; the last to
+  // arrive sums the ranges in order (its own from registers) and goes on
+  // with the epilogue, the others are done
+  if (S > 1) {
+    const int64_t pbytes = (int64_t)nunits * TT * 256 * 16;
+    const rsrc_t rpp = make_rsrc(a.part, clamp_bytes(pbytes));
+    auto poff = [&](int r, int j) { return (uint32_t)(((((int64_t)lt * S + r) * TT + j) * 256 + tid) * 16); };
+#pragma unroll
+    for (int j = 0; j < TT; ++j) mstore16_dev(rpp, opaque_u32(poff(sp, j)), __builtin_bit_cast(u32x4, acc[j]));
+    __builtin_amdgcn_s_waitcnt(0);
+    __shared__ int last_range;
+    __syncthreads();
+    if (tid == 0) {
+      last_range = madd_dev(a.mcnt + lt) + 1 == (uint32_t)S;
+      if (last_range) mzero_dev(a.mcnt + lt);
+    }
+    __syncthreads();
+    if (!last_range) return;
+    u32x4 pr[MID_MAX_SPLIT][TT];
+#pragma unroll
+    for (int r = 0; r < MID_MAX_SPLIT; ++r)
+#pragma unroll
+      for (int j = 0; j < TT; ++j) pr[r][j] = mbload16_dev(rpp, opaque_u32(r < S && r != sp ? poff(r, j) : LRQ_OOB));
+#pragma unroll
+    for (int j = 0; j < TT; ++j) {
+      f32x4 sum = sp == 0 ? acc[j] : __builtin_bit_cast(f32x4, pr[0][j]);
+#pragma unroll
+      for (int r = 1; r < MID_MAX_SPLIT; ++r)
+        if (r < S) sum += r == sp ? acc[j] : __builtin_bit_cast(f32x4, pr[r][j]);
+      acc[j] = sum;
+    }
+  }
+
   // ---- epilogue
   const int rp = a.rp;
   if (FOLD) {
@@ -598,19 +642,20 @@ hipError_t run_mid(hipStream_t st, const GemmArgs& a, int variant) {
   const int tiles_e = (int)((a.e + MR - 1) / MR);
   const int group_m = tiles_m < 8 ? tiles_m : 8;
   const int ntiles = tiles_m * tiles_e;
+  const int S = a.msplit > 1 ? a.msplit : 1;
   // k_mid: two 64-wide blocks per stage with 64-token tiles, one with 128;
-  // 64 KiB of LDS in every variant, two workgroups per CU; with the fold,
-  // its workgroups first
+  // 64 KiB of LDS in every variant, two workgroups per CU; S units per tile
+  // with depth ranges; with the fold, its workgroups first
   if (a.fold) {
-    const unsigned grid = (unsigned)(ntiles + a.fold_wgs + (BWD ? a.tn_blocks : 0));
+    const unsigned grid = (unsigned)(ntiles * S + a.fold_wgs + (BWD ? a.tn_blocks : 0));
     if (variant == MID_128)
       hipLaunchKernelGGL((k_mid<BWD, FMT, 8, 1, true>), dim3(grid), dim3(256), 0, st, a, tiles_m, tiles_e, group_m);
     else
       hipLaunchKernelGGL((k_mid<BWD, FMT, 4, 2, true>), dim3(grid), dim3(256), 0, st, a, tiles_m, tiles_e, group_m);
   } else if (variant == MID_128) {
-    hipLaunchKernelGGL((k_mid<BWD, FMT, 8, 1, false>), dim3(ntiles), dim3(256), 0, st, a, tiles_m, tiles_e, group_m);
+    hipLaunchKernelGGL((k_mid<BWD, FMT, 8, 1, false>), dim3(ntiles * S), dim3(256), 0, st, a, tiles_m, tiles_e, group_m);
   } else {
-    hipLaunchKernelGGL((k_mid<BWD, FMT, 4, 2, false>), dim3(ntiles), dim3(256), 0, st, a, tiles_m, tiles_e, group_m);
+    hipLaunchKernelGGL((k_mid<BWD, FMT, 4, 2, false>), dim3(ntiles * S), dim3(256), 0, st, a, tiles_m, tiles_e, group_m);
   }
   return hipGetLastError();
 }
@@ -621,6 +666,18 @@ hipError_t launch_mid(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, int 
   if (a.m <= 0 || a.e <= 0) return hipSuccess;
   if (variant != MID_64 && variant != MID_128) return hipErrorInvalidValue;
   if (a.rp > 64 || a.rp % 16 != 0) return hipErrorInvalidValue;
+  // depth ranges: at most MID_MAX_SPLIT, each whole rounds of stages, the
+  // last one non-empty; partials for every unit and a counter per tile
+  const int T = variant == MID_64 ? 64 : 128, SDv = variant == MID_64 ? 2 : 1;
+  const int64_t ntiles = (a.m + T - 1) / T * ((a.e + MR - 1) / MR);
+  const int S = a.msplit > 1 ? a.msplit : 1;
+  if (S > 1) {
+    const int64_t nst = ((a.l + 63) / 64 + SDv - 1) / SDv;
+    if (S > MID_MAX_SPLIT || a.mspl <= 0 || a.mspl % MST != 0 || (int64_t)(S - 1) * a.mspl >= nst ||
+        (int64_t)S * a.mspl < nst || !a.part || !a.mcnt ||
+        (int64_t)S * ntiles * T * 64 * 4 >= ((int64_t)1 << 32))
+      return hipErrorInvalidValue;
+  }
   // the fold: rank 8 or 16, both raw factors, its output, partials and
   // counters (groups' arrivals and flags within the counter area), and
   // enough factor workgroups, whole groups of eight
@@ -640,6 +697,7 @@ hipError_t launch_mid(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, int 
           a.tn_da > 1 || (a.tn_da >= 0 && a.tj[a.tn_da].blocks == 0))
         return hipErrorInvalidValue;
       const uint32_t* lo = a.fcnt + 2 * G;
+      if (S > 1 && a.mcnt + ntiles > lo) lo = a.mcnt + ntiles;
       for (int i = 0; i < 2; ++i) {
         const TnArgs& j = a.tj[i];
         if (j.blocks == 0) continue;
@@ -655,6 +713,8 @@ hipError_t launch_mid(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, int 
         lo = j.cnt + TN_WAVES * j.tiles;
       }
     }
+    // the tiles' range counters past the fold's
+    if (S > 1 && (a.mcnt < a.fcnt + 2 * G || a.mcnt + ntiles > a.fcnt + SK_MAX_NB)) return hipErrorInvalidValue;
   } else if (a.tn_blocks != 0) {
     return hipErrorInvalidValue;
   }

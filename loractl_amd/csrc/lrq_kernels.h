@@ -88,6 +88,13 @@ struct GemmArgs {
   // the counter area past the fold's [0, 2 G).
   TnArgs tj[2];
   int tn_blocks, tn_da;
+  // lrq_gemm_mid.hip with depth ranges (msplit in 2 .. MID_MAX_SPLIT): each
+  // tile's depth in msplit ranges of mspl stages (a multiple of 4; the last
+  // range to the end), one workgroup each; their f32 accumulators go to
+  // `part` (msplit x tiles x tokens x 64), mcnt holds one arrival counter per
+  // tile (zero on entry and exit). Set by lrq_gemm.hip's planner.
+  int msplit, mspl;
+  uint32_t* mcnt;
 };
 
 // lrq_gemm.hip: the forward for m > 16 and the input gradient, weight
@@ -102,10 +109,22 @@ hipError_t launch_bwd(hipStream_t st, int fmt, const GemmArgs& a);
 int64_t gemm_split_floats(int64_t m, int64_t e, int64_t depth);
 int get_num_cus();
 // lrq_gemm_mid.hip: the same products on 64-row tiles of 64 or 128 tokens
-// over the whole depth, 16 rows per wavefront, no partials (MID_64,
-// MID_128); lrq_gemm.hip's launchers take one when it is modelled faster
-// (gemm_mid_tokens: its tile's tokens, or 0)
+// over the whole depth or a few depth ranges finished in the launch, 16
+// rows per wavefront (MID_64, MID_128); lrq_gemm.hip's launchers take one
+// when it is modelled faster (gemm_mid_tokens: its tile's tokens, or 0).
+// With depth ranges the caller provides a.part (gemm_split_floats) and
+// a.mcnt (mid_split_plan(...).tiles counters).
 enum { MID_NONE = 0, MID_64 = 1, MID_128 = 2 };
+constexpr int MID_MAX_SPLIT = 4;
+constexpr int MID_MST = 4;  // the mid kernel's pipeline stages (a range is whole rounds of them)
+// The mid-size tiles' depth ranges for a product (m tokens, e outputs,
+// `depth`): S = 1 (whole depth) when the large tiles or one range per tile
+// are modelled faster; tiles and the partial floats the ranges need.
+struct MidSplit {
+  int S, spl;
+  int64_t tiles, floats;
+};
+MidSplit mid_split_plan(int64_t m, int64_t e, int64_t depth);
 hipError_t launch_mid(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, int variant);
 int gemm_mid_tokens(int64_t m, int64_t e, int64_t depth);
 // depth per slice of the folded factor's workgroups (GemmArgs.fold)

@@ -371,14 +371,16 @@ def debug_force_wait_timeout(on: bool):
     L.load().lrq_debug_force_wait_timeout(int(on))
 
 
-GEMM_PATHS = {"planned": 0, "large": 1, "mid64": 2, "mid128": 3}
+GEMM_PATHS = {"planned": 0, "large": 1, "mid64": 2, "mid128": 3, "mid64s": 4, "mid128s": 5}
 
 
 def debug_gemm_path(path: str):
     """Tuning and test hook: force the kernel the fused products of m > 16
     tokens take in this process ("planned", "large": the 256-token tiles,
     split in depth when too few, "mid64" / "mid128": 64-row tiles of 64 or
-    128 tokens over the whole depth). Every path computes the same products."""
+    128 tokens, with depth ranges as planned, "mid64s" / "mid128s": the same
+    with at least two depth ranges where the depth allows). Every path
+    computes the same products."""
     L.load().lrq_debug_gemm_path(GEMM_PATHS[path])
 
 

@@ -195,14 +195,14 @@ def test_bias_epilogue(cuda):
     check("y+bias", y, y_ref)
 
 
-@pytest.mark.parametrize("path", ["large", "mid64", "mid128"])
+@pytest.mark.parametrize("path", ["large", "mid64", "mid128", "mid64s", "mid128s"])
 @pytest.mark.parametrize("fmt,per_channel", [("int4", True), ("fp8", True), ("fp8", False), ("int8", True)])
 def test_split_depth_bias_and_scales(cuda, fmt, per_channel, path):
     """Few output tiles (M = 200, d_out = 3072). On the large tiles the depth
     is split into ranges whose f32 partials a reduction sums, and the bias
     and the forward fp8 channel scales (or the scalar) are applied there,
-    once; the mid-size tiles run the whole depth and apply them in their
-    epilogue."""
+    once; the mid-size tiles run the whole depth ("mid64s", "mid128s": in
+    depth ranges summed in the launch) and apply them in their epilogue."""
     M, K, N, r = 200, 3072, 3072, 16
     g = torch.Generator(device=cuda).manual_seed(7)
     w = torch.randn(N, K, device=cuda, generator=g) * 0.02
@@ -335,11 +335,11 @@ def test_baseline_shapes_against_torch_fp32(cuda, M, K, N, r, fmt):
 
 # m > 16: ragged token counts (not a multiple of 64 or 128), K % 64 == 32,
 # d_out not a multiple of 64, groups 32 to 128
-PATH_SHAPES = [(37, 96, 72, 32), (130, 192, 520, 64), (300, 320, 264, 64), (513, 512, 392, 128)]
+PATH_SHAPES = [(37, 96, 72, 32), (130, 192, 520, 64), (300, 320, 264, 64), (513, 512, 392, 128), (200, 1536, 1280, 64)]
 
 
 @pytest.mark.parametrize("r", [33, 16, 8])
-@pytest.mark.parametrize("path", ["large", "mid64", "mid128"])
+@pytest.mark.parametrize("path", ["large", "mid64", "mid128", "mid64s", "mid128s"])
 @pytest.mark.parametrize("fmt,per_channel", [("int4", True), ("int8", True), ("fp8", True), ("fp8", False)])
 @pytest.mark.parametrize("M,K,N,g", PATH_SHAPES)
 def test_gemm_paths_against_oracle(cuda, M, K, N, g, fmt, per_channel, path, r):
@@ -347,7 +347,8 @@ def test_gemm_paths_against_oracle(cuda, M, K, N, g, fmt, per_channel, path, r):
     they are few, and the 64-row tiles of 64 or 128 tokens) on the same
     inputs: y (with bias), t, dx, dA and dB of the fused site, and the plain
     product and its input gradient, against the f64 oracle. At ranks 8 and
-    16 the 64-row tiles form t and u themselves (no side launches)."""
+    16 the 64-row tiles form t, u, dA and dB in their own launches; "mid64s"
+    and "mid128s" split their depth into ranges where it allows."""
     w, x, a, b, dy = case_inputs(M, K, N, r, seed=7 * M + N + g)
     wq, wdq = _weight(w, fmt, g, cuda, per_channel)
     bias = np.linspace(-0.5, 0.5, N).astype(np.float32)

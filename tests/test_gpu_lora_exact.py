@@ -39,6 +39,8 @@ PATHS = [
     ("tiled r256", 4096, 4096, 4096, "large"),
     ("mid 64-token tiles", 300, 3072, 3064, "mid64"),
     ("mid 128-token tiles", 300, 1088, 1032, "mid128"),
+    ("mid 64-token tiles, depth ranges", 200, 3072, 2560, "mid64s"),
+    ("mid 128-token tiles, depth ranges", 256, 2560, 9728, "mid128s"),
 ]
 RANKS = [16, 32, 33, 48, 64]
 
