@@ -673,7 +673,7 @@ constexpr int MID_T[3] = {0, 64, 128};
 constexpr double MID_T1[3] = {0, 0.342, 0.441}, MID_T2[3] = {0, 0.423, 0.696};
 constexpr double MID_FIX[3] = {0, 2.0, 2.0};
 constexpr int MID_SD[3] = {0, 2, 1};  // 64-deep blocks per pipeline stage
-constexpr double MID_FINISH_US = 3.0;
+constexpr double MID_FINISH_US = 5.0;
 // lrq_debug_gemm_path: 0 planned, 1 large tiles, 2 + (variant - 1) a mid
 // variant, 4 + (variant - 1) a mid variant with at least two depth ranges
 // where the depth has them

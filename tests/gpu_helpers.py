@@ -41,7 +41,7 @@ def check(name, got, ref, tol_rel=TOL_REL, tol_cos=TOL_COS):
 @contextlib.contextmanager
 def gemm_path(path):
     """Run the block with the fused products of m > 16 tokens forced onto one
-    kernel path ("planned", "large", "mid64", "mid128")."""
+    kernel path ("planned", "large", "mid64", "mid128", "mid64s", "mid128s")."""
     from loractl_amd import device as D
 
     D.debug_gemm_path(path)

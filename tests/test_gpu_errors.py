@@ -28,8 +28,9 @@ def _weight(cuda, w, group=64):
 
 @pytest.mark.parametrize(
     "M,K,N,path",
-    [(4, 3072, 12288, "planned"), (4, 1024, 4096, "planned"), (192, 1024, 1536, "mid64"), (256, 1152, 1024, "mid128")],
-    ids=["whole-depth", "splits", "mid64-fold", "mid128-fold"],
+    [(4, 3072, 12288, "planned"), (4, 1024, 4096, "planned"), (192, 1024, 1536, "mid64"), (256, 1152, 1024, "mid128"),
+     (200, 3072, 2560, "mid64s")],
+    ids=["whole-depth", "splits", "mid64-fold", "mid128-fold", "mid64-ranges-fold"],
 )
 def test_few_token_wait_timeout_is_reported_and_cleared(cuda, M, K, N, path):
     r = 16

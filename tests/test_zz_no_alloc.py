@@ -48,6 +48,19 @@ def test_noalloc_matches_lora_fwd_twice(cuda, fmt):
         assert torch.isfinite(y1.float()).all()
 
 
+def test_noalloc_mid_depth_ranges(cuda):
+    """The mid-size tiles with depth ranges (their f32 accumulators summed in
+    the launch, t formed by the fold) on the scratch array: two calls, the
+    second smaller, each bit-identical to lrq_lora_fwd."""
+    with gemm_path("mid64s"):
+        for (M, K, N, r, seed) in ((200, 3072, 2560, 16, 6), (150, 2048, 1024, 8, 7)):
+            wq, xb, ab, bb = _case(cuda, M, K, N, r, "int4", seed)
+            (y0, t0), (y1, t1) = _both(cuda, wq, xb, ab, bb, 0.75)
+            assert torch.equal(y0.view(torch.int16), y1.view(torch.int16)), (M, K, N, r)
+            assert torch.equal(t0.view(torch.int16), t1.view(torch.int16)), (M, K, N, r)
+            assert torch.isfinite(y1.float()).all()
+
+
 def test_noalloc_against_the_oracle(cuda):
     """And within the north star's tolerance of the f64 oracle."""
     M, K, N, r = 130, 512, 384, 16
