@@ -328,9 +328,11 @@ PROBE_BYTES = 256 << 20
 def profile_run(args, dev):
     """The kernels of one workload for a counter run, untimed: one warm step,
     then ``--steps`` steps (the site workloads: host-launched fwd + bwd; c5:
-    every site at M = 16, then at M = 256; skinny: the few-token forward
-    over the rotated weight copies), then one streaming read of PROBE_BYTES
-    by lrq_probe_stream_read, whose byte count calibrates FETCH_SIZE."""
+    every site at M = 16, then at M = 256; c3: every site of both streams;
+    mmdit: the checkpointed training step with its optimizer step; skinny:
+    the few-token forward over the rotated weight copies), then one
+    streaming read of PROBE_BYTES by lrq_probe_stream_read, whose byte count
+    calibrates FETCH_SIZE."""
     import math
 
     import torch
@@ -377,8 +379,29 @@ def profile_run(args, dev):
             del ls
             torch.cuda.empty_cache()
         ran = "; ".join(ran)
+    elif w == "c3":
+        sites = [(M, K, N, 32, 32.0) for (_name, M) in C3_STREAMS for (K, N) in C3_SITES]
+        ls = LinearSet(dev, sites, seed=3)
+        ls.run(1 + args.steps)
+        torch.cuda.synchronize()
+        ran = f"c3: {1 + args.steps} steps"
+    elif w == "mmdit":
+        from loractl_amd.mmdit import Mmdit, MmditConfig, build_mmdit_adapters, checkpointed_step, flow_batch
+
+        cfg = MmditConfig()
+        model = Mmdit(cfg, dev, seed=0)
+        ad = build_mmdit_adapters(cfg, dev, seed=1)
+        batch = flow_batch(cfg, *MMDIT_TOKENS, dev, seed=2)
+        opt = torch.optim.AdamW([p for d in ad.deltas for p in (d.lora_a, d.lora_b)], lr=1e-4, eps=1e-5,
+                                weight_decay=0.0, fused=True)
+        for i in range(1 + args.steps):
+            opt.zero_grad(set_to_none=True)
+            checkpointed_step(model, ad, batch)
+            opt.step()
+        torch.cuda.synchronize()
+        ran = f"mmdit: {1 + args.steps} steps"
     else:
-        raise SystemExit(f"--profile-run covers ns, ns8, c1, c2, c5, skinny, skinny8, not {w}")
+        raise SystemExit(f"--profile-run covers ns, ns8, c1, c2, c3, c5, mmdit, skinny, skinny8, not {w}")
     buf = torch.empty(PROBE_BYTES, dtype=torch.uint8, device=dev)
     D.probe_stream_read(buf)
     torch.cuda.synchronize()
@@ -1017,14 +1040,16 @@ def profile_kernels(run, n):
     return {k: v for k, v in prof.items() if v[1]}
 
 
-def mfma_roofline(prof, kflops, steps):
+def mfma_roofline(prof, kflops, steps, workload):
     """The roofline object of the dominant fused GEMM kernel: its algorithmic
-    flops over the profiled steps / its total launch time."""
+    flops over the profiled steps / its total launch time; `traffic` its
+    committed HBM bytes per launch (averaged over the workload's launches of
+    it), if profiled."""
     dom = max((k for k in kflops if k in prof), key=lambda k: prof[k][0])
     ms, n = prof[dom]
     achieved = kflops[dom] * steps / (ms * 1e-3) / 1e12
     return {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
-            "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+            "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": load_traffic(dom, workload),
             "flops_per_launch": kflops[dom] * steps / n, "avg_launch_us": round(1e3 * ms / n, 2),
             "launch_time_from": "per-launch HIP event brackets averaged over every site's launches (each "
                                 "bracket adds a few microseconds of markers)"}
@@ -1098,7 +1123,7 @@ def bench_c3(args, dev):
         "sanity_x2_ratio": round(ratio, 3), "warm_ms": round(warm_ms, 1),
         "kernels_us": {k: round(1e3 * v[0] / v[1], 2) for k, v in prof.items()},
         "kernel_share": {k: round(v[0] / sum(x[0] for x in prof.values()), 4) for k, v in prof.items()},
-        "roofline": mfma_roofline(prof, ls.kernel_flops(), args.steps),
+        "roofline": mfma_roofline(prof, ls.kernel_flops(), args.steps, "c3"),
         "cpu_baseline": cpu,
     }), flush=True)
 
@@ -1138,13 +1163,15 @@ def c5_measure(args, dev, Ms, with_cpu=True):
             achieved = F / (ms_step * 1e-3) / 1e12
             entry["roofline"] = {"kernel": "whole step (196 sites, forward and backward)", "bound": "mfma",
                                  "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                                 "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                                 "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                                 "traffic": load_traffic(f"step_M{M}", "c5"),
                                  "flops_per_step": F, "time_from": "graph replay of the whole step"}
         else:
             achieved = B / (ms_step * 1e-3) / 1e9
             entry["roofline"] = {"kernel": "whole step (196 weights streamed by both passes)", "bound": "hbm",
                                  "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                                 "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                                 "frac": round(achieved / PEAK_HBM_GBS, 4),
+                                 "traffic": load_traffic(f"step_M{M}", "c5"),
                                  "bytes_per_step": B, "time_from": "graph replay of the whole step"}
         if with_cpu:
             c = cpu_baseline_set(ls.rows, sites[:len(C5_LAYER)], 64, args.cpu_seconds / len(Ms),
@@ -1255,7 +1282,7 @@ def mmdit_measure(args, dev, steps, warmup, with_cpu=True):
         "fused_kernels_ms_per_step": round(fused_ms, 2),
         "fused_share_of_step": round(fused_ms / ms_step, 4),
         "kernels_ms_per_step": {k: round(v[0], 3) for k, v in fused.items()},
-        "roofline": mfma_roofline(prof, kflops, 1),
+        "roofline": mfma_roofline(prof, kflops, 1, "mmdit"),
         "workload": f"batch 1 of {img_tokens} image + {txt_tokens} text tokens, hidden {cfg.hidden}, {cfg.heads} "
                     f"heads, {cfg.layers} double-stream blocks, MLP x{cfg.mlp_ratio}, int4-g{cfg.group} frozen "
                     f"base and LoRA r={cfg.rank} on all {len(cfg.site_paths())} block linears (modulation on the "
