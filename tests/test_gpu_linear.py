@@ -278,6 +278,42 @@ def test_outputs_are_deterministic(cuda):
         assert torch.equal(u, v)
 
 
+# (M, K, N, r, path): the mid-size passes that keep state in the context's
+# counter area (fold groups' arrivals and ready flags, depth-range counters,
+# the weight gradients' counters), interleaved with a few-token call and a
+# large-tile call that use the same area
+INTERLEAVED = [(200, 3072, 2560, 16, "mid64s"), (130, 192, 520, 8, "mid128"), (9, 512, 768, 16, "planned"),
+               (513, 512, 392, 16, "mid64"), (256, 2560, 1536, 8, "mid128s"), (300, 1024, 768, 32, "large"),
+               (64, 1536, 1024, 16, "mid64")]
+
+
+def test_interleaved_calls_repeat_bit_for_bit(cuda):
+    """Three rounds over differently planned calls, forward and backward,
+    each call bit-identical to its first round: every kernel that counts or
+    flags across its workgroups leaves the counter area as it found it,
+    whatever ran before it."""
+    cases = []
+    for i, (M, K, N, r, path) in enumerate(INTERLEAVED):
+        w, x, a, b, dy = case_inputs(M, K, N, r, seed=50 + i)
+        wq, _ = _weight(w, "int4", 64, cuda)
+        cases.append((path, wq, to_dev(x, cuda), to_dev(a, cuda), to_dev(b, cuda), to_dev(dy, cuda)))
+    first = None
+    for rnd in range(3):
+        outs = []
+        for path, wq, xd, ad, bd, dyd in cases:
+            with gemm_path(path):
+                y, t = D.lora_fwd(xd, wq, ad, bd, 0.5)
+                dx, da, db = D.lora_bwd(xd, dyd, wq, ad, bd, 0.5, t)
+            outs.append((y, t, dx, da, db))
+        D.sync()
+        if first is None:
+            first = outs
+            continue
+        for i, (o1, o2) in enumerate(zip(first, outs)):
+            for name, u, v in zip(("y", "t", "dx", "dA", "dB"), o1, o2):
+                assert torch.equal(u, v), (rnd, INTERLEAVED[i], name)
+
+
 def test_shape_errors_are_loud(cuda):
     w = torch.randn(64, 96, device=cuda)
     wq = D.quantize_int4(w, 32)
