@@ -1273,6 +1273,15 @@ def mmdit_measure(args, dev, steps, warmup, with_cpu=True):
         "ms_per_step": round(ms_step, 2),
         "tflops": round(fl["total"] / (ms_step * 1e-3) / 1e12, 2),
         "flop_model": {k: fl[k] for k in ("proj", "attn", "lora", "total")},
+        # the same step's work if the modulation linears ran at the stream's
+        # token count, as a work model that treats them like the other
+        # projections counts them (not what this step executes)
+        "flop_model_mod_at_stream": {
+            k: v for k, v in mmdit_step_flops(cfg, img_tokens, txt_tokens, mod_at_stream=True).items()
+            if k in ("proj", "total")},
+        "flop_model_note": "the modulation (adaLN) linears run on the one conditioning row per batch element, "
+                           "as in a FLUX-style double-stream block; a work model that counts them at the "
+                           "stream's token count (flop_model_mod_at_stream) adds work this step does not do",
         "checkpointing": "per block, whole-block replay (re-forward in backward)",
         "attention_kept": kept,
         "sanity_x2_ratio": round(ratio, 3),

@@ -338,7 +338,7 @@ def _checkpointed_step(model: Mmdit, adapters: LoraAdapters, batch, loss_scale: 
 
 
 def mmdit_step_flops(cfg: MmditConfig, img_tokens: int, txt_tokens: int, batch: int = 1,
-                     grad_checkpointing: bool = True) -> Dict[str, float]:
+                     grad_checkpointing: bool = True, mod_at_stream: bool = False) -> Dict[str, float]:
     """The step work model of ``bench.rs:274-311`` for the double-stream
     trunk: dense block projections at 2 d_in d_out per token (the
     modulation linears at one row per batch element), the two attention
@@ -346,13 +346,15 @@ def mmdit_step_flops(cfg: MmditConfig, img_tokens: int, txt_tokens: int, batch: 
     base's backward costs one forward and attention's two, and block
     checkpointing replays one more forward (x3 projections, x4 attention).
     The LoRA terms are reported apart (``lora``), as the reference excludes
-    them."""
+    them. ``mod_at_stream`` counts the modulation linears at the stream's
+    token count instead (a work model that treats them like the other
+    projections; this model does not run them that way)."""
     shapes = cfg.site_shapes()
     proj = 0.0
     lora = 0.0
     for s, M in (("img", img_tokens * batch), ("txt", txt_tokens * batch)):
         for n, (k, nn) in shapes.items():
-            rows = batch if n == "mod" else M
+            rows = batch if (n == "mod" and not mod_at_stream) else M
             proj += 2.0 * rows * k * nn
             lora += 2.0 * rows * cfg.rank * (k + nn)
     proj *= cfg.layers
