@@ -206,7 +206,7 @@ def main():
         print(json.dumps(few_token_fit(dev)), flush=True)
         return None
     out, ceilings_for = site_measure(args, dev, args.workload, with_cpu=not args.no_cpu_baseline,
-                                     ceilings=args.workload == "ns")
+                                     ceilings=args.workload in ("ns", "c1"))
     if args.workload == "ns" and not args.no_skinny:
         # the north star's second bar, the few-token forward of the same layer
         out["skinny"] = skinny_measure(args, dev, with_cpu=not args.no_cpu_baseline)
@@ -219,7 +219,7 @@ def main():
         # the mid-size configurations, timed by the driver too: C1, and C5
         # at the few-token and mid token counts
         torch.cuda.empty_cache()
-        out["c1"] = site_measure(args, dev, "c1", with_cpu=False)[0]
+        out["c1"] = site_measure(args, dev, "c1", with_cpu=False, ceilings=True)[0]
         torch.cuda.empty_cache()
         out["c5"] = c5_measure(args, dev, (16, 256), with_cpu=False)
         torch.cuda.empty_cache()
@@ -498,6 +498,21 @@ def in_step_kernel_us(fwd, bwd, kernels, reserve, n_steps=10, rounds=10):
     return {k: per[k] - per[None] for k in kernels}, per[None]
 
 
+GEMM_CEILING_HOW = ("50 calls per HIP graph, replayed (best of three); the faster of W^T as a transposed view and "
+                    "as a contiguous copy for the forward, of W and of a transposed view of the copy for dx")
+
+
+def gemm_pair_us(x, w, wt, dy):
+    """The vendor library's bf16 GEMM time for x . W^T and dy . W (w [N, K],
+    wt its contiguous transpose), graph-replayed, the faster operand layout
+    of each."""
+    import torch
+
+    fwd = min(graph_us(lambda: torch.matmul(x, w.t())), graph_us(lambda: torch.matmul(x, wt)))
+    dx = min(graph_us(lambda: torch.matmul(dy, w)), graph_us(lambda: torch.matmul(dy, wt.t())))
+    return fwd, dx
+
+
 def measure_ceilings(M, K, N, weights, row_bytes):
     """What the part delivers on this box, for the fractions of the bench
     line: the bf16 GEMM of the vendor library (torch.matmul, hipBLASLt) at
@@ -529,8 +544,7 @@ def measure_ceilings(M, K, N, weights, row_bytes):
             best = min(best, e0.elapsed_time(e1) * 1e3 / n)
         return best
 
-    fwd_us = timed(lambda: torch.matmul(x, wt))
-    dx_us = timed(lambda: torch.matmul(dy, w))
+    fwd_us, dx_us = gemm_pair_us(x, w, wt, dy)
     del w, wt, x, dy
     from loractl_amd import device as D
 
@@ -552,7 +566,8 @@ def measure_ceilings(M, K, N, weights, row_bytes):
     return {
         "gemm_bf16_hipblaslt": {"fwd_us": round(fwd_us, 2), "fwd_tflops": round(fl / (fwd_us * 1e-6) / 1e12, 1),
                                 "dx_us": round(dx_us, 2), "dx_tflops": round(fl / (dx_us * 1e-6) / 1e12, 1),
-                                "shape": f"x[{M},{K}] . W^T[{K},{N}] and dy[{M},{N}] . W[{N},{K}], bf16, torch.matmul"},
+                                "shape": f"x[{M},{K}] . W^T[{K},{N}] and dy[{M},{N}] . W[{N},{K}], bf16, torch.matmul",
+                                "how": GEMM_CEILING_HOW},
         "stream_read_packed_weight": {"us": round(read_us, 3), "bytes": row_bytes,
                                       "gbs": round(row_bytes / (read_us * 1e-6) / 1e9, 1),
                                       "how": f"lrq_probe_stream_read over the blocked weight's row section, "
@@ -1128,6 +1143,55 @@ def bench_c3(args, dev):
     }), flush=True)
 
 
+def graph_us(fn, reps=50):
+    """Microseconds per call of `fn` (GPU work only): `reps` calls captured
+    in a HIP graph on a side stream, replayed; the best of three replays."""
+    import torch
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        fn()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            for _ in range(reps):
+                fn()
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(3):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        best = min(best, e0.elapsed_time(e1) * 1e3 / reps)
+    return best
+
+
+def c5_gemm_ceiling(M):
+    """The vendor library's bf16 GEMMs (torch.matmul, hipBLASLt) at every C5
+    site's forward and input-gradient shapes for M tokens, no dequantization
+    and no LoRA: their sum over one step (28 layers), the time a step of the
+    plain products would take."""
+    import torch
+
+    g = torch.Generator(device="cuda").manual_seed(11)
+    per, total = {}, 0.0
+    for (K, N) in dict.fromkeys(C5_LAYER):
+        w = (torch.randn(N, K, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+        wt = w.t().contiguous()
+        x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+        dy = torch.randn(M, N, device="cuda", generator=g).to(torch.bfloat16)
+        f, b = gemm_pair_us(x, w, wt, dy)
+        per[f"{K}->{N}"] = {"fwd_us": round(f, 2), "dx_us": round(b, 2)}
+        total += (f + b) * C5_LAYER.count((K, N)) * C5_LAYERS
+        del w, wt, x, dy
+    return total / 1e3, per
+
+
 def c5_measure(args, dev, Ms, with_cpu=True):
     """C5 at each token count of ``Ms``: the linears of a Qwen3-style 28-layer
     decoder (q/k/v/o/gate/up/down, int4 g64, LoRA r=16), forward + backward
@@ -1166,6 +1230,16 @@ def c5_measure(args, dev, Ms, with_cpu=True):
                                  "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                                  "traffic": load_traffic(f"step_M{M}", "c5"),
                                  "flops_per_step": F, "time_from": "graph replay of the whole step"}
+            # the measured ceiling: the same step's plain bf16 GEMMs in the
+            # vendor library (the rate at which this step's work would run
+            # at their speed, and this step's time as a fraction of theirs)
+            ceil_ms, per = c5_gemm_ceiling(M)
+            entry["ceiling"] = {"gemm_bf16_hipblaslt": {
+                "step_ms": round(ceil_ms, 4), "per_site_us": per,
+                "how": "torch.matmul of x[M,K] . W^T and dy[M,N] . W in bf16 at every site's shape, no "
+                       "dequantization and no LoRA, summed over the step's 196 sites; " + GEMM_CEILING_HOW}}
+            entry["roofline"]["measured_ceiling"] = round(F / (ceil_ms * 1e-3) / 1e12, 2)
+            entry["roofline"]["frac_of_measured"] = round(ceil_ms / ms_step, 4)
         else:
             achieved = B / (ms_step * 1e-3) / 1e9
             entry["roofline"] = {"kernel": "whole step (196 weights streamed by both passes)", "bound": "hbm",
