@@ -240,7 +240,7 @@ int lrq_profile_read(lrq_ctx* ctx, int kid, double* total_ms, int64_t* launches)
  * forgets the kept launches, and each forward (backward) call forgets those
  * of the kernels its pass may launch, so only the pass's latest call's
  * launches repeat (a kernel that call did not launch is refused with
- * LRQ_EINVAL: at ranks 8 and 16 on the mid-size tiles, one bwd_dx launch
+ * LRQ_EINVAL: at ranks 8 to 32 (multiples of 8) on the mid-size tiles, one bwd_dx launch
  * also forms u, dA and dB). A repeat writes the same outputs again while
  * the buffers it reads hold what they held at the launch: the workspace is
  * shared by the passes (the backward reuses the forward's slot of the B^T

@@ -449,18 +449,19 @@ int lrq_debug_force_wait_timeout(int on) {
 
 const char* lrq_last_error(const lrq_ctx* c) { return c ? c->err : "null context"; }
 
-// Workspace floats of the mid-size passes at ranks 8 and 16 that form the
+// Workspace floats of the mid-size passes at ranks 8 to 32 (multiples of 8)
+// that form the
 // LoRA factors in their own launch: the factor's slice partials, then the
 // tiles' depth-range partials, then (backward) dB's and dA's token-slice
 // partials (both jobs counted).
-static int64_t fold_fwd_floats(int64_t m, int64_t n, int64_t k) {
+static int64_t fold_fwd_floats(int64_t m, int64_t n, int64_t k, int rp) {
   const int64_t G = (m + 63) / 64, fs = (k + MID_FOLD_KT - 1) / MID_FOLD_KT;
-  return round_up(fs * G * 64 * 16, 64) + mid_split_plan(m, n, k).floats;
+  return round_up(fs * G * 64 * rp, 64) + mid_split_plan(m, n, k).floats;
 }
 static int64_t fold_bwd_floats(int64_t m, int64_t n, int64_t k, int rp) {
   const int64_t G = (m + 63) / 64, fs = (n + MID_FOLD_KT - 1) / MID_FOLD_KT;
   const LoraPlan tpb = mid_tn_plan(m, n, rp), tpa = mid_tn_plan(m, k, rp);
-  return round_up(fs * G * 64 * 16, 64) + round_up(mid_split_plan(m, k, n).floats, 64) +
+  return round_up(fs * G * 64 * rp, 64) + round_up(mid_split_plan(m, k, n).floats, 64) +
          (tpb.splits > 1 ? (int64_t)tpb.splits * n * rp : 0) + (tpa.splits > 1 ? (int64_t)tpa.splits * k * rp : 0);
 }
 
@@ -485,12 +486,12 @@ int lrq_reserve(lrq_ctx* c, int64_t m, int64_t n, int64_t k, int64_t r) {
                        skinny_ws_bytes(skinny_plan(k, n, rp, get_num_cus()), mm, k, rp);
     if (skd > need) need = skd;
   }
-  if ((r == 8 || r == 16) && m > 16) {
+  if (r % 8 == 0 && r > 0 && r <= 32 && m > 16) {
     // the one-launch mid-size passes, at every token count up to m
     const size_t lb = lora_layout(nullptr, m, n, k, rp).bytes;
     for (int64_t mm = 64;; mm += 64) {
       const int64_t mt = mm < m ? mm : m;
-      need = std::max(need, (size_t)fold_fwd_floats(mt, n, k) * 4);
+      need = std::max(need, (size_t)fold_fwd_floats(mt, n, k, rp) * 4);
       need = std::max(need, lb + (size_t)fold_bwd_floats(mt, n, k, rp) * 4);
       if (mt == m) break;
     }
@@ -702,15 +703,15 @@ static int fwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, int64_t 
   if (lora) {
     const int rp = (int)round_up(r, 16);
     LRQ_TRY(check_lora_shapes(c, m, w->n, w->k, rp));
-    // mid-size tiles at rank 8 or 16: t is formed in the same launch by
+    // mid-size tiles at ranks 8 to 32 (multiples of 8): t is formed in the same launch by
     // workgroups ahead of the tiles (no side launch)
     const int64_t G = (m + 63) / 64, fs = (w->k + MID_FOLD_KT - 1) / MID_FOLD_KT;
     // (and the tiles' depth ranges, if any: partials after t's, counters
     // after the fold's)
     const MidSplit ms = mid_split_plan(m, w->n, w->k);
-    if ((r == 8 || r == 16) && gemm_mid_tokens(m, w->n, w->k) > 0 && aligned16(a) && t_out && aligned16(t_out) &&
+    if (r % 8 == 0 && r <= 32 && gemm_mid_tokens(m, w->n, w->k) > 0 && aligned16(a) && t_out && aligned16(t_out) &&
         2 * G + ms.tiles <= SK_MAX_NB) {
-      const int64_t fp = round_up(fs * G * 64 * 16, 64);
+      const int64_t fp = round_up(fs * G * 64 * rp, 64);
       LRQ_TRY(acquire_ws(c, src, (size_t)(fp + ms.floats) * 4, &ws, &cnt));
       ga.fold = force_wait_timeout() ? -1 : 1;
       ga.fold_slices = (int)fs;
@@ -833,11 +834,11 @@ static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const ui
     const bool few = dx && m >= 1 && m <= 16;
     const SkinnyPlan sp = skinny_plan(w->k, w->n, rp, get_num_cus());
     const size_t lbytes = lora_layout(nullptr, m, w->n, w->k, rp).bytes;
-    // mid-size tiles at rank 8 or 16: u is formed in the input gradient's
+    // mid-size tiles at ranks 8 to 32 (multiples of 8): u is formed in the input gradient's
     // launch by workgroups ahead of the tiles (partials after the LoRA
     // workspace)
     const int64_t G = (m + 63) / 64, fs = (w->n + MID_FOLD_KT - 1) / MID_FOLD_KT;
-    const bool fold = !few && dx && (r == 8 || r == 16) && gemm_mid_tokens(m, w->k, w->n) > 0 && aligned16(a) &&
+    const bool fold = !few && dx && r % 8 == 0 && r <= 32 && gemm_mid_tokens(m, w->k, w->n) > 0 && aligned16(a) &&
                       2 * G + mid_split_plan(m, w->k, w->n).tiles <= SK_MAX_NB;
     // and the weight gradients by workgroups after its tiles, in token
     // slices that fit its LDS (their counters after the fold's, partials
@@ -849,7 +850,7 @@ static int bwd_impl(lrq_ctx* c, const lrq_weight* w, const uint16_t* x, const ui
     const MidSplit ms = fold ? mid_split_plan(m, w->k, w->n) : MidSplit{1, 0, 0, 0};
     const bool fold_tn = fold && (da || db) && tpb.splits > 0 && tpa.splits > 0 &&
                          2 * G + ms.tiles + TN_WAVES * ((db ? tpb.tiles : 0) + (da ? tpa.tiles : 0)) <= SK_MAX_NB;
-    const int64_t fp_floats = round_up(fs * G * 64 * 16, 64);
+    const int64_t fp_floats = round_up(fs * G * 64 * rp, 64);
     const int64_t ms_floats = round_up(ms.floats, 64);
     const size_t fbytes = fold ? (size_t)(fp_floats + ms_floats + (fold_tn ? tb_floats + ta_floats : 0)) * 4 : 0;
     LRQ_TRY(ensure_ws(c, lbytes + (few ? skinny_ws_bytes(sp, m, w->k, rp) : fbytes)));

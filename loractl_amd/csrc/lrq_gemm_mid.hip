@@ -36,7 +36,7 @@
 //   - epilogue: the LoRA term as rank-wide matrix-core steps (the tile's
 //     token-side rows t or u and weight-side rows B^T or A from the
 //     workspace), the forward fp8 channel scales and the bias, bf16 stores;
-//   - FOLD (rank 8 or 16): the token-side rows are formed in the same
+//   - FOLD (ranks 8 to 32, multiples of 8): the token-side rows are formed in the same
 //     launch, so no side launch precedes it. The first workgroups of the
 //     grid (dispatched first, on the CU slots the tiles leave free) each
 //     take 64 tokens and a depth slice of 384: t = x . A (or u = dy . B^T)
@@ -86,16 +86,16 @@ constexpr int MST = MID_MST;  // pipeline stages
 LRQ_DEV int mswz(int r) { return (r >> 1) & 7; }
 
 // FOLD: workgroup fw of the factor workgroups: 64-token group fw / fold_slices,
-// depth slice fw % fold_slices. Wavefront w takes tokens 16 w .. + 16 of the
-// group; each of its lanes loads the group's token row 16 w + (l & 15) at
-// depths 32 ss + 8 (l >> 4) .. + 8 of the slice (every load of the slice at
-// once) and the factor fragment of the same depths for rank l & 15:
-// forward A's rows staged transposed in LDS (aT [16][FKT + 8]), backward B's
-// rows read directly. `lds` holds 16 (FKT + 8) bf16. `want` is the
-// launch's stamp.
-template <bool BWD>
-LRQ_DEV void mid_fold_slice(const GemmArgs& a, int fw, uint16_t* lds, uint32_t want) {
-  constexpr int FKT = MID_FOLD_KT, NSS = FKT / 32, AST = FKT + 8;
+// depth slice fw % fold_slices, RT rank tiles of 16 (rp = 16 RT). Wavefront
+// w takes tokens 16 w .. + 16 of the group; each of its lanes loads the
+// group's token row 16 w + (l & 15) at depths 32 ss + 8 (l >> 4) .. + 8 of
+// the slice (every load of the slice at once) and the factor fragments of
+// the same depths for ranks 16 rt + (l & 15): forward A's rows staged
+// transposed in LDS (rank tile rt's aT [16][FKT + 8] in lds[rt]), backward
+// B's rows read directly. `want` is the launch's stamp.
+template <bool BWD, int RT>
+LRQ_DEV void mid_fold_slice(const GemmArgs& a, int fw, uint16_t* lds0, uint16_t* lds1, uint32_t want) {
+  constexpr int FKT = MID_FOLD_KT, NSS = FKT / 32, AST = FKT + 8, RP = 16 * RT;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c16 = lane & 15, kq = lane >> 4;
@@ -106,39 +106,58 @@ LRQ_DEV void mid_fold_slice(const GemmArgs& a, int fw, uint16_t* lds, uint32_t w
   const int64_t tok = (int64_t)g * 64 + 16 * w + c16;
   const rsrc_t rx = make_rsrc(a.act, clamp_bytes(M * D * 2));
   const rsrc_t rf = make_rsrc(a.lact, clamp_bytes(D * r * 2));
-  u32x4 xf[NSS], bf[NSS];
+  uint16_t* const lds[2] = {lds0, lds1};
+  u32x4 xf[NSS], bf[RT][NSS];
 #pragma unroll
   for (int ss = 0; ss < NSS; ++ss) {
     const int64_t k = k0 + 32 * ss + 8 * kq;
     xf[ss] = bload16(rx, opaque_u32(tok < M && k < k1 ? (uint32_t)((tok * D + k) * 2) : LRQ_OOB));
-    if (BWD) bf[ss] = bload16(rf, opaque_u32(c16 < r && k < k1 ? (uint32_t)(((int64_t)c16 * D + k) * 2) : LRQ_OOB));
+    if (BWD) {
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        const int j = 16 * rt + c16;
+        bf[rt][ss] = bload16(rf, opaque_u32(j < r && k < k1 ? (uint32_t)(((int64_t)j * D + k) * 2) : LRQ_OOB));
+      }
+    }
   }
   if (!BWD) {
     // A [D][r] rows of the slice, 8 ranks per 16-byte run: pair i = tid +
-    // 256 q is depth i / 2, ranks 8 (i % 2) ..; zeros past the rank or depth
-    constexpr int AQ = 2 * FKT / 256;
+    // 256 q is depth i / JB, ranks 8 (i % JB) ..; zeros past the rank or depth
+    constexpr int JB = RP / 8, AQ = JB * FKT / 256;
     u32x4 av[AQ];
 #pragma unroll
     for (int qq = 0; qq < AQ; ++qq) {
-      const int i = tid + 256 * qq, dd = i >> 1, j0 = 8 * (i & 1);
+      const int i = tid + 256 * qq, dd = i / JB, j0 = 8 * (i % JB);
       av[qq] = bload16(rf, opaque_u32(k0 + dd < k1 && j0 < r ? (uint32_t)(((k0 + dd) * r + j0) * 2) : LRQ_OOB));
     }
 #pragma unroll
     for (int qq = 0; qq < AQ; ++qq) {
-      const int i = tid + 256 * qq, dd = i >> 1, j0 = 8 * (i & 1);
+      const int i = tid + 256 * qq, dd = i / JB, j0 = 8 * (i % JB);
+      uint16_t* t = lds[j0 >> 4];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) lds[(j0 + e) * AST + dd] = (uint16_t)(av[qq][e >> 1] >> (16 * (e & 1)));
+      for (int e = 0; e < 8; ++e) t[((j0 & 15) + e) * AST + dd] = (uint16_t)(av[qq][e >> 1] >> (16 * (e & 1)));
     }
     __syncthreads();
 #pragma unroll
-    for (int ss = 0; ss < NSS; ++ss) bf[ss] = *reinterpret_cast<const u32x4*>(lds + c16 * AST + 32 * ss + 8 * kq);
-  }
-  // C element v of lane (c16, kq): rank 4 kq + v, token 16 w + c16
-  f32x4 acc = acc_zero4();
+    for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-  for (int ss = 0; ss < NSS; ++ss) acc = mfma16(as_bf16x8(bf[ss]), as_bf16x8(xf[ss]), acc);
-  const rsrc_t rp = make_rsrc(a.fpart, clamp_bytes((int64_t)fs * Mp * 16 * 4));
-  mstore16_dev(rp, opaque_u32((uint32_t)((((int64_t)sl * Mp + tok) * 16 + 4 * kq) * 4)), __builtin_bit_cast(u32x4, acc));
+      for (int ss = 0; ss < NSS; ++ss)
+        bf[rt][ss] = *reinterpret_cast<const u32x4*>(lds[rt] + c16 * AST + 32 * ss + 8 * kq);
+  }
+  // C element v of lane (c16, kq) in rank tile rt: rank 16 rt + 4 kq + v,
+  // token 16 w + c16
+  f32x4 acc[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    acc[rt] = acc_zero4();
+#pragma unroll
+    for (int ss = 0; ss < NSS; ++ss) acc[rt] = mfma16(as_bf16x8(bf[rt][ss]), as_bf16x8(xf[ss]), acc[rt]);
+  }
+  const rsrc_t rp = make_rsrc(a.fpart, clamp_bytes((int64_t)fs * Mp * RP * 4));
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+    mstore16_dev(rp, opaque_u32((uint32_t)((((int64_t)sl * Mp + tok) * RP + 16 * rt + 4 * kq) * 4)),
+                 __builtin_bit_cast(u32x4, acc[rt]));
   // counted once the partial is acknowledged; the last slice of the group
   // sums the slices in order, stores the factor and publishes the flag
   __builtin_amdgcn_s_waitcnt(0);
@@ -151,22 +170,25 @@ LRQ_DEV void mid_fold_slice(const GemmArgs& a, int fw, uint16_t* lds, uint32_t w
   }
   __syncthreads();
   if (!last) return;
-  // thread: token g 64 + tid / 4, ranks 4 (tid % 4) ..
+  // thread: token g 64 + tid / 4, ranks 16 rt + 4 (tid % 4) ..
   const int64_t tk = (int64_t)g * 64 + (tid >> 2);
-  const int rq = 4 * (tid & 3);
-  f32x4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int s0 = 0; s0 < fs; s0 += 8) {
-    u32x4 pv[8];
+  const rsrc_t ro = make_rsrc(a.fout, clamp_bytes(M * a.fout_ld * 2));
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
-      pv[u] = mbload16_dev(rp, opaque_u32(s0 + u < fs ? (uint32_t)((((int64_t)(s0 + u) * Mp + tk) * 16 + rq) * 4) : LRQ_OOB));
+  for (int rt = 0; rt < RT; ++rt) {
+    const int rq = 16 * rt + 4 * (tid & 3);
+    f32x4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s0 = 0; s0 < fs; s0 += 8) {
+      u32x4 pv[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) sum += __builtin_bit_cast(f32x4, pv[u]);
-  }
-  if (a.fout && tk < M && rq < a.fout_ld) {
-    const rsrc_t ro = make_rsrc(a.fout, clamp_bytes(M * a.fout_ld * 2));
-    const u32x2 o = {pack_bf16x2(a.fscale * sum[0], a.fscale * sum[1]), pack_bf16x2(a.fscale * sum[2], a.fscale * sum[3])};
-    mstore8_dev(ro, opaque_u32((uint32_t)((tk * a.fout_ld + rq) * 2)), o);
+      for (int u = 0; u < 8; ++u)
+        pv[u] = mbload16_dev(rp, opaque_u32(s0 + u < fs ? (uint32_t)((((int64_t)(s0 + u) * Mp + tk) * RP + rq) * 4) : LRQ_OOB));
+#pragma unroll
+      for (int u = 0; u < 8; ++u) sum += __builtin_bit_cast(f32x4, pv[u]);
+    }
+    if (a.fout && tk < M && rq < a.fout_ld) {
+      const u32x2 o = {pack_bf16x2(a.fscale * sum[0], a.fscale * sum[1]), pack_bf16x2(a.fscale * sum[2], a.fscale * sum[3])};
+      mstore8_dev(ro, opaque_u32((uint32_t)((tk * a.fout_ld + rq) * 2)), o);
+    }
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -202,8 +224,12 @@ LRQ_DEV void mid_tn(const GemmArgs& a, int tb, uint32_t want, int readers, uint1
   const int ji = second ? 1 : 0;
   const TnArgs& j = a.tj[ji];
   const int bid = tb - (second ? a.tj[0].blocks : 0);
+  float* const red = reinterpret_cast<float*>(sr);
   if (ji != a.tn_da) {
-    tn_block<1, MID_TN_LDS, MID_TN_LDS, false>(j, bid, sq, reinterpret_cast<float*>(sr), false);
+    if (a.rp == 32)
+      tn_block<2, MID_TN_LDS, MID_TN_LDS, false>(j, bid, sq, red, false);
+    else
+      tn_block<1, MID_TN_LDS, MID_TN_LDS, false>(j, bid, sq, red, false);
     return;
   }
   __shared__ int bad;
@@ -230,7 +256,10 @@ LRQ_DEV void mid_tn(const GemmArgs& a, int tb, uint32_t want, int readers, uint1
   __syncthreads();
   const bool poison = bad != 0;
   mid_flags_done(a, readers);
-  tn_block<1, MID_TN_LDS, MID_TN_LDS, true>(j, bid, sq, reinterpret_cast<float*>(sr), poison);
+  if (a.rp == 32)
+    tn_block<2, MID_TN_LDS, MID_TN_LDS, true>(j, bid, sq, red, poison);
+  else
+    tn_block<1, MID_TN_LDS, MID_TN_LDS, true>(j, bid, sq, red, poison);
 }
 
 template <bool BWD, int FMT, int TT, int SD, bool FOLD>
@@ -260,7 +289,12 @@ __global__ void __launch_bounds__(256, 2) k_mid(GemmArgs a, int tiles_m, int til
   if (FOLD) {
     const uint32_t stamp = mstamp(mload_dev(a.fcnt + SK_EPOCH));
     if ((int)blockIdx.x < a.fold_wgs) {
-      if ((int)blockIdx.x < a.fold_slices * (int)((a.m + 63) / 64)) mid_fold_slice<BWD>(a, (int)blockIdx.x, sx0, stamp);
+      if ((int)blockIdx.x < a.fold_slices * (int)((a.m + 63) / 64)) {
+        if (a.rp == 32)
+          mid_fold_slice<BWD, 2>(a, (int)blockIdx.x, sx0, sx1, stamp);
+        else
+          mid_fold_slice<BWD, 1>(a, (int)blockIdx.x, sx0, sx1, stamp);
+      }
       return;
     }
     want = stamp + (a.fold < 0 ? 0x40000000u : 0u);
@@ -459,7 +493,7 @@ __global__ void __launch_bounds__(256, 2) k_mid(GemmArgs a, int tiles_m, int til
   };
 
   // FOLD: the weight-side factor rows of the LoRA step, fetched first (row
-  // e0 + 16w + l16; ranks 8q .. + 8, q < 2): forward B [r][E] across its
+  // e0 + 16w + l16; ranks 8q .. + 8, up to the rank): forward B [r][E] across its
   // rows, backward A [E][r] as stored
   const int64_t frow = e0 + 16 * w + l16;
   u32x4 fla = zero4();
@@ -470,14 +504,14 @@ __global__ void __launch_bounds__(256, 2) k_mid(GemmArgs a, int tiles_m, int til
 #pragma unroll
       for (int e = 0; e < 8; e += 2) {
         const int j = 8 * q + e;
-        const uint32_t lo = bload2(rb, opaque_u32(q < 2 && j < fr_r && frow < E ? (uint32_t)((j * E + frow) * 2) : LRQ_OOB));
+        const uint32_t lo = bload2(rb, opaque_u32(j < fr_r && frow < E ? (uint32_t)((j * E + frow) * 2) : LRQ_OOB));
         const uint32_t hi =
-            bload2(rb, opaque_u32(q < 2 && j + 1 < fr_r && frow < E ? (uint32_t)(((j + 1) * E + frow) * 2) : LRQ_OOB));
+            bload2(rb, opaque_u32(j + 1 < fr_r && frow < E ? (uint32_t)(((j + 1) * E + frow) * 2) : LRQ_OOB));
         fla[e >> 1] = lo | (hi << 16);
       }
     } else {
       const rsrc_t ra = make_rsrc(a.lw, clamp_bytes(E * fr_r * 2));
-      fla = bload16(ra, opaque_u32(q < 2 && 8 * q < fr_r && frow < E ? (uint32_t)((frow * fr_r + 8 * q) * 2) : LRQ_OOB));
+      fla = bload16(ra, opaque_u32(8 * q < fr_r && frow < E ? (uint32_t)((frow * fr_r + 8 * q) * 2) : LRQ_OOB));
     }
   }
   // prologue: stage 0's weights, then stages 0 .. MST-2 of activations
@@ -575,7 +609,7 @@ __global__ void __launch_bounds__(256, 2) k_mid(GemmArgs a, int tiles_m, int til
     const bool bad = fold_bad != 0;
 #pragma unroll
     for (int j = 0; j < TT; ++j) {
-      u32x4 lb = mbload16_dev(rfo, opaque_u32(q < 2 && 8 * q < a.fout_ld ? (uint32_t)(((16 * j + l16) * a.fout_ld + 8 * q) * 2) : LRQ_OOB));
+      u32x4 lb = mbload16_dev(rfo, opaque_u32(8 * q < a.fout_ld ? (uint32_t)(((16 * j + l16) * a.fout_ld + 8 * q) * 2) : LRQ_OOB));
       if (bad) lb = (u32x4){0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u};
       acc[j] = mfma16(as_bf16x8(la), as_bf16x8(lb), acc[j]);
     }
@@ -678,16 +712,17 @@ hipError_t launch_mid(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, int 
         (int64_t)S * ntiles * T * 64 * 4 >= ((int64_t)1 << 32))
       return hipErrorInvalidValue;
   }
-  // the fold: rank 8 or 16, both raw factors, its output, partials and
+  // the fold: ranks 8 to 32 (multiples of 8, padded to 16 or 32), both raw factors, its output, partials and
   // counters (groups' arrivals and flags within the counter area), and
   // enough factor workgroups, whole groups of eight
   if (a.fold) {
     const int64_t G = (a.m + 63) / 64;
-    if (a.rp != 16 || (a.r != 8 && a.r != 16) || !a.lact || !a.lw || !a.fout || a.fout_ld % 8 != 0 ||
-        a.fout_ld < a.r || !a.fpart || !a.fcnt || 2 * G > SK_MAX_NB || a.fold_wgs % 8 != 0 ||
+    if ((a.rp != 16 && a.rp != 32) || a.r % 8 != 0 || a.r > a.rp || a.r <= a.rp - 16 || !a.lact || !a.lw ||
+        !a.fout || a.fout_ld % 8 != 0 || a.fout_ld < a.r || a.fout_ld > a.rp || !a.fpart || !a.fcnt ||
+        2 * G > SK_MAX_NB || a.fold_wgs % 8 != 0 ||
         a.fold_slices != (int)((a.l + MID_FOLD_KT - 1) / MID_FOLD_KT) || a.fold_wgs < a.fold_slices * G ||
         a.m * a.l * 2 >= ((int64_t)1 << 32) || a.m * a.fout_ld * 2 >= ((int64_t)1 << 32) ||
-        (int64_t)a.fold_slices * G * 64 * 16 * 4 >= ((int64_t)1 << 32))
+        (int64_t)a.fold_slices * G * 64 * a.rp * 4 >= ((int64_t)1 << 32))
       return hipErrorInvalidValue;
     // the weight gradients' jobs after the tiles (backward): each a whole
     // plan of token slices that fit MID_TN_LDS, over all the launch's
@@ -702,11 +737,11 @@ hipError_t launch_mid(hipStream_t st, int fmt, bool bwd, const GemmArgs& a, int 
         const TnArgs& j = a.tj[i];
         if (j.blocks == 0) continue;
         if (j.C <= 0 || j.tiles != (j.C + 127) / 128 || j.splits < 1 || j.blocks != j.tiles * j.splits ||
-            j.m_per <= 0 || j.m_per % 128 != 0 || 16 * (j.m_per + 8) * 2 > MID_TN_LDS || j.M != a.m ||
+            j.m_per <= 0 || j.m_per % 128 != 0 || a.rp * (j.m_per + 8) * 2 > MID_TN_LDS || j.M != a.m ||
             (int64_t)j.splits * j.m_per < j.M || (int64_t)(j.splits - 1) * j.m_per >= j.M || !j.p || !j.q ||
-            !j.out || j.R < 1 || j.R > 16 || j.ldq < j.R || (j.splits > 1 && !j.partial) || !j.cnt ||
+            !j.out || j.R < 1 || j.R > a.rp || j.ldq < j.R || (j.splits > 1 && !j.partial) || !j.cnt ||
             j.cnt < lo || j.cnt + TN_WAVES * j.tiles > a.fcnt + SK_MAX_NB ||
-            j.m_per * j.C * 2 >= ((int64_t)1 << 31) || (int64_t)j.splits * j.C * 16 * 4 >= ((int64_t)1 << 32))
+            j.m_per * j.C * 2 >= ((int64_t)1 << 31) || (int64_t)j.splits * j.C * a.rp * 4 >= ((int64_t)1 << 32))
           return hipErrorInvalidValue;
         if (i == a.tn_da && (j.ldq % 8 != 0 || (reinterpret_cast<uintptr_t>(j.q) & 15) != 0))
           return hipErrorInvalidValue;

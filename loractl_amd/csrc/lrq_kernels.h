@@ -65,14 +65,14 @@ struct GemmArgs {
   float* part;           // lrq_gemm.hip split-depth partials [S][m][e] (gemm_split_floats), or null
   int splits, spl;       // set by lrq_gemm.hip: depth ranges and steps per range
   // lrq_gemm_mid.hip with the token-side LoRA factor formed in the same
-  // launch (fold != 0, rank 8 or 16): the first fold_wgs workgroups (a
+  // launch (fold != 0, rank 8 to 32, a multiple of 8): the first fold_wgs workgroups (a
   // multiple of 8) form bf16(fscale . act . F) for 64-token groups over
   // fold_slices depth slices of MID_FOLD_KT (F = lact: forward A [l, r],
   // backward B [r, l]), sum the slices in order, store it to fout
   // [m][fout_ld] and publish a stamped ready flag per group; the tiles read
   // it after the flag. lw is then the raw weight-side factor (forward B
   // [r, e], backward A [e, r]). fpart holds the slices' f32 partials
-  // [fold_slices][round_up(m, 64)][16]; fcnt is the counter area (zero on
+  // [fold_slices][round_up(m, 64)][rp]; fcnt is the counter area (zero on
   // entry and exit; the epoch only grows).
   int fold, fold_wgs, fold_slices;
   float fscale;
@@ -130,7 +130,7 @@ int gemm_mid_tokens(int64_t m, int64_t e, int64_t depth);
 // depth per slice of the folded factor's workgroups (GemmArgs.fold)
 constexpr int MID_FOLD_KT = 384;
 // the token slices of a weight-gradient job run inside the mid-size
-// backward: the factor slice takes at most 16 KiB of LDS (rank 16)
+// backward: the factor slice takes at most 16 KiB of LDS (ranks padded to 16 or 32)
 constexpr int MID_TN_LDS = 16384;
 // tuning and test hook (lrq_debug_gemm_path): 0 planned, 1 large tiles,
 // 2 MID_64, 3 MID_128

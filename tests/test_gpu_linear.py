@@ -374,7 +374,7 @@ def test_baseline_shapes_against_torch_fp32(cuda, M, K, N, r, fmt):
 PATH_SHAPES = [(37, 96, 72, 32), (130, 192, 520, 64), (300, 320, 264, 64), (513, 512, 392, 128), (200, 1536, 1280, 64)]
 
 
-@pytest.mark.parametrize("r", [33, 16, 8])
+@pytest.mark.parametrize("r", [33, 32, 24, 16, 8])
 @pytest.mark.parametrize("path", ["large", "mid64", "mid128", "mid64s", "mid128s"])
 @pytest.mark.parametrize("fmt,per_channel", [("int4", True), ("int8", True), ("fp8", True), ("fp8", False)])
 @pytest.mark.parametrize("M,K,N,g", PATH_SHAPES)
@@ -382,8 +382,8 @@ def test_gemm_paths_against_oracle(cuda, M, K, N, g, fmt, per_channel, path, r):
     """Every kernel path of m > 16 (the 256-token tiles, split in depth where
     they are few, and the 64-row tiles of 64 or 128 tokens) on the same
     inputs: y (with bias), t, dx, dA and dB of the fused site, and the plain
-    product and its input gradient, against the f64 oracle. At ranks 8 and
-    16 the 64-row tiles form t, u, dA and dB in their own launches; "mid64s"
+    product and its input gradient, against the f64 oracle. At ranks 8, 16,
+    24 and 32 the 64-row tiles form t, u, dA and dB in their own launches; "mid64s"
     and "mid128s" split their depth into ranges where it allows."""
     w, x, a, b, dy = case_inputs(M, K, N, r, seed=7 * M + N + g)
     wq, wdq = _weight(w, fmt, g, cuda, per_channel)
