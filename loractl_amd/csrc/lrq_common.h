@@ -181,33 +181,35 @@ LRQ_DEV int xcd_remap(int bid, int nblk) {
 }
 
 // ---------------------------------------------------------------- lane broadcast
-// Lane n of each 16-lane row, broadcast to the whole row (DPP row_newbcast).
-template <int N>
-LRQ_DEV float row_bcast(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x150 + N, 0xf, 0xf,
-                                                               true));
+// f[e] *= lane 8h + e of v's 16-lane row (e = 0..7, h = 0 or 1): the
+// per-depth scales of a transposed weight fragment. Written as eight VOP2
+// multiplies that take the row broadcast as their DPP operand, because the
+// compiler fuses only some of its v_mov_b32_dpp broadcasts into the multiply
+// (it left half of them as separate moves in the backward GEMM's main loop:
+// 64 extra VALU instructions per two steps; written out, that kernel's
+// input gradient takes 2.5% less time). The compiler does not see the DPP
+// reads inside the asm: s_nop 1 supplies the 2 wait states a DPP read needs
+// after a VALU write of its source, and tests/test_isa_hazards.py checks on
+// the emitted code that no EXEC write comes within the 5 wait states a DPP
+// instruction needs after one (s_nop 4 here measured 1.5% slower). volatile
+// keeps the blocks where the source puts them (without it the compiler's
+// placement measured slower). h is a constant once the callers' loops are
+// unrolled.
+#define LRQ_MUL_BCAST(I, L) \
+  "v_mul_f32_dpp %" #I ", %8, %" #I " row_newbcast:" #L " row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+LRQ_DEV void mul_row_bcast8(float (&f)[8], float v, int h) {
+  if (h == 0)
+    asm volatile("s_nop 1\n" LRQ_MUL_BCAST(0, 0) LRQ_MUL_BCAST(1, 1) LRQ_MUL_BCAST(2, 2) LRQ_MUL_BCAST(3, 3)
+            LRQ_MUL_BCAST(4, 4) LRQ_MUL_BCAST(5, 5) LRQ_MUL_BCAST(6, 6) LRQ_MUL_BCAST(7, 7)
+        : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]), "+v"(f[6]), "+v"(f[7])
+        : "v"(v));
+  else
+    asm volatile("s_nop 1\n" LRQ_MUL_BCAST(0, 8) LRQ_MUL_BCAST(1, 9) LRQ_MUL_BCAST(2, 10) LRQ_MUL_BCAST(3, 11)
+            LRQ_MUL_BCAST(4, 12) LRQ_MUL_BCAST(5, 13) LRQ_MUL_BCAST(6, 14) LRQ_MUL_BCAST(7, 15)
+        : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]), "+v"(f[6]), "+v"(f[7])
+        : "v"(v));
 }
-// n is a constant once the callers' loops are unrolled; the switch folds away
-LRQ_DEV float row_bcast_n(float v, int n) {
-  switch (n) {
-    case 0: return row_bcast<0>(v);
-    case 1: return row_bcast<1>(v);
-    case 2: return row_bcast<2>(v);
-    case 3: return row_bcast<3>(v);
-    case 4: return row_bcast<4>(v);
-    case 5: return row_bcast<5>(v);
-    case 6: return row_bcast<6>(v);
-    case 7: return row_bcast<7>(v);
-    case 8: return row_bcast<8>(v);
-    case 9: return row_bcast<9>(v);
-    case 10: return row_bcast<10>(v);
-    case 11: return row_bcast<11>(v);
-    case 12: return row_bcast<12>(v);
-    case 13: return row_bcast<13>(v);
-    case 14: return row_bcast<14>(v);
-    default: return row_bcast<15>(v);
-  }
-}
+#undef LRQ_MUL_BCAST
 
 // ---------------------------------------------------------------- buffer loads
 // Raw buffer loads with a wave-uniform resource: an offset at or past

@@ -296,8 +296,7 @@ k_gemm(GemmArgs a, int tiles_m, int ntiles) {
       fp8x4_to_f32(v[2 * (kk & 1)], f);
       fp8x4_to_f32(v[2 * (kk & 1) + 1], f + 4);
     }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) f[e] = row_bcast_n(S, 8 * (kk & 1) + e) * f[e];
+    mul_row_bcast8(f, S, kk & 1);
     u32x4 o;
 #pragma unroll
     for (int q = 0; q < 4; ++q) o[q] = pack_bf16x2(f[2 * q], f[2 * q + 1]);

@@ -267,6 +267,9 @@ __global__ void __launch_bounds__(256, 2) k_mid(GemmArgs a, int tiles_m, int til
   constexpr bool I4 = FMT == LRQ_FMT_INT4;
   constexpr bool I8 = FMT == LRQ_FMT_INT8;
   constexpr bool GS = I4 || I8;                    // group scales (int4, int8) or channel scales (fp8)
+  // the main loop loads a scale per block unless nothing reads it (the fp8
+  // forward applies its channel scales in the epilogue)
+  constexpr bool USE_SC = BWD || GS;
   constexpr int T = 16 * TT;                       // tokens per tile
   constexpr int XB = T * MD * SD;                  // bf16 per stage: SD sub-tiles [T][64]
   constexpr int XL = T / 32;                       // activation copies per wavefront per step
@@ -402,7 +405,7 @@ __global__ void __launch_bounds__(256, 2) k_mid(GemmArgs a, int tiles_m, int til
   // register sets; loaded one stage ahead of the activations, so a step can
   // dequantize the next stage while its matrix-core steps run
   u32x4 wv[MST][SD];
-  float sv[MST][SD];
+  float sv[MST][SD] = {};
   auto load_w = [&](int set, int st) {
 #pragma unroll
     for (int d = 0; d < SD; ++d) {
@@ -413,8 +416,10 @@ __global__ void __launch_bounds__(256, 2) k_mid(GemmArgs a, int tiles_m, int til
       } else {
         wv[set][d] = bload16(rw, opaque_u32(woff + kt * blkb));
       }
-      const uint32_t so = !BWD ? ((kt * 64u) >> a.gshift) * 256u : kt * 256u;
-      sv[set][d] = bloadf(rs, opaque_u32(sbase + so));
+      if (USE_SC) {
+        const uint32_t so = !BWD ? ((kt * 64u) >> a.gshift) * 256u : kt * 256u;
+        sv[set][d] = bloadf(rs, opaque_u32(sbase + so));
+      }
     }
   };
   // A-role fragment of block d, sub-step kk from register set `set`
@@ -440,8 +445,7 @@ __global__ void __launch_bounds__(256, 2) k_mid(GemmArgs a, int tiles_m, int til
       fp8x4_to_f32(v[2 * kk + 1], f + 4);
     }
     const float S = sc + s0add;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) f[e] = row_bcast_n(S, 8 * kk + e) * f[e];
+    mul_row_bcast8(f, S, kk);
     u32x4 o;
 #pragma unroll
     for (int i = 0; i < 4; ++i) o[i] = pack_bf16x2(f[2 * i], f[2 * i + 1]);
@@ -456,8 +460,11 @@ __global__ void __launch_bounds__(256, 2) k_mid(GemmArgs a, int tiles_m, int til
   // A fragments of the current and the next stage
   bf16x8 fa[2][SD][2];
   // per-lane memory instructions of one stage: per block the activation
-  // copies, the weight bytes and the scale
-  constexpr int NST = SD * (XL + 2);
+  // copies, the weight bytes and (USE_SC) the scale. The waits below count
+  // them, so this must be exactly what a stage issues: a count one too high
+  // lets a stage's last activation copy (8 token rows) still be in flight
+  // when the fragment reads start
+  constexpr int NST = SD * (XL + 1 + (USE_SC ? 1 : 0));
   // Stage st: activations in bufs[st % MST] (issued MST - 1 stages ahead),
   // weights in register set st % MST (MST stages ahead), A fragments in
   // fa[st % 2] (dequantized during stage st - 1).

@@ -707,8 +707,7 @@ LRQ_DEV void sk_math(const GemmArgs& a, const SkRun<FMT, BWD, WB, RTN>& R, f32x4
             fp8x4_to_f32(R.w8[b][rt][jj][1], f + 4);
           }
           const float S = R.sc[b][(I4 || I8) && !MQ ? rt : 0];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) f[e] = row_bcast_n(S, 8 * jj + e) * f[e];
+          mul_row_bcast8(f, S, jj);
 #pragma unroll
           for (int q = 0; q < 4; ++q) wb[q] = pack_bf16x2(f[2 * q], f[2 * q + 1]);
         } else if constexpr (I4) {

@@ -206,6 +206,122 @@ def check_kernel(k: Kernel) -> tuple:
     return out, count
 
 
+def _successors(k: Kernel) -> list:
+    n = len(k.insns)
+    succ = []
+    for i, ins in enumerate(k.insns):
+        s = []
+        if ins.mnem == "s_branch":
+            if ins.label in k.labels:
+                s.append(k.labels[ins.label])
+        elif ins.mnem != "s_endpgm":
+            if i + 1 < n:
+                s.append(i + 1)
+            if ins.label in k.labels:
+                s.append(k.labels[ins.label])
+        succ.append(s)
+    return succ
+
+
+def _writes_exec(ins: Insn) -> bool:
+    return ("saveexec" in ins.mnem or ins.mnem.startswith("v_cmpx")
+            or (ins.mnem.startswith("s_") and bool(ins.ops) and ins.ops[0] == "exec"))
+
+
+DPP_AFTER_VALU = 2  # wait states between a VALU write of a VGPR and a DPP read of it
+DPP_AFTER_EXEC = 5  # wait states between a write of EXEC and a DPP instruction
+
+
+def check_dpp(k: Kernel) -> tuple:
+    """(violations, number of DPP instructions checked): on every path into a
+    DPP instruction (…_dpp), no VALU instruction writes its DPP source (the
+    first source operand) within DPP_AFTER_VALU wait states and nothing
+    writes EXEC within DPP_AFTER_EXEC. The compiler keeps these distances
+    for the DPP instructions it creates, but not for ones written in inline
+    asm."""
+    succ = _successors(k)
+    pred = [[] for _ in k.insns]
+    for i, s in enumerate(succ):
+        for j in s:
+            pred[j].append(i)
+    out, count = [], 0
+    for i, ins in enumerate(k.insns):
+        if not ins.mnem.endswith("_dpp"):
+            continue
+        count += 1
+        src = _regs(ins.ops[1]) if len(ins.ops) > 1 else set()
+        stack = [(p, 0) for p in pred[i]]
+        seen = {}
+        while stack:
+            j, dist = stack.pop()
+            if dist >= DPP_AFTER_EXEC or seen.get(j, DPP_AFTER_EXEC + 1) <= dist:
+                continue
+            seen[j] = dist
+            prev = k.insns[j]
+            if _writes_exec(prev):
+                out.append(Violation(k.name, i, ins.text, j, prev.text, dist, DPP_AFTER_EXEC))
+                continue
+            if (dist < DPP_AFTER_VALU and prev.mnem.startswith("v_") and not prev.mnem.startswith("v_mfma")
+                    and prev.ops and _regs(prev.ops[0]) & src):
+                out.append(Violation(k.name, i, ins.text, j, prev.text, dist, DPP_AFTER_VALU))
+                continue
+            for p in pred[j]:
+                stack.append((p, dist + prev.waits))
+    return out, count
+
+
+_VMCNT = re.compile(r"\bvmcnt\((\d+)\)")
+
+
+def _lds_copy(ins: Insn) -> bool:
+    return ins.mnem.startswith("buffer_load") and ins.text.endswith(" lds")
+
+
+def main_loop(k: Kernel):
+    """(first, last) instruction indices of the kernel's pipelined loop: of
+    the loops (a label and a later branch back to it) that copy global
+    memory into LDS (buffer_load ... lds), the one with the most MFMAs.
+    None without one."""
+    best, most = None, -1
+    for i, ins in enumerate(k.insns):
+        if ins.label is None or ins.label not in k.labels or k.labels[ins.label] > i:
+            continue
+        lo = k.labels[ins.label]
+        if not any(_lds_copy(k.insns[j]) for j in range(lo, i + 1)):
+            continue
+        n = sum(1 for j in range(lo, i + 1) if k.insns[j].mnem.startswith("v_mfma"))
+        if n > most:
+            best, most = (lo, i), n
+    return best
+
+
+def stage_waits(k: Kernel) -> list:
+    """A pipelined loop of the shape `s_waitcnt vmcnt(W); s_barrier; <this
+    step's loads>; <matrix-core work>` per step: for each s_barrier of the
+    main loop, (W of the last vmcnt wait before it, buffer loads from it to
+    the next barrier or the loop's end). W is None if no wait precedes the
+    barrier inside the loop."""
+    loop = main_loop(k)
+    if loop is None:
+        return []
+    lo, hi = loop
+    bars = [j for j in range(lo, hi + 1) if k.insns[j].mnem == "s_barrier"]
+    out = []
+    for n, j in enumerate(bars):
+        w = None
+        for p in range(j - 1, lo - 1, -1):
+            if k.insns[p].mnem == "s_barrier":
+                break
+            m = _VMCNT.search(k.insns[p].text) if k.insns[p].mnem == "s_waitcnt" else None
+            if m:
+                w = int(m.group(1))
+                break
+        end = bars[n + 1] if n + 1 < len(bars) else hi + 1
+        loads = sum(1 for q in range(j + 1, end) if k.insns[q].mnem.startswith("buffer_load"))
+        out.append((w, loads))
+    return out
+
+
 def compile_asm(src: str, include: str, out_dir: str) -> str:
     """Device assembly of one HIP source for gfx950, with the library's flags."""
     out = os.path.join(out_dir, os.path.splitext(os.path.basename(src))[0] + ".s")

@@ -224,6 +224,36 @@ def test_split_depth_bias_and_scales(cuda, fmt, per_channel, path):
     check("dx", dx, dx_ref.cpu().numpy())
 
 
+@pytest.mark.parametrize("per_channel", [True, False])
+def test_fp8_mid_forward_repeats(cuda, per_channel):
+    """The fp8 forward's mid-size tiles load no scale in their main loop (the
+    channel scales apply in the epilogue), so a stage issues one load fewer
+    per block than the other formats, and the counted waits for a stage's
+    activation copies must count exactly that. Every mid path's forward,
+    three times over, against the fp32 reference and bit-identical across
+    the repeats: a count one too high let a wavefront read 8 token rows of
+    its stage before their copy landed (16 outputs x 8 tokens wrong, in the
+    ragged last token tile, in about a third of the calls)."""
+    M, K, N, r = 200, 3072, 3072, 16
+    g = torch.Generator(device=cuda).manual_seed(11)
+    w = torch.randn(N, K, device=cuda, generator=g) * 0.02
+    wq = _quantize(w, "fp8", 64, per_channel)
+    wdq = D.dequant(wq)
+    x = torch.randn(M, K, device=cuda, generator=g).to(torch.bfloat16)
+    a = ((torch.rand(K, r, device=cuda, generator=g) * 2 - 1) / K ** 0.5).to(torch.bfloat16)
+    b = (torch.randn(r, N, device=cuda, generator=g) * 1e-2).to(torch.bfloat16)
+    xf = x.float()
+    y_ref = (xf @ wdq.t() + 0.5 * (xf @ a.float()) @ b.float()).cpu().numpy()
+    for path in ("mid64", "mid128", "mid64s", "mid128s"):
+        outs = []
+        for _ in range(3):
+            with gemm_path(path):
+                y, _t = D.lora_fwd(x, wq, a, b, 0.5)
+            check(f"y {path}", y, y_ref)
+            outs.append(y)
+        assert all(torch.equal(outs[0], o) for o in outs[1:]), path
+
+
 @pytest.mark.parametrize("M,r", [(1, 17), (3, 32), (16, 17), (16, 64)])
 @pytest.mark.parametrize("fmt,per_channel,group", [("int4", True, 32), ("int4", True, 128), ("fp8", True, 0),
                                                    ("fp8", False, 0), ("int8", True, 32), ("int8", True, 128)])
