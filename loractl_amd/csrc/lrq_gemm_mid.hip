@@ -434,9 +434,7 @@ __global__ void __launch_bounds__(256, 2) k_mid(GemmArgs a, int tiles_m, int til
     }
     float f[8];
     if (I4) {
-      const uint32_t dw = v[kk];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) f[e] = (float)((int)(dw << (28 - 4 * e)) >> 28);
+      int4x8_to_f32_div16(v[kk], f);  // q / 16, times 16 x the scale below
     } else if (I8) {
       int8x4_to_f32(v[2 * kk], f);
       int8x4_to_f32(v[2 * kk + 1], f + 4);
@@ -444,7 +442,7 @@ __global__ void __launch_bounds__(256, 2) k_mid(GemmArgs a, int tiles_m, int til
       fp8x4_to_f32(v[2 * kk], f);
       fp8x4_to_f32(v[2 * kk + 1], f + 4);
     }
-    const float S = sc + s0add;
+    const float S = I4 ? 16.0f * sc : sc + s0add;
     mul_row_bcast8(f, S, kk);
     u32x4 o;
 #pragma unroll

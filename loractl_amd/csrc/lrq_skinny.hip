@@ -696,9 +696,7 @@ LRQ_DEV void sk_math(const GemmArgs& a, const SkRun<FMT, BWD, WB, RTN>& R, f32x4
           // kd + 8 jj + e, then bf16
           float f[8];
           if (I4) {
-            const uint32_t d = w4[rt][jj];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) f[e] = (float)((int)(d << (28 - 4 * e)) >> 28);
+            int4x8_to_f32_div16(w4[rt][jj], f);  // q / 16, times 16 x the scale below
           } else if (I8) {
             int8x4_to_f32(R.w8[b][rt][jj][0], f);
             int8x4_to_f32(R.w8[b][rt][jj][1], f + 4);
@@ -706,7 +704,7 @@ LRQ_DEV void sk_math(const GemmArgs& a, const SkRun<FMT, BWD, WB, RTN>& R, f32x4
             fp8x4_to_f32(R.w8[b][rt][jj][0], f);
             fp8x4_to_f32(R.w8[b][rt][jj][1], f + 4);
           }
-          const float S = R.sc[b][(I4 || I8) && !MQ ? rt : 0];
+          const float S = (I4 ? 16.0f : 1.0f) * R.sc[b][(I4 || I8) && !MQ ? rt : 0];
           mul_row_bcast8(f, S, jj);
 #pragma unroll
           for (int q = 0; q < 4; ++q) wb[q] = pack_bf16x2(f[2 * q], f[2 * q + 1]);
