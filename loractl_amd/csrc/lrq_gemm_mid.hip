@@ -669,7 +669,7 @@ __global__ void __launch_bounds__(256, 2) k_mid(GemmArgs a, int tiles_m, int til
     o[0] = pack_bf16x2(__builtin_fmaf(c[0], sc[0], bv[0]), __builtin_fmaf(c[1], sc[1], bv[1]));
     o[1] = pack_bf16x2(__builtin_fmaf(c[2], sc[2], bv[2]), __builtin_fmaf(c[3], sc[3], bv[3]));
     const uint32_t off = nok ? (uint32_t)(((16 * j + l16) * E + n) * 2) : LRQ_OOB;
-    __builtin_amdgcn_raw_buffer_store_b64(o, ry, opaque_u32(off), 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b64(o, ry, opaque_u32(off), 0, 2);  // non-temporal, as the large tiles' output
   }
   if (FOLD) mid_flags_done(a, ntiles + ((BWD && a.tn_da >= 0) ? a.tj[a.tn_da].blocks : 0));
 }
