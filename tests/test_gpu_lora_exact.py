@@ -37,6 +37,7 @@ PATHS = [
     ("split-depth r192", 256, 3072, 3072, "large"),
     ("tiled r192 fwd / split bwd", 4096, 256, 3072, "large"),
     ("tiled r256", 4096, 4096, 4096, "large"),
+    ("tiled, ragged tokens", 1100, 1024, 2048, "large"),
     ("mid 64-token tiles", 300, 3072, 3064, "mid64"),
     ("mid 128-token tiles", 300, 1088, 1032, "mid128"),
     ("mid 64-token tiles, depth ranges", 200, 3072, 2560, "mid64s"),
