@@ -90,3 +90,45 @@ def test_random_shape_forward_backward(cuda, M, K, N, r, fmt, grp):
     for name, rv in ref.items():
         check(name, got[name], rv.cpu().numpy())
     assert torch.equal(dx, dx2) and torch.equal(da, da2) and torch.equal(db, db2), "repeated backward differs"
+
+
+@pytest.mark.parametrize("M,K,N,r,fmt,grp", CASES[::2], ids=[f"m{c[0]}-k{c[1]}-n{c[2]}-r{c[3]}-{c[4]}" +
+                                                             (f"-g{c[5]}" if c[5] else "") for c in CASES[::2]])
+def test_random_shape_base_bias_and_noalloc(cuda, M, K, N, r, fmt, grp):
+    """Every other shape of the sweep without LoRA and with a bias:
+    y = x W^T + bias (quant_matmul_t, crates/loractl-core/src/quant.rs's
+    QuantBackend::quant_matmul_t), dx = dy W (its backward), and the LoRA
+    forward with the bias through lrq_lora_fwd_noalloc, bit-identical to
+    lrq_lora_fwd where its fixed scratch holds the shape's workspace (else
+    it refuses the shape with LRQ_EINVAL)."""
+    from loractl_amd._lib import LrqError
+
+    g = torch.Generator(device=cuda).manual_seed(M * 137 + K * 5 + N + r)
+    w = torch.randn(N, K, device=cuda, generator=g) * 0.02
+    bias = torch.randn(N, device=cuda, generator=g) * 0.1
+    wq = D.compute_weight(_quantize(w, fmt, grp).with_bias(bias))
+    W = D.dequant(wq).float()
+    x = torch.randn(M, K, device=cuda, generator=g).to(torch.bfloat16)
+    a = ((torch.rand(K, r, device=cuda, generator=g) * 2 - 1) / K ** 0.5).to(torch.bfloat16)
+    b = (torch.randn(r, N, device=cuda, generator=g) * 1e-1).to(torch.bfloat16)
+    dy = torch.randn(M, N, device=cuda, generator=g).to(torch.bfloat16)
+    s = 16.0 / r
+    y0 = D.quant_matmul_t(x, wq)
+    dx0 = D.quant_matmul_t_bwd(dy, wq)
+    y1, t1 = D.lora_fwd(x, wq, a, b, s)
+    y2, t2 = torch.empty_like(y1), torch.empty_like(t1)
+    try:
+        D.lora_fwd_noalloc(x, wq, a, b, s, y2, t2)
+        noalloc = True
+    except LrqError as e:
+        assert "scratch" in str(e), str(e)
+        noalloc = False
+    D.sync()
+
+    xf = x.float()
+    tb = (s * xf @ a.float()).to(torch.bfloat16).float()
+    check("y base + bias", y0, (xf @ W.t() + bias).cpu().numpy())
+    check("dx base", dx0, (dy.float() @ W).cpu().numpy())
+    check("y LoRA + bias", y1, (xf @ W.t() + tb @ b.float() + bias).cpu().numpy())
+    if noalloc:
+        assert torch.equal(y1, y2) and torch.equal(t1, t2), "noalloc forward differs from lrq_lora_fwd"
