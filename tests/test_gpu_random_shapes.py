@@ -132,3 +132,37 @@ def test_random_shape_base_bias_and_noalloc(cuda, M, K, N, r, fmt, grp):
     check("y LoRA + bias", y1, (xf @ W.t() + tb @ b.float() + bias).cpu().numpy())
     if noalloc:
         assert torch.equal(y1, y2) and torch.equal(t1, t2), "noalloc forward differs from lrq_lora_fwd"
+
+
+@pytest.mark.parametrize("M,K,N,r,fmt,grp", [(65536, 1024, 2048, 32, "int4", 64), (259456, 256, 512, 16, "int8", 128),
+                                            (259456, 256, 512, 64, "fp8", 0)],
+                         ids=["m65536-int4", "m-limit-int8", "m-limit-fp8-r64"])
+def test_large_token_counts(cuda, M, K, N, r, fmt, grp):
+    """Token counts far past the benchmark's 4096, up to LRQ_MAX_LORA_TOKENS
+    itself (259456: the t and u kernels' one arrival counter per 16 tokens
+    then fills the counter area to its limit), forward and backward against
+    the fp32 reference; dA and dB then reduce over a quarter million
+    tokens."""
+    from loractl_amd import _lib as L
+
+    assert M <= L.LRQ_MAX_LORA_TOKENS
+    g = torch.Generator(device=cuda).manual_seed(M + K + N + r)
+    w = torch.randn(N, K, device=cuda, generator=g) * 0.02
+    wq = _quantize(w, fmt, grp)
+    W = D.dequant(wq).float()
+    x = torch.randn(M, K, device=cuda, generator=g).to(torch.bfloat16)
+    a = ((torch.rand(K, r, device=cuda, generator=g) * 2 - 1) / K ** 0.5).to(torch.bfloat16)
+    b = (torch.randn(r, N, device=cuda, generator=g) * 1e-1).to(torch.bfloat16)
+    dy = torch.randn(M, N, device=cuda, generator=g).to(torch.bfloat16)
+    s = 16.0 / r
+    y, t = D.lora_fwd(x, wq, a, b, s)
+    dx, da, db = D.lora_bwd(x, dy, wq, a, b, s, t)
+    D.sync()
+    xf, af, bf, dyf = x.float(), a.float(), b.float(), dy.float()
+    tb = (s * xf @ af).to(torch.bfloat16).float()
+    u = (s * dyf @ bf.t()).to(torch.bfloat16).float()
+    check("t", t, (s * xf @ af).cpu().numpy())
+    check("y", y, (xf @ W.t() + tb @ bf).cpu().numpy())
+    check("dx", dx, (dyf @ W + u @ af.t()).cpu().numpy())
+    check("dA", da, (xf.t() @ u).cpu().numpy())
+    check("dB", db, (tb.t() @ dyf).cpu().numpy())
