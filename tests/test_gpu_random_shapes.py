@@ -166,3 +166,47 @@ def test_large_token_counts(cuda, M, K, N, r, fmt, grp):
     check("dx", dx, (dyf @ W + u @ af.t()).cpu().numpy())
     check("dA", da, (xf.t() @ u).cpu().numpy())
     check("dB", db, (tb.t() @ dyf).cpu().numpy())
+
+
+@pytest.mark.parametrize("M,path", [(5, "planned"), (300, "mid64"), (300, "mid128"), (200, "mid64s"), (2048, "large")])
+@pytest.mark.parametrize("grp", [256, 512])
+@pytest.mark.parametrize("fmt", ["int4", "int8"])
+def test_large_quant_blocks(cuda, fmt, grp, M, path):
+    """Quant blocks of 256 and 512 (any power of two >= 32 that divides d_in
+    is accepted; crates/loractl-core/src/quant.rs's group argument): the
+    device quantization and dequantization are bit-exact against the oracle
+    (Q4S / Q8S with that block), and every kernel path (few-token, both
+    mid-size tiles, depth ranges, large tiles) gives y, t, dx, dA and dB
+    within the tolerance. A block then spans four or eight of the kernels'
+    64-deep steps, and in the transposed section four or eight 64-row
+    block rows share one scale row."""
+    import oracle as O
+    from gpu_helpers import case_inputs, gemm_path, to_dev
+
+    K, N, r = 2048, 1032, 16
+    w, x, a, b, dy = case_inputs(M, K, N, r, seed=M + grp + len(fmt))
+    t32 = torch.from_numpy(w).to(cuda)
+    if fmt == "int4":
+        wq = D.quantize_int4(t32, grp)
+        p, sc = O.quantize_int4_packed(w, grp)
+        wdq = O.dequant_int4(p, sc, K, grp)
+    else:
+        wq = D.quantize_int8(t32, grp)
+        q, sc = O.quantize(w, grp, 127)
+        wdq = O.dequant_q(q, sc, grp)
+    assert np.array_equal(D.dequant(wq).cpu().numpy(), wdq), "dequantized weight differs from the oracle"
+    xd, ad, bd, dyd = (to_dev(v, cuda) for v in (x, a, b, dy))
+    s = 16.0 / r
+    with gemm_path(path):
+        y, t = D.lora_fwd(xd, wq, ad, bd, s)
+        dx, da, db = D.lora_bwd(xd, dyd, wq, ad, bd, s, t)
+    D.sync()
+    W = torch.from_numpy(wdq).to(cuda)
+    xf, af, bf, dyf = xd.float(), ad.float(), bd.float(), dyd.float()
+    tb = (s * xf @ af).to(torch.bfloat16).float()
+    u = (s * dyf @ bf.t()).to(torch.bfloat16).float()
+    check("t", t, (s * xf @ af).cpu().numpy())
+    check("y", y, (xf @ W.t() + tb @ bf).cpu().numpy())
+    check("dx", dx, (dyf @ W + u @ af.t()).cpu().numpy())
+    check("dA", da, (xf.t() @ u).cpu().numpy())
+    check("dB", db, (tb.t() @ dyf).cpu().numpy())
