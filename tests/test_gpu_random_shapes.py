@@ -210,3 +210,43 @@ def test_large_quant_blocks(cuda, fmt, grp, M, path):
     check("dx", dx, (dyf @ W + u @ af.t()).cpu().numpy())
     check("dA", da, (xf.t() @ u).cpu().numpy())
     check("dB", db, (tb.t() @ dyf).cpu().numpy())
+
+
+@pytest.mark.parametrize("path", ["mid64", "mid128", "mid64s", "mid128s"])
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_mid_paths_repeat_bit_identical(cuda, fmt, path):
+    """The mid-size tiles' pipelines count their copies per stage (one load
+    fewer per stage in the fp8 forward, which loads no scales in its loop):
+    a miscounted wait lets a wavefront read a stage before its copy lands,
+    which shows up in some calls and not others. Forward and backward on
+    every mid-size path and format, at a ragged token count (200: three full
+    64-token tiles and 8 tokens), five times over: within the tolerance and
+    bit-identical across the repeats."""
+    M, K, N, r = 200, 3072, 3072, 16
+    g = torch.Generator(device=cuda).manual_seed(23)
+    w = torch.randn(N, K, device=cuda, generator=g) * 0.02
+    wq = _quantize(w, fmt, 64)
+    W = D.dequant(wq).float()
+    x = torch.randn(M, K, device=cuda, generator=g).to(torch.bfloat16)
+    a = ((torch.rand(K, r, device=cuda, generator=g) * 2 - 1) / K ** 0.5).to(torch.bfloat16)
+    b = (torch.randn(r, N, device=cuda, generator=g) * 1e-1).to(torch.bfloat16)
+    dy = torch.randn(M, N, device=cuda, generator=g).to(torch.bfloat16)
+    s = 1.0
+    from gpu_helpers import gemm_path
+
+    runs = []
+    with gemm_path(path):
+        for _ in range(5):
+            y, t = D.lora_fwd(x, wq, a, b, s)
+            runs.append((y, t) + D.lora_bwd(x, dy, wq, a, b, s, t))
+    D.sync()
+    xf, af, bf, dyf = x.float(), a.float(), b.float(), dy.float()
+    tb = (s * xf @ af).to(torch.bfloat16).float()
+    u = (s * dyf @ bf.t()).to(torch.bfloat16).float()
+    ref = (xf @ W.t() + tb @ bf, s * xf @ af, dyf @ W + u @ af.t(), xf.t() @ u, tb.t() @ dyf)
+    names = ("y", "t", "dx", "dA", "dB")
+    for name, got, want in zip(names, runs[0], ref):
+        check(f"{name} {path}", got, want.cpu().numpy())
+    for i, run in enumerate(runs[1:], 1):
+        for name, first, again in zip(names, runs[0], run):
+            assert torch.equal(first, again), f"{path} {fmt}: {name} of call {i} differs from call 0"
