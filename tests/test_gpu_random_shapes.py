@@ -212,7 +212,7 @@ def test_large_quant_blocks(cuda, fmt, grp, M, path):
     check("dB", db, (tb.t() @ dyf).cpu().numpy())
 
 
-@pytest.mark.parametrize("path", ["mid64", "mid128", "mid64s", "mid128s"])
+@pytest.mark.parametrize("path", ["mid64", "mid128", "mid64s", "mid128s", "large"])
 @pytest.mark.parametrize("fmt", FORMATS)
 def test_mid_paths_repeat_bit_identical(cuda, fmt, path):
     """The mid-size tiles' pipelines count their copies per stage (one load
@@ -221,7 +221,9 @@ def test_mid_paths_repeat_bit_identical(cuda, fmt, path):
     which shows up in some calls and not others. Forward and backward on
     every mid-size path and format, at a ragged token count (200: three full
     64-token tiles and 8 tokens), five times over: within the tolerance and
-    bit-identical across the repeats."""
+    bit-identical across the repeats. "large" at this token count is the
+    256-token tiles split in depth, with their partials summed in range
+    order by k_split_reduce."""
     M, K, N, r = 200, 3072, 3072, 16
     g = torch.Generator(device=cuda).manual_seed(23)
     w = torch.randn(N, K, device=cuda, generator=g) * 0.02
